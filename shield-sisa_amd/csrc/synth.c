@@ -1,0 +1,324 @@
+/* Seeded synthetic SHIELD-V inputs: a SHLDV001 weight file (+ "<file>.json" sidecar) and uint8 crops.
+ *
+ * The real checkpoint is not available offline, so every test and benchmark runs on weights drawn here from a
+ * seed.  Only IEEE add/mul/div/sqrt on doubles are used (no libm transcendentals), so the same seed yields the
+ * same bytes, hence the same SHA-256, on every x86-64 host.
+ *
+ * Tensor names and shapes are those of the reference export (tools/export_v.py:52-71, which writes every
+ * parameter and buffer of ShieldV; the architecture is fixed by engine/model/runtime.cpp:212-330 and
+ * oracle/shieldv_ref.py:359-375).  Distributions:
+ *   convolutions (stem, expand, depthwise, project, SE fc1/fc2, last 1x1): He-normal, std sqrt(2 / fan_in)
+ *   BatchNorm: weight 1, bias 0, running_mean 0, running_var 1
+ *   linears: Xavier-uniform, bound sqrt(6 / (fan_in + fan_out)); all biases 0
+ *   RMSNorm / gated-norm weights 1; time/row/col embeddings and readout N(0, 0.02^2)
+ *   GDN: A_log = ln U[1,16], dt_bias 0, short convs He-normal (fan_in 4), conv biases 0; SISA lambda_raw 0
+ * Normal deviates are Irwin-Hall sums of 12 uniforms minus 6. */
+#include "sha256.h"
+
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define SHV_SYNTH_API __attribute__((visibility("default")))
+
+/* ---------------------------------------------------------------------------------------------- generator */
+typedef struct { uint64_t s[4]; } Rng;
+
+static uint64_t splitmix(uint64_t* x) {
+    uint64_t z = (*x += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+static void rng_seed(Rng* r, uint64_t seed) {
+    uint64_t x = seed;
+    for (int i = 0; i < 4; ++i) r->s[i] = splitmix(&x);
+}
+static uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+static uint64_t rng_next(Rng* r) { /* xoshiro256** */
+    const uint64_t out = rotl(r->s[1] * 5, 7) * 9;
+    const uint64_t t = r->s[1] << 17;
+    r->s[2] ^= r->s[0];
+    r->s[3] ^= r->s[1];
+    r->s[1] ^= r->s[2];
+    r->s[0] ^= r->s[3];
+    r->s[2] ^= t;
+    r->s[3] = rotl(r->s[3], 45);
+    return out;
+}
+static double rng_unit(Rng* r) { return (double)(rng_next(r) >> 11) * (1.0 / 9007199254740992.0); } /* [0,1) */
+static double rng_normal(Rng* r) {
+    double s = 0.0;
+    for (int i = 0; i < 12; ++i) s += rng_unit(r);
+    return s - 6.0;
+}
+/* ln(x) for x in [1, 16]: 2 atanh(z), z = (x-1)/(x+1), by its power series (converges for z < 1) */
+static double ln_series(double x) {
+    const double z = (x - 1.0) / (x + 1.0), z2 = z * z;
+    double term = z, sum = 0.0;
+    for (int k = 0; k < 400; ++k) {
+        sum += term / (double)(2 * k + 1);
+        term *= z2;
+    }
+    return 2.0 * sum;
+}
+
+/* ---------------------------------------------------------------------------------------------- tensor table */
+enum { D_HE = 0, D_XAVIER, D_ONE, D_ZERO, D_EMB, D_ALOG };
+
+typedef struct {
+    char name[96];
+    int rank, dims[4];
+    int dist, fan_in, fan_out;
+    int param;  /* 1 = parameter (counts towards the model's parameter total), 0 = buffer */
+} Spec;
+
+typedef struct {
+    Spec* v;
+    int n, cap;
+} Table;
+
+static void add(Table* t, const char* name, int rank, const int* dims, int dist, int fan_in, int fan_out, int param) {
+    if (t->n == t->cap) {
+        t->cap = t->cap ? 2 * t->cap : 64;
+        t->v = (Spec*)realloc(t->v, sizeof(Spec) * (size_t)t->cap);
+    }
+    Spec* s = &t->v[t->n++];
+    memset(s, 0, sizeof *s);
+    snprintf(s->name, sizeof s->name, "%s", name);
+    s->rank = rank;
+    for (int i = 0; i < rank; ++i) s->dims[i] = dims[i];
+    s->dist = dist;
+    s->fan_in = fan_in;
+    s->fan_out = fan_out;
+    s->param = param;
+}
+static void t1(Table* t, const char* n, int a, int dist) { int d[1] = {a}; add(t, n, 1, d, dist, 0, 0, 1); }
+static void lin(Table* t, const char* n, int out, int in) { int d[2] = {out, in}; add(t, n, 2, d, D_XAVIER, in, out, 1); }
+static void conv(Table* t, const char* n, int out, int per_in, int k) {
+    int d[4] = {out, per_in, k, k};
+    add(t, n, 4, d, D_HE, per_in * k * k, 0, 1);
+}
+static void bn(Table* t, const char* prefix, int c) {
+    char n[96];
+    int d[1] = {c};
+    snprintf(n, sizeof n, "%s.weight", prefix); add(t, n, 1, d, D_ONE, 0, 0, 1);
+    snprintf(n, sizeof n, "%s.bias", prefix); add(t, n, 1, d, D_ZERO, 0, 0, 1);
+    snprintf(n, sizeof n, "%s.running_mean", prefix); add(t, n, 1, d, D_ZERO, 0, 0, 0);
+    snprintf(n, sizeof n, "%s.running_var", prefix); add(t, n, 1, d, D_ONE, 0, 0, 0);
+}
+static int make_div8(int v) { /* torchvision _make_divisible(v, 8) for integer v */
+    int nv = (v + 4) / 8 * 8;
+    if (nv < 8) nv = 8;
+    if (10 * nv < 9 * v) nv += 8;
+    return nv;
+}
+
+/* MobileNetV3-Large features[1..15]: in, kernel, expanded, out, SE, stride (torchvision inverted-residual table) */
+static const int kBlk[15][6] = {
+    {16, 3, 16, 16, 0, 1},   {16, 3, 64, 24, 0, 2},   {24, 3, 72, 24, 0, 1},   {24, 5, 72, 40, 1, 2},
+    {40, 5, 120, 40, 1, 1},  {40, 5, 120, 40, 1, 1},  {40, 3, 240, 80, 0, 2},  {80, 3, 200, 80, 0, 1},
+    {80, 3, 184, 80, 0, 1},  {80, 3, 184, 80, 0, 1},  {80, 3, 480, 112, 1, 1}, {112, 3, 672, 112, 1, 1},
+    {112, 5, 672, 160, 1, 2}, {160, 5, 960, 160, 1, 1}, {160, 5, 960, 160, 1, 1}};
+
+static void build_table(Table* t) {
+    char n[96];
+    conv(t, "cnn.0.0.weight", 16, 3, 3);
+    bn(t, "cnn.0.1", 16);
+    for (int i = 0; i < 15; ++i) {
+        const int in = kBlk[i][0], k = kBlk[i][1], ex = kBlk[i][2], out = kBlk[i][3], se = kBlk[i][4];
+        int j = 0;
+        if (ex != in) {
+            snprintf(n, sizeof n, "cnn.%d.block.%d.0.weight", i + 1, j); conv(t, n, ex, in, 1);
+            snprintf(n, sizeof n, "cnn.%d.block.%d.1", i + 1, j); bn(t, n, ex);
+            ++j;
+        }
+        snprintf(n, sizeof n, "cnn.%d.block.%d.0.weight", i + 1, j); conv(t, n, ex, 1, k);
+        snprintf(n, sizeof n, "cnn.%d.block.%d.1", i + 1, j); bn(t, n, ex);
+        ++j;
+        if (se) {
+            const int sq = make_div8(ex / 4);
+            snprintf(n, sizeof n, "cnn.%d.block.%d.fc1.weight", i + 1, j); conv(t, n, sq, ex, 1);
+            snprintf(n, sizeof n, "cnn.%d.block.%d.fc1.bias", i + 1, j); t1(t, n, sq, D_ZERO);
+            snprintf(n, sizeof n, "cnn.%d.block.%d.fc2.weight", i + 1, j); conv(t, n, ex, sq, 1);
+            snprintf(n, sizeof n, "cnn.%d.block.%d.fc2.bias", i + 1, j); t1(t, n, ex, D_ZERO);
+            ++j;
+        }
+        snprintf(n, sizeof n, "cnn.%d.block.%d.0.weight", i + 1, j); conv(t, n, out, ex, 1);
+        snprintf(n, sizeof n, "cnn.%d.block.%d.1", i + 1, j); bn(t, n, out);
+    }
+    conv(t, "cnn.16.0.weight", 960, 160, 1);
+    bn(t, "cnn.16.1", 960);
+    lin(t, "projection.weight", 384, 960);
+    { int d[2] = {20, 384}; add(t, "time_embedding", 2, d, D_EMB, 0, 0, 1); }
+    { int d[2] = {4, 384}; add(t, "row_embedding", 2, d, D_EMB, 0, 0, 1); }
+    { int d[2] = {4, 384}; add(t, "col_embedding", 2, d, D_EMB, 0, 0, 1); }
+    { int d[3] = {1, 1, 384}; add(t, "readout", 3, d, D_EMB, 0, 0, 1); }
+    const char* stages[2] = {"gdn_a", "gdn_b"};
+    for (int s = 0; s < 2; ++s) {
+        const char* p = stages[s];
+        snprintf(n, sizeof n, "%s.norm.weight", p); t1(t, n, 384, D_ONE);
+        snprintf(n, sizeof n, "%s.ffn_norm.weight", p); t1(t, n, 384, D_ONE);
+        snprintf(n, sizeof n, "%s.mixer.q_proj.weight", p); lin(t, n, 384, 384);
+        snprintf(n, sizeof n, "%s.mixer.k_proj.weight", p); lin(t, n, 384, 384);
+        snprintf(n, sizeof n, "%s.mixer.v_proj.weight", p); lin(t, n, 768, 384);
+        snprintf(n, sizeof n, "%s.mixer.a_proj.weight", p); lin(t, n, 6, 384);
+        snprintf(n, sizeof n, "%s.mixer.b_proj.weight", p); lin(t, n, 6, 384);
+        snprintf(n, sizeof n, "%s.mixer.A_log", p); t1(t, n, 6, D_ALOG);
+        snprintf(n, sizeof n, "%s.mixer.dt_bias", p); t1(t, n, 6, D_ZERO);
+        const char* cv[3] = {"q_conv1d", "k_conv1d", "v_conv1d"};
+        const int cw[3] = {384, 384, 768};
+        for (int c = 0; c < 3; ++c) {
+            int d[3] = {cw[c], 1, 4};
+            snprintf(n, sizeof n, "%s.mixer.%s.weight", p, cv[c]); add(t, n, 3, d, D_HE, 4, 0, 1);
+            snprintf(n, sizeof n, "%s.mixer.%s.bias", p, cv[c]); t1(t, n, cw[c], D_ZERO);
+        }
+        snprintf(n, sizeof n, "%s.mixer.g_proj.weight", p); lin(t, n, 768, 384);
+        snprintf(n, sizeof n, "%s.mixer.o_norm.weight", p); t1(t, n, 128, D_ONE);
+        snprintf(n, sizeof n, "%s.mixer.o_proj.weight", p); lin(t, n, 384, 768);
+        snprintf(n, sizeof n, "%s.ffn.gate.weight", p); lin(t, n, 960, 384);
+        snprintf(n, sizeof n, "%s.ffn.up.weight", p); lin(t, n, 960, 384);
+        snprintf(n, sizeof n, "%s.ffn.down.weight", p); lin(t, n, 384, 960);
+    }
+    t1(t, "sisa.attn_norm.weight", 384, D_ONE);
+    lin(t, "sisa.attn.W_Q.weight", 384, 384);
+    lin(t, "sisa.attn.W_K.weight", 384, 384);
+    lin(t, "sisa.attn.W_V.weight", 384, 384);
+    lin(t, "sisa.attn.W_O.weight", 384, 384);
+    lin(t, "sisa.attn.W_B.weight", 192, 384);
+    lin(t, "sisa.attn.W_C.weight", 192, 384);
+    lin(t, "sisa.attn.alpha_proj.weight", 6, 384);
+    t1(t, "sisa.attn.alpha_proj.bias", 6, D_ZERO);
+    lin(t, "sisa.attn.theta_proj.weight", 96, 384);
+    lin(t, "sisa.attn.forget_proj.weight", 6, 384);
+    t1(t, "sisa.attn.forget_proj.bias", 6, D_ZERO);
+    t1(t, "sisa.attn.lambda_raw", 6, D_ZERO);
+    t1(t, "sisa.ffn_norm.weight", 384, D_ONE);
+    lin(t, "sisa.ffn.w_gate.weight", 960, 384);
+    lin(t, "sisa.ffn.w_up.weight", 960, 384);
+    lin(t, "sisa.ffn.w_down.weight", 384, 960);
+    t1(t, "final_norm.weight", 384, D_ONE);
+    lin(t, "head.0.weight", 128, 384);
+    t1(t, "head.0.bias", 128, D_ZERO);
+    lin(t, "head.2.weight", 1, 128);
+    t1(t, "head.2.bias", 1, D_ZERO);
+}
+
+static size_t numel(const Spec* s) {
+    size_t e = 1;
+    for (int i = 0; i < s->rank; ++i) e *= (size_t)s->dims[i];
+    return e;
+}
+
+static void fill(const Spec* s, float* out, Rng* r) {
+    const size_t e = numel(s);
+    double scale = 0.0;
+    if (s->dist == D_HE) scale = __builtin_sqrt(2.0 / (double)s->fan_in);
+    if (s->dist == D_XAVIER) scale = __builtin_sqrt(6.0 / (double)(s->fan_in + s->fan_out));
+    for (size_t i = 0; i < e; ++i) {
+        double v = 0.0;
+        switch (s->dist) {
+        case D_HE: v = rng_normal(r) * scale; break;
+        case D_XAVIER: v = (2.0 * rng_unit(r) - 1.0) * scale; break;
+        case D_ONE: v = 1.0; break;
+        case D_ZERO: v = 0.0; break;
+        case D_EMB: v = rng_normal(r) * 0.02; break;
+        case D_ALOG: v = ln_series(1.0 + 15.0 * rng_unit(r)); break;
+        default: break;
+        }
+        out[i] = (float)v;
+    }
+}
+
+/* ---------------------------------------------------------------------------------------------- C API */
+/* Writes `path` (SHLDV001) and `path`.json.  Returns 0 on success, -1 on I/O failure.  sha_hex (65 bytes) may be
+ * NULL; parameter/tensor totals may be NULL. */
+SHV_SYNTH_API int shv_synth_weights(const char* path, uint64_t seed, double threshold, char* sha_hex,
+                                     long long* parameters, int* tensors) {
+    Table t = {0};
+    build_table(&t);
+    FILE* f = fopen(path, "wb");
+    if (!f) { free(t.v); return -1; }
+    shv_sha256 h;
+    shv_sha256_init(&h);
+    Rng r;
+    rng_seed(&r, seed);
+    long long params = 0;
+    size_t bytes = 0;
+    int ok = 1;
+#define PUT(p, n)                                              \
+    do {                                                       \
+        if (fwrite((p), 1, (n), f) != (size_t)(n)) ok = 0;     \
+        shv_sha256_update(&h, (p), (n));                       \
+        bytes += (n);                                          \
+    } while (0)
+    PUT("SHLDV001", 8);
+    const uint32_t count = (uint32_t)t.n;
+    PUT(&count, 4);
+    for (int i = 0; i < t.n && ok; ++i) {
+        const Spec* s = &t.v[i];
+        const uint32_t nl = (uint32_t)strlen(s->name), rank = (uint32_t)s->rank;
+        PUT(&nl, 4);
+        PUT(s->name, nl);
+        PUT(&rank, 4);
+        for (int d = 0; d < s->rank; ++d) { const uint32_t dim = (uint32_t)s->dims[d]; PUT(&dim, 4); }
+        const uint64_t e = numel(s);
+        PUT(&e, 8);
+        float* buf = (float*)malloc(sizeof(float) * e);
+        fill(s, buf, &r);
+        PUT(buf, sizeof(float) * e);
+        free(buf);
+        if (s->param) params += (long long)e;
+    }
+#undef PUT
+    if (fclose(f) != 0) ok = 0;
+    uint8_t dg[32];
+    char hex[65];
+    shv_sha256_final(&h, dg);
+    shv_sha256_hex(dg, hex);
+    if (ok) {
+        char jp[4096];
+        snprintf(jp, sizeof jp, "%s.json", path);
+        FILE* j = fopen(jp, "w");
+        if (!j) ok = 0;
+        else {
+            fprintf(j,
+                    "{\n \"format\": \"SHLDV001\",\n \"generator\": \"shv_synth_weights\",\n \"seed\": %llu,\n"
+                    " \"threshold\": %.17g,\n \"parameters\": %lld,\n \"tensor_count\": %d,\n"
+                    " \"output_bytes\": %zu,\n \"output_sha256\": \"%s\"\n}\n",
+                    (unsigned long long)seed, threshold, params, t.n, bytes, hex);
+            if (fclose(j) != 0) ok = 0;
+        }
+    }
+    if (sha_hex) memcpy(sha_hex, hex, 65);
+    if (parameters) *parameters = params;
+    if (tensors) *tensors = t.n;
+    free(t.v);
+    return ok ? 0 : -1;
+}
+
+/* n uniform bytes on {0..255} from `seed` (crops: 172800 bytes per frame, 20 frames per clip). */
+SHV_SYNTH_API void shv_synth_bytes(uint8_t* out, size_t n, uint64_t seed) {
+    Rng r;
+    rng_seed(&r, seed);
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        const uint64_t x = rng_next(&r);
+        memcpy(out + i, &x, 8);
+    }
+    if (i < n) {
+        const uint64_t x = rng_next(&r);
+        memcpy(out + i, &x, n - i);
+    }
+}
+
+/* SHA-256 of a buffer (hex), for fixture checks of generated inputs. */
+SHV_SYNTH_API void shv_synth_sha256(const void* data, size_t n, char* hex) {
+    shv_sha256 h;
+    uint8_t dg[32];
+    shv_sha256_init(&h);
+    shv_sha256_update(&h, data, n);
+    shv_sha256_final(&h, dg);
+    shv_sha256_hex(dg, hex);
+}
