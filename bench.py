@@ -1,0 +1,202 @@
+#!/usr/bin/env python3
+"""SHIELD-V batched forward benchmark on one MI355X (BASELINE.json metric).
+
+value: clips/s of the full SHIELD-V forward (uint8 crops -> logit) in FP16 at batch 128 clips (2560 frames),
+       inputs resident in HBM, through the C-ABI device entry point (shv_hip_forward_device), timed with HIP events
+       on the launching stream over exactly --steps forwards after --warmup untimed ones.
+extra: batch-1 end-to-end latency through shv_hip_predict (pinned host clip, H2D included, like the reference's
+       2.89 ms at README.md:117), encoder-only frames/s, roofline of the dominant kernel family, and the reference
+       CPU engine (compiled from the reference sources, oracle/_ref) timed on this host's cores.
+Synthetic data: seeded random-init weights in the reference weight-file layout and uniform uint8 crops.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+MFMA_FP16_TFLOPS = 2500.0   # MI355X dense fp16
+REF_B128_CLIPS_PER_S = 128 / 0.191   # reference README.md:118 (RTX A6000, batch 128 FP16)
+
+
+def load_shv():
+    spec = importlib.util.spec_from_file_location("shv_hip", ROOT / "shield-sisa_amd" / "shv_hip.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["shv_hip"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(weights: Path, clips: np.ndarray, seconds: float) -> dict | None:
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    if not oracle.REF_SO.exists():
+        return None
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    ref = oracle.Reference(weights, threads=threads)
+    batch = clips[: min(len(clips), 2 * threads)]
+    ref.predict(batch[:1])
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ref.predict(batch)
+        n += len(batch)
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    isa = ref.isa
+    ref.close()
+    return {"value": round(n / dt, 3), "unit": "clips/s", "cores": threads, "kind": "reference",
+            "sample": f"reference CPU engine exact FP32 ({isa}), shv_cpu_predict on {len(batch)}-clip batches "
+                      f"repeated for {dt:.1f} s ({n} clips)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=128)
+    ap.add_argument("--mode", default="fp16", choices=["fp16", "bf16", "fp32"])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--latency-iters", type=int, default=100)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the SHIELD-V forward has no cross-GPU step "
+              "(clips are independent rows); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    shv = load_shv()
+    B = args.batch
+    with tempfile.TemporaryDirectory() as td:
+        w = Path(td) / "bench.weights"
+        shv.write_weights(w, seed=1, threshold=0.5)
+        clips = shv.synth_clips(B, 1000)
+        log(f"[bench] load {args.mode} model, batch {B} clips")
+        model = shv.Model(w, args.mode, experimental=args.mode != "fp32", max_frames=B * 20, max_windows=B)
+        stream = torch.cuda.Stream()
+        d_frames = torch.from_numpy(clips.reshape(-1)).to("cuda")
+        d_logits = torch.empty(B, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        sh = stream.cuda_stream
+        with torch.cuda.stream(stream):
+            for _ in range(args.warmup):
+                model.forward_device(d_frames.data_ptr(), B, d_logits.data_ptr(), sh)
+            stream.synchronize()
+            log("[bench] warmup done")
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(args.steps):
+                model.forward_device(d_frames.data_ptr(), B, d_logits.data_ptr(), sh)
+            e1.record(stream)
+            e1.synchronize()
+            torch.cuda.synchronize()
+            total_ms = e0.elapsed_time(e1)
+        ms = total_ms / args.steps
+        value = B / (ms / 1000.0)
+        logits = d_logits.cpu().numpy()
+        log(f"[bench] {ms:.3f} ms/step -> {value:.1f} clips/s; finite logits {np.isfinite(logits).all()}")
+
+        # encoder only (config 1: 2560 frames FP16)
+        d_tok = torch.empty((B * 20, 6144), dtype=torch.float32, device="cuda")
+        with torch.cuda.stream(stream):
+            model.encode_device(d_frames.data_ptr(), B * 20, d_tok.data_ptr(), sh)
+            stream.synchronize()
+            e0.record(stream)
+            enc_steps = max(3, args.steps // 2)
+            for _ in range(enc_steps):
+                model.encode_device(d_frames.data_ptr(), B * 20, d_tok.data_ptr(), sh)
+            e1.record(stream)
+            e1.synchronize()
+        enc_ms = e0.elapsed_time(e1) / enc_steps
+        log(f"[bench] encoder {enc_ms:.3f} ms / {B * 20} frames")
+
+        # per-family kernel timing with HIP events on the launching stream (graphs off while profiling)
+        fams = ["gemm_pw", "dw", "stem", "se_pool", "pool", "gemm_seq", "gemm_f32_small", "rmsnorm", "gdn_prep",
+                "delta", "gated_norm", "sisa", "head", "assemble"]
+        model.profile_enable(True)
+        prof_steps = min(args.steps, 5)
+        with torch.cuda.stream(stream):
+            for _ in range(prof_steps):
+                model.forward_device(d_frames.data_ptr(), B, d_logits.data_ptr(), sh)
+            stream.synchronize()
+        stats = {f: model.profile_read(f) for f in fams}
+        model.profile_enable(False)
+        stats = {k: v for k, v in stats.items() if v and v["launches"]}
+        per_step = {k: round(v["ms"] / prof_steps, 3) for k, v in stats.items()}
+        log("[bench] per-step ms by family: " + json.dumps(per_step))
+        dom = max(stats, key=lambda k: stats[k]["ms"])
+        d = stats[dom]
+        avg_ms = d["ms"] / d["launches"]
+        achieved = (d["bytes"] / d["launches"]) / (avg_ms / 1000.0) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                    "avg_launch_ms": round(avg_ms, 4), "launches_per_step": d["launches"] // prof_steps}
+        model.close()
+
+        # batch-1 latency through the synchronous API (pinned host clip, H2D included)
+        lat = None
+        with shv.Model(w, args.mode, experimental=args.mode != "fp32") as m1:
+            lib = m1.lib
+            p = lib.shv_hip_host_alloc(20 * shv.FRAME_BYTES)
+            pinned = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_uint8 * (20 * shv.FRAME_BYTES)).from_address(p))
+            pinned[:] = clips[0].reshape(-1)
+            out = np.empty(1, np.float32)
+            for _ in range(10):
+                lib.shv_hip_predict(m1.h, p, 1, out.ctypes.data)
+            ts = []
+            for _ in range(args.latency_iters):
+                t0 = time.perf_counter()
+                lib.shv_hip_predict(m1.h, p, 1, out.ctypes.data)
+                ts.append((time.perf_counter() - t0) * 1000.0)
+            lib.shv_hip_host_free(p)
+            lat = float(np.percentile(ts, 50))
+            log(f"[bench] batch-1 latency p50 {lat:.3f} ms (p95 {np.percentile(ts, 95):.3f})")
+
+        cpu = None
+        if not args.no_cpu:
+            cpu = cpu_baseline(w, clips, args.cpu_seconds)
+
+    line = {
+        "metric": "SHIELD-V clips/sec at batch 128 FP16 on 1 MI355X; batch-1 latency (ms)",
+        "value": round(value, 2),
+        "unit": "clips/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REF_B128_CLIPS_PER_S, 3) if B == 128 and args.mode == "fp16" else None,
+        "dtype": args.mode,
+        "data": "synthetic (seeded random-init weights in the SHLDV001 layout, uniform uint8 crops)",
+        "config": {"workload": f"shieldv_forward_{args.mode}_b{B}", "clips": B, "frames_per_clip": 20,
+                   "crop": "180x320x3 uint8", "tokens_per_window": 321, "d_model": 384,
+                   "inputs": "device-resident (HBM)", "entry": "shv_hip_forward_device"},
+        "latency_b1_ms": None if lat is None else round(lat, 3),
+        "encoder_frames_per_s": round(B * 20 / (enc_ms / 1000.0), 1),
+        "family_ms_per_step": per_step,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

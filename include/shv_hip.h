@@ -1,0 +1,144 @@
+/*
+ * shv_hip.h -- SHIELD-V video detector, MI355X (gfx950) HIP inference engine, C API (libshield_v_hip.so).
+ *
+ * Drop-in counterpart of the reference CUDA engine API (engine/include/shv_cuda.h:74-151): every function,
+ * struct and constant below replaces the shv_cuda_* item of the same suffix, with the same argument meaning,
+ * the same struct layouts and the same error behaviour.  Per-item citations name the replaced declaration.
+ *
+ * Function: uint8 RGB crops [20][180][320][3] -> MobileNetV3-Large features (folded BatchNorm) -> 4x4 pool ->
+ * Linear 960->384 = 16 tokens per frame -> + (time + row) + col, readout -> GDN-A -> GDN-B x2 -> SISA (last row)
+ * -> RMSNorm -> head -> logit.  Decision (caller side): score = sigmoid(logit) in double, alert iff
+ * score >= shv_hip_threshold(m).  A NaN logit means "unavailable" (failed job or non-finite result).
+ *
+ * MODES: "fp32" = IEEE fp32 everywhere, same per-element operation order as the reference CPU exact engine
+ * (GEMM K blocks of 64, the same reduction trees); always loadable.  "bf16" / "fp16" = convolution and all-row
+ * GEMM operands in that type on MFMA with fp32 accumulation; residual stream, norms, recurrences, SE, SISA last
+ * row and head in fp32, SISA prefix sums in double.  Approximate modes load only with a passing certificate line
+ *   "<weights sha256> <mode> <shv_hip_compute_revision()> PASS <cert json> <cert json sha256> threshold=<%.17g>"
+ * in "<weights>.hip.cert" (first line "SHIELDV_HIP_CERT_V2") whose threshold equals the loaded one exactly.
+ * SIDECAR "<weights>.json": "output_sha256" must equal the weight file's SHA-256 and "threshold" must be present,
+ * finite and in (0, 1), in every mode.
+ *
+ * ROW INDEPENDENCE: the logit of a window and the tokens of a frame are bitwise identical whatever else is in
+ * the batch (size, order, padding, coalescing), in every mode: no split-K, fixed reduction orders, no atomics.
+ *
+ * THREADING AND LIFETIMES: as the reference contract (engine/include/shv_cuda.h:36-59).  One worker thread per
+ * model drives a copy stream and a compute stream; jobs run in FIFO order and consecutive jobs coalesce into one
+ * GPU batch up to the limits; callbacks run on the worker thread; every job is freed exactly once with
+ * shv_hip_job_free; shv_hip_free completes queued jobs first; errors are thread-local.
+ *
+ * DEVICE TOKEN SLOTS (options.token_slots > 0): a pool of 16x384 fp32 token blocks resident in HBM, written by
+ * store_slots and read by window_slots, with the reference's hazard rule for coalescing.
+ */
+#ifndef SHV_HIP_H
+#define SHV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+/* constants: shv_cuda.h:74-77 */
+#define SHV_HIP_API_VERSION 1
+#define SHV_HIP_FRAME_BYTES 172800    /* 180 x 320 x 3 uint8 RGB */
+#define SHV_HIP_TOKEN_FLOATS 6144     /* 16 tokens x 384, one frame */
+#define SHV_HIP_WINDOW_FRAMES 20
+
+typedef struct shv_hip_model shv_hip_model;   /* shv_cuda.h:79 */
+typedef struct shv_hip_job shv_hip_job;       /* shv_cuda.h:80 */
+
+/* shv_cuda.h:82-89 (same fields, same defaults) */
+typedef struct shv_hip_options {
+    int max_frames;       /* frames per GPU batch (CNN); default 640 */
+    int max_windows;      /* windows per GPU batch (sequence); default 512 */
+    int max_host_tokens;  /* host-provided token blocks per GPU batch; default 2048 */
+    int token_slots;      /* device token slots (0 = none); default 0 */
+    int use_graphs;       /* HIP graphs per batch bucket; default 1 */
+    int max_delay_us;     /* scheduler: wait up to this long for more jobs before launching; default 0 */
+} shv_hip_options;
+
+void shv_hip_default_options(shv_hip_options* opt);                                     /* shv_cuda.h:91 */
+/* weights: SHLDV001 file (+ "<weights>.json").  mode: "fp32" | "bf16" | "fp16" (NULL = "fp32").
+ * device: HIP device ordinal.  NULL on error. */
+shv_hip_model* shv_hip_load(const char* weights, const char* mode, int device);          /* shv_cuda.h:94 */
+shv_hip_model* shv_hip_load_ex(const char* weights, const char* mode, int device,
+                               const shv_hip_options* opt);                              /* shv_cuda.h:95 */
+void shv_hip_free(shv_hip_model* m);                                                     /* shv_cuda.h:96 */
+
+const char* shv_hip_last_error(void);                                                    /* shv_cuda.h:98 */
+const char* shv_hip_mode(const shv_hip_model* m);                                        /* shv_cuda.h:99 */
+const char* shv_hip_fingerprint(const shv_hip_model* m);  /* SHA-256 hex of the weights; shv_cuda.h:100 */
+double shv_hip_threshold(const shv_hip_model* m);         /* from "<weights>.json"; shv_cuda.h:101 */
+const char* shv_hip_compute_revision(void);               /* "hip-<16 hex>" of the numeric sources; :102 */
+int shv_hip_limits(const shv_hip_model* m, int* max_frames, int* max_windows, int* max_host_tokens,
+                   int* token_slots);                                                    /* shv_cuda.h:103 */
+size_t shv_hip_weight_bytes(const shv_hip_model* m);      /* device bytes of weights; shv_cuda.h:104 */
+size_t shv_hip_device_bytes(const shv_hip_model* m);      /* device bytes allocated in total; :105 */
+
+/* synchronous (split into GPU batches internally); shv_cuda.h:107-114.
+ * rgb: n x 180x320x3 uint8; tokens: n x 16 x 384 fp32 (before positions).  tokens (classify): b x 20 x 16 x 384
+ * fp32; clips (predict): b x 20 x 180x320x3 uint8; logits: b fp32.  On failure outputs are NaN and -1 returned. */
+int shv_hip_encode_frames(shv_hip_model* m, const uint8_t* rgb, size_t n, float* tokens);   /* :112 */
+int shv_hip_classify(shv_hip_model* m, const float* tokens, size_t b, float* logits);       /* :113 */
+int shv_hip_predict(shv_hip_model* m, const uint8_t* clips, size_t b, float* logits);       /* :114 */
+
+/* asynchronous; shv_cuda.h:116-147 */
+typedef void (*shv_hip_callback)(shv_hip_job* job, int status /* 1 done, -1 failed */, void* user);
+
+typedef struct shv_hip_request {      /* shv_cuda.h:118-135, same layout */
+    const uint8_t* frames;            /* n_frames x 180x320x3 uint8 */
+    size_t n_frames;
+    float* tokens_out;                /* optional: n_frames x 6144 fp32 (host) */
+    const int32_t* store_slots;       /* optional: n_frames device token slots (-1 = do not store) */
+    size_t n_windows;                 /* entry e = window*20 + frame position: */
+    const int32_t* window_frames;     /*   >= 0 -> frame of this request (NULL = all -1) */
+    const int32_t* window_slots;      /*   else >= 0 -> device token slot */
+    const float* const* window_tokens;/*   else host pointer to 6144 fp32 */
+    float* logits_out;                /* n_windows fp32 (NaN for every window of a failed job) */
+    shv_hip_callback callback;        /* optional */
+    void* user;
+} shv_hip_request;
+
+shv_hip_job* shv_hip_submit(shv_hip_model* m, const shv_hip_request* req);               /* shv_cuda.h:139 */
+int shv_hip_job_status(const shv_hip_job* job);   /* 0 pending, 1 done, -1 failed; shv_cuda.h:140 */
+int shv_hip_job_wait(shv_hip_job* job);           /* blocks; 0 done, -1 failed; shv_cuda.h:141 */
+const char* shv_hip_job_error(const shv_hip_job* job);                                   /* shv_cuda.h:142 */
+int shv_hip_job_timing(const shv_hip_job* job, double* queue_ms, double* run_ms, double* gpu_ms,
+                       int* batch_frames, int* batch_windows);                           /* shv_cuda.h:145 */
+void shv_hip_job_free(shv_hip_job* job);                                                 /* shv_cuda.h:147 */
+
+/* pinned host memory (hipHostMalloc); frames in it are DMA'd without staging; shv_cuda.h:149-151 */
+void* shv_hip_host_alloc(size_t bytes);
+void shv_hip_host_free(void* p);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Engine-level entry points.  No counterpart in shv_cuda.h: the reference reaches its Engine class directly from
+ * C++ tools (bench/gpu_kbench.cu:59-98, bench/gpu_dump.cu).  They serve benchmarks and parity tools that run the
+ * forward on buffers already resident in HBM, without the scheduler or any host copy.
+ * Device pointers only; `stream` is a hipStream_t (NULL = the model's compute stream).  Not thread-safe against
+ * the model's own worker: call them only while no job is queued or running on `m`.
+ */
+/* d_frames: n_clips*20 crops in device memory; d_logits: n_clips fp32 in device memory.  n_clips <= limits. */
+int shv_hip_forward_device(shv_hip_model* m, const uint8_t* d_frames, int n_clips, float* d_logits, void* stream);
+/* encode only: d_frames (n_frames crops) -> d_tokens (n_frames x 6144 fp32), device memory. */
+int shv_hip_encode_device(shv_hip_model* m, const uint8_t* d_frames, int n_frames, float* d_tokens, void* stream);
+/* Per-kernel-family timing with HIP events on the launching stream: enable(1)/disable(0) and read
+ * the accumulated milliseconds and launch count of family `name` ("gemm_mfma", "dw", ...); returns -1 if unknown. */
+int shv_hip_profile_enable(shv_hip_model* m, int on);
+int shv_hip_profile_read(shv_hip_model* m, const char* name, double* total_ms, long long* launches,
+                         double* bytes);
+/* Debug: write float32 intermediates of frame 0 / window 0 of the next synchronous call into dir (graphs off). */
+int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+#ifdef __cplusplus
+}
+#endif
+#endif /* SHV_HIP_H */

@@ -1,0 +1,173 @@
+"""TEST INFRASTRUCTURE ONLY.  ctypes access to the oracle (this repo's C restatement, oracle/_build) and to the
+reference CPU engine compiled from /root/reference (oracle/_ref).  Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg may use this module, and only as the checker / the timed CPU baseline.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "_build" / "libshv_oracle.so"
+REF_SO = HERE / "_ref" / "libshield_v_cpu.so"
+FRAME_BYTES = 172800
+
+DUMP_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), ctypes.c_size_t)
+
+EPI = dict(store=0, relu=1, hs=2, res=3, acc=4, acc_div2=5, swiglu=6, hsig=7, silu=8)
+
+
+def build(ref: bool = False) -> None:
+    """Compile the oracle (and, when /root/reference exists, the reference CPU engine)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    if ref and Path("/root/reference/engine/model/runtime.cpp").exists():
+        subprocess.run(["make", "-s", "-C", str(HERE), "-j4", "ref"], check=True)
+
+
+class Oracle:
+    def __init__(self, weights):
+        if not ORACLE_SO.exists():
+            build()
+        lib = ctypes.CDLL(str(ORACLE_SO))
+        lib.orc_load.restype = ctypes.c_void_p
+        lib.orc_load.argtypes = [ctypes.c_char_p]
+        lib.orc_free.argtypes = [ctypes.c_void_p]
+        lib.orc_last_error.restype = ctypes.c_char_p
+        lib.orc_encode_frame.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, DUMP_FN, ctypes.c_void_p]
+        lib.orc_classify.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, DUMP_FN, ctypes.c_void_p]
+        lib.orc_gemm.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_void_p, ctypes.c_int]
+        lib.orc_exp.restype = ctypes.c_float
+        lib.orc_exp.argtypes = [ctypes.c_float]
+        lib.orc_silu.restype = ctypes.c_float
+        lib.orc_silu.argtypes = [ctypes.c_float]
+        lib.orc_hswish.restype = ctypes.c_float
+        lib.orc_hswish.argtypes = [ctypes.c_float]
+        lib.orc_delta_rule.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int]
+        self.lib = lib
+        self.h = None
+        if weights is not None:
+            self.h = lib.orc_load(str(weights).encode())
+            if not self.h:
+                raise RuntimeError("oracle load failed: " + lib.orc_last_error().decode())
+
+    def close(self):
+        if self.h:
+            self.lib.orc_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode_frame(self, rgb: np.ndarray, dumps: dict | None = None) -> np.ndarray:
+        rgb = np.ascontiguousarray(rgb, dtype=np.uint8)
+        out = np.empty((16, 384), np.float32)
+        cb = DUMP_FN(0)
+        if dumps is not None:
+            def f(ctx, name, data, n):
+                dumps[name.decode()] = np.ctypeslib.as_array(data, (n,)).copy()
+            cb = DUMP_FN(f)
+        self.lib.orc_encode_frame(self.h, rgb.ctypes.data, out.ctypes.data, cb, None)
+        return out
+
+    def classify(self, tokens20: np.ndarray, dumps: dict | None = None) -> float:
+        """tokens20: [20, 16, 384] float32"""
+        t = np.ascontiguousarray(tokens20, dtype=np.float32).reshape(20, 6144)
+        ptrs = (ctypes.c_void_p * 20)(*[t[i].ctypes.data for i in range(20)])
+        out = np.zeros(1, np.float32)
+        cb = DUMP_FN(0)
+        if dumps is not None:
+            def f(ctx, name, data, n):
+                dumps[name.decode()] = np.ctypeslib.as_array(data, (n,)).copy()
+            cb = DUMP_FN(f)
+        self.lib.orc_classify(self.h, ptrs, out.ctypes.data, cb, None)
+        return out
+
+    def predict(self, clip: np.ndarray, dumps: dict | None = None):
+        """clip uint8 [20,180,320,3] -> (logit float32 [1], tokens [20,16,384])"""
+        clip = np.ascontiguousarray(clip, dtype=np.uint8).reshape(20, FRAME_BYTES)
+        toks = np.stack([self.encode_frame(clip[f], dumps if f == 0 else None) for f in range(20)])
+        return self.classify(toks, dumps), toks
+
+    def gemm(self, A, W, bias=None, epi="store", R=None, C=None):
+        A = np.ascontiguousarray(A, np.float32)
+        W = np.ascontiguousarray(W, np.float32)
+        M, K = A.shape
+        N = W.shape[0]
+        ncol = N // 2 if epi == "swiglu" else N
+        if C is None:
+            C = np.zeros((M, ncol), np.float32)
+        C = np.ascontiguousarray(C, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        Rr = None if R is None else np.ascontiguousarray(R, np.float32)
+        self.lib.orc_gemm(A.ctypes.data, K, M, W.ctypes.data, None if b is None else b.ctypes.data, N, K,
+                          C.ctypes.data, ncol, EPI[epi], None if Rr is None else Rr.ctypes.data,
+                          0 if Rr is None else Rr.shape[1])
+        return C
+
+    def delta_rule(self, q, k, v, decay, beta):
+        q, k, v = (np.ascontiguousarray(x, np.float32) for x in (q, k, v))
+        decay = np.ascontiguousarray(decay, np.float32)
+        beta = np.ascontiguousarray(beta, np.float32)
+        T = q.shape[0]
+        o = np.zeros((T, 128), np.float32)
+        self.lib.orc_delta_rule(q.ctypes.data, k.ctypes.data, v.ctypes.data, decay.ctypes.data, beta.ctypes.data, T,
+                                64, 128, o.ctypes.data, 128)
+        return o
+
+
+class Reference:
+    """The reference CPU engine (engine/model, compiled by `make -C oracle ref`)."""
+
+    def __init__(self, weights, threads: int = 1, mode: str = "exact", isa: str | None = None):
+        if not REF_SO.exists():
+            raise RuntimeError(f"{REF_SO} not built (make -C oracle ref needs /root/reference)")
+        lib = ctypes.CDLL(str(REF_SO))
+        lib.shv_cpu_load_ex.restype = ctypes.c_void_p
+        lib.shv_cpu_load_ex.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int, ctypes.c_char_p]
+        lib.shv_cpu_predict.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.shv_cpu_encode_frames.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.shv_cpu_classify.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.shv_cpu_last_error.restype = ctypes.c_char_p
+        lib.shv_cpu_free.argtypes = [ctypes.c_void_p]
+        lib.shv_cpu_isa.restype = ctypes.c_char_p
+        lib.shv_cpu_isa.argtypes = [ctypes.c_void_p]
+        self.lib = lib
+        self.h = lib.shv_cpu_load_ex(str(weights).encode(), mode.encode(), threads,
+                                     None if isa is None else isa.encode())
+        if not self.h:
+            raise RuntimeError("reference load failed: " + lib.shv_cpu_last_error().decode())
+        self.threads = threads
+
+    @property
+    def isa(self) -> str:
+        return self.lib.shv_cpu_isa(self.h).decode()
+
+    def predict(self, clips: np.ndarray) -> np.ndarray:
+        clips = np.ascontiguousarray(clips, np.uint8)
+        b = clips.size // (20 * FRAME_BYTES)
+        out = np.empty(b, np.float32)
+        if self.lib.shv_cpu_predict(self.h, clips.ctypes.data, b, out.ctypes.data) != 0:
+            raise RuntimeError(self.lib.shv_cpu_last_error().decode())
+        return out
+
+    def encode_frames(self, frames: np.ndarray) -> np.ndarray:
+        frames = np.ascontiguousarray(frames, np.uint8)
+        n = frames.size // FRAME_BYTES
+        out = np.empty((n, 16, 384), np.float32)
+        if self.lib.shv_cpu_encode_frames(self.h, frames.ctypes.data, n, out.ctypes.data) != 0:
+            raise RuntimeError(self.lib.shv_cpu_last_error().decode())
+        return out
+
+    def close(self):
+        if self.h:
+            self.lib.shv_cpu_free(self.h)
+            self.h = None

@@ -1,0 +1,97 @@
+// Device helpers shared by the gfx950 kernels: storage types, conversions, activations.
+// All code is compiled with -ffp-contract=off: every fused multiply-add below is written explicitly, so the
+// fp32 tier performs the same IEEE operations per element as the reference CPU engine
+// (engine/model/isa_impl.hpp:159-187).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace shv {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_HS = 2, ACT_HSIG = 3, ACT_SILU = 4 };
+
+template <typename T> __device__ __forceinline__ float to_f(T x) { return float(x); }
+template <typename T> __device__ __forceinline__ T from_f(float x) { return T(x); }
+
+// exp(x): Cephes expf polynomial with the reference's clamp and round-to-nearest trick (isa_impl.hpp:159-177).
+// Used wherever the reference uses its vector exp (SiLU in the GEMM epilogues, short conv, gated norm, head).
+__device__ __forceinline__ float cephes_exp(float x) {
+    x = x > -87.33654f ? x : -87.33654f;
+    x = x < 88.37626f ? x : 88.37626f;
+    const float n = __builtin_fmaf(x, 1.44269504088896341f, 12582912.0f) - 12582912.0f;
+    float r = __builtin_fmaf(n, -0.693359375f, x);
+    r = __builtin_fmaf(n, 2.12194440e-4f, r);
+    const float z = r * r;
+    float p = 1.9875691500e-4f;
+    p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+    p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+    p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+    p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+    p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+    p = __builtin_fmaf(p, z, r);
+    p = p + 1.0f;
+    const int ni = int(n);
+    return p * __int_as_float((ni + 127) << 23);
+}
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + cephes_exp(0.0f - x)); }
+__device__ __forceinline__ float clamp06(float x) {
+    float t = x + 3.0f;
+    t = t > 0.0f ? t : 0.0f;
+    return t < 6.0f ? t : 6.0f;
+}
+__device__ __forceinline__ float hswish(float x) { return (x * clamp06(x)) / 6.0f; }
+__device__ __forceinline__ float hsigmoid(float x) { return clamp06(x) / 6.0f; }
+__device__ __forceinline__ float relu(float x) { return x > 0.0f ? x : 0.0f; }
+__device__ __forceinline__ float apply_act(float v, int act) {
+    switch (act) {
+    case ACT_RELU: return relu(v);
+    case ACT_HS: return hswish(v);
+    case ACT_HSIG: return hsigmoid(v);
+    case ACT_SILU: return silu(v);
+    default: return v;
+    }
+}
+// gate nonlinearities evaluated with the device libm (the reference uses glibc expf/log1pf here)
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float logsigmoid_f(float x) { return (x < 0.0f ? x : 0.0f) - log1pf(expf(-fabsf(x))); }
+
+// 8 consecutive storage elements <-> 8 floats (16-byte access for half types, 2 x 16 bytes for float)
+template <typename T> __device__ __forceinline__ void load8(const T* p, float* v) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const T* h = reinterpret_cast<const T*>(&u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = to_f(h[i]);
+}
+template <> __device__ __forceinline__ void load8<float>(const float* p, float* v) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+template <typename T> __device__ __forceinline__ void store8(T* p, const float* v) {
+    uint4 u;
+    T* h = reinterpret_cast<T*>(&u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = from_f<T>(v[i]);
+    *reinterpret_cast<uint4*>(p) = u;
+}
+template <> __device__ __forceinline__ void store8<float>(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// Sum over 16 lanes of one 16-lane group with the fixed tree ((l_i + l_i+8) + (.. +4)) + (.. +2) + (.. +1)
+// of the reference vector code (isa_impl.hpp:45-53): every lane of the group ends with the same total.
+__device__ __forceinline__ float tree16(float v) {
+    v = v + __shfl_xor(v, 8, 16);
+    v = v + __shfl_xor(v, 4, 16);
+    v = v + __shfl_xor(v, 2, 16);
+    v = v + __shfl_xor(v, 1, 16);
+    return v;
+}
+
+}  // namespace shv

@@ -1,0 +1,632 @@
+// SHIELD-V HIP engine core.  Orchestration of the forward (the reference's engine/cuda/engine.cu:338-470 and the
+// CPU engine's isa_impl.hpp:793-851, 1071-1141 define the function), device memory, GPU weight repacking, HIP
+// graphs, per-family event timing and debug dumps.
+#include "engine.hpp"
+
+#include "dev_common.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <tuple>
+#include <type_traits>
+
+namespace shv {
+
+const char* precision_name(Precision p) {
+    switch (p) {
+    case Precision::FP32: return "fp32";
+    case Precision::BF16: return "bf16";
+    case Precision::FP16: return "fp16";
+    }
+    return "?";
+}
+bool parse_precision(const std::string& s, Precision* p) {
+    if (s == "fp32") { *p = Precision::FP32; return true; }
+    if (s == "bf16") { *p = Precision::BF16; return true; }
+    if (s == "fp16") { *p = Precision::FP16; return true; }
+    return false;
+}
+
+// batch buckets: a graph per bucket size; sizes between buckets run padded to the next one
+static std::vector<int> make_buckets(int maxv) {
+    static const int base[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256,
+                               320, 384, 448, 512, 640, 768, 896, 1024, 1280, 1536, 2048, 2560, 3072, 4096};
+    std::vector<int> b;
+    for (int v : base)
+        if (v < maxv) b.push_back(v);
+    b.push_back(maxv);
+    return b;
+}
+static int bucket_of(const std::vector<int>& b, int n) {
+    for (int v : b)
+        if (v >= n) return v;
+    throw std::runtime_error("batch larger than the configured maximum");
+}
+int Engine::frame_bucket(int F) const { return cfg_.use_graphs ? bucket_of(fbuckets_, F) : F; }
+int Engine::window_bucket(int B) const { return cfg_.use_graphs ? bucket_of(wbuckets_, B) : B; }
+
+// ------------------------------------------------------------------------------------------------ profiling
+int Engine::family_id(const char* name) {
+    for (size_t i = 0; i < fam_names_.size(); ++i)
+        if (fam_names_[i] == name) return int(i);
+    fam_names_.push_back(name);
+    fam_stats_.push_back(ProfStat{});
+    return int(fam_names_.size() - 1);
+}
+hipEvent_t Engine::take_event() {
+    if (!event_pool_.empty()) {
+        hipEvent_t e = event_pool_.back();
+        event_pool_.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    SHV_HIP_CHECK(hipEventCreate(&e));
+    return e;
+}
+void Engine::prof_flush() {
+    for (const Pending& p : pending_) {
+        SHV_HIP_CHECK(hipEventSynchronize(p.e1));
+        float ms = 0.0f;
+        SHV_HIP_CHECK(hipEventElapsedTime(&ms, p.e0, p.e1));
+        ProfStat& st = fam_stats_[size_t(p.family)];
+        st.ms += ms;
+        st.bytes += p.bytes;
+        st.launches += 1;
+        event_pool_.push_back(p.e0);
+        event_pool_.push_back(p.e1);
+    }
+    pending_.clear();
+}
+void Engine::profile_enable(bool on) {
+    prof_flush();
+    for (ProfStat& s : fam_stats_) s = ProfStat{};
+    prof_on_ = on;
+}
+bool Engine::profile_read(const std::string& family, ProfStat* out) {
+    prof_flush();
+    for (size_t i = 0; i < fam_names_.size(); ++i)
+        if (fam_names_[i] == family) {
+            *out = fam_stats_[i];
+            return true;
+        }
+    return false;
+}
+
+namespace {
+
+inline void check_launch() { SHV_HIP_CHECK(hipGetLastError()); }
+
+template <typename T> void gemm_t(const GemmArgs& p, hipStream_t s);
+template <> void gemm_t<float>(const GemmArgs& p, hipStream_t s) { gemm_f32(p, s); }
+template <> void gemm_t<f16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<f16>(p, s); }
+template <> void gemm_t<bf16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<bf16>(p, s); }
+
+// owner of device allocations
+class DevMem {
+public:
+    DevMem() = default;
+    DevMem(const DevMem&) = delete;
+    DevMem& operator=(const DevMem&) = delete;
+    ~DevMem() { release(); }
+    void release() {
+        for (void* p : ptrs_) (void)hipFree(p);
+        ptrs_.clear();
+        bytes_ = 0;
+    }
+    template <class U> U* make(size_t n) {
+        void* p = nullptr;
+        const size_t bytes = std::max<size_t>(n * sizeof(U), 256);
+        SHV_HIP_CHECK(hipMalloc(&p, bytes));
+        ptrs_.push_back(p);
+        bytes_ += bytes;
+        return static_cast<U*>(p);
+    }
+    size_t bytes() const { return bytes_; }
+
+private:
+    std::vector<void*> ptrs_;
+    size_t bytes_ = 0;
+};
+
+struct GraphKey {
+    int kind;
+    const void* in;
+    const void* out;
+    int n;
+    bool operator<(const GraphKey& o) const {
+        return std::tie(kind, in, out, n) < std::tie(o.kind, o.in, o.out, o.n);
+    }
+};
+
+double gemm_bytes(long long M, int N, int K, int ta, int tw, int tc, int tr) {
+    return double(M) * K * ta + double(N) * K * tw + double(M) * N * tc + (tr ? double(M) * N * tr : 0.0);
+}
+
+template <typename T>
+class EngineT final : public Engine {
+    static constexpr bool kF32 = std::is_same<T, float>::value;
+    static constexpr int TS = int(sizeof(T));
+
+public:
+    EngineT(const HostModel& hm, Precision p, const EngineConfig& cfg) {
+        prec_ = p;
+        cfg_ = cfg;
+        if (cfg_.max_frames < 1 || cfg_.max_windows < 1 || cfg_.slots < 1 || cfg_.slots > 4 ||
+            cfg_.max_host_tokens < 0)
+            throw std::runtime_error("invalid engine configuration");
+        fbuckets_ = make_buckets(cfg_.max_frames);
+        wbuckets_ = make_buckets(cfg_.max_windows);
+        SHV_HIP_CHECK(hipStreamCreateWithFlags(&setup_, hipStreamNonBlocking));
+        try {
+            upload_weights(hm);
+            alloc_buffers(hm);
+        } catch (...) {
+            (void)hipStreamDestroy(setup_);
+            throw;
+        }
+        SHV_HIP_CHECK(hipStreamSynchronize(setup_));
+        SHV_HIP_CHECK(hipStreamDestroy(setup_));
+        setup_ = nullptr;
+        weight_bytes_ = wmem_.bytes();
+        device_bytes_ = wmem_.bytes() + amem_.bytes();
+    }
+    ~EngineT() override {
+        for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
+        for (const Pending& p : pending_) { (void)hipEventDestroy(p.e0); (void)hipEventDestroy(p.e1); }
+        for (hipEvent_t e : event_pool_) (void)hipEventDestroy(e);
+    }
+
+    void encode_slot(int slot, int F, hipStream_t s) override {
+        if (F <= 0) return;
+        if (F > cfg_.max_frames) throw std::runtime_error("encode: too many frames");
+        const Slot& sl = slots_.at(size_t(slot));
+        const int Fb = frame_bucket(F);
+        run_graph(GraphKey{0, sl.d_frames, sl.d_tokens, Fb}, s, [&] { run_encode(sl.d_frames, Fb, sl.d_tokens, s); });
+    }
+    void classify_slot(int slot, int B, hipStream_t s) override {
+        if (B <= 0) return;
+        if (B > cfg_.max_windows) throw std::runtime_error("classify: too many windows");
+        const Slot& sl = slots_.at(size_t(slot));
+        const int Bb = window_bucket(B);
+        run_graph(GraphKey{1, sl.d_tokptr, sl.d_logits, Bb}, s, [&] { run_classify(sl.d_tokptr, Bb, sl.d_logits, s); });
+    }
+    void encode_direct(const uint8_t* d_frames, int F, float* d_tokens, hipStream_t s) override {
+        if (F <= 0) return;
+        if (F > cfg_.max_frames) throw std::runtime_error("encode: too many frames");
+        run_graph(GraphKey{2, d_frames, d_tokens, F}, s, [&] { run_encode(d_frames, F, d_tokens, s); });
+    }
+    void forward_direct(const uint8_t* d_frames, int n, float* d_logits, hipStream_t s) override {
+        if (n <= 0) return;
+        if (n > cfg_.max_windows || n * kFrames > cfg_.max_frames) throw std::runtime_error("forward: too many clips");
+        run_graph(GraphKey{3, d_frames, d_logits, n}, s, [&] {
+            run_encode(d_frames, n * kFrames, tok_direct_, s);
+            run_classify(tokptr_direct_, n, d_logits, s);
+        });
+    }
+
+private:
+    hipStream_t setup_ = nullptr;
+    DevMem wmem_, amem_, staging_;
+
+    // ---------------------------------------------------------------- weights
+    struct Blk {
+        BlockCfg cfg{};
+        int H = 0, W = 0, Ho = 0, Wo = 0, csq = 0;
+        bool has_expand = false, residual = false;
+        const T* exp_w = nullptr;
+        const float* exp_b = nullptr;
+        const float *dw_w = nullptr, *dw_b = nullptr;
+        const float *se1_w = nullptr, *se1_b = nullptr, *se2_w = nullptr, *se2_b = nullptr;
+        const T* proj_w = nullptr;
+        const float* proj_b = nullptr;
+    };
+    struct Gdn {
+        const float *norm_w, *ffn_norm_w, *conv_w, *conv_b, *neg_rate, *dt_bias, *o_norm_w;
+        const T *in_w, *out_w, *up_w, *down_w;   // up_w: SwiGLU gate/up interleaved, 1920 rows
+    };
+    const float *lut_ = nullptr, *stem_w_ = nullptr, *stem_b_ = nullptr;
+    Blk blk_[15];
+    const T* last_w_ = nullptr;
+    const float* last_b_ = nullptr;
+    const T* proj_w_ = nullptr;
+    const float *pos_ = nullptr, *readout_ = nullptr;
+    Gdn gdn_[2]{};
+    const float *s_attn_norm_ = nullptr, *s_ffn_norm_ = nullptr, *s_in_b_ = nullptr, *s_lam_ = nullptr;
+    const T* s_in_w_ = nullptr;
+    const float *s_qc_w_ = nullptr, *s_o_w_ = nullptr, *s_up_w_ = nullptr, *s_down_w_ = nullptr;
+    const float *fn_w_ = nullptr, *h_w0_ = nullptr, *h_b0_ = nullptr, *h_w2_ = nullptr;
+    float h_b2_ = 0.0f;
+
+    const float* up(const float* src, size_t n) {
+        float* d = wmem_.make<float>(n);
+        SHV_HIP_CHECK(hipMemcpy(d, src, n * sizeof(float), hipMemcpyHostToDevice));
+        return d;
+    }
+    const float* up(const std::vector<float>& v) { return up(v.data(), v.size()); }
+    // fp32 [N][K] rows -> device T (or fp32) with a row permutation, converted by the repack kernel on the GPU
+    template <typename U> const U* repack(const std::vector<float>& src, int N, int K, int perm) {
+        float* st = staging_.make<float>(src.size());
+        SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
+        U* d = wmem_.make<U>(size_t(N) * K);
+        launch_repack<U>(st, d, N, K, perm, setup_);
+        check_launch();
+        return d;
+    }
+    static std::vector<float> concat(const Linear& a, const Linear& b) {
+        std::vector<float> v(a.w);
+        v.insert(v.end(), b.w.begin(), b.w.end());
+        return v;
+    }
+
+    void upload_weights(const HostModel& hm) {
+        lut_ = up(&hm.lut[0][0], 768);
+        stem_w_ = up(hm.stem_w);
+        stem_b_ = up(hm.stem_b);
+        for (int i = 0; i < 15; ++i) {
+            const BlockHost& b = hm.blocks[i];
+            Blk& d = blk_[i];
+            d.cfg = b.cfg;
+            d.H = b.H; d.W = b.W; d.Ho = b.Ho; d.Wo = b.Wo; d.csq = b.csq;
+            d.has_expand = b.has_expand;
+            d.residual = b.residual;
+            if (b.has_expand) {
+                d.exp_w = repack<T>(b.expand.w, b.expand.N, b.expand.K, 0);
+                d.exp_b = up(b.expand.b);
+            }
+            d.dw_w = up(b.dw_w);
+            d.dw_b = up(b.dw_b);
+            if (b.cfg.se) {
+                d.se1_w = up(b.se1.w); d.se1_b = up(b.se1.b);
+                d.se2_w = up(b.se2.w); d.se2_b = up(b.se2.b);
+            }
+            d.proj_w = repack<T>(b.project.w, b.project.N, b.project.K, 0);
+            d.proj_b = up(b.project.b);
+        }
+        last_w_ = repack<T>(hm.last.w, hm.last.N, hm.last.K, 0);
+        last_b_ = up(hm.last.b);
+        proj_w_ = repack<T>(hm.proj.w, hm.proj.N, hm.proj.K, 0);
+        pos_ = up(hm.pos);
+        readout_ = up(hm.readout);
+        const int swiglu_perm = kF32 ? 1 : 2;
+        for (int g = 0; g < 2; ++g) {
+            const GdnHost& G = hm.gdn[g];
+            Gdn& d = gdn_[g];
+            d.norm_w = up(G.norm_w);
+            d.ffn_norm_w = up(G.ffn_norm_w);
+            d.conv_w = up(G.conv_w);
+            d.conv_b = up(G.conv_b);
+            d.neg_rate = up(G.neg_rate, kHeads);
+            d.dt_bias = up(G.dt_bias, kHeads);
+            d.o_norm_w = up(G.o_norm_w);
+            d.in_w = repack<T>(G.in.w, G.in.N, G.in.K, 0);
+            d.out_w = repack<T>(G.out.w, G.out.N, G.out.K, 0);
+            d.up_w = repack<T>(concat(G.gate, G.up), 2 * kFF, kD, swiglu_perm);
+            d.down_w = repack<T>(G.down.w, G.down.N, G.down.K, 0);
+        }
+        const SisaHost& S = hm.sisa;
+        s_attn_norm_ = up(S.attn_norm_w);
+        s_ffn_norm_ = up(S.ffn_norm_w);
+        s_in_w_ = repack<T>(S.in.w, S.in.N, S.in.K, 0);
+        s_in_b_ = up(S.in.b);
+        s_qc_w_ = up(concat(S.q, S.c));                      // [576][384]: W_Q rows then W_C rows
+        s_o_w_ = up(S.o.w);
+        s_up_w_ = repack<float>(concat(S.gate, S.up), 2 * kFF, kD, 1);
+        s_down_w_ = up(S.down.w);
+        s_lam_ = up(S.lam, kHeads);
+        fn_w_ = up(hm.final_norm_w);
+        h_w0_ = up(hm.head0.w);
+        h_b0_ = up(hm.head0.b);
+        h_w2_ = up(hm.head2_w);
+        h_b2_ = hm.head2_b;
+        SHV_HIP_CHECK(hipStreamSynchronize(setup_));
+        staging_.release();
+    }
+
+    // ---------------------------------------------------------------- activations
+    T *X_ = nullptr, *E_ = nullptr, *D_ = nullptr, *PO_ = nullptr;
+    float *se_pool_ = nullptr, *se_hid_ = nullptr, *se_scale_ = nullptr;
+    float *H_ = nullptr, *P_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *dec_ = nullptr, *beta_ = nullptr,
+          *O_ = nullptr;
+    T *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;
+    float *XL_ = nullptr, *QC_ = nullptr, *Y_ = nullptr, *X1_ = nullptr, *X2_ = nullptr, *HIDL_ = nullptr;
+    float* tok_direct_ = nullptr;
+    const float** tokptr_direct_ = nullptr;
+
+    void alloc_buffers(const HostModel& hm) {
+        const size_t Fm = size_t(cfg_.max_frames), Bm = size_t(cfg_.max_windows), Mm = Bm * kT;
+        size_t xe = size_t(90) * 160 * 16, ee = size_t(60) * kCnnOut, de = 0;
+        for (int i = 0; i < 15; ++i) {
+            const BlockHost& b = hm.blocks[i];
+            xe = std::max(xe, size_t(b.Ho) * b.Wo * b.cfg.cout);
+            if (b.has_expand) ee = std::max(ee, size_t(b.H) * b.W * b.cfg.cexp);
+            de = std::max(de, size_t(b.Ho) * b.Wo * b.cfg.cexp);
+        }
+        X_ = amem_.make<T>(Fm * xe);
+        E_ = amem_.make<T>(Fm * ee);
+        D_ = amem_.make<T>(Fm * de);
+        PO_ = amem_.make<T>(Fm * 16 * kCnnOut);
+        se_pool_ = amem_.make<float>(Fm * kCnnOut);
+        se_hid_ = amem_.make<float>(Fm * 256);
+        se_scale_ = amem_.make<float>(Fm * kCnnOut);
+        H_ = amem_.make<float>(Mm * kD);
+        P_ = amem_.make<float>(Mm * kGld);
+        Q_ = amem_.make<float>(Mm * kD);
+        K_ = amem_.make<float>(Mm * kD);
+        V_ = amem_.make<float>(Mm * kVD);
+        dec_ = amem_.make<float>(Mm * 8);
+        beta_ = amem_.make<float>(Mm * 8);
+        O_ = amem_.make<float>(Mm * kVD);
+        XN_ = amem_.make<T>(Mm * kD);
+        ON_ = amem_.make<T>(Mm * kVD);
+        HID_ = amem_.make<T>(Mm * kFF);
+        XL_ = amem_.make<float>(Bm * kD);
+        QC_ = amem_.make<float>(Bm * 576);
+        Y_ = amem_.make<float>(Bm * kD);
+        X1_ = amem_.make<float>(Bm * kD);
+        X2_ = amem_.make<float>(Bm * kD);
+        HIDL_ = amem_.make<float>(Bm * kFF);
+        // direct path: the engine's own token buffer and the window -> frame table of a plain predict
+        const size_t Fd = std::min(Fm, Bm * kFrames);
+        tok_direct_ = amem_.make<float>(Fd * kTokenFloats);
+        tokptr_direct_ = amem_.make<const float*>(Bm * kFrames);
+        {
+            std::vector<const float*> t(Bm * kFrames);
+            for (size_t e = 0; e < t.size(); ++e) t[e] = tok_direct_ + (e % Fd) * kTokenFloats;
+            SHV_HIP_CHECK(hipMemcpy(tokptr_direct_, t.data(), t.size() * sizeof(float*), hipMemcpyHostToDevice));
+        }
+        slots_.resize(size_t(cfg_.slots));
+        for (Slot& sl : slots_) {
+            sl.d_frames = amem_.make<uint8_t>(Fm * kFrameBytes);
+            sl.d_tokens = amem_.make<float>(Fm * kTokenFloats);
+            sl.d_tok_stage = amem_.make<float>(std::max<size_t>(size_t(cfg_.max_host_tokens), 1) * kTokenFloats);
+            sl.d_tokptr = amem_.make<const float*>(Bm * kFrames);
+            sl.d_logits = amem_.make<float>(Bm);
+            sl.d_store = amem_.make<int32_t>(Fm);
+            // every table entry starts valid: padding windows of a bucket read it
+            std::vector<const float*> init(Bm * kFrames, sl.d_tokens);
+            SHV_HIP_CHECK(hipMemcpy(sl.d_tokptr, init.data(), init.size() * sizeof(float*), hipMemcpyHostToDevice));
+            SHV_HIP_CHECK(hipMemset(sl.d_frames, 0, Fm * kFrameBytes));
+        }
+    }
+
+    // ---------------------------------------------------------------- graphs
+    std::map<GraphKey, hipGraphExec_t> graphs_;
+    template <class F> void run_graph(const GraphKey& key, hipStream_t s, F&& body) {
+        if (!cfg_.use_graphs || !dump_dir_.empty() || prof_on_) {
+            body();
+            return;
+        }
+        auto it = graphs_.find(key);
+        if (it == graphs_.end()) {
+            hipGraph_t g = nullptr;
+            SHV_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            try {
+                body();
+            } catch (...) {
+                (void)hipStreamEndCapture(s, &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            SHV_HIP_CHECK(hipStreamEndCapture(s, &g));
+            hipGraphExec_t ex = nullptr;
+            const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            SHV_HIP_CHECK(e);
+            it = graphs_.emplace(key, ex).first;
+        }
+        SHV_HIP_CHECK(hipGraphLaunch(it->second, s));
+    }
+
+    // ---------------------------------------------------------------- debug dumps (frame 0 / window 0)
+    template <typename U> void dump(const char* name, const U* dev, size_t n, hipStream_t s) {
+        if (dump_dir_.empty()) return;
+        SHV_HIP_CHECK(hipStreamSynchronize(s));
+        std::vector<U> h(n);
+        SHV_HIP_CHECK(hipMemcpy(h.data(), dev, n * sizeof(U), hipMemcpyDeviceToHost));
+        std::vector<float> f(n);
+        for (size_t i = 0; i < n; ++i) f[i] = float(h[i]);
+        std::ofstream o(dump_dir_ + "/" + name + ".f32", std::ios::binary);
+        o.write(reinterpret_cast<const char*>(f.data()), std::streamsize(n * sizeof(float)));
+    }
+
+    void gemm(const char* fam, const GemmArgs& p, hipStream_t s, bool f32 = false) {
+        const int ta = f32 ? 4 : TS, tc = p.c_f32 ? 4 : TS;
+        const int tr = p.res ? (p.r_f32 ? 4 : TS) : 0;
+        const double bytes = gemm_bytes(p.M, p.N, p.K, ta, ta, p.swiglu ? tc / 2 : tc, tr);
+        timed(fam, bytes, s, [&] {
+            if (f32) gemm_f32(p, s);
+            else gemm_t<T>(p, s);
+        });
+        check_launch();
+    }
+
+    // ---------------------------------------------------------------- CNN
+    void run_encode(const uint8_t* frames, int F, float* tokens, hipStream_t s) {
+        timed("stem", double(F) * (kFrameBytes + 90.0 * 160 * 16 * TS), s,
+              [&] { launch_stem<T>(frames, X_, lut_, stem_w_, stem_b_, F, s); });
+        check_launch();
+        dump("cnn00", X_, size_t(90) * 160 * 16, s);
+        for (int i = 0; i < 15; ++i) {
+            const Blk& b = blk_[i];
+            const long long HWi = (long long)b.H * b.W, HWo = (long long)b.Ho * b.Wo;
+            const int act = b.cfg.hs ? ACT_HS : ACT_RELU;
+            const T* dwin = X_;
+            if (b.has_expand) {
+                GemmArgs p;
+                p.M = int(F * HWi); p.N = b.cfg.cexp; p.K = b.cfg.cin;
+                p.A = X_; p.lda = b.cfg.cin; p.W = b.exp_w; p.ldw = b.cfg.cin;
+                p.bias = b.exp_b; p.act = act;
+                p.C = E_; p.ldc = b.cfg.cexp;
+                gemm("gemm_pw", p, s);
+                dwin = E_;
+            }
+            timed("dw", double(F) * (HWi + HWo) * b.cfg.cexp * TS, s, [&] {
+                launch_dw<T>(dwin, D_, b.dw_w, b.dw_b, F, b.H, b.W, b.cfg.cexp, b.cfg.k, b.cfg.stride, b.Ho, b.Wo, act, s);
+            });
+            check_launch();
+            if (b.cfg.se) {
+                timed("se_pool", double(F) * HWo * b.cfg.cexp * TS, s,
+                      [&] { launch_se_pool<T>(D_, se_pool_, F, b.Ho, b.Wo, b.cfg.cexp, s); });
+                check_launch();
+                GemmArgs p1;
+                p1.M = F; p1.N = b.csq; p1.K = b.cfg.cexp;
+                p1.A = se_pool_; p1.lda = b.cfg.cexp; p1.W = b.se1_w; p1.ldw = b.cfg.cexp;
+                p1.bias = b.se1_b; p1.act = ACT_RELU;
+                p1.C = se_hid_; p1.ldc = b.csq; p1.c_f32 = 1;
+                gemm("gemm_f32_small", p1, s, true);
+                GemmArgs p2;
+                p2.M = F; p2.N = b.cfg.cexp; p2.K = b.csq;
+                p2.A = se_hid_; p2.lda = b.csq; p2.W = b.se2_w; p2.ldw = b.csq;
+                p2.bias = b.se2_b; p2.act = ACT_HSIG;
+                p2.C = se_scale_; p2.ldc = b.cfg.cexp; p2.c_f32 = 1;
+                gemm("gemm_f32_small", p2, s, true);
+            }
+            GemmArgs p;
+            p.M = int(F * HWo); p.N = b.cfg.cout; p.K = b.cfg.cexp;
+            p.A = D_; p.lda = b.cfg.cexp; p.W = b.proj_w; p.ldw = b.cfg.cexp;
+            p.bias = b.proj_b;
+            p.C = X_; p.ldc = b.cfg.cout;
+            if (b.cfg.se) { p.scale = se_scale_; p.scale_rows = int(HWo); p.ld_scale = b.cfg.cexp; }
+            if (b.residual) { p.R = X_; p.ldr = b.cfg.cout; p.res = 1; }
+            gemm("gemm_pw", p, s);
+            if (!dump_dir_.empty()) {
+                char name[8];
+                std::snprintf(name, sizeof name, "cnn%02d", i + 1);
+                dump(name, X_, size_t(HWo) * b.cfg.cout, s);
+            }
+        }
+        {
+            GemmArgs p;
+            p.M = F * 60; p.N = kCnnOut; p.K = 160;
+            p.A = X_; p.lda = 160; p.W = last_w_; p.ldw = 160;
+            p.bias = last_b_; p.act = ACT_HS;
+            p.C = E_; p.ldc = kCnnOut;
+            gemm("gemm_pw", p, s);
+        }
+        dump("cnn16", E_, size_t(60) * kCnnOut, s);
+        timed("pool", double(F) * (60.0 + 16.0) * kCnnOut * TS, s, [&] { launch_pool<T>(E_, PO_, F, s); });
+        check_launch();
+        {
+            GemmArgs p;
+            p.M = F * 16; p.N = kD; p.K = kCnnOut;
+            p.A = PO_; p.lda = kCnnOut; p.W = proj_w_; p.ldw = kCnnOut;
+            p.C = tokens; p.ldc = kD; p.c_f32 = 1;
+            gemm("gemm_pw", p, s);
+        }
+        dump("tokens", tokens, kTokenFloats, s);
+    }
+
+    // ---------------------------------------------------------------- sequence
+    void rmsnorm_all(const float* w, hipStream_t s, int M) {
+        timed("rmsnorm", double(M) * kD * (4 + TS), s, [&] { launch_rmsnorm<T>(H_, kD, w, XN_, kD, M, s); });
+        check_launch();
+    }
+
+    void run_classify(const float* const* tokptr, int B, float* logits, hipStream_t s) {
+        const int M = B * kT;
+        timed("assemble", double(M) * kD * 8, s, [&] { launch_assemble(tokptr, pos_, readout_, H_, B, s); });
+        check_launch();
+        dump("h0", H_, size_t(kT) * kD, s);
+        for (int st = 0; st < 2; ++st) {
+            const Gdn& g = gdn_[st];
+            const int reps = st == 0 ? 1 : 2;
+            for (int r = 0; r < reps; ++r) {
+                rmsnorm_all(g.norm_w, s, M);
+                GemmArgs pi;
+                pi.M = M; pi.N = kGn; pi.K = kD;
+                pi.A = XN_; pi.lda = kD; pi.W = g.in_w; pi.ldw = kD;
+                pi.C = P_; pi.ldc = kGld; pi.c_f32 = 1;
+                gemm("gemm_seq", pi, s);
+                timed("gdn_prep", double(M) * (4.0 * 1548 * 4 + 4.0 * (2 * kD + kVD + 16)), s, [&] {
+                    launch_gdn_prep(P_, g.conv_w, g.conv_b, g.neg_rate, g.dt_bias, Q_, K_, V_, dec_, beta_, B, s);
+                });
+                check_launch();
+                timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s,
+                      [&] { launch_delta(Q_, K_, V_, dec_, beta_, O_, B, s); });
+                check_launch();
+                timed("gated_norm", double(M) * (4.0 * 2 * kVD + TS * kVD), s,
+                      [&] { launch_gated_norm<T>(O_, P_, g.o_norm_w, ON_, M, s); });
+                check_launch();
+                GemmArgs po;
+                po.M = M; po.N = kD; po.K = kVD;
+                po.A = ON_; po.lda = kVD; po.W = g.out_w; po.ldw = kVD;
+                po.C = H_; po.ldc = kD; po.c_f32 = 1;
+                po.R = H_; po.ldr = kD; po.r_f32 = 1; po.res = reps == 2 ? 2 : 1;
+                gemm("gemm_seq", po, s);
+            }
+            rmsnorm_all(g.ffn_norm_w, s, M);
+            GemmArgs pu;
+            pu.M = M; pu.N = 2 * kFF; pu.K = kD;
+            pu.A = XN_; pu.lda = kD; pu.W = g.up_w; pu.ldw = kD;
+            pu.C = HID_; pu.ldc = kFF; pu.swiglu = 1;
+            gemm("gemm_seq", pu, s);
+            GemmArgs pd;
+            pd.M = M; pd.N = kD; pd.K = kFF;
+            pd.A = HID_; pd.lda = kFF; pd.W = g.down_w; pd.ldw = kFF;
+            pd.C = H_; pd.ldc = kD; pd.c_f32 = 1;
+            pd.R = H_; pd.ldr = kD; pd.r_f32 = 1; pd.res = 1;
+            gemm("gemm_seq", pd, s);
+            dump(st == 0 ? "after_gdn_a" : "after_gdn_b", H_, size_t(kT) * kD, s);
+        }
+        // SISA block, last row only: all-row K/V/B/theta/alpha/forget projection, last-row Q|C in fp32
+        rmsnorm_all(s_attn_norm_, s, M);
+        GemmArgs pa;
+        pa.M = M; pa.N = kSn; pa.K = kD;
+        pa.A = XN_; pa.lda = kD; pa.W = s_in_w_; pa.ldw = kD;
+        pa.bias = s_in_b_;
+        pa.C = P_; pa.ldc = kSld; pa.c_f32 = 1;
+        gemm("gemm_seq", pa, s);
+        const float* hlast = H_ + size_t(kT - 1) * kD;
+        const long long ldlast = (long long)kT * kD;
+        timed("rmsnorm", double(B) * kD * 8, s,
+              [&] { launch_rmsnorm<float>(hlast, ldlast, s_attn_norm_, XL_, kD, B, s); });
+        check_launch();
+        GemmArgs pq;
+        pq.M = B; pq.N = 576; pq.K = kD;
+        pq.A = XL_; pq.lda = kD; pq.W = s_qc_w_; pq.ldw = kD;
+        pq.C = QC_; pq.ldc = 576; pq.c_f32 = 1;
+        gemm("gemm_f32_small", pq, s, true);
+        timed("sisa", double(B) * kT * kSn * 4, s, [&] { launch_sisa(P_, QC_, s_lam_, Y_, B, s); });
+        check_launch();
+        GemmArgs pw;
+        pw.M = B; pw.N = kD; pw.K = kD;
+        pw.A = Y_; pw.lda = kD; pw.W = s_o_w_; pw.ldw = kD;
+        pw.C = X1_; pw.ldc = kD; pw.c_f32 = 1;
+        pw.R = hlast; pw.ldr = ldlast; pw.r_f32 = 1; pw.res = 1;
+        gemm("gemm_f32_small", pw, s, true);
+        timed("rmsnorm", double(B) * kD * 8, s, [&] { launch_rmsnorm<float>(X1_, kD, s_ffn_norm_, XL_, kD, B, s); });
+        check_launch();
+        GemmArgs pu;
+        pu.M = B; pu.N = 2 * kFF; pu.K = kD;
+        pu.A = XL_; pu.lda = kD; pu.W = s_up_w_; pu.ldw = kD;
+        pu.C = HIDL_; pu.ldc = kFF; pu.c_f32 = 1; pu.swiglu = 1;
+        gemm("gemm_f32_small", pu, s, true);
+        GemmArgs pd;
+        pd.M = B; pd.N = kD; pd.K = kFF;
+        pd.A = HIDL_; pd.lda = kFF; pd.W = s_down_w_; pd.ldw = kFF;
+        pd.C = X2_; pd.ldc = kD; pd.c_f32 = 1;
+        pd.R = X1_; pd.ldr = kD; pd.r_f32 = 1; pd.res = 1;
+        gemm("gemm_f32_small", pd, s, true);
+        dump("after_sisa_last", X2_, kD, s);
+        timed("head", double(B) * kD * 4, s, [&] { launch_head(X2_, fn_w_, h_w0_, h_b0_, h_w2_, h_b2_, logits, B, s); });
+        check_launch();
+        dump("logit", logits, 1, s);
+    }
+};
+
+}  // namespace
+
+std::unique_ptr<Engine> make_engine(const HostModel& hm, Precision p, const EngineConfig& cfg) {
+    switch (p) {
+    case Precision::FP32: return std::unique_ptr<Engine>(new EngineT<float>(hm, p, cfg));
+    case Precision::BF16: return std::unique_ptr<Engine>(new EngineT<bf16>(hm, p, cfg));
+    case Precision::FP16: return std::unique_ptr<Engine>(new EngineT<f16>(hm, p, cfg));
+    }
+    throw std::runtime_error("unknown precision");
+}
+
+}  // namespace shv

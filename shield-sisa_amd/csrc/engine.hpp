@@ -1,0 +1,108 @@
+// SHIELD-V HIP engine core: device weights (repacked on the GPU), activation buffers, the encode / classify
+// forward passes and their HIP graphs.  One thread drives an Engine (the API worker, or a benchmark).
+#pragma once
+#include "host_model.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#define SHV_HIP_CHECK(expr)                                                                                 \
+    do {                                                                                                    \
+        const hipError_t err__ = (expr);                                                                    \
+        if (err__ != hipSuccess)                                                                            \
+            throw std::runtime_error(std::string("HIP error ") + hipGetErrorString(err__) + " at " +        \
+                                     __FILE__ + ":" + std::to_string(__LINE__) + ": " #expr);               \
+    } while (0)
+
+namespace shv {
+
+enum class Precision { FP32 = 0, BF16 = 1, FP16 = 2 };
+const char* precision_name(Precision p);
+bool parse_precision(const std::string& s, Precision* p);
+
+struct EngineConfig {
+    int max_frames = 640;       // frames per encode launch
+    int max_windows = 512;      // windows per classify launch
+    int max_host_tokens = 2048; // host token blocks staged per batch
+    bool use_graphs = true;     // one HIP graph per (kind, buffers, bucket)
+    int slots = 2;              // input/output buffer sets for the scheduler's pipelining
+};
+
+// Per-family kernel timing (HIP events on the launching stream) and algorithmic bytes.
+struct ProfStat {
+    double ms = 0.0, bytes = 0.0;
+    long long launches = 0;
+};
+
+class Engine {
+public:
+    struct Slot {
+        uint8_t* d_frames = nullptr;      // [max_frames][172800]
+        float* d_tokens = nullptr;        // [max_frames][6144]
+        float* d_tok_stage = nullptr;     // [max(max_host_tokens,1)][6144]
+        const float** d_tokptr = nullptr; // [max_windows * 20]
+        float* d_logits = nullptr;        // [max_windows]
+        int32_t* d_store = nullptr;       // [max_frames]
+    };
+    virtual ~Engine() = default;
+
+    Precision precision() const { return prec_; }
+    const EngineConfig& config() const { return cfg_; }
+    const Slot& slot(int i) const { return slots_.at(size_t(i)); }
+    // Slot path (scheduler): frames of slot -> its tokens; windows through its pointer table -> its logits.
+    // F / B are padded to a bucket when graphs are on (padding rows are computed and ignored).
+    virtual void encode_slot(int slot, int F, hipStream_t s) = 0;
+    virtual void classify_slot(int slot, int B, hipStream_t s) = 0;
+    // Direct path on caller device buffers (no padding): frames [F] -> tokens [F][6144]
+    virtual void encode_direct(const uint8_t* d_frames, int F, float* d_tokens, hipStream_t s) = 0;
+    // clips [n][20] frames -> logits [n], through the engine's own token buffer
+    virtual void forward_direct(const uint8_t* d_frames, int n, float* d_logits, hipStream_t s) = 0;
+
+    size_t weight_bytes() const { return weight_bytes_; }
+    size_t device_bytes() const { return device_bytes_; }
+    int frame_bucket(int F) const;
+    int window_bucket(int B) const;
+
+    void set_dump_dir(const std::string& d) { dump_dir_ = d; }
+    void profile_enable(bool on);
+    // flushes pending events; false if the family is unknown
+    bool profile_read(const std::string& family, ProfStat* out);
+
+protected:
+    Precision prec_ = Precision::FP32;
+    EngineConfig cfg_;
+    std::vector<Slot> slots_;
+    std::vector<int> fbuckets_, wbuckets_;
+    size_t weight_bytes_ = 0, device_bytes_ = 0;
+    std::string dump_dir_;
+
+    struct Pending {
+        int family;
+        double bytes;
+        hipEvent_t e0, e1;
+    };
+    bool prof_on_ = false;
+    std::vector<std::string> fam_names_;
+    std::vector<ProfStat> fam_stats_;
+    std::vector<Pending> pending_;
+    std::vector<hipEvent_t> event_pool_;
+    int family_id(const char* name);
+    hipEvent_t take_event();
+    void prof_flush();
+    template <class F> void timed(const char* family, double bytes, hipStream_t s, F&& launch) {
+        if (!prof_on_) { launch(); return; }
+        Pending p{family_id(family), bytes, take_event(), take_event()};
+        SHV_HIP_CHECK(hipEventRecord(p.e0, s));
+        launch();
+        SHV_HIP_CHECK(hipEventRecord(p.e1, s));
+        pending_.push_back(p);
+    }
+};
+
+std::unique_ptr<Engine> make_engine(const HostModel& hm, Precision p, const EngineConfig& cfg);
+
+}  // namespace shv

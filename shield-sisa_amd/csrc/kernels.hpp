@@ -1,0 +1,72 @@
+// Launchers of the gfx950 kernels (host-callable).  Storage type T is float (fp32 tier), f16 or bf16.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace shv {
+
+// C[m][n] = epilogue(sum_k A[m][k] * W[n][k]); W row-major [N][K] (PyTorch Linear / 1x1 conv layout).
+// Epilogue, per element in this order: + bias[n]; activation; residual (res 1: + R[m][n], res 2: + (v / sqrt2)
+// with R added first: R + v / 1.41421356f); stored as T or fp32.  swiglu: fp32 tier -- W rows (2j, 2j+1) =
+// (gate_j, up_j); MFMA tier -- W rows in 16-row panels (gate panel, up panel, ...); out[m][j] = silu(gate) * up.
+// Optional SE prologue: A[m][k] *= scale[(m / scale_rows) * ld_scale + k].
+struct GemmArgs {
+    int M = 0, N = 0, K = 0;
+    const void* A = nullptr; long long lda = 0;
+    const void* W = nullptr; long long ldw = 0;
+    const float* scale = nullptr; int scale_rows = 1; int ld_scale = 0;
+    const float* bias = nullptr; int act = 0;
+    void* C = nullptr; long long ldc = 0; int c_f32 = 0;
+    const void* R = nullptr; long long ldr = 0; int r_f32 = 0; int res = 0;
+    int swiglu = 0;
+};
+
+// fp32 tier: VALU GEMM, each output accumulated in K blocks of 64 (fma chain from +0 per block, block sums added
+// in order) exactly as the reference CPU engine (engine/model/isa_impl.hpp:188-317).  A, W, C, R all fp32.
+void gemm_f32(const GemmArgs& p, hipStream_t s);
+// bf16 / fp16 tier: MFMA 16x16x32 with fp32 accumulation, K consumed in 32-wide steps in increasing order
+// (no split-K): a row's outputs do not depend on M, the tile, or other rows.  A, W in T; C, R in T or fp32.
+template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
+
+// ---------------------------------------------------------------- CNN (NHWC)
+// uint8 [F][180][320][3] -> T [F][90][160][16]; lut [3][256], w [27][16] (tap (dy,dx,c) major), b [16]
+template <typename T>
+void launch_stem(const uint8_t* in, T* out, const float* lut, const float* w, const float* b, int F, hipStream_t s);
+// depthwise KxK stride S pad (K-1)/2 + bias + act; w [K*K][C], C % 8 == 0
+template <typename T>
+void launch_dw(const T* in, T* out, const float* w, const float* b, int F, int H, int W, int C, int K, int S, int Ho,
+               int Wo, int act, hipStream_t s);
+// SE squeeze: pooled[f][c] = mean over the map (row sums left to right, rows in order, / (float)HW)
+template <typename T> void launch_se_pool(const T* x, float* pooled, int F, int Ho, int Wo, int C, hipStream_t s);
+// 4x4 adaptive average pool of [F][6][10][960] -> [F][16][960]
+template <typename T> void launch_pool(const T* in, T* out, int F, hipStream_t s);
+// weight repack on the GPU: dst[r][k] = T(src[perm(r)][k]); perm 0 identity, 1 SwiGLU pair interleave
+// (rows 2j, 2j+1 <- gate j, up j of src = [gate; up]), 2 SwiGLU 16-row panel interleave
+template <typename T> void launch_repack(const float* src, T* dst, int N, int K, int perm, hipStream_t s);
+
+// ---------------------------------------------------------------- sequence (fp32 residual stream)
+void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,
+                     hipStream_t s);
+// out[r] = (x[r] * (1 / sqrt(sum(x^2) / 384 + 1e-6))) * w with the reference's 16-lane sum tree
+template <typename T>
+void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s);
+// short conv4 + SiLU on q|k|v, per-head L2 norm (q * 0.125), decay = exp(neg_rate * softplus(a + dt_bias)),
+// beta = sigmoid(b).  P [rows][2320] -> Q, K [rows][384], V [rows][768], dec, beta [rows][8]
+void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
+                     const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
+                     hipStream_t s);
+// gated delta rule, sequential over 321 tokens from zero state, fp32; O [rows][768]
+void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
+                  int B, hipStream_t s);
+// ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768]
+template <typename T>
+void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s);
+// SISA last-row attention per (window, head): S [rows][1072] (B rotated in place), QC [B][576] -> Y [B][384]
+void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s);
+// final RMSNorm + Linear(384,128) + SiLU + Linear(128,1); w0 [128][384]
+void launch_head(const float* X, const float* norm_w, const float* w0, const float* b0, const float* w2, float b2,
+                 float* logits, int B, hipStream_t s);
+// pool[slots[f]] = tokens[f] for slots[f] >= 0
+void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool, int F, hipStream_t s);
+
+}  // namespace shv

@@ -1,0 +1,382 @@
+// Sequence-stage kernels (GDN-A, GDN-B, SISA last row, head).  Residual stream and all non-GEMM arithmetic in
+// fp32, SISA prefix sums in double.  Reductions reproduce the reference CPU engine's order: 16 lane partial sums
+// (element i into lane i % 16, first product unfused, then fmas) and the fixed 16-lane tree
+// (engine/model/isa_impl.hpp:45-53, 854-863, 866-962, 996-1069, 1127-1133).
+#include "dev_common.hpp"
+#include "host_model.hpp"
+#include "kernels.hpp"
+
+namespace shv {
+namespace {
+
+inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
+
+// ------------------------------------------------------------------------------------------------ assemble
+// h[b*321 + t] = tokens(b, t / 16)[t % 16] + pos[t] (t < 320); readout at t = 320.  One block per row, float4.
+__global__ void __launch_bounds__(96)
+assemble_kernel(const float* const* __restrict__ tok_ptrs, const float* __restrict__ pos,
+                const float* __restrict__ readout, float* __restrict__ h) {
+    const long long row = blockIdx.x;
+    const int b = int(row / kT), t = int(row % kT), j = threadIdx.x * 4;
+    float4 v;
+    if (t == kT - 1) {
+        v = *reinterpret_cast<const float4*>(readout + j);
+    } else {
+        const float4 a = *reinterpret_cast<const float4*>(tok_ptrs[b * kFrames + t / 16] + (t % 16) * kD + j);
+        const float4 p = *reinterpret_cast<const float4*>(pos + t * kD + j);
+        v = make_float4(a.x + p.x, a.y + p.y, a.z + p.z, a.w + p.w);
+    }
+    *reinterpret_cast<float4*>(h + row * kD + j) = v;
+}
+
+// ------------------------------------------------------------------------------------------------ RMSNorm
+// 16 lanes per row (4 rows per wave): lane l accumulates x[l + 16 i]^2, tree16, then (x * inv) * w
+template <typename T>
+__global__ void __launch_bounds__(256)
+rmsnorm_kernel(const float* __restrict__ x, long long ldx, const float* __restrict__ w, T* __restrict__ out,
+               long long ldo, int rows) {
+    const long long row = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    const int l = threadIdx.x & 15;
+    const bool live = row < rows;
+    const float* xr = x + (live ? row : 0) * ldx;
+    float v[24];
+#pragma unroll
+    for (int i = 0; i < 24; ++i) v[i] = xr[i * 16 + l];
+    float acc = v[0] * v[0];
+#pragma unroll
+    for (int i = 1; i < 24; ++i) acc = __builtin_fmaf(v[i], v[i], acc);
+    const float s = tree16(acc);
+    if (!live) return;
+    const float inv = 1.0f / sqrtf(s / 384.0f + 1e-6f);
+    T* o = out + row * ldo;
+#pragma unroll
+    for (int i = 0; i < 24; ++i) o[i * 16 + l] = from_f<T>((v[i] * inv) * w[i * 16 + l]);
+}
+
+// ------------------------------------------------------------------------------------------------ GDN prep
+// One block per row, wave h = head h.  Lane l: q channel h*64+l, k channel h*64+l, v channels h*128+l (+64).
+// Short conv: acc from +0, taps t-3..t in order, + bias, SiLU (isa_impl.hpp:871-889).  L2 norms with the
+// 16-lane structure over 64 elements (isa_impl.hpp:893-906).  Gates with device libm (expf, log1pf).
+__global__ void __launch_bounds__(384)
+gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const float* __restrict__ cb,
+                const float* __restrict__ neg_rate, const float* __restrict__ dt_bias, float* __restrict__ Q,
+                float* __restrict__ K, float* __restrict__ V, float* __restrict__ dec, float* __restrict__ beta) {
+    const long long row = blockIdx.x;
+    const int t = int(row % kT), h = threadIdx.x >> 6, l = threadIdx.x & 63;
+    auto conv = [&](int col, int wc) {
+        float acc = 0.0f;
+        if (t >= 3) acc = __builtin_fmaf(P[(row - 3) * kGld + col], cw[0 * 1536 + wc], acc);
+        if (t >= 2) acc = __builtin_fmaf(P[(row - 2) * kGld + col], cw[1 * 1536 + wc], acc);
+        if (t >= 1) acc = __builtin_fmaf(P[(row - 1) * kGld + col], cw[2 * 1536 + wc], acc);
+        acc = __builtin_fmaf(P[row * kGld + col], cw[3 * 1536 + wc], acc);
+        return silu(acc + cb[wc]);
+    };
+    const float q = conv(kGq + h * 64 + l, h * 64 + l);
+    const float k = conv(kGk + h * 64 + l, 384 + h * 64 + l);
+    V[row * kVD + h * 128 + l] = conv(kGv + h * 128 + l, 768 + h * 128 + l);
+    V[row * kVD + h * 128 + 64 + l] = conv(kGv + h * 128 + 64 + l, 768 + h * 128 + 64 + l);
+    // lanes 0..15 gather elements l, l+16, l+32, l+48
+    float aq = q * q, ak = k * k;
+#pragma unroll
+    for (int s = 1; s < 4; ++s) {
+        const float qs = __shfl(q, l + 16 * s), ks = __shfl(k, l + 16 * s);
+        aq = __builtin_fmaf(qs, qs, aq);
+        ak = __builtin_fmaf(ks, ks, ak);
+    }
+    aq = tree16(aq);
+    ak = tree16(ak);
+    aq = __shfl(aq, 0);
+    ak = __shfl(ak, 0);
+    const float iq = 1.0f / sqrtf(aq + 1e-6f), ik = 1.0f / sqrtf(ak + 1e-6f);
+    Q[row * kD + h * 64 + l] = (q * iq) * 0.125f;
+    K[row * kD + h * 64 + l] = k * ik;
+    if (l == 0) {
+        const float* p = P + row * kGld;
+        dec[row * 8 + h] = expf(neg_rate[h] * softplus_f(p[kGa + h] + dt_bias[h]));
+        beta[row * 8 + h] = 1.0f / (1.0f + expf(-p[kGb + h]));
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ delta rule
+// One block per (window, head), one thread per value column c (128).  The thread keeps S[0..63][c] in registers.
+// Per token (isa_impl.hpp:911-947): u = (v - a * pred) * beta; S[j] = fma(k_j, u, S[j] * a); o = fma chain over j
+// of S[j] * q_j; pred = fma chain over j of S[j] * k_{t+1, j}.  q and k of 32-token chunks are staged in LDS and
+// read as broadcasts.
+constexpr int DCH = 32;
+__global__ void __launch_bounds__(128)
+delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+             const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ O) {
+    const int b = blockIdx.x / kHeads, h = blockIdx.x % kHeads, c = threadIdx.x;
+    __shared__ float sq[DCH][64];
+    __shared__ float sk[DCH + 1][64];
+    __shared__ float sa[DCH], sb[DCH];
+    const long long row0 = (long long)b * kT;
+    float S[64];
+#pragma unroll
+    for (int j = 0; j < 64; ++j) S[j] = 0.0f;
+    float pred = 0.0f;
+    for (int t0 = 0; t0 < kT; t0 += DCH) {
+        const int nt = min(DCH, kT - t0);
+        for (int i = threadIdx.x; i < (DCH + 1) * 64; i += 128) {
+            const int tt = i >> 6, j = i & 63, t = t0 + tt;
+            if (tt < DCH) sq[tt][j] = t < kT ? Q[(row0 + t) * kD + h * 64 + j] : 0.0f;
+            // k of token t (t < kT); for the last token, the next-k slot repeats its own k (unused downstream)
+            const int tk = t < kT ? t : kT - 1;
+            sk[tt][j] = K[(row0 + tk) * kD + h * 64 + j];
+        }
+        if (threadIdx.x < DCH) {
+            const int t = t0 + threadIdx.x;
+            sa[threadIdx.x] = t < kT ? dec[(row0 + t) * 8 + h] : 0.0f;
+            sb[threadIdx.x] = t < kT ? beta[(row0 + t) * 8 + h] : 0.0f;
+        }
+        __syncthreads();
+        for (int i = 0; i < nt; ++i) {
+            const long long row = row0 + t0 + i;
+            const float a = sa[i], bt = sb[i];
+            const float v = V[row * kVD + h * 128 + c];
+            const float u = (v - a * pred) * bt;
+            float o = 0.0f, pn = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 64; ++j) {
+                const float x = __builtin_fmaf(sk[i][j], u, S[j] * a);
+                S[j] = x;
+                o = __builtin_fmaf(x, sq[i][j], o);
+                pn = __builtin_fmaf(x, sk[i + 1][j], pn);
+            }
+            pred = pn;
+            O[row * kVD + h * 128 + c] = o;
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ gated norm
+// 16 lanes per (row, head): lane l accumulates o[l + 16 z]^2 (z = 0..7), tree16, then ((o * rstd) * w) * silu(g)
+template <typename T>
+__global__ void __launch_bounds__(256)
+gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, const float* __restrict__ w,
+                  T* __restrict__ out, int rows) {
+    const long long grp = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    const int l = threadIdx.x & 15;
+    const bool live = grp < (long long)rows * kHeads;
+    const long long row = live ? grp / kHeads : 0;
+    const int h = int(grp % kHeads);
+    const float* o = O + row * kVD + h * 128;
+    float v[8];
+#pragma unroll
+    for (int z = 0; z < 8; ++z) v[z] = o[z * 16 + l];
+    float acc = v[0] * v[0];
+#pragma unroll
+    for (int z = 1; z < 8; ++z) acc = __builtin_fmaf(v[z], v[z], acc);
+    const float s = tree16(acc);
+    if (!live) return;
+    const float rstd = 1.0f / sqrtf(s / 128.0f + 1e-6f);
+    const float* g = P + row * kGld + kGg + h * 128;
+    T* dst = out + row * kVD + h * 128;
+#pragma unroll
+    for (int z = 0; z < 8; ++z) {
+        const int i = z * 16 + l;
+        dst[i] = from_f<T>(((v[z] * rstd) * w[i]) * silu(g[i]));
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ SISA
+// One block per (window, head), 256 threads (isa_impl.hpp:996-1069).
+// 1. per token: -softplus(alpha), logsigmoid(forget), theta (device libm)
+// 2. prefix sums in double, one thread per series, rounded to float per element
+// 3. rotate c (last token's angles) and each b_t; scores with the 16-lane dot structure
+// 4. softmax: max, expf, sum in double in token order (one thread); y_j = sum over 64-token blocks of fma chains
+constexpr int SA_THREADS = 256;
+__global__ void __launch_bounds__(SA_THREADS)
+sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __restrict__ lam_h,
+            float* __restrict__ Y) {
+    const int b = blockIdx.x / kHeads, h = blockIdx.x % kHeads, tid = threadIdx.x;
+    float* S0 = S + (long long)b * kT * kSld;
+    __shared__ float gt[kT], ft[kT], sco[kT];
+    __shared__ float phi[kT][kPairs + 1];
+    __shared__ float sq[64], crot[32];
+    __shared__ float s_inv;
+    for (int t = tid; t < kT; t += SA_THREADS) {
+        const float* row = S0 + (long long)t * kSld;
+        gt[t] = -softplus_f(row[kSal + h]);
+        ft[t] = logsigmoid_f(row[kSfg + h]);
+#pragma unroll
+        for (int p = 0; p < kPairs; ++p) phi[t][p] = row[kSth + h * kPairs + p];
+    }
+    if (tid < 64) sq[tid] = QC[(long long)b * 576 + h * 64 + tid];
+    __syncthreads();
+    if (tid < 2 + kPairs) {
+        double acc = 0.0;
+        float* series = tid == 0 ? gt : tid == 1 ? ft : nullptr;
+        for (int t = 0; t < kT; ++t) {
+            if (series) {
+                acc += double(series[t]);
+                series[t] = float(acc);
+            } else {
+                acc += double(phi[t][tid - 2]);
+                phi[t][tid - 2] = float(acc);
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < kPairs) {
+        float sn, cs;
+        sincosf(phi[kT - 1][tid], &sn, &cs);
+        const float* c = QC + (long long)b * 576 + 384 + h * 32;
+        const float ce = c[2 * tid], co = c[2 * tid + 1];
+        crot[2 * tid] = ce * cs - co * sn;
+        crot[2 * tid + 1] = ce * sn + co * cs;
+    }
+    __syncthreads();
+    const float lam = lam_h[h], gl = gt[kT - 1], fl = ft[kT - 1];
+    for (int t = tid; t < kT; t += SA_THREADS) {
+        const float* row = S0 + (long long)t * kSld;
+        const float* k = row + kSk + h * 64;
+        const float* bb = row + kSb + h * 32;
+        float br[32];
+#pragma unroll
+        for (int p = 0; p < kPairs; ++p) {
+            float sn, cs;
+            sincosf(phi[t][p], &sn, &cs);
+            const float e = bb[2 * p], o = bb[2 * p + 1];
+            br[2 * p] = e * cs - o * sn;
+            br[2 * p + 1] = e * sn + o * cs;
+        }
+        float la[16], ls[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            la[i] = sq[i] * k[i];
+            la[i] = __builtin_fmaf(sq[16 + i], k[16 + i], la[i]);
+            la[i] = __builtin_fmaf(sq[32 + i], k[32 + i], la[i]);
+            la[i] = __builtin_fmaf(sq[48 + i], k[48 + i], la[i]);
+            ls[i] = crot[i] * br[i];
+            ls[i] = __builtin_fmaf(crot[16 + i], br[16 + i], ls[i]);
+        }
+        float a8[8], s8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { a8[i] = la[i] + la[i + 8]; s8[i] = ls[i] + ls[i + 8]; }
+        const float content = ((a8[0] + a8[4]) + (a8[2] + a8[6])) + ((a8[1] + a8[5]) + (a8[3] + a8[7]));
+        const float ssm = ((s8[0] + s8[4]) + (s8[2] + s8[6])) + ((s8[1] + s8[5]) + (s8[3] + s8[7]));
+        float score = content * 0.125f;
+        score = score + (lam * expf(gl - gt[t])) * ssm;
+        score = score + (fl - ft[t]);
+        sco[t] = score;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float mx = -INFINITY;
+        for (int t = 0; t < kT; ++t) mx = sco[t] > mx ? sco[t] : mx;
+        double sum = 0.0;
+        for (int t = 0; t < kT; ++t) {
+            const float e = expf(sco[t] - mx);
+            sco[t] = e;
+            sum += double(e);
+        }
+        s_inv = 1.0f / float(sum);
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const float inv = s_inv;
+        float tot = 0.0f;
+        for (int t0 = 0; t0 < kT; t0 += 64) {
+            float blk = 0.0f;
+            const int t1 = min(kT, t0 + 64);
+            for (int t = t0; t < t1; ++t)
+                blk = __builtin_fmaf(sco[t] * inv, S0[(long long)t * kSld + kSv + h * 64 + tid], blk);
+            tot = t0 == 0 ? blk : tot + blk;
+        }
+        Y[(long long)b * kD + h * 64 + tid] = tot;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ head
+// final RMSNorm (16-lane tree), Linear(384,128) as K blocks of 64 (one thread per output), SiLU, then the
+// 128-long dot with the 16-lane structure + bias.  w0 row-major [128][384].
+__global__ void __launch_bounds__(128)
+head_kernel(const float* __restrict__ X, const float* __restrict__ nw, const float* __restrict__ w0,
+            const float* __restrict__ b0, const float* __restrict__ w2, float b2, float* __restrict__ logits) {
+    const int b = blockIdx.x, tid = threadIdx.x;
+    __shared__ float xn[kD];
+    __shared__ float hid[128];
+    const float* x = X + (long long)b * kD;
+    if (tid < 16) {
+        float acc = x[tid] * x[tid];
+        for (int i = 1; i < 24; ++i) acc = __builtin_fmaf(x[i * 16 + tid], x[i * 16 + tid], acc);
+        const float s = tree16(acc);
+        const float inv = 1.0f / sqrtf(s / 384.0f + 1e-6f);
+        for (int i = 0; i < 24; ++i) xn[i * 16 + tid] = (x[i * 16 + tid] * inv) * nw[i * 16 + tid];
+    }
+    __syncthreads();
+    {
+        const float* wr = w0 + (long long)tid * kD;
+        float tot = 0.0f;
+        for (int k0 = 0; k0 < kD; k0 += 64) {
+            float blk = 0.0f;
+            for (int k = k0; k < k0 + 64; ++k) blk = __builtin_fmaf(xn[k], wr[k], blk);
+            tot = k0 == 0 ? blk : tot + blk;
+        }
+        hid[tid] = silu(tot + b0[tid]);
+    }
+    __syncthreads();
+    if (tid < 16) {
+        float acc = hid[tid] * w2[tid];
+        for (int i = 1; i < 8; ++i) acc = __builtin_fmaf(hid[i * 16 + tid], w2[i * 16 + tid], acc);
+        const float s = tree16(acc);
+        if (tid == 0) logits[b] = s + b2;
+    }
+}
+
+__global__ void __launch_bounds__(256)
+store_tokens_kernel(const float* __restrict__ src, const int32_t* __restrict__ slots, float* __restrict__ pool) {
+    const int f = blockIdx.x, s = slots[f];
+    if (s < 0) return;
+    const float4* a = reinterpret_cast<const float4*>(src + (long long)f * kTokenFloats);
+    float4* d = reinterpret_cast<float4*>(pool + (long long)s * kTokenFloats);
+    for (int i = threadIdx.x; i < int(kTokenFloats / 4); i += blockDim.x) d[i] = a[i];
+}
+
+}  // namespace
+
+void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,
+                     hipStream_t s) {
+    hipLaunchKernelGGL(assemble_kernel, dim3(B * kT), dim3(96), 0, s, tok_ptrs, pos, readout, h);
+}
+template <typename T>
+void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s) {
+    hipLaunchKernelGGL(rmsnorm_kernel<T>, dim3(cdiv((long long)rows * 16, 256)), dim3(256), 0, s, x, ldx, w, out, ldo,
+                       rows);
+}
+void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
+                     const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
+                     hipStream_t s) {
+    hipLaunchKernelGGL(gdn_prep_kernel, dim3(B * kT), dim3(384), 0, s, P, conv_w, conv_b, neg_rate, dt_bias, Q, K, V,
+                       dec, beta);
+}
+void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
+                  int B, hipStream_t s) {
+    hipLaunchKernelGGL(delta_kernel, dim3(B * kHeads), dim3(128), 0, s, Q, K, V, dec, beta, O);
+}
+template <typename T>
+void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s) {
+    hipLaunchKernelGGL(gated_norm_kernel<T>, dim3(cdiv((long long)rows * kHeads * 16, 256)), dim3(256), 0, s, O, P, w,
+                       out, rows);
+}
+void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s) {
+    hipLaunchKernelGGL(sisa_kernel, dim3(B * kHeads), dim3(SA_THREADS), 0, s, S, QC, lam, Y);
+}
+void launch_head(const float* X, const float* norm_w, const float* w0, const float* b0, const float* w2, float b2,
+                 float* logits, int B, hipStream_t s) {
+    hipLaunchKernelGGL(head_kernel, dim3(B), dim3(128), 0, s, X, norm_w, w0, b0, w2, b2, logits);
+}
+void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool, int F, hipStream_t s) {
+    hipLaunchKernelGGL(store_tokens_kernel, dim3(F), dim3(256), 0, s, tokens, slots, pool);
+}
+
+#define SHV_INST_SEQ(T)                                                                                      \
+    template void launch_rmsnorm<T>(const float*, long long, const float*, T*, long long, int, hipStream_t); \
+    template void launch_gated_norm<T>(const float*, const float*, const float*, T*, int, hipStream_t);
+SHV_INST_SEQ(float)
+SHV_INST_SEQ(f16)
+SHV_INST_SEQ(bf16)
+
+}  // namespace shv

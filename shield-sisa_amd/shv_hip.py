@@ -1,0 +1,321 @@
+"""ctypes binding of libshield_v_hip.so (include/shv_hip.h) and of the synthetic-input library.
+
+This is the Python-side mirror of the reference engine's C API (engine/include/shv_cuda.h): the same calls,
+argument meaning and error behaviour (-1 / NULL plus a thread-local error string, NaN outputs on failure).
+The product is the C-ABI library; this module only marshals numpy buffers.  It refuses to run when the HIP
+library is missing -- there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_DIR = PKG / "lib"
+FRAME_BYTES = 172800
+TOKEN_FLOATS = 6144
+WINDOW_FRAMES = 20
+
+
+class ShvError(RuntimeError):
+    pass
+
+
+class Options(ctypes.Structure):
+    _fields_ = [("max_frames", ctypes.c_int), ("max_windows", ctypes.c_int), ("max_host_tokens", ctypes.c_int),
+                ("token_slots", ctypes.c_int), ("use_graphs", ctypes.c_int), ("max_delay_us", ctypes.c_int)]
+
+
+CALLBACK = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p)
+
+
+class Request(ctypes.Structure):
+    _fields_ = [("frames", ctypes.c_void_p), ("n_frames", ctypes.c_size_t), ("tokens_out", ctypes.c_void_p),
+                ("store_slots", ctypes.c_void_p), ("n_windows", ctypes.c_size_t),
+                ("window_frames", ctypes.c_void_p), ("window_slots", ctypes.c_void_p),
+                ("window_tokens", ctypes.c_void_p), ("logits_out", ctypes.c_void_p), ("callback", CALLBACK),
+                ("user", ctypes.c_void_p)]
+
+
+_P = ctypes.c_void_p
+_SIGS = {
+    "shv_hip_default_options": (None, [_P]),
+    "shv_hip_load": (_P, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int]),
+    "shv_hip_load_ex": (_P, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int, _P]),
+    "shv_hip_free": (None, [_P]),
+    "shv_hip_last_error": (ctypes.c_char_p, []),
+    "shv_hip_mode": (ctypes.c_char_p, [_P]),
+    "shv_hip_fingerprint": (ctypes.c_char_p, [_P]),
+    "shv_hip_threshold": (ctypes.c_double, [_P]),
+    "shv_hip_compute_revision": (ctypes.c_char_p, []),
+    "shv_hip_limits": (ctypes.c_int, [_P, _P, _P, _P, _P]),
+    "shv_hip_weight_bytes": (ctypes.c_size_t, [_P]),
+    "shv_hip_device_bytes": (ctypes.c_size_t, [_P]),
+    "shv_hip_encode_frames": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P]),
+    "shv_hip_classify": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P]),
+    "shv_hip_predict": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P]),
+    "shv_hip_submit": (_P, [_P, _P]),
+    "shv_hip_job_status": (ctypes.c_int, [_P]),
+    "shv_hip_job_wait": (ctypes.c_int, [_P]),
+    "shv_hip_job_error": (ctypes.c_char_p, [_P]),
+    "shv_hip_job_timing": (ctypes.c_int, [_P, _P, _P, _P, _P, _P]),
+    "shv_hip_job_free": (None, [_P]),
+    "shv_hip_host_alloc": (_P, [ctypes.c_size_t]),
+    "shv_hip_host_free": (None, [_P]),
+    "shv_hip_forward_device": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
+    "shv_hip_encode_device": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
+    "shv_hip_profile_enable": (ctypes.c_int, [_P, ctypes.c_int]),
+    "shv_hip_profile_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P, _P]),
+    "shv_hip_set_dump_dir": (ctypes.c_int, [_P, ctypes.c_char_p]),
+}
+
+_libs: dict[str, ctypes.CDLL] = {}
+
+
+def library(experimental: bool = False) -> ctypes.CDLL:
+    name = "libshield_v_hip_experimental.so" if experimental else "libshield_v_hip.so"
+    if name not in _libs:
+        path = LIB_DIR / name
+        if not path.exists():
+            raise ShvError(f"{path} is not built (run __graft_entry__.build())")
+        lib = ctypes.CDLL(str(path))
+        for fn, (res, args) in _SIGS.items():
+            f = getattr(lib, fn)
+            f.restype = res
+            f.argtypes = args
+        _libs[name] = lib
+    return _libs[name]
+
+
+def synth_library() -> ctypes.CDLL:
+    if "synth" not in _libs:
+        path = LIB_DIR / "libshv_synth.so"
+        if not path.exists():
+            raise ShvError(f"{path} is not built (run __graft_entry__.build())")
+        lib = ctypes.CDLL(str(path))
+        lib.shv_synth_weights.restype = ctypes.c_int
+        lib.shv_synth_weights.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_double, ctypes.c_char_p,
+                                          ctypes.POINTER(ctypes.c_longlong), ctypes.POINTER(ctypes.c_int)]
+        lib.shv_synth_bytes.restype = None
+        lib.shv_synth_bytes.argtypes = [_P, ctypes.c_size_t, ctypes.c_uint64]
+        lib.shv_synth_sha256.restype = None
+        lib.shv_synth_sha256.argtypes = [_P, ctypes.c_size_t, ctypes.c_char_p]
+        _libs["synth"] = lib
+    return _libs["synth"]
+
+
+def write_weights(path, seed: int = 1, threshold: float = 0.5) -> str:
+    """Seeded synthetic SHLDV001 weights + sidecar; returns the SHA-256 hex."""
+    sha = ctypes.create_string_buffer(65)
+    rc = synth_library().shv_synth_weights(str(path).encode(), seed, threshold, sha, None, None)
+    if rc != 0:
+        raise ShvError(f"cannot write {path}")
+    return sha.value.decode()
+
+
+def synth_clips(n_clips: int, seed0: int = 1000) -> np.ndarray:
+    """uint8 [n, 20, 180, 320, 3]; clip i from seed seed0 + i, uniform on {0..255}."""
+    out = np.empty((n_clips, WINDOW_FRAMES, 180, 320, 3), np.uint8)
+    lib = synth_library()
+    for i in range(n_clips):
+        lib.shv_synth_bytes(out[i].ctypes.data, out[i].nbytes, seed0 + i)
+    return out
+
+
+def sha256_bytes(a: np.ndarray) -> str:
+    buf = ctypes.create_string_buffer(65)
+    a = np.ascontiguousarray(a)
+    synth_library().shv_synth_sha256(a.ctypes.data, a.nbytes, buf)
+    return buf.value.decode()
+
+
+def last_error(experimental: bool = False) -> str:
+    return library(experimental).shv_hip_last_error().decode()
+
+
+def default_options() -> Options:
+    o = Options()
+    library().shv_hip_default_options(ctypes.byref(o))
+    return o
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+class Model:
+    """One loaded model (shv_hip_load_ex)."""
+
+    def __init__(self, weights, mode: str | None = "fp32", device: int = 0, experimental: bool = False,
+                 **options):
+        self.lib = library(experimental)
+        self.experimental = experimental
+        opt = Options()
+        self.lib.shv_hip_default_options(ctypes.byref(opt))
+        for k, v in options.items():
+            setattr(opt, k, int(v))
+        self.options = opt
+        self.h = self.lib.shv_hip_load_ex(str(weights).encode(), None if mode is None else mode.encode(), device,
+                                          ctypes.byref(opt))
+        if not self.h:
+            raise ShvError(self.lib.shv_hip_last_error().decode())
+
+    def close(self):
+        if self.h:
+            self.lib.shv_hip_free(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _err(self) -> str:
+        return self.lib.shv_hip_last_error().decode()
+
+    @property
+    def mode(self) -> str:
+        return self.lib.shv_hip_mode(self.h).decode()
+
+    @property
+    def fingerprint(self) -> str:
+        return self.lib.shv_hip_fingerprint(self.h).decode()
+
+    @property
+    def threshold(self) -> float:
+        return self.lib.shv_hip_threshold(self.h)
+
+    def limits(self):
+        v = [ctypes.c_int() for _ in range(4)]
+        if self.lib.shv_hip_limits(self.h, *[ctypes.byref(x) for x in v]) != 0:
+            raise ShvError(self._err())
+        return tuple(x.value for x in v)
+
+    def weight_bytes(self) -> int:
+        return self.lib.shv_hip_weight_bytes(self.h)
+
+    def device_bytes(self) -> int:
+        return self.lib.shv_hip_device_bytes(self.h)
+
+    def predict(self, clips: np.ndarray) -> np.ndarray:
+        clips = np.ascontiguousarray(clips, dtype=np.uint8)
+        b = clips.size // (WINDOW_FRAMES * FRAME_BYTES)
+        out = np.empty(b, np.float32)
+        if self.lib.shv_hip_predict(self.h, _ptr(clips), b, _ptr(out)) != 0:
+            raise ShvError(self._err())
+        return out
+
+    def encode_frames(self, frames: np.ndarray) -> np.ndarray:
+        frames = np.ascontiguousarray(frames, dtype=np.uint8)
+        n = frames.size // FRAME_BYTES
+        out = np.empty((n, 16, 384), np.float32)
+        if self.lib.shv_hip_encode_frames(self.h, _ptr(frames), n, _ptr(out)) != 0:
+            raise ShvError(self._err())
+        return out
+
+    def classify(self, tokens: np.ndarray) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, dtype=np.float32)
+        b = tokens.size // (WINDOW_FRAMES * TOKEN_FLOATS)
+        out = np.empty(b, np.float32)
+        if self.lib.shv_hip_classify(self.h, _ptr(tokens), b, _ptr(out)) != 0:
+            raise ShvError(self._err())
+        return out
+
+    def submit(self, frames=None, n_windows=0, window_frames=None, window_slots=None, window_tokens=None,
+               tokens_out=None, store_slots=None, logits_out=None, callback=None):
+        """Returns (job handle, keep-alive list); the caller must keep buffers alive until the job completes."""
+        keep = []
+        r = Request()
+        if frames is not None:
+            frames = np.ascontiguousarray(frames, dtype=np.uint8)
+            keep.append(frames)
+            r.frames = frames.ctypes.data
+            r.n_frames = frames.size // FRAME_BYTES
+        for name, arr, dt in (("store_slots", store_slots, np.int32), ("window_frames", window_frames, np.int32),
+                              ("window_slots", window_slots, np.int32)):
+            if arr is not None:
+                a = np.ascontiguousarray(arr, dtype=dt)
+                keep.append(a)
+                setattr(r, name, a.ctypes.data)
+        if window_tokens is not None:
+            ptrs = (ctypes.c_void_p * len(window_tokens))(*window_tokens)
+            keep.append(ptrs)
+            r.window_tokens = ctypes.cast(ptrs, ctypes.c_void_p)
+        if tokens_out is not None:
+            r.tokens_out = tokens_out.ctypes.data
+        r.n_windows = n_windows
+        if logits_out is not None:
+            r.logits_out = logits_out.ctypes.data
+        if callback is not None:
+            keep.append(callback)
+            r.callback = callback
+        keep.append(r)
+        job = self.lib.shv_hip_submit(self.h, ctypes.byref(r))
+        if not job:
+            raise ShvError(self._err())
+        return job, keep
+
+    def job_wait(self, job) -> int:
+        return self.lib.shv_hip_job_wait(job)
+
+    def job_status(self, job) -> int:
+        return self.lib.shv_hip_job_status(job)
+
+    def job_error(self, job) -> str:
+        return self.lib.shv_hip_job_error(job).decode()
+
+    def job_timing(self, job):
+        q, r, g = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        bf, bw = ctypes.c_int(), ctypes.c_int()
+        rc = self.lib.shv_hip_job_timing(job, ctypes.byref(q), ctypes.byref(r), ctypes.byref(g), ctypes.byref(bf),
+                                         ctypes.byref(bw))
+        return rc, dict(queue_ms=q.value, run_ms=r.value, gpu_ms=g.value, batch_frames=bf.value,
+                        batch_windows=bw.value)
+
+    def job_free(self, job) -> None:
+        self.lib.shv_hip_job_free(job)
+
+    # engine-level (device buffers)
+    def forward_device(self, d_frames: int, n_clips: int, d_logits: int, stream: int | None = None) -> None:
+        if self.lib.shv_hip_forward_device(self.h, d_frames, n_clips, d_logits, stream) != 0:
+            raise ShvError(self._err())
+
+    def encode_device(self, d_frames: int, n_frames: int, d_tokens: int, stream: int | None = None) -> None:
+        if self.lib.shv_hip_encode_device(self.h, d_frames, n_frames, d_tokens, stream) != 0:
+            raise ShvError(self._err())
+
+    def profile_enable(self, on: bool) -> None:
+        if self.lib.shv_hip_profile_enable(self.h, 1 if on else 0) != 0:
+            raise ShvError(self._err())
+
+    def profile_read(self, family: str):
+        ms, n, b = ctypes.c_double(), ctypes.c_longlong(), ctypes.c_double()
+        rc = self.lib.shv_hip_profile_read(self.h, family.encode(), ctypes.byref(ms), ctypes.byref(n),
+                                           ctypes.byref(b))
+        if rc != 0:
+            return None
+        return dict(ms=ms.value, launches=n.value, bytes=b.value)
+
+    def set_dump_dir(self, d: str) -> None:
+        if self.lib.shv_hip_set_dump_dir(self.h, d.encode()) != 0:
+            raise ShvError(self._err())
+
+
+def sigmoid64(logit: float) -> float:
+    """Score in double precision (the decision contract: score >= threshold)."""
+    import math
+    x = float(logit)
+    if x >= 0:
+        return 1.0 / (1.0 + math.exp(-x))
+    e = math.exp(x)
+    return e / (1.0 + e)

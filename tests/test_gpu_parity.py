@@ -1,0 +1,209 @@
+"""GPU parity of the HIP engine against the reference CPU engine's golden fixtures (through the C-ABI).
+
+Bars:
+  fp32  : tokens bitwise equal to the reference; logits within 4e-4 absolute; no decision flips.
+  fp16  : max |logit - exact| <= FP16_TOL on the 64-clip seeded set, 0 flips at the sidecar threshold.
+  bf16  : max |logit - exact| <= BF16_TOL, 0 flips.
+Row independence: a window's logit and a frame's tokens are bitwise identical whatever else is in the batch.
+"""
+import ctypes
+import os
+import sys
+import tempfile
+import threading
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 4e-4
+FP16_TOL = 0.05
+BF16_TOL = 0.15
+CNN_STAGES = ["cnn%02d" % i for i in range(17)]
+
+
+def flips(a, b, thr):
+    from math import exp
+    sa = np.array([x >= 0 for x in a])  # threshold 0.5 <=> logit >= 0 (sigmoid is monotone)
+    sb = np.array([x >= 0 for x in b])
+    assert thr == 0.5
+    return int((sa != sb).sum())
+
+
+def digest(a):
+    a = np.ascontiguousarray(a, np.float32).reshape(-1)
+    d = a.astype(np.float64)
+    return {"n": int(a.size), "sum": float(d.sum()), "sq": float((d * d).sum()),
+            "head": [int(x) for x in a[:16].view(np.uint32)]}
+
+
+@pytest.fixture(scope="module")
+def fp32_model(shv, weights):
+    print("[gpu] load fp32", flush=True)
+    m = shv.Model(weights, "fp32")
+    yield m
+    m.close()
+
+
+def test_fp32_tokens_bitwise(fp32_model, clips, golden_tokens):
+    print("[gpu] fp32 encode clip 0", flush=True)
+    toks = fp32_model.encode_frames(clips[0])
+    assert toks.shape == (20, 16, 384)
+    assert np.array_equal(toks[0], golden_tokens[0]), np.abs(toks[0] - golden_tokens[0]).max()
+    assert np.array_equal(toks[19], golden_tokens[1])
+
+
+def test_fp32_logits(fp32_model, clips, golden_logits, golden):
+    print("[gpu] fp32 predict 8 clips", flush=True)
+    lg = fp32_model.predict(clips[:8])
+    err = np.abs(lg - golden_logits[:8]).max()
+    print(f"[gpu] fp32 max|dlogit| = {err:.3e}", flush=True)
+    assert err <= FP32_TOL
+    assert flips(lg, golden_logits[:8], golden["threshold"]) == 0
+
+
+def test_fp32_stages(shv, weights, clips, golden):
+    print("[gpu] fp32 stage dumps", flush=True)
+    stages = golden["stages_clip0"]
+    with tempfile.TemporaryDirectory() as d, shv.Model(weights, "fp32", use_graphs=0) as m:
+        m.set_dump_dir(d)
+        m.encode_frames(clips[0][19:20])          # golden CNN stages are frame 19's
+        for name in CNN_STAGES + ["tokens"]:
+            got = digest(np.fromfile(Path(d) / f"{name}.f32", np.float32))
+            g = stages[name]
+            assert got["n"] == g["n"] and got["head"] == g["head"] and got["sum"] == g["sum"], name
+        m.predict(clips[:1])
+        for name in ["h0", "after_gdn_a", "after_gdn_b", "after_sisa_last", "logit"]:
+            a = np.fromfile(Path(d) / f"{name}.f32", np.float32).astype(np.float64)
+            g = stages[name]
+            assert a.size == g["n"], name
+            rel = abs(a.sum() - g["sum"]) / max(1.0, g["abs"])
+            assert rel < 1e-4, (name, rel)
+
+
+def test_row_independence_fp32(fp32_model, clips):
+    print("[gpu] fp32 row independence", flush=True)
+    batch = fp32_model.predict(clips[:6])
+    rev = fp32_model.predict(clips[:6][::-1])[::-1]
+    single = np.concatenate([fp32_model.predict(clips[i:i + 1]) for i in (0, 3, 5)])
+    assert np.array_equal(batch, rev)
+    assert np.array_equal(batch[[0, 3, 5]], single)
+
+
+def test_classify_matches_predict(fp32_model, clips):
+    print("[gpu] fp32 classify(tokens) == predict", flush=True)
+    toks = fp32_model.encode_frames(clips[:2].reshape(-1, 180, 320, 3))
+    lg = fp32_model.classify(toks.reshape(2, 20, 16, 384))
+    assert np.array_equal(lg, fp32_model.predict(clips[:2]))
+
+
+@pytest.mark.parametrize("mode,tol", [("fp16", FP16_TOL), ("bf16", BF16_TOL)])
+def test_half_modes(shv, weights, clips, golden_logits, golden, mode, tol):
+    print(f"[gpu] {mode} predict 64 clips", flush=True)
+    with shv.Model(weights, mode, experimental=True) as m:
+        lg = m.predict(clips)
+        err = np.abs(lg - golden_logits).max()
+        nf = flips(lg, golden_logits, golden["threshold"])
+        print(f"[gpu] {mode}: max|dlogit| = {err:.4e}, mean = {np.abs(lg - golden_logits).mean():.3e}, "
+              f"flips = {nf}", flush=True)
+        assert np.all(np.isfinite(lg))
+        assert err <= tol
+        assert nf == 0
+        # row independence in the MFMA tier
+        sub = m.predict(clips[5:8])
+        assert np.array_equal(sub, lg[5:8])
+        one = m.predict(clips[7:8])
+        assert np.array_equal(one, lg[7:8])
+
+
+def test_async_coalescing_and_slots(shv, weights, clips):
+    print("[gpu] async API", flush=True)
+    with shv.Model(weights, "fp32", token_slots=64) as m:
+        ref = m.predict(clips[:3])
+        toks = m.encode_frames(clips[:3].reshape(-1, 180, 320, 3)).reshape(3, 20, 6144)
+        # job A encodes clip 0, stores its frames into slots 0..19 and classifies window 0 from its own frames
+        la = np.full(1, -7.0, np.float32)
+        ja, ka = m.submit(frames=clips[0], store_slots=np.arange(20), n_windows=1,
+                          window_frames=np.arange(20), logits_out=la)
+        # job B: window from slots 0..19 (reads what A stored; A is earlier in FIFO order)
+        lb = np.full(1, -7.0, np.float32)
+        jb, kb = m.submit(n_windows=1, window_frames=np.full(20, -1), window_slots=np.arange(20), logits_out=lb)
+        # job C: window from host tokens of clip 2, mixed with frames of its own request for clip 1
+        lc = np.full(2, -7.0, np.float32)
+        tok2 = np.ascontiguousarray(toks[2])
+        ptrs = [tok2[i].ctypes.data for i in range(20)] + [0] * 20
+        wf = np.concatenate([np.full(20, -1), np.arange(20)])
+        seen = []
+        cb = shv.CALLBACK(lambda job, status, user: seen.append(status))
+        jc, kc = m.submit(frames=clips[1], n_windows=2, window_frames=wf, window_tokens=ptrs, logits_out=lc,
+                          callback=cb)
+        for j in (ja, jb, jc):
+            assert m.job_wait(j) == 0
+        rc, t = m.job_timing(jc)
+        assert rc == 0 and t["batch_windows"] >= 2
+        for j in (ja, jb, jc):
+            m.job_free(j)
+        assert seen == [1]
+        assert la[0] == ref[0] and lb[0] == ref[0]
+        assert lc[0] == ref[2] and lc[1] == ref[1]
+
+
+def test_failed_batch_gives_nan(shv, weights, clips):
+    print("[gpu] injected batch failure", flush=True)
+    with shv.Model(weights, "fp32") as m:
+        os.environ["SHV_HIP_TEST_FAIL_BATCH"] = "1"
+        try:
+            out = np.zeros(1, np.float32)
+            j, keep = m.submit(frames=clips[0], n_windows=1, window_frames=np.arange(20), logits_out=out)
+            assert m.job_wait(j) == -1
+            assert "injected" in m.job_error(j)
+            assert m.job_status(j) == -1
+            m.job_free(j)
+            assert np.isnan(out[0])
+        finally:
+            del os.environ["SHV_HIP_TEST_FAIL_BATCH"]
+        assert np.all(np.isfinite(m.predict(clips[:1])))
+
+
+def test_invalid_requests(shv, weights, clips):
+    with shv.Model(weights, "fp32", max_frames=40, max_windows=2, token_slots=4) as m:
+        out = np.zeros(3, np.float32)
+        with pytest.raises(shv.ShvError, match="more frames than max_frames"):
+            m.submit(frames=np.zeros((41, 180, 320, 3), np.uint8))
+        with pytest.raises(shv.ShvError, match="more windows"):
+            m.submit(n_windows=3, logits_out=out)
+        with pytest.raises(shv.ShvError, match="store slot out of range"):
+            m.submit(frames=clips[0][:2], store_slots=[0, 4])
+        with pytest.raises(shv.ShvError, match="duplicate store slot"):
+            m.submit(frames=clips[0][:2], store_slots=[1, 1])
+        with pytest.raises(shv.ShvError, match="window frame index out of range"):
+            m.submit(frames=clips[0][:2], n_windows=1, window_frames=np.full(20, 5), logits_out=out)
+        with pytest.raises(shv.ShvError, match="no token source"):
+            m.submit(n_windows=1, logits_out=out)
+        with pytest.raises(shv.ShvError, match="empty request"):
+            m.submit()
+        # predict splits into GPU batches of min(max_windows, max_frames / 20) = 2 clips
+        lg = m.predict(clips[:3])
+        assert np.all(np.isfinite(lg))
+
+
+def test_forward_device_matches_predict(shv, weights, clips):
+    import torch
+    print("[gpu] forward_device", flush=True)
+    n = 3
+    with shv.Model(weights, "fp16", experimental=True, max_frames=n * 20, max_windows=n) as m:
+        ref = m.predict(clips[:n])
+        d_frames = torch.from_numpy(clips[:n].reshape(-1)).to("cuda")
+        d_logits = torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+        torch.cuda.synchronize()
+        for _ in range(2):   # capture, then graph replay
+            m.forward_device(d_frames.data_ptr(), n, d_logits.data_ptr(), stream)
+            torch.cuda.synchronize()
+            assert np.array_equal(d_logits.cpu().numpy(), ref)
+        d_tok = torch.empty((20, 6144), dtype=torch.float32, device="cuda")
+        m.encode_device(d_frames.data_ptr(), 20, d_tok.data_ptr(), stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(d_tok.cpu().numpy().reshape(20, 16, 384), m.encode_frames(clips[0]))
