@@ -79,8 +79,8 @@ def main() -> int:
               "(clips are independent rows); run with --gpus 1", file=sys.stderr)
         return 2
 
-    import torch
     shv = load_shv()
+    hip = shv.Hip()
     B = args.batch
     with tempfile.TemporaryDirectory() as td:
         w = Path(td) / "bench.weights"
@@ -88,42 +88,36 @@ def main() -> int:
         clips = shv.synth_clips(B, 1000)
         log(f"[bench] load {args.mode} model, batch {B} clips")
         model = shv.Model(w, args.mode, experimental=args.mode != "fp32", max_frames=B * 20, max_windows=B)
-        stream = torch.cuda.Stream()
-        d_frames = torch.from_numpy(clips.reshape(-1)).to("cuda")
-        d_logits = torch.empty(B, dtype=torch.float32, device="cuda")
-        torch.cuda.synchronize()
-        sh = stream.cuda_stream
-        with torch.cuda.stream(stream):
-            for _ in range(args.warmup):
-                model.forward_device(d_frames.data_ptr(), B, d_logits.data_ptr(), sh)
-            stream.synchronize()
-            log("[bench] warmup done")
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            e0.record(stream)
-            for _ in range(args.steps):
-                model.forward_device(d_frames.data_ptr(), B, d_logits.data_ptr(), sh)
-            e1.record(stream)
-            e1.synchronize()
-            torch.cuda.synchronize()
-            total_ms = e0.elapsed_time(e1)
+        stream = hip.stream()
+        d_frames = hip.upload(clips)
+        d_logits = hip.malloc(B * 4)
+        d_tok = hip.malloc(B * 20 * 6144 * 4)
+        e0, e1 = hip.event(), hip.event()
+        hip.sync()
+        for _ in range(args.warmup):
+            model.forward_device(d_frames, B, d_logits, stream)
+        hip.stream_sync(stream)
+        log("[bench] warmup done")
+        hip.record(e0, stream)
+        for _ in range(args.steps):
+            model.forward_device(d_frames, B, d_logits, stream)
+        hip.record(e1, stream)
+        total_ms = hip.elapsed_ms(e0, e1)
+        hip.sync()
         ms = total_ms / args.steps
         value = B / (ms / 1000.0)
-        logits = d_logits.cpu().numpy()
+        logits = hip.download(d_logits, B, np.float32)
         log(f"[bench] {ms:.3f} ms/step -> {value:.1f} clips/s; finite logits {np.isfinite(logits).all()}")
 
-        # encoder only (config 1: 2560 frames FP16)
-        d_tok = torch.empty((B * 20, 6144), dtype=torch.float32, device="cuda")
-        with torch.cuda.stream(stream):
-            model.encode_device(d_frames.data_ptr(), B * 20, d_tok.data_ptr(), sh)
-            stream.synchronize()
-            e0.record(stream)
-            enc_steps = max(3, args.steps // 2)
-            for _ in range(enc_steps):
-                model.encode_device(d_frames.data_ptr(), B * 20, d_tok.data_ptr(), sh)
-            e1.record(stream)
-            e1.synchronize()
-        enc_ms = e0.elapsed_time(e1) / enc_steps
+        # encoder only (config 1: 2560 frames)
+        model.encode_device(d_frames, B * 20, d_tok, stream)
+        hip.stream_sync(stream)
+        enc_steps = max(3, args.steps // 2)
+        hip.record(e0, stream)
+        for _ in range(enc_steps):
+            model.encode_device(d_frames, B * 20, d_tok, stream)
+        hip.record(e1, stream)
+        enc_ms = hip.elapsed_ms(e0, e1) / enc_steps
         log(f"[bench] encoder {enc_ms:.3f} ms / {B * 20} frames")
 
         # per-family kernel timing with HIP events on the launching stream (graphs off while profiling)
@@ -131,10 +125,9 @@ def main() -> int:
                 "delta", "gated_norm", "sisa", "head", "assemble"]
         model.profile_enable(True)
         prof_steps = min(args.steps, 5)
-        with torch.cuda.stream(stream):
-            for _ in range(prof_steps):
-                model.forward_device(d_frames.data_ptr(), B, d_logits.data_ptr(), sh)
-            stream.synchronize()
+        for _ in range(prof_steps):
+            model.forward_device(d_frames, B, d_logits, stream)
+        hip.stream_sync(stream)
         stats = {f: model.profile_read(f) for f in fams}
         model.profile_enable(False)
         stats = {k: v for k, v in stats.items() if v and v["launches"]}
@@ -148,6 +141,9 @@ def main() -> int:
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
                     "avg_launch_ms": round(avg_ms, 4), "launches_per_step": d["launches"] // prof_steps}
         model.close()
+        for p_ in (d_frames, d_logits, d_tok):
+            hip.free(p_)
+        hip.stream_destroy(stream)
 
         # batch-1 latency through the synchronous API (pinned host clip, H2D included)
         lat = None

@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(256) pool_kernel(const T* __restrict__ in, T* 
 // ------------------------------------------------------------------------------------------------ repack
 template <typename T>
 __global__ void __launch_bounds__(256)
-repack_kernel(const float* __restrict__ src, T* __restrict__ dst, int N, int K, int perm) {
+repack_kernel(const float* __restrict__ src, T* __restrict__ dst, int N, int K, int perm, int parts) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long long)N * K) return;
     const int r = int(idx / K), k = int(idx % K);
@@ -161,7 +161,12 @@ repack_kernel(const float* __restrict__ src, T* __restrict__ dst, int N, int K, 
         const int panel = r >> 4, l = r & 15;
         sr = ((panel & 1) ? F : 0) + (panel >> 1) * 16 + l;
     }
-    dst[idx] = from_f<T>(src[(long long)sr * K + k]);
+    float rest = src[(long long)sr * K + k];
+    for (int q = 0; q < parts; ++q) {   // part q = T(rounding residual left by parts 0..q-1)
+        const T v = from_f<T>(rest);
+        dst[(long long)q * N * K + idx] = v;
+        rest = rest - to_f(v);
+    }
 }
 
 }  // namespace
@@ -191,19 +196,18 @@ template <typename T> void launch_pool(const T* in, T* out, int F, hipStream_t s
     hipLaunchKernelGGL(pool_kernel<T>, dim3(cdiv((long long)F * 16 * 120, 256)), dim3(256), 0, s, in, out, F);
 }
 
-template <typename T> void launch_repack(const float* src, T* dst, int N, int K, int perm, hipStream_t s) {
-    hipLaunchKernelGGL(repack_kernel<T>, dim3(cdiv((long long)N * K, 256)), dim3(256), 0, s, src, dst, N, K, perm);
+template <typename T> void launch_repack(const float* src, T* dst, int N, int K, int perm, int parts, hipStream_t s) {
+    hipLaunchKernelGGL(repack_kernel<T>, dim3(cdiv((long long)N * K, 256)), dim3(256), 0, s, src, dst, N, K, perm,
+                       parts);
 }
 
-#define SHV_INST_CNN(T)                                                                                          \
-    template void launch_stem<T>(const uint8_t*, T*, const float*, const float*, const float*, int, hipStream_t); \
-    template void launch_dw<T>(const T*, T*, const float*, const float*, int, int, int, int, int, int, int, int, \
-                               int, hipStream_t);                                                                \
-    template void launch_se_pool<T>(const T*, float*, int, int, int, int, hipStream_t);                          \
-    template void launch_pool<T>(const T*, T*, int, hipStream_t);                                                \
-    template void launch_repack<T>(const float*, T*, int, int, int, hipStream_t);
-SHV_INST_CNN(float)
-SHV_INST_CNN(f16)
-SHV_INST_CNN(bf16)
+template void launch_stem<float>(const uint8_t*, float*, const float*, const float*, const float*, int, hipStream_t);
+template void launch_dw<float>(const float*, float*, const float*, const float*, int, int, int, int, int, int, int, int,
+                               int, hipStream_t);
+template void launch_se_pool<float>(const float*, float*, int, int, int, int, hipStream_t);
+template void launch_pool<float>(const float*, float*, int, hipStream_t);
+template void launch_repack<float>(const float*, float*, int, int, int, int, hipStream_t);
+template void launch_repack<f16>(const float*, f16*, int, int, int, int, hipStream_t);
+template void launch_repack<bf16>(const float*, bf16*, int, int, int, int, hipStream_t);
 
 }  // namespace shv

@@ -100,10 +100,17 @@ namespace {
 
 inline void check_launch() { SHV_HIP_CHECK(hipGetLastError()); }
 
-template <typename T> void gemm_t(const GemmArgs& p, hipStream_t s);
+// G selects how GEMM operands reach the multipliers: float = exact-order VALU, f16 / bf16 = split-operand MFMA
+template <typename G> void gemm_t(const GemmArgs& p, hipStream_t s);
 template <> void gemm_t<float>(const GemmArgs& p, hipStream_t s) { gemm_f32(p, s); }
 template <> void gemm_t<f16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<f16>(p, s); }
 template <> void gemm_t<bf16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<bf16>(p, s); }
+
+// a GEMM weight on the device: `parts` arrays of N*K elements of the flavour's type, `stride` elements apart
+struct DevW {
+    const void* w = nullptr;
+    long long stride = 0;
+};
 
 // owner of device allocations
 class DevMem {
@@ -146,10 +153,10 @@ double gemm_bytes(long long M, int N, int K, int ta, int tw, int tc, int tr) {
     return double(M) * K * ta + double(N) * K * tw + double(M) * N * tc + (tr ? double(M) * N * tr : 0.0);
 }
 
-template <typename T>
+template <typename G>
 class EngineT final : public Engine {
-    static constexpr bool kF32 = std::is_same<T, float>::value;
-    static constexpr int TS = int(sizeof(T));
+    static constexpr bool kF32 = std::is_same<G, float>::value;
+    static constexpr int TS = 4;   // activations are fp32 in HBM in every mode
 
 public:
     EngineT(const HostModel& hm, Precision p, const EngineConfig& cfg) {
@@ -217,26 +224,26 @@ private:
         BlockCfg cfg{};
         int H = 0, W = 0, Ho = 0, Wo = 0, csq = 0;
         bool has_expand = false, residual = false;
-        const T* exp_w = nullptr;
+        DevW exp_w;
         const float* exp_b = nullptr;
         const float *dw_w = nullptr, *dw_b = nullptr;
         const float *se1_w = nullptr, *se1_b = nullptr, *se2_w = nullptr, *se2_b = nullptr;
-        const T* proj_w = nullptr;
+        DevW proj_w;
         const float* proj_b = nullptr;
     };
     struct Gdn {
         const float *norm_w, *ffn_norm_w, *conv_w, *conv_b, *neg_rate, *dt_bias, *o_norm_w;
-        const T *in_w, *out_w, *up_w, *down_w;   // up_w: SwiGLU gate/up interleaved, 1920 rows
+        DevW in_w, out_w, up_w, down_w;   // up_w: SwiGLU gate/up interleaved, 1920 rows
     };
     const float *lut_ = nullptr, *stem_w_ = nullptr, *stem_b_ = nullptr;
     Blk blk_[15];
-    const T* last_w_ = nullptr;
+    DevW last_w_;
     const float* last_b_ = nullptr;
-    const T* proj_w_ = nullptr;
+    DevW proj_w_;
     const float *pos_ = nullptr, *readout_ = nullptr;
     Gdn gdn_[2]{};
     const float *s_attn_norm_ = nullptr, *s_ffn_norm_ = nullptr, *s_in_b_ = nullptr, *s_lam_ = nullptr;
-    const T* s_in_w_ = nullptr;
+    DevW s_in_w_;
     const float *s_qc_w_ = nullptr, *s_o_w_ = nullptr, *s_up_w_ = nullptr, *s_down_w_ = nullptr;
     const float *fn_w_ = nullptr, *h_w0_ = nullptr, *h_b0_ = nullptr, *h_w2_ = nullptr;
     float h_b2_ = 0.0f;
@@ -247,14 +254,15 @@ private:
         return d;
     }
     const float* up(const std::vector<float>& v) { return up(v.data(), v.size()); }
-    // fp32 [N][K] rows -> device T (or fp32) with a row permutation, converted by the repack kernel on the GPU
-    template <typename U> const U* repack(const std::vector<float>& src, int N, int K, int perm) {
+    // fp32 [N][K] rows -> device parts of U with a row permutation, converted by the repack kernel on the GPU
+    template <typename U> DevW repack(const std::vector<float>& src, int N, int K, int perm) {
+        const int parts = weight_parts<U>();
         float* st = staging_.make<float>(src.size());
         SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
-        U* d = wmem_.make<U>(size_t(N) * K);
-        launch_repack<U>(st, d, N, K, perm, setup_);
+        U* d = wmem_.make<U>(size_t(parts) * N * K);
+        launch_repack<U>(st, d, N, K, perm, parts, setup_);
         check_launch();
-        return d;
+        return DevW{d, (long long)N * K};
     }
     static std::vector<float> concat(const Linear& a, const Linear& b) {
         std::vector<float> v(a.w);
@@ -274,7 +282,7 @@ private:
             d.has_expand = b.has_expand;
             d.residual = b.residual;
             if (b.has_expand) {
-                d.exp_w = repack<T>(b.expand.w, b.expand.N, b.expand.K, 0);
+                d.exp_w = repack<G>(b.expand.w, b.expand.N, b.expand.K, 0);
                 d.exp_b = up(b.expand.b);
             }
             d.dw_w = up(b.dw_w);
@@ -283,38 +291,38 @@ private:
                 d.se1_w = up(b.se1.w); d.se1_b = up(b.se1.b);
                 d.se2_w = up(b.se2.w); d.se2_b = up(b.se2.b);
             }
-            d.proj_w = repack<T>(b.project.w, b.project.N, b.project.K, 0);
+            d.proj_w = repack<G>(b.project.w, b.project.N, b.project.K, 0);
             d.proj_b = up(b.project.b);
         }
-        last_w_ = repack<T>(hm.last.w, hm.last.N, hm.last.K, 0);
+        last_w_ = repack<G>(hm.last.w, hm.last.N, hm.last.K, 0);
         last_b_ = up(hm.last.b);
-        proj_w_ = repack<T>(hm.proj.w, hm.proj.N, hm.proj.K, 0);
+        proj_w_ = repack<G>(hm.proj.w, hm.proj.N, hm.proj.K, 0);
         pos_ = up(hm.pos);
         readout_ = up(hm.readout);
         const int swiglu_perm = kF32 ? 1 : 2;
         for (int g = 0; g < 2; ++g) {
-            const GdnHost& G = hm.gdn[g];
+            const GdnHost& gh = hm.gdn[g];
             Gdn& d = gdn_[g];
-            d.norm_w = up(G.norm_w);
-            d.ffn_norm_w = up(G.ffn_norm_w);
-            d.conv_w = up(G.conv_w);
-            d.conv_b = up(G.conv_b);
-            d.neg_rate = up(G.neg_rate, kHeads);
-            d.dt_bias = up(G.dt_bias, kHeads);
-            d.o_norm_w = up(G.o_norm_w);
-            d.in_w = repack<T>(G.in.w, G.in.N, G.in.K, 0);
-            d.out_w = repack<T>(G.out.w, G.out.N, G.out.K, 0);
-            d.up_w = repack<T>(concat(G.gate, G.up), 2 * kFF, kD, swiglu_perm);
-            d.down_w = repack<T>(G.down.w, G.down.N, G.down.K, 0);
+            d.norm_w = up(gh.norm_w);
+            d.ffn_norm_w = up(gh.ffn_norm_w);
+            d.conv_w = up(gh.conv_w);
+            d.conv_b = up(gh.conv_b);
+            d.neg_rate = up(gh.neg_rate, kHeads);
+            d.dt_bias = up(gh.dt_bias, kHeads);
+            d.o_norm_w = up(gh.o_norm_w);
+            d.in_w = repack<G>(gh.in.w, gh.in.N, gh.in.K, 0);
+            d.out_w = repack<G>(gh.out.w, gh.out.N, gh.out.K, 0);
+            d.up_w = repack<G>(concat(gh.gate, gh.up), 2 * kFF, kD, swiglu_perm);
+            d.down_w = repack<G>(gh.down.w, gh.down.N, gh.down.K, 0);
         }
         const SisaHost& S = hm.sisa;
         s_attn_norm_ = up(S.attn_norm_w);
         s_ffn_norm_ = up(S.ffn_norm_w);
-        s_in_w_ = repack<T>(S.in.w, S.in.N, S.in.K, 0);
+        s_in_w_ = repack<G>(S.in.w, S.in.N, S.in.K, 0);
         s_in_b_ = up(S.in.b);
         s_qc_w_ = up(concat(S.q, S.c));                      // [576][384]: W_Q rows then W_C rows
         s_o_w_ = up(S.o.w);
-        s_up_w_ = repack<float>(concat(S.gate, S.up), 2 * kFF, kD, 1);
+        s_up_w_ = static_cast<const float*>(repack<float>(concat(S.gate, S.up), 2 * kFF, kD, 1).w);
         s_down_w_ = up(S.down.w);
         s_lam_ = up(S.lam, kHeads);
         fn_w_ = up(hm.final_norm_w);
@@ -327,11 +335,11 @@ private:
     }
 
     // ---------------------------------------------------------------- activations
-    T *X_ = nullptr, *E_ = nullptr, *D_ = nullptr, *PO_ = nullptr;
+    float *X_ = nullptr, *E_ = nullptr, *D_ = nullptr, *PO_ = nullptr;
     float *se_pool_ = nullptr, *se_hid_ = nullptr, *se_scale_ = nullptr;
     float *H_ = nullptr, *P_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *dec_ = nullptr, *beta_ = nullptr,
           *O_ = nullptr;
-    T *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;
+    float *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;
     float *XL_ = nullptr, *QC_ = nullptr, *Y_ = nullptr, *X1_ = nullptr, *X2_ = nullptr, *HIDL_ = nullptr;
     float* tok_direct_ = nullptr;
     const float** tokptr_direct_ = nullptr;
@@ -345,10 +353,10 @@ private:
             if (b.has_expand) ee = std::max(ee, size_t(b.H) * b.W * b.cfg.cexp);
             de = std::max(de, size_t(b.Ho) * b.Wo * b.cfg.cexp);
         }
-        X_ = amem_.make<T>(Fm * xe);
-        E_ = amem_.make<T>(Fm * ee);
-        D_ = amem_.make<T>(Fm * de);
-        PO_ = amem_.make<T>(Fm * 16 * kCnnOut);
+        X_ = amem_.make<float>(Fm * xe);
+        E_ = amem_.make<float>(Fm * ee);
+        D_ = amem_.make<float>(Fm * de);
+        PO_ = amem_.make<float>(Fm * 16 * kCnnOut);
         se_pool_ = amem_.make<float>(Fm * kCnnOut);
         se_hid_ = amem_.make<float>(Fm * 256);
         se_scale_ = amem_.make<float>(Fm * kCnnOut);
@@ -360,9 +368,9 @@ private:
         dec_ = amem_.make<float>(Mm * 8);
         beta_ = amem_.make<float>(Mm * 8);
         O_ = amem_.make<float>(Mm * kVD);
-        XN_ = amem_.make<T>(Mm * kD);
-        ON_ = amem_.make<T>(Mm * kVD);
-        HID_ = amem_.make<T>(Mm * kFF);
+        XN_ = amem_.make<float>(Mm * kD);
+        ON_ = amem_.make<float>(Mm * kVD);
+        HID_ = amem_.make<float>(Mm * kFF);
         XL_ = amem_.make<float>(Bm * kD);
         QC_ = amem_.make<float>(Bm * 576);
         Y_ = amem_.make<float>(Bm * kD);
@@ -433,66 +441,69 @@ private:
         o.write(reinterpret_cast<const char*>(f.data()), std::streamsize(n * sizeof(float)));
     }
 
-    void gemm(const char* fam, const GemmArgs& p, hipStream_t s, bool f32 = false) {
-        const int ta = f32 ? 4 : TS, tc = p.c_f32 ? 4 : TS;
-        const int tr = p.res ? (p.r_f32 ? 4 : TS) : 0;
-        const double bytes = gemm_bytes(p.M, p.N, p.K, ta, ta, p.swiglu ? tc / 2 : tc, tr);
-        timed(fam, bytes, s, [&] {
-            if (f32) gemm_f32(p, s);
-            else gemm_t<T>(p, s);
-        });
+    // GEMM in this engine's flavour (or the exact fp32 VALU kernel for the fp32-only layers)
+    void gemm(const char* fam, GemmArgs p, const DevW& w, hipStream_t s) {
+        p.W = w.w;
+        p.wstride = w.stride;
+        const double bytes = gemm_bytes(p.M, p.N, p.K, 4, kF32 ? 4 : int(sizeof(G)) * weight_parts<G>(),
+                                        p.swiglu ? 2 : 4, p.res ? 4 : 0);
+        timed(fam, bytes, s, [&] { gemm_t<G>(p, s); });
+        check_launch();
+    }
+    void gemm32(const char* fam, const GemmArgs& p, hipStream_t s) {
+        timed(fam, gemm_bytes(p.M, p.N, p.K, 4, 4, p.swiglu ? 2 : 4, p.res ? 4 : 0), s, [&] { gemm_f32(p, s); });
         check_launch();
     }
 
     // ---------------------------------------------------------------- CNN
     void run_encode(const uint8_t* frames, int F, float* tokens, hipStream_t s) {
         timed("stem", double(F) * (kFrameBytes + 90.0 * 160 * 16 * TS), s,
-              [&] { launch_stem<T>(frames, X_, lut_, stem_w_, stem_b_, F, s); });
+              [&] { launch_stem<float>(frames, X_, lut_, stem_w_, stem_b_, F, s); });
         check_launch();
         dump("cnn00", X_, size_t(90) * 160 * 16, s);
         for (int i = 0; i < 15; ++i) {
             const Blk& b = blk_[i];
             const long long HWi = (long long)b.H * b.W, HWo = (long long)b.Ho * b.Wo;
             const int act = b.cfg.hs ? ACT_HS : ACT_RELU;
-            const T* dwin = X_;
+            const float* dwin = X_;
             if (b.has_expand) {
                 GemmArgs p;
                 p.M = int(F * HWi); p.N = b.cfg.cexp; p.K = b.cfg.cin;
-                p.A = X_; p.lda = b.cfg.cin; p.W = b.exp_w; p.ldw = b.cfg.cin;
+                p.A = X_; p.lda = b.cfg.cin; p.ldw = b.cfg.cin;
                 p.bias = b.exp_b; p.act = act;
                 p.C = E_; p.ldc = b.cfg.cexp;
-                gemm("gemm_pw", p, s);
+                gemm("gemm_pw", p, b.exp_w, s);
                 dwin = E_;
             }
             timed("dw", double(F) * (HWi + HWo) * b.cfg.cexp * TS, s, [&] {
-                launch_dw<T>(dwin, D_, b.dw_w, b.dw_b, F, b.H, b.W, b.cfg.cexp, b.cfg.k, b.cfg.stride, b.Ho, b.Wo, act, s);
+                launch_dw<float>(dwin, D_, b.dw_w, b.dw_b, F, b.H, b.W, b.cfg.cexp, b.cfg.k, b.cfg.stride, b.Ho, b.Wo, act, s);
             });
             check_launch();
             if (b.cfg.se) {
                 timed("se_pool", double(F) * HWo * b.cfg.cexp * TS, s,
-                      [&] { launch_se_pool<T>(D_, se_pool_, F, b.Ho, b.Wo, b.cfg.cexp, s); });
+                      [&] { launch_se_pool<float>(D_, se_pool_, F, b.Ho, b.Wo, b.cfg.cexp, s); });
                 check_launch();
                 GemmArgs p1;
                 p1.M = F; p1.N = b.csq; p1.K = b.cfg.cexp;
                 p1.A = se_pool_; p1.lda = b.cfg.cexp; p1.W = b.se1_w; p1.ldw = b.cfg.cexp;
                 p1.bias = b.se1_b; p1.act = ACT_RELU;
-                p1.C = se_hid_; p1.ldc = b.csq; p1.c_f32 = 1;
-                gemm("gemm_f32_small", p1, s, true);
+                p1.C = se_hid_; p1.ldc = b.csq;
+                gemm32("gemm_f32_small", p1, s);
                 GemmArgs p2;
                 p2.M = F; p2.N = b.cfg.cexp; p2.K = b.csq;
                 p2.A = se_hid_; p2.lda = b.csq; p2.W = b.se2_w; p2.ldw = b.csq;
                 p2.bias = b.se2_b; p2.act = ACT_HSIG;
-                p2.C = se_scale_; p2.ldc = b.cfg.cexp; p2.c_f32 = 1;
-                gemm("gemm_f32_small", p2, s, true);
+                p2.C = se_scale_; p2.ldc = b.cfg.cexp;
+                gemm32("gemm_f32_small", p2, s);
             }
             GemmArgs p;
             p.M = int(F * HWo); p.N = b.cfg.cout; p.K = b.cfg.cexp;
-            p.A = D_; p.lda = b.cfg.cexp; p.W = b.proj_w; p.ldw = b.cfg.cexp;
+            p.A = D_; p.lda = b.cfg.cexp; p.ldw = b.cfg.cexp;
             p.bias = b.proj_b;
             p.C = X_; p.ldc = b.cfg.cout;
             if (b.cfg.se) { p.scale = se_scale_; p.scale_rows = int(HWo); p.ld_scale = b.cfg.cexp; }
             if (b.residual) { p.R = X_; p.ldr = b.cfg.cout; p.res = 1; }
-            gemm("gemm_pw", p, s);
+            gemm("gemm_pw", p, b.proj_w, s);
             if (!dump_dir_.empty()) {
                 char name[8];
                 std::snprintf(name, sizeof name, "cnn%02d", i + 1);
@@ -502,27 +513,27 @@ private:
         {
             GemmArgs p;
             p.M = F * 60; p.N = kCnnOut; p.K = 160;
-            p.A = X_; p.lda = 160; p.W = last_w_; p.ldw = 160;
+            p.A = X_; p.lda = 160; p.ldw = 160;
             p.bias = last_b_; p.act = ACT_HS;
             p.C = E_; p.ldc = kCnnOut;
-            gemm("gemm_pw", p, s);
+            gemm("gemm_pw", p, last_w_, s);
         }
         dump("cnn16", E_, size_t(60) * kCnnOut, s);
-        timed("pool", double(F) * (60.0 + 16.0) * kCnnOut * TS, s, [&] { launch_pool<T>(E_, PO_, F, s); });
+        timed("pool", double(F) * (60.0 + 16.0) * kCnnOut * TS, s, [&] { launch_pool<float>(E_, PO_, F, s); });
         check_launch();
         {
             GemmArgs p;
             p.M = F * 16; p.N = kD; p.K = kCnnOut;
-            p.A = PO_; p.lda = kCnnOut; p.W = proj_w_; p.ldw = kCnnOut;
-            p.C = tokens; p.ldc = kD; p.c_f32 = 1;
-            gemm("gemm_pw", p, s);
+            p.A = PO_; p.lda = kCnnOut; p.ldw = kCnnOut;
+            p.C = tokens; p.ldc = kD;
+            gemm("gemm_pw", p, proj_w_, s);
         }
         dump("tokens", tokens, kTokenFloats, s);
     }
 
     // ---------------------------------------------------------------- sequence
     void rmsnorm_all(const float* w, hipStream_t s, int M) {
-        timed("rmsnorm", double(M) * kD * (4 + TS), s, [&] { launch_rmsnorm<T>(H_, kD, w, XN_, kD, M, s); });
+        timed("rmsnorm", double(M) * kD * (4 + TS), s, [&] { launch_rmsnorm<float>(H_, kD, w, XN_, kD, M, s); });
         check_launch();
     }
 
@@ -538,9 +549,9 @@ private:
                 rmsnorm_all(g.norm_w, s, M);
                 GemmArgs pi;
                 pi.M = M; pi.N = kGn; pi.K = kD;
-                pi.A = XN_; pi.lda = kD; pi.W = g.in_w; pi.ldw = kD;
-                pi.C = P_; pi.ldc = kGld; pi.c_f32 = 1;
-                gemm("gemm_seq", pi, s);
+                pi.A = XN_; pi.lda = kD; pi.ldw = kD;
+                pi.C = P_; pi.ldc = kGld;
+                gemm("gemm_seq", pi, g.in_w, s);
                 timed("gdn_prep", double(M) * (4.0 * 1548 * 4 + 4.0 * (2 * kD + kVD + 16)), s, [&] {
                     launch_gdn_prep(P_, g.conv_w, g.conv_b, g.neg_rate, g.dt_bias, Q_, K_, V_, dec_, beta_, B, s);
                 });
@@ -549,37 +560,37 @@ private:
                       [&] { launch_delta(Q_, K_, V_, dec_, beta_, O_, B, s); });
                 check_launch();
                 timed("gated_norm", double(M) * (4.0 * 2 * kVD + TS * kVD), s,
-                      [&] { launch_gated_norm<T>(O_, P_, g.o_norm_w, ON_, M, s); });
+                      [&] { launch_gated_norm<float>(O_, P_, g.o_norm_w, ON_, M, s); });
                 check_launch();
                 GemmArgs po;
                 po.M = M; po.N = kD; po.K = kVD;
-                po.A = ON_; po.lda = kVD; po.W = g.out_w; po.ldw = kVD;
-                po.C = H_; po.ldc = kD; po.c_f32 = 1;
-                po.R = H_; po.ldr = kD; po.r_f32 = 1; po.res = reps == 2 ? 2 : 1;
-                gemm("gemm_seq", po, s);
+                po.A = ON_; po.lda = kVD; po.ldw = kVD;
+                po.C = H_; po.ldc = kD;
+                po.R = H_; po.ldr = kD; po.res = reps == 2 ? 2 : 1;
+                gemm("gemm_seq", po, g.out_w, s);
             }
             rmsnorm_all(g.ffn_norm_w, s, M);
             GemmArgs pu;
             pu.M = M; pu.N = 2 * kFF; pu.K = kD;
-            pu.A = XN_; pu.lda = kD; pu.W = g.up_w; pu.ldw = kD;
+            pu.A = XN_; pu.lda = kD; pu.ldw = kD;
             pu.C = HID_; pu.ldc = kFF; pu.swiglu = 1;
-            gemm("gemm_seq", pu, s);
+            gemm("gemm_seq", pu, g.up_w, s);
             GemmArgs pd;
             pd.M = M; pd.N = kD; pd.K = kFF;
-            pd.A = HID_; pd.lda = kFF; pd.W = g.down_w; pd.ldw = kFF;
-            pd.C = H_; pd.ldc = kD; pd.c_f32 = 1;
-            pd.R = H_; pd.ldr = kD; pd.r_f32 = 1; pd.res = 1;
-            gemm("gemm_seq", pd, s);
+            pd.A = HID_; pd.lda = kFF; pd.ldw = kFF;
+            pd.C = H_; pd.ldc = kD;
+            pd.R = H_; pd.ldr = kD; pd.res = 1;
+            gemm("gemm_seq", pd, g.down_w, s);
             dump(st == 0 ? "after_gdn_a" : "after_gdn_b", H_, size_t(kT) * kD, s);
         }
         // SISA block, last row only: all-row K/V/B/theta/alpha/forget projection, last-row Q|C in fp32
         rmsnorm_all(s_attn_norm_, s, M);
         GemmArgs pa;
         pa.M = M; pa.N = kSn; pa.K = kD;
-        pa.A = XN_; pa.lda = kD; pa.W = s_in_w_; pa.ldw = kD;
+        pa.A = XN_; pa.lda = kD; pa.ldw = kD;
         pa.bias = s_in_b_;
-        pa.C = P_; pa.ldc = kSld; pa.c_f32 = 1;
-        gemm("gemm_seq", pa, s);
+        pa.C = P_; pa.ldc = kSld;
+        gemm("gemm_seq", pa, s_in_w_, s);
         const float* hlast = H_ + size_t(kT - 1) * kD;
         const long long ldlast = (long long)kT * kD;
         timed("rmsnorm", double(B) * kD * 8, s,
@@ -588,29 +599,29 @@ private:
         GemmArgs pq;
         pq.M = B; pq.N = 576; pq.K = kD;
         pq.A = XL_; pq.lda = kD; pq.W = s_qc_w_; pq.ldw = kD;
-        pq.C = QC_; pq.ldc = 576; pq.c_f32 = 1;
-        gemm("gemm_f32_small", pq, s, true);
+        pq.C = QC_; pq.ldc = 576;
+        gemm32("gemm_f32_small", pq, s);
         timed("sisa", double(B) * kT * kSn * 4, s, [&] { launch_sisa(P_, QC_, s_lam_, Y_, B, s); });
         check_launch();
         GemmArgs pw;
         pw.M = B; pw.N = kD; pw.K = kD;
         pw.A = Y_; pw.lda = kD; pw.W = s_o_w_; pw.ldw = kD;
-        pw.C = X1_; pw.ldc = kD; pw.c_f32 = 1;
-        pw.R = hlast; pw.ldr = ldlast; pw.r_f32 = 1; pw.res = 1;
-        gemm("gemm_f32_small", pw, s, true);
+        pw.C = X1_; pw.ldc = kD;
+        pw.R = hlast; pw.ldr = ldlast; pw.res = 1;
+        gemm32("gemm_f32_small", pw, s);
         timed("rmsnorm", double(B) * kD * 8, s, [&] { launch_rmsnorm<float>(X1_, kD, s_ffn_norm_, XL_, kD, B, s); });
         check_launch();
         GemmArgs pu;
         pu.M = B; pu.N = 2 * kFF; pu.K = kD;
         pu.A = XL_; pu.lda = kD; pu.W = s_up_w_; pu.ldw = kD;
-        pu.C = HIDL_; pu.ldc = kFF; pu.c_f32 = 1; pu.swiglu = 1;
-        gemm("gemm_f32_small", pu, s, true);
+        pu.C = HIDL_; pu.ldc = kFF; pu.swiglu = 1;
+        gemm32("gemm_f32_small", pu, s);
         GemmArgs pd;
         pd.M = B; pd.N = kD; pd.K = kFF;
         pd.A = HIDL_; pd.lda = kFF; pd.W = s_down_w_; pd.ldw = kFF;
-        pd.C = X2_; pd.ldc = kD; pd.c_f32 = 1;
-        pd.R = X1_; pd.ldr = kD; pd.r_f32 = 1; pd.res = 1;
-        gemm("gemm_f32_small", pd, s, true);
+        pd.C = X2_; pd.ldc = kD;
+        pd.R = X1_; pd.ldr = kD; pd.res = 1;
+        gemm32("gemm_f32_small", pd, s);
         dump("after_sisa_last", X2_, kD, s);
         timed("head", double(B) * kD * 4, s, [&] { launch_head(X2_, fn_w_, h_w0_, h_b0_, h_w2_, h_b2_, logits, B, s); });
         check_launch();

@@ -1,13 +1,19 @@
-// GEMM kernels for gfx950.  C[m][n] = epilogue(sum_k A[m][k] W[n][k]).
+// GEMM kernels for gfx950.  C[m][n] = epilogue(sum_k A[m][k] W[n][k]); A, C, R fp32 in HBM.
 //
 // gemm_f32 (exact tier): 64x64 block tile, 256 threads, 4x4 outputs per thread, K staged through LDS in blocks
 //   of 64.  Each output is one fma chain from +0 per K block, block totals added left to right -- the per-element
 //   operation sequence of the reference CPU engine (engine/model/isa_impl.hpp:188-317), so results are bitwise
-//   independent of the tile, of M and of the other rows.
-// gemm_mfma<T> (bf16/fp16 tier): v_mfma_f32_16x16x32_{f16,bf16}.  A wave owns MT x NT 16x16 output tiles
-//   (64 rows x NT*16 columns); operand fragments are 16-byte loads straight from the row-major A [M][K] and
-//   W [N][K] arrays (lane l: row l%16, k = k0 + (l/16)*8 .. +8), so no LDS is needed; W stays in L1/L2.
-//   K advances in steps of 32 in increasing order; a K tail is zero-filled, never split.
+//   independent of the tile, of M and of the other rows, and equal to the reference's.
+// gemm_mfma<T> (fp16 / bf16 tiers): v_mfma_f32_16x16x32_{f16,bf16} on split operands.  Every fp32 operand value x
+//   is carried as a sum of T parts (fp16: hi + lo, bf16: hi + mid + lo, each part the rounding of what the previous
+//   parts leave), and the products whose magnitude exceeds ~2^-24 of hi*hi are issued as separate MFMAs into one
+//   fp32 accumulator (fp16: 3 products, bf16: 6).  This keeps the matrix cores while giving fp32-level operand
+//   precision: the random-init SHIELD-V encoder amplifies operand rounding ~100x, and plain fp16 operands moved
+//   logits by up to 1.1 on the seeded set.  Weights are split once at load (repack kernel); activations are split
+//   in registers after their 32-byte fp32 loads.
+//   A wave owns MT x NT 16x16 output tiles (64 rows x NT*16 columns); operand fragments come straight from the
+//   row-major A [M][K] and W [N][K] arrays (lane l: row l%16, k = k0 + (l/16)*8 .. +8); no LDS.  K advances in
+//   steps of 32 in increasing order; a K tail is zero-filled, never split across waves.
 #include "dev_common.hpp"
 #include "kernels.hpp"
 
@@ -18,21 +24,14 @@ namespace shv {
 namespace {
 
 // ------------------------------------------------------------------------------------------------ epilogue
-__device__ __forceinline__ float epi_value(const GemmArgs& p, long long m, int n, float v) {
+__device__ __forceinline__ void epi_store(const GemmArgs& p, long long m, int n, float v) {
     if (p.bias) v = v + p.bias[n];
     v = apply_act(v, p.act);
-    return v;
-}
-template <typename T>
-__device__ __forceinline__ void epi_store(const GemmArgs& p, long long m, int n, float v) {
     if (p.res) {
-        const long long ri = m * p.ldr + n;
-        const float r = p.r_f32 ? static_cast<const float*>(p.R)[ri] : to_f(static_cast<const T*>(p.R)[ri]);
+        const float r = p.R[m * p.ldr + n];
         v = p.res == 2 ? r + v / 1.41421356237309515f : r + v;
     }
-    const long long ci = m * p.ldc + n;
-    if (p.c_f32) static_cast<float*>(p.C)[ci] = v;
-    else static_cast<T*>(p.C)[ci] = from_f<T>(v);
+    p.C[m * p.ldc + n] = v;
 }
 
 // ------------------------------------------------------------------------------------------------ fp32 VALU
@@ -45,7 +44,7 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     const long long m0 = (long long)blockIdx.x * F32_BM;
     const int n0 = blockIdx.y * F32_BN;
-    const float* A = static_cast<const float*>(p.A);
+    const float* A = p.A;
     const float* W = static_cast<const float*>(p.W);
     float tot[4][4], blk[4][4];
 #pragma unroll
@@ -106,30 +105,51 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int n = n0 + tx * 4 + 2 * q;
-                if (n + 1 < p.N)
-                    static_cast<float*>(p.C)[m * p.ldc + (n >> 1)] = silu(tot[i][2 * q]) * tot[i][2 * q + 1];
+                if (n + 1 < p.N) p.C[m * p.ldc + (n >> 1)] = silu(tot[i][2 * q]) * tot[i][2 * q + 1];
             }
             continue;
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int n = n0 + tx * 4 + j;
-            if (n < p.N) epi_store<float>(p, m, n, epi_value(p, m, n, tot[i][j]));
+            if (n < p.N) epi_store(p, m, n, tot[i][j]);
         }
     }
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA
-template <typename T> struct Frag;
-template <> struct Frag<f16> {
-    typedef f16x8 type;
-    static __device__ __forceinline__ f32x4 mfma(type a, type b, f32x4 c) {
+template <typename T> struct Split;
+template <> struct Split<f16> {
+    typedef f16x8 V8;
+    static constexpr int P = 2;     // hi, lo
+    static constexpr int NPROD = 3; // (a part, w part) products, smallest first
+    static __device__ __forceinline__ int ap(int i) { return i == 0 ? 1 : 0; }
+    static __device__ __forceinline__ int wp(int i) { return i == 1 ? 1 : 0; }
+    static __device__ __forceinline__ void split(float x, f16* part) {
+        const f16 h = f16(x);
+        part[0] = h;
+        part[1] = f16(x - float(h));
+    }
+    static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
 };
-template <> struct Frag<bf16> {
-    typedef bf16x8 type;
-    static __device__ __forceinline__ f32x4 mfma(type a, type b, f32x4 c) {
+template <> struct Split<bf16> {
+    typedef bf16x8 V8;
+    static constexpr int P = 3;     // hi, mid, lo
+    static constexpr int NPROD = 6;
+    // products (lo,hi) (hi,lo) (mid,mid) (mid,hi) (hi,mid) (hi,hi)
+    static __device__ __forceinline__ int ap(int i) { const int t[6] = {2, 0, 1, 1, 0, 0}; return t[i]; }
+    static __device__ __forceinline__ int wp(int i) { const int t[6] = {0, 2, 1, 0, 1, 0}; return t[i]; }
+    static __device__ __forceinline__ void split(float x, bf16* part) {
+        const bf16 h = bf16(x);
+        const float r = x - float(h);
+        const bf16 m = bf16(r);
+        part[0] = h;
+        part[1] = m;
+        part[2] = bf16(r - float(m));
+    }
+    static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
 };
@@ -139,13 +159,13 @@ constexpr int MFMA_WAVES = 4;   // waves per block, stacked along M (256 rows)
 
 template <typename T, int NT, bool SCALE>
 __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_mfma_kernel(GemmArgs p) {
-    typedef typename Frag<T>::type V8;
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
     const long long mbase = ((long long)blockIdx.x * MFMA_WAVES + wave) * (MFMA_MT * 16);
     const int nbase = blockIdx.y * (NT * 16);
     if (mbase >= p.M) return;
-    const T* A = static_cast<const T*>(p.A);
     const T* W = static_cast<const T*>(p.W);
     f32x4 acc[MFMA_MT][NT];
 #pragma unroll
@@ -155,36 +175,49 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_mfma_kernel(GemmArgs p) 
     for (int k0 = 0; k0 < p.K; k0 += 32) {
         const int kk = k0 + g * 8;
         const bool kin = kk < p.K;
-        V8 a[MFMA_MT], b[NT];
+        V8 a[MFMA_MT][S::P], b[NT][S::P];
 #pragma unroll
         for (int mt = 0; mt < MFMA_MT; ++mt) {
             const long long row = mbase + mt * 16 + r;
-            V8 v = {};
-            if (kin && row < p.M) {
-                const uint4 u = *reinterpret_cast<const uint4*>(A + row * p.lda + kk);
-                v = *reinterpret_cast<const V8*>(&u);
-                if (SCALE) {
-                    const float* sc = p.scale + (row / p.scale_rows) * p.ld_scale + kk;
+            float x[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = from_f<T>(to_f(T(v[e])) * sc[e]);
+            for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+            if (kin && row < p.M) {
+                load8(p.A + row * p.lda + kk, x);
+                if (SCALE) {
+                    float sc[8];
+                    load8(p.scale + (row / p.scale_rows) * p.ld_scale + kk, sc);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = sc[e] * x[e];
                 }
             }
-            a[mt] = v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                T part[S::P];
+                S::split(x[e], part);
+#pragma unroll
+                for (int q = 0; q < S::P; ++q) a[mt][q][e] = part[q];
+            }
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int col = nbase + nt * 16 + r;
-            V8 v = {};
-            if (kin && col < p.N) {
-                const uint4 u = *reinterpret_cast<const uint4*>(W + (long long)col * p.ldw + kk);
-                v = *reinterpret_cast<const V8*>(&u);
+#pragma unroll
+            for (int q = 0; q < S::P; ++q) {
+                V8 v = {};
+                if (kin && col < p.N) {
+                    const uint4 u = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)col * p.ldw + kk);
+                    v = *reinterpret_cast<const V8*>(&u);
+                }
+                b[nt][q] = v;
             }
-            b[nt] = v;
         }
 #pragma unroll
-        for (int mt = 0; mt < MFMA_MT; ++mt)
+        for (int i = 0; i < S::NPROD; ++i)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = Frag<T>::mfma(a[mt], b[nt], acc[mt][nt]);
+            for (int mt = 0; mt < MFMA_MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[nt][S::wp(i)], acc[mt][nt]);
     }
     // lane holds C[mbase + mt*16 + g*4 + i][nbase + nt*16 + r]
 #pragma unroll
@@ -197,19 +230,15 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_mfma_kernel(GemmArgs p) 
 #pragma unroll
                 for (int nt = 0; nt + 1 < NT; nt += 2) {
                     const int panel = nbase / 16 + nt;
-                    const int j = (panel / 2) * 16 + r;
-                    if ((panel + 1) * 16 <= p.N) {
-                        const float v = silu(acc[mt][nt][i]) * acc[mt][nt + 1][i];
-                        if (p.c_f32) static_cast<float*>(p.C)[m * p.ldc + j] = v;
-                        else static_cast<T*>(p.C)[m * p.ldc + j] = from_f<T>(v);
-                    }
+                    if ((panel + 1) * 16 <= p.N)
+                        p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[mt][nt][i]) * acc[mt][nt + 1][i];
                 }
                 continue;
             }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const int n = nbase + nt * 16 + r;
-                if (n < p.N) epi_store<T>(p, m, n, epi_value(p, m, n, acc[mt][nt][i]));
+                if (n < p.N) epi_store(p, m, n, acc[mt][nt][i]);
             }
         }
     }
@@ -224,7 +253,7 @@ void launch_mfma_nt(const GemmArgs& p, hipStream_t s) {
     else hipLaunchKernelGGL((gemm_mfma_kernel<T, NT, false>), grid, dim3(64 * MFMA_WAVES), 0, s, p);
 }
 
-// N tiles per wave: minimise padded columns, at most 5 tiles (64 + 16*NT accumulator VGPRs)
+// N tiles per wave: minimise padded columns, at most 5 tiles
 int pick_nt(int N, bool swiglu) {
     if (swiglu) return 4;
     const int tiles = (N + 15) / 16;
@@ -243,10 +272,11 @@ void check_args(const GemmArgs& p, bool mfma) {
     if (p.res && !p.R) throw std::runtime_error("gemm: residual without R");
     if (p.scale && (p.scale_rows <= 0 || p.ld_scale < p.K)) throw std::runtime_error("gemm: bad SE scale");
     if (mfma) {
-        // 16-byte fragments: K, lda, ldw multiples of 8 elements
-        if (p.K % 8 || p.lda % 8 || p.ldw % 8 || p.lda < p.K || p.ldw < p.K)
+        // 32-byte A and 16-byte W fragments: K, lda, ldw, ld_scale multiples of 8 elements
+        if (p.K % 8 || p.lda % 8 || p.ldw % 8 || p.lda < p.K || p.ldw < p.K || (p.scale && p.ld_scale % 8))
             throw std::runtime_error("gemm_mfma: K/lda/ldw must be multiples of 8 (K=" + std::to_string(p.K) + ")");
         if (p.swiglu && (p.N % 32)) throw std::runtime_error("gemm_mfma: swiglu needs N % 32 == 0");
+        if (p.wstride < (long long)p.N * p.ldw) throw std::runtime_error("gemm_mfma: bad weight part stride");
     } else {
         if (p.lda < p.K || p.ldw < p.K) throw std::runtime_error("gemm_f32: bad leading dimension");
         if (p.swiglu && (p.N % 2)) throw std::runtime_error("gemm_f32: swiglu needs even N");

@@ -1,32 +1,43 @@
-// Launchers of the gfx950 kernels (host-callable).  Storage type T is float (fp32 tier), f16 or bf16.
+// Launchers of the gfx950 kernels (host-callable).  Activations are fp32 in HBM in every mode; the mode only
+// selects how GEMM operands reach the multipliers (exact VALU order, or split fp16 / bf16 parts on MFMA).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
+
 namespace shv {
 
-// C[m][n] = epilogue(sum_k A[m][k] * W[n][k]); W row-major [N][K] (PyTorch Linear / 1x1 conv layout).
-// Epilogue, per element in this order: + bias[n]; activation; residual (res 1: + R[m][n], res 2: + (v / sqrt2)
-// with R added first: R + v / 1.41421356f); stored as T or fp32.  swiglu: fp32 tier -- W rows (2j, 2j+1) =
-// (gate_j, up_j); MFMA tier -- W rows in 16-row panels (gate panel, up panel, ...); out[m][j] = silu(gate) * up.
-// Optional SE prologue: A[m][k] *= scale[(m / scale_rows) * ld_scale + k].
+typedef _Float16 f16;   // same storage types as the device code (host-visible)
+typedef __bf16 bf16;
+
+// C[m][n] = epilogue(sum_k A[m][k] * W[n][k]); A, C, R fp32 row-major; W row-major [N][K] (PyTorch Linear /
+// 1x1 conv layout).  Epilogue, per element in this order: + bias[n]; activation; residual (res 1: R + v,
+// res 2: R + v / 1.41421356f); stored fp32.  swiglu: fp32 tier -- W rows (2j, 2j+1) = (gate_j, up_j); MFMA tiers --
+// W rows in 16-row panels (gate panel, up panel, ...); out[m][j] = silu(gate) * up.
+// Optional SE prologue: A[m][k] := scale[(m / scale_rows) * ld_scale + k] * A[m][k].
+// MFMA tiers: W holds the weight's parts (fp16: hi, lo; bf16: hi, mid, lo) wstride elements apart.
 struct GemmArgs {
     int M = 0, N = 0, K = 0;
-    const void* A = nullptr; long long lda = 0;
-    const void* W = nullptr; long long ldw = 0;
+    const float* A = nullptr; long long lda = 0;
+    const void* W = nullptr; long long ldw = 0; long long wstride = 0;
     const float* scale = nullptr; int scale_rows = 1; int ld_scale = 0;
     const float* bias = nullptr; int act = 0;
-    void* C = nullptr; long long ldc = 0; int c_f32 = 0;
-    const void* R = nullptr; long long ldr = 0; int r_f32 = 0; int res = 0;
+    float* C = nullptr; long long ldc = 0;
+    const float* R = nullptr; long long ldr = 0; int res = 0;
     int swiglu = 0;
 };
 
 // fp32 tier: VALU GEMM, each output accumulated in K blocks of 64 (fma chain from +0 per block, block sums added
-// in order) exactly as the reference CPU engine (engine/model/isa_impl.hpp:188-317).  A, W, C, R all fp32.
+// in order) exactly as the reference CPU engine (engine/model/isa_impl.hpp:188-317).
 void gemm_f32(const GemmArgs& p, hipStream_t s);
-// bf16 / fp16 tier: MFMA 16x16x32 with fp32 accumulation, K consumed in 32-wide steps in increasing order
-// (no split-K): a row's outputs do not depend on M, the tile, or other rows.  A, W in T; C, R in T or fp32.
+// fp16 / bf16 tiers: MFMA 16x16x32 on split operands (fp16 2 parts / 3 products, bf16 3 parts / 6 products) with
+// fp32 accumulation, K consumed in 32-wide steps in increasing order (no split-K): a row's outputs do not depend
+// on M, the tile, or other rows.
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
+// number of weight parts an MFMA tier stores
+template <typename T> constexpr int weight_parts() { return sizeof(T) == 4 ? 1 : (std::is_same<T, bf16>::value ? 3 : 2); }
 
 // ---------------------------------------------------------------- CNN (NHWC)
 // uint8 [F][180][320][3] -> T [F][90][160][16]; lut [3][256], w [27][16] (tap (dy,dx,c) major), b [16]
@@ -40,9 +51,10 @@ void launch_dw(const T* in, T* out, const float* w, const float* b, int F, int H
 template <typename T> void launch_se_pool(const T* x, float* pooled, int F, int Ho, int Wo, int C, hipStream_t s);
 // 4x4 adaptive average pool of [F][6][10][960] -> [F][16][960]
 template <typename T> void launch_pool(const T* in, T* out, int F, hipStream_t s);
-// weight repack on the GPU: dst[r][k] = T(src[perm(r)][k]); perm 0 identity, 1 SwiGLU pair interleave
-// (rows 2j, 2j+1 <- gate j, up j of src = [gate; up]), 2 SwiGLU 16-row panel interleave
-template <typename T> void launch_repack(const float* src, T* dst, int N, int K, int perm, hipStream_t s);
+// weight repack on the GPU: part q of dst (q < parts, N*K elements apart) holds the q-th rounding residual of
+// src[perm(r)][k] in T (T = float: the value itself).  perm 0 identity, 1 SwiGLU pair interleave (rows 2j, 2j+1
+// <- gate j, up j of src = [gate; up]), 2 SwiGLU 16-row panel interleave.
+template <typename T> void launch_repack(const float* src, T* dst, int N, int K, int perm, int parts, hipStream_t s);
 
 // ---------------------------------------------------------------- sequence (fp32 residual stream)
 void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,

@@ -372,11 +372,7 @@ void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool,
     hipLaunchKernelGGL(store_tokens_kernel, dim3(F), dim3(256), 0, s, tokens, slots, pool);
 }
 
-#define SHV_INST_SEQ(T)                                                                                      \
-    template void launch_rmsnorm<T>(const float*, long long, const float*, T*, long long, int, hipStream_t); \
-    template void launch_gated_norm<T>(const float*, const float*, const float*, T*, int, hipStream_t);
-SHV_INST_SEQ(float)
-SHV_INST_SEQ(f16)
-SHV_INST_SEQ(bf16)
+template void launch_rmsnorm<float>(const float*, long long, const float*, float*, long long, int, hipStream_t);
+template void launch_gated_norm<float>(const float*, const float*, const float*, float*, int, hipStream_t);
 
 }  // namespace shv

@@ -311,6 +311,81 @@ class Model:
             raise ShvError(self._err())
 
 
+class Hip:
+    """Minimal ctypes view of the HIP runtime that libshield_v_hip.so itself links (one runtime per process):
+    device buffers, streams and events for callers of the device-pointer entry points."""
+
+    H2D, D2H, D2D = 1, 2, 3
+
+    def __init__(self):
+        library()
+        rt = ctypes.CDLL("libamdhip64.so.7")
+        for name, args in (("hipMalloc", [_P, ctypes.c_size_t]), ("hipFree", [_P]),
+                           ("hipMemcpy", [_P, _P, ctypes.c_size_t, ctypes.c_int]),
+                           ("hipDeviceSynchronize", []), ("hipStreamCreate", [_P]), ("hipStreamDestroy", [_P]),
+                           ("hipStreamSynchronize", [_P]), ("hipEventCreate", [_P]), ("hipEventDestroy", [_P]),
+                           ("hipEventRecord", [_P, _P]), ("hipEventSynchronize", [_P]),
+                           ("hipEventElapsedTime", [_P, _P, _P]), ("hipSetDevice", [ctypes.c_int])):
+            f = getattr(rt, name)
+            f.restype = ctypes.c_int
+            f.argtypes = args
+        self.rt = rt
+
+    def check(self, rc: int, what: str) -> None:
+        if rc != 0:
+            raise ShvError(f"{what} failed with HIP error {rc}")
+
+    def malloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        self.check(self.rt.hipMalloc(ctypes.byref(p), nbytes), "hipMalloc")
+        return p.value
+
+    def free(self, p: int) -> None:
+        self.check(self.rt.hipFree(p), "hipFree")
+
+    def upload(self, arr: np.ndarray) -> int:
+        arr = np.ascontiguousarray(arr)
+        p = self.malloc(arr.nbytes)
+        self.check(self.rt.hipMemcpy(p, arr.ctypes.data, arr.nbytes, self.H2D), "hipMemcpy H2D")
+        return p
+
+    def download(self, p: int, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        self.check(self.rt.hipMemcpy(out.ctypes.data, p, out.nbytes, self.D2H), "hipMemcpy D2H")
+        return out
+
+    def sync(self) -> None:
+        self.check(self.rt.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        self.check(self.rt.hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        return s.value
+
+    def stream_sync(self, s: int) -> None:
+        self.check(self.rt.hipStreamSynchronize(s), "hipStreamSynchronize")
+
+    def stream_destroy(self, s: int) -> None:
+        self.check(self.rt.hipStreamDestroy(s), "hipStreamDestroy")
+
+    def event(self) -> int:
+        e = ctypes.c_void_p()
+        self.check(self.rt.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e.value
+
+    def record(self, e: int, s: int) -> None:
+        self.check(self.rt.hipEventRecord(e, s), "hipEventRecord")
+
+    def elapsed_ms(self, e0: int, e1: int) -> float:
+        self.check(self.rt.hipEventSynchronize(e1), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self.check(self.rt.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
+        return ms.value
+
+    def event_destroy(self, e: int) -> None:
+        self.check(self.rt.hipEventDestroy(e), "hipEventDestroy")
+
+
 def sigmoid64(logit: float) -> float:
     """Score in double precision (the decision contract: score >= threshold)."""
     import math

@@ -19,8 +19,9 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 FP32_TOL = 4e-4
-FP16_TOL = 0.05
-BF16_TOL = 0.15
+# half tiers: split-operand MFMA (fp32-level operand precision); measured max 3.7e-3 (fp16) on 64 clips
+FP16_TOL = 1e-2
+BF16_TOL = 1e-2
 CNN_STAGES = ["cnn%02d" % i for i in range(17)]
 
 
@@ -190,20 +191,25 @@ def test_invalid_requests(shv, weights, clips):
 
 
 def test_forward_device_matches_predict(shv, weights, clips):
-    import torch
     print("[gpu] forward_device", flush=True)
     n = 3
+    hip = shv.Hip()
     with shv.Model(weights, "fp16", experimental=True, max_frames=n * 20, max_windows=n) as m:
         ref = m.predict(clips[:n])
-        d_frames = torch.from_numpy(clips[:n].reshape(-1)).to("cuda")
-        d_logits = torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
-        stream = torch.cuda.current_stream().cuda_stream
-        torch.cuda.synchronize()
-        for _ in range(2):   # capture, then graph replay
-            m.forward_device(d_frames.data_ptr(), n, d_logits.data_ptr(), stream)
-            torch.cuda.synchronize()
-            assert np.array_equal(d_logits.cpu().numpy(), ref)
-        d_tok = torch.empty((20, 6144), dtype=torch.float32, device="cuda")
-        m.encode_device(d_frames.data_ptr(), 20, d_tok.data_ptr(), stream)
-        torch.cuda.synchronize()
-        assert np.array_equal(d_tok.cpu().numpy().reshape(20, 16, 384), m.encode_frames(clips[0]))
+        d_frames = hip.upload(clips[:n])
+        d_logits = hip.upload(np.full(n, np.nan, np.float32))
+        d_tok = hip.malloc(20 * 6144 * 4)
+        stream = hip.stream()
+        try:
+            for _ in range(2):   # capture, then graph replay
+                m.forward_device(d_frames, n, d_logits, stream)
+                hip.stream_sync(stream)
+                assert np.array_equal(hip.download(d_logits, n, np.float32), ref)
+            m.encode_device(d_frames, 20, d_tok, stream)
+            hip.stream_sync(stream)
+            got = hip.download(d_tok, (20, 16, 384), np.float32)
+            assert np.array_equal(got, m.encode_frames(clips[0]))
+        finally:
+            hip.stream_destroy(stream)
+            for p in (d_frames, d_logits, d_tok):
+                hip.free(p)
