@@ -121,8 +121,8 @@ def main() -> int:
         log(f"[bench] encoder {enc_ms:.3f} ms / {B * 20} frames")
 
         # per-family kernel timing with HIP events on the launching stream (graphs off while profiling)
-        fams = ["gemm_pw", "dw", "stem", "se_pool", "pool", "gemm_seq", "gemm_f32_small", "rmsnorm", "gdn_prep",
-                "delta", "gated_norm", "sisa", "head", "assemble"]
+        fams = ["ir_block", "ir_se", "se_reduce", "gemm_pw", "dw", "stem", "se_pool", "pool", "gemm_seq",
+                "gemm_f32_small", "rmsnorm", "gdn_prep", "delta", "gated_norm", "sisa", "head", "assemble"]
         model.profile_enable(True)
         prof_steps = min(args.steps, 5)
         for _ in range(prof_steps):

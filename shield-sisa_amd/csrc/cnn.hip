@@ -169,7 +169,29 @@ repack_kernel(const float* __restrict__ src, T* __restrict__ dst, int N, int K, 
     }
 }
 
+template <typename T>
+__global__ void __launch_bounds__(256)
+repack_pad_kernel(const float* __restrict__ src, T* __restrict__ dst, int N, int K, int Np, int Kp, int parts) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)Np * Kp) return;
+    const int r = int(idx / Kp), k = int(idx % Kp);
+    float rest = (r < N && k < K) ? src[(long long)r * K + k] : 0.0f;
+    for (int q = 0; q < parts; ++q) {
+        const T v = from_f<T>(rest);
+        dst[(long long)q * Np * Kp + idx] = v;
+        rest = rest - to_f(v);
+    }
+}
+
 }  // namespace
+
+template <typename T>
+void launch_repack_pad(const float* src, T* dst, int N, int K, int Np, int Kp, int parts, hipStream_t s) {
+    hipLaunchKernelGGL(repack_pad_kernel<T>, dim3(cdiv((long long)Np * Kp, 256)), dim3(256), 0, s, src, dst, N, K, Np,
+                       Kp, parts);
+}
+template void launch_repack_pad<f16>(const float*, f16*, int, int, int, int, int, hipStream_t);
+template void launch_repack_pad<bf16>(const float*, bf16*, int, int, int, int, int, hipStream_t);
 
 template <typename T>
 void launch_stem(const uint8_t* in, T* out, const float* lut, const float* w, const float* b, int F, hipStream_t s) {

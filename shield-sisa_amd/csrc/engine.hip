@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <map>
@@ -167,6 +168,9 @@ public:
             throw std::runtime_error("invalid engine configuration");
         fbuckets_ = make_buckets(cfg_.max_frames);
         wbuckets_ = make_buckets(cfg_.max_windows);
+        // half tiers run the fused inverted-residual kernels unless SHV_HIP_NO_FUSE is set (layer-by-layer A/B)
+        const char* nf = std::getenv("SHV_HIP_NO_FUSE");
+        fused_ = !kF32 && !(nf && *nf && std::strcmp(nf, "0") != 0);
         SHV_HIP_CHECK(hipStreamCreateWithFlags(&setup_, hipStreamNonBlocking));
         try {
             upload_weights(hm);
@@ -230,6 +234,11 @@ private:
         const float *se1_w = nullptr, *se1_b = nullptr, *se2_w = nullptr, *se2_b = nullptr;
         DevW proj_w;
         const float* proj_b = nullptr;
+        // fused-kernel operands (half tiers): padded, pre-split weights
+        IrShape shp{};
+        int tiles_x = 0, ntiles = 0;
+        DevW fexp_w, fproj_w;
+        const float *fexp_b = nullptr, *fdw_w = nullptr, *fdw_b = nullptr, *fproj_b = nullptr;
     };
     struct Gdn {
         const float *norm_w, *ffn_norm_w, *conv_w, *conv_b, *neg_rate, *dt_bias, *o_norm_w;
@@ -264,10 +273,52 @@ private:
         check_launch();
         return DevW{d, (long long)N * K};
     }
+    template <typename U> DevW repack_pad(const std::vector<float>& src, int N, int K, int Np, int Kp) {
+        const int parts = weight_parts<U>();
+        float* st = staging_.make<float>(src.size());
+        SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
+        U* d = wmem_.make<U>(size_t(parts) * Np * Kp);
+        launch_repack_pad<U>(st, d, N, K, Np, Kp, parts, setup_);
+        check_launch();
+        return DevW{d, (long long)Np * Kp};
+    }
+    // [rows][n] -> [rows][np], zero padded
+    const float* up_pad(const std::vector<float>& v, int rows, int n, int np) {
+        std::vector<float> o(size_t(rows) * np, 0.0f);
+        for (int r = 0; r < rows; ++r)
+            for (int j = 0; j < n; ++j) o[size_t(r) * np + j] = v[size_t(r) * n + j];
+        return up(o);
+    }
     static std::vector<float> concat(const Linear& a, const Linear& b) {
         std::vector<float> v(a.w);
         v.insert(v.end(), b.w.begin(), b.w.end());
         return v;
+    }
+
+    void upload_fused(int i, const BlockHost& b, Blk& d) {
+        if constexpr (kF32) {
+            (void)i; (void)b; (void)d;
+            throw std::runtime_error("fused blocks exist for the half tiers only");
+        } else {
+        const IrShape sh = ir_shape(i);
+        const BlockCfg& c = b.cfg;
+        if (sh.cin != c.cin || sh.cexp != c.cexp || sh.cout != c.cout || sh.k != c.k || sh.stride != c.stride ||
+            sh.se != c.se || sh.hs != c.hs)
+            throw std::runtime_error("fused block table disagrees with the architecture at block " + std::to_string(i));
+        d.shp = sh;
+        d.tiles_x = (b.Wo + sh.tw - 1) / sh.tw;
+        d.ntiles = d.tiles_x * ((b.Ho + sh.th - 1) / sh.th);
+        if (b.has_expand) {
+            d.fexp_w = repack_pad<G>(b.expand.w, c.cexp, c.cin, sh.cexpp, sh.cinp);
+            d.fexp_b = up_pad(b.expand.b, 1, c.cexp, sh.cexpp);
+        }
+        d.fdw_w = up_pad(b.dw_w, c.k * c.k, c.cexp, sh.cexpp);
+        d.fdw_b = up_pad(b.dw_b, 1, c.cexp, sh.cexpp);
+        if (!c.se) {
+            d.fproj_w = repack_pad<G>(b.project.w, c.cout, c.cexp, sh.coutp, sh.cexpp);
+            d.fproj_b = up_pad(b.project.b, 1, c.cout, sh.coutp);
+        }
+        }
     }
 
     void upload_weights(const HostModel& hm) {
@@ -293,6 +344,7 @@ private:
             }
             d.proj_w = repack<G>(b.project.w, b.project.N, b.project.K, 0);
             d.proj_b = up(b.project.b);
+            if (fused_) upload_fused(i, b, d);
         }
         last_w_ = repack<G>(hm.last.w, hm.last.N, hm.last.K, 0);
         last_b_ = up(hm.last.b);
@@ -335,7 +387,8 @@ private:
     }
 
     // ---------------------------------------------------------------- activations
-    float *X_ = nullptr, *E_ = nullptr, *D_ = nullptr, *PO_ = nullptr;
+    float *X_ = nullptr, *XB_ = nullptr, *E_ = nullptr, *D_ = nullptr, *PO_ = nullptr, *se_part_ = nullptr;
+    bool fused_ = false;
     float *se_pool_ = nullptr, *se_hid_ = nullptr, *se_scale_ = nullptr;
     float *H_ = nullptr, *P_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *dec_ = nullptr, *beta_ = nullptr,
           *O_ = nullptr;
@@ -354,6 +407,13 @@ private:
             de = std::max(de, size_t(b.Ho) * b.Wo * b.cfg.cexp);
         }
         X_ = amem_.make<float>(Fm * xe);
+        if (fused_) {
+            XB_ = amem_.make<float>(Fm * xe);
+            size_t pe = 0;
+            for (int i = 0; i < 15; ++i)
+                if (blk_[i].cfg.se) pe = std::max(pe, size_t(blk_[i].ntiles) * blk_[i].shp.cexpp);
+            se_part_ = amem_.make<float>(Fm * pe);
+        }
         E_ = amem_.make<float>(Fm * ee);
         D_ = amem_.make<float>(Fm * de);
         PO_ = amem_.make<float>(Fm * 16 * kCnnOut);
@@ -457,6 +517,108 @@ private:
 
     // ---------------------------------------------------------------- CNN
     void run_encode(const uint8_t* frames, int F, float* tokens, hipStream_t s) {
+        if constexpr (!kF32) {
+            if (fused_) {
+                run_encode_fused(frames, F, tokens, s);
+                return;
+            }
+        }
+        run_encode_layers(frames, F, tokens, s);
+    }
+
+    // last 1x1 160 -> 960 + hardswish, 4x4 pool, projection 960 -> 384 (fp32 tokens)
+    void run_tail(const float* x, int F, float* tokens, hipStream_t s) {
+        {
+            GemmArgs p;
+            p.M = F * 60; p.N = kCnnOut; p.K = 160;
+            p.A = x; p.lda = 160; p.ldw = 160;
+            p.bias = last_b_; p.act = ACT_HS;
+            p.C = E_; p.ldc = kCnnOut;
+            gemm("gemm_pw", p, last_w_, s);
+        }
+        dump("cnn16", E_, size_t(60) * kCnnOut, s);
+        timed("pool", double(F) * (60.0 + 16.0) * kCnnOut * TS, s, [&] { launch_pool<float>(E_, PO_, F, s); });
+        check_launch();
+        {
+            GemmArgs p;
+            p.M = F * 16; p.N = kD; p.K = kCnnOut;
+            p.A = PO_; p.lda = kCnnOut; p.ldw = kCnnOut;
+            p.C = tokens; p.ldc = kD;
+            gemm("gemm_pw", p, proj_w_, s);
+        }
+        dump("tokens", tokens, kTokenFloats, s);
+    }
+
+    void se_fc(const Blk& b, int F, hipStream_t s) {
+        GemmArgs p1;
+        p1.M = F; p1.N = b.csq; p1.K = b.cfg.cexp;
+        p1.A = se_pool_; p1.lda = b.cfg.cexp; p1.W = b.se1_w; p1.ldw = b.cfg.cexp;
+        p1.bias = b.se1_b; p1.act = ACT_RELU;
+        p1.C = se_hid_; p1.ldc = b.csq;
+        gemm32("gemm_f32_small", p1, s);
+        GemmArgs p2;
+        p2.M = F; p2.N = b.cfg.cexp; p2.K = b.csq;
+        p2.A = se_hid_; p2.lda = b.csq; p2.W = b.se2_w; p2.ldw = b.csq;
+        p2.bias = b.se2_b; p2.act = ACT_HSIG;
+        p2.C = se_scale_; p2.ldc = b.cfg.cexp;
+        gemm32("gemm_f32_small", p2, s);
+    }
+
+    // half tiers: one fused kernel per block (SE blocks: fused expand + depthwise, SE, project GEMM)
+    void run_encode_fused(const uint8_t* frames, int F, float* tokens, hipStream_t s) {
+        timed("stem", double(F) * (kFrameBytes + 90.0 * 160 * 16 * TS), s,
+              [&] { launch_stem<float>(frames, X_, lut_, stem_w_, stem_b_, F, s); });
+        check_launch();
+        dump("cnn00", X_, size_t(90) * 160 * 16, s);
+        float* cur = X_;
+        float* nxt = XB_;
+        for (int i = 0; i < 15; ++i) {
+            const Blk& b = blk_[i];
+            const BlockCfg& c = b.cfg;
+            const long long HWi = (long long)b.H * b.W, HWo = (long long)b.Ho * b.Wo;
+            IrArgs a;
+            a.X = cur;
+            a.H = b.H; a.W = b.W; a.Ho = b.Ho; a.Wo = b.Wo;
+            a.tiles_x = b.tiles_x; a.ntiles = b.ntiles; a.frames = F;
+            a.wexp = b.fexp_w.w; a.wexp_stride = b.fexp_w.stride; a.bexp = b.fexp_b;
+            a.wdw = b.fdw_w; a.bdw = b.fdw_b;
+            if (!c.se) {
+                a.wproj = b.fproj_w.w; a.wproj_stride = b.fproj_w.stride; a.bproj = b.fproj_b;
+                a.Y = nxt;
+                timed("ir_block", double(F) * (HWi * c.cin + HWo * c.cout) * TS, s,
+                      [&] { launch_ir_block<G>(i, a, F, s); });
+                check_launch();
+            } else {
+                a.D = D_; a.part = se_part_;
+                timed("ir_se", double(F) * (HWi * c.cin + HWo * c.cexp + double(b.ntiles) * b.shp.cexpp) * TS, s,
+                      [&] { launch_ir_block<G>(i, a, F, s); });
+                check_launch();
+                timed("se_reduce", double(F) * (double(b.ntiles) * b.shp.cexpp + c.cexp) * TS, s, [&] {
+                    launch_se_reduce(se_part_, b.ntiles, b.shp.cexpp, c.cexp, int(HWo), se_pool_, F, s);
+                });
+                check_launch();
+                se_fc(b, F, s);
+                GemmArgs p;
+                p.M = int(F * HWo); p.N = c.cout; p.K = c.cexp;
+                p.A = D_; p.lda = c.cexp; p.ldw = c.cexp;
+                p.bias = b.proj_b;
+                p.C = nxt; p.ldc = c.cout;
+                p.scale = se_scale_; p.scale_rows = int(HWo); p.ld_scale = c.cexp;
+                if (b.residual) { p.R = cur; p.ldr = c.cout; p.res = 1; }
+                gemm("gemm_pw", p, b.proj_w, s);
+            }
+            std::swap(cur, nxt);
+            if (!dump_dir_.empty()) {
+                char name[8];
+                std::snprintf(name, sizeof name, "cnn%02d", i + 1);
+                dump(name, cur, size_t(HWo) * c.cout, s);
+            }
+        }
+        run_tail(cur, F, tokens, s);
+    }
+
+    // exact tier (and SHV_HIP_NO_FUSE): layer by layer
+    void run_encode_layers(const uint8_t* frames, int F, float* tokens, hipStream_t s) {
         timed("stem", double(F) * (kFrameBytes + 90.0 * 160 * 16 * TS), s,
               [&] { launch_stem<float>(frames, X_, lut_, stem_w_, stem_b_, F, s); });
         check_launch();
@@ -483,18 +645,7 @@ private:
                 timed("se_pool", double(F) * HWo * b.cfg.cexp * TS, s,
                       [&] { launch_se_pool<float>(D_, se_pool_, F, b.Ho, b.Wo, b.cfg.cexp, s); });
                 check_launch();
-                GemmArgs p1;
-                p1.M = F; p1.N = b.csq; p1.K = b.cfg.cexp;
-                p1.A = se_pool_; p1.lda = b.cfg.cexp; p1.W = b.se1_w; p1.ldw = b.cfg.cexp;
-                p1.bias = b.se1_b; p1.act = ACT_RELU;
-                p1.C = se_hid_; p1.ldc = b.csq;
-                gemm32("gemm_f32_small", p1, s);
-                GemmArgs p2;
-                p2.M = F; p2.N = b.cfg.cexp; p2.K = b.csq;
-                p2.A = se_hid_; p2.lda = b.csq; p2.W = b.se2_w; p2.ldw = b.csq;
-                p2.bias = b.se2_b; p2.act = ACT_HSIG;
-                p2.C = se_scale_; p2.ldc = b.cfg.cexp;
-                gemm32("gemm_f32_small", p2, s);
+                se_fc(b, F, s);
             }
             GemmArgs p;
             p.M = int(F * HWo); p.N = b.cfg.cout; p.K = b.cfg.cexp;
@@ -510,25 +661,7 @@ private:
                 dump(name, X_, size_t(HWo) * b.cfg.cout, s);
             }
         }
-        {
-            GemmArgs p;
-            p.M = F * 60; p.N = kCnnOut; p.K = 160;
-            p.A = X_; p.lda = 160; p.ldw = 160;
-            p.bias = last_b_; p.act = ACT_HS;
-            p.C = E_; p.ldc = kCnnOut;
-            gemm("gemm_pw", p, last_w_, s);
-        }
-        dump("cnn16", E_, size_t(60) * kCnnOut, s);
-        timed("pool", double(F) * (60.0 + 16.0) * kCnnOut * TS, s, [&] { launch_pool<float>(E_, PO_, F, s); });
-        check_launch();
-        {
-            GemmArgs p;
-            p.M = F * 16; p.N = kD; p.K = kCnnOut;
-            p.A = PO_; p.lda = kCnnOut; p.ldw = kCnnOut;
-            p.C = tokens; p.ldc = kD;
-            gemm("gemm_pw", p, proj_w_, s);
-        }
-        dump("tokens", tokens, kTokenFloats, s);
+        run_tail(X_, F, tokens, s);
     }
 
     // ---------------------------------------------------------------- sequence

@@ -16,6 +16,7 @@
 //   steps of 32 in increasing order; a K tail is zero-filled, never split across waves.
 #include "dev_common.hpp"
 #include "kernels.hpp"
+#include "mfma.hpp"
 
 #include <stdexcept>
 #include <string>
@@ -118,42 +119,6 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA
-template <typename T> struct Split;
-template <> struct Split<f16> {
-    typedef f16x8 V8;
-    static constexpr int P = 2;     // hi, lo
-    static constexpr int NPROD = 3; // (a part, w part) products, smallest first
-    static __device__ __forceinline__ int ap(int i) { return i == 0 ? 1 : 0; }
-    static __device__ __forceinline__ int wp(int i) { return i == 1 ? 1 : 0; }
-    static __device__ __forceinline__ void split(float x, f16* part) {
-        const f16 h = f16(x);
-        part[0] = h;
-        part[1] = f16(x - float(h));
-    }
-    static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-    }
-};
-template <> struct Split<bf16> {
-    typedef bf16x8 V8;
-    static constexpr int P = 3;     // hi, mid, lo
-    static constexpr int NPROD = 6;
-    // products (lo,hi) (hi,lo) (mid,mid) (mid,hi) (hi,mid) (hi,hi)
-    static __device__ __forceinline__ int ap(int i) { const int t[6] = {2, 0, 1, 1, 0, 0}; return t[i]; }
-    static __device__ __forceinline__ int wp(int i) { const int t[6] = {0, 2, 1, 0, 1, 0}; return t[i]; }
-    static __device__ __forceinline__ void split(float x, bf16* part) {
-        const bf16 h = bf16(x);
-        const float r = x - float(h);
-        const bf16 m = bf16(r);
-        part[0] = h;
-        part[1] = m;
-        part[2] = bf16(r - float(m));
-    }
-    static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-    }
-};
-
 constexpr int MFMA_MT = 4;      // 16-row tiles per wave (64 rows)
 constexpr int MFMA_WAVES = 4;   // waves per block, stacked along M (256 rows)
 

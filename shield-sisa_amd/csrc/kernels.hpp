@@ -56,6 +56,36 @@ template <typename T> void launch_pool(const T* in, T* out, int F, hipStream_t s
 // <- gate j, up j of src = [gate; up]), 2 SwiGLU 16-row panel interleave.
 template <typename T> void launch_repack(const float* src, T* dst, int N, int K, int perm, int parts, hipStream_t s);
 
+// padded repack: dst part q is [Np][Kp] (zero outside [N][K]) holding the q-th rounding residual of src [N][K]
+template <typename T>
+void launch_repack_pad(const float* src, T* dst, int N, int K, int Np, int Kp, int parts, hipStream_t s);
+
+// ---------------------------------------------------------------- fused inverted-residual blocks (half tiers)
+// Compile-time shape of block i's fused kernel (channel counts padded: cinp, cexpp to 32, coutp to 16).
+struct IrShape { int cin, cexp, cout, k, stride, se, hs, th, tw, cinp, cexpp, coutp; };
+IrShape ir_shape(int block);
+// Operands of one fused block over F frames.  Weights are padded and pre-split: wexp parts [cexpp][cinp],
+// wproj parts [coutp][cexpp] (wexp_stride / wproj_stride elements apart); bexp, bdw [cexpp]; wdw [k*k][cexpp];
+// bproj [coutp].  Non-SE blocks: X [F][H][W][cin] -> Y [F][Ho][Wo][cout] (Y must not alias X).  SE blocks:
+// X -> D [F][Ho][Wo][cexp] and part [F][ntiles][cexpp] (per-tile channel sums of D).
+struct IrArgs {
+    const float* X = nullptr;
+    float* Y = nullptr;
+    float* D = nullptr;
+    float* part = nullptr;
+    const void* wexp = nullptr; long long wexp_stride = 0;
+    const float* bexp = nullptr;
+    const float* wdw = nullptr;
+    const float* bdw = nullptr;
+    const void* wproj = nullptr; long long wproj_stride = 0;
+    const float* bproj = nullptr;
+    int H = 0, W = 0, Ho = 0, Wo = 0, tiles_x = 0, ntiles = 0, frames = 0;
+};
+template <typename T> void launch_ir_block(int block, const IrArgs& a, int F, hipStream_t s);
+// SE squeeze from the fused kernel's tile sums: pooled[f][c] = (sum over tiles in order) / (float)hw
+void launch_se_reduce(const float* part, int ntiles, int cexpp, int cexp, int hw, float* pooled, int F,
+                      hipStream_t s);
+
 // ---------------------------------------------------------------- sequence (fp32 residual stream)
 void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,
                      hipStream_t s);

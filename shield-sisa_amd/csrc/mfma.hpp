@@ -1,0 +1,83 @@
+// Split-operand MFMA for the fp16 / bf16 tiers on gfx950.
+//
+// Every fp32 operand value x is carried as a sum of T parts (fp16: hi + lo, bf16: hi + mid + lo, each part the
+// rounding of what the previous parts leave).  The products whose magnitude can exceed ~2^-24 of hi*hi are issued
+// as separate v_mfma_f32_16x16x32_{f16,bf16} into one fp32 accumulator, smallest first (fp16: 3 products,
+// bf16: 6).  The matrix cores then deliver fp32-level operand precision: the random-init SHIELD-V encoder
+// amplifies operand rounding ~100x, and plain fp16 operands moved logits by up to 1.1 on the seeded set.
+//
+// Fragment layout of v_mfma_f32_16x16x32 (64 lanes, lane l = 16 g + r):
+//   A (16 x 32): lane holds row r, k = 8 g .. 8 g + 7
+//   B (32 x 16): lane holds column r, k = 8 g .. 8 g + 7
+//   C (16 x 16): lane holds column r, rows 4 g .. 4 g + 3 (element i of the f32x4)
+#pragma once
+#include "dev_common.hpp"
+
+namespace shv {
+
+template <typename T> struct Split;
+
+template <> struct Split<f16> {
+    typedef f16x8 V8;
+    static constexpr int P = 2;     // hi, lo
+    static constexpr int NPROD = 3; // (a part, w part) products, smallest first
+    static __device__ __forceinline__ int ap(int i) { return i == 0 ? 1 : 0; }
+    static __device__ __forceinline__ int wp(int i) { return i == 1 ? 1 : 0; }
+    static __device__ __forceinline__ void split(float x, f16* part) {
+        const f16 h = f16(x);
+        part[0] = h;
+        part[1] = f16(x - float(h));
+    }
+    static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <> struct Split<bf16> {
+    typedef bf16x8 V8;
+    static constexpr int P = 3;     // hi, mid, lo
+    static constexpr int NPROD = 6;
+    // products (lo,hi) (hi,lo) (mid,mid) (mid,hi) (hi,mid) (hi,hi)
+    static __device__ __forceinline__ int ap(int i) { const int t[6] = {2, 0, 1, 1, 0, 0}; return t[i]; }
+    static __device__ __forceinline__ int wp(int i) { const int t[6] = {0, 2, 1, 0, 1, 0}; return t[i]; }
+    static __device__ __forceinline__ void split(float x, bf16* part) {
+        const bf16 h = bf16(x);
+        const float r = x - float(h);
+        const bf16 m = bf16(r);
+        part[0] = h;
+        part[1] = m;
+        part[2] = bf16(r - float(m));
+    }
+    static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+// 8 fp32 values -> the P part vectors of an MFMA A / B fragment
+template <typename T>
+__device__ __forceinline__ void split8(const float* x, typename Split<T>::V8* parts) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        T p[Split<T>::P];
+        Split<T>::split(x[e], p);
+#pragma unroll
+        for (int q = 0; q < Split<T>::P; ++q) parts[q][e] = p[q];
+    }
+}
+
+// 16 bytes of pre-split weight parts (8 elements of part q) -> V8
+template <typename T>
+__device__ __forceinline__ typename Split<T>::V8 load_part8(const T* p) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    return *reinterpret_cast<const typename Split<T>::V8*>(&u);
+}
+
+// acc += A * B over all split products (fixed order, smallest first)
+template <typename T>
+__device__ __forceinline__ f32x4 mfma_split(const typename Split<T>::V8* a, const typename Split<T>::V8* b, f32x4 acc) {
+#pragma unroll
+    for (int i = 0; i < Split<T>::NPROD; ++i) acc = Split<T>::mfma(a[Split<T>::ap(i)], b[Split<T>::wp(i)], acc);
+    return acc;
+}
+
+}  // namespace shv

@@ -213,3 +213,35 @@ def test_forward_device_matches_predict(shv, weights, clips):
             hip.stream_destroy(stream)
             for p in (d_frames, d_logits, d_tok):
                 hip.free(p)
+
+
+@pytest.mark.parametrize("mode", ["fp16", "bf16"])
+def test_fused_blocks_match_layer_path(shv, weights, clips, mode):
+    """The fused inverted-residual kernels against the layer-by-layer path of the same tier (SHV_HIP_NO_FUSE).
+    Blocks 1-3 (no squeeze-excite) perform identical arithmetic, so their outputs are bitwise equal; from block 4 on
+    the SE mean sums per-tile partials, a different (fixed) order, so later stages agree to fp32 rounding."""
+    print(f"[gpu] {mode} fused vs layer-by-layer stage dumps", flush=True)
+    dumps = {}
+    for fuse in (False, True):
+        if fuse:
+            os.environ.pop("SHV_HIP_NO_FUSE", None)
+        else:
+            os.environ["SHV_HIP_NO_FUSE"] = "1"
+        try:
+            with tempfile.TemporaryDirectory() as d, shv.Model(weights, mode, experimental=True, use_graphs=0) as m:
+                m.set_dump_dir(d)
+                toks = m.encode_frames(clips[0][19:20])
+                dumps[fuse] = {n: np.fromfile(Path(d) / f"{n}.f32", np.float32) for n in CNN_STAGES + ["tokens"]}
+                dumps[fuse]["out"] = toks.reshape(-1)
+        finally:
+            os.environ.pop("SHV_HIP_NO_FUSE", None)
+    for name in CNN_STAGES + ["tokens", "out"]:
+        a, b = dumps[True][name], dumps[False][name]
+        assert a.shape == b.shape, name
+        assert np.all(np.isfinite(a)), name
+        if name in ("cnn00", "cnn01", "cnn02", "cnn03"):
+            assert np.array_equal(a, b), (name, float(np.abs(a - b).max()))
+        else:
+            err = float(np.abs(a - b).max()) / max(1e-30, float(np.abs(b).max()))
+            print(f"[gpu] {mode} {name}: max rel diff {err:.2e}", flush=True)
+            assert err <= 1e-4, (name, err)
