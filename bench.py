@@ -5,9 +5,17 @@ value: clips/s of the full SHIELD-V forward (uint8 crops -> logit) in FP16 at ba
        inputs resident in HBM, through the C-ABI device entry point (shv_hip_forward_device), timed with HIP events
        on the launching stream over exactly --steps forwards after --warmup untimed ones.
 extra: batch-1 end-to-end latency through shv_hip_predict (pinned host clip, H2D included, like the reference's
-       2.89 ms at README.md:117), encoder-only frames/s, roofline of the dominant kernel family, and the reference
-       CPU engine (compiled from the reference sources, oracle/_ref) timed on this host's cores.
+       2.89 ms at README.md:117), encoder-only frames/s, the roofline of the dominant kernel, and the reference CPU
+       engine (compiled from the reference sources into oracle/_ref) timed on this host's cores.
+roofline: the dominant kernel is the one with the largest device time per step; its average launch duration is
+       measured here with HIP events on the launching stream (per-kernel profiling pass, graphs off) and its
+       algorithmic bytes per launch are the input, output and side-output maps it must move (weights excluded).
+       `traffic` (HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a plain device copy)
+       is read from profiles/roofline_traffic.json only when that file was measured on this library's compute
+       revision and names the same kernel; else null.
 Synthetic data: seeded random-init weights in the reference weight-file layout and uniform uint8 crops.
+--kernel-only runs just the batch forwards (timed + profiling pass) and an optional device copy of --copy-mb MiB,
+so that a rocprofv3 run over it averages exactly the launches this line reports.
 """
 from __future__ import annotations
 
@@ -24,8 +32,14 @@ import numpy as np
 
 ROOT = Path(__file__).resolve().parent
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
-MFMA_FP16_TFLOPS = 2500.0   # MI355X dense fp16
 REF_B128_CLIPS_PER_S = 128 / 0.191   # reference README.md:118 (RTX A6000, batch 128 FP16)
+# MobileNetV3-Large blocks (cin, cexp, cout): the fused kernels are profiled per instantiation "ir_<cin>x<cexp>x<cout>"
+BLOCKS = [(16, 16, 16), (16, 64, 24), (24, 72, 24), (24, 72, 40), (40, 120, 40), (40, 120, 40), (40, 240, 80),
+          (80, 200, 80), (80, 184, 80), (80, 184, 80), (80, 480, 112), (112, 672, 112), (112, 672, 160),
+          (160, 960, 160), (160, 960, 160)]
+FAMILIES = sorted({"ir_%dx%dx%d" % b for b in BLOCKS}) + [
+    "se_reduce", "gemm_pw", "dw", "stem", "se_pool", "pool", "gemm_seq", "gemm_f32_small", "rmsnorm", "gdn_prep",
+    "delta", "gated_norm", "sisa", "head", "assemble"]
 
 
 def load_shv():
@@ -63,6 +77,19 @@ def cpu_baseline(weights: Path, clips: np.ndarray, seconds: float) -> dict | Non
                       f"repeated for {dt:.1f} s ({n} clips)"}
 
 
+def measured_traffic(kernel: str, revision: str) -> float | None:
+    path = ROOT / "profiles" / "roofline_traffic.json"
+    if not path.exists():
+        return None
+    try:
+        t = json.loads(path.read_text())
+    except ValueError:
+        return None
+    if t.get("revision") != revision or t.get("family") != kernel:
+        return None
+    return float(t["traffic_bytes_per_launch"])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -73,6 +100,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--latency-iters", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the SHIELD-V forward has no cross-GPU step "
@@ -82,16 +111,16 @@ def main() -> int:
     shv = load_shv()
     hip = shv.Hip()
     B = args.batch
+    revision = shv.library().shv_hip_compute_revision().decode()
     with tempfile.TemporaryDirectory() as td:
         w = Path(td) / "bench.weights"
         shv.write_weights(w, seed=1, threshold=0.5)
         clips = shv.synth_clips(B, 1000)
-        log(f"[bench] load {args.mode} model, batch {B} clips")
+        log(f"[bench] load {args.mode} model, batch {B} clips, revision {revision}")
         model = shv.Model(w, args.mode, experimental=args.mode != "fp32", max_frames=B * 20, max_windows=B)
         stream = hip.stream()
         d_frames = hip.upload(clips)
         d_logits = hip.malloc(B * 4)
-        d_tok = hip.malloc(B * 20 * 6144 * 4)
         e0, e1 = hip.event(), hip.event()
         hip.sync()
         for _ in range(args.warmup):
@@ -109,63 +138,89 @@ def main() -> int:
         logits = hip.download(d_logits, B, np.float32)
         log(f"[bench] {ms:.3f} ms/step -> {value:.1f} clips/s; finite logits {np.isfinite(logits).all()}")
 
-        # encoder only (config 1: 2560 frames)
-        model.encode_device(d_frames, B * 20, d_tok, stream)
-        hip.stream_sync(stream)
-        enc_steps = max(3, args.steps // 2)
-        hip.record(e0, stream)
-        for _ in range(enc_steps):
-            model.encode_device(d_frames, B * 20, d_tok, stream)
-        hip.record(e1, stream)
-        enc_ms = hip.elapsed_ms(e0, e1) / enc_steps
-        log(f"[bench] encoder {enc_ms:.3f} ms / {B * 20} frames")
-
-        # per-family kernel timing with HIP events on the launching stream (graphs off while profiling)
-        fams = ["ir_block", "ir_se", "se_reduce", "gemm_pw", "dw", "stem", "se_pool", "pool", "gemm_seq",
-                "gemm_f32_small", "rmsnorm", "gdn_prep", "delta", "gated_norm", "sisa", "head", "assemble"]
+        # per-kernel timing with HIP events on the launching stream (graphs off while profiling)
         model.profile_enable(True)
-        prof_steps = min(args.steps, 5)
+        prof_steps = max(1, min(args.steps, 3))
         for _ in range(prof_steps):
             model.forward_device(d_frames, B, d_logits, stream)
         hip.stream_sync(stream)
-        stats = {f: model.profile_read(f) for f in fams}
+        stats = {f: model.profile_read(f) for f in FAMILIES}
         model.profile_enable(False)
         stats = {k: v for k, v in stats.items() if v and v["launches"]}
         per_step = {k: round(v["ms"] / prof_steps, 3) for k, v in stats.items()}
-        log("[bench] per-step ms by family: " + json.dumps(per_step))
-        dom = max(stats, key=lambda k: stats[k]["ms"])
+        log("[bench] per-step ms by kernel family: " + json.dumps(per_step))
+        # dominant kernel: the fused-block kernel with the most device time per step (each such family is one kernel
+        # symbol at one shape, so rocprofv3's per-kernel average can be set beside this one)
+        dom = max((k for k in stats if k.startswith("ir_")), key=lambda k: stats[k]["ms"])
         d = stats[dom]
         avg_ms = d["ms"] / d["launches"]
-        achieved = (d["bytes"] / d["launches"]) / (avg_ms / 1000.0) / 1e9
+        bytes_per_launch = d["bytes"] / d["launches"]
+        achieved = bytes_per_launch / (avg_ms / 1000.0) / 1e9
+        traffic = measured_traffic(dom, revision)
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                    "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": None if traffic is None else round(traffic),
+                    "kernel": dom, "algorithmic_bytes_per_launch": round(bytes_per_launch),
                     "avg_launch_ms": round(avg_ms, 4), "launches_per_step": d["launches"] // prof_steps}
+        log("[bench] roofline " + json.dumps(roofline))
+
+        copy = None
+        if args.copy_mb > 0:   # plain device copy: calibrates the PMC byte counters and shows achievable HBM rate
+            nbytes = args.copy_mb << 20
+            src, dst = hip.malloc(nbytes), hip.malloc(nbytes)
+            hip.memset(src, 1, nbytes)
+            hip.copy_d2d(dst, src, nbytes, stream)
+            hip.stream_sync(stream)
+            hip.record(e0, stream)
+            for _ in range(5):
+                hip.copy_d2d(dst, src, nbytes, stream)
+            hip.record(e1, stream)
+            cms = hip.elapsed_ms(e0, e1) / 5
+            copy = {"bytes": nbytes, "ms": round(cms, 4), "GB/s": round(2 * nbytes / (cms / 1000.0) / 1e9, 1)}
+            log(f"[bench] device copy {args.copy_mb} MiB: {cms:.3f} ms -> {copy['GB/s']} GB/s (read + write)")
+            hip.free(src)
+            hip.free(dst)
+
+        enc_ms = None
+        if not args.kernel_only:   # encoder only (config 1: 2560 frames)
+            d_tok = hip.malloc(B * 20 * 6144 * 4)
+            model.encode_device(d_frames, B * 20, d_tok, stream)
+            hip.stream_sync(stream)
+            enc_steps = max(3, args.steps // 2)
+            hip.record(e0, stream)
+            for _ in range(enc_steps):
+                model.encode_device(d_frames, B * 20, d_tok, stream)
+            hip.record(e1, stream)
+            enc_ms = hip.elapsed_ms(e0, e1) / enc_steps
+            log(f"[bench] encoder {enc_ms:.3f} ms / {B * 20} frames")
+            hip.free(d_tok)
         model.close()
-        for p_ in (d_frames, d_logits, d_tok):
-            hip.free(p_)
+        hip.free(d_frames)
+        hip.free(d_logits)
         hip.stream_destroy(stream)
 
         # batch-1 latency through the synchronous API (pinned host clip, H2D included)
         lat = None
-        with shv.Model(w, args.mode, experimental=args.mode != "fp32") as m1:
-            lib = m1.lib
-            p = lib.shv_hip_host_alloc(20 * shv.FRAME_BYTES)
-            pinned = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_uint8 * (20 * shv.FRAME_BYTES)).from_address(p))
-            pinned[:] = clips[0].reshape(-1)
-            out = np.empty(1, np.float32)
-            for _ in range(10):
-                lib.shv_hip_predict(m1.h, p, 1, out.ctypes.data)
-            ts = []
-            for _ in range(args.latency_iters):
-                t0 = time.perf_counter()
-                lib.shv_hip_predict(m1.h, p, 1, out.ctypes.data)
-                ts.append((time.perf_counter() - t0) * 1000.0)
-            lib.shv_hip_host_free(p)
-            lat = float(np.percentile(ts, 50))
-            log(f"[bench] batch-1 latency p50 {lat:.3f} ms (p95 {np.percentile(ts, 95):.3f})")
+        if not args.kernel_only and args.latency_iters > 0:
+            with shv.Model(w, args.mode, experimental=args.mode != "fp32") as m1:
+                lib = m1.lib
+                p = lib.shv_hip_host_alloc(20 * shv.FRAME_BYTES)
+                pinned = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_uint8 * (20 * shv.FRAME_BYTES)).from_address(p))
+                pinned[:] = clips[0].reshape(-1)
+                out = np.empty(1, np.float32)
+                for _ in range(10):
+                    lib.shv_hip_predict(m1.h, p, 1, out.ctypes.data)
+                ts = []
+                for _ in range(args.latency_iters):
+                    t0 = time.perf_counter()
+                    lib.shv_hip_predict(m1.h, p, 1, out.ctypes.data)
+                    ts.append((time.perf_counter() - t0) * 1000.0)
+                lib.shv_hip_host_free(p)
+                lat = float(np.percentile(ts, 50))
+                log(f"[bench] batch-1 latency p50 {lat:.3f} ms (p95 {np.percentile(ts, 95):.3f})")
 
         cpu = None
-        if not args.no_cpu:
+        if not args.no_cpu and not args.kernel_only:
             cpu = cpu_baseline(w, clips, args.cpu_seconds)
 
     line = {
@@ -178,17 +233,20 @@ def main() -> int:
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(value / REF_B128_CLIPS_PER_S, 3) if B == 128 and args.mode == "fp16" else None,
+        "vs_baseline": None,
         "dtype": args.mode,
         "data": "synthetic (seeded random-init weights in the SHLDV001 layout, uniform uint8 crops)",
         "config": {"workload": f"shieldv_forward_{args.mode}_b{B}", "clips": B, "frames_per_clip": 20,
                    "crop": "180x320x3 uint8", "tokens_per_window": 321, "d_model": 384,
-                   "inputs": "device-resident (HBM)", "entry": "shv_hip_forward_device"},
+                   "inputs": "device-resident (HBM)", "entry": "shv_hip_forward_device",
+                   "reference_gpu_clips_per_s": round(REF_B128_CLIPS_PER_S, 1)},
         "latency_b1_ms": None if lat is None else round(lat, 3),
-        "encoder_frames_per_s": round(B * 20 / (enc_ms / 1000.0), 1),
+        "encoder_frames_per_s": None if enc_ms is None else round(B * 20 / (enc_ms / 1000.0), 1),
         "family_ms_per_step": per_step,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "device_copy": copy,
+        "revision": revision,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
@@ -237,6 +238,7 @@ private:
         // fused-kernel operands (half tiers): padded, pre-split weights
         IrShape shp{};
         int tiles_x = 0, ntiles = 0;
+        char fam[32] = {};   // profiling family: one per fused-kernel instantiation, "ir_<cin>x<cexp>x<cout>"
         DevW fexp_w, fproj_w;
         const float *fexp_b = nullptr, *fdw_w = nullptr, *fdw_b = nullptr, *fproj_b = nullptr;
     };
@@ -306,6 +308,7 @@ private:
             sh.se != c.se || sh.hs != c.hs)
             throw std::runtime_error("fused block table disagrees with the architecture at block " + std::to_string(i));
         d.shp = sh;
+        std::snprintf(d.fam, sizeof d.fam, "ir_%dx%dx%d", c.cin, c.cexp, c.cout);
         d.tiles_x = (b.Wo + sh.tw - 1) / sh.tw;
         d.ntiles = d.tiles_x * ((b.Ho + sh.th - 1) / sh.th);
         if (b.has_expand) {
@@ -585,12 +588,12 @@ private:
             if (!c.se) {
                 a.wproj = b.fproj_w.w; a.wproj_stride = b.fproj_w.stride; a.bproj = b.fproj_b;
                 a.Y = nxt;
-                timed("ir_block", double(F) * (HWi * c.cin + HWo * c.cout) * TS, s,
+                timed(b.fam, double(F) * (HWi * c.cin + HWo * c.cout) * TS, s,
                       [&] { launch_ir_block<G>(i, a, F, s); });
                 check_launch();
             } else {
                 a.D = D_; a.part = se_part_;
-                timed("ir_se", double(F) * (HWi * c.cin + HWo * c.cexp + double(b.ntiles) * b.shp.cexpp) * TS, s,
+                timed(b.fam, double(F) * (HWi * c.cin + HWo * c.cexp + double(b.ntiles) * b.shp.cexpp) * TS, s,
                       [&] { launch_ir_block<G>(i, a, F, s); });
                 check_launch();
                 timed("se_reduce", double(F) * (double(b.ntiles) * b.shp.cexpp + c.cexp) * TS, s, [&] {

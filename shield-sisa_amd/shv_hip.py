@@ -325,7 +325,9 @@ class Hip:
                            ("hipDeviceSynchronize", []), ("hipStreamCreate", [_P]), ("hipStreamDestroy", [_P]),
                            ("hipStreamSynchronize", [_P]), ("hipEventCreate", [_P]), ("hipEventDestroy", [_P]),
                            ("hipEventRecord", [_P, _P]), ("hipEventSynchronize", [_P]),
-                           ("hipEventElapsedTime", [_P, _P, _P]), ("hipSetDevice", [ctypes.c_int])):
+                           ("hipEventElapsedTime", [_P, _P, _P]), ("hipSetDevice", [ctypes.c_int]),
+                           ("hipMemset", [_P, ctypes.c_int, ctypes.c_size_t]),
+                           ("hipMemcpyAsync", [_P, _P, ctypes.c_size_t, ctypes.c_int, _P])):
             f = getattr(rt, name)
             f.restype = ctypes.c_int
             f.argtypes = args
@@ -353,6 +355,12 @@ class Hip:
         out = np.empty(shape, dtype)
         self.check(self.rt.hipMemcpy(out.ctypes.data, p, out.nbytes, self.D2H), "hipMemcpy D2H")
         return out
+
+    def memset(self, p: int, value: int, nbytes: int) -> None:
+        self.check(self.rt.hipMemset(p, value, nbytes), "hipMemset")
+
+    def copy_d2d(self, dst: int, src: int, nbytes: int, stream: int | None = None) -> None:
+        self.check(self.rt.hipMemcpyAsync(dst, src, nbytes, self.D2D, stream), "hipMemcpyAsync D2D")
 
     def sync(self) -> None:
         self.check(self.rt.hipDeviceSynchronize(), "hipDeviceSynchronize")
