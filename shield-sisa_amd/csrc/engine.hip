@@ -302,7 +302,7 @@ private:
             (void)i; (void)b; (void)d;
             throw std::runtime_error("fused blocks exist for the half tiers only");
         } else {
-        const IrShape sh = ir_shape(i);
+        const IrShape sh = ir_shape(i, std::is_same<G, bf16>::value);
         const BlockCfg& c = b.cfg;
         if (sh.cin != c.cin || sh.cexp != c.cexp || sh.cout != c.cout || sh.k != c.k || sh.stride != c.stride ||
             sh.se != c.se || sh.hs != c.hs)

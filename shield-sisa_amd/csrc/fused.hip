@@ -508,6 +508,240 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Squeeze-excite blocks, barrier-free: the workgroup stages the split input tile once; then each of its 4 waves
+// owns chunks of 16 expanded channels (chunk c = wave, wave + 4, ...) and runs expand -> depthwise -> D store and
+// channel sums for them in its own LDS region.  A wave's LDS traffic is ordered by the hardware (one wave's LDS
+// instructions execute in issue order), so no workgroup barrier is needed inside the chunk loop and the 4 waves
+// never wait for each other.
+constexpr int WCW = 16;            // channels per wave chunk (one MFMA n-tile)
+constexpr int WCS_LD = WCW + 4;    // fp32 row stride of the per-wave chunk buffers
+
+template <int CIN_, int CEXP_, int KS_, int S_, int HS_, int TH_, int TW_, int R_>
+struct SeCfg {
+    static constexpr int CIN = CIN_, CEXP = CEXP_, KS = KS_, S = S_, TH = TH_, TW = TW_, R = R_;
+    static constexpr int ACT = HS_ ? ACT_HS : ACT_RELU;
+    static constexpr int PAD = (KS - 1) / 2;
+    static constexpr int IH = (TH - 1) * S + KS, IW = (TW - 1) * S + KS;
+    static constexpr int PIN = IH * IW, POUT = TH * TW;
+    static constexpr int CINP = (CIN + 31) / 32 * 32;
+    static constexpr int CEXPP = (CEXP + WCW - 1) / WCW * WCW;
+    static constexpr int MT_IN = (PIN + 15) / 16, MT_OUT = (POUT + 15) / 16;
+    static constexpr int NCH = CEXPP / WCW;
+    static constexpr int KST = CINP / 32;
+    static constexpr int XH_LD = CINP + 8;
+    static constexpr int XH_ROWS = MT_IN * 16;
+    static constexpr int ES_W = MT_IN * 16 * WCS_LD;
+    static constexpr int DS_W = MT_OUT * 16 * WCS_LD;
+    static constexpr int WD_W = (KS * KS + 1) * WCW;
+    static constexpr int NSTRIP = TH / R;
+    static constexpr int DW_UNITS = (WCW / 4) * TW * NSTRIP;
+    static_assert(TH % R == 0, "depthwise strips must tile the output rows");
+    static_assert(MT_IN <= 8, "inside mask holds 8 m-tiles");
+};
+template <typename T, class C> struct SeLayout {
+    static constexpr int P = Split<T>::P;
+    static constexpr int XS_BYTES = P * C::XH_ROWS * C::XH_LD * 2;
+    static constexpr int WAVE_FLOATS = C::ES_W + C::DS_W + C::WD_W;
+    static constexpr int BYTES = XS_BYTES + 4 * WAVE_FLOATS * 4;
+    static constexpr bool FITS = BYTES <= LDS_BUDGET;
+};
+
+__device__ __forceinline__ void wave_lds_fence() { asm volatile("" ::: "memory"); }
+
+template <typename T, class C>
+__global__ void __launch_bounds__(IR_THREADS) ir_se_wave_kernel(IrArgs a) {
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    typedef SeLayout<T, C> L;
+    static_assert(L::FITS, "tile exceeds the LDS budget");
+    __shared__ __attribute__((aligned(16))) unsigned char lds_raw[L::BYTES];
+    T* Xh = reinterpret_cast<T*>(lds_raw);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    float* Es = reinterpret_cast<float*>(lds_raw + L::XS_BYTES) + wave * L::WAVE_FLOATS;
+    float* Ds = Es + C::ES_W;
+    float* Wd = Ds + C::DS_W;
+    const int tile = blockIdx.x % a.ntiles;
+    const long long f = blockIdx.x / a.ntiles;
+    const int ty0 = (tile / a.tiles_x) * C::TH, tx0 = (tile % a.tiles_x) * C::TW;
+    const int iy0 = ty0 * C::S - C::PAD, ix0 = tx0 * C::S - C::PAD;
+    const T* wexp = static_cast<const T*>(a.wexp);
+    const float* Xf = a.X + f * a.H * a.W * C::CIN;
+
+    // weights of this wave's next chunk (expand fragments, expand bias, depthwise taps + bias) are fetched into
+    // registers one chunk ahead, the first ones while the tile is staged
+    constexpr int WD4 = (C::KS * C::KS + 1) * (WCW / 4);   // float4s of a chunk's depthwise table
+    constexpr int WDR = (WD4 + 63) / 64;                   // per lane
+    V8 ew_n[C::KST][S::P];
+    float eb_n = 0.0f;
+    float4 wd_n[WDR];
+    auto fetch = [&](int c0) {
+#pragma unroll
+        for (int ks = 0; ks < C::KST; ++ks)
+#pragma unroll
+            for (int q = 0; q < S::P; ++q)
+                ew_n[ks][q] = load_part8<T>(wexp + q * a.wexp_stride + (long long)(c0 + r) * C::CINP + ks * 32 + g * 8);
+        eb_n = a.bexp[c0 + r];
+#pragma unroll
+        for (int k = 0; k < WDR; ++k) {
+            const int i = lane + 64 * k;
+            const int t = i / (WCW / 4), q = i - t * (WCW / 4);
+            wd_n[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (i < WD4) {
+                const float* src = t < C::KS * C::KS ? a.wdw + t * C::CEXPP + c0 + q * 4 : a.bdw + c0 + q * 4;
+                wd_n[k] = *reinterpret_cast<const float4*>(src);
+            }
+        }
+    };
+    if (wave < C::NCH) fetch(wave * WCW);
+
+    // ---- input tile (+halo, zero outside the map and in the K padding) -> LDS, split into the operand parts
+    {
+        constexpr int XQ = C::CINP / 4;
+        for (int i = tid; i < C::XH_ROWS * XQ; i += IR_THREADS) {
+            const int row = i / XQ, q = i - row * XQ;
+            const int ly = row / C::IW, lx = row - ly * C::IW;
+            const int iy = iy0 + ly, ix = ix0 + lx;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (row < C::PIN && q * 4 < C::CIN && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
+                v = *reinterpret_cast<const float4*>(Xf + ((long long)iy * a.W + ix) * C::CIN + q * 4);
+            const float x[4] = {v.x, v.y, v.z, v.w};
+            T part[4][S::P];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
+#pragma unroll
+            for (int pq = 0; pq < S::P; ++pq) {
+                T four[4] = {part[0][pq], part[1][pq], part[2][pq], part[3][pq]};
+                *reinterpret_cast<uint2*>(Xh + (pq * C::XH_ROWS + row) * C::XH_LD + q * 4) =
+                    *reinterpret_cast<const uint2*>(four);
+            }
+        }
+    }
+    // expand rows of this lane inside the map: bit 4 mt + i
+    unsigned inside = 0;
+#pragma unroll
+    for (int mt = 0; mt < C::MT_IN; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = mt * 16 + g * 4 + i;
+            const int ly = row / C::IW, lx = row - ly * C::IW;
+            const int iy = iy0 + ly, ix = ix0 + lx;
+            if (row < C::PIN && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W) inside |= 1u << (4 * mt + i);
+        }
+    lds_barrier();   // the only workgroup barrier: the staged tile is read-only from here on
+
+    for (int ch = wave; ch < C::NCH; ch += 4) {
+        const int c0 = ch * WCW;
+        V8 ew[C::KST][S::P];
+#pragma unroll
+        for (int ks = 0; ks < C::KST; ++ks)
+#pragma unroll
+            for (int q = 0; q < S::P; ++q) ew[ks][q] = ew_n[ks][q];
+        const float bias = eb_n;
+        // depthwise taps and bias of the chunk -> this wave's Wd (layout [t][16] = float4 index i)
+#pragma unroll
+        for (int k = 0; k < WDR; ++k) {
+            const int i = lane + 64 * k;
+            if (i < WD4) *reinterpret_cast<float4*>(Wd + i * 4) = wd_n[k];
+        }
+        if (ch + 4 < C::NCH) fetch(c0 + 4 * WCW);
+        // ---- expand: E[rows][16] = act(X . Wexp[c0 .. c0+16) + b) over all input-tile rows
+#pragma unroll
+        for (int mt = 0; mt < C::MT_IN; ++mt) {
+            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < C::KST; ++ks) {
+                V8 ap[S::P];
+#pragma unroll
+                for (int q = 0; q < S::P; ++q)
+                    ap[q] = *reinterpret_cast<const V8*>(Xh + (q * C::XH_ROWS + mt * 16 + r) * C::XH_LD + ks * 32 + g * 8);
+                acc = mfma_split<T>(ap, ew[ks], acc);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v = 0.0f;
+                if (inside & (1u << (4 * mt + i))) v = apply_act_nb(acc[i] + bias, C::ACT);
+                Es[(mt * 16 + g * 4 + i) * WCS_LD + r] = v;
+            }
+        }
+        wave_lds_fence();
+        // ---- depthwise: unit = (4 channels, tile column, R rows); fma chain over (dy, dx) from +0, padding taps
+        // read the staged zeros (the same values as skipping them)
+        for (int u = lane; u < C::DW_UNITS; u += 64) {
+            const int cgi = u % (WCW / 4), rest = u / (WCW / 4);
+            const int ox = rest % C::TW, oy0 = (rest / C::TW) * C::R;
+            const float* src = Es + (oy0 * C::S * C::IW + ox * C::S) * WCS_LD + cgi * 4;
+            float4 acc[C::R];
+#pragma unroll
+            for (int rr = 0; rr < C::R; ++rr) acc[rr] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 1
+            for (int dy = 0; dy < C::KS; ++dy) {
+#pragma unroll
+                for (int dx = 0; dx < C::KS; ++dx) {
+                    const float4 w = *reinterpret_cast<const float4*>(Wd + (dy * C::KS + dx) * WCW + cgi * 4);
+#pragma unroll
+                    for (int rr = 0; rr < C::R; ++rr) {
+                        const float4 x =
+                            *reinterpret_cast<const float4*>(src + ((rr * C::S + dy) * C::IW + dx) * WCS_LD);
+                        acc[rr].x = __builtin_fmaf(x.x, w.x, acc[rr].x);
+                        acc[rr].y = __builtin_fmaf(x.y, w.y, acc[rr].y);
+                        acc[rr].z = __builtin_fmaf(x.z, w.z, acc[rr].z);
+                        acc[rr].w = __builtin_fmaf(x.w, w.w, acc[rr].w);
+                    }
+                }
+            }
+            const float4 bb = *reinterpret_cast<const float4*>(Wd + C::KS * C::KS * WCW + cgi * 4);
+#pragma unroll
+            for (int rr = 0; rr < C::R; ++rr) {
+                const int oy = oy0 + rr;
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (ty0 + oy < a.Ho && tx0 + ox < a.Wo) {
+                    v.x = apply_act_nb(acc[rr].x + bb.x, C::ACT);
+                    v.y = apply_act_nb(acc[rr].y + bb.y, C::ACT);
+                    v.z = apply_act_nb(acc[rr].z + bb.z, C::ACT);
+                    v.w = apply_act_nb(acc[rr].w + bb.w, C::ACT);
+                }
+                *reinterpret_cast<float4*>(Ds + (oy * C::TW + ox) * WCS_LD + cgi * 4) = v;
+            }
+        }
+        wave_lds_fence();
+        // ---- D chunk -> HBM and the tile's channel sums: lane (pixel group pg, 4 channels q) sums pixels
+        // pg, pg + 16, ... in order; lanes with equal q are combined by an xor tree (a fixed, frame-local order)
+        {
+            const int q = lane & 3, pg = lane >> 2;
+            float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int p = pg; p < C::POUT; p += 16) {
+                const int oy = p / C::TW, ox = p - oy * C::TW;
+                const int gy = ty0 + oy, gx = tx0 + ox;
+                if (gy < a.Ho && gx < a.Wo) {
+                    const float4 v = *reinterpret_cast<const float4*>(Ds + p * WCS_LD + q * 4);
+                    if (c0 + q * 4 < C::CEXP)
+                        *reinterpret_cast<float4*>(a.D + ((f * a.Ho + gy) * a.Wo + gx) * C::CEXP + c0 + q * 4) = v;
+                    sum.x = sum.x + v.x; sum.y = sum.y + v.y; sum.z = sum.z + v.z; sum.w = sum.w + v.w;
+                }
+            }
+#pragma unroll
+            for (int m = 4; m < 64; m <<= 1) {
+                sum.x = sum.x + __shfl_xor(sum.x, m);
+                sum.y = sum.y + __shfl_xor(sum.y, m);
+                sum.z = sum.z + __shfl_xor(sum.z, m);
+                sum.w = sum.w + __shfl_xor(sum.w, m);
+            }
+            if (lane < 4)
+                *reinterpret_cast<float4*>(a.part + (f * a.ntiles + tile) * C::CEXPP + c0 + lane * 4) = sum;
+        }
+        wave_lds_fence();
+    }
+}
+
+// SE blocks that take the barrier-free kernel (fp16 tier; a type whose staged tile does not fit keeps the
+// chunk-synchronous kernel)
+//                 cin cexp k  s hs TH TW R
+typedef SeCfg<40, 120, 5, 1, 0, 4, 8, 2> W5;       // 23x40 (b5, b6)
+typedef SeCfg<80, 480, 3, 1, 1, 3, 10, 1> W11;     // 12x20
+typedef SeCfg<112, 672, 3, 1, 1, 3, 10, 1> W12;    // 12x20
+typedef SeCfg<160, 960, 5, 1, 1, 3, 5, 1> W14;     // 6x10 (b14, b15)
+
 // pooled[f][c] = (sum over tiles t in order of part[f][t][c]) / (float)hw
 __global__ void __launch_bounds__(256)
 se_reduce_kernel(const float* __restrict__ part, int ntiles, int cexpp, int cexp, float hw, float* __restrict__ pooled,
@@ -527,6 +761,18 @@ template <class C> IrShape shape_of() {
     s.cin = C::CIN; s.cexp = C::CEXP; s.cout = C::COUT; s.k = C::KS; s.stride = C::S; s.se = C::SE;
     s.hs = C::ACT == ACT_HS; s.th = C::TH; s.tw = C::TW; s.cinp = C::CINP; s.cexpp = C::CEXPP; s.coutp = C::COUTP;
     return s;
+}
+// the barrier-free kernel's shape, with the block's cout / padding taken from its chunk-synchronous twin
+template <class W, class C> IrShape shape_of_wave() {
+    IrShape s = shape_of<C>();
+    s.th = W::TH; s.tw = W::TW; s.cexpp = W::CEXPP;
+    return s;
+}
+
+template <typename T, class W> void launch_wave(const IrArgs& a, int F, hipStream_t s) {
+    const int ty = (a.Ho + W::TH - 1) / W::TH, tx = (a.Wo + W::TW - 1) / W::TW;
+    if (tx != a.tiles_x || ty * tx != a.ntiles || a.frames != F) throw std::runtime_error("ir_se_wave: tile grid mismatch");
+    hipLaunchKernelGGL((ir_se_wave_kernel<T, W>), dim3((unsigned)((long long)a.ntiles * F)), dim3(IR_THREADS), 0, s, a);
 }
 
 template <typename T, class C> void launch_cfg(const IrArgs& a, int F, hipStream_t s) {
@@ -552,22 +798,28 @@ template <typename T, class C> void launch_cfg(const IrArgs& a, int F, hipStream
 
 }  // namespace
 
-IrShape ir_shape(int block) {
+template <typename T> IrShape ir_shape_t(int block) {
     switch (block) {
     case 0: return shape_of<B1>();
     case 1: return shape_of<B2>();
     case 2: return shape_of<B3>();
     case 3: return shape_of<B4>();
-    case 4: case 5: return shape_of<B5>();
+    case 4: case 5: return SeLayout<T, W5>::FITS ? shape_of_wave<W5, B5>() : shape_of<B5>();
     case 6: return shape_of<B7>();
     case 7: return shape_of<B8>();
     case 8: case 9: return shape_of<B9>();
-    case 10: return shape_of<B11>();
-    case 11: return shape_of<B12>();
+    case 10: return SeLayout<T, W11>::FITS ? shape_of_wave<W11, B11>() : shape_of<B11>();
+    case 11: return SeLayout<T, W12>::FITS ? shape_of_wave<W12, B12>() : shape_of<B12>();
     case 12: return shape_of<B13>();
-    case 13: case 14: return shape_of<B14>();
+    case 13: case 14: return SeLayout<T, W14>::FITS ? shape_of_wave<W14, B14>() : shape_of<B14>();
     }
     throw std::runtime_error("ir_shape: block index out of range");
+}
+IrShape ir_shape(int block, bool bf16_tier) { return bf16_tier ? ir_shape_t<bf16>(block) : ir_shape_t<f16>(block); }
+
+template <typename T, class W, class C> void launch_se(const IrArgs& a, int F, hipStream_t s) {
+    if constexpr (SeLayout<T, W>::FITS) launch_wave<T, W>(a, F, s);
+    else launch_cfg<T, C>(a, F, s);
 }
 
 template <typename T> void launch_ir_block(int block, const IrArgs& a, int F, hipStream_t s) {
@@ -577,14 +829,14 @@ template <typename T> void launch_ir_block(int block, const IrArgs& a, int F, hi
     case 1: launch_cfg<T, B2>(a, F, s); break;
     case 2: launch_cfg<T, B3>(a, F, s); break;
     case 3: launch_cfg<T, B4>(a, F, s); break;
-    case 4: case 5: launch_cfg<T, B5>(a, F, s); break;
+    case 4: case 5: launch_se<T, W5, B5>(a, F, s); break;
     case 6: launch_cfg<T, B7>(a, F, s); break;
     case 7: launch_cfg<T, B8>(a, F, s); break;
     case 8: case 9: launch_cfg<T, B9>(a, F, s); break;
-    case 10: launch_cfg<T, B11>(a, F, s); break;
-    case 11: launch_cfg<T, B12>(a, F, s); break;
+    case 10: launch_se<T, W11, B11>(a, F, s); break;
+    case 11: launch_se<T, W12, B12>(a, F, s); break;
     case 12: launch_cfg<T, B13>(a, F, s); break;
-    case 13: case 14: launch_cfg<T, B14>(a, F, s); break;
+    case 13: case 14: launch_se<T, W14, B14>(a, F, s); break;
     default: throw std::runtime_error("launch_ir_block: block index out of range");
     }
 }

@@ -11,9 +11,8 @@
 //   precision: the random-init SHIELD-V encoder amplifies operand rounding ~100x, and plain fp16 operands moved
 //   logits by up to 1.1 on the seeded set.  Weights are split once at load (repack kernel); activations are split
 //   in registers after their 32-byte fp32 loads.
-//   A wave owns MT x NT 16x16 output tiles (64 rows x NT*16 columns); operand fragments come straight from the
-//   row-major A [M][K] and W [N][K] arrays (lane l: row l%16, k = k0 + (l/16)*8 .. +8); no LDS.  K advances in
-//   steps of 32 in increasing order; a K tail is zero-filled, never split across waves.
+//   A and W tiles are staged through LDS (A split once per workgroup), the next K step prefetched into registers;
+//   K advances in steps of 32 in increasing order; a K tail is zero-filled, never split across waves.
 #include "dev_common.hpp"
 #include "kernels.hpp"
 #include "mfma.hpp"
@@ -119,11 +118,14 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA
+// Direct-fragment GEMM for N <= 160 (the SE-block projects, CNN 1x1 layers): the workgroup covers every output
+// column in at most two column blocks, so A is read once or twice straight into MFMA fragments and staging it
+// through LDS buys nothing.  A wave owns MFMA_MT x NT 16x16 tiles.
 constexpr int MFMA_MT = 4;      // 16-row tiles per wave (64 rows)
 constexpr int MFMA_WAVES = 4;   // waves per block, stacked along M (256 rows)
 
 template <typename T, int NT, bool SCALE>
-__global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_mfma_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -209,26 +211,182 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_mfma_kernel(GemmArgs p) 
     }
 }
 
+// Workgroup barrier that waits for LDS traffic only (the next K step's global loads stay in flight across it).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// LDS-staged split-operand GEMM.  A workgroup (4 waves, WGM x WGN) owns a BM x BN tile of C; per K step of 32 it
+// stages A[BM][32] (fp32 from HBM, SE-scaled, split into the T parts once per workgroup) and the pre-split W parts
+// [BN][32] in LDS, while the next step's global loads are already in flight; each wave multiplies WM x WN 16x16
+// tiles from LDS fragments.  Every accumulator receives, per K step, the same NPROD MFMAs in the same order as
+// before staging existed, so results do not depend on the tiling.
+constexpr int LG_KT = 32;          // K per step: one MFMA K
+constexpr int LG_LD = LG_KT + 8;   // staged row stride in T elements (80 B): 16-lane fragment reads hit 64 banks once
+
+template <typename T, int WM, int WN, int WGM, int WGN, bool SCALE>
+__global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
+    static_assert(WGM * WGN == 4, "4 waves");
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    constexpr int P = S::P;
+    constexpr int BM = 16 * WM * WGM, BN = 16 * WN * WGN;
+    __shared__ __attribute__((aligned(16))) T As[P][BM][LG_LD];
+    __shared__ __attribute__((aligned(16))) T Ws[P][BN][LG_LD];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const long long m0 = (long long)blockIdx.x * BM;
+    const int n0 = blockIdx.y * BN;
+    const T* W = static_cast<const T*>(p.W);
+
+    constexpr int A4 = BM * (LG_KT / 4);      // float4s of an A tile
+    constexpr int AR = (A4 + 255) / 256;
+    constexpr int W8 = BN * (LG_KT / 8);      // 8-element groups of a W part tile
+    constexpr int WR = (W8 + 255) / 256;
+    float4 ra[AR];
+    uint4 rw[WR][P];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int k = 0; k < AR; ++k) {
+            const int i = tid + 256 * k;
+            const int row = i >> 3, c = i & 7;
+            const long long gm = m0 + row;
+            const int kk = k0 + c * 4;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (i < A4 && gm < p.M && kk < p.K) {
+                v = *reinterpret_cast<const float4*>(p.A + gm * p.lda + kk);
+                if constexpr (SCALE) {
+                    const float4 sc = *reinterpret_cast<const float4*>(p.scale + (gm / p.scale_rows) * p.ld_scale + kk);
+                    v.x = sc.x * v.x; v.y = sc.y * v.y; v.z = sc.z * v.z; v.w = sc.w * v.w;
+                }
+            }
+            ra[k] = v;
+        }
+#pragma unroll
+        for (int k = 0; k < WR; ++k) {
+            const int i = tid + 256 * k;
+            const int row = i >> 2, c = i & 3;
+            const int gn = n0 + row, kk = k0 + c * 8;
+            const bool in = i < W8 && gn < p.N && kk < p.K;
+#pragma unroll
+            for (int q = 0; q < P; ++q)
+                rw[k][q] = in ? *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)gn * p.ldw + kk)
+                              : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int k = 0; k < AR; ++k) {
+            const int i = tid + 256 * k;
+            if (i >= A4) continue;
+            const int row = i >> 3, c = i & 7;
+            const float x[4] = {ra[k].x, ra[k].y, ra[k].z, ra[k].w};
+            T part[4][P];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
+#pragma unroll
+            for (int q = 0; q < P; ++q) {
+                T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
+                *reinterpret_cast<uint2*>(&As[q][row][c * 4]) = *reinterpret_cast<const uint2*>(four);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < WR; ++k) {
+            const int i = tid + 256 * k;
+            if (i >= W8) continue;
+            const int row = i >> 2, c = i & 3;
+#pragma unroll
+            for (int q = 0; q < P; ++q) *reinterpret_cast<uint4*>(&Ws[q][row][c * 8]) = rw[k][q];
+        }
+    };
+
+    f32x4 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    load(0);
+    for (int k0 = 0; k0 < p.K; k0 += LG_KT) {
+        store();
+        lds_barrier();
+        if (k0 + LG_KT < p.K) load(k0 + LG_KT);
+        V8 a[WM][P], b[WN][P];
+#pragma unroll
+        for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+            for (int q = 0; q < P; ++q) a[mt][q] = *reinterpret_cast<const V8*>(&As[q][(wm * WM + mt) * 16 + r][g * 8]);
+#pragma unroll
+        for (int nt = 0; nt < WN; ++nt)
+#pragma unroll
+            for (int q = 0; q < P; ++q) b[nt][q] = *reinterpret_cast<const V8*>(&Ws[q][(wn * WN + nt) * 16 + r][g * 8]);
+#pragma unroll
+        for (int i = 0; i < S::NPROD; ++i)
+#pragma unroll
+            for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < WN; ++nt) acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[nt][S::wp(i)], acc[mt][nt]);
+        lds_barrier();
+    }
+    // lane holds C[m0 + (wm*WM + mt)*16 + g*4 + i][n0 + (wn*WN + nt)*16 + r]
+    const int nbase = n0 + wn * WN * 16;
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long long m = m0 + (wm * WM + mt) * 16 + g * 4 + i;
+            if (m >= p.M) continue;
+            if (p.swiglu) {  // 16-row panels alternate gate / up; WN is even and nbase a multiple of 32
+#pragma unroll
+                for (int nt = 0; nt + 1 < WN; nt += 2) {
+                    const int panel = nbase / 16 + nt;
+                    if ((panel + 1) * 16 <= p.N)
+                        p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[mt][nt][i]) * acc[mt][nt + 1][i];
+                }
+                continue;
+            }
+#pragma unroll
+            for (int nt = 0; nt < WN; ++nt) {
+                const int n = nbase + nt * 16 + r;
+                if (n < p.N) epi_store(p, m, n, acc[mt][nt][i]);
+            }
+        }
+    }
+}
+
 inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
 
 template <typename T, int NT>
-void launch_mfma_nt(const GemmArgs& p, hipStream_t s) {
+void launch_direct(const GemmArgs& p, hipStream_t s) {
     const dim3 grid(cdiv(p.M, 16LL * MFMA_MT * MFMA_WAVES), cdiv(p.N, NT * 16));
-    if (p.scale) hipLaunchKernelGGL((gemm_mfma_kernel<T, NT, true>), grid, dim3(64 * MFMA_WAVES), 0, s, p);
-    else hipLaunchKernelGGL((gemm_mfma_kernel<T, NT, false>), grid, dim3(64 * MFMA_WAVES), 0, s, p);
+    if (p.scale) hipLaunchKernelGGL((gemm_direct_kernel<T, NT, true>), grid, dim3(64 * MFMA_WAVES), 0, s, p);
+    else hipLaunchKernelGGL((gemm_direct_kernel<T, NT, false>), grid, dim3(64 * MFMA_WAVES), 0, s, p);
 }
 
-// N tiles per wave: minimise padded columns, at most 5 tiles
-int pick_nt(int N, bool swiglu) {
-    if (swiglu) return 4;
-    const int tiles = (N + 15) / 16;
-    if (tiles <= 5) return tiles;
-    int best = 5, best_cols = 1 << 30;
-    for (int nt = 5; nt >= 3; --nt) {
-        const int cols = (tiles + nt - 1) / nt * nt;
-        if (cols < best_cols) { best_cols = cols; best = nt; }
+template <typename T, int WM, int WN, int WGM, int WGN>
+void launch_lds(const GemmArgs& p, hipStream_t s) {
+    const dim3 grid(cdiv(p.M, 16LL * WM * WGM), cdiv(p.N, 16 * WN * WGN));
+    if (p.scale) hipLaunchKernelGGL((gemm_lds_kernel<T, WM, WN, WGM, WGN, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gemm_lds_kernel<T, WM, WN, WGM, WGN, false>), grid, dim3(256), 0, s, p);
+}
+
+// N up to 160 (CNN projects and 1x1 layers): direct fragments, 16-column tiles per wave chosen to minimise
+// padded columns (at most 5 per wave); wider N (last 1x1, sequence): LDS-staged 128 x 128 workgroup tiles.
+template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
+    const int tiles = (p.N + 15) / 16;
+    if (p.swiglu || tiles > 10) { launch_lds<T, 4, 4, 2, 2>(p, s); return; }
+    int nt = tiles;
+    if (tiles > 5) {
+        int best_cols = 1 << 30;
+        for (int c = 5; c >= 3; --c) {
+            const int cols = (tiles + c - 1) / c * c;
+            if (cols < best_cols) { best_cols = cols; nt = c; }
+        }
     }
-    return best;
+    switch (nt) {
+    case 1: launch_direct<T, 1>(p, s); break;
+    case 2: launch_direct<T, 2>(p, s); break;
+    case 3: launch_direct<T, 3>(p, s); break;
+    case 4: launch_direct<T, 4>(p, s); break;
+    default: launch_direct<T, 5>(p, s); break;
+    }
 }
 
 void check_args(const GemmArgs& p, bool mfma) {
@@ -259,13 +417,7 @@ void gemm_f32(const GemmArgs& p, hipStream_t s) {
 
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s) {
     check_args(p, true);
-    switch (pick_nt(p.N, p.swiglu != 0)) {
-    case 1: launch_mfma_nt<T, 1>(p, s); break;
-    case 2: launch_mfma_nt<T, 2>(p, s); break;
-    case 3: launch_mfma_nt<T, 3>(p, s); break;
-    case 4: launch_mfma_nt<T, 4>(p, s); break;
-    default: launch_mfma_nt<T, 5>(p, s); break;
-    }
+    launch_gemm<T>(p, s);
 }
 template void gemm_mfma<f16>(const GemmArgs&, hipStream_t);
 template void gemm_mfma<bf16>(const GemmArgs&, hipStream_t);

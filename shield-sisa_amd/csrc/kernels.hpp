@@ -61,9 +61,10 @@ template <typename T>
 void launch_repack_pad(const float* src, T* dst, int N, int K, int Np, int Kp, int parts, hipStream_t s);
 
 // ---------------------------------------------------------------- fused inverted-residual blocks (half tiers)
-// Compile-time shape of block i's fused kernel (channel counts padded: cinp, cexpp to 32, coutp to 16).
+// Compile-time shape of block i's fused kernel for the fp16 or bf16 tier (tile; channel counts padded: cinp to 32,
+// cexpp to the kernel's chunk width, coutp to 16).
 struct IrShape { int cin, cexp, cout, k, stride, se, hs, th, tw, cinp, cexpp, coutp; };
-IrShape ir_shape(int block);
+IrShape ir_shape(int block, bool bf16_tier);
 // Operands of one fused block over F frames.  Weights are padded and pre-split: wexp parts [cexpp][cinp],
 // wproj parts [coutp][cexpp] (wexp_stride / wproj_stride elements apart); bexp, bdw [cexpp]; wdw [k*k][cexpp];
 // bproj [coutp].  Non-SE blocks: X [F][H][W][cin] -> Y [F][Ho][Wo][cout] (Y must not alias X).  SE blocks:
