@@ -98,17 +98,22 @@ gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const
 }
 
 // ------------------------------------------------------------------------------------------------ delta rule
-// One block per (window, head), one thread per value column c (128).  The thread keeps S[0..63][c] in registers.
-// Per token (isa_impl.hpp:911-947): u = (v - a * pred) * beta; S[j] = fma(k_j, u, S[j] * a); o = fma chain over j
-// of S[j] * q_j; pred = fma chain over j of S[j] * k_{t+1, j}.  q and k of 32-token chunks are staged in LDS and
-// read as broadcasts.
+// One workgroup per (window, head, half of the value columns); one thread per value column c (64).  The recurrence
+// of a value column needs only that column (S[:, c], v_c), so the halves are independent.  The thread keeps
+// S[0..63][c] in registers.  Per token (isa_impl.hpp:911-947): u = (v - a * pred) * beta; S[j] = fma(k_j, u, S[j] * a);
+// o = fma chain over j of S[j] * q_j; pred = fma chain over j of S[j] * k_{t+1, j}.  q, k, v, decay and beta of
+// 32-token chunks are staged in LDS (q and k read as broadcasts), so no global load sits on the serial chain.
 constexpr int DCH = 32;
-__global__ void __launch_bounds__(128)
+constexpr int DCOLS = 64;   // value columns per workgroup
+__global__ void __launch_bounds__(DCOLS)
 delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
              const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ O) {
-    const int b = blockIdx.x / kHeads, h = blockIdx.x % kHeads, c = threadIdx.x;
-    __shared__ float sq[DCH][64];
-    __shared__ float sk[DCH + 1][64];
+    const int half = blockIdx.x & 1, wh = blockIdx.x >> 1;
+    const int b = wh / kHeads, h = wh % kHeads, c = threadIdx.x;
+    const int col = h * 128 + half * DCOLS + c;   // value column in [0, 768)
+    __shared__ __attribute__((aligned(16))) float sq[DCH][64];
+    __shared__ __attribute__((aligned(16))) float sk[DCH + 1][64];
+    __shared__ float sv[DCH][DCOLS];
     __shared__ float sa[DCH], sb[DCH];
     const long long row0 = (long long)b * kT;
     float S[64];
@@ -117,13 +122,39 @@ delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const flo
     float pred = 0.0f;
     for (int t0 = 0; t0 < kT; t0 += DCH) {
         const int nt = min(DCH, kT - t0);
-        for (int i = threadIdx.x; i < (DCH + 1) * 64; i += 128) {
-            const int tt = i >> 6, j = i & 63, t = t0 + tt;
-            if (tt < DCH) sq[tt][j] = t < kT ? Q[(row0 + t) * kD + h * 64 + j] : 0.0f;
-            // k of token t (t < kT); for the last token, the next-k slot repeats its own k (unused downstream)
-            const int tk = t < kT ? t : kT - 1;
-            sk[tt][j] = K[(row0 + tk) * kD + h * 64 + j];
+        // staging loads are unconditional (token index clamped) so that all of them are in flight together;
+        // slots past the last token are then zeroed (q, v) or repeat the last k (the next-k slot of the last
+        // token, unused downstream)
+        constexpr int QK4 = (DCH + 1) * 16;                       // float4s of q (DCH rows) and k (DCH+1 rows)
+        constexpr int QKR = (QK4 + DCOLS - 1) / DCOLS;
+        float4 rq[QKR], rk[QKR];
+        float rv[DCH];
+#pragma unroll
+        for (int k = 0; k < QKR; ++k) {
+            const int i = threadIdx.x + k * DCOLS;
+            const int tt = i >> 4, j4 = (i & 15) * 4;
+            const int t = min(t0 + tt, kT - 1);
+            rq[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            rk[k] = rq[k];
+            if (i < QK4) {
+                rq[k] = *reinterpret_cast<const float4*>(Q + (row0 + t) * kD + h * 64 + j4);
+                rk[k] = *reinterpret_cast<const float4*>(K + (row0 + t) * kD + h * 64 + j4);
+            }
         }
+#pragma unroll
+        for (int tt = 0; tt < DCH; ++tt) rv[tt] = V[(row0 + min(t0 + tt, kT - 1)) * kVD + col];
+#pragma unroll
+        for (int k = 0; k < QKR; ++k) {
+            const int i = threadIdx.x + k * DCOLS;
+            const int tt = i >> 4, j4 = (i & 15) * 4;
+            if (i < QK4) {
+                if (tt < DCH)
+                    *reinterpret_cast<float4*>(&sq[tt][j4]) = t0 + tt < kT ? rq[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                *reinterpret_cast<float4*>(&sk[tt][j4]) = rk[k];
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < DCH; ++tt) sv[tt][c] = t0 + tt < kT ? rv[tt] : 0.0f;
         if (threadIdx.x < DCH) {
             const int t = t0 + threadIdx.x;
             sa[threadIdx.x] = t < kT ? dec[(row0 + t) * 8 + h] : 0.0f;
@@ -133,18 +164,26 @@ delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const flo
         for (int i = 0; i < nt; ++i) {
             const long long row = row0 + t0 + i;
             const float a = sa[i], bt = sb[i];
-            const float v = V[row * kVD + h * 128 + c];
-            const float u = (v - a * pred) * bt;
+            const float u = (sv[i][c] - a * pred) * bt;
             float o = 0.0f, pn = 0.0f;
+            // q, k and next-k as float4 broadcasts (48 LDS reads per token); j still runs 0..63 in order
 #pragma unroll
-            for (int j = 0; j < 64; ++j) {
-                const float x = __builtin_fmaf(sk[i][j], u, S[j] * a);
-                S[j] = x;
-                o = __builtin_fmaf(x, sq[i][j], o);
-                pn = __builtin_fmaf(x, sk[i + 1][j], pn);
+            for (int j4 = 0; j4 < 64; j4 += 4) {
+                const float4 kk = *reinterpret_cast<const float4*>(&sk[i][j4]);
+                const float4 qq = *reinterpret_cast<const float4*>(&sq[i][j4]);
+                const float4 kn = *reinterpret_cast<const float4*>(&sk[i + 1][j4]);
+                const float kv[4] = {kk.x, kk.y, kk.z, kk.w}, qv[4] = {qq.x, qq.y, qq.z, qq.w},
+                            nv[4] = {kn.x, kn.y, kn.z, kn.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x = __builtin_fmaf(kv[e], u, S[j4 + e] * a);
+                    S[j4 + e] = x;
+                    o = __builtin_fmaf(x, qv[e], o);
+                    pn = __builtin_fmaf(x, nv[e], pn);
+                }
             }
             pred = pn;
-            O[row * kVD + h * 128 + c] = o;
+            O[row * kVD + col] = o;
         }
         __syncthreads();
     }
@@ -354,7 +393,7 @@ void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, c
 }
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
                   int B, hipStream_t s) {
-    hipLaunchKernelGGL(delta_kernel, dim3(B * kHeads), dim3(128), 0, s, Q, K, V, dec, beta, O);
+    hipLaunchKernelGGL(delta_kernel, dim3(B * kHeads * 2), dim3(DCOLS), 0, s, Q, K, V, dec, beta, O);
 }
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s) {
