@@ -38,8 +38,8 @@ template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int
 struct IrCfg {
     static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, KS = KS_, S = S_, TH = TH_, TW = TW_, R = R_;
     // Launch and pipeline style, chosen per block by measurement (they trade registers against latency hiding):
-    //   PERSIST  (MODE bit 0) workgroups loop over (frame, tile) items, loading the next item's input tile while
-    //            computing;
+    //   PERSIST  (MODE bit 0) workgroups loop over (frame, tile) items, loading the next item's input tile into
+    //            registers while computing (else one workgroup per item);
     //   RELOAD   (MODE bit 1) expand / project fragments re-issued right after their last use (one register set,
     //            live across the chunk) instead of expand fragments double-buffered a chunk ahead and project
     //            fragments issued at the top of their own chunk;
@@ -47,6 +47,12 @@ struct IrCfg {
     static constexpr bool PERSIST = (MODE_ & 1) != 0;
     static constexpr bool RELOAD = (MODE_ & 2) != 0;
     static constexpr bool NOSPLIT = (MODE_ & 4) != 0;
+    //   ROLLED   (MODE bit 3) the tile is staged by a rolled copy loop (one float4 in flight per thread at a time)
+    //            instead of grouped loads -- fewer live registers where the grouped form costs a wave per SIMD.
+    static constexpr bool ROLLED = (MODE_ & 8) != 0;
+    //   WHOLE    (MODE bit 4) a non-persistent workgroup issues the loads of its whole tile before storing any
+    //            (else 4 float4s per thread at a time).
+    static constexpr bool WHOLE = (MODE_ & 16) != 0;
     static constexpr int ACT = HS_ ? ACT_HS : ACT_RELU;
     static constexpr bool SE = SE_ != 0;
     static constexpr bool EXPAND = CEXP != CIN;
@@ -91,19 +97,20 @@ template <typename T, class C> struct IrLayout {
 };
 
 // The 15 blocks of MobileNetV3-Large (engine/cuda/model.hpp:23-29) with their output tiles, depthwise strips and
-// launch / pipeline mode (bit 0 persistent, bit 1 reload-after-use, bit 2 fp32 tile; see IrCfg).
+// launch / pipeline mode (bit 0 persistent, bit 1 reload-after-use, bit 2 fp32 tile, bit 3 rolled staging, bit 4
+// whole-tile staging; see IrCfg).
 //                  cin cexp cout k  s hs se TH TW R  mode
 typedef IrCfg<16, 16, 16, 3, 1, 0, 0, 10, 16, 5, 1> B1;    // 90x160
 typedef IrCfg<16, 64, 24, 3, 2, 0, 0, 5, 8, 1, 4> B2;      // 90x160 -> 45x80
-typedef IrCfg<24, 72, 24, 3, 1, 0, 0, 9, 16, 3, 0> B3;     // 45x80
+typedef IrCfg<24, 72, 24, 3, 1, 0, 0, 9, 16, 3, 8> B3;     // 45x80
 typedef IrCfg<24, 72, 40, 5, 2, 0, 1, 4, 8, 1, 3> B4;      // 45x80 -> 23x40
 typedef IrCfg<40, 120, 40, 5, 1, 0, 1, 8, 8, 2, 2> B5;     // 23x40 (b5, b6)
-typedef IrCfg<40, 240, 80, 3, 2, 1, 0, 4, 10, 1, 2> B7;    // 23x40 -> 12x20
+typedef IrCfg<40, 240, 80, 3, 2, 1, 0, 4, 10, 1, 18> B7;    // 23x40 -> 12x20
 typedef IrCfg<80, 200, 80, 3, 1, 1, 0, 6, 10, 2, 2> B8;    // 12x20
 typedef IrCfg<80, 184, 80, 3, 1, 1, 0, 6, 10, 2, 2> B9;    // 12x20 (b9, b10)
 typedef IrCfg<80, 480, 112, 3, 1, 1, 1, 6, 10, 2, 3> B11;  // 12x20
 typedef IrCfg<112, 672, 112, 3, 1, 1, 1, 6, 10, 2, 0> B12; // 12x20
-typedef IrCfg<112, 672, 160, 5, 2, 1, 1, 3, 5, 1, 0> B13;  // 12x20 -> 6x10
+typedef IrCfg<112, 672, 160, 5, 2, 1, 1, 3, 5, 1, 8> B13;  // 12x20 -> 6x10
 typedef IrCfg<160, 960, 160, 5, 1, 1, 1, 3, 5, 1, 4> B14;  // 6x10 (b14, b15)
 
 template <typename T, class C>
@@ -178,28 +185,33 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
     constexpr int XQ = L::PRESPLIT ? C::CINP / 4 : C::CIN / 4;   // float4 columns per tile row
     constexpr int XROWS = L::PRESPLIT ? L::XH_ROWS : C::PIN;
     constexpr int XN = XROWS * XQ;
-    constexpr int XR = C::PERSIST ? (XN + IR_THREADS - 1) / IR_THREADS : 1;
-    float4 xr[XR];
-    auto load_x = [&](int item) {
+    constexpr int XR = (XN + IR_THREADS - 1) / IR_THREADS;
+    float4 xr[(C::PERSIST || C::WHOLE) ? XR : (XR < 4 ? XR : 4)];
+    // staging of one tile in groups of float4s per thread: within a group every load is issued (at a clamped,
+    // always valid address) before any is used; positions outside the map or the channel count take zero.
+    // Persistent workgroups hold the whole next tile in registers; the others stage 4 float4s at a time.
+    constexpr int XG = (C::PERSIST || C::WHOLE) ? XR : (XR < 4 ? XR : 4);
+    auto load_x = [&](int item, int k0) {
         const int tile = item % a.ntiles;
         const long long f = item / a.ntiles;
         const int iy0 = (tile / a.tiles_x) * C::TH * C::S - C::PAD, ix0 = (tile % a.tiles_x) * C::TW * C::S - C::PAD;
         const float* Xf = a.X + f * a.H * a.W * C::CIN;
 #pragma unroll
-        for (int k = 0; k < XR; ++k) {
-            const int i = tid + k * IR_THREADS;
+        for (int k = 0; k < XG; ++k) {
+            const int i = tid + (k0 + k) * IR_THREADS;
             const int row = i / XQ, q = i - row * XQ;
             const int ly = row / C::IW, lx = row - ly * C::IW;
             const int iy = iy0 + ly, ix = ix0 + lx;
-            xr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (i < XN && row < C::PIN && q * 4 < C::CIN && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
-                xr[k] = *reinterpret_cast<const float4*>(Xf + ((long long)iy * a.W + ix) * C::CIN + q * 4);
+            const bool in = i < XN && row < C::PIN && q * 4 < C::CIN && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
+            const int cy = min(max(iy, 0), a.H - 1), cx = min(max(ix, 0), a.W - 1), cq = min(q, C::CIN / 4 - 1);
+            const float4 v = *reinterpret_cast<const float4*>(Xf + ((long long)cy * a.W + cx) * C::CIN + cq * 4);
+            xr[k] = in ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     };
-    auto store_x = [&]() {
+    auto store_x = [&](int k0) {
 #pragma unroll
-        for (int k = 0; k < XR; ++k) {
-            const int i = tid + k * IR_THREADS;
+        for (int k = 0; k < XG; ++k) {
+            const int i = tid + (k0 + k) * IR_THREADS;
             if (i >= XN) continue;
             const int row = i / XQ, q = i - row * XQ;
             if constexpr (L::PRESPLIT) {
@@ -219,37 +231,6 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
         }
     };
 
-    // non-persistent launches stage their one tile straight from global memory to LDS (a rolled loop: one float4
-    // live at a time)
-    auto stage_direct = [&](int item) {
-        const int tile = item % a.ntiles;
-        const long long f = item / a.ntiles;
-        const int iy0 = (tile / a.tiles_x) * C::TH * C::S - C::PAD, ix0 = (tile % a.tiles_x) * C::TW * C::S - C::PAD;
-        const float* Xf = a.X + f * a.H * a.W * C::CIN;
-        for (int i = tid; i < XN; i += IR_THREADS) {
-            const int row = i / XQ, q = i - row * XQ;
-            const int ly = row / C::IW, lx = row - ly * C::IW;
-            const int iy = iy0 + ly, ix = ix0 + lx;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (row < C::PIN && q * 4 < C::CIN && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
-                v = *reinterpret_cast<const float4*>(Xf + ((long long)iy * a.W + ix) * C::CIN + q * 4);
-            if constexpr (L::PRESPLIT) {
-                const float x[4] = {v.x, v.y, v.z, v.w};
-                T part[4][S::P];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
-#pragma unroll
-                for (int pq = 0; pq < S::P; ++pq) {
-                    T four[4] = {part[0][pq], part[1][pq], part[2][pq], part[3][pq]};
-                    *reinterpret_cast<uint2*>(Xh + (pq * L::XH_ROWS + row) * L::XH_LD + q * 4) =
-                        *reinterpret_cast<const uint2*>(four);
-                }
-            } else {
-                *reinterpret_cast<float4*>(Xs + row * C::XS_LD + q * 4) = v;
-            }
-        }
-    };
-
     fetch_wd(0);
     if constexpr (PF_EXP) load_ew_into(ew_n, 0);
     if constexpr (C::RELOAD) {
@@ -257,7 +238,7 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
         load_pw(0);
     }
     if constexpr (C::PERSIST) {
-        if ((int)blockIdx.x < items) load_x(blockIdx.x);
+        if ((int)blockIdx.x < items) load_x(blockIdx.x, 0);
     }
 
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
@@ -268,10 +249,36 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
         const float* Xf = a.X + f * a.H * a.W * C::CIN;
 
         if constexpr (C::PERSIST) {
-            store_x();
-            if (item + (int)gridDim.x < items) load_x(item + gridDim.x);
+            store_x(0);
+            if (item + (int)gridDim.x < items) load_x(item + gridDim.x, 0);
+        } else if constexpr (C::ROLLED) {
+            for (int i = tid; i < XN; i += IR_THREADS) {
+                const int row = i / XQ, q = i - row * XQ;
+                const int ly = row / C::IW, lx = row - ly * C::IW;
+                const int iy = iy0 + ly, ix = ix0 + lx;
+                float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (row < C::PIN && q * 4 < C::CIN && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
+                    v = *reinterpret_cast<const float4*>(Xf + ((long long)iy * a.W + ix) * C::CIN + q * 4);
+                if constexpr (L::PRESPLIT) {
+                    const float x[4] = {v.x, v.y, v.z, v.w};
+                    T part[4][S::P];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
+#pragma unroll
+                    for (int pq = 0; pq < S::P; ++pq) {
+                        T four[4] = {part[0][pq], part[1][pq], part[2][pq], part[3][pq]};
+                        *reinterpret_cast<uint2*>(Xh + (pq * L::XH_ROWS + row) * L::XH_LD + q * 4) =
+                            *reinterpret_cast<const uint2*>(four);
+                    }
+                } else {
+                    *reinterpret_cast<float4*>(Xs + row * C::XS_LD + q * 4) = v;
+                }
+            }
         } else {
-            stage_direct(item);
+            for (int k0 = 0; k0 < XR; k0 += XG) {
+                load_x(item, k0);
+                store_x(k0);
+            }
         }
         // Ds entries the depthwise never writes (channels past cexp of a narrow block, rows past the tile) stay 0
         for (int i = tid; i < C::DS_FLOATS; i += IR_THREADS) Ds[i] = 0.0f;
@@ -595,17 +602,30 @@ __global__ void __launch_bounds__(IR_THREADS) ir_se_wave_kernel(IrArgs a) {
     };
     if (wave < C::NCH) fetch(wave * WCW);
 
-    // ---- input tile (+halo, zero outside the map and in the K padding) -> LDS, split into the operand parts
+    // ---- input tile (+halo, zero outside the map and in the K padding) -> LDS, split into the operand parts.
+    // All loads are issued (at clamped, always valid addresses) before any is used: the tile is in flight at once.
     {
         constexpr int XQ = C::CINP / 4;
-        for (int i = tid; i < C::XH_ROWS * XQ; i += IR_THREADS) {
+        constexpr int XN = C::XH_ROWS * XQ;
+        constexpr int XR = (XN + IR_THREADS - 1) / IR_THREADS;
+        float4 xr[XR];
+#pragma unroll
+        for (int k = 0; k < XR; ++k) {
+            const int i = tid + k * IR_THREADS;
             const int row = i / XQ, q = i - row * XQ;
             const int ly = row / C::IW, lx = row - ly * C::IW;
             const int iy = iy0 + ly, ix = ix0 + lx;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (row < C::PIN && q * 4 < C::CIN && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W)
-                v = *reinterpret_cast<const float4*>(Xf + ((long long)iy * a.W + ix) * C::CIN + q * 4);
-            const float x[4] = {v.x, v.y, v.z, v.w};
+            const bool in = i < XN && row < C::PIN && q * 4 < C::CIN && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
+            const int cy = min(max(iy, 0), a.H - 1), cx = min(max(ix, 0), a.W - 1), cq = min(q, C::CIN / 4 - 1);
+            const float4 v = *reinterpret_cast<const float4*>(Xf + ((long long)cy * a.W + cx) * C::CIN + cq * 4);
+            xr[k] = in ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < XR; ++k) {
+            const int i = tid + k * IR_THREADS;
+            if (i >= XN) continue;
+            const int row = i / XQ, q = i - row * XQ;
+            const float x[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
             T part[4][S::P];
 #pragma unroll
             for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
