@@ -140,43 +140,48 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = 0; k0 < p.K; k0 += 32) {
+        // all loads of the K step are issued unconditionally (rows, columns and K clamped into range) before any
+        // is used, then out-of-range values are zeroed: one wait per step instead of one per tile
         const int kk = k0 + g * 8;
         const bool kin = kk < p.K;
+        const int kc = kin ? kk : p.K - 8;
         V8 a[MFMA_MT][S::P], b[NT][S::P];
+        float x[MFMA_MT][8], sc[SCALE ? MFMA_MT : 1][8];
+        uint4 wv[NT][S::P];
 #pragma unroll
         for (int mt = 0; mt < MFMA_MT; ++mt) {
             const long long row = mbase + mt * 16 + r;
-            float x[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-            if (kin && row < p.M) {
-                load8(p.A + row * p.lda + kk, x);
-                if (SCALE) {
-                    float sc[8];
-                    load8(p.scale + (row / p.scale_rows) * p.ld_scale + kk, sc);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) x[e] = sc[e] * x[e];
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                T part[S::P];
-                S::split(x[e], part);
-#pragma unroll
-                for (int q = 0; q < S::P; ++q) a[mt][q][e] = part[q];
-            }
+            const long long rc = row < p.M ? row : p.M - 1;
+            load8(p.A + rc * p.lda + kc, x[mt]);
+            if constexpr (SCALE) load8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, sc[mt]);
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int col = nbase + nt * 16 + r;
+            const int cc = col < p.N ? col : p.N - 1;
+#pragma unroll
+            for (int q = 0; q < S::P; ++q)
+                wv[nt][q] = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)cc * p.ldw + kc);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MFMA_MT; ++mt) {
+            const bool live = kin && mbase + mt * 16 + r < p.M;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float t = x[mt][e];
+                if constexpr (SCALE) t = sc[mt][e] * t;
+                v[e] = live ? t : 0.0f;
+            }
+            split8<T>(v, a[mt]);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const bool live = kin && nbase + nt * 16 + r < p.N;
 #pragma unroll
             for (int q = 0; q < S::P; ++q) {
-                V8 v = {};
-                if (kin && col < p.N) {
-                    const uint4 u = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)col * p.ldw + kk);
-                    v = *reinterpret_cast<const V8*>(&u);
-                }
-                b[nt][q] = v;
+                const uint4 u = live ? wv[nt][q] : make_uint4(0u, 0u, 0u, 0u);
+                b[nt][q] = *reinterpret_cast<const V8*>(&u);
             }
         }
 #pragma unroll
