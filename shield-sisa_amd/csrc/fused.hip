@@ -19,6 +19,7 @@
 #include "mfma.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <stdexcept>
 
 namespace shv {
@@ -844,6 +845,9 @@ template <typename T, class W, class C> void launch_se(const IrArgs& a, int F, h
 
 template <typename T> void launch_ir_block(int block, const IrArgs& a, int F, hipStream_t s) {
     if (F <= 0) return;
+    // blocks 1-3 run in the strip kernel unless SHV_HIP_NO_STRIP is set (tile kernels kept for comparison)
+    static const bool strip = std::getenv("SHV_HIP_NO_STRIP") == nullptr;
+    if (strip && launch_ir_strip<T>(block, a, F, s)) return;
     switch (block) {
     case 0: launch_cfg<T, B1>(a, F, s); break;
     case 1: launch_cfg<T, B2>(a, F, s); break;

@@ -1,0 +1,386 @@
+// Fused inverted-residual blocks 1-3 of MobileNetV3-Large (3x3 depthwise, ReLU, no squeeze-excite) for the fp16 /
+// bf16 tiers, in a pixel-per-lane layout that keeps every intermediate in registers.
+//
+// Each wave works alone on a column strip of one frame, 16 lanes wide, walking down the map R output rows per
+// step.  The expand runs transposed, E^T[ch][px] = Wexp[ch][:] . X^T[:][px], on v_mfma_f32_16x16x16 with split
+// operands; its result fragment gives lane (r, g) = (16 g + r) pixel r of the strip and channels 4 g .. 4 g + 3 of
+// a 16-channel tile.  In that layout
+//   * the depthwise neighbours along x are lanes r - 1 / r + 1 of the same 16-lane row (DPP row shifts), the
+//     neighbours along y are other rows held by the same lane, and the tap weights are broadcast from lane t of a
+//     register that holds the 9 taps and the bias of the lane row's 4 channels (DPP row_newbcast);
+//   * the depthwise result is exactly the B fragment (k = channels 4 g .., column = pixel r) of the projection
+//     Y^T = Wproj^T . D^T, whose result is again one pixel per lane with 4 consecutive output channels -- one
+//     float4 store into the NHWC output.
+// So the expanded tensor never leaves the registers, and nothing but the weights uses LDS.  A 16-lane strip
+// yields 14 output columns at stride 1 (lanes 1 .. 14; lanes 0 and 15 only provide the x halo) and 15 at
+// stride 2 (the row holds the even input columns in one tile and the odd ones in another; lane 0's odd column is
+// the left halo).  Rows outside the map give E = 0 (uniform per step); columns outside the map give E = 0
+// because the expand accumulator starts at -inf there (ReLU(-inf) = 0).
+//
+// Numerics: the same split-operand products as the other fused kernels; expand and project accumulators start
+// from their bias, the depthwise chain runs over (dy, dx) in order and adds its bias last.  Per-element results
+// therefore differ from the layer path by accumulation rounding only.
+#include "dev_common.hpp"
+#include "kernels.hpp"
+#include "mfma.hpp"
+
+#include <algorithm>
+#include <stdexcept>
+#include <type_traits>
+
+namespace shv {
+namespace {
+
+constexpr int ST_THREADS = 256;   // 4 independent waves; the workgroup shares the LDS copy of the weights
+
+// v_mfma_f32_16x16x16 fragments (lane l = 16 g + r): A row r, k = 4 g .. 4 g + 3; B column r, k = 4 g ..
+// 4 g + 3; C column r, rows 4 g .. 4 g + 3.  Products as in Split<T> (smallest first).
+template <typename T> struct Split16;
+template <> struct Split16<f16> {
+    typedef _Float16 V4 __attribute__((ext_vector_type(4)));
+    static __device__ __forceinline__ f32x4 mfma(V4 a, V4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ _Float16 bits(f16 x) { return x; }
+};
+template <> struct Split16<bf16> {
+    typedef short V4 __attribute__((ext_vector_type(4)));
+    static __device__ __forceinline__ f32x4 mfma(V4 a, V4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ short bits(bf16 x) { return __builtin_bit_cast(short, x); }
+};
+
+// float4 -> the P part fragments (k = the 4 values)
+template <typename T> __device__ __forceinline__ void split4(const float4 v, typename Split16<T>::V4* parts) {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        T p[Split<T>::P];
+        Split<T>::split(x[e], p);
+#pragma unroll
+        for (int q = 0; q < Split<T>::P; ++q) parts[q][e] = Split16<T>::bits(p[q]);
+    }
+}
+// acc += W . A over the split products; w = weight parts (A operand), x = activation parts (B operand)
+template <typename T>
+__device__ __forceinline__ f32x4 mfma_split16(const typename Split16<T>::V4* w, const typename Split16<T>::V4* x,
+                                              f32x4 acc) {
+#pragma unroll
+    for (int i = 0; i < Split<T>::NPROD; ++i) acc = Split16<T>::mfma(w[Split<T>::wp(i)], x[Split<T>::ap(i)], acc);
+    return acc;
+}
+
+// 8 bytes of LDS -> one part fragment
+template <typename T> __device__ __forceinline__ typename Split16<T>::V4 lds_frag(const T* p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return __builtin_bit_cast(typename Split16<T>::V4, u);
+}
+
+__device__ __forceinline__ float row_shr1(float v) {   // lane r <- lane r - 1 of its 16-lane row (lane 0 <- 0)
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float row_shl1(float v) {   // lane r <- lane r + 1 of its 16-lane row (lane 15 <- 0)
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x101, 0xf, 0xf, true));
+}
+
+// 3x3 depthwise output: ((e0 w0 + e1 w1) + ... + e8 w8) + bias as an fma chain, with tap t's weight taken from
+// lane t and the bias from lane 9 of wv's 16-lane row.  The leading s_nop covers the two wait states a DPP read
+// needs after a VALU write of its source register.
+__device__ __forceinline__ float dw9(float wv, float e0, float e1, float e2, float e3, float e4, float e5, float e6,
+                                     float e7, float e8) {
+    float acc;
+    asm("s_nop 1\n\t"
+        "v_mul_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %0, %1, %0 row_newbcast:9 row_mask:0xf bank_mask:0xf"
+        : "=&v"(acc)
+        : "v"(wv), "v"(e0), "v"(e1), "v"(e2), "v"(e3), "v"(e4), "v"(e5), "v"(e6), "v"(e7), "v"(e8));
+    return acc;
+}
+
+template <int CIN_, int CEXP_, int COUT_, int S_, int R_>
+struct StripCfg {
+    static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, S = S_, R = R_;
+    static constexpr bool EXPAND = CIN != CEXP;
+    static constexpr bool RES = S == 1 && CIN == COUT;
+    static constexpr int KSI = (CIN + 15) / 16;              // expand K steps
+    static constexpr int CT = (CEXP + 15) / 16;              // expanded-channel tiles
+    static constexpr int OT = (COUT + 15) / 16;              // output-channel tiles
+    static constexpr int VALID = S == 1 ? 14 : 15;           // output columns per strip (lanes 1 .. VALID)
+    static constexpr int NT = S;                             // pixel tiles per input row (stride 2: even, odd)
+    static constexpr int IR = S == 1 ? R + 2 : 2 * R + 1;    // input rows per step
+    static constexpr int KP = KSI * 16 + 4;                  // LDS row stride (elements) of the expand weights
+    static constexpr int CP = CT * 16 + 4;                   // LDS row stride of the project weights
+    static_assert(CIN % 4 == 0 && COUT % 4 == 0, "channel counts must be multiples of 4");
+    static_assert(EXPAND || (CT == 1 && KSI == 1), "blocks without expand have one 16-channel tile");
+};
+
+//                  cin cexp cout s  R
+typedef StripCfg<16, 16, 16, 1, 6> S1;    // 90x160
+typedef StripCfg<16, 64, 24, 2, 1> S2;    // 90x160 -> 45x80
+typedef StripCfg<24, 72, 24, 1, 2> S3;    // 45x80
+
+template <typename T, class C> struct StripLds {
+    static constexpr int P = Split<T>::P;
+    static constexpr int WE = C::EXPAND ? P * C::CT * 16 * C::KP : 0;   // T elements
+    static constexpr int WP = P * C::OT * 16 * C::CP;
+    static constexpr int BE = C::EXPAND ? 2 * C::CT * 16 : 0;           // floats: expand bias, then -inf
+    static constexpr int BYTES = (WE + WP) * (int)sizeof(T) + BE * 4;
+};
+
+template <typename T, class C>
+__global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int strips, int items) {
+    typedef Split16<T> S16;
+    typedef typename S16::V4 V4;
+    typedef StripLds<T, C> L;
+    constexpr int P = Split<T>::P;
+    __shared__ __attribute__((aligned(16))) unsigned char lds_raw[(L::BYTES + 15) / 16 * 16];
+    T* We = reinterpret_cast<T*>(lds_raw);                               // [P][CT*16][KP]
+    T* Wp = We + L::WE;                                                  // [P][OT*16][CP]
+    float* Be = reinterpret_cast<float*>(lds_raw + (L::WE + L::WP) * sizeof(T));   // [2][CT*16]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+
+    // ---- weights -> LDS (the only workgroup-wide step)
+    {
+        const T* wexp = static_cast<const T*>(a.wexp);
+        const T* wproj = static_cast<const T*>(a.wproj);
+        constexpr int CEXPP = (C::CEXP + 31) / 32 * 32, CINP = (C::CIN + 31) / 32 * 32, COUTP = C::OT * 16;
+        if constexpr (C::EXPAND) {
+            for (int i = tid; i < P * C::CT * 16 * C::KSI * 16; i += ST_THREADS) {
+                const int k = i % (C::KSI * 16), rest = i / (C::KSI * 16);
+                const int c = rest % (C::CT * 16), q = rest / (C::CT * 16);
+                We[(q * C::CT * 16 + c) * C::KP + k] = wexp[q * a.wexp_stride + (long long)c * CINP + k];
+            }
+            for (int i = tid; i < C::CT * 16; i += ST_THREADS) {
+                Be[i] = a.bexp[i];
+                Be[C::CT * 16 + i] = -__builtin_inff();
+            }
+        }
+        for (int i = tid; i < P * COUTP * C::CT * 16; i += ST_THREADS) {
+            const int k = i % (C::CT * 16), rest = i / (C::CT * 16);
+            const int o = rest % COUTP, q = rest / COUTP;
+            Wp[(q * COUTP + o) * C::CP + k] = wproj[q * a.wproj_stride + (long long)o * CEXPP + k];
+        }
+        (void)CEXPP;
+    }
+    __syncthreads();
+
+    // ---- per-lane constants: depthwise taps + bias (lane r <= 9 of each row: tap r, bias), project bias
+    constexpr int CEXPP_DW = (C::CEXP + 31) / 32 * 32;
+    float wdw[C::CT][4];
+#pragma unroll
+    for (int ct = 0; ct < C::CT; ++ct) {
+        const int c = ct * 16 + 4 * g;
+        const float* src = r < 9 ? a.wdw + r * CEXPP_DW + c : a.bdw + c;
+        const float4 v = *reinterpret_cast<const float4*>(src);
+        wdw[ct][0] = v.x; wdw[ct][1] = v.y; wdw[ct][2] = v.z; wdw[ct][3] = v.w;
+    }
+    f32x4 pb[C::OT];
+#pragma unroll
+    for (int ot = 0; ot < C::OT; ++ot) {
+        const float4 v = *reinterpret_cast<const float4*>(a.bproj + ot * 16 + 4 * g);
+        pb[ot] = f32x4{v.x, v.y, v.z, v.w};
+    }
+
+    const int H = a.H, W = a.W, Ho = a.Ho, Wo = a.Wo;
+    for (int item = blockIdx.x * (ST_THREADS / 64) + wave; item < items; item += gridDim.x * (ST_THREADS / 64)) {
+        const int strip = item % strips;
+        const long long f = item / strips;
+        const int ox = strip * C::VALID + r - 1;                   // this lane's output column
+        int ixc[C::NT];
+        bool pin[C::NT];
+#pragma unroll
+        for (int t = 0; t < C::NT; ++t) {
+            const int ix = C::S == 1 ? ox : 2 * ox + t;
+            pin[t] = ix >= 0 && ix < W;
+            ixc[t] = min(max(ix, 0), W - 1);
+        }
+        const bool store_lane = r >= 1 && r <= C::VALID && ox < Wo;
+        const float* Xf = a.X + f * H * W * C::CIN;
+        float* Yf = a.Y + f * Ho * Wo * C::COUT;
+        // expand accumulator start: the bias, or -inf for columns outside the map
+        int be_off[C::NT];
+#pragma unroll
+        for (int t = 0; t < C::NT; ++t) be_off[t] = pin[t] ? 0 : C::CT * 16;
+
+        for (int oy0 = 0; oy0 < Ho; oy0 += C::R) {
+            const int iy0 = C::S * oy0 - 1;
+            // ---- the step's input rows: fp32 (no expand) or split into B fragments
+            V4 xf[C::EXPAND ? C::IR : 1][C::NT][C::KSI][P];
+            float4 xe[C::EXPAND ? 1 : C::IR];
+            bool rin[C::IR];
+#pragma unroll
+            for (int j = 0; j < C::IR; ++j) {
+                const int iy = iy0 + j;
+                rin[j] = iy >= 0 && iy < H;
+                const int iyc = min(max(iy, 0), H - 1);
+#pragma unroll
+                for (int t = 0; t < C::NT; ++t)
+#pragma unroll
+                    for (int ks = 0; ks < C::KSI; ++ks) {
+                        const int ch = min(ks * 16 + 4 * g, C::CIN - 4);
+                        const float4 v =
+                            *reinterpret_cast<const float4*>(Xf + ((long long)iyc * W + ixc[t]) * C::CIN + ch);
+                        if constexpr (C::EXPAND) {
+                            split4<T>(v, xf[j][t][ks]);
+                        } else {
+                            const bool ok = rin[j] && pin[0];
+                            xe[j] = ok ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                        }
+                    }
+            }
+            f32x4 y[C::R][C::OT];
+#pragma unroll
+            for (int q = 0; q < C::R; ++q)
+#pragma unroll
+                for (int ot = 0; ot < C::OT; ++ot) y[q][ot] = pb[ot];
+
+#pragma unroll
+            for (int ct = 0; ct < C::CT; ++ct) {
+                // ---- expanded rows of this channel tile (fp32, zero outside the map)
+                f32x4 e[C::IR][C::NT];
+                if constexpr (C::EXPAND) {
+                    V4 wf[C::KSI][P];
+#pragma unroll
+                    for (int ks = 0; ks < C::KSI; ++ks)
+#pragma unroll
+                        for (int q = 0; q < P; ++q)
+                            wf[ks][q] = lds_frag<T>(We + (q * C::CT * 16 + ct * 16 + r) * C::KP + ks * 16 + 4 * g);
+                    f32x4 init[C::NT];
+#pragma unroll
+                    for (int t = 0; t < C::NT; ++t) {
+                        const float4 b = *reinterpret_cast<const float4*>(Be + be_off[t] + ct * 16 + 4 * g);
+                        init[t] = f32x4{b.x, b.y, b.z, b.w};
+                    }
+#pragma unroll
+                    for (int j = 0; j < C::IR; ++j)
+#pragma unroll
+                        for (int t = 0; t < C::NT; ++t) {
+                            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                            if (rin[j]) {   // uniform: the whole wave is on the same input row
+                                acc = init[t];
+#pragma unroll
+                                for (int ks = 0; ks < C::KSI; ++ks) acc = mfma_split16<T>(wf[ks], xf[j][t][ks], acc);
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) acc[i] = relu(acc[i]);
+                            }
+                            e[j][t] = acc;
+                        }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < C::IR; ++j) e[j][0] = f32x4{xe[j].x, xe[j].y, xe[j].z, xe[j].w};
+                }
+                // ---- left / right neighbours along x
+                f32x4 el[C::IR], er[C::S == 1 ? C::IR : 1];
+#pragma unroll
+                for (int j = 0; j < C::IR; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if constexpr (C::S == 1) {
+                            el[j][i] = row_shr1(e[j][0][i]);
+                            er[j][i] = row_shl1(e[j][0][i]);
+                        } else {
+                            el[j][i] = row_shr1(e[j][1][i]);
+                        }
+                    }
+                V4 wp[C::OT][P];
+#pragma unroll
+                for (int ot = 0; ot < C::OT; ++ot)
+#pragma unroll
+                    for (int q = 0; q < P; ++q)
+                        wp[ot][q] = lds_frag<T>(Wp + (q * C::OT * 16 + ot * 16 + r) * C::CP + ct * 16 + 4 * g);
+                // ---- depthwise + ReLU, then the projection of this channel tile, one output row at a time
+#pragma unroll
+                for (int qr = 0; qr < C::R; ++qr) {
+                    const int j0 = C::S * qr;
+                    float d[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float v;
+                        if constexpr (C::S == 1)
+                            v = dw9(wdw[ct][i], el[j0][i], e[j0][0][i], er[j0][i], el[j0 + 1][i], e[j0 + 1][0][i],
+                                    er[j0 + 1][i], el[j0 + 2][i], e[j0 + 2][0][i], er[j0 + 2][i]);
+                        else
+                            v = dw9(wdw[ct][i], el[j0][i], e[j0][0][i], e[j0][1][i], el[j0 + 1][i], e[j0 + 1][0][i],
+                                    e[j0 + 1][1][i], el[j0 + 2][i], e[j0 + 2][0][i], e[j0 + 2][1][i]);
+                        d[i] = relu(v);
+                    }
+                    V4 df[P];
+                    split4<T>(make_float4(d[0], d[1], d[2], d[3]), df);
+#pragma unroll
+                    for (int ot = 0; ot < C::OT; ++ot) y[qr][ot] = mfma_split16<T>(wp[ot], df, y[qr][ot]);
+                }
+            }
+
+            // ---- epilogue: (+ residual) and one float4 per (row, output tile) per lane
+#pragma unroll
+            for (int qr = 0; qr < C::R; ++qr) {
+                const int oy = oy0 + qr;
+                if (oy >= Ho) break;
+#pragma unroll
+                for (int ot = 0; ot < C::OT; ++ot) {
+                    const int n = ot * 16 + 4 * g;
+                    if (!store_lane || n >= C::COUT) continue;
+                    float4 v = make_float4(y[qr][ot][0], y[qr][ot][1], y[qr][ot][2], y[qr][ot][3]);
+                    if constexpr (C::RES) {
+                        float4 x;
+                        if constexpr (C::EXPAND)
+                            x = *reinterpret_cast<const float4*>(Xf + ((long long)oy * W + ox) * C::CIN + n);
+                        else
+                            x = xe[qr + 1];
+                        v.x = x.x + v.x; v.y = x.y + v.y; v.z = x.z + v.z; v.w = x.w + v.w;
+                    }
+                    *reinterpret_cast<float4*>(Yf + ((long long)oy * Wo + ox) * C::COUT + n) = v;
+                }
+            }
+        }
+    }
+}
+
+template <typename T, class C> void launch_strip(int block, const IrArgs& a, int F, hipStream_t s) {
+    // the engine pads the weights to the block's IrShape; the kernel reads them with these paddings
+    const IrShape sh = ir_shape(block, std::is_same<T, bf16>::value);
+    if (sh.cin != C::CIN || sh.cexp != C::CEXP || sh.cout != C::COUT || sh.k != 3 || sh.stride != C::S || sh.se ||
+        sh.hs || sh.cinp != (C::CIN + 31) / 32 * 32 || sh.cexpp != (C::CEXP + 31) / 32 * 32 || sh.coutp != C::OT * 16)
+        throw std::runtime_error("ir_strip: weight padding disagrees with the block shape");
+    const int strips = (a.Wo + C::VALID - 1) / C::VALID;
+    if ((C::S == 1 && (a.Ho != a.H || a.Wo != a.W)) || (C::S == 2 && (a.Ho != (a.H + 1) / 2 || a.Wo != (a.W + 1) / 2)))
+        throw std::runtime_error("ir_strip: map shape does not match the stride");
+    if (a.frames != F || (long long)F * strips > (1ll << 30)) throw std::runtime_error("ir_strip: bad frame count");
+    const int items = F * strips;
+    // persistent workgroups: as many as the device holds at once (per-instantiation occupancy, cached)
+    static const int resident = [] {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_strip_kernel<T, C>, ST_THREADS, 0) != hipSuccess)
+            throw std::runtime_error("ir_strip: cannot query the device occupancy");
+        return std::max(1, cus) * std::max(1, per_cu);
+    }();
+    const int waves_per_wg = ST_THREADS / 64;
+    const int grid = std::min((items + waves_per_wg - 1) / waves_per_wg, resident);
+    hipLaunchKernelGGL((ir_strip_kernel<T, C>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, items);
+}
+
+}  // namespace
+
+template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hipStream_t s) {
+    switch (block) {
+    case 0: launch_strip<T, S1>(block, a, F, s); return true;
+    case 1: launch_strip<T, S2>(block, a, F, s); return true;
+    case 2: launch_strip<T, S3>(block, a, F, s); return true;
+    default: return false;
+    }
+}
+template bool launch_ir_strip<f16>(int, const IrArgs&, int, hipStream_t);
+template bool launch_ir_strip<bf16>(int, const IrArgs&, int, hipStream_t);
+
+}  // namespace shv

@@ -218,11 +218,12 @@ def test_forward_device_matches_predict(shv, weights, clips):
 @pytest.mark.parametrize("mode", ["fp16", "bf16"])
 def test_fused_blocks_match_layer_path(shv, weights, clips, mode):
     """The fused inverted-residual kernels against the layer-by-layer path of the same tier (SHV_HIP_NO_FUSE).
-    Blocks 1-3 (no squeeze-excite) perform identical arithmetic, so their outputs are bitwise equal.  From block 4 on
-    the SE mean sums per-tile partials in another fixed order; the random-init encoder amplifies that rounding
-    difference smoothly through the late blocks (measured: 1.6e-7 relative after block 4, 9e-6 after block 12,
-    1.4e-4 after block 15), so later stages are held to 1e-3 of the stage's largest magnitude -- a wrong weight,
-    channel or tap moves them by O(1)."""
+    The stem is the same kernel in both paths (bitwise equal).  Blocks 1-3 run in the strip kernel, whose expand and
+    project accumulators start from the bias and whose K = 16 matrix steps round in another order than the layer
+    GEMMs: accumulation rounding only, held to 1e-5 of the stage's largest magnitude.  From block 4 on the SE mean
+    also sums per-tile partials in another fixed order; the random-init encoder amplifies such rounding differences
+    smoothly through the late blocks (measured: 1.6e-7 relative after block 4, 9e-6 after block 12, 1.4e-4 after
+    block 15), so later stages are held to 1e-3 -- a wrong weight, channel, tap or pixel moves them by O(1)."""
     print(f"[gpu] {mode} fused vs layer-by-layer stage dumps", flush=True)
     dumps = {}
     for fuse in (False, True):
@@ -242,9 +243,9 @@ def test_fused_blocks_match_layer_path(shv, weights, clips, mode):
         a, b = dumps[True][name], dumps[False][name]
         assert a.shape == b.shape, name
         assert np.all(np.isfinite(a)), name
-        if name in ("cnn00", "cnn01", "cnn02", "cnn03"):
+        if name == "cnn00":
             assert np.array_equal(a, b), (name, float(np.abs(a - b).max()))
         else:
             err = float(np.abs(a - b).max()) / max(1e-30, float(np.abs(b).max()))
             print(f"[gpu] {mode} {name}: max rel diff {err:.2e}", flush=True)
-            assert err <= 1e-3, (name, err)
+            assert err <= (1e-5 if name in ("cnn01", "cnn02", "cnn03") else 1e-3), (name, err)
