@@ -124,14 +124,22 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
 constexpr int MFMA_MT = 4;      // 16-row tiles per wave (64 rows)
 constexpr int MFMA_WAVES = 4;   // waves per block, stacked along M (256 rows)
 
+// Workgroup order: the 1-D grid is dealt round robin over the 8 XCDs (each with its own L2); workgroup id goes to
+// XCD id % 8, and the column blocks of one row block take consecutive ids on the same XCD, so the second column
+// block reads its rows of A from that L2 instead of HBM.
+constexpr int XCDS = 8;
+
 template <typename T, int NT, bool SCALE>
-__global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p, int mblocks, int nblocks) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
-    const long long mbase = ((long long)blockIdx.x * MFMA_WAVES + wave) * (MFMA_MT * 16);
-    const int nbase = blockIdx.y * (NT * 16);
+    const int xcd = blockIdx.x % XCDS, slot = blockIdx.x / XCDS;
+    const int mb = (slot / nblocks) * XCDS + xcd, nb = slot % nblocks;
+    if (mb >= mblocks) return;
+    const long long mbase = ((long long)mb * MFMA_WAVES + wave) * (MFMA_MT * 16);
+    const int nbase = nb * (NT * 16);
     if (mbase >= p.M) return;
     const T* W = static_cast<const T*>(p.W);
     f32x4 acc[MFMA_MT][NT];
@@ -153,7 +161,14 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p
             const long long row = mbase + mt * 16 + r;
             const long long rc = row < p.M ? row : p.M - 1;
             load8(p.A + rc * p.lda + kc, x[mt]);
-            if constexpr (SCALE) load8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, sc[mt]);
+        }
+        if constexpr (SCALE) {
+#pragma unroll
+            for (int mt = 0; mt < MFMA_MT; ++mt) {
+                const long long row = mbase + mt * 16 + r;
+                const long long rc = row < p.M ? row : p.M - 1;
+                load8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, sc[mt]);
+            }
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
@@ -360,9 +375,14 @@ inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + 
 
 template <typename T, int NT>
 void launch_direct(const GemmArgs& p, hipStream_t s) {
-    const dim3 grid(cdiv(p.M, 16LL * MFMA_MT * MFMA_WAVES), cdiv(p.N, NT * 16));
-    if (p.scale) hipLaunchKernelGGL((gemm_direct_kernel<T, NT, true>), grid, dim3(64 * MFMA_WAVES), 0, s, p);
-    else hipLaunchKernelGGL((gemm_direct_kernel<T, NT, false>), grid, dim3(64 * MFMA_WAVES), 0, s, p);
+    const int mblocks = (int)cdiv(p.M, 16LL * MFMA_MT * MFMA_WAVES), nblocks = (int)cdiv(p.N, NT * 16);
+    const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
+    if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_direct: grid too large");
+    const dim3 grid((unsigned)blocks);
+    if (p.scale)
+        hipLaunchKernelGGL((gemm_direct_kernel<T, NT, true>), grid, dim3(64 * MFMA_WAVES), 0, s, p, mblocks, nblocks);
+    else
+        hipLaunchKernelGGL((gemm_direct_kernel<T, NT, false>), grid, dim3(64 * MFMA_WAVES), 0, s, p, mblocks, nblocks);
 }
 
 template <typename T, int WM, int WN, int WGM, int WGN>
