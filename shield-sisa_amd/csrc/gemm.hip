@@ -24,14 +24,38 @@ namespace shv {
 namespace {
 
 // ------------------------------------------------------------------------------------------------ epilogue
-__device__ __forceinline__ void epi_store(const GemmArgs& p, long long m, int n, float v) {
-    if (p.bias) v = v + p.bias[n];
+// out = act(v + bias) (+ residual, or + residual after / sqrt(2) when res == 2)
+__device__ __forceinline__ float epi_value(const GemmArgs& p, float v, float b, float res) {
+    if (p.bias) v = v + b;
     v = apply_act(v, p.act);
+    if (p.res) v = p.res == 2 ? res + v / 1.41421356237309515f : res + v;
+    return v;
+}
+// Epilogue of the 4 x J outputs one thread holds (rows row(i), columns col(j)).  Every bias and residual operand is
+// loaded (at clamped, valid addresses) before the first store: C may alias R or the bias as far as the compiler
+// knows, so a load written after a store would wait for it, one memory round trip per output.
+template <int J, class Row, class Col, class Val>
+__device__ __forceinline__ void epi_block(const GemmArgs& p, Row row, Col col, Val val) {
+    float bv[J], rv[4][J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) bv[j] = p.bias ? p.bias[min(col(j), p.N - 1)] : 0.0f;
     if (p.res) {
-        const float r = p.R[m * p.ldr + n];
-        v = p.res == 2 ? r + v / 1.41421356237309515f : r + v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                rv[i][j] = p.R[min(row(i), (long long)p.M - 1) * p.ldr + min(col(j), p.N - 1)];
     }
-    p.C[m * p.ldc + n] = v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const long long m = row(i);
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int n = col(j);
+            if (n < p.N) p.C[m * p.ldc + n] = epi_value(p, val(i, j), bv[j], p.res ? rv[i][j] : 0.0f);
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ fp32 VALU
@@ -97,24 +121,21 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
         }
         __syncthreads();
     }
+    if (p.swiglu) {  // rows (2j, 2j+1) = (gate_j, up_j): this thread holds pairs j0, j0+1
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const long long m = m0 + ty * 4 + i;
-        if (m >= p.M) continue;
-        if (p.swiglu) {  // rows (2j, 2j+1) = (gate_j, up_j): this thread holds pairs j0, j0+1
+        for (int i = 0; i < 4; ++i) {
+            const long long m = m0 + ty * 4 + i;
+            if (m >= p.M) continue;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int n = n0 + tx * 4 + 2 * q;
                 if (n + 1 < p.N) p.C[m * p.ldc + (n >> 1)] = silu(tot[i][2 * q]) * tot[i][2 * q + 1];
             }
-            continue;
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + tx * 4 + j;
-            if (n < p.N) epi_store(p, m, n, tot[i][j]);
-        }
+        return;
     }
+    epi_block<4>(p, [&](int i) { return m0 + ty * 4 + i; }, [&](int j) { return n0 + tx * 4 + j; },
+                 [&](int i, int j) { return tot[i][j]; });
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA
@@ -207,28 +228,26 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p
                 for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[nt][S::wp(i)], acc[mt][nt]);
     }
     // lane holds C[mbase + mt*16 + g*4 + i][nbase + nt*16 + r]
+    if (p.swiglu) {  // 16-row panels alternate gate / up; NT is even and nbase is a multiple of 32
 #pragma unroll
-    for (int mt = 0; mt < MFMA_MT; ++mt) {
+        for (int mt = 0; mt < MFMA_MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const long long m = mbase + mt * 16 + g * 4 + i;
-            if (m >= p.M) continue;
-            if (p.swiglu) {  // 16-row panels alternate gate / up; NT is even and nbase is a multiple of 32
+            for (int i = 0; i < 4; ++i) {
+                const long long m = mbase + mt * 16 + g * 4 + i;
+                if (m >= p.M) continue;
 #pragma unroll
                 for (int nt = 0; nt + 1 < NT; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
                         p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[mt][nt][i]) * acc[mt][nt + 1][i];
                 }
-                continue;
             }
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const int n = nbase + nt * 16 + r;
-                if (n < p.N) epi_store(p, m, n, acc[mt][nt][i]);
-            }
-        }
+        return;
     }
+#pragma unroll
+    for (int mt = 0; mt < MFMA_MT; ++mt)
+        epi_block<NT>(p, [&](int i) { return mbase + mt * 16 + g * 4 + i; }, [&](int j) { return nbase + j * 16 + r; },
+                      [&](int i, int j) { return acc[mt][j][i]; });
 }
 
 // Workgroup barrier that waits for LDS traffic only (the next K step's global loads stay in flight across it).
@@ -347,28 +366,26 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
     }
     // lane holds C[m0 + (wm*WM + mt)*16 + g*4 + i][n0 + (wn*WN + nt)*16 + r]
     const int nbase = n0 + wn * WN * 16;
+    if (p.swiglu) {  // 16-row panels alternate gate / up; WN is even and nbase a multiple of 32
 #pragma unroll
-    for (int mt = 0; mt < WM; ++mt) {
+        for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const long long m = m0 + (wm * WM + mt) * 16 + g * 4 + i;
-            if (m >= p.M) continue;
-            if (p.swiglu) {  // 16-row panels alternate gate / up; WN is even and nbase a multiple of 32
+            for (int i = 0; i < 4; ++i) {
+                const long long m = m0 + (wm * WM + mt) * 16 + g * 4 + i;
+                if (m >= p.M) continue;
 #pragma unroll
                 for (int nt = 0; nt + 1 < WN; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
                         p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[mt][nt][i]) * acc[mt][nt + 1][i];
                 }
-                continue;
             }
-#pragma unroll
-            for (int nt = 0; nt < WN; ++nt) {
-                const int n = nbase + nt * 16 + r;
-                if (n < p.N) epi_store(p, m, n, acc[mt][nt][i]);
-            }
-        }
+        return;
     }
+#pragma unroll
+    for (int mt = 0; mt < WM; ++mt)
+        epi_block<WN>(p, [&](int i) { return m0 + (wm * WM + mt) * 16 + g * 4 + i; },
+                      [&](int j) { return nbase + j * 16 + r; }, [&](int i, int j) { return acc[mt][j][i]; });
 }
 
 inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
