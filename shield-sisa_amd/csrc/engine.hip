@@ -233,6 +233,7 @@ private:
         const float* exp_b = nullptr;
         const float *dw_w = nullptr, *dw_b = nullptr;
         const float *se1_w = nullptr, *se1_b = nullptr, *se2_w = nullptr, *se2_b = nullptr;
+        DevW se1_h, se2_h;   // half tiers: the SE fc weights pre-split for the matrix-core GEMM
         DevW proj_w;
         const float* proj_b = nullptr;
         // fused-kernel operands (half tiers): padded, pre-split weights
@@ -344,6 +345,10 @@ private:
             if (b.cfg.se) {
                 d.se1_w = up(b.se1.w); d.se1_b = up(b.se1.b);
                 d.se2_w = up(b.se2.w); d.se2_b = up(b.se2.b);
+                if constexpr (!kF32) {
+                    d.se1_h = repack<G>(b.se1.w, b.se1.N, b.se1.K, 0);
+                    d.se2_h = repack<G>(b.se2.w, b.se2.N, b.se2.K, 0);
+                }
             }
             d.proj_w = repack<G>(b.project.w, b.project.N, b.project.K, 0);
             d.proj_b = up(b.project.b);
@@ -558,13 +563,18 @@ private:
         p1.A = se_pool_; p1.lda = b.cfg.cexp; p1.W = b.se1_w; p1.ldw = b.cfg.cexp;
         p1.bias = b.se1_b; p1.act = ACT_RELU;
         p1.C = se_hid_; p1.ldc = b.csq;
-        gemm32("gemm_f32_small", p1, s);
         GemmArgs p2;
         p2.M = F; p2.N = b.cfg.cexp; p2.K = b.csq;
         p2.A = se_hid_; p2.lda = b.csq; p2.W = b.se2_w; p2.ldw = b.csq;
         p2.bias = b.se2_b; p2.act = ACT_HSIG;
         p2.C = se_scale_; p2.ldc = b.cfg.cexp;
-        gemm32("gemm_f32_small", p2, s);
+        if constexpr (kF32) {   // exact reference order
+            gemm32("gemm_f32_small", p1, s);
+            gemm32("gemm_f32_small", p2, s);
+        } else {                // split-operand matrix cores, like every other 1x1 layer of the half tiers
+            gemm("gemm_se_fc", p1, b.se1_h, s);
+            gemm("gemm_se_fc", p2, b.se2_h, s);
+        }
     }
 
     // half tiers: one fused kernel per block (SE blocks: fused expand + depthwise, SE, project GEMM)

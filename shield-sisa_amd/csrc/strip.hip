@@ -320,7 +320,24 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
                 }
             }
 
-            // ---- epilogue: (+ residual) and one float4 per (row, output tile) per lane
+            // ---- epilogue: (+ residual) and one float4 per (row, output tile) per lane.  Expand blocks re-read
+            // the residual (clamped) before the first store: the memory counter retires in order, so a load issued
+            // after a store would wait for that store.
+            float4 res[C::RES ? C::R : 1][C::OT];
+            if constexpr (C::RES) {
+#pragma unroll
+                for (int qr = 0; qr < C::R; ++qr)
+#pragma unroll
+                    for (int ot = 0; ot < C::OT; ++ot) {
+                        if constexpr (C::EXPAND) {
+                            const int oyc = min(oy0 + qr, Ho - 1), oxc = min(max(ox, 0), Wo - 1);
+                            const int n = min(ot * 16 + 4 * g, C::COUT - 4);
+                            res[qr][ot] = *reinterpret_cast<const float4*>(Xf + ((long long)oyc * W + oxc) * C::CIN + n);
+                        } else {
+                            res[qr][ot] = xe[qr + 1];
+                        }
+                    }
+            }
 #pragma unroll
             for (int qr = 0; qr < C::R; ++qr) {
                 const int oy = oy0 + qr;
@@ -331,11 +348,7 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
                     if (!store_lane || n >= C::COUT) continue;
                     float4 v = make_float4(y[qr][ot][0], y[qr][ot][1], y[qr][ot][2], y[qr][ot][3]);
                     if constexpr (C::RES) {
-                        float4 x;
-                        if constexpr (C::EXPAND)
-                            x = *reinterpret_cast<const float4*>(Xf + ((long long)oy * W + ox) * C::CIN + n);
-                        else
-                            x = xe[qr + 1];
+                        const float4 x = res[qr][ot];
                         v.x = x.x + v.x; v.y = x.y + v.y; v.z = x.z + v.z; v.w = x.w + v.w;
                     }
                     *reinterpret_cast<float4*>(Yf + ((long long)oy * Wo + ox) * C::COUT + n) = v;
