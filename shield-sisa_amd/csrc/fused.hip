@@ -485,16 +485,32 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
         }
 
         if constexpr (PROJ) {
-            // ---- epilogue: + bias (+ residual: the block input at the same pixel), fp32 NHWC store
+            // ---- epilogue: + bias (+ residual: the block input at the same pixel), fp32 NHWC store.  Per 16-row
+            // tile, the bias and residual operands are loaded (clamped) before its first store: the memory counter
+            // retires in order, so a load issued after a store would wait for that store.
+            float bias[C::NT_OUT];
+#pragma unroll
+            for (int nt = 0; nt < C::NT_OUT; ++nt) bias[nt] = a.bproj[nt * 16 + r];   // padded to COUTP
 #pragma unroll
             for (int j = 0; j < C::MPW_OUT; ++j) {
                 const int mt = wave + 4 * j;
                 if (mt >= C::MT_OUT) continue;
+                float res[C::RES && L::PRESPLIT ? C::NT_OUT : 1][4];
+                if constexpr (C::RES && L::PRESPLIT) {
+#pragma unroll
+                    for (int nt = 0; nt < C::NT_OUT; ++nt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int p = min(mt * 16 + g * 4 + i, C::POUT - 1);
+                            const int oy = p / C::TW, ox = p - oy * C::TW;
+                            const int gy = min(ty0 + oy, a.Ho - 1), gx = min(tx0 + ox, a.Wo - 1);
+                            res[nt][i] = Xf[((long long)gy * a.W + gx) * C::CIN + min(nt * 16 + r, C::CIN - 1)];
+                        }
+                }
 #pragma unroll
                 for (int nt = 0; nt < C::NT_OUT; ++nt) {
                     const int n = nt * 16 + r;
                     if (n >= C::COUT) continue;
-                    const float bias = a.bproj[n];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int p = mt * 16 + g * 4 + i;
@@ -502,9 +518,9 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
                         const int oy = p / C::TW, ox = p - oy * C::TW;
                         const int gy = ty0 + oy, gx = tx0 + ox;
                         if (gy >= a.Ho || gx >= a.Wo) continue;
-                        float v = yacc[j][nt][i] + bias;
+                        float v = yacc[j][nt][i] + bias[nt];
                         if constexpr (C::RES) {
-                            if constexpr (L::PRESPLIT) v = Xf[((long long)gy * a.W + gx) * C::CIN + n] + v;
+                            if constexpr (L::PRESPLIT) v = res[nt][i] + v;
                             else v = Xs[((oy + C::PAD) * C::IW + ox + C::PAD) * C::XS_LD + n] + v;
                         }
                         a.Y[((f * a.Ho + gy) * a.Wo + gx) * C::COUT + n] = v;
