@@ -20,12 +20,10 @@ template <typename T>
 __global__ void __launch_bounds__(256)
 stem_kernel(const uint8_t* __restrict__ in, T* __restrict__ out, const float* __restrict__ lut,
             const float* __restrict__ w, const float* __restrict__ b, int F) {
+    // the byte -> float table in LDS (per-lane index); weights and bias are read at wave-uniform constant offsets,
+    // which the compiler serves from the scalar data cache into SGPR operands
     __shared__ float slut[768];
-    __shared__ float sw[27 * 16];
-    __shared__ float sb[16];
     for (int i = threadIdx.x; i < 768; i += blockDim.x) slut[i] = lut[i];
-    for (int i = threadIdx.x; i < 27 * 16; i += blockDim.x) sw[i] = w[i];
-    if (threadIdx.x < 16) sb[threadIdx.x] = b[threadIdx.x];
     __syncthreads();
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long long)F * 90 * 160) return;
@@ -34,27 +32,24 @@ stem_kernel(const uint8_t* __restrict__ in, T* __restrict__ out, const float* __
     float acc[16];
 #pragma unroll
     for (int o = 0; o < 16; ++o) acc[o] = 0.0f;
+    // taps (dy, dx) in order, one at a time (rolled: one tap's 48 weights live in scalar registers)
+#pragma unroll 1
+    for (int t = 0; t < 9; ++t) {
+        const int dy = t / 3, dx = t - dy * 3;
+        const int iy = 2 * oy - 1 + dy, ix = 2 * ox - 1 + dx;
+        if (iy < 0 || iy >= 180 || ix < 0 || ix >= 320) continue;
+        const uint8_t* px = in + ((f * 180 + iy) * 320 + ix) * 3;
 #pragma unroll
-    for (int dy = 0; dy < 3; ++dy) {
-        const int iy = 2 * oy - 1 + dy;
-        if (iy < 0 || iy >= 180) continue;
+        for (int c = 0; c < 3; ++c) {
+            const float x = slut[c * 256 + px[c]];
+            const float* wr = w + (t * 3 + c) * 16;
 #pragma unroll
-        for (int dx = 0; dx < 3; ++dx) {
-            const int ix = 2 * ox - 1 + dx;
-            if (ix < 0 || ix >= 320) continue;
-            const uint8_t* px = in + ((f * 180 + iy) * 320 + ix) * 3;
-#pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                const float x = slut[c * 256 + px[c]];
-                const float* wr = sw + ((dy * 3 + dx) * 3 + c) * 16;
-#pragma unroll
-                for (int o = 0; o < 16; ++o) acc[o] = __builtin_fmaf(x, wr[o], acc[o]);
-            }
+            for (int o = 0; o < 16; ++o) acc[o] = __builtin_fmaf(x, wr[o], acc[o]);
         }
     }
     float v[16];
 #pragma unroll
-    for (int o = 0; o < 16; ++o) v[o] = hswish(acc[o] + sb[o]);
+    for (int o = 0; o < 16; ++o) v[o] = hswish(acc[o] + b[o]);
     store8(out + idx * 16, v);
     store8(out + idx * 16 + 8, v + 8);
 }
