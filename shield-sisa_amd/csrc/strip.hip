@@ -33,6 +33,9 @@ namespace {
 
 constexpr int ST_THREADS = 256;   // 4 independent waves; the workgroup shares the LDS copy of the weights
 
+// Workgroup barrier that waits for LDS traffic only (global loads issued before it stay in flight).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // v_mfma_f32_16x16x16 fragments (lane l = 16 g + r): A row r, k = 4 g .. 4 g + 3; B column r, k = 4 g ..
 // 4 g + 3; C column r, rows 4 g .. 4 g + 3.  Products as in Split<T> (smallest first).
 template <typename T> struct Split16;
@@ -383,6 +386,436 @@ template <typename T, class C> void launch_strip(int block, const IrArgs& a, int
     hipLaunchKernelGGL((ir_strip_kernel<T, C>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, items);
 }
 
+
+// ------------------------------------------------------------------------------------------------------------
+// Workgroup strip kernel (blocks 4-15: wider channel counts, 5x5 taps, hardswish, squeeze-excite).
+//
+// The 4 waves of a workgroup share one strip (16 lanes = 16 pixel columns) of one frame and walk down it R output
+// rows per step.  Each step's input rows are staged once in LDS, already split into the operand parts; each wave
+// then takes the 16-channel tiles ct = wave, wave + 4, ... and, per tile, computes the expanded rows (transposed
+// split MFMA 16x16x32, K = input channels), the depthwise outputs and either
+//   * (squeeze-excite blocks) the D rows to HBM and the step's channel sums, or
+//   * (other blocks) its share of the projection Y^T += Wproj^T[:, tile] . D^T (16x16x16), the 4 wave partials
+//     being added in wave order through LDS at the end of the step (+ bias, + residual).
+// The depthwise streams over the step's input rows in order, adding each row's taps to every output row that uses
+// it, so each output is still one fma chain over (dy, dx) in order, then + bias.  Tap weights are broadcast from
+// lane t (tap t < 16) of a first register and lane t - 16 of a second one (5x5), the bias from the lane after the
+// last tap.  Columns outside the map expand from -1e30 (ReLU and hardswish both give 0 there), rows outside the
+// map are skipped (E = 0).
+template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_>
+struct WgCfg {
+    static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, KS = KS_, S = S_, R = R_;
+    static constexpr bool HS = HS_ != 0, SE = SE_ != 0, PROJ = !SE;
+    static constexpr int ACT = HS ? ACT_HS : ACT_RELU;
+    static constexpr int PADK = KS / 2;
+    static constexpr int KS32 = (CIN + 31) / 32, CINP = KS32 * 32, XLD = CINP + 8;
+    static constexpr int CEXPP = (CEXP + 31) / 32 * 32;     // weight padding of the engine (IrShape cexpp)
+    static constexpr int CT = (CEXP + 15) / 16, OT = (COUT + 15) / 16, COUTP = OT * 16;
+    static constexpr int NT = S, IR = S * (R - 1) + KS;
+    static constexpr int VALID = S == 1 ? 16 - 2 * PADK : (KS == 3 ? 15 : 14);
+    static constexpr int LO = S == 1 ? PADK : 1;            // first output lane
+    static constexpr bool RES = PROJ && S == 1 && CIN == COUT;
+    static constexpr int NWR = (KS * KS + 1 + 15) / 16;    // depthwise weight registers per value (taps + bias)
+    static_assert(CIN % 4 == 0 && CEXP % 4 == 0 && COUT % 4 == 0, "channel counts must be multiples of 4");
+    static_assert(KS == 3 || KS == 5, "3x3 or 5x5 depthwise");
+};
+
+template <typename T, class C> struct WgLds {
+    static constexpr int P = Split<T>::P;
+    static constexpr int XS = C::IR * C::NT * P * 16 * C::XLD;     // T elements
+    static constexpr int YB = C::PROJ ? 4 * C::R * C::OT * 64 : 0;  // float4s
+    static constexpr int BYTES = XS * (int)sizeof(T) + YB * 16;
+};
+
+// acc (op)= the KS taps of one input row: first row of an output starts the chain with a product
+template <bool FIRST, int L0, int L1, int L2>
+__device__ __forceinline__ float taps3(float acc, float w0, float w1, float w2, float e0, float e1, float e2) {
+    if constexpr (FIRST)
+        asm("s_nop 1\n\t"
+            "v_mul_f32_dpp %0, %1, %4 row_newbcast:%7 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %2, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %3, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+            : "=&v"(acc)
+            : "v"(w0), "v"(w1), "v"(w2), "v"(e0), "v"(e1), "v"(e2), "i"(L0), "i"(L1), "i"(L2));
+    else
+        asm("s_nop 1\n\t"
+            "v_fmac_f32_dpp %0, %1, %4 row_newbcast:%7 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %2, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %3, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+            : "+v"(acc)
+            : "v"(w0), "v"(w1), "v"(w2), "v"(e0), "v"(e1), "v"(e2), "i"(L0), "i"(L1), "i"(L2));
+    return acc;
+}
+template <bool FIRST, int L0, int L1, int L2, int L3, int L4>
+__device__ __forceinline__ float taps5(float acc, float w0, float w1, float w2, float w3, float w4, float e0, float e1,
+                                       float e2, float e3, float e4) {
+    if constexpr (FIRST)
+        asm("s_nop 1\n\t"
+            "v_mul_f32_dpp %0, %1, %6 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %2, %7 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %3, %8 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %4, %9 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %5, %10 row_newbcast:%15 row_mask:0xf bank_mask:0xf"
+            : "=&v"(acc)
+            : "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(w4), "v"(e0), "v"(e1), "v"(e2), "v"(e3), "v"(e4), "i"(L0),
+              "i"(L1), "i"(L2), "i"(L3), "i"(L4));
+    else
+        asm("s_nop 1\n\t"
+            "v_fmac_f32_dpp %0, %1, %6 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %2, %7 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %3, %8 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %4, %9 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f32_dpp %0, %5, %10 row_newbcast:%15 row_mask:0xf bank_mask:0xf"
+            : "+v"(acc)
+            : "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(w4), "v"(e0), "v"(e1), "v"(e2), "v"(e3), "v"(e4), "i"(L0),
+              "i"(L1), "i"(L2), "i"(L3), "i"(L4));
+    return acc;
+}
+// v + (lane L of wv's row)
+template <int L> __device__ __forceinline__ float add_bcast(float v, float wv) {
+    float out;
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "=v"(out) : "v"(wv), "v"(v), "i"(L));
+    return out;
+}
+// lane r <- lane r + D of its 16-lane row (0 where that is outside the row)
+template <int D> __device__ __forceinline__ float lane_shift(float v) {
+    if constexpr (D == 0) return v;
+    else if constexpr (D > 0)
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + D, 0xf, 0xf, true));
+    else
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x110 - D, 0xf, 0xf, true));
+}
+// transposed split product: acc += W . X with W the A operand (weight parts), X the B operand (activation parts)
+template <typename T>
+__device__ __forceinline__ f32x4 mfma_wx(const typename Split<T>::V8* w, const typename Split<T>::V8* x, f32x4 acc) {
+#pragma unroll
+    for (int i = 0; i < Split<T>::NPROD; ++i) acc = Split<T>::mfma(w[Split<T>::wp(i)], x[Split<T>::ap(i)], acc);
+    return acc;
+}
+
+// one input row's taps (weights of kernel row DY) into an output accumulator, per value i of the lane
+template <class C, bool FIRST, int DY>
+__device__ __forceinline__ float row_taps(float acc, const float (&wd)[C::NWR], const float* v) {
+    constexpr int t0 = DY * C::KS;
+    if constexpr (C::KS == 3) {
+        return taps3<FIRST, t0 % 16, (t0 + 1) % 16, (t0 + 2) % 16>(acc, wd[t0 / 16], wd[(t0 + 1) / 16], wd[(t0 + 2) / 16],
+                                                                  v[0], v[1], v[2]);
+    } else {
+        return taps5<FIRST, t0 % 16, (t0 + 1) % 16, (t0 + 2) % 16, (t0 + 3) % 16, (t0 + 4) % 16>(
+            acc, wd[t0 / 16], wd[(t0 + 1) / 16], wd[(t0 + 2) / 16], wd[(t0 + 3) / 16], wd[(t0 + 4) / 16], v[0], v[1],
+            v[2], v[3], v[4]);
+    }
+}
+
+template <class C, int J, int Q>
+__device__ __forceinline__ void accum_row(f32x4 (&acc)[C::R], const float (&wd)[4][C::NWR], const f32x4 (&v)[C::KS]) {
+    if constexpr (Q < C::R) {
+        constexpr int DY = J - C::S * Q;
+        if constexpr (DY >= 0 && DY < C::KS) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float vi[C::KS];
+#pragma unroll
+                for (int dx = 0; dx < C::KS; ++dx) vi[dx] = v[dx][i];
+                acc[Q][i] = row_taps<C, DY == 0, DY>(acc[Q][i], wd[i], vi);
+            }
+        }
+        accum_row<C, J, Q + 1>(acc, wd, v);
+    }
+}
+
+template <typename T, class C, int J>
+__device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4][C::NWR], const typename Split<T>::V8 (&wf)[C::KS32][Split<T>::P],
+                                        const f32x4 (&init)[C::NT], const T* Xs, int r, int g, int iy0, int H) {
+    if constexpr (J < C::IR) {
+        typedef typename Split<T>::V8 V8;
+        constexpr int P = Split<T>::P;
+        f32x4 e[C::NT];
+        const int iy = iy0 + J;
+        if (iy >= 0 && iy < H) {   // uniform
+#pragma unroll
+            for (int t = 0; t < C::NT; ++t) {
+                f32x4 x = init[t];
+#pragma unroll
+                for (int ks = 0; ks < C::KS32; ++ks) {
+                    V8 xf[P];
+#pragma unroll
+                    for (int q = 0; q < P; ++q)
+                        xf[q] = *reinterpret_cast<const V8*>(Xs + (((J * C::NT + t) * P + q) * 16 + r) * C::XLD + ks * 32 + g * 8);
+                    x = mfma_wx<T>(wf[ks], xf, x);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[i] = apply_act_nb(x[i], C::ACT);
+                e[t] = x;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < C::NT; ++t) e[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        // tap variants dx = 0 .. KS-1 of this row for the lane's output column
+        f32x4 v[C::KS];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (C::S == 1) {
+#pragma unroll
+                for (int dx = 0; dx < C::KS; ++dx) {
+                    if constexpr (C::KS == 3) {
+                        if (dx == 0) v[dx][i] = lane_shift<-1>(e[0][i]);
+                        else if (dx == 1) v[dx][i] = e[0][i];
+                        else v[dx][i] = lane_shift<1>(e[0][i]);
+                    } else {
+                        if (dx == 0) v[dx][i] = lane_shift<-2>(e[0][i]);
+                        else if (dx == 1) v[dx][i] = lane_shift<-1>(e[0][i]);
+                        else if (dx == 2) v[dx][i] = e[0][i];
+                        else if (dx == 3) v[dx][i] = lane_shift<1>(e[0][i]);
+                        else v[dx][i] = lane_shift<2>(e[0][i]);
+                    }
+                }
+            } else if constexpr (C::KS == 3) {   // even tile 0, odd tile 1: cols 2ox-1, 2ox, 2ox+1
+                v[0][i] = lane_shift<-1>(e[1][i]);
+                v[1][i] = e[0][i];
+                v[2][i] = e[1][i];
+            } else {                             // cols 2ox-2 .. 2ox+2
+                v[0][i] = lane_shift<-1>(e[0][i]);
+                v[1][i] = lane_shift<-1>(e[1][i]);
+                v[2][i] = e[0][i];
+                v[3][i] = e[1][i];
+                v[4][i] = lane_shift<1>(e[0][i]);
+            }
+        }
+        accum_row<C, J, 0>(acc, wd, v);
+        wg_rows<T, C, J + 1>(acc, wd, wf, init, Xs, r, g, iy0, H);
+    }
+}
+
+template <typename T, class C>
+__global__ void __launch_bounds__(ST_THREADS) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items) {
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    typedef typename Split16<T>::V4 V4;
+    typedef WgLds<T, C> L;
+    constexpr int P = S::P;
+    __shared__ __attribute__((aligned(16))) unsigned char lds_raw[L::BYTES];
+    T* Xs = reinterpret_cast<T*>(lds_raw);                                   // [IR][NT][P][16][XLD]
+    float4* Yb = reinterpret_cast<float4*>(lds_raw + L::XS * sizeof(T));    // [4][R][OT][64]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const T* wexp = static_cast<const T*>(a.wexp);
+    const T* wproj = static_cast<const T*>(a.wproj);
+    const int H = a.H, W = a.W, Ho = a.Ho, Wo = a.Wo;
+
+    // staging of a step's input rows: float4 i -> (row j, tile t, pixel p, channel quad c4); loads at clamped,
+    // always valid addresses, zero outside the map and past cin
+    constexpr int XQ = C::CINP / 4;
+    constexpr int XN = C::IR * C::NT * 16 * XQ;
+    constexpr int XPT = (XN + ST_THREADS - 1) / ST_THREADS;
+    float4 xpre[XPT];
+    auto col_of = [&](int strip, int p, int t) {
+        return C::S == 1 ? strip * C::VALID - C::PADK + p : 2 * (strip * C::VALID - 1 + p) + t;
+    };
+    auto load_step = [&](int item, int step) {
+        const int strip = item % strips;
+        const long long f = item / strips;
+        const float* Xf = a.X + f * H * W * C::CIN;
+        const int iy0 = C::S * step * C::R - C::PADK;
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {
+            const int i = min(tid + k * ST_THREADS, XN - 1);
+            const int c4 = i % XQ, rest = i / XQ;
+            const int p = rest % 16, jt = rest / 16;
+            const int t = jt % C::NT, j = jt / C::NT;
+            const int iy = iy0 + j, ix = col_of(strip, p, t);
+            const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W && c4 * 4 < C::CIN;
+            const int cy = min(max(iy, 0), H - 1), cx = min(max(ix, 0), W - 1), cc = min(c4, C::CIN / 4 - 1);
+            const float4 v = *reinterpret_cast<const float4*>(Xf + ((long long)cy * W + cx) * C::CIN + cc * 4);
+            xpre[k] = in ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    auto store_step = [&]() {
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {
+            const int i = tid + k * ST_THREADS;
+            if (i >= XN) continue;
+            const int c4 = i % XQ, rest = i / XQ;
+            const int p = rest % 16, jt = rest / 16;
+            const float x[4] = {xpre[k].x, xpre[k].y, xpre[k].z, xpre[k].w};
+            T part[4][P];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
+#pragma unroll
+            for (int q = 0; q < P; ++q) {
+                T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
+                *reinterpret_cast<uint2*>(Xs + ((jt * P + q) * 16 + p) * C::XLD + c4 * 4) = *reinterpret_cast<const uint2*>(four);
+            }
+        }
+    };
+
+    if ((int)blockIdx.x < items) load_step(blockIdx.x, 0);
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        const int strip = item % strips;
+        const long long f = item / strips;
+        // this lane's output column and the map columns of its pixel tiles
+        const int ox = C::S == 1 ? strip * C::VALID - C::PADK + r : strip * C::VALID - 1 + r;
+        const bool out_lane = r >= C::LO && r < C::LO + C::VALID && ox < Wo;
+        bool pin[C::NT];
+#pragma unroll
+        for (int t = 0; t < C::NT; ++t) {
+            const int ix = col_of(strip, r, t);
+            pin[t] = ix >= 0 && ix < W;
+        }
+        for (int step = 0; step < steps; ++step) {
+            const int oy0 = step * C::R;
+            store_step();
+            lds_barrier();
+            // the next step's (or next item's first) rows are in flight while this step computes
+            if (step + 1 < steps) load_step(item, step + 1);
+            else if (item + (int)gridDim.x < items) load_step(item + gridDim.x, 0);
+
+            f32x4 y[C::PROJ ? C::R : 1][C::PROJ ? C::OT : 1];
+            if constexpr (C::PROJ) {
+#pragma unroll
+                for (int ot = 0; ot < C::OT; ++ot) {
+                    float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (wave == 0) b = *reinterpret_cast<const float4*>(a.bproj + ot * 16 + 4 * g);
+#pragma unroll
+                    for (int q = 0; q < C::R; ++q) y[q][ot] = f32x4{b.x, b.y, b.z, b.w};
+                }
+            }
+            for (int ct = wave; ct < C::CT; ct += 4) {
+                const int c = ct * 16 + 4 * g;
+                // ---- this tile's weights
+                V8 wf[C::KS32][P];
+#pragma unroll
+                for (int ks = 0; ks < C::KS32; ++ks)
+#pragma unroll
+                    for (int q = 0; q < P; ++q)
+                        wf[ks][q] = load_part8<T>(wexp + q * a.wexp_stride + (long long)(ct * 16 + r) * C::CINP + ks * 32 + g * 8);
+                float wd[4][C::NWR];
+#pragma unroll
+                for (int w = 0; w < C::NWR; ++w) {
+                    const int t = min(w * 16 + r, C::KS * C::KS);
+                    const float* src = t < C::KS * C::KS ? a.wdw + t * C::CEXPP + c : a.bdw + c;
+                    const float4 v = *reinterpret_cast<const float4*>(src);
+                    wd[0][w] = v.x; wd[1][w] = v.y; wd[2][w] = v.z; wd[3][w] = v.w;
+                }
+                const float4 be = *reinterpret_cast<const float4*>(a.bexp + c);
+                f32x4 init[C::NT];
+#pragma unroll
+                for (int t = 0; t < C::NT; ++t)
+                    init[t] = pin[t] ? f32x4{be.x, be.y, be.z, be.w} : f32x4{-1e30f, -1e30f, -1e30f, -1e30f};
+                V4 pw[C::PROJ ? C::OT : 1][P];
+                if constexpr (C::PROJ) {
+#pragma unroll
+                    for (int ot = 0; ot < C::OT; ++ot)
+#pragma unroll
+                        for (int q = 0; q < P; ++q) {
+                            const uint2 u = *reinterpret_cast<const uint2*>(wproj + q * a.wproj_stride +
+                                                                            (long long)(ot * 16 + r) * C::CEXPP + c);
+                            pw[ot][q] = __builtin_bit_cast(V4, u);
+                        }
+                }
+                // ---- expand + depthwise, streaming over the step's input rows
+                f32x4 acc[C::R];
+#pragma unroll
+                for (int q = 0; q < C::R; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                wg_rows<T, C, 0>(acc, wd, wf, init, Xs, r, g, C::S * oy0 - C::PADK, H);
+                constexpr int BL = C::KS * C::KS;   // bias lane index (taps 0 .. BL-1)
+                f32x4 d[C::R];
+#pragma unroll
+                for (int q = 0; q < C::R; ++q)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        d[q][i] = apply_act_nb(add_bcast<BL % 16>(acc[q][i], wd[i][BL / 16]), C::ACT);
+                if constexpr (C::SE) {
+                    // D rows -> HBM; channel sums of the step's valid pixels (rows in order, then the 16 lanes)
+                    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                    for (int q = 0; q < C::R; ++q) {
+                        const int oy = oy0 + q;
+                        if (out_lane && oy < Ho) {
+                            const float4 v = make_float4(d[q][0], d[q][1], d[q][2], d[q][3]);
+                            if (c < C::CEXP)
+                                *reinterpret_cast<float4*>(a.D + ((f * Ho + oy) * Wo + ox) * C::CEXP + c) = v;
+                            sum.x = sum.x + v.x; sum.y = sum.y + v.y; sum.z = sum.z + v.z; sum.w = sum.w + v.w;
+                        }
+                    }
+                    sum.x = tree16(sum.x); sum.y = tree16(sum.y); sum.z = tree16(sum.z); sum.w = tree16(sum.w);
+                    if (r == 0)
+                        *reinterpret_cast<float4*>(a.part + (f * a.ntiles + step * strips + strip) * C::CEXPP + c) = sum;
+                } else {
+#pragma unroll
+                    for (int q = 0; q < C::R; ++q) {
+                        V4 df[P];
+                        split4<T>(make_float4(d[q][0], d[q][1], d[q][2], d[q][3]), df);
+#pragma unroll
+                        for (int ot = 0; ot < C::OT; ++ot) y[q][ot] = mfma_split16<T>(pw[ot], df, y[q][ot]);
+                    }
+                }
+            }
+            if constexpr (C::PROJ) {
+#pragma unroll
+                for (int q = 0; q < C::R; ++q)
+#pragma unroll
+                    for (int ot = 0; ot < C::OT; ++ot)
+                        Yb[((wave * C::R + q) * C::OT + ot) * 64 + lane] = make_float4(y[q][ot][0], y[q][ot][1], y[q][ot][2], y[q][ot][3]);
+            }
+            lds_barrier();   // Xs free for the next step; the wave partials of Y complete
+            if constexpr (C::PROJ) {
+                // (row, output tile) pairs round robin over the waves: wave partials added in wave order
+                for (int pr = wave; pr < C::R * C::OT; pr += 4) {
+                    const int q = pr / C::OT, ot = pr % C::OT;
+                    const int oy = oy0 + q, n = ot * 16 + 4 * g;
+                    float4 res = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if constexpr (C::RES) {
+                        const int oyc = min(oy, Ho - 1), oxc = min(max(ox, 0), Wo - 1), nc = min(n, C::COUT - 4);
+                        res = *reinterpret_cast<const float4*>(a.X + ((f * H + oyc) * W + oxc) * C::CIN + nc);
+                    }
+                    float4 v = Yb[((0 * C::R + q) * C::OT + ot) * 64 + lane];
+#pragma unroll
+                    for (int w = 1; w < 4; ++w) {
+                        const float4 u = Yb[((w * C::R + q) * C::OT + ot) * 64 + lane];
+                        v.x = v.x + u.x; v.y = v.y + u.y; v.z = v.z + u.z; v.w = v.w + u.w;
+                    }
+                    if constexpr (C::RES) {
+                        v.x = res.x + v.x; v.y = res.y + v.y; v.z = res.z + v.z; v.w = res.w + v.w;
+                    }
+                    if (out_lane && oy < Ho && n < C::COUT)
+                        *reinterpret_cast<float4*>(a.Y + ((f * Ho + oy) * Wo + ox) * C::COUT + n) = v;
+                }
+            }
+        }
+    }
+}
+
+//                cin  cexp cout k  s  hs se R
+typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 1> G7;      // 23x40 -> 12x20
+typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;      // 12x20
+typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 2> G9;      // 12x20 (b9, b10)
+
+template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, int F, hipStream_t s) {
+    const IrShape sh = ir_shape(block, std::is_same<T, bf16>::value);
+    if (sh.cin != C::CIN || sh.cexp != C::CEXP || sh.cout != C::COUT || sh.k != C::KS || sh.stride != C::S ||
+        sh.se != (int)C::SE || sh.hs != (int)C::HS || sh.cinp != C::CINP || sh.cexpp != C::CEXPP ||
+        sh.coutp != C::COUTP)
+        throw std::runtime_error("ir_wgstrip: weight padding disagrees with the block shape");
+    const int strips = (a.Wo + C::VALID - 1) / C::VALID, steps = (a.Ho + C::R - 1) / C::R;
+    if ((C::S == 1 && (a.Ho != a.H || a.Wo != a.W)) || (C::S == 2 && (a.Ho != (a.H + 1) / 2 || a.Wo != (a.W + 1) / 2)))
+        throw std::runtime_error("ir_wgstrip: map shape does not match the stride");
+    if (a.frames != F || (long long)F * strips > (1ll << 30)) throw std::runtime_error("ir_wgstrip: bad frame count");
+    if (C::SE && (a.tiles_x != strips || a.ntiles != strips * steps))
+        throw std::runtime_error("ir_wgstrip: SE partial-sum grid mismatch");
+    const int items = F * strips;
+    static const int resident = [] {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_wgstrip_kernel<T, C>, ST_THREADS, 0) != hipSuccess)
+            throw std::runtime_error("ir_wgstrip: cannot query the device occupancy");
+        return std::max(1, cus) * std::max(1, per_cu);
+    }();
+    const int grid = std::min(items, resident);
+    hipLaunchKernelGGL((ir_wgstrip_kernel<T, C>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, steps, items);
+}
+
 }  // namespace
 
 template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hipStream_t s) {
@@ -390,6 +823,9 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
     case 0: launch_strip<T, S1>(block, a, F, s); return true;
     case 1: launch_strip<T, S2>(block, a, F, s); return true;
     case 2: launch_strip<T, S3>(block, a, F, s); return true;
+    case 6: launch_wgstrip<T, G7>(block, a, F, s); return true;
+    case 7: launch_wgstrip<T, G8>(block, a, F, s); return true;
+    case 8: case 9: launch_wgstrip<T, G9>(block, a, F, s); return true;
     default: return false;
     }
 }
