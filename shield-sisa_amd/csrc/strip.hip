@@ -402,9 +402,10 @@ template <typename T, class C> void launch_strip(int block, const IrArgs& a, int
 // lane t (tap t < 16) of a first register and lane t - 16 of a second one (5x5), the bias from the lane after the
 // last tap.  Columns outside the map expand from -1e30 (ReLU and hardswish both give 0 there), rows outside the
 // map are skipped (E = 0).
-template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_>
+template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_, int MINB_ = 1>
 struct WgCfg {
     static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, KS = KS_, S = S_, R = R_;
+    static constexpr int MINB = MINB_;   // workgroups per CU the register allocation must allow
     static constexpr bool HS = HS_ != 0, SE = SE_ != 0, PROJ = !SE;
     static constexpr int ACT = HS ? ACT_HS : ACT_RELU;
     static constexpr int PADK = KS / 2;
@@ -589,7 +590,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
 }
 
 template <typename T, class C>
-__global__ void __launch_bounds__(ST_THREADS) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items) {
+__global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     typedef typename Split16<T>::V4 V4;
@@ -787,7 +788,7 @@ __global__ void __launch_bounds__(ST_THREADS) ir_wgstrip_kernel(IrArgs a, int st
 }
 
 //                cin  cexp cout k  s  hs se R
-typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 1> G7;      // 23x40 -> 12x20
+typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 1, 3> G7;      // 23x40 -> 12x20
 typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;      // 12x20
 typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 2> G9;      // 12x20 (b9, b10)
 
