@@ -852,7 +852,11 @@ template <typename T> IrShape ir_shape_t(int block) {
     }
     throw std::runtime_error("ir_shape: block index out of range");
 }
-IrShape ir_shape(int block, bool bf16_tier) { return bf16_tier ? ir_shape_t<bf16>(block) : ir_shape_t<f16>(block); }
+IrShape ir_shape(int block, bool bf16_tier) {
+    IrShape s;
+    if (strip_kernels_enabled() && ir_strip_shape(block, &s)) return s;
+    return bf16_tier ? ir_shape_t<bf16>(block) : ir_shape_t<f16>(block);
+}
 
 template <typename T, class W, class C> void launch_se(const IrArgs& a, int F, hipStream_t s) {
     if constexpr (SeLayout<T, W>::FITS) launch_wave<T, W>(a, F, s);
@@ -861,9 +865,7 @@ template <typename T, class W, class C> void launch_se(const IrArgs& a, int F, h
 
 template <typename T> void launch_ir_block(int block, const IrArgs& a, int F, hipStream_t s) {
     if (F <= 0) return;
-    // blocks 1-3 run in the strip kernel unless SHV_HIP_NO_STRIP is set (tile kernels kept for comparison)
-    static const bool strip = std::getenv("SHV_HIP_NO_STRIP") == nullptr;
-    if (strip && launch_ir_strip<T>(block, a, F, s)) return;
+    if (strip_kernels_enabled() && launch_ir_strip<T>(block, a, F, s)) return;
     switch (block) {
     case 0: launch_cfg<T, B1>(a, F, s); break;
     case 1: launch_cfg<T, B2>(a, F, s); break;

@@ -83,8 +83,13 @@ struct IrArgs {
     int H = 0, W = 0, Ho = 0, Wo = 0, tiles_x = 0, ntiles = 0, frames = 0;
 };
 template <typename T> void launch_ir_block(int block, const IrArgs& a, int F, hipStream_t s);
-// blocks 1-3 (index 0-2) in the pixel-per-lane strip kernel; false for other blocks (the tile-grid fields of the
-// arguments are not used)
+// Strip kernels (pixel-per-lane layout): blocks 1-3 one wave per strip, later blocks one workgroup per strip.
+// Enabled unless SHV_HIP_NO_STRIP is set (then every block takes the tile kernels).
+bool strip_kernels_enabled();
+// the shape of block i's strip kernel when it has one that is not interchangeable with its tile kernel's (the tile
+// is then (rows per step, columns per strip), which the SE partial sums are laid out by)
+bool ir_strip_shape(int block, IrShape* out);
+// launches block i's strip kernel; false when the block has none
 template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hipStream_t s);
 // SE squeeze from the fused kernel's tile sums: pooled[f][c] = (sum over tiles in order) / (float)hw
 void launch_se_reduce(const float* part, int ntiles, int cexpp, int cexp, int hw, float* pooled, int F,

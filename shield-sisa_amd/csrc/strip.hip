@@ -25,6 +25,7 @@
 #include "mfma.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <stdexcept>
 #include <type_traits>
 
@@ -787,10 +788,21 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     }
 }
 
-//                cin  cexp cout k  s  hs se R
+//                cin  cexp cout k  s  hs se R  minb
+typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 4> G5;         // 23x40 (b5, b6)
 typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 1, 3> G7;      // 23x40 -> 12x20
-typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;      // 12x20
-typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 2> G9;      // 12x20 (b9, b10)
+typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;         // 12x20
+typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 2> G9;         // 12x20 (b9, b10)
+typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
+typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 4> G12;      // 12x20
+
+// the block shape the engine pads weights to and sizes the SE partial sums by: tile = (R rows, VALID columns)
+template <class C> IrShape wg_shape() {
+    IrShape s;
+    s.cin = C::CIN; s.cexp = C::CEXP; s.cout = C::COUT; s.k = C::KS; s.stride = C::S; s.se = C::SE; s.hs = C::HS;
+    s.th = C::R; s.tw = C::VALID; s.cinp = C::CINP; s.cexpp = C::CEXPP; s.coutp = C::COUTP;
+    return s;
+}
 
 template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, int F, hipStream_t s) {
     const IrShape sh = ir_shape(block, std::is_same<T, bf16>::value);
@@ -819,14 +831,34 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
 
 }  // namespace
 
+bool strip_kernels_enabled() {
+    static const bool on = std::getenv("SHV_HIP_NO_STRIP") == nullptr;
+    return on;
+}
+
+bool ir_strip_shape(int block, IrShape* out) {
+    switch (block) {
+    case 4: case 5: *out = wg_shape<G5>(); return true;
+    case 6: *out = wg_shape<G7>(); return true;
+    case 7: *out = wg_shape<G8>(); return true;
+    case 8: case 9: *out = wg_shape<G9>(); return true;
+    case 10: *out = wg_shape<G11>(); return true;
+    case 11: *out = wg_shape<G12>(); return true;
+    default: return false;
+    }
+}
+
 template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hipStream_t s) {
     switch (block) {
     case 0: launch_strip<T, S1>(block, a, F, s); return true;
     case 1: launch_strip<T, S2>(block, a, F, s); return true;
     case 2: launch_strip<T, S3>(block, a, F, s); return true;
+    case 4: case 5: launch_wgstrip<T, G5>(block, a, F, s); return true;
     case 6: launch_wgstrip<T, G7>(block, a, F, s); return true;
     case 7: launch_wgstrip<T, G8>(block, a, F, s); return true;
     case 8: case 9: launch_wgstrip<T, G9>(block, a, F, s); return true;
+    case 10: launch_wgstrip<T, G11>(block, a, F, s); return true;
+    case 11: launch_wgstrip<T, G12>(block, a, F, s); return true;
     default: return false;
     }
 }
