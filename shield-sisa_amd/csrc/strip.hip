@@ -789,12 +789,12 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 }
 
 //                cin  cexp cout k  s  hs se R  minb
-typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 4> G5;         // 23x40 (b5, b6)
+typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 6> G5;         // 23x40 (b5, b6)
 typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 1, 3> G7;      // 23x40 -> 12x20
 typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;         // 12x20
 typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 2> G9;         // 12x20 (b9, b10)
 typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
-typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 4> G12;      // 12x20
+typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6> G12;      // 12x20
 
 // the block shape the engine pads weights to and sizes the SE partial sums by: tile = (R rows, VALID columns)
 template <class C> IrShape wg_shape() {
