@@ -789,6 +789,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 }
 
 //                cin  cexp cout k  s  hs se R  minb
+typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 2> G4;         // 45x80 -> 23x40
 typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 6> G5;         // 23x40 (b5, b6)
 typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 1, 3> G7;      // 23x40 -> 12x20
 typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;         // 12x20
@@ -838,6 +839,7 @@ bool strip_kernels_enabled() {
 
 bool ir_strip_shape(int block, IrShape* out) {
     switch (block) {
+    case 3: *out = wg_shape<G4>(); return true;
     case 4: case 5: *out = wg_shape<G5>(); return true;
     case 6: *out = wg_shape<G7>(); return true;
     case 7: *out = wg_shape<G8>(); return true;
@@ -853,6 +855,7 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
     case 0: launch_strip<T, S1>(block, a, F, s); return true;
     case 1: launch_strip<T, S2>(block, a, F, s); return true;
     case 2: launch_strip<T, S3>(block, a, F, s); return true;
+    case 3: launch_wgstrip<T, G4>(block, a, F, s); return true;
     case 4: case 5: launch_wgstrip<T, G5>(block, a, F, s); return true;
     case 6: launch_wgstrip<T, G7>(block, a, F, s); return true;
     case 7: launch_wgstrip<T, G8>(block, a, F, s); return true;
