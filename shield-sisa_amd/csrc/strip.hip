@@ -789,7 +789,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 }
 
 //                cin  cexp cout k  s  hs se R  minb
-typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 2> G4;         // 45x80 -> 23x40
+typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 4> G4;         // 45x80 -> 23x40
 typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 6> G5;         // 23x40 (b5, b6)
 typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 1, 3> G7;      // 23x40 -> 12x20
 typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;         // 12x20
