@@ -390,6 +390,152 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
 
 inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
 
+// SE-block projects (A rows scaled per frame, N <= 160).  The direct kernel spends two thirds of its vector-memory
+// instructions on operands its 4 waves share: the scale row of a frame and the K step's weight tile.  Here the
+// workgroup stages the scale rows of the (at most SE_MAXF) frames its 256 rows span in LDS once, and each K step's
+// weight tile [NT*16][32] in a double-buffered LDS tile (one LDS barrier per step); only A is read per wave.  Same
+// fragments, products and K order as the direct kernel.
+constexpr int SE_MAXF = 8;
+constexpr int SE_WLD = 32 + 8;   // staged W row stride in T elements
+
+template <typename T, int NT, bool PF>
+__global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_se_kernel(GemmArgs p, int mblocks, int nblocks) {
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    constexpr int P = S::P, BN = NT * 16;
+    constexpr int WV = P * BN * 4;                          // 16-byte vectors of one staged W tile
+    constexpr int WR = (WV + 64 * MFMA_WAVES - 1) / (64 * MFMA_WAVES);
+    __shared__ __attribute__((aligned(16))) T Ws[2][P][BN][SE_WLD];
+    extern __shared__ __attribute__((aligned(16))) float Sc[];   // [nf][K]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int r = lane & 15, g = lane >> 4;
+    const int xcd = blockIdx.x % XCDS, slot = blockIdx.x / XCDS;
+    const int mb = (slot / nblocks) * XCDS + xcd, nb = slot % nblocks;
+    if (mb >= mblocks) return;   // uniform over the workgroup
+    const long long m0 = (long long)mb * MFMA_WAVES * MFMA_MT * 16;
+    const long long mbase = m0 + wave * MFMA_MT * 16;
+    const int nbase = nb * BN;
+    const T* W = static_cast<const T*>(p.W);
+    const long long f0 = m0 / p.scale_rows;
+    const int nf = int((min(m0 + MFMA_WAVES * MFMA_MT * 16, (long long)p.M) - 1) / p.scale_rows - f0) + 1;
+    for (int i = tid; i < nf * (p.K / 4); i += 64 * MFMA_WAVES) {
+        const int fi = i / (p.K / 4), k4 = i - fi * (p.K / 4);
+        *reinterpret_cast<float4*>(Sc + fi * p.K + k4 * 4) =
+            *reinterpret_cast<const float4*>(p.scale + (f0 + fi) * p.ld_scale + k4 * 4);
+    }
+    // rows of this lane (clamped) and their frames' scale rows in LDS
+    long long arow[MFMA_MT];
+    int srow[MFMA_MT];
+#pragma unroll
+    for (int mt = 0; mt < MFMA_MT; ++mt) {
+        const long long row = mbase + mt * 16 + r;
+        arow[mt] = row < p.M ? row : p.M - 1;
+        srow[mt] = int(arow[mt] / p.scale_rows - f0) * p.K;
+    }
+    uint4 wr[WR];
+    auto load_w = [&](int k0) {
+#pragma unroll
+        for (int k = 0; k < WR; ++k) {
+            const int i = min(tid + k * 64 * MFMA_WAVES, WV - 1);
+            const int c8 = i & 3, n = (i >> 2) % BN, q = (i >> 2) / BN;
+            const int col = nbase + n, kk = k0 + c8 * 8;
+            const bool in = col < p.N && kk < p.K;
+            const uint4 v = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)min(col, p.N - 1) * p.ldw +
+                                                          min(kk, p.K - 8));
+            wr[k] = in ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto store_w = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < WR; ++k) {
+            const int i = tid + k * 64 * MFMA_WAVES;
+            if (i >= WV) continue;
+            const int c8 = i & 3, n = (i >> 2) % BN, q = (i >> 2) / BN;
+            *reinterpret_cast<uint4*>(&Ws[buf][q][n][c8 * 8]) = wr[k];
+        }
+    };
+    load_w(0);
+    store_w(0);
+    lds_barrier();
+
+    f32x4 acc[MFMA_MT][NT];
+#pragma unroll
+    for (int i = 0; i < MFMA_MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // PF: A rows one K step ahead (the next step's loads in flight while this one computes; costs 32 VGPRs)
+    float xn[PF ? MFMA_MT : 1][8];
+    auto load_a = [&](int k0, float (*dst)[8]) {
+        const int kc = min(k0 + g * 8, p.K - 8);
+#pragma unroll
+        for (int mt = 0; mt < MFMA_MT; ++mt) load8(p.A + arow[mt] * p.lda + kc, dst[mt]);
+    };
+    if constexpr (PF) load_a(0, xn);
+    int buf = 0;
+    for (int k0 = 0; k0 < p.K; k0 += 32) {
+        const bool more = k0 + 32 < p.K;
+        const int kk = k0 + g * 8;
+        const bool kin = kk < p.K;
+        const int kc = kin ? kk : p.K - 8;
+        float x[MFMA_MT][8];
+        if constexpr (PF) {
+#pragma unroll
+            for (int mt = 0; mt < MFMA_MT; ++mt)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[mt][e] = xn[mt][e];
+            if (more) {
+                load_w(k0 + 32);
+                load_a(k0 + 32, xn);
+            }
+        } else {
+            if (more) load_w(k0 + 32);
+            load_a(k0, x);
+        }
+        V8 a[MFMA_MT][P], b[NT][P];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int q = 0; q < P; ++q) b[nt][q] = *reinterpret_cast<const V8*>(&Ws[buf][q][nt * 16 + r][g * 8]);
+#pragma unroll
+        for (int mt = 0; mt < MFMA_MT; ++mt) {
+            const bool live = kin && mbase + mt * 16 + r < p.M;
+            float sc[8];
+            load8(Sc + srow[mt] + kc, sc);
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = live ? sc[e] * x[mt][e] : 0.0f;
+            split8<T>(v, a[mt]);
+        }
+#pragma unroll
+        for (int i = 0; i < S::NPROD; ++i)
+#pragma unroll
+            for (int mt = 0; mt < MFMA_MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[nt][S::wp(i)], acc[mt][nt]);
+        if (more) store_w(buf ^ 1);
+        lds_barrier();
+        buf ^= 1;
+    }
+    if (mbase >= p.M) return;
+#pragma unroll
+    for (int mt = 0; mt < MFMA_MT; ++mt)
+        epi_block<NT>(p, [&](int i) { return mbase + mt * 16 + g * 4 + i; }, [&](int j) { return nbase + j * 16 + r; },
+                      [&](int i, int j) { return acc[mt][j][i]; });
+}
+
+template <typename T, int NT, bool PF>
+void launch_se(const GemmArgs& p, hipStream_t s) {
+    const int rows_wg = 16 * MFMA_MT * MFMA_WAVES;
+    if ((rows_wg - 1) / p.scale_rows + 2 > SE_MAXF || p.K % 8)
+        throw std::runtime_error("gemm_se: a workgroup would span too many frames");
+    const int mblocks = (int)cdiv(p.M, rows_wg), nblocks = (int)cdiv(p.N, NT * 16);
+    const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
+    if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_se: grid too large");
+    const size_t lds = size_t(std::min(SE_MAXF, (rows_wg - 1) / p.scale_rows + 2)) * p.K * sizeof(float);
+    hipLaunchKernelGGL((gemm_se_kernel<T, NT, PF>), dim3((unsigned)blocks), dim3(64 * MFMA_WAVES), lds, s, p, mblocks,
+                       nblocks);
+}
+
 template <typename T, int NT>
 void launch_direct(const GemmArgs& p, hipStream_t s) {
     const int mblocks = (int)cdiv(p.M, 16LL * MFMA_MT * MFMA_WAVES), nblocks = (int)cdiv(p.N, NT * 16);
@@ -421,6 +567,11 @@ template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
             const int cols = (tiles + c - 1) / c * c;
             if (cols < best_cols) { best_cols = cols; nt = c; }
         }
+    }
+    if (p.scale && nt >= 4) {   // wide SE projects: shared operands staged in LDS (A prefetch where registers allow;
+        if (nt == 4) launch_se<T, 4, true>(p, s);   // 3 column tiles measured faster in the direct kernel)
+        else launch_se<T, 5, false>(p, s);
+        return;
     }
     switch (nt) {
     case 1: launch_direct<T, 1>(p, s); break;
