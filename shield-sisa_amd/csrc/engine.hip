@@ -536,6 +536,20 @@ private:
 
     // last 1x1 160 -> 960 + hardswish, 4x4 pool, projection 960 -> 384 (fp32 tokens)
     void run_tail(const float* x, int F, float* tokens, hipStream_t s) {
+        if constexpr (!kF32) {
+            if (dump_dir_.empty()) {   // fused last 1x1 + pool (the 60x960 map is dumped only by the unfused path)
+                timed("tail_pool", double(F) * (60.0 * 160 + 16.0 * kCnnOut) * TS, s, [&] {
+                    launch_tail_pool<G>(x, last_w_.w, last_w_.stride, last_b_, PO_, F, s);
+                });
+                check_launch();
+                GemmArgs p;
+                p.M = F * 16; p.N = kD; p.K = kCnnOut;
+                p.A = PO_; p.lda = kCnnOut; p.ldw = kCnnOut;
+                p.C = tokens; p.ldc = kD;
+                gemm("gemm_pw", p, proj_w_, s);
+                return;
+            }
+        }
         {
             GemmArgs p;
             p.M = F * 60; p.N = kCnnOut; p.K = 160;

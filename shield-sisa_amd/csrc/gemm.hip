@@ -582,6 +582,89 @@ template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
     }
 }
 
+// Last 1x1 (160 -> 960, + bias, hardswish) fused with the 4x4 adaptive pool of the 6x10 map, half tiers.  One
+// workgroup per frame: the frame's 60 x 160 input is staged in LDS (split into the operand parts, rows 60..63
+// zero), each wave takes output-channel tiles nt = wave, wave + 4, ... and computes C[64 px][16 ch] with the same
+// split products in the same K order as the GEMM kernels, applies the same epilogue, writes the tile to its own LDS
+// rows and pools it exactly as the pool kernel does (bin = rows {0,1,3,4}[r] + [0,2) x cols {0,2,5,7}[c] + [0,3),
+// sum from +0 row by row, then (sum / 2) / 3).  The pooled tokens are therefore bitwise those of the unfused path,
+// and the 60 x 960 map never reaches HBM.
+constexpr int TAIL_K = 160, TAIL_N = 960, TAIL_XLD = TAIL_K + 8, TAIL_ELD = 16 + 1;
+
+template <typename T>
+__global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict__ X, const T* __restrict__ W,
+                                                        long long wstride, const float* __restrict__ bias,
+                                                        float* __restrict__ out, int F) {
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    constexpr int P = S::P;
+    __shared__ __attribute__((aligned(16))) T Xs[P][64][TAIL_XLD];
+    __shared__ float Es[4][64][TAIL_ELD];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const long long f = blockIdx.x;
+    const float* Xf = X + f * 60 * TAIL_K;
+    // stage: 64 rows x 40 float4 (rows 60..63 zero), split into the parts
+    for (int i = tid; i < 64 * (TAIL_K / 4); i += 256) {
+        const int row = i / (TAIL_K / 4), c4 = i - row * (TAIL_K / 4);
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (row < 60) v = *reinterpret_cast<const float4*>(Xf + row * TAIL_K + c4 * 4);
+        const float x[4] = {v.x, v.y, v.z, v.w};
+        T part[4][P];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+            T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
+            *reinterpret_cast<uint2*>(&Xs[q][row][c4 * 4]) = *reinterpret_cast<const uint2*>(four);
+        }
+    }
+    __syncthreads();
+    float(*E)[TAIL_ELD] = Es[wave];
+    for (int nt = wave; nt < TAIL_N / 16; nt += 4) {
+        V8 w[TAIL_K / 32][P];
+#pragma unroll
+        for (int ks = 0; ks < TAIL_K / 32; ++ks)
+#pragma unroll
+            for (int q = 0; q < P; ++q)
+                w[ks][q] = load_part8<T>(W + q * wstride + (long long)(nt * 16 + r) * TAIL_K + ks * 32 + g * 8);
+        const float b = bias[nt * 16 + r];
+        f32x4 acc[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < TAIL_K / 32; ++ks) {
+            V8 a[4][P];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int q = 0; q < P; ++q) a[mt][q] = *reinterpret_cast<const V8*>(&Xs[q][mt * 16 + r][ks * 32 + g * 8]);
+#pragma unroll
+            for (int i = 0; i < S::NPROD; ++i)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) acc[mt] = S::mfma(a[mt][S::ap(i)], w[ks][S::wp(i)], acc[mt]);
+        }
+        // lane holds C[mt*16 + 4g + i][nt*16 + r]: + bias, hardswish (the GEMM epilogue), into this wave's rows
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) E[mt * 16 + 4 * g + i][r] = apply_act(acc[mt][i] + b, ACT_HS);
+        asm volatile("" ::: "memory");   // one wave's LDS accesses execute in issue order
+        // pool: lane (channel r, bins g, g + 4, g + 8, g + 12)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int tok = g + 4 * j;
+            const int r0 = ((tok >> 2) * 3) >> 1, c0 = ((tok & 3) * 5) >> 1;
+            float sum = 0.0f;
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int x = 0; x < 3; ++x) sum = sum + E[(r0 + y) * 10 + c0 + x][r];
+            out[(f * 16 + tok) * TAIL_N + nt * 16 + r] = (sum / 2.0f) / 3.0f;
+        }
+        asm volatile("" ::: "memory");
+    }
+}
+
 void check_args(const GemmArgs& p, bool mfma) {
     if (p.M <= 0 || p.N <= 0 || p.K <= 0) throw std::runtime_error("gemm: empty shape");
     if (!p.A || !p.W || !p.C) throw std::runtime_error("gemm: null operand");
@@ -614,5 +697,16 @@ template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s) {
 }
 template void gemm_mfma<f16>(const GemmArgs&, hipStream_t);
 template void gemm_mfma<bf16>(const GemmArgs&, hipStream_t);
+
+template <typename T>
+void launch_tail_pool(const float* x, const void* w, long long wstride, const float* bias, float* pooled, int F,
+                      hipStream_t s) {
+    if (F <= 0) return;
+    if (wstride < (long long)TAIL_N * TAIL_K) throw std::runtime_error("tail_pool: bad weight part stride");
+    hipLaunchKernelGGL(tail_pool_kernel<T>, dim3((unsigned)F), dim3(256), 0, s, x, static_cast<const T*>(w), wstride,
+                       bias, pooled, F);
+}
+template void launch_tail_pool<f16>(const float*, const void*, long long, const float*, float*, int, hipStream_t);
+template void launch_tail_pool<bf16>(const float*, const void*, long long, const float*, float*, int, hipStream_t);
 
 }  // namespace shv

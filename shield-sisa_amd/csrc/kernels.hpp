@@ -36,6 +36,11 @@ void gemm_f32(const GemmArgs& p, hipStream_t s);
 // fp32 accumulation, K consumed in 32-wide steps in increasing order (no split-K): a row's outputs do not depend
 // on M, the tile, or other rows.
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
+// half tiers: last 1x1 (x [F*60][160] fp32, pre-split weight parts [960][160], + bias, hardswish) fused with the 4x4
+// pool -> pooled [F][16][960] fp32, bitwise equal to gemm_mfma + launch_pool
+template <typename T>
+void launch_tail_pool(const float* x, const void* w, long long wstride, const float* bias, float* pooled, int F,
+                      hipStream_t s);
 // number of weight parts an MFMA tier stores
 template <typename T> constexpr int weight_parts() { return sizeof(T) == 4 ? 1 : (std::is_same<T, bf16>::value ? 3 : 2); }
 

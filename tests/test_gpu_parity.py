@@ -249,3 +249,19 @@ def test_fused_blocks_match_layer_path(shv, weights, clips, mode):
             err = float(np.abs(a - b).max()) / max(1e-30, float(np.abs(b).max()))
             print(f"[gpu] {mode} {name}: max rel diff {err:.2e}", flush=True)
             assert err <= (1e-5 if name in ("cnn01", "cnn02", "cnn03") else 1e-3), (name, err)
+
+
+@pytest.mark.parametrize("mode", ["fp16", "bf16"])
+def test_fused_tail_matches_unfused(shv, weights, clips, mode):
+    """The fused last 1x1 + hardswish + 4x4 pool of the half tiers (taken when no dump directory is set) repeats
+    the unfused GEMM's split products in the same K order, its epilogue and the pool kernel's bin sums: tokens are
+    bitwise those of the unfused path (taken while dumping)."""
+    print(f"[gpu] {mode} fused tail vs unfused tail, frames of clip 0", flush=True)
+    frames = clips[0][:8]
+    with shv.Model(weights, mode, experimental=True, use_graphs=0) as m:
+        fused = m.encode_frames(frames)
+        with tempfile.TemporaryDirectory() as d:
+            m.set_dump_dir(d)
+            unfused = m.encode_frames(frames)
+    assert np.all(np.isfinite(fused))
+    assert np.array_equal(fused.view(np.uint32), unfused.view(np.uint32)), float(np.abs(fused - unfused).max())
