@@ -54,46 +54,96 @@ rmsnorm_kernel(const float* __restrict__ x, long long ldx, const float* __restri
 }
 
 // ------------------------------------------------------------------------------------------------ GDN prep
-// One block per row, wave h = head h.  Lane l: q channel h*64+l, k channel h*64+l, v channels h*128+l (+64).
-// Short conv: acc from +0, taps t-3..t in order, + bias, SiLU (isa_impl.hpp:871-889).  L2 norms with the
-// 16-lane structure over 64 elements (isa_impl.hpp:893-906).  Gates with device libm (expf, log1pf).
+// One block per (window, run of GP_T tokens), wave h = head h.  Lane l owns q channel h*64+l, k channel h*64+l and
+// v channels h*128+l, h*128+64+l, and keeps those columns of the last 4 rows of P in registers while it walks the
+// run, so each element of P is read once (plus a 3-row halo per run).  Per row: short conv acc from +0, taps t-3..t
+// in order, + bias, SiLU (isa_impl.hpp:871-889); L2 norms with the 16-lane structure over 64 elements
+// (isa_impl.hpp:893-906); gates with device libm (expf, log1pf).
+constexpr int GP_T = 32;
 __global__ void __launch_bounds__(384)
 gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const float* __restrict__ cb,
                 const float* __restrict__ neg_rate, const float* __restrict__ dt_bias, float* __restrict__ Q,
                 float* __restrict__ K, float* __restrict__ V, float* __restrict__ dec, float* __restrict__ beta) {
-    const long long row = blockIdx.x;
-    const int t = int(row % kT), h = threadIdx.x >> 6, l = threadIdx.x & 63;
-    auto conv = [&](int col, int wc) {
-        float acc = 0.0f;
-        if (t >= 3) acc = __builtin_fmaf(P[(row - 3) * kGld + col], cw[0 * 1536 + wc], acc);
-        if (t >= 2) acc = __builtin_fmaf(P[(row - 2) * kGld + col], cw[1 * 1536 + wc], acc);
-        if (t >= 1) acc = __builtin_fmaf(P[(row - 1) * kGld + col], cw[2 * 1536 + wc], acc);
-        acc = __builtin_fmaf(P[row * kGld + col], cw[3 * 1536 + wc], acc);
-        return silu(acc + cb[wc]);
-    };
-    const float q = conv(kGq + h * 64 + l, h * 64 + l);
-    const float k = conv(kGk + h * 64 + l, 384 + h * 64 + l);
-    V[row * kVD + h * 128 + l] = conv(kGv + h * 128 + l, 768 + h * 128 + l);
-    V[row * kVD + h * 128 + 64 + l] = conv(kGv + h * 128 + 64 + l, 768 + h * 128 + 64 + l);
-    // lanes 0..15 gather elements l, l+16, l+32, l+48
-    float aq = q * q, ak = k * k;
+    constexpr int RUNS = (kT + GP_T - 1) / GP_T;
+    const int b = blockIdx.x / RUNS, t0 = (blockIdx.x % RUNS) * GP_T, t1 = min(kT, t0 + GP_T);
+    const int h = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const long long row0 = (long long)b * kT;
+    const int cq = kGq + h * 64 + l, ck = kGk + h * 64 + l, cv0 = kGv + h * 128 + l, cv1 = cv0 + 64;
+    const int wq = h * 64 + l, wk = 384 + h * 64 + l, wv0 = 768 + h * 128 + l, wv1 = wv0 + 64;
+    float w[4][4], bias[4];   // [column][tap]
+    const int wc[4] = {wq, wk, wv0, wv1}, pc[4] = {cq, ck, cv0, cv1};
 #pragma unroll
-    for (int s = 1; s < 4; ++s) {
-        const float qs = __shfl(q, l + 16 * s), ks = __shfl(k, l + 16 * s);
-        aq = __builtin_fmaf(qs, qs, aq);
-        ak = __builtin_fmaf(ks, ks, ak);
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[c][j] = cw[j * 1536 + wc[c]];
+        bias[c] = cb[wc[c]];
     }
-    aq = tree16(aq);
-    ak = tree16(ak);
-    aq = __shfl(aq, 0);
-    ak = __shfl(ak, 0);
-    const float iq = 1.0f / sqrtf(aq + 1e-6f), ik = 1.0f / sqrtf(ak + 1e-6f);
-    Q[row * kD + h * 64 + l] = (q * iq) * 0.125f;
-    K[row * kD + h * 64 + l] = k * ik;
+    // hist[c][j]: column c of row t - 3 + j (rows before the window's first token are 0 and never used)
+    float hist[4][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int t = t0 - 3 + j;
+            hist[c][j] = t >= 0 ? P[(row0 + t) * kGld + pc[c]] : 0.0f;
+        }
+    float na = 0.0f, nb = 0.0f;
     if (l == 0) {
-        const float* p = P + row * kGld;
-        dec[row * 8 + h] = expf(neg_rate[h] * softplus_f(p[kGa + h] + dt_bias[h]));
-        beta[row * 8 + h] = 1.0f / (1.0f + expf(-p[kGb + h]));
+        na = P[(row0 + t0) * kGld + kGa + h];
+        nb = P[(row0 + t0) * kGld + kGb + h];
+    }
+    float nxt[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) nxt[c] = P[(row0 + t0) * kGld + pc[c]];
+    for (int t = t0; t < t1; ++t) {
+        const long long row = row0 + t;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) hist[c][3] = nxt[c];
+        const float ga = na, gb = nb;
+        if (t + 1 < t1) {   // the next row's loads are in flight during this row's work
+#pragma unroll
+            for (int c = 0; c < 4; ++c) nxt[c] = P[(row + 1) * kGld + pc[c]];
+            if (l == 0) {
+                na = P[(row + 1) * kGld + kGa + h];
+                nb = P[(row + 1) * kGld + kGb + h];
+            }
+        }
+        float y[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float acc = 0.0f;
+            if (t >= 3) acc = __builtin_fmaf(hist[c][0], w[c][0], acc);
+            if (t >= 2) acc = __builtin_fmaf(hist[c][1], w[c][1], acc);
+            if (t >= 1) acc = __builtin_fmaf(hist[c][2], w[c][2], acc);
+            acc = __builtin_fmaf(hist[c][3], w[c][3], acc);
+            y[c] = silu(acc + bias[c]);
+        }
+        const float q = y[0], k = y[1];
+        V[row * kVD + h * 128 + l] = y[2];
+        V[row * kVD + h * 128 + 64 + l] = y[3];
+        // lanes 0..15 gather elements l, l+16, l+32, l+48
+        float aq = q * q, ak = k * k;
+#pragma unroll
+        for (int s = 1; s < 4; ++s) {
+            const float qs = __shfl(q, l + 16 * s), ks = __shfl(k, l + 16 * s);
+            aq = __builtin_fmaf(qs, qs, aq);
+            ak = __builtin_fmaf(ks, ks, ak);
+        }
+        aq = tree16(aq);
+        ak = tree16(ak);
+        aq = __shfl(aq, 0);
+        ak = __shfl(ak, 0);
+        const float iq = 1.0f / sqrtf(aq + 1e-6f), ik = 1.0f / sqrtf(ak + 1e-6f);
+        Q[row * kD + h * 64 + l] = (q * iq) * 0.125f;
+        K[row * kD + h * 64 + l] = k * ik;
+        if (l == 0) {
+            dec[row * 8 + h] = expf(neg_rate[h] * softplus_f(ga + dt_bias[h]));
+            beta[row * 8 + h] = 1.0f / (1.0f + expf(-gb));
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) hist[c][j] = hist[c][j + 1];
     }
 }
 
@@ -388,8 +438,8 @@ void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long 
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
                      const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
                      hipStream_t s) {
-    hipLaunchKernelGGL(gdn_prep_kernel, dim3(B * kT), dim3(384), 0, s, P, conv_w, conv_b, neg_rate, dt_bias, Q, K, V,
-                       dec, beta);
+    hipLaunchKernelGGL(gdn_prep_kernel, dim3(B * ((kT + GP_T - 1) / GP_T)), dim3(384), 0, s, P, conv_w, conv_b, neg_rate,
+                       dt_bias, Q, K, V, dec, beta);
 }
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
                   int B, hipStream_t s) {
