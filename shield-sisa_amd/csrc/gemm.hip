@@ -258,8 +258,8 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // [BN][32] in LDS, while the next step's global loads are already in flight; each wave multiplies WM x WN 16x16
 // tiles from LDS fragments.  Every accumulator receives, per K step, the same NPROD MFMAs in the same order as
 // before staging existed, so results do not depend on the tiling.
-constexpr int LG_KT = 32;          // K per step: one MFMA K
-constexpr int LG_LD = LG_KT + 8;   // staged row stride in T elements (80 B): 16-lane fragment reads hit 64 banks once
+constexpr int LG_KT = 64;          // K per staged step: two MFMA K steps
+constexpr int LG_LD = LG_KT + 8;   // staged row stride in T elements (144 B): 16-lane fragment reads hit 64 banks once
 
 template <typename T, int WM, int WN, int WGM, int WGN, bool SCALE>
 __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
@@ -286,7 +286,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
 #pragma unroll
         for (int k = 0; k < AR; ++k) {
             const int i = tid + 256 * k;
-            const int row = i >> 3, c = i & 7;
+            const int row = i / (LG_KT / 4), c = i % (LG_KT / 4);
             const long long gm = m0 + row;
             const int kk = k0 + c * 4;
             float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -302,7 +302,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
 #pragma unroll
         for (int k = 0; k < WR; ++k) {
             const int i = tid + 256 * k;
-            const int row = i >> 2, c = i & 3;
+            const int row = i / (LG_KT / 8), c = i % (LG_KT / 8);
             const int gn = n0 + row, kk = k0 + c * 8;
             const bool in = i < W8 && gn < p.N && kk < p.K;
 #pragma unroll
@@ -316,7 +316,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
         for (int k = 0; k < AR; ++k) {
             const int i = tid + 256 * k;
             if (i >= A4) continue;
-            const int row = i >> 3, c = i & 7;
+            const int row = i / (LG_KT / 4), c = i % (LG_KT / 4);
             const float x[4] = {ra[k].x, ra[k].y, ra[k].z, ra[k].w};
             T part[4][P];
 #pragma unroll
@@ -331,7 +331,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
         for (int k = 0; k < WR; ++k) {
             const int i = tid + 256 * k;
             if (i >= W8) continue;
-            const int row = i >> 2, c = i & 3;
+            const int row = i / (LG_KT / 8), c = i % (LG_KT / 8);
 #pragma unroll
             for (int q = 0; q < P; ++q) *reinterpret_cast<uint4*>(&Ws[q][row][c * 8]) = rw[k][q];
         }
@@ -347,21 +347,28 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
         store();
         lds_barrier();
         if (k0 + LG_KT < p.K) load(k0 + LG_KT);
-        V8 a[WM][P], b[WN][P];
-#pragma unroll
-        for (int mt = 0; mt < WM; ++mt)
-#pragma unroll
-            for (int q = 0; q < P; ++q) a[mt][q] = *reinterpret_cast<const V8*>(&As[q][(wm * WM + mt) * 16 + r][g * 8]);
-#pragma unroll
-        for (int nt = 0; nt < WN; ++nt)
-#pragma unroll
-            for (int q = 0; q < P; ++q) b[nt][q] = *reinterpret_cast<const V8*>(&Ws[q][(wn * WN + nt) * 16 + r][g * 8]);
-#pragma unroll
-        for (int i = 0; i < S::NPROD; ++i)
+#pragma unroll 1
+        for (int ks = 0; ks < LG_KT / 32; ++ks) {   // MFMA K steps of the staged step, in increasing K
+            if (k0 + ks * 32 >= p.K) break;          // uniform
+            V8 a[WM][P], b[WN][P];
 #pragma unroll
             for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
-                for (int nt = 0; nt < WN; ++nt) acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[nt][S::wp(i)], acc[mt][nt]);
+                for (int q = 0; q < P; ++q)
+                    a[mt][q] = *reinterpret_cast<const V8*>(&As[q][(wm * WM + mt) * 16 + r][ks * 32 + g * 8]);
+#pragma unroll
+            for (int nt = 0; nt < WN; ++nt)
+#pragma unroll
+                for (int q = 0; q < P; ++q)
+                    b[nt][q] = *reinterpret_cast<const V8*>(&Ws[q][(wn * WN + nt) * 16 + r][ks * 32 + g * 8]);
+#pragma unroll
+            for (int i = 0; i < S::NPROD; ++i)
+#pragma unroll
+                for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < WN; ++nt)
+                        acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[nt][S::wp(i)], acc[mt][nt]);
+        }
         lds_barrier();
     }
     // lane holds C[m0 + (wm*WM + mt)*16 + g*4 + i][n0 + (wn*WN + nt)*16 + r]
