@@ -403,10 +403,23 @@ template <typename T, class C> void launch_strip(int block, const IrArgs& a, int
 // lane t (tap t < 16) of a first register and lane t - 16 of a second one (5x5), the bias from the lane after the
 // last tap.  Columns outside the map expand from -1e30 (ReLU and hardswish both give 0 there), rows outside the
 // map are skipped (E = 0).
-template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_, int MINB_ = 1>
+template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_, int MINB_ = 1, int ROLLK_ = 0,
+          int NOPF_ = 0, int WHOLE_H_ = 0>
 struct WgCfg {
     static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, KS = KS_, S = S_, R = R_;
     static constexpr int MINB = MINB_;   // workgroups per CU the register allocation must allow
+    // ROLLK: the expand runs K-step-outer in a rolled loop (weight parts loaded per K step, one step ahead), so only
+    // one K step's fragments are live -- for wide inputs, where the unrolled form holds every row's fragments
+    static constexpr bool ROLLK = ROLLK_ != 0;
+    // NOPF: a step's input rows are staged at the start of the step (4 float4 per thread at a time) instead of being
+    // held in registers during the previous step -- for wide inputs with long steps, where those registers would
+    // cost occupancy and one exposed load per step is cheap
+    static constexpr bool NOPF = NOPF_ != 0;
+    // WHOLE_H (stride 1, one step covers the map's WHOLE_H rows): only the map's own rows are staged -- the padding
+    // rows above and below are never read, the expand skips them -- so LDS holds WHOLE_H rows instead of IR
+    static constexpr int XR0 = WHOLE_H_ ? KS_ / 2 : 0;     // first staged input row of a step (relative)
+    static constexpr int XRN = WHOLE_H_ ? WHOLE_H_ : S_ * (R_ - 1) + KS_;
+    static_assert(!WHOLE_H_ || (S_ == 1 && R_ >= WHOLE_H_), "whole-map staging: stride 1, one step per map");
     static constexpr bool HS = HS_ != 0, SE = SE_ != 0, PROJ = !SE;
     static constexpr int ACT = HS ? ACT_HS : ACT_RELU;
     static constexpr int PADK = KS / 2;
@@ -424,7 +437,7 @@ struct WgCfg {
 
 template <typename T, class C> struct WgLds {
     static constexpr int P = Split<T>::P;
-    static constexpr int XS = C::IR * C::NT * P * 16 * C::XLD;     // T elements
+    static constexpr int XS = C::XRN * C::NT * P * 16 * C::XLD;    // T elements
     static constexpr int YB = C::PROJ ? 4 * C::R * C::OT * 64 : 0;  // float4s
     static constexpr int BYTES = XS * (int)sizeof(T) + YB * 16;
 };
@@ -543,7 +556,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
                     V8 xf[P];
 #pragma unroll
                     for (int q = 0; q < P; ++q)
-                        xf[q] = *reinterpret_cast<const V8*>(Xs + (((J * C::NT + t) * P + q) * 16 + r) * C::XLD + ks * 32 + g * 8);
+                        xf[q] = *reinterpret_cast<const V8*>(Xs + ((((J - C::XR0) * C::NT + t) * P + q) * 16 + r) * C::XLD + ks * 32 + g * 8);
                     x = mfma_wx<T>(wf[ks], xf, x);
                 }
 #pragma unroll
@@ -590,6 +603,103 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
     }
 }
 
+// ROLLK expand: ea[staged row][tile] = init + W . X over the K steps in order (rows outside the map left at init,
+// unused); staged row j holds input row XR0 + j of the step
+template <typename T, class C>
+__device__ __forceinline__ void wg_expand_rolled(f32x4 (&ea)[C::XRN][C::NT], const T* wexp, long long wstride, int ct,
+                                                 const f32x4 (&init)[C::NT], const T* Xs, int r, int g, int iy0,
+                                                 int H) {
+    typedef typename Split<T>::V8 V8;
+    constexpr int P = Split<T>::P;
+#pragma unroll
+    for (int j = 0; j < C::XRN; ++j)
+#pragma unroll
+        for (int t = 0; t < C::NT; ++t) ea[j][t] = init[t];
+    const T* wrow = wexp + (long long)(ct * 16 + r) * C::CINP + g * 8;
+    V8 wn[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) wn[q] = load_part8<T>(wrow + q * wstride);
+#pragma unroll 1
+    for (int ks = 0; ks < C::KS32; ++ks) {
+        V8 w[P];
+#pragma unroll
+        for (int q = 0; q < P; ++q) w[q] = wn[q];
+        if (ks + 1 < C::KS32) {
+#pragma unroll
+            for (int q = 0; q < P; ++q) wn[q] = load_part8<T>(wrow + q * wstride + (ks + 1) * 32);
+        }
+#pragma unroll
+        for (int j = 0; j < C::XRN; ++j) {
+            const int iy = iy0 + C::XR0 + j;
+            if (iy >= 0 && iy < H) {   // uniform
+#pragma unroll
+                for (int t = 0; t < C::NT; ++t) {
+                    V8 xf[P];
+#pragma unroll
+                    for (int q = 0; q < P; ++q)
+                        xf[q] = *reinterpret_cast<const V8*>(Xs + (((j * C::NT + t) * P + q) * 16 + r) * C::XLD + ks * 32 + g * 8);
+                    ea[j][t] = mfma_wx<T>(w, xf, ea[j][t]);
+                }
+            }
+        }
+    }
+}
+
+// tap variants dx = 0 .. KS-1 of one input row (E tiles e) for the lane's output column
+template <class C>
+__device__ __forceinline__ void tap_variants(const f32x4 (&e)[C::NT], f32x4 (&v)[C::KS]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (C::S == 1) {
+            if constexpr (C::KS == 3) {
+                v[0][i] = lane_shift<-1>(e[0][i]);
+                v[1][i] = e[0][i];
+                v[2][i] = lane_shift<1>(e[0][i]);
+            } else {
+                v[0][i] = lane_shift<-2>(e[0][i]);
+                v[1][i] = lane_shift<-1>(e[0][i]);
+                v[2][i] = e[0][i];
+                v[3][i] = lane_shift<1>(e[0][i]);
+                v[4][i] = lane_shift<2>(e[0][i]);
+            }
+        } else if constexpr (C::KS == 3) {   // even tile 0, odd tile 1: cols 2ox-1, 2ox, 2ox+1
+            v[0][i] = lane_shift<-1>(e[1][i]);
+            v[1][i] = e[0][i];
+            v[2][i] = e[1][i];
+        } else {                             // cols 2ox-2 .. 2ox+2
+            v[0][i] = lane_shift<-1>(e[0][i]);
+            v[1][i] = lane_shift<-1>(e[1][i]);
+            v[2][i] = e[0][i];
+            v[3][i] = e[1][i];
+            v[4][i] = lane_shift<1>(e[0][i]);
+        }
+    }
+}
+
+// the depthwise over rows whose expand accumulators are ready (ROLLK)
+template <class C, int J>
+__device__ __forceinline__ void wg_rows_acc(f32x4 (&acc)[C::R], const float (&wd)[4][C::NWR],
+                                            const f32x4 (&ea)[C::XRN][C::NT], int iy0, int H) {
+    if constexpr (J < C::IR) {
+        f32x4 e[C::NT];
+        if constexpr (J >= C::XR0 && J < C::XR0 + C::XRN) {
+            const int iy = iy0 + J;
+            const bool in = iy >= 0 && iy < H;   // uniform
+#pragma unroll
+            for (int t = 0; t < C::NT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) e[t][i] = in ? apply_act_nb(ea[J - C::XR0][t][i], C::ACT) : 0.0f;
+        } else {   // never staged: outside the map (whole-map staging)
+#pragma unroll
+            for (int t = 0; t < C::NT; ++t) e[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        f32x4 v[C::KS];
+        tap_variants<C>(e, v);
+        accum_row<C, J, 0>(acc, wd, v);
+        wg_rows_acc<C, J + 1>(acc, wd, ea, iy0, H);
+    }
+}
+
 template <typename T, class C>
 __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items) {
     typedef Split<T> S;
@@ -608,20 +718,21 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     // staging of a step's input rows: float4 i -> (row j, tile t, pixel p, channel quad c4); loads at clamped,
     // always valid addresses, zero outside the map and past cin
     constexpr int XQ = C::CINP / 4;
-    constexpr int XN = C::IR * C::NT * 16 * XQ;
-    constexpr int XPT = (XN + ST_THREADS - 1) / ST_THREADS;
+    constexpr int XN = C::XRN * C::NT * 16 * XQ;
+    constexpr int XPT_ALL = (XN + ST_THREADS - 1) / ST_THREADS;
+    constexpr int XPT = C::NOPF ? (XPT_ALL < 4 ? XPT_ALL : 4) : XPT_ALL;   // float4s per thread held at a time
     float4 xpre[XPT];
     auto col_of = [&](int strip, int p, int t) {
         return C::S == 1 ? strip * C::VALID - C::PADK + p : 2 * (strip * C::VALID - 1 + p) + t;
     };
-    auto load_step = [&](int item, int step) {
+    auto load_step = [&](int item, int step, int k0) {
         const int strip = item % strips;
         const long long f = item / strips;
         const float* Xf = a.X + f * H * W * C::CIN;
-        const int iy0 = C::S * step * C::R - C::PADK;
+        const int iy0 = C::S * step * C::R - C::PADK + C::XR0;
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int i = min(tid + k * ST_THREADS, XN - 1);
+            const int i = min(tid + (k0 + k) * ST_THREADS, XN - 1);
             const int c4 = i % XQ, rest = i / XQ;
             const int p = rest % 16, jt = rest / 16;
             const int t = jt % C::NT, j = jt / C::NT;
@@ -632,10 +743,10 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             xpre[k] = in ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     };
-    auto store_step = [&]() {
+    auto store_step = [&](int k0) {
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int i = tid + k * ST_THREADS;
+            const int i = tid + (k0 + k) * ST_THREADS;
             if (i >= XN) continue;
             const int c4 = i % XQ, rest = i / XQ;
             const int p = rest % 16, jt = rest / 16;
@@ -651,7 +762,9 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
         }
     };
 
-    if ((int)blockIdx.x < items) load_step(blockIdx.x, 0);
+    if constexpr (!C::NOPF) {
+        if ((int)blockIdx.x < items) load_step(blockIdx.x, 0, 0);
+    }
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
         const int strip = item % strips;
         const long long f = item / strips;
@@ -666,11 +779,19 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
         }
         for (int step = 0; step < steps; ++step) {
             const int oy0 = step * C::R;
-            store_step();
-            lds_barrier();
-            // the next step's (or next item's first) rows are in flight while this step computes
-            if (step + 1 < steps) load_step(item, step + 1);
-            else if (item + (int)gridDim.x < items) load_step(item + gridDim.x, 0);
+            if constexpr (C::NOPF) {
+                for (int k0 = 0; k0 < XPT_ALL; k0 += XPT) {
+                    load_step(item, step, k0);
+                    store_step(k0);
+                }
+                lds_barrier();
+            } else {
+                store_step(0);
+                lds_barrier();
+                // the next step's (or next item's first) rows are in flight while this step computes
+                if (step + 1 < steps) load_step(item, step + 1, 0);
+                else if (item + (int)gridDim.x < items) load_step(item + gridDim.x, 0, 0);
+            }
 
             f32x4 y[C::PROJ ? C::R : 1][C::PROJ ? C::OT : 1];
             if constexpr (C::PROJ) {
@@ -685,12 +806,14 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             for (int ct = wave; ct < C::CT; ct += 4) {
                 const int c = ct * 16 + 4 * g;
                 // ---- this tile's weights
-                V8 wf[C::KS32][P];
+                V8 wf[C::ROLLK ? 1 : C::KS32][P];
+                if constexpr (!C::ROLLK) {
 #pragma unroll
-                for (int ks = 0; ks < C::KS32; ++ks)
+                    for (int ks = 0; ks < C::KS32; ++ks)
 #pragma unroll
-                    for (int q = 0; q < P; ++q)
-                        wf[ks][q] = load_part8<T>(wexp + q * a.wexp_stride + (long long)(ct * 16 + r) * C::CINP + ks * 32 + g * 8);
+                        for (int q = 0; q < P; ++q)
+                            wf[ks][q] = load_part8<T>(wexp + q * a.wexp_stride + (long long)(ct * 16 + r) * C::CINP + ks * 32 + g * 8);
+                }
                 float wd[4][C::NWR];
 #pragma unroll
                 for (int w = 0; w < C::NWR; ++w) {
@@ -719,7 +842,13 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                 f32x4 acc[C::R];
 #pragma unroll
                 for (int q = 0; q < C::R; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                wg_rows<T, C, 0>(acc, wd, wf, init, Xs, r, g, C::S * oy0 - C::PADK, H);
+                if constexpr (C::ROLLK) {
+                    f32x4 ea[C::XRN][C::NT];
+                    wg_expand_rolled<T, C>(ea, wexp, a.wexp_stride, ct, init, Xs, r, g, C::S * oy0 - C::PADK, H);
+                    wg_rows_acc<C, 0>(acc, wd, ea, C::S * oy0 - C::PADK, H);
+                } else {
+                    wg_rows<T, C, 0>(acc, wd, wf, init, Xs, r, g, C::S * oy0 - C::PADK, H);
+                }
                 constexpr int BL = C::KS * C::KS;   // bias lane index (taps 0 .. BL-1)
                 f32x4 d[C::R];
 #pragma unroll
@@ -796,6 +925,7 @@ typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;         // 12x20
 typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 2> G9;         // 12x20 (b9, b10)
 typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
 typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6> G12;      // 12x20
+typedef WgCfg<160, 960, 160, 5, 1, 1, 1, 6, 1, 1, 1, 6> G14;   // 6x10 (b14, b15)
 
 // the block shape the engine pads weights to and sizes the SE partial sums by: tile = (R rows, VALID columns)
 template <class C> IrShape wg_shape() {
@@ -817,6 +947,8 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
     if (a.frames != F || (long long)F * strips > (1ll << 30)) throw std::runtime_error("ir_wgstrip: bad frame count");
     if (C::SE && (a.tiles_x != strips || a.ntiles != strips * steps))
         throw std::runtime_error("ir_wgstrip: SE partial-sum grid mismatch");
+    if (C::XRN != C::IR && (steps != 1 || a.H != C::XRN))
+        throw std::runtime_error("ir_wgstrip: whole-map staging needs the map in one step");
     const int items = F * strips;
     static const int resident = [] {
         int dev = 0, cus = 0, per_cu = 0;
@@ -846,6 +978,7 @@ bool ir_strip_shape(int block, IrShape* out) {
     case 8: case 9: *out = wg_shape<G9>(); return true;
     case 10: *out = wg_shape<G11>(); return true;
     case 11: *out = wg_shape<G12>(); return true;
+    case 13: case 14: *out = wg_shape<G14>(); return true;
     default: return false;
     }
 }
@@ -862,6 +995,7 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
     case 8: case 9: launch_wgstrip<T, G9>(block, a, F, s); return true;
     case 10: launch_wgstrip<T, G11>(block, a, F, s); return true;
     case 11: launch_wgstrip<T, G12>(block, a, F, s); return true;
+    case 13: case 14: launch_wgstrip<T, G14>(block, a, F, s); return true;
     default: return false;
     }
 }
