@@ -717,7 +717,7 @@ private:
                 });
                 check_launch();
                 timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s,
-                      [&] { launch_delta(Q_, K_, V_, dec_, beta_, O_, B, s); });
+                      [&] { launch_delta(Q_, K_, V_, dec_, beta_, O_, B, kF32, s); });
                 check_launch();
                 timed("gated_norm", double(M) * (4.0 * 2 * kVD + TS * kVD), s,
                       [&] { launch_gated_norm<float>(O_, P_, g.o_norm_w, ON_, M, s); });

@@ -111,9 +111,10 @@ void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long 
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
                      const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
                      hipStream_t s);
-// gated delta rule, sequential over 321 tokens from zero state, fp32; O [rows][768]
+// gated delta rule, sequential over 321 tokens from zero state, fp32; O [rows][768].  exact: the reference's
+// 64-key fma chains (fp32 tier); else each column's keys split over 4 lane rows, partial sums added in a fixed order
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
-                  int B, hipStream_t s);
+                  int B, bool exact, hipStream_t s);
 // ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768]
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s);

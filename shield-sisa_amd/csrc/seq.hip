@@ -239,6 +239,121 @@ delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const flo
     }
 }
 
+// Half tiers: the same recurrence with each value column's 64 keys split over KQ lane groups of a wave (group kq
+// holds keys (64/KQ) kq .. of S[:, c]; 64/KQ columns per workgroup).  Per token a lane updates its state entries
+// and forms partial dots of the output and of the next prediction over its keys; the KQ partials are added in a
+// fixed order by cross-row lane swaps ((p0 + p1) + (p2 + p3) for KQ = 4, p0 + p1 for KQ = 2), so every lane holds
+// the same o and pred.  The dependent chain per token is 64/KQ instead of 64 fmas, which is what a small batch
+// waits on; at KQ = 2 the instruction count stays within a few percent of the exact kernel's.  The sums are
+// rounded in another (fixed) order than the reference's 64-key chain.
+__device__ __forceinline__ float row_pair_sum(float v, int g) {   // rows (0,1) and (2,3): v + partner row
+    const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    return v + __builtin_bit_cast(float, (g & 1) ? s[0] : s[1]);
+}
+__device__ __forceinline__ float half_sum(float v, int g) {       // rows (0,1) + (2,3)
+    const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    const float other = __builtin_bit_cast(float, g < 2 ? s[1] : s[0]);
+    return g < 2 ? v + other : other + v;
+}
+constexpr int DELTA_KQ = 2;   // key groups per value column in the half tiers
+template <int KQ>   // key groups per column: 2 (halves: lanes 0-31 / 32-63) or 4 (rows)
+__global__ void __launch_bounds__(64)
+delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+                   const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ O) {
+    constexpr int DS_COLS = 64 / KQ, KEYS = 64 / KQ;
+    constexpr int NB = 128 / DS_COLS;   // column blocks per head
+    const int cb = blockIdx.x % NB, wh = blockIdx.x / NB;
+    const int b = wh / kHeads, h = wh % kHeads;
+    const int lane = threadIdx.x, c16 = lane % DS_COLS, kq = lane / DS_COLS, g = lane >> 4;
+    const int col = h * 128 + cb * DS_COLS + c16;
+    __shared__ __attribute__((aligned(16))) float sq[DCH][64];
+    __shared__ __attribute__((aligned(16))) float sk[DCH + 1][64];
+    __shared__ float sv[DCH][DS_COLS];
+    __shared__ float sa[DCH], sb[DCH];
+    const long long row0 = (long long)b * kT;
+    float S[KEYS];
+#pragma unroll
+    for (int j = 0; j < KEYS; ++j) S[j] = 0.0f;
+    float pred = 0.0f;
+    for (int t0 = 0; t0 < kT; t0 += DCH) {
+        const int nt = min(DCH, kT - t0);
+        // staging (unconditional, token index clamped; slots past the last token zeroed / repeating the last k)
+        constexpr int QK4 = (DCH + 1) * 16;
+        constexpr int QKR = (QK4 + 63) / 64;
+        float4 rq[QKR], rk[QKR];
+        float rv[DCH * DS_COLS / 64];
+#pragma unroll
+        for (int k = 0; k < QKR; ++k) {
+            const int i = lane + k * 64;
+            const int tt = i >> 4, j4 = (i & 15) * 4;
+            const int t = min(t0 + tt, kT - 1);
+            rq[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            rk[k] = rq[k];
+            if (i < QK4) {
+                rq[k] = *reinterpret_cast<const float4*>(Q + (row0 + t) * kD + h * 64 + j4);
+                rk[k] = *reinterpret_cast<const float4*>(K + (row0 + t) * kD + h * 64 + j4);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < DCH * DS_COLS / 64; ++k) {
+            const int tt = kq + KQ * k;
+            rv[k] = V[(row0 + min(t0 + tt, kT - 1)) * kVD + col];
+        }
+#pragma unroll
+        for (int k = 0; k < QKR; ++k) {
+            const int i = lane + k * 64;
+            const int tt = i >> 4, j4 = (i & 15) * 4;
+            if (i < QK4) {
+                if (tt < DCH)
+                    *reinterpret_cast<float4*>(&sq[tt][j4]) = t0 + tt < kT ? rq[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                *reinterpret_cast<float4*>(&sk[tt][j4]) = rk[k];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < DCH * DS_COLS / 64; ++k) {
+            const int tt = kq + KQ * k;
+            sv[tt][c16] = t0 + tt < kT ? rv[k] : 0.0f;
+        }
+        if (lane < DCH) {
+            const int t = t0 + lane;
+            sa[lane] = t < kT ? dec[(row0 + t) * 8 + h] : 0.0f;
+            sb[lane] = t < kT ? beta[(row0 + t) * 8 + h] : 0.0f;
+        }
+        __syncthreads();
+        for (int i = 0; i < nt; ++i) {
+            const float a = sa[i], bt = sb[i];
+            const float u = (sv[i][c16] - a * pred) * bt;
+            float o = 0.0f, pn = 0.0f;
+#pragma unroll
+            for (int j4 = 0; j4 < KEYS; j4 += 4) {
+                const float4 kk = *reinterpret_cast<const float4*>(&sk[i][kq * KEYS + j4]);
+                const float4 qq = *reinterpret_cast<const float4*>(&sq[i][kq * KEYS + j4]);
+                const float4 kn = *reinterpret_cast<const float4*>(&sk[i + 1][kq * KEYS + j4]);
+                const float kv[4] = {kk.x, kk.y, kk.z, kk.w}, qv[4] = {qq.x, qq.y, qq.z, qq.w},
+                            nv[4] = {kn.x, kn.y, kn.z, kn.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x = __builtin_fmaf(kv[e], u, S[j4 + e] * a);
+                    S[j4 + e] = x;
+                    o = __builtin_fmaf(x, qv[e], o);
+                    pn = __builtin_fmaf(x, nv[e], pn);
+                }
+            }
+            if constexpr (KQ == 4) {
+                o = half_sum(row_pair_sum(o, g), g);
+                pred = half_sum(row_pair_sum(pn, g), g);
+            } else {
+                o = half_sum(o, g);
+                pred = half_sum(pn, g);
+            }
+            if (kq == 0) O[(row0 + t0 + i) * kVD + col] = o;
+        }
+        __syncthreads();
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ gated norm
 // 16 lanes per (row, head): lane l accumulates o[l + 16 z]^2 (z = 0..7), tree16, then ((o * rstd) * w) * silu(g)
 template <typename T>
@@ -442,8 +557,12 @@ void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, c
                        dt_bias, Q, K, V, dec, beta);
 }
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
-                  int B, hipStream_t s) {
-    hipLaunchKernelGGL(delta_kernel, dim3(B * kHeads * 2), dim3(DCOLS), 0, s, Q, K, V, dec, beta, O);
+                  int B, bool exact, hipStream_t s) {
+    if (exact)
+        hipLaunchKernelGGL(delta_kernel, dim3(B * kHeads * 2), dim3(DCOLS), 0, s, Q, K, V, dec, beta, O);
+    else
+        hipLaunchKernelGGL(delta_split_kernel<DELTA_KQ>, dim3(B * kHeads * (128 / (64 / DELTA_KQ))), dim3(64), 0, s, Q, K, V,
+                           dec, beta, O);
 }
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s) {
