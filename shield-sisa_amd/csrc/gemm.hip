@@ -138,6 +138,43 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
                  [&](int i, int j) { return tot[i][j]; });
 }
 
+// Small M (<= 4 rows, e.g. one window's SISA row): one thread per output (per SwiGLU pair), the same per-element
+// arithmetic as gemm_f32_kernel -- K blocks of 64, fma chain from +0 inside a block, the first block's sum taken
+// as is and the later ones added in order -- so results are bitwise those of the tiled kernel.
+template <bool SCALE>
+__global__ void __launch_bounds__(256) gemv_f32_kernel(GemmArgs p) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const long long m = blockIdx.y;
+    const int cols = p.swiglu ? p.N / 2 : p.N;
+    if (n >= cols) return;
+    const float* W = static_cast<const float*>(p.W);
+    const float* a = p.A + m * p.lda;
+    const float* sc = SCALE ? p.scale + (m / p.scale_rows) * p.ld_scale : nullptr;
+    auto dot = [&](int wn) {
+        const float* w = W + (long long)wn * p.ldw;
+        float tot = 0.0f;
+        for (int k0 = 0; k0 < p.K; k0 += F32_BK) {
+            const int k1 = min(p.K, k0 + F32_BK);
+            float blk = 0.0f;
+            for (int k = k0; k < k1; ++k) {
+                float av = a[k];
+                if constexpr (SCALE) av = sc[k] * av;
+                blk = __builtin_fmaf(av, w[k], blk);
+            }
+            tot = k0 == 0 ? blk : tot + blk;
+        }
+        return tot;
+    };
+    if (p.swiglu) {
+        const float gte = dot(2 * n), up = dot(2 * n + 1);
+        p.C[m * p.ldc + n] = silu(gte) * up;
+        return;
+    }
+    const float b = p.bias ? p.bias[n] : 0.0f;
+    const float r = p.res ? p.R[m * p.ldr + n] : 0.0f;
+    p.C[m * p.ldc + n] = epi_value(p, dot(n), b, r);
+}
+
 // ------------------------------------------------------------------------------------------------ MFMA
 // Direct-fragment GEMM for N <= 160 (the SE-block projects, CNN 1x1 layers): the workgroup covers every output
 // column in at most two column blocks, so A is read once or twice straight into MFMA fragments and staging it
@@ -397,6 +434,97 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
 
 inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
 
+// Small M (one clip's frames or window): one wave per 16 rows x SM_NT*16 columns, the operands of SM_D K steps in
+// flight (a ring of registers refilled as each step is consumed), so a wave waits on memory once per SM_D steps
+// instead of once per step.  The MFMA sequence of every output (K steps in order, the split products in order) is
+// the direct kernel's, so results are bitwise those of the large-M kernels: the kernel choice by M keeps rows
+// independent of the batch.
+constexpr int SM_NT = 2, SM_D = 4;
+
+template <typename T, bool SCALE>
+__global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    constexpr int P = S::P;
+    const int lane = threadIdx.x, r = lane & 15, g = lane >> 4;
+    const long long mbase = (long long)blockIdx.x * 16;
+    const int nbase = blockIdx.y * (SM_NT * 16);
+    const T* W = static_cast<const T*>(p.W);
+    const long long row = mbase + r, rc = row < p.M ? row : p.M - 1;
+    const bool row_live = row < p.M;
+    const int ksteps = (p.K + 31) / 32;
+    float xa[SM_D][8], xs[SCALE ? SM_D : 1][8];
+    uint4 wv[SM_D][SM_NT][P];
+    auto load = [&](int slot, int st) {
+        const int kc = min(st * 32 + g * 8, p.K - 8);
+        load8(p.A + rc * p.lda + kc, xa[slot]);
+        if constexpr (SCALE) load8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, xs[slot]);
+#pragma unroll
+        for (int nt = 0; nt < SM_NT; ++nt) {
+            const int col = min(nbase + nt * 16 + r, p.N - 1);
+#pragma unroll
+            for (int q = 0; q < P; ++q)
+                wv[slot][nt][q] = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)col * p.ldw + kc);
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < SM_D; ++d)
+        if (d < ksteps) load(d, d);
+    f32x4 acc[SM_NT];
+#pragma unroll
+    for (int nt = 0; nt < SM_NT; ++nt) acc[nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < ksteps; s0 += SM_D) {
+#pragma unroll
+        for (int d = 0; d < SM_D; ++d) {
+            const int st = s0 + d;
+            if (st >= ksteps) break;   // uniform
+            const bool kin = st * 32 + g * 8 < p.K;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float t = xa[d][e];
+                if constexpr (SCALE) t = xs[d][e] * t;
+                v[e] = kin && row_live ? t : 0.0f;
+            }
+            V8 a[P], b[SM_NT][P];
+            split8<T>(v, a);
+#pragma unroll
+            for (int nt = 0; nt < SM_NT; ++nt) {
+                const bool live = kin && nbase + nt * 16 + r < p.N;
+#pragma unroll
+                for (int q = 0; q < P; ++q) {
+                    const uint4 u = live ? wv[d][nt][q] : make_uint4(0u, 0u, 0u, 0u);
+                    b[nt][q] = *reinterpret_cast<const V8*>(&u);
+                }
+            }
+            if (st + SM_D < ksteps) load(d, st + SM_D);
+#pragma unroll
+            for (int i = 0; i < S::NPROD; ++i)
+#pragma unroll
+                for (int nt = 0; nt < SM_NT; ++nt) acc[nt] = S::mfma(a[S::ap(i)], b[nt][S::wp(i)], acc[nt]);
+        }
+    }
+    // lane holds C[mbase + g*4 + i][nbase + nt*16 + r]
+    if (p.swiglu) {  // 16-row panels alternate gate / up; SM_NT is 2 and nbase a multiple of 32
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long long m = mbase + g * 4 + i;
+            if (m >= p.M) continue;
+            const int panel = nbase / 16;
+            if ((panel + 1) * 16 <= p.N) p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[0][i]) * acc[1][i];
+        }
+        return;
+    }
+    epi_block<SM_NT>(p, [&](int i) { return mbase + g * 4 + i; }, [&](int j) { return nbase + j * 16 + r; },
+                     [&](int i, int j) { return acc[j][i]; });
+}
+
+template <typename T> void launch_small(const GemmArgs& p, hipStream_t s) {
+    const dim3 grid(cdiv(p.M, 16), cdiv(p.N, SM_NT * 16));
+    if (p.scale) hipLaunchKernelGGL((gemm_small_kernel<T, true>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((gemm_small_kernel<T, false>), grid, dim3(64), 0, s, p);
+}
+
 // SE-block projects (A rows scaled per frame, N <= 160).  The direct kernel spends two thirds of its vector-memory
 // instructions on operands its 4 waves share: the scale row of a frame and the K step's weight tile.  Here the
 // workgroup stages the scale rows of the (at most SE_MAXF) frames its 256 rows span in LDS once, and each K step's
@@ -565,6 +693,7 @@ void launch_lds(const GemmArgs& p, hipStream_t s) {
 // N up to 160 (CNN projects and 1x1 layers): direct fragments, 16-column tiles per wave chosen to minimise
 // padded columns (at most 5 per wave); wider N (last 1x1, sequence): LDS-staged 128 x 128 workgroup tiles.
 template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
+    if (p.M <= 2048) { launch_small<T>(p, s); return; }   // latency: one clip's shapes
     const int tiles = (p.N + 15) / 16;
     if (p.swiglu || tiles > 10) { launch_lds<T, 4, 4, 2, 2>(p, s); return; }
     int nt = tiles;
@@ -693,6 +822,13 @@ void check_args(const GemmArgs& p, bool mfma) {
 
 void gemm_f32(const GemmArgs& p, hipStream_t s) {
     check_args(p, false);
+    if (p.M <= 4) {
+        const int cols = p.swiglu ? p.N / 2 : p.N;
+        const dim3 grid(cdiv(cols, 256), p.M);
+        if (p.scale) hipLaunchKernelGGL(gemv_f32_kernel<true>, grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(gemv_f32_kernel<false>, grid, dim3(256), 0, s, p);
+        return;
+    }
     const dim3 grid(cdiv(p.M, F32_BM), cdiv(p.N, F32_BN));
     if (p.scale) hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(256), 0, s, p);

@@ -265,3 +265,16 @@ def test_fused_tail_matches_unfused(shv, weights, clips, mode):
             unfused = m.encode_frames(frames)
     assert np.all(np.isfinite(fused))
     assert np.array_equal(fused.view(np.uint32), unfused.view(np.uint32)), float(np.abs(fused - unfused).max())
+
+
+@pytest.mark.parametrize("mode", ["fp16", "bf16"])
+def test_row_independence_half(shv, weights, clips, mode):
+    """A clip's logit does not depend on the rest of the batch in the half tiers either.  A batch of 8 clips puts
+    the sequence GEMMs (8 x 321 rows) and the late SE projects above the small-M kernel's 2048-row limit while single
+    clips stay below it, so this also holds the small-M and large-M kernels to bitwise equal results."""
+    print(f"[gpu] {mode} row independence: batch of 8 vs one by one", flush=True)
+    with shv.Model(weights, mode, experimental=True, max_frames=160, max_windows=8) as m:
+        batch = m.predict(clips[:8])
+        single = np.concatenate([m.predict(clips[i:i + 1]) for i in range(8)])
+    assert np.all(np.isfinite(batch))
+    assert np.array_equal(batch.view(np.uint32), single.view(np.uint32)), float(np.abs(batch - single).max())
