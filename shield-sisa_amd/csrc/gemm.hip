@@ -138,41 +138,82 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
                  [&](int i, int j) { return tot[i][j]; });
 }
 
-// Small M (<= 4 rows, e.g. one window's SISA row): one thread per output (per SwiGLU pair), the same per-element
-// arithmetic as gemm_f32_kernel -- K blocks of 64, fma chain from +0 inside a block, the first block's sum taken
-// as is and the later ones added in order -- so results are bitwise those of the tiled kernel.
-template <bool SCALE>
-__global__ void __launch_bounds__(256) gemv_f32_kernel(GemmArgs p) {
-    const int n = blockIdx.x * 256 + threadIdx.x;
-    const long long m = blockIdx.y;
-    const int cols = p.swiglu ? p.N / 2 : p.N;
-    if (n >= cols) return;
-    const float* W = static_cast<const float*>(p.W);
-    const float* a = p.A + m * p.lda;
-    const float* sc = SCALE ? p.scale + (m / p.scale_rows) * p.ld_scale : nullptr;
-    auto dot = [&](int wn) {
-        const float* w = W + (long long)wn * p.ldw;
-        float tot = 0.0f;
-        for (int k0 = 0; k0 < p.K; k0 += F32_BK) {
-            const int k1 = min(p.K, k0 + F32_BK);
-            float blk = 0.0f;
-            for (int k = k0; k < k1; ++k) {
-                float av = a[k];
-                if constexpr (SCALE) av = sc[k] * av;
-                blk = __builtin_fmaf(av, w[k], blk);
-            }
-            tot = k0 == 0 ? blk : tot + blk;
+// Small M (<= 4 rows, e.g. one window's SISA row): the same per-element arithmetic as gemm_f32_kernel -- K blocks
+// of 64, fma chain from +0 inside a block, the first block's sum taken as is and the later ones added in order -- so
+// results are bitwise those of the tiled kernel.  Only the chain inside a K block is serial, so a lane owns one
+// (weight row, K block) pair: a wave covers GV_OPW = 64 / nkb weight rows (even for SwiGLU, whose gate and up rows
+// are adjacent) with all their K blocks, and the block sums are added in order through LDS.  The lane's 64 weights
+// stay in registers across the M rows.
+constexpr int GV_MAXM = 4;
+template <bool SCALE, bool VEC>
+__device__ __forceinline__ void gv_load64(float* dst, const float* src, const float* sc, int n) {
+    if (VEC && n == F32_BK) {
+#pragma unroll
+        for (int j = 0; j < F32_BK / 4; ++j) {
+            const float4 v = reinterpret_cast<const float4*>(src)[j];
+            dst[4 * j] = v.x; dst[4 * j + 1] = v.y; dst[4 * j + 2] = v.z; dst[4 * j + 3] = v.w;
         }
+        if constexpr (SCALE) {
+#pragma unroll
+            for (int j = 0; j < F32_BK / 4; ++j) {
+                const float4 c = reinterpret_cast<const float4*>(sc)[j];
+                dst[4 * j] = c.x * dst[4 * j]; dst[4 * j + 1] = c.y * dst[4 * j + 1];
+                dst[4 * j + 2] = c.z * dst[4 * j + 2]; dst[4 * j + 3] = c.w * dst[4 * j + 3];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < F32_BK; ++k) {
+            float v = k < n ? src[k] : 0.0f;
+            if constexpr (SCALE) v = k < n ? sc[k] * v : 0.0f;
+            dst[k] = v;
+        }
+    }
+}
+template <bool SCALE, bool VEC>
+__global__ void __launch_bounds__(64) gemv_f32_kernel(GemmArgs p, int nkb, int opw) {
+    __shared__ float part[GV_MAXM][64];
+    const int lane = threadIdx.x;
+    const int o = lane / nkb, kb = lane - o * nkb;
+    const int wn = blockIdx.x * opw + o;
+    const bool live = o < opw && wn < p.N;
+    const int k0 = kb * F32_BK, n = min(F32_BK, p.K - k0);
+    const float* W = static_cast<const float*>(p.W);
+    if (live) {
+        float w[F32_BK];
+        gv_load64<false, VEC>(w, W + (long long)wn * p.ldw + k0, nullptr, n);
+        for (int m = 0; m < p.M; ++m) {
+            float a[F32_BK];
+            gv_load64<SCALE, VEC>(a, p.A + (long long)m * p.lda + k0,
+                                  SCALE ? p.scale + (m / p.scale_rows) * p.ld_scale + k0 : nullptr, n);
+            float blk = 0.0f;
+            if (n == F32_BK) {
+#pragma unroll
+                for (int k = 0; k < F32_BK; ++k) blk = __builtin_fmaf(a[k], w[k], blk);
+            } else {
+#pragma unroll
+                for (int k = 0; k < F32_BK; ++k)
+                    if (k < n) blk = __builtin_fmaf(a[k], w[k], blk);
+            }
+            part[m][lane] = blk;
+        }
+    }
+    __syncthreads();
+    if (!live || kb != 0 || (p.swiglu && (o & 1))) return;
+    auto total = [&](int m, int l0) {
+        float tot = part[m][l0];
+        for (int i = 1; i < nkb; ++i) tot = tot + part[m][l0 + i];
         return tot;
     };
-    if (p.swiglu) {
-        const float gte = dot(2 * n), up = dot(2 * n + 1);
-        p.C[m * p.ldc + n] = silu(gte) * up;
-        return;
+    for (int m = 0; m < p.M; ++m) {
+        if (p.swiglu) {   // weight rows (wn, wn + 1) = (gate, up) of output wn / 2
+            p.C[(long long)m * p.ldc + (wn >> 1)] = silu(total(m, lane)) * total(m, lane + nkb);
+            continue;
+        }
+        const float b = p.bias ? p.bias[wn] : 0.0f;
+        const float r = p.res ? p.R[(long long)m * p.ldr + wn] : 0.0f;
+        p.C[(long long)m * p.ldc + wn] = epi_value(p, total(m, lane), b, r);
     }
-    const float b = p.bias ? p.bias[n] : 0.0f;
-    const float r = p.res ? p.R[m * p.ldr + n] : 0.0f;
-    p.C[m * p.ldc + n] = epi_value(p, dot(n), b, r);
 }
 
 // ------------------------------------------------------------------------------------------------ MFMA
@@ -822,11 +863,20 @@ void check_args(const GemmArgs& p, bool mfma) {
 
 void gemm_f32(const GemmArgs& p, hipStream_t s) {
     check_args(p, false);
-    if (p.M <= 4) {
-        const int cols = p.swiglu ? p.N / 2 : p.N;
-        const dim3 grid(cdiv(cols, 256), p.M);
-        if (p.scale) hipLaunchKernelGGL(gemv_f32_kernel<true>, grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL(gemv_f32_kernel<false>, grid, dim3(256), 0, s, p);
+    const int nkb = cdiv(p.K, F32_BK);
+    if (p.M <= GV_MAXM && nkb <= 32) {
+        const int opw = p.swiglu ? (64 / nkb) & ~1 : 64 / nkb;
+        const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+        const bool vec = al16(p.A) && al16(p.W) && p.lda % 4 == 0 && p.ldw % 4 == 0 &&
+                         (!p.scale || (al16(p.scale) && p.ld_scale % 4 == 0));
+        const dim3 grid(cdiv(p.N, opw));
+        if (p.scale) {
+            if (vec) hipLaunchKernelGGL((gemv_f32_kernel<true, true>), grid, dim3(64), 0, s, p, nkb, opw);
+            else hipLaunchKernelGGL((gemv_f32_kernel<true, false>), grid, dim3(64), 0, s, p, nkb, opw);
+        } else {
+            if (vec) hipLaunchKernelGGL((gemv_f32_kernel<false, true>), grid, dim3(64), 0, s, p, nkb, opw);
+            else hipLaunchKernelGGL((gemv_f32_kernel<false, false>), grid, dim3(64), 0, s, p, nkb, opw);
+        }
         return;
     }
     const dim3 grid(cdiv(p.M, F32_BM), cdiv(p.N, F32_BN));

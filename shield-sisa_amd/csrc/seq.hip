@@ -257,8 +257,64 @@ __device__ __forceinline__ float half_sum(float v, int g) {       // rows (0,1) 
     const float other = __builtin_bit_cast(float, g < 2 ? s[1] : s[0]);
     return g < 2 ? v + other : other + v;
 }
+// One token's operands for a lane's KEYS keys: k, q and the next token's k (for the prediction), decay, beta, v.
+template <int KEYS>
+struct DTok {
+    float4 k[KEYS / 4], q[KEYS / 4], n[KEYS / 4];
+    float a, b, v;
+    __device__ __forceinline__ void load_k(const float* sk) {
+#pragma unroll
+        for (int j = 0; j < KEYS / 4; ++j) k[j] = reinterpret_cast<const float4*>(sk)[j];
+    }
+    __device__ __forceinline__ void take_k(const DTok& prev) {
+#pragma unroll
+        for (int j = 0; j < KEYS / 4; ++j) k[j] = prev.n[j];
+    }
+    __device__ __forceinline__ void load_rest(const float* sq, const float* skn, float a_, float b_, float v_) {
+#pragma unroll
+        for (int j = 0; j < KEYS / 4; ++j) {
+            q[j] = reinterpret_cast<const float4*>(sq)[j];
+            n[j] = reinterpret_cast<const float4*>(skn)[j];
+        }
+        a = a_;
+        b = b_;
+        v = v_;
+    }
+};
+// One token of the split recurrence: updates S and pred, returns o.  Per key j (in order): S_j = fma(k_j, u, S_j a);
+// o and the next prediction are fma chains from +0 over the lane's keys, then summed across the key groups.
+template <int KQ, int KEYS>
+__device__ __forceinline__ float delta_token(const DTok<KEYS>& t, float* S, float& pred, int g) {
+    const float u = (t.v - t.a * pred) * t.b;
+    float o = 0.0f, pn = 0.0f;
+#pragma unroll
+    for (int j4 = 0; j4 < KEYS / 4; ++j4) {
+        const float kv[4] = {t.k[j4].x, t.k[j4].y, t.k[j4].z, t.k[j4].w};
+        const float qv[4] = {t.q[j4].x, t.q[j4].y, t.q[j4].z, t.q[j4].w};
+        const float nv[4] = {t.n[j4].x, t.n[j4].y, t.n[j4].z, t.n[j4].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float x = __builtin_fmaf(kv[e], u, S[4 * j4 + e] * t.a);
+            S[4 * j4 + e] = x;
+            o = __builtin_fmaf(x, qv[e], o);
+            pn = __builtin_fmaf(x, nv[e], pn);
+        }
+    }
+    if constexpr (KQ == 4) {
+        o = half_sum(row_pair_sum(o, g), g);
+        pred = half_sum(row_pair_sum(pn, g), g);
+    } else {
+        o = half_sum(o, g);
+        pred = half_sum(pn, g);
+    }
+    return o;
+}
 constexpr int DELTA_KQ = 2;   // key groups per value column in the half tiers
-template <int KQ>   // key groups per column: 2 (halves: lanes 0-31 / 32-63) or 4 (rows)
+constexpr int kDeltaPipeWaves = 1024;   // one wave per SIMD (256 CUs x 4)
+// PIPE: full 32-token chunks run unrolled with token i+1's operands read from LDS ahead of token i's chain (for
+// grids of at most one wave per SIMD, where nothing else hides the LDS latency; the unrolled chunk holds ~256
+// VGPRs).  Both forms issue the same arithmetic per token, so their results are bitwise equal.
+template <int KQ, bool PIPE>   // KQ: key groups per column: 2 (halves: lanes 0-31 / 32-63) or 4 (rows)
 __global__ void __launch_bounds__(64)
 delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
                    const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ O) {
@@ -322,33 +378,33 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
             sb[lane] = t < kT ? beta[(row0 + t) * 8 + h] : 0.0f;
         }
         __syncthreads();
-        for (int i = 0; i < nt; ++i) {
-            const float a = sa[i], bt = sb[i];
-            const float u = (sv[i][c16] - a * pred) * bt;
-            float o = 0.0f, pn = 0.0f;
+        // both lane halves hold the same o after the cross-half sum and store it (same value, same address), so
+        // the token step has no branch
+        if (PIPE && nt == DCH) {
+            // full chunk, unrolled: token i+1's q, next k, decay, beta and v are read from LDS before token i's
+            // chain, so with one wave per SIMD (small batches) no LDS round trip sits on the serial path; token
+            // i+1's k is token i's next k, already in registers
+            DTok<KEYS> cur;
+            cur.load_k(&sk[0][kq * KEYS]);
+            cur.load_rest(&sq[0][kq * KEYS], &sk[1][kq * KEYS], sa[0], sb[0], sv[0][c16]);
 #pragma unroll
-            for (int j4 = 0; j4 < KEYS; j4 += 4) {
-                const float4 kk = *reinterpret_cast<const float4*>(&sk[i][kq * KEYS + j4]);
-                const float4 qq = *reinterpret_cast<const float4*>(&sq[i][kq * KEYS + j4]);
-                const float4 kn = *reinterpret_cast<const float4*>(&sk[i + 1][kq * KEYS + j4]);
-                const float kv[4] = {kk.x, kk.y, kk.z, kk.w}, qv[4] = {qq.x, qq.y, qq.z, qq.w},
-                            nv[4] = {kn.x, kn.y, kn.z, kn.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float x = __builtin_fmaf(kv[e], u, S[j4 + e] * a);
-                    S[j4 + e] = x;
-                    o = __builtin_fmaf(x, qv[e], o);
-                    pn = __builtin_fmaf(x, nv[e], pn);
+            for (int i = 0; i < DCH; ++i) {
+                DTok<KEYS> nxt;
+                if (i + 1 < DCH) {
+                    nxt.take_k(cur);
+                    nxt.load_rest(&sq[i + 1][kq * KEYS], &sk[i + 2][kq * KEYS], sa[i + 1], sb[i + 1],
+                                  sv[i + 1][c16]);
                 }
+                O[(row0 + t0 + i) * kVD + col] = delta_token<KQ, KEYS>(cur, S, pred, g);
+                if (i + 1 < DCH) cur = nxt;
             }
-            if constexpr (KQ == 4) {
-                o = half_sum(row_pair_sum(o, g), g);
-                pred = half_sum(row_pair_sum(pn, g), g);
-            } else {
-                o = half_sum(o, g);
-                pred = half_sum(pn, g);
+        } else {
+            for (int i = 0; i < nt; ++i) {
+                DTok<KEYS> cur;
+                cur.load_k(&sk[i][kq * KEYS]);
+                cur.load_rest(&sq[i][kq * KEYS], &sk[i + 1][kq * KEYS], sa[i], sb[i], sv[i][c16]);
+                O[(row0 + t0 + i) * kVD + col] = delta_token<KQ, KEYS>(cur, S, pred, g);
             }
-            if (kq == 0) O[(row0 + t0 + i) * kVD + col] = o;
         }
         __syncthreads();
     }
@@ -561,8 +617,13 @@ void launch_delta(const float* Q, const float* K, const float* V, const float* d
     if (exact)
         hipLaunchKernelGGL(delta_kernel, dim3(B * kHeads * 2), dim3(DCOLS), 0, s, Q, K, V, dec, beta, O);
     else
-        hipLaunchKernelGGL(delta_split_kernel<DELTA_KQ>, dim3(B * kHeads * (128 / (64 / DELTA_KQ))), dim3(64), 0, s, Q, K, V,
-                           dec, beta, O);
+    {
+        const int waves = B * kHeads * (128 / (64 / DELTA_KQ));
+        if (waves <= kDeltaPipeWaves)
+            hipLaunchKernelGGL((delta_split_kernel<DELTA_KQ, true>), dim3(waves), dim3(64), 0, s, Q, K, V, dec, beta, O);
+        else
+            hipLaunchKernelGGL((delta_split_kernel<DELTA_KQ, false>), dim3(waves), dim3(64), 0, s, Q, K, V, dec, beta, O);
+    }
 }
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s) {
