@@ -38,7 +38,7 @@ BLOCKS = [(16, 16, 16), (16, 64, 24), (24, 72, 24), (24, 72, 40), (40, 120, 40),
           (80, 200, 80), (80, 184, 80), (80, 184, 80), (80, 480, 112), (112, 672, 112), (112, 672, 160),
           (160, 960, 160), (160, 960, 160)]
 FAMILIES = sorted({"ir_%dx%dx%d" % b for b in BLOCKS}) + [
-    "se_reduce", "gemm_pw", "dw", "stem", "se_pool", "pool", "tail_pool", "gemm_seq", "gemm_f32_small", "gemm_se_fc", "rmsnorm", "gdn_prep",
+    "se_reduce", "gemm_pw", "dw", "stem", "stem_ir_16x16x16", "se_pool", "pool", "tail_pool", "gemm_seq", "gemm_f32_small", "gemm_se_fc", "rmsnorm", "gdn_prep",
     "delta", "gated_norm", "sisa", "head", "assemble"]
 
 

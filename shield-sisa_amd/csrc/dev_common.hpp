@@ -65,6 +65,7 @@ __device__ __forceinline__ float div6_nb(float v) {
     const float q = v * r;
     return __builtin_fmaf(__builtin_fmaf(-q, 6.0f, v), r, q);
 }
+__device__ __forceinline__ float hswish_nb(float x) { return div6_nb(x * clamp06(x)); }
 __device__ __forceinline__ float apply_act_nb(float v, int act) {
     switch (act) {
     case ACT_RELU: return relu(v);

@@ -400,7 +400,9 @@ private:
     float *se_pool_ = nullptr, *se_hid_ = nullptr, *se_scale_ = nullptr;
     float *H_ = nullptr, *P_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *dec_ = nullptr, *beta_ = nullptr,
           *O_ = nullptr;
-    float *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;
+    float *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;   // fp32 tier: the sequence GEMMs' A operands
+    G *XNh_ = nullptr, *ONh_ = nullptr, *HIDh_ = nullptr;    // MFMA tiers: the same, written pre-split by producers
+    long long mrows_ = 0;                                     // rows of those buffers (part stride = mrows_ * width)
     float *XL_ = nullptr, *QC_ = nullptr, *Y_ = nullptr, *X1_ = nullptr, *X2_ = nullptr, *HIDL_ = nullptr;
     float* tok_direct_ = nullptr;
     const float** tokptr_direct_ = nullptr;
@@ -436,9 +438,16 @@ private:
         dec_ = amem_.make<float>(Mm * 8);
         beta_ = amem_.make<float>(Mm * 8);
         O_ = amem_.make<float>(Mm * kVD);
-        XN_ = amem_.make<float>(Mm * kD);
-        ON_ = amem_.make<float>(Mm * kVD);
-        HID_ = amem_.make<float>(Mm * kFF);
+        mrows_ = (long long)Mm;
+        if constexpr (kF32) {
+            XN_ = amem_.make<float>(Mm * kD);
+            ON_ = amem_.make<float>(Mm * kVD);
+            HID_ = amem_.make<float>(Mm * kFF);
+        } else {
+            XNh_ = amem_.make<G>(weight_parts<G>() * Mm * kD);
+            ONh_ = amem_.make<G>(weight_parts<G>() * Mm * kVD);
+            HIDh_ = amem_.make<G>(weight_parts<G>() * Mm * kFF);
+        }
         XL_ = amem_.make<float>(Bm * kD);
         QC_ = amem_.make<float>(Bm * 576);
         Y_ = amem_.make<float>(Bm * kD);
@@ -593,10 +602,14 @@ private:
 
     // half tiers: one fused kernel per block (SE blocks: fused expand + depthwise, SE, project GEMM)
     void run_encode_fused(const uint8_t* frames, int F, float* tokens, hipStream_t s) {
-        timed("stem", double(F) * (kFrameBytes + 90.0 * 160 * 16 * TS), s,
-              [&] { launch_stem<float>(frames, X_, lut_, stem_w_, stem_b_, F, s); });
-        check_launch();
-        dump("cnn00", X_, size_t(90) * 160 * 16, s);
+        // the stem runs inside block 1's strip kernel unless its output is to be dumped (or SHV_HIP_NO_STEM_FUSE)
+        const bool stem_fused = strip_kernels_enabled() && dump_dir_.empty() && !std::getenv("SHV_HIP_NO_STEM_FUSE");
+        if (!stem_fused) {
+            timed("stem", double(F) * (kFrameBytes + 90.0 * 160 * 16 * TS), s,
+                  [&] { launch_stem<float>(frames, X_, lut_, stem_w_, stem_b_, F, s); });
+            check_launch();
+            dump("cnn00", X_, size_t(90) * 160 * 16, s);
+        }
         float* cur = X_;
         float* nxt = XB_;
         for (int i = 0; i < 15; ++i) {
@@ -612,8 +625,15 @@ private:
             if (!c.se) {
                 a.wproj = b.fproj_w.w; a.wproj_stride = b.fproj_w.stride; a.bproj = b.fproj_b;
                 a.Y = nxt;
-                timed(b.fam, double(F) * (HWi * c.cin + HWo * c.cout) * TS, s,
-                      [&] { launch_ir_block<G>(i, a, F, s); });
+                if (i == 0 && stem_fused) {
+                    a.X = nullptr;
+                    a.img = frames; a.lut = lut_; a.stem_w = stem_w_; a.stem_b = stem_b_;
+                    timed("stem_ir_16x16x16", double(F) * (kFrameBytes + HWo * c.cout * TS), s,
+                          [&] { launch_stem_block1<G>(a, F, s); });
+                } else {
+                    timed(b.fam, double(F) * (HWi * c.cin + HWo * c.cout) * TS, s,
+                          [&] { launch_ir_block<G>(i, a, F, s); });
+                }
                 check_launch();
             } else {
                 a.D = D_; a.part = se_part_;
@@ -692,8 +712,18 @@ private:
     }
 
     // ---------------------------------------------------------------- sequence
+    // the A operand of a sequence GEMM: fp32 (exact tier) or the producer's split parts (MFMA tiers)
+    static constexpr int kAS = kF32 ? 4 : int(sizeof(G)) * weight_parts<G>();   // bytes per A value
+    void set_a(GemmArgs& p, const float* a32, const G* ah, int width) const {
+        p.lda = width;
+        if constexpr (kF32) p.A = a32;
+        else { p.Ah = ah; p.astride = mrows_ * width; }
+    }
     void rmsnorm_all(const float* w, hipStream_t s, int M) {
-        timed("rmsnorm", double(M) * kD * (4 + TS), s, [&] { launch_rmsnorm<float>(H_, kD, w, XN_, kD, M, s); });
+        timed("rmsnorm", double(M) * kD * (4 + kAS), s, [&] {
+            if constexpr (kF32) launch_rmsnorm<float>(H_, kD, w, XN_, kD, M, s);
+            else launch_rmsnorm<G>(H_, kD, w, XNh_, kD, M, s, mrows_ * kD);
+        });
         check_launch();
     }
 
@@ -709,7 +739,7 @@ private:
                 rmsnorm_all(g.norm_w, s, M);
                 GemmArgs pi;
                 pi.M = M; pi.N = kGn; pi.K = kD;
-                pi.A = XN_; pi.lda = kD; pi.ldw = kD;
+                set_a(pi, XN_, XNh_, kD); pi.ldw = kD;
                 pi.C = P_; pi.ldc = kGld;
                 gemm("gemm_seq", pi, g.in_w, s);
                 timed("gdn_prep", double(M) * (4.0 * 1548 * 4 + 4.0 * (2 * kD + kVD + 16)), s, [&] {
@@ -719,12 +749,14 @@ private:
                 timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s,
                       [&] { launch_delta(Q_, K_, V_, dec_, beta_, O_, B, kF32, s); });
                 check_launch();
-                timed("gated_norm", double(M) * (4.0 * 2 * kVD + TS * kVD), s,
-                      [&] { launch_gated_norm<float>(O_, P_, g.o_norm_w, ON_, M, s); });
+                timed("gated_norm", double(M) * (4.0 * 2 * kVD + kAS * kVD), s, [&] {
+                    if constexpr (kF32) launch_gated_norm<float>(O_, P_, g.o_norm_w, ON_, M, s);
+                    else launch_gated_norm<G>(O_, P_, g.o_norm_w, ONh_, M, s, mrows_ * kVD);
+                });
                 check_launch();
                 GemmArgs po;
                 po.M = M; po.N = kD; po.K = kVD;
-                po.A = ON_; po.lda = kVD; po.ldw = kVD;
+                set_a(po, ON_, ONh_, kVD); po.ldw = kVD;
                 po.C = H_; po.ldc = kD;
                 po.R = H_; po.ldr = kD; po.res = reps == 2 ? 2 : 1;
                 gemm("gemm_seq", po, g.out_w, s);
@@ -732,12 +764,14 @@ private:
             rmsnorm_all(g.ffn_norm_w, s, M);
             GemmArgs pu;
             pu.M = M; pu.N = 2 * kFF; pu.K = kD;
-            pu.A = XN_; pu.lda = kD; pu.ldw = kD;
-            pu.C = HID_; pu.ldc = kFF; pu.swiglu = 1;
+            set_a(pu, XN_, XNh_, kD); pu.ldw = kD;
+            pu.ldc = kFF; pu.swiglu = 1;
+            if constexpr (kF32) pu.C = HID_;
+            else { pu.Ch = HIDh_; pu.cstride = mrows_ * kFF; }
             gemm("gemm_seq", pu, g.up_w, s);
             GemmArgs pd;
             pd.M = M; pd.N = kD; pd.K = kFF;
-            pd.A = HID_; pd.lda = kFF; pd.ldw = kFF;
+            set_a(pd, HID_, HIDh_, kFF); pd.ldw = kFF;
             pd.C = H_; pd.ldc = kD;
             pd.R = H_; pd.ldr = kD; pd.res = 1;
             gemm("gemm_seq", pd, g.down_w, s);
@@ -747,7 +781,7 @@ private:
         rmsnorm_all(s_attn_norm_, s, M);
         GemmArgs pa;
         pa.M = M; pa.N = kSn; pa.K = kD;
-        pa.A = XN_; pa.lda = kD; pa.ldw = kD;
+        set_a(pa, XN_, XNh_, kD); pa.ldw = kD;
         pa.bias = s_in_b_;
         pa.C = P_; pa.ldc = kSld;
         gemm("gemm_seq", pa, s_in_w_, s);

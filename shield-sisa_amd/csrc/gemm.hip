@@ -58,6 +58,19 @@ __device__ __forceinline__ void epi_block(const GemmArgs& p, Row row, Col col, V
     }
 }
 
+// A SwiGLU output: fp32, or its split parts when the consumer takes pre-split A
+template <typename T>
+__device__ __forceinline__ void swiglu_store(const GemmArgs& p, long long m, int col, float v) {
+    if (p.Ch) {
+        T part[Split<T>::P];
+        Split<T>::split(v, part);
+#pragma unroll
+        for (int q = 0; q < Split<T>::P; ++q) static_cast<T*>(p.Ch)[q * p.cstride + m * p.ldc + col] = part[q];
+    } else {
+        p.C[m * p.ldc + col] = v;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ fp32 VALU
 constexpr int F32_BM = 64, F32_BN = 64, F32_BK = 64;
 
@@ -138,13 +151,14 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
                  [&](int i, int j) { return tot[i][j]; });
 }
 
-// Small M (<= 4 rows, e.g. one window's SISA row): the same per-element arithmetic as gemm_f32_kernel -- K blocks
+// Small M (<= 256 rows, e.g. the windows' last SISA rows): the same per-element arithmetic as gemm_f32_kernel -- K blocks
 // of 64, fma chain from +0 inside a block, the first block's sum taken as is and the later ones added in order -- so
 // results are bitwise those of the tiled kernel.  Only the chain inside a K block is serial, so a lane owns one
 // (weight row, K block) pair: a wave covers GV_OPW = 64 / nkb weight rows (even for SwiGLU, whose gate and up rows
 // are adjacent) with all their K blocks, and the block sums are added in order through LDS.  The lane's 64 weights
-// stay in registers across the M rows.
-constexpr int GV_MAXM = 4;
+// stay in registers across the block's rows (blockIdx.y takes GV_ROWS-row chunks of M).
+constexpr int GV_ROWS = 8;      // rows per workgroup
+constexpr int GV_MAXM = 256;    // larger M goes to the tiled kernel
 template <bool SCALE, bool VEC>
 __device__ __forceinline__ void gv_load64(float* dst, const float* src, const float* sc, int n) {
     if (VEC && n == F32_BK) {
@@ -172,8 +186,9 @@ __device__ __forceinline__ void gv_load64(float* dst, const float* src, const fl
 }
 template <bool SCALE, bool VEC>
 __global__ void __launch_bounds__(64) gemv_f32_kernel(GemmArgs p, int nkb, int opw) {
-    __shared__ float part[GV_MAXM][64];
+    __shared__ float part[GV_ROWS][64];
     const int lane = threadIdx.x;
+    const int mbase = blockIdx.y * GV_ROWS, mrows = min(GV_ROWS, p.M - mbase);
     const int o = lane / nkb, kb = lane - o * nkb;
     const int wn = blockIdx.x * opw + o;
     const bool live = o < opw && wn < p.N;
@@ -182,9 +197,10 @@ __global__ void __launch_bounds__(64) gemv_f32_kernel(GemmArgs p, int nkb, int o
     if (live) {
         float w[F32_BK];
         gv_load64<false, VEC>(w, W + (long long)wn * p.ldw + k0, nullptr, n);
-        for (int m = 0; m < p.M; ++m) {
+        for (int i = 0; i < mrows; ++i) {
+            const long long m = mbase + i;
             float a[F32_BK];
-            gv_load64<SCALE, VEC>(a, p.A + (long long)m * p.lda + k0,
+            gv_load64<SCALE, VEC>(a, p.A + m * p.lda + k0,
                                   SCALE ? p.scale + (m / p.scale_rows) * p.ld_scale + k0 : nullptr, n);
             float blk = 0.0f;
             if (n == F32_BK) {
@@ -195,24 +211,25 @@ __global__ void __launch_bounds__(64) gemv_f32_kernel(GemmArgs p, int nkb, int o
                 for (int k = 0; k < F32_BK; ++k)
                     if (k < n) blk = __builtin_fmaf(a[k], w[k], blk);
             }
-            part[m][lane] = blk;
+            part[i][lane] = blk;
         }
     }
     __syncthreads();
     if (!live || kb != 0 || (p.swiglu && (o & 1))) return;
-    auto total = [&](int m, int l0) {
-        float tot = part[m][l0];
-        for (int i = 1; i < nkb; ++i) tot = tot + part[m][l0 + i];
+    auto total = [&](int i, int l0) {
+        float tot = part[i][l0];
+        for (int j = 1; j < nkb; ++j) tot = tot + part[i][l0 + j];
         return tot;
     };
-    for (int m = 0; m < p.M; ++m) {
+    const float b = p.bias && !p.swiglu ? p.bias[wn] : 0.0f;
+    for (int i = 0; i < mrows; ++i) {
+        const long long m = mbase + i;
         if (p.swiglu) {   // weight rows (wn, wn + 1) = (gate, up) of output wn / 2
-            p.C[(long long)m * p.ldc + (wn >> 1)] = silu(total(m, lane)) * total(m, lane + nkb);
+            p.C[m * p.ldc + (wn >> 1)] = silu(total(i, lane)) * total(i, lane + nkb);
             continue;
         }
-        const float b = p.bias ? p.bias[wn] : 0.0f;
-        const float r = p.res ? p.R[(long long)m * p.ldr + wn] : 0.0f;
-        p.C[(long long)m * p.ldc + wn] = epi_value(p, total(m, lane), b, r);
+        const float r = p.res ? p.R[m * p.ldr + wn] : 0.0f;
+        p.C[m * p.ldc + wn] = epi_value(p, total(i, lane), b, r);
     }
 }
 
@@ -317,7 +334,7 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p
                 for (int nt = 0; nt + 1 < NT; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
-                        p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[mt][nt][i]) * acc[mt][nt + 1][i];
+                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
                 }
             }
         return;
@@ -339,8 +356,9 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 constexpr int LG_KT = 64;          // K per staged step: two MFMA K steps
 constexpr int LG_LD = LG_KT + 8;   // staged row stride in T elements (144 B): 16-lane fragment reads hit 64 banks once
 
-template <typename T, int WM, int WN, int WGM, int WGN, bool SCALE>
-__global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
+template <typename T, int WM, int WN, int WGM, int WGN, bool SCALE, bool AH>
+__global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p, int mblocks, int nblocks) {
+    static_assert(!(SCALE && AH), "pre-split A carries no SE scale");
     static_assert(WGM * WGN == 4, "4 waves");
     typedef Split<T> S;
     typedef typename S::V8 V8;
@@ -350,19 +368,41 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) T Ws[P][BN][LG_LD];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
     const int wm = wave / WGN, wn = wave % WGN;
-    const long long m0 = (long long)blockIdx.x * BM;
-    const int n0 = blockIdx.y * BN;
+    // XCD-aware order (as in gemm_direct_kernel): the column blocks of a row block take consecutive ids on one XCD
+    const int xcd = blockIdx.x % XCDS, slot = blockIdx.x / XCDS;
+    const int mb = (slot / nblocks) * XCDS + xcd, nb = slot % nblocks;
+    if (mb >= mblocks) return;
+    const long long m0 = (long long)mb * BM;
+    const int n0 = nb * BN;
     const T* W = static_cast<const T*>(p.W);
 
     constexpr int A4 = BM * (LG_KT / 4);      // float4s of an A tile
-    constexpr int AR = (A4 + 255) / 256;
+    constexpr int AR = AH ? 1 : (A4 + 255) / 256;
+    constexpr int A8 = BM * (LG_KT / 8);      // 8-element groups of a pre-split A part tile
+    constexpr int AHR = AH ? (A8 + 255) / 256 : 1;
     constexpr int W8 = BN * (LG_KT / 8);      // 8-element groups of a W part tile
     constexpr int WR = (W8 + 255) / 256;
     float4 ra[AR];
+    uint4 rah[AHR][AH ? P : 1];
     uint4 rw[WR][P];
+    const T* Ah = static_cast<const T*>(p.Ah);
     auto load = [&](int k0) {
+        if constexpr (AH) {
 #pragma unroll
-        for (int k = 0; k < AR; ++k) {
+            for (int k = 0; k < AHR; ++k) {
+                const int i = tid + 256 * k;
+                const int row = i / (LG_KT / 8), c = i % (LG_KT / 8);
+                const long long gm = m0 + row;
+                const int kk = k0 + c * 8;
+                const bool in = i < A8 && gm < p.M && kk < p.K;
+#pragma unroll
+                for (int q = 0; q < P; ++q)
+                    rah[k][q] = in ? *reinterpret_cast<const uint4*>(Ah + q * p.astride + gm * p.lda + kk)
+                                   : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < (AH ? 0 : AR); ++k) {
             const int i = tid + 256 * k;
             const int row = i / (LG_KT / 4), c = i % (LG_KT / 4);
             const long long gm = m0 + row;
@@ -390,8 +430,18 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
         }
     };
     auto store = [&]() {
+        if constexpr (AH) {
 #pragma unroll
-        for (int k = 0; k < AR; ++k) {
+            for (int k = 0; k < AHR; ++k) {
+                const int i = tid + 256 * k;
+                if (i >= A8) continue;
+                const int row = i / (LG_KT / 8), c = i % (LG_KT / 8);
+#pragma unroll
+                for (int q = 0; q < P; ++q) *reinterpret_cast<uint4*>(&As[q][row][c * 8]) = rah[k][q];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < (AH ? 0 : AR); ++k) {
             const int i = tid + 256 * k;
             if (i >= A4) continue;
             const int row = i / (LG_KT / 4), c = i % (LG_KT / 4);
@@ -462,7 +512,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p) {
                 for (int nt = 0; nt + 1 < WN; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
-                        p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[mt][nt][i]) * acc[mt][nt + 1][i];
+                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
                 }
             }
         return;
@@ -482,8 +532,9 @@ inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + 
 // independent of the batch.
 constexpr int SM_NT = 2, SM_D = 4;
 
-template <typename T, bool SCALE>
+template <typename T, bool SCALE, bool AH>
 __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
+    static_assert(!(SCALE && AH), "pre-split A carries no SE scale");
     typedef Split<T> S;
     typedef typename S::V8 V8;
     constexpr int P = S::P;
@@ -494,11 +545,18 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
     const long long row = mbase + r, rc = row < p.M ? row : p.M - 1;
     const bool row_live = row < p.M;
     const int ksteps = (p.K + 31) / 32;
-    float xa[SM_D][8], xs[SCALE ? SM_D : 1][8];
+    float xa[AH ? 1 : SM_D][8], xs[SCALE ? SM_D : 1][8];
+    uint4 xh[AH ? SM_D : 1][P];
     uint4 wv[SM_D][SM_NT][P];
+    const T* Ah = static_cast<const T*>(p.Ah);
     auto load = [&](int slot, int st) {
         const int kc = min(st * 32 + g * 8, p.K - 8);
-        load8(p.A + rc * p.lda + kc, xa[slot]);
+        if constexpr (AH) {
+#pragma unroll
+            for (int q = 0; q < P; ++q) xh[slot][q] = *reinterpret_cast<const uint4*>(Ah + q * p.astride + rc * p.lda + kc);
+        } else {
+            load8(p.A + rc * p.lda + kc, xa[slot]);
+        }
         if constexpr (SCALE) load8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, xs[slot]);
 #pragma unroll
         for (int nt = 0; nt < SM_NT; ++nt) {
@@ -520,15 +578,23 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
             const int st = s0 + d;
             if (st >= ksteps) break;   // uniform
             const bool kin = st * 32 + g * 8 < p.K;
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float t = xa[d][e];
-                if constexpr (SCALE) t = xs[d][e] * t;
-                v[e] = kin && row_live ? t : 0.0f;
-            }
             V8 a[P], b[SM_NT][P];
-            split8<T>(v, a);
+            if constexpr (AH) {
+#pragma unroll
+                for (int q = 0; q < P; ++q) {
+                    const uint4 u = kin && row_live ? xh[d][q] : make_uint4(0u, 0u, 0u, 0u);
+                    a[q] = *reinterpret_cast<const V8*>(&u);
+                }
+            } else {
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float t = xa[d][e];
+                    if constexpr (SCALE) t = xs[d][e] * t;
+                    v[e] = kin && row_live ? t : 0.0f;
+                }
+                split8<T>(v, a);
+            }
 #pragma unroll
             for (int nt = 0; nt < SM_NT; ++nt) {
                 const bool live = kin && nbase + nt * 16 + r < p.N;
@@ -552,7 +618,7 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
             const long long m = mbase + g * 4 + i;
             if (m >= p.M) continue;
             const int panel = nbase / 16;
-            if ((panel + 1) * 16 <= p.N) p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[0][i]) * acc[1][i];
+            if ((panel + 1) * 16 <= p.N) swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu(acc[0][i]) * acc[1][i]);
         }
         return;
     }
@@ -562,8 +628,9 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
 
 template <typename T> void launch_small(const GemmArgs& p, hipStream_t s) {
     const dim3 grid(cdiv(p.M, 16), cdiv(p.N, SM_NT * 16));
-    if (p.scale) hipLaunchKernelGGL((gemm_small_kernel<T, true>), grid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL((gemm_small_kernel<T, false>), grid, dim3(64), 0, s, p);
+    if (p.Ah) hipLaunchKernelGGL((gemm_small_kernel<T, false, true>), grid, dim3(64), 0, s, p);
+    else if (p.scale) hipLaunchKernelGGL((gemm_small_kernel<T, true, false>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((gemm_small_kernel<T, false, false>), grid, dim3(64), 0, s, p);
 }
 
 // SE-block projects (A rows scaled per frame, N <= 160).  The direct kernel spends two thirds of its vector-memory
@@ -726,9 +793,19 @@ void launch_direct(const GemmArgs& p, hipStream_t s) {
 
 template <typename T, int WM, int WN, int WGM, int WGN>
 void launch_lds(const GemmArgs& p, hipStream_t s) {
-    const dim3 grid(cdiv(p.M, 16LL * WM * WGM), cdiv(p.N, 16 * WN * WGN));
-    if (p.scale) hipLaunchKernelGGL((gemm_lds_kernel<T, WM, WN, WGM, WGN, true>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((gemm_lds_kernel<T, WM, WN, WGM, WGN, false>), grid, dim3(256), 0, s, p);
+    const int mblocks = (int)cdiv(p.M, 16LL * WM * WGM), nblocks = (int)cdiv(p.N, 16 * WN * WGN);
+    const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
+    if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_lds: grid too large");
+    const dim3 grid((unsigned)blocks);
+    if (p.Ah)
+        hipLaunchKernelGGL((gemm_lds_kernel<T, WM, WN, WGM, WGN, false, true>), grid, dim3(256), 0, s, p, mblocks,
+                           nblocks);
+    else if (p.scale)
+        hipLaunchKernelGGL((gemm_lds_kernel<T, WM, WN, WGM, WGN, true, false>), grid, dim3(256), 0, s, p, mblocks,
+                           nblocks);
+    else
+        hipLaunchKernelGGL((gemm_lds_kernel<T, WM, WN, WGM, WGN, false, false>), grid, dim3(256), 0, s, p, mblocks,
+                           nblocks);
 }
 
 // N up to 160 (CNN projects and 1x1 layers): direct fragments, 16-column tiles per wave chosen to minimise
@@ -737,6 +814,7 @@ template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
     if (p.M <= 2048) { launch_small<T>(p, s); return; }   // latency: one clip's shapes
     const int tiles = (p.N + 15) / 16;
     if (p.swiglu || tiles > 10) { launch_lds<T, 4, 4, 2, 2>(p, s); return; }
+    if (p.Ah) throw std::runtime_error("gemm: pre-split A needs N > 160 or M <= 2048");
     int nt = tiles;
     if (tiles > 5) {
         int best_cols = 1 << 30;
@@ -844,7 +922,12 @@ __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict_
 
 void check_args(const GemmArgs& p, bool mfma) {
     if (p.M <= 0 || p.N <= 0 || p.K <= 0) throw std::runtime_error("gemm: empty shape");
-    if (!p.A || !p.W || !p.C) throw std::runtime_error("gemm: null operand");
+    if (!(p.A || p.Ah) || !p.W || !(p.C || p.Ch)) throw std::runtime_error("gemm: null operand");
+    if ((p.Ah || p.Ch) && !mfma) throw std::runtime_error("gemm_f32: pre-split operands are for the MFMA tiers");
+    if (p.Ah && (p.A || p.scale || p.astride < (long long)(p.M - 1) * p.lda + p.K))
+        throw std::runtime_error("gemm: pre-split A takes no fp32 A or SE scale and needs a part stride");
+    if (p.Ch && (p.C || !p.swiglu || p.cstride < (long long)(p.M - 1) * p.ldc + p.N / 2))
+        throw std::runtime_error("gemm: a pre-split output is a SwiGLU output with a part stride");
     if (p.res && !p.R) throw std::runtime_error("gemm: residual without R");
     if (p.scale && (p.scale_rows <= 0 || p.ld_scale < p.K)) throw std::runtime_error("gemm: bad SE scale");
     if (mfma) {
@@ -869,7 +952,7 @@ void gemm_f32(const GemmArgs& p, hipStream_t s) {
         const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
         const bool vec = al16(p.A) && al16(p.W) && p.lda % 4 == 0 && p.ldw % 4 == 0 &&
                          (!p.scale || (al16(p.scale) && p.ld_scale % 4 == 0));
-        const dim3 grid(cdiv(p.N, opw));
+        const dim3 grid(cdiv(p.N, opw), cdiv(p.M, GV_ROWS));
         if (p.scale) {
             if (vec) hipLaunchKernelGGL((gemv_f32_kernel<true, true>), grid, dim3(64), 0, s, p, nkb, opw);
             else hipLaunchKernelGGL((gemv_f32_kernel<true, false>), grid, dim3(64), 0, s, p, nkb, opw);

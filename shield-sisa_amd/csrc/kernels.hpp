@@ -27,6 +27,11 @@ struct GemmArgs {
     float* C = nullptr; long long ldc = 0;
     const float* R = nullptr; long long ldr = 0; int res = 0;
     int swiglu = 0;
+    // MFMA tiers: A given pre-split (parts [P][..][lda] of the tier's type, part stride astride elements) instead of
+    // fp32 A; and a SwiGLU output written pre-split (parts [P][..][ldc], part stride cstride) instead of fp32 C.  The
+    // split is a function of each fp32 value, so both give results bitwise equal to the fp32 forms.
+    const void* Ah = nullptr; long long astride = 0;
+    void* Ch = nullptr; long long cstride = 0;
 };
 
 // fp32 tier: VALU GEMM, each output accumulated in K blocks of 64 (fma chain from +0 per block, block sums added
@@ -86,11 +91,18 @@ struct IrArgs {
     const void* wproj = nullptr; long long wproj_stride = 0;
     const float* bproj = nullptr;
     int H = 0, W = 0, Ho = 0, Wo = 0, tiles_x = 0, ntiles = 0, frames = 0;
+    // block 1 with the stem fused in: uint8 frames [F][180][320][3], byte -> float table [3][256], stem weights
+    // [27][16] (tap (dy,dx,c) major) and bias [16]; X is then unused
+    const uint8_t* img = nullptr;
+    const float *lut = nullptr, *stem_w = nullptr, *stem_b = nullptr;
 };
 template <typename T> void launch_ir_block(int block, const IrArgs& a, int F, hipStream_t s);
 // Strip kernels (pixel-per-lane layout): blocks 1-3 one wave per strip, later blocks one workgroup per strip.
 // Enabled unless SHV_HIP_NO_STRIP is set (then every block takes the tile kernels).
 bool strip_kernels_enabled();
+// stem + block 1 in one strip kernel (half tiers): the stem output never reaches HBM; bitwise equal to launch_stem
+// followed by block 1's strip kernel
+template <typename T> void launch_stem_block1(const IrArgs& a, int F, hipStream_t s);
 // the shape of block i's strip kernel when it has one that is not interchangeable with its tile kernel's (the tile
 // is then (rows per step, columns per strip), which the SE partial sums are laid out by)
 bool ir_strip_shape(int block, IrShape* out);
@@ -103,9 +115,11 @@ void launch_se_reduce(const float* part, int ntiles, int cexpp, int cexp, int hw
 // ---------------------------------------------------------------- sequence (fp32 residual stream)
 void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,
                      hipStream_t s);
-// out[r] = (x[r] * (1 / sqrt(sum(x^2) / 384 + 1e-6))) * w with the reference's 16-lane sum tree
+// out[r] = (x[r] * (1 / sqrt(sum(x^2) / 384 + 1e-6))) * w with the reference's 16-lane sum tree.  T = f16 / bf16:
+// out holds the split parts of each value (part stride pstride elements), the pre-split A of the next GEMM.
 template <typename T>
-void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s);
+void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s,
+                    long long pstride = 0);
 // short conv4 + SiLU on q|k|v, per-head L2 norm (q * 0.125), decay = exp(neg_rate * softplus(a + dt_bias)),
 // beta = sigmoid(b).  P [rows][2320] -> Q, K [rows][384], V [rows][768], dec, beta [rows][8]
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
@@ -115,9 +129,10 @@ void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, c
 // 64-key fma chains (fp32 tier); else each column's keys split over 4 lane rows, partial sums added in a fixed order
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
                   int B, bool exact, hipStream_t s);
-// ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768]
+// ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768] (T = f16 / bf16: split parts, as launch_rmsnorm)
 template <typename T>
-void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s);
+void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,
+                       long long pstride = 0);
 // SISA last-row attention per (window, head): S [rows][1072] (B rotated in place), QC [B][576] -> Y [B][384]
 void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s);
 // final RMSNorm + Linear(384,128) + SiLU + Linear(128,1); w0 [128][384]

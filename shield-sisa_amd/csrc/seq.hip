@@ -5,11 +5,27 @@
 #include "dev_common.hpp"
 #include "host_model.hpp"
 #include "kernels.hpp"
+#include "mfma.hpp"
+
+#include <type_traits>
 
 namespace shv {
 namespace {
 
 inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
+
+// A normalised value for the next GEMM: fp32, or (MFMA tiers) its split parts, part q at base[q * pstride + idx]
+template <typename T>
+__device__ __forceinline__ void put_value(T* base, long long pstride, long long idx, float y) {
+    if constexpr (std::is_same<T, float>::value) {
+        base[idx] = y;
+    } else {
+        T part[Split<T>::P];
+        Split<T>::split(y, part);
+#pragma unroll
+        for (int q = 0; q < Split<T>::P; ++q) base[q * pstride + idx] = part[q];
+    }
+}
 
 // ------------------------------------------------------------------------------------------------ assemble
 // h[b*321 + t] = tokens(b, t / 16)[t % 16] + pos[t] (t < 320); readout at t = 320.  One block per row, float4.
@@ -34,7 +50,7 @@ assemble_kernel(const float* const* __restrict__ tok_ptrs, const float* __restri
 template <typename T>
 __global__ void __launch_bounds__(256)
 rmsnorm_kernel(const float* __restrict__ x, long long ldx, const float* __restrict__ w, T* __restrict__ out,
-               long long ldo, int rows) {
+               long long ldo, long long pstride, int rows) {
     const long long row = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
     const int l = threadIdx.x & 15;
     const bool live = row < rows;
@@ -48,9 +64,8 @@ rmsnorm_kernel(const float* __restrict__ x, long long ldx, const float* __restri
     const float s = tree16(acc);
     if (!live) return;
     const float inv = 1.0f / sqrtf(s / 384.0f + 1e-6f);
-    T* o = out + row * ldo;
 #pragma unroll
-    for (int i = 0; i < 24; ++i) o[i * 16 + l] = from_f<T>((v[i] * inv) * w[i * 16 + l]);
+    for (int i = 0; i < 24; ++i) put_value(out, pstride, row * ldo + i * 16 + l, (v[i] * inv) * w[i * 16 + l]);
 }
 
 // ------------------------------------------------------------------------------------------------ GDN prep
@@ -415,7 +430,7 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
 template <typename T>
 __global__ void __launch_bounds__(256)
 gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, const float* __restrict__ w,
-                  T* __restrict__ out, int rows) {
+                  T* __restrict__ out, long long pstride, int rows) {
     const long long grp = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
     const int l = threadIdx.x & 15;
     const bool live = grp < (long long)rows * kHeads;
@@ -432,11 +447,10 @@ gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, cons
     if (!live) return;
     const float rstd = 1.0f / sqrtf(s / 128.0f + 1e-6f);
     const float* g = P + row * kGld + kGg + h * 128;
-    T* dst = out + row * kVD + h * 128;
 #pragma unroll
     for (int z = 0; z < 8; ++z) {
         const int i = z * 16 + l;
-        dst[i] = from_f<T>(((v[z] * rstd) * w[i]) * silu(g[i]));
+        put_value(out, pstride, row * kVD + h * 128 + i, ((v[z] * rstd) * w[i]) * silu(g[i]));
     }
 }
 
@@ -602,9 +616,10 @@ void launch_assemble(const float* const* tok_ptrs, const float* pos, const float
     hipLaunchKernelGGL(assemble_kernel, dim3(B * kT), dim3(96), 0, s, tok_ptrs, pos, readout, h);
 }
 template <typename T>
-void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s) {
+void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s,
+                    long long pstride) {
     hipLaunchKernelGGL(rmsnorm_kernel<T>, dim3(cdiv((long long)rows * 16, 256)), dim3(256), 0, s, x, ldx, w, out, ldo,
-                       rows);
+                       pstride, rows);
 }
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
                      const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
@@ -626,9 +641,10 @@ void launch_delta(const float* Q, const float* K, const float* V, const float* d
     }
 }
 template <typename T>
-void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s) {
+void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,
+                       long long pstride) {
     hipLaunchKernelGGL(gated_norm_kernel<T>, dim3(cdiv((long long)rows * kHeads * 16, 256)), dim3(256), 0, s, O, P, w,
-                       out, rows);
+                       out, pstride, rows);
 }
 void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s) {
     hipLaunchKernelGGL(sisa_kernel, dim3(B * kHeads), dim3(SA_THREADS), 0, s, S, QC, lam, Y);
@@ -641,7 +657,13 @@ void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool,
     hipLaunchKernelGGL(store_tokens_kernel, dim3(F), dim3(256), 0, s, tokens, slots, pool);
 }
 
-template void launch_rmsnorm<float>(const float*, long long, const float*, float*, long long, int, hipStream_t);
-template void launch_gated_norm<float>(const float*, const float*, const float*, float*, int, hipStream_t);
+#define SHV_NORMS(T)                                                                                             \
+    template void launch_rmsnorm<T>(const float*, long long, const float*, T*, long long, int, hipStream_t,      \
+                                    long long);                                                                  \
+    template void launch_gated_norm<T>(const float*, const float*, const float*, T*, int, hipStream_t, long long);
+SHV_NORMS(float)
+SHV_NORMS(f16)
+SHV_NORMS(bf16)
+#undef SHV_NORMS
 
 }  // namespace shv

@@ -140,17 +140,54 @@ template <typename T, class C> struct StripLds {
     static constexpr int BYTES = (WE + WP) * (int)sizeof(T) + BE * 4;
 };
 
-template <typename T, class C>
-__global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int strips, int items) {
+// Stem fused into block 1 (STEM): per step a wave needs stem rows iy0 .. iy0 + 7 at its 16 columns, i.e. frame rows
+// 2 iy0 - 1 .. 2 iy0 + 15 (17) and frame columns 2 x - 1 .. 2 x + 1 of the strip's stem columns x (33 frame pixels).
+// The stem convolution runs on the matrix cores in the same transposed form as the expand layers: with the K order
+// k = 4 tap + channel (channel 3 a zero pad; taps 9 .. 11 zero weights), the B fragment of lane (r, g) for K chunk
+// q is the 4 channels of frame pixel (2 j + dy, 2 r + dx), tap 4 q + g = (dy, dx), and the result fragment is
+// already the pixel-per-lane layout of block 1's input rows (pixel r, channels 4 g ..).  The wave stages its frame
+// pixels in a private LDS tile [part][17][33][4], each byte mapped through a table that holds the split parts of
+// the byte -> float value, so no split arithmetic runs per pixel; pixels outside the frame stage as 0.  Per stem row:
+// 3 K chunks x the split products, + bias, hardswish.  Split operands keep fp32-level operand precision; the result
+// differs from the fp32 stem kernel by accumulation rounding.  The tile is private to the wave: in-order LDS
+// execution plus a wait on the wave's own LDS traffic separates staging from use.
+constexpr int STEM_FR = 17, STEM_FC = 33 * 3;    // staged frame rows, bytes per staged row
+constexpr int STEM_TILE = STEM_FR * 33 * 4;      // T elements of one part of a wave's tile
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Lane l stages byte columns l and l + 64 (the latter for l < STEM_FC - 64) of the step's 17 frame rows.  Addresses
+// are clamped into the frame so that every load is unconditional and all are in flight together; bytes outside the
+// frame are masked when staged.
+constexpr int STEM_NB = 2 * STEM_FR;
+__device__ __forceinline__ void stem_fetch(const uint8_t* img, long long f, int fy0, int fb0, int lane,
+                                           int (&bytes)[STEM_NB]) {
+    const uint8_t* fr = img + f * (180 * 320 * 3);
+    // unsigned 32-bit offsets from the frame's (scalar) base address
+    const unsigned b0 = min(max(fb0 + lane, 0), 320 * 3 - 1), b1 = min(max(fb0 + lane + 64, 0), 320 * 3 - 1);
+#pragma unroll
+    for (int u = 0; u < STEM_FR; ++u) {
+        const unsigned row = unsigned(min(max(fy0 + u, 0), 179)) * (320 * 3);
+        bytes[2 * u] = fr[row + b0];
+        bytes[2 * u + 1] = fr[row + b1];
+    }
+}
+
+template <typename T, class C, bool STEM = false>
+__global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int strips, int items,
+                                                              const float* __restrict__ stem_w,
+                                                              const float* __restrict__ stem_b) {
     typedef Split16<T> S16;
     typedef typename S16::V4 V4;
     typedef StripLds<T, C> L;
     constexpr int P = Split<T>::P;
+    static_assert(!STEM || (!C::EXPAND && C::S == 1 && C::CIN == 16 && C::IR == 8), "the stem feeds block 1 only");
     __shared__ __attribute__((aligned(16))) unsigned char lds_raw[(L::BYTES + 15) / 16 * 16];
+    // STEM: the waves' frame tiles [wave][part][STEM_TILE], then the byte -> parts table [part][768]
+    __shared__ __attribute__((aligned(16))) T stem_lds[STEM ? (ST_THREADS / 64) * P * STEM_TILE + P * 768 : 1];
     T* We = reinterpret_cast<T*>(lds_raw);                               // [P][CT*16][KP]
     T* Wp = We + L::WE;                                                  // [P][OT*16][CP]
     float* Be = reinterpret_cast<float*>(lds_raw + (L::WE + L::WP) * sizeof(T));   // [2][CT*16]
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: item and frame math stays scalar
 
     // ---- weights -> LDS (the only workgroup-wide step)
     {
@@ -174,8 +211,37 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
             Wp[(q * COUTP + o) * C::CP + k] = wproj[q * a.wproj_stride + (long long)o * CEXPP + k];
         }
         (void)CEXPP;
+        if constexpr (STEM) {
+            for (int i = tid; i < (ST_THREADS / 64) * P * STEM_TILE; i += ST_THREADS) stem_lds[i] = T(0.0f);
+            for (int i = tid; i < 768; i += ST_THREADS) {
+                T part[P];
+                Split<T>::split(a.lut[i], part);
+#pragma unroll
+                for (int q = 0; q < P; ++q) stem_lds[(ST_THREADS / 64) * P * STEM_TILE + q * 768 + i] = part[q];
+            }
+        }
     }
     __syncthreads();
+    T* const stile = stem_lds + (STEM ? wave * P * STEM_TILE : 0);
+    const T* const stab = stem_lds + (STEM ? (ST_THREADS / 64) * P * STEM_TILE : 0);
+    // STEM: stem weight fragments (A row r = output channel r, k = 4 tap + channel), bias, per-lane tile offsets
+    V4 sw[STEM ? 3 : 1][P];
+    float sbias[4];
+    int soff[STEM ? 3 : 1];
+    if constexpr (STEM) {
+#pragma unroll
+        for (int qc = 0; qc < 3; ++qc) {
+            const int t = 4 * qc + g;
+            float w4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w4[i] = t < 9 && i < 3 ? stem_w[(t * 3 + i) * 16 + r] : 0.0f;
+            split4<T>(make_float4(w4[0], w4[1], w4[2], w4[3]), sw[qc]);
+            const int tt = min(t, 8), dy = tt / 3, dx = tt - 3 * dy;   // taps 9 .. 11 read tap 8 (zero weights)
+            soff[qc] = (dy * 33 + 2 * r + dx) * 4;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sbias[i] = stem_b[4 * g + i];
+    }
 
     // ---- per-lane constants: depthwise taps + bias (lane r <= 9 of each row: tap r, bias), project bias
     constexpr int CEXPP_DW = (C::CEXP + 31) / 32 * 32;
@@ -215,12 +281,53 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
 #pragma unroll
         for (int t = 0; t < C::NT; ++t) be_off[t] = pin[t] ? 0 : C::CT * 16;
 
+        int sbytes[STEM ? STEM_NB : 1];   // STEM: the step's staged frame bytes
         for (int oy0 = 0; oy0 < Ho; oy0 += C::R) {
             const int iy0 = C::S * oy0 - 1;
             // ---- the step's input rows: fp32 (no expand) or split into B fragments
             V4 xf[C::EXPAND ? C::IR : 1][C::NT][C::KSI][P];
             float4 xe[C::EXPAND ? 1 : C::IR];
             bool rin[C::IR];
+            float4 sx[STEM ? C::IR : 1];   // STEM: the step's stem rows (pixel r, channels 4 g ..)
+            if constexpr (STEM) {
+                const int fy0 = 2 * iy0 - 1, fb0 = (2 * (strip * C::VALID - 1) - 1) * 3;   // first row, first byte
+                if (oy0 == 0) stem_fetch(a.img, f, fy0, fb0, lane, sbytes);
+                wave_lds_sync();   // the previous step's reads of the tile are done
+                {
+                    const int e1 = lane + 64;
+                    const bool c0 = fb0 + lane >= 0 && fb0 + lane < 320 * 3, c1 = e1 < STEM_FC && fb0 + e1 < 320 * 3;
+                    const int d0 = (lane / 3) * 4 + lane % 3, d1 = (e1 / 3) * 4 + e1 % 3;   // tile slots
+                    const int t0 = (lane % 3) * 256, t1 = (e1 % 3) * 256;                 // table rows
+#pragma unroll
+                    for (int u = 0; u < STEM_FR; ++u) {
+                        const bool rin_u = fy0 + u >= 0 && fy0 + u < 180;   // uniform
+#pragma unroll
+                        for (int q = 0; q < P; ++q) {
+                            const T x0 = stab[q * 768 + t0 + sbytes[2 * u]];
+                            stile[q * STEM_TILE + u * 132 + d0] = rin_u && c0 ? x0 : T(0.0f);
+                            if (e1 < STEM_FC) {
+                                const T x1 = stab[q * 768 + t1 + sbytes[2 * u + 1]];
+                                stile[q * STEM_TILE + u * 132 + d1] = rin_u && c1 ? x1 : T(0.0f);
+                            }
+                        }
+                    }
+                }
+                // the next step's bytes load while this step computes
+                if (oy0 + C::R < Ho) stem_fetch(a.img, f, fy0 + 2 * C::R, fb0, lane, sbytes);
+                wave_lds_sync();
+#pragma unroll
+                for (int j = 0; j < C::IR; ++j) {
+                    f32x4 acc = f32x4{sbias[0], sbias[1], sbias[2], sbias[3]};
+#pragma unroll
+                    for (int qc = 0; qc < 3; ++qc) {
+                        V4 xf[P];
+#pragma unroll
+                        for (int q = 0; q < P; ++q) xf[q] = lds_frag<T>(stile + q * STEM_TILE + 2 * j * 132 + soff[qc]);
+                        acc = mfma_split16<T>(sw[qc], xf, acc);
+                    }
+                    sx[j] = make_float4(hswish_nb(acc[0]), hswish_nb(acc[1]), hswish_nb(acc[2]), hswish_nb(acc[3]));
+                }
+            }
 #pragma unroll
             for (int j = 0; j < C::IR; ++j) {
                 const int iy = iy0 + j;
@@ -232,7 +339,8 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
                     for (int ks = 0; ks < C::KSI; ++ks) {
                         const int ch = min(ks * 16 + 4 * g, C::CIN - 4);
                         const float4 v =
-                            *reinterpret_cast<const float4*>(Xf + ((long long)iyc * W + ixc[t]) * C::CIN + ch);
+                            STEM ? sx[j]
+                                 : *reinterpret_cast<const float4*>(Xf + ((long long)iyc * W + ixc[t]) * C::CIN + ch);
                         if constexpr (C::EXPAND) {
                             split4<T>(v, xf[j][t][ks]);
                         } else {
@@ -362,7 +470,7 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
     }
 }
 
-template <typename T, class C> void launch_strip(int block, const IrArgs& a, int F, hipStream_t s) {
+template <typename T, class C, bool STEM = false> void launch_strip(int block, const IrArgs& a, int F, hipStream_t s) {
     // the engine pads the weights to the block's IrShape; the kernel reads them with these paddings
     const IrShape sh = ir_shape(block, std::is_same<T, bf16>::value);
     if (sh.cin != C::CIN || sh.cexp != C::CEXP || sh.cout != C::COUT || sh.k != 3 || sh.stride != C::S || sh.se ||
@@ -378,13 +486,15 @@ template <typename T, class C> void launch_strip(int block, const IrArgs& a, int
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_strip_kernel<T, C>, ST_THREADS, 0) != hipSuccess)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_strip_kernel<T, C, STEM>, ST_THREADS, 0) !=
+                hipSuccess)
             throw std::runtime_error("ir_strip: cannot query the device occupancy");
         return std::max(1, cus) * std::max(1, per_cu);
     }();
     const int waves_per_wg = ST_THREADS / 64;
     const int grid = std::min((items + waves_per_wg - 1) / waves_per_wg, resident);
-    hipLaunchKernelGGL((ir_strip_kernel<T, C>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, items);
+    hipLaunchKernelGGL((ir_strip_kernel<T, C, STEM>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, items, a.stem_w,
+                       a.stem_b);
 }
 
 
@@ -1001,5 +1111,13 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
 }
 template bool launch_ir_strip<f16>(int, const IrArgs&, int, hipStream_t);
 template bool launch_ir_strip<bf16>(int, const IrArgs&, int, hipStream_t);
+
+template <typename T> void launch_stem_block1(const IrArgs& a, int F, hipStream_t s) {
+    if (!a.img || !a.lut || !a.stem_w || !a.stem_b || a.H != 90 || a.W != 160)
+        throw std::runtime_error("stem + block 1: needs the frames, the table, the stem weights and the 90x160 map");
+    launch_strip<T, S1, true>(0, a, F, s);
+}
+template void launch_stem_block1<f16>(const IrArgs&, int, hipStream_t);
+template void launch_stem_block1<bf16>(const IrArgs&, int, hipStream_t);
 
 }  // namespace shv

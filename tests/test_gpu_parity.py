@@ -252,11 +252,12 @@ def test_fused_blocks_match_layer_path(shv, weights, clips, mode):
 
 
 @pytest.mark.parametrize("mode", ["fp16", "bf16"])
-def test_fused_tail_matches_unfused(shv, weights, clips, mode):
-    """The fused last 1x1 + hardswish + 4x4 pool of the half tiers (taken when no dump directory is set) repeats
-    the unfused GEMM's split products in the same K order, its epilogue and the pool kernel's bin sums: tokens are
-    bitwise those of the unfused path (taken while dumping)."""
+def test_fused_tail_matches_unfused(shv, weights, clips, mode, monkeypatch):
+    """The fused last 1x1 + hardswish + 4x4 pool of the half tiers (taken when no dump directory is set) repeats the
+    unfused GEMM's split products in the same K order, its epilogue and the pool kernel's bin sums: tokens are bitwise
+    those of the unfused path (taken while dumping).  The stem runs unfused on both sides."""
     print(f"[gpu] {mode} fused tail vs unfused tail, frames of clip 0", flush=True)
+    monkeypatch.setenv("SHV_HIP_NO_STEM_FUSE", "1")
     frames = clips[0][:8]
     with shv.Model(weights, mode, experimental=True, use_graphs=0) as m:
         fused = m.encode_frames(frames)
@@ -265,6 +266,28 @@ def test_fused_tail_matches_unfused(shv, weights, clips, mode):
             unfused = m.encode_frames(frames)
     assert np.all(np.isfinite(fused))
     assert np.array_equal(fused.view(np.uint32), unfused.view(np.uint32)), float(np.abs(fused - unfused).max())
+
+
+@pytest.mark.parametrize("mode", ["fp16", "bf16"])
+def test_fused_stem_close_to_unfused(shv, weights, clips, mode, monkeypatch):
+    """The stem inside block 1's strip kernel runs on the matrix cores with split operands (fp32-level operand
+    precision) instead of the fp32 stem kernel's fma chains: over whole frames (borders included) its tokens stay
+    within accumulation-rounding distance of the unfused path's, and so do the logits."""
+    print(f"[gpu] {mode} fused stem vs stem kernel, frames of clips 0-3", flush=True)
+    frames = clips[:4].reshape(-1, 180, 320, 3)
+    with shv.Model(weights, mode, experimental=True, use_graphs=0, max_frames=80, max_windows=4) as m:
+        fused = m.encode_frames(frames)
+        lf = m.predict(clips[:4])
+        monkeypatch.setenv("SHV_HIP_NO_STEM_FUSE", "1")
+        unfused = m.encode_frames(frames)
+        lu = m.predict(clips[:4])
+    assert np.all(np.isfinite(fused))
+    scale = float(np.abs(unfused).max())
+    err = float(np.abs(fused - unfused).max())
+    print(f"[gpu] {mode}: token max|diff| {err:.3e} (max |token| {scale:.3e}), logit max|diff| "
+          f"{float(np.abs(lf - lu).max()):.3e}", flush=True)
+    assert err <= 1e-3 * scale
+    assert float(np.abs(lf - lu).max()) <= 2e-3
 
 
 @pytest.mark.parametrize("mode", ["fp16", "bf16"])
