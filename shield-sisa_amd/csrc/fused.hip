@@ -854,7 +854,7 @@ template <typename T> IrShape ir_shape_t(int block) {
 }
 IrShape ir_shape(int block, bool bf16_tier) {
     IrShape s;
-    if (strip_kernels_enabled() && ir_strip_shape(block, &s)) return s;
+    if (strip_kernels_enabled() && ir_strip_shape(block, bf16_tier, &s)) return s;
     return bf16_tier ? ir_shape_t<bf16>(block) : ir_shape_t<f16>(block);
 }
 

@@ -105,7 +105,7 @@ bool strip_kernels_enabled();
 template <typename T> void launch_stem_block1(const IrArgs& a, int F, hipStream_t s);
 // the shape of block i's strip kernel when it has one that is not interchangeable with its tile kernel's (the tile
 // is then (rows per step, columns per strip), which the SE partial sums are laid out by)
-bool ir_strip_shape(int block, IrShape* out);
+bool ir_strip_shape(int block, bool bf16_tier, IrShape* out);
 // launches block i's strip kernel; false when the block has none
 template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hipStream_t s);
 // SE squeeze from the fused kernel's tile sums: pooled[f][c] = (sum over tiles in order) / (float)hw

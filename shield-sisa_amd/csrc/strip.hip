@@ -514,22 +514,23 @@ template <typename T, class C, bool STEM = false> void launch_strip(int block, c
 // last tap.  Columns outside the map expand from -1e30 (ReLU and hardswish both give 0 there), rows outside the
 // map are skipped (E = 0).
 template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_, int MINB_ = 1, int ROLLK_ = 0,
-          int NOPF_ = 0, int WHOLE_H_ = 0>
+          int NOPF_ = 0, int WHOLE_H_ = 0, int NPOS_ = 16>
 struct WgCfg {
     static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, KS = KS_, S = S_, R = R_;
     static constexpr int MINB = MINB_;   // workgroups per CU the register allocation must allow
     // ROLLK: the expand runs K-step-outer in a rolled loop (weight parts loaded per K step, one step ahead), so only
     // one K step's fragments are live -- for wide inputs, where the unrolled form holds every row's fragments
     static constexpr bool ROLLK = ROLLK_ != 0;
-    // NOPF: a step's input rows are staged at the start of the step (4 float4 per thread at a time) instead of being
-    // held in registers during the previous step -- for wide inputs with long steps, where those registers would
-    // cost occupancy and one exposed load per step is cheap
+    // NOPF: a step's input rows are staged at the start of the step (NOPF_ float4 per thread at a time, 4 for
+    // NOPF_ = 1) instead of being held in registers during the previous step -- for wide inputs with long steps,
+    // where those registers would cost occupancy and an exposed load per step is cheap
     static constexpr bool NOPF = NOPF_ != 0;
-    // WHOLE_H (stride 1, one step covers the map's WHOLE_H rows): only the map's own rows are staged -- the padding
-    // rows above and below are never read, the expand skips them -- so LDS holds WHOLE_H rows instead of IR
+    static constexpr int NOPF_CHUNK = NOPF_ > 1 ? NOPF_ : 4;
+    // WHOLE_H (one step covers the map's WHOLE_H rows): only the map's own rows are staged -- the padding rows above
+    // and below are never read, the expand skips them -- so LDS holds WHOLE_H rows instead of IR
     static constexpr int XR0 = WHOLE_H_ ? KS_ / 2 : 0;     // first staged input row of a step (relative)
     static constexpr int XRN = WHOLE_H_ ? WHOLE_H_ : S_ * (R_ - 1) + KS_;
-    static_assert(!WHOLE_H_ || (S_ == 1 && R_ >= WHOLE_H_), "whole-map staging: stride 1, one step per map");
+    static_assert(!WHOLE_H_ || S_ * R_ >= WHOLE_H_, "whole-map staging: one step per map");
     static constexpr bool HS = HS_ != 0, SE = SE_ != 0, PROJ = !SE;
     static constexpr int ACT = HS ? ACT_HS : ACT_RELU;
     static constexpr int PADK = KS / 2;
@@ -539,6 +540,10 @@ struct WgCfg {
     static constexpr int NT = S, IR = S * (R - 1) + KS;
     static constexpr int VALID = S == 1 ? 16 - 2 * PADK : (KS == 3 ? 15 : 14);
     static constexpr int LO = S == 1 ? PADK : 1;            // first output lane
+    // NPOS < 16 (one strip covers the map): only the NPOS pixel positions of a tile from lane POS0 on are staged --
+    // the map's columns; the other lanes are outside the map (their expand starts at -1e30) and read a clamped one
+    static constexpr int NPOS = NPOS_, POS0 = NPOS_ == 16 ? 0 : LO;
+    static_assert(NPOS >= 1 && NPOS <= 16 && POS0 + NPOS <= 16, "staged positions within the 16 lanes");
     static constexpr bool RES = PROJ && S == 1 && CIN == COUT;
     static constexpr int NWR = (KS * KS + 1 + 15) / 16;    // depthwise weight registers per value (taps + bias)
     static_assert(CIN % 4 == 0 && CEXP % 4 == 0 && COUT % 4 == 0, "channel counts must be multiples of 4");
@@ -547,7 +552,7 @@ struct WgCfg {
 
 template <typename T, class C> struct WgLds {
     static constexpr int P = Split<T>::P;
-    static constexpr int XS = C::XRN * C::NT * P * 16 * C::XLD;    // T elements
+    static constexpr int XS = C::XRN * C::NT * P * C::NPOS * C::XLD;    // T elements
     static constexpr int YB = C::PROJ ? 4 * C::R * C::OT * 64 : 0;  // float4s
     static constexpr int BYTES = XS * (int)sizeof(T) + YB * 16;
 };
@@ -618,6 +623,12 @@ __device__ __forceinline__ f32x4 mfma_wx(const typename Split<T>::V8* w, const t
     return acc;
 }
 
+// the staged pixel position a lane's B fragments come from (its own, or the nearest staged one: NPOS < 16)
+template <class C> __device__ __forceinline__ int staged_pos(int r) {
+    if constexpr (C::NPOS == 16) return r;
+    else return min(max(r - C::POS0, 0), C::NPOS - 1);
+}
+
 // one input row's taps (weights of kernel row DY) into an output accumulator, per value i of the lane
 template <class C, bool FIRST, int DY>
 __device__ __forceinline__ float row_taps(float acc, const float (&wd)[C::NWR], const float* v) {
@@ -666,7 +677,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
                     V8 xf[P];
 #pragma unroll
                     for (int q = 0; q < P; ++q)
-                        xf[q] = *reinterpret_cast<const V8*>(Xs + ((((J - C::XR0) * C::NT + t) * P + q) * 16 + r) * C::XLD + ks * 32 + g * 8);
+                        xf[q] = *reinterpret_cast<const V8*>(Xs + ((((J - C::XR0) * C::NT + t) * P + q) * C::NPOS + staged_pos<C>(r)) * C::XLD + ks * 32 + g * 8);
                     x = mfma_wx<T>(wf[ks], xf, x);
                 }
 #pragma unroll
@@ -747,7 +758,7 @@ __device__ __forceinline__ void wg_expand_rolled(f32x4 (&ea)[C::XRN][C::NT], con
                     V8 xf[P];
 #pragma unroll
                     for (int q = 0; q < P; ++q)
-                        xf[q] = *reinterpret_cast<const V8*>(Xs + (((j * C::NT + t) * P + q) * 16 + r) * C::XLD + ks * 32 + g * 8);
+                        xf[q] = *reinterpret_cast<const V8*>(Xs + (((j * C::NT + t) * P + q) * C::NPOS + staged_pos<C>(r)) * C::XLD + ks * 32 + g * 8);
                     ea[j][t] = mfma_wx<T>(w, xf, ea[j][t]);
                 }
             }
@@ -820,7 +831,8 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     __shared__ __attribute__((aligned(16))) unsigned char lds_raw[L::BYTES];
     T* Xs = reinterpret_cast<T*>(lds_raw);                                   // [IR][NT][P][16][XLD]
     float4* Yb = reinterpret_cast<float4*>(lds_raw + L::XS * sizeof(T));    // [4][R][OT][64]
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: tile and LDS-slot math stays scalar
     const T* wexp = static_cast<const T*>(a.wexp);
     const T* wproj = static_cast<const T*>(a.wproj);
     const int H = a.H, W = a.W, Ho = a.Ho, Wo = a.Wo;
@@ -828,9 +840,9 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     // staging of a step's input rows: float4 i -> (row j, tile t, pixel p, channel quad c4); loads at clamped,
     // always valid addresses, zero outside the map and past cin
     constexpr int XQ = C::CINP / 4;
-    constexpr int XN = C::XRN * C::NT * 16 * XQ;
+    constexpr int XN = C::XRN * C::NT * C::NPOS * XQ;
     constexpr int XPT_ALL = (XN + ST_THREADS - 1) / ST_THREADS;
-    constexpr int XPT = C::NOPF ? (XPT_ALL < 4 ? XPT_ALL : 4) : XPT_ALL;   // float4s per thread held at a time
+    constexpr int XPT = C::NOPF ? (XPT_ALL < C::NOPF_CHUNK ? XPT_ALL : C::NOPF_CHUNK) : XPT_ALL;   // held at a time
     float4 xpre[XPT];
     auto col_of = [&](int strip, int p, int t) {
         return C::S == 1 ? strip * C::VALID - C::PADK + p : 2 * (strip * C::VALID - 1 + p) + t;
@@ -844,9 +856,9 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
         for (int k = 0; k < XPT; ++k) {
             const int i = min(tid + (k0 + k) * ST_THREADS, XN - 1);
             const int c4 = i % XQ, rest = i / XQ;
-            const int p = rest % 16, jt = rest / 16;
+            const int p = rest % C::NPOS, jt = rest / C::NPOS;
             const int t = jt % C::NT, j = jt / C::NT;
-            const int iy = iy0 + j, ix = col_of(strip, p, t);
+            const int iy = iy0 + j, ix = col_of(strip, p + C::POS0, t);
             const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W && c4 * 4 < C::CIN;
             const int cy = min(max(iy, 0), H - 1), cx = min(max(ix, 0), W - 1), cc = min(c4, C::CIN / 4 - 1);
             const float4 v = *reinterpret_cast<const float4*>(Xf + ((long long)cy * W + cx) * C::CIN + cc * 4);
@@ -859,7 +871,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             const int i = tid + (k0 + k) * ST_THREADS;
             if (i >= XN) continue;
             const int c4 = i % XQ, rest = i / XQ;
-            const int p = rest % 16, jt = rest / 16;
+            const int p = rest % C::NPOS, jt = rest / C::NPOS;
             const float x[4] = {xpre[k].x, xpre[k].y, xpre[k].z, xpre[k].w};
             T part[4][P];
 #pragma unroll
@@ -867,7 +879,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 #pragma unroll
             for (int q = 0; q < P; ++q) {
                 T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
-                *reinterpret_cast<uint2*>(Xs + ((jt * P + q) * 16 + p) * C::XLD + c4 * 4) = *reinterpret_cast<const uint2*>(four);
+                *reinterpret_cast<uint2*>(Xs + ((jt * P + q) * C::NPOS + p) * C::XLD + c4 * 4) = *reinterpret_cast<const uint2*>(four);
             }
         }
     };
@@ -1035,6 +1047,7 @@ typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;         // 12x20
 typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 2> G9;         // 12x20 (b9, b10)
 typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
 typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6> G12;      // 12x20
+typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 6, 1, 1, 16, 12, 10> G13;   // 12x20 -> 6x10: whole map, 10 columns/tile
 typedef WgCfg<160, 960, 160, 5, 1, 1, 1, 6, 1, 1, 1, 6> G14;   // 6x10 (b14, b15)
 
 // the block shape the engine pads weights to and sizes the SE partial sums by: tile = (R rows, VALID columns)
@@ -1059,6 +1072,11 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
         throw std::runtime_error("ir_wgstrip: SE partial-sum grid mismatch");
     if (C::XRN != C::IR && (steps != 1 || a.H != C::XRN))
         throw std::runtime_error("ir_wgstrip: whole-map staging needs the map in one step");
+    if (C::NPOS < 16) {   // the staged positions must hold every map column of both pixel tiles
+        const auto col = [](int lane, int t) { return C::S == 1 ? lane - C::PADK : 2 * (lane - 1) + t; };
+        if (strips != 1 || col(C::POS0, 0) > 0 || col(C::POS0 + C::NPOS - 1, C::NT - 1) < a.W - 1)
+            throw std::runtime_error("ir_wgstrip: staged positions do not cover the map");
+    }
     const int items = F * strips;
     static const int resident = [] {
         int dev = 0, cus = 0, per_cu = 0;
@@ -1079,7 +1097,7 @@ bool strip_kernels_enabled() {
     return on;
 }
 
-bool ir_strip_shape(int block, IrShape* out) {
+bool ir_strip_shape(int block, bool bf16_tier, IrShape* out) {
     switch (block) {
     case 3: *out = wg_shape<G4>(); return true;
     case 4: case 5: *out = wg_shape<G5>(); return true;
@@ -1088,6 +1106,10 @@ bool ir_strip_shape(int block, IrShape* out) {
     case 8: case 9: *out = wg_shape<G9>(); return true;
     case 10: *out = wg_shape<G11>(); return true;
     case 11: *out = wg_shape<G12>(); return true;
+    case 12:   // whole-map staging of block 13 fits LDS with two operand parts (fp16) only
+        if (bf16_tier) return false;
+        *out = wg_shape<G13>();
+        return true;
     case 13: case 14: *out = wg_shape<G14>(); return true;
     default: return false;
     }
@@ -1105,6 +1127,12 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
     case 8: case 9: launch_wgstrip<T, G9>(block, a, F, s); return true;
     case 10: launch_wgstrip<T, G11>(block, a, F, s); return true;
     case 11: launch_wgstrip<T, G12>(block, a, F, s); return true;
+    case 12:
+        if constexpr (std::is_same<T, f16>::value) {
+            launch_wgstrip<T, G13>(block, a, F, s);
+            return true;
+        }
+        return false;
     case 13: case 14: launch_wgstrip<T, G14>(block, a, F, s); return true;
     default: return false;
     }
