@@ -111,14 +111,24 @@ template <> __device__ __forceinline__ void store8<float>(float* p, const float*
     *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-// Sum over 16 lanes of one 16-lane group with the fixed tree ((l_i + l_i+8) + (.. +4)) + (.. +2) + (.. +1)
-// of the reference vector code (isa_impl.hpp:45-53): every lane of the group ends with the same total.
-__device__ __forceinline__ float tree16(float v) {
-    v = v + __shfl_xor(v, 8, 16);
-    v = v + __shfl_xor(v, 4, 16);
-    v = v + __shfl_xor(v, 2, 16);
-    v = v + __shfl_xor(v, 1, 16);
+// Sums over a 16-lane row with the fixed tree ((l_i + l_i+8) + (.. +4)) + (.. +2) + (.. +1) of the reference vector
+// code (isa_impl.hpp:45-53).
+// Lane 0 of each 16-lane row: the row's sum as the xor butterfly (v + v^8, then ^4, ^2, ^1) brackets it, computed
+// with DPP row rotations (8, 4, 2, 1).  At lane 0 the rotations pair the same partial sums as the butterfly, only
+// with some operands of an addition swapped, which IEEE addition does not notice; other lanes hold other
+// bracketings.
+__device__ __forceinline__ float tree16_lane0(float v) {
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
     return v;
+}
+// The butterfly sum in every lane of the row (the butterfly gives all 16 lanes the same value): lane 0's, broadcast
+// to its row (DPP row_newbcast)
+__device__ __forceinline__ float tree16(float v) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, tree16_lane0(v)), 0x150, 0xf, 0xf, false));
 }
 
 }  // namespace shv

@@ -19,6 +19,7 @@
 
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 
 namespace shv {
 namespace {

@@ -68,6 +68,17 @@ rmsnorm_kernel(const float* __restrict__ x, long long ldx, const float* __restri
     for (int i = 0; i < 24; ++i) put_value(out, pstride, row * ldo + i * 16 + l, (v[i] * inv) * w[i * 16 + l]);
 }
 
+// Row 3 (lanes 48 + l): the values of lanes l, l + 16, l + 32 (rows 0, 1, 2), moved up by row swaps.  Only the
+// first result of the swap builtins is used (the first operand after the swap): with this compiler the second
+// result is not reliably the second operand's.
+__device__ __forceinline__ void row3_gather(float v, float (&out)[3]) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const unsigned up2 = __builtin_amdgcn_permlane32_swap(0u, u, false, false)[0];   // rows 2, 3 <- rows 0, 1
+    out[0] = __builtin_bit_cast(float, __builtin_amdgcn_permlane16_swap(0u, up2, false, false)[0]);  // row 3 <- row 0
+    out[1] = __builtin_bit_cast(float, up2);                                                           // row 3 <- row 1
+    out[2] = __builtin_bit_cast(float, __builtin_amdgcn_permlane16_swap(0u, u, false, false)[0]);    // row 3 <- row 2
+}
+
 // ------------------------------------------------------------------------------------------------ GDN prep
 // One block per (window, run of GP_T tokens), wave h = head h.  Lane l owns q channel h*64+l, k channel h*64+l and
 // v channels h*128+l, h*128+64+l, and keeps those columns of the last 4 rows of P in registers while it walks the
@@ -107,20 +118,34 @@ gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const
         na = P[(row0 + t0) * kGld + kGa + h];
         nb = P[(row0 + t0) * kGld + kGb + h];
     }
-    float nxt[4];
+    // rows t + 1 and t + 2 are in flight while row t is worked on (row index clamped into the run)
+    float nxt[4], nxt2[4], na2 = 0.0f, nb2 = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) nxt[c] = P[(row0 + t0) * kGld + pc[c]];
+    for (int c = 0; c < 4; ++c) {
+        nxt[c] = P[(row0 + t0) * kGld + pc[c]];
+        nxt2[c] = P[(row0 + min(t0 + 1, t1 - 1)) * kGld + pc[c]];
+    }
+    if (l == 0) {
+        na2 = P[(row0 + min(t0 + 1, t1 - 1)) * kGld + kGa + h];
+        nb2 = P[(row0 + min(t0 + 1, t1 - 1)) * kGld + kGb + h];
+    }
     for (int t = t0; t < t1; ++t) {
         const long long row = row0 + t;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) hist[c][3] = nxt[c];
+        for (int c = 0; c < 4; ++c) {
+            hist[c][3] = nxt[c];
+            nxt[c] = nxt2[c];
+        }
         const float ga = na, gb = nb;
-        if (t + 1 < t1) {   // the next row's loads are in flight during this row's work
+        na = na2;
+        nb = nb2;
+        {
+            const long long r2 = row0 + min(t + 2, t1 - 1);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) nxt[c] = P[(row + 1) * kGld + pc[c]];
+            for (int c = 0; c < 4; ++c) nxt2[c] = P[r2 * kGld + pc[c]];
             if (l == 0) {
-                na = P[(row + 1) * kGld + kGa + h];
-                nb = P[(row + 1) * kGld + kGb + h];
+                na2 = P[r2 * kGld + kGa + h];
+                nb2 = P[r2 * kGld + kGb + h];
             }
         }
         float y[4];
@@ -136,18 +161,25 @@ gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const
         const float q = y[0], k = y[1];
         V[row * kVD + h * 128 + l] = y[2];
         V[row * kVD + h * 128 + 64 + l] = y[3];
-        // lanes 0..15 gather elements l, l+16, l+32, l+48
-        float aq = q * q, ak = k * k;
+        // lanes 48 + l (row 3) gather elements l, l+16, l+32, l+48 (row swaps), then the 16-lane tree; lane 48's
+        // total is the head's
+        float aq, ak;
+        {
+            float g[2][3];
+            row3_gather(q, g[0]);
+            row3_gather(k, g[1]);
+            aq = g[0][0] * g[0][0];
+            ak = g[1][0] * g[1][0];
 #pragma unroll
-        for (int s = 1; s < 4; ++s) {
-            const float qs = __shfl(q, l + 16 * s), ks = __shfl(k, l + 16 * s);
-            aq = __builtin_fmaf(qs, qs, aq);
-            ak = __builtin_fmaf(ks, ks, ak);
+            for (int s = 1; s < 3; ++s) {
+                aq = __builtin_fmaf(g[0][s], g[0][s], aq);
+                ak = __builtin_fmaf(g[1][s], g[1][s], ak);
+            }
+            aq = __builtin_fmaf(q, q, aq);
+            ak = __builtin_fmaf(k, k, ak);
         }
-        aq = tree16(aq);
-        ak = tree16(ak);
-        aq = __shfl(aq, 0);
-        ak = __shfl(ak, 0);
+        aq = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tree16_lane0(aq)), 48));
+        ak = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tree16_lane0(ak)), 48));
         const float iq = 1.0f / sqrtf(aq + 1e-6f), ik = 1.0f / sqrtf(ak + 1e-6f);
         Q[row * kD + h * 64 + l] = (q * iq) * 0.125f;
         K[row * kD + h * 64 + l] = k * ik;
