@@ -85,7 +85,7 @@ __device__ __forceinline__ void row3_gather(float v, float (&out)[3]) {
 // run, so each element of P is read once (plus a 3-row halo per run).  Per row: short conv acc from +0, taps t-3..t
 // in order, + bias, SiLU (isa_impl.hpp:871-889); L2 norms with the 16-lane structure over 64 elements
 // (isa_impl.hpp:893-906); gates with device libm (expf, log1pf).
-constexpr int GP_T = 32;
+constexpr int GP_T = 4;
 __global__ void __launch_bounds__(384)
 gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const float* __restrict__ cb,
                 const float* __restrict__ neg_rate, const float* __restrict__ dt_bias, float* __restrict__ Q,
