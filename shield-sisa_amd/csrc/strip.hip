@@ -822,7 +822,11 @@ __device__ __forceinline__ void wg_rows_acc(f32x4 (&acc)[C::R], const float (&wd
 }
 
 template <typename T, class C>
-__global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items) {
+// csplit (squeeze-excite blocks; 1 otherwise): the channel tiles of a (frame, strip) are dealt over csplit
+// workgroups (item = (frame, strip) * csplit + group), so that few frames still fill the device.  Every output is
+// computed the same way whichever workgroup takes its tile.
+__global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items,
+                                                                           int csplit) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     typedef typename Split16<T>::V4 V4;
@@ -885,11 +889,12 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     };
 
     if constexpr (!C::NOPF) {
-        if ((int)blockIdx.x < items) load_step(blockIdx.x, 0, 0);
+        if ((int)blockIdx.x < items) load_step(blockIdx.x / csplit, 0, 0);
     }
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
-        const int strip = item % strips;
-        const long long f = item / strips;
+        const int fs = item / csplit, cgroup = item - fs * csplit;   // (frame, strip) index, channel-tile group
+        const int strip = fs % strips;
+        const long long f = fs / strips;
         // this lane's output column and the map columns of its pixel tiles
         const int ox = C::S == 1 ? strip * C::VALID - C::PADK + r : strip * C::VALID - 1 + r;
         const bool out_lane = r >= C::LO && r < C::LO + C::VALID && ox < Wo;
@@ -903,7 +908,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             const int oy0 = step * C::R;
             if constexpr (C::NOPF) {
                 for (int k0 = 0; k0 < XPT_ALL; k0 += XPT) {
-                    load_step(item, step, k0);
+                    load_step(fs, step, k0);
                     store_step(k0);
                 }
                 lds_barrier();
@@ -911,8 +916,8 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                 store_step(0);
                 lds_barrier();
                 // the next step's (or next item's first) rows are in flight while this step computes
-                if (step + 1 < steps) load_step(item, step + 1, 0);
-                else if (item + (int)gridDim.x < items) load_step(item + gridDim.x, 0, 0);
+                if (step + 1 < steps) load_step(fs, step + 1, 0);
+                else if (item + (int)gridDim.x < items) load_step((item + gridDim.x) / csplit, 0, 0);
             }
 
             f32x4 y[C::PROJ ? C::R : 1][C::PROJ ? C::OT : 1];
@@ -925,7 +930,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                     for (int q = 0; q < C::R; ++q) y[q][ot] = f32x4{b.x, b.y, b.z, b.w};
                 }
             }
-            for (int ct = wave; ct < C::CT; ct += 4) {
+            for (int ct = wave + 4 * cgroup; ct < C::CT; ct += 4 * csplit) {
                 const int c = ct * 16 + 4 * g;
                 // ---- this tile's weights
                 V8 wf[C::ROLLK ? 1 : C::KS32][P];
@@ -1077,7 +1082,6 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
         if (strips != 1 || col(C::POS0, 0) > 0 || col(C::POS0 + C::NPOS - 1, C::NT - 1) < a.W - 1)
             throw std::runtime_error("ir_wgstrip: staged positions do not cover the map");
     }
-    const int items = F * strips;
     static const int resident = [] {
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -1086,8 +1090,15 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
             throw std::runtime_error("ir_wgstrip: cannot query the device occupancy");
         return std::max(1, cus) * std::max(1, per_cu);
     }();
+    // squeeze-excite blocks with fewer (frame, strip) items than resident workgroups deal each item's channel
+    // tiles over several workgroups (at least one tile per wave each)
+    int csplit = 1;
+    if (C::SE && (long long)F * strips < resident)
+        csplit = std::max(1, std::min(int(resident / ((long long)F * strips)), C::CT / 4));
+    const int items = F * strips * csplit;
     const int grid = std::min(items, resident);
-    hipLaunchKernelGGL((ir_wgstrip_kernel<T, C>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, steps, items);
+    hipLaunchKernelGGL((ir_wgstrip_kernel<T, C>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, steps, items,
+                       csplit);
 }
 
 }  // namespace
