@@ -514,7 +514,7 @@ template <typename T, class C, bool STEM = false> void launch_strip(int block, c
 // last tap.  Columns outside the map expand from -1e30 (ReLU and hardswish both give 0 there), rows outside the
 // map are skipped (E = 0).
 template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_, int MINB_ = 1, int ROLLK_ = 0,
-          int NOPF_ = 0, int WHOLE_H_ = 0, int NPOS_ = 16>
+          int NOPF_ = 0, int WHOLE_H_ = 0, int NPOS_ = 16, int YBA_ = 0>
 struct WgCfg {
     static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, KS = KS_, S = S_, R = R_;
     static constexpr int MINB = MINB_;   // workgroups per CU the register allocation must allow
@@ -543,6 +543,9 @@ struct WgCfg {
     // NPOS < 16 (one strip covers the map): only the NPOS pixel positions of a tile from lane POS0 on are staged --
     // the map's columns; the other lanes are outside the map (their expand starts at -1e30) and read a clamped one
     static constexpr int NPOS = NPOS_, POS0 = NPOS_ == 16 ? 0 : LO;
+    // YBA (projection blocks): the wave partials of the projection share LDS with the staged rows (two more
+    // barriers per step: before the partials are written, and before the next step's rows are staged)
+    static constexpr bool YBA = YBA_ != 0;
     static_assert(NPOS >= 1 && NPOS <= 16 && POS0 + NPOS <= 16, "staged positions within the 16 lanes");
     static constexpr bool RES = PROJ && S == 1 && CIN == COUT;
     static constexpr int NWR = (KS * KS + 1 + 15) / 16;    // depthwise weight registers per value (taps + bias)
@@ -554,7 +557,8 @@ template <typename T, class C> struct WgLds {
     static constexpr int P = Split<T>::P;
     static constexpr int XS = C::XRN * C::NT * P * C::NPOS * C::XLD;    // T elements
     static constexpr int YB = C::PROJ ? 4 * C::R * C::OT * 64 : 0;  // float4s
-    static constexpr int BYTES = XS * (int)sizeof(T) + YB * 16;
+    static constexpr int BYTES = C::YBA ? (XS * (int)sizeof(T) > YB * 16 ? XS * (int)sizeof(T) : YB * 16)
+                                        : XS * (int)sizeof(T) + YB * 16;
 };
 
 // acc (op)= the KS taps of one input row: first row of an output starts the chain with a product
@@ -834,7 +838,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     constexpr int P = S::P;
     __shared__ __attribute__((aligned(16))) unsigned char lds_raw[L::BYTES];
     T* Xs = reinterpret_cast<T*>(lds_raw);                                   // [IR][NT][P][16][XLD]
-    float4* Yb = reinterpret_cast<float4*>(lds_raw + L::XS * sizeof(T));    // [4][R][OT][64]
+    float4* Yb = reinterpret_cast<float4*>(lds_raw + (C::YBA ? 0 : L::XS * sizeof(T)));    // [4][R][OT][64]
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: tile and LDS-slot math stays scalar
     const T* wexp = static_cast<const T*>(a.wexp);
@@ -1010,6 +1014,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                 }
             }
             if constexpr (C::PROJ) {
+                if constexpr (C::YBA) lds_barrier();   // every wave is done with the staged rows
 #pragma unroll
                 for (int q = 0; q < C::R; ++q)
 #pragma unroll
@@ -1039,6 +1044,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                     if (out_lane && oy < Ho && n < C::COUT)
                         *reinterpret_cast<float4*>(a.Y + ((f * Ho + oy) * Wo + ox) * C::COUT + n) = v;
                 }
+                if constexpr (C::YBA) lds_barrier();   // the partials are read before the next rows are staged
             }
         }
     }
@@ -1047,7 +1053,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 //                cin  cexp cout k  s  hs se R  minb
 typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 4> G4;         // 45x80 -> 23x40
 typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 6> G5;         // 23x40 (b5, b6)
-typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 1, 3> G7;      // 23x40 -> 12x20
+typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 2, 3, 0, 0, 0, 16, 1> G7;    // 23x40 -> 12x20
 typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 2> G8;         // 12x20
 typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 2> G9;         // 12x20 (b9, b10)
 typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
