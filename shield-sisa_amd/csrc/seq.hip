@@ -287,12 +287,15 @@ delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const flo
 }
 
 // Half tiers: the same recurrence with each value column's 64 keys split over KQ lane groups of a wave (group kq
-// holds keys (64/KQ) kq .. of S[:, c]; 64/KQ columns per workgroup).  Per token a lane updates its state entries
-// and forms partial dots of the output and of the next prediction over its keys; the KQ partials are added in a
-// fixed order by cross-row lane swaps ((p0 + p1) + (p2 + p3) for KQ = 4, p0 + p1 for KQ = 2), so every lane holds
-// the same o and pred.  The dependent chain per token is 64/KQ instead of 64 fmas, which is what a small batch
-// waits on; at KQ = 2 the instruction count stays within a few percent of the exact kernel's.  The sums are
-// rounded in another (fixed) order than the reference's 64-key chain.
+// holds keys (64/KQ) kq .. of S[:, c]; 64/KQ columns per wave).  Per token a lane updates its state entries and
+// forms the partial dots of the output and of the next prediction.  Every split sums in ONE canonical order: eight
+// fma chains from +0 over keys 8m .. 8m+7 (m = 0..7), combined as ((p0 + p1) + (p2 + p3)) + ((p4 + p5) + (p6 + p7)).
+// A lane adds the chains it holds in that bracketing and the lane groups add the rest by cross-lane exchanges
+// (KQ = 8: DPP row rotation by 8, then row swaps; KQ = 4: row swaps; KQ = 2: half swap), and IEEE addition is
+// commutative, so o and pred are bitwise the same for KQ = 2, 4 and 8 and in every lane of a column.  That lets the
+// launch pick the split from the batch size without breaking row independence: small batches take KQ = 8 (the
+// dependent chain per token is 8 fmas + 3 exchanges), large ones KQ = 2 (fewest instructions per token overall).
+// The sums are rounded in another (fixed) order than the reference's 64-key chain.
 __device__ __forceinline__ float row_pair_sum(float v, int g) {   // rows (0,1) and (2,3): v + partner row
     const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
                                                     false, false);
@@ -303,6 +306,10 @@ __device__ __forceinline__ float half_sum(float v, int g) {       // rows (0,1) 
                                                     false, false);
     const float other = __builtin_bit_cast(float, g < 2 ? s[1] : s[0]);
     return g < 2 ? v + other : other + v;
+}
+__device__ __forceinline__ float ror8_sum(float v) {               // lanes l, l ^ 8 of a 16-lane row
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf,
+                                                                     false));
 }
 // One token's operands for a lane's KEYS keys: k, q and the next token's k (for the prediction), decay, beta, v.
 template <int KEYS>
@@ -328,40 +335,55 @@ struct DTok {
         v = v_;
     }
 };
-// One token of the split recurrence: updates S and pred, returns o.  Per key j (in order): S_j = fma(k_j, u, S_j a);
-// o and the next prediction are fma chains from +0 over the lane's keys, then summed across the key groups.
+// Sum of a lane's 8-key chains in the canonical bracketing, then across the KQ lane groups.
+template <int KQ>
+__device__ __forceinline__ float delta_combine(const float* c, int g) {
+    constexpr int NC = 8 / KQ;
+    float v = c[0];
+    if constexpr (NC == 2) v = c[0] + c[1];
+    if constexpr (NC == 4) v = (c[0] + c[1]) + (c[2] + c[3]);
+    if constexpr (KQ == 8) v = ror8_sum(v);
+    if constexpr (KQ >= 4) v = row_pair_sum(v, g);
+    return half_sum(v, g);
+}
+// One token of the split recurrence: updates S and pred, returns o.  Per key j (in order): S_j = fma(k_j, u, S_j a).
 template <int KQ, int KEYS>
 __device__ __forceinline__ float delta_token(const DTok<KEYS>& t, float* S, float& pred, int g) {
+    constexpr int NC = KEYS / 8;
     const float u = (t.v - t.a * pred) * t.b;
-    float o = 0.0f, pn = 0.0f;
+    float o[NC], pn[NC];
+#pragma unroll
+    for (int m = 0; m < NC; ++m) {
+        o[m] = 0.0f;
+        pn[m] = 0.0f;
+    }
 #pragma unroll
     for (int j4 = 0; j4 < KEYS / 4; ++j4) {
         const float kv[4] = {t.k[j4].x, t.k[j4].y, t.k[j4].z, t.k[j4].w};
         const float qv[4] = {t.q[j4].x, t.q[j4].y, t.q[j4].z, t.q[j4].w};
         const float nv[4] = {t.n[j4].x, t.n[j4].y, t.n[j4].z, t.n[j4].w};
+        const int m = j4 / 2;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const float x = __builtin_fmaf(kv[e], u, S[4 * j4 + e] * t.a);
             S[4 * j4 + e] = x;
-            o = __builtin_fmaf(x, qv[e], o);
-            pn = __builtin_fmaf(x, nv[e], pn);
+            o[m] = __builtin_fmaf(x, qv[e], o[m]);
+            pn[m] = __builtin_fmaf(x, nv[e], pn[m]);
         }
     }
-    if constexpr (KQ == 4) {
-        o = half_sum(row_pair_sum(o, g), g);
-        pred = half_sum(row_pair_sum(pn, g), g);
-    } else {
-        o = half_sum(o, g);
-        pred = half_sum(pn, g);
-    }
-    return o;
+    pred = delta_combine<KQ>(pn, g);
+    return delta_combine<KQ>(o, g);
 }
-constexpr int DELTA_KQ = 2;   // key groups per value column in the half tiers
 constexpr int kDeltaPipeWaves = 1024;   // one wave per SIMD (256 CUs x 4)
 // PIPE: full 32-token chunks run unrolled with token i+1's operands read from LDS ahead of token i's chain (for
-// grids of at most one wave per SIMD, where nothing else hides the LDS latency; the unrolled chunk holds ~256
-// VGPRs).  Both forms issue the same arithmetic per token, so their results are bitwise equal.
-template <int KQ, bool PIPE>   // KQ: key groups per column: 2 (halves: lanes 0-31 / 32-63) or 4 (rows)
+// grids of at most one wave per SIMD, where nothing else hides the LDS latency), and the outputs of a chunk are
+// kept in registers (lane group kq keeps tokens i = kq mod KQ) and stored after the next chunk's operands have been
+// staged: one vmcnt counter retires loads and stores in order, so a store issued just before the wait for the
+// prefetched operands would put a full memory round trip on the serial path.  The next chunk's operands are loaded
+// into registers while the current chunk runs (the rolled form, for grids of several waves per SIMD, loads them at
+// the start of the chunk and keeps its registers for occupancy).  Both forms issue the same arithmetic per token, so their results
+// are bitwise equal.
+template <int KQ, bool PIPE>   // KQ: key groups per column: 2 (halves), 4 (rows) or 8 (half rows)
 __global__ void __launch_bounds__(64)
 delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
                    const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ O) {
@@ -376,17 +398,15 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
     __shared__ float sv[DCH][DS_COLS];
     __shared__ float sa[DCH], sb[DCH];
     const long long row0 = (long long)b * kT;
-    float S[KEYS];
-#pragma unroll
-    for (int j = 0; j < KEYS; ++j) S[j] = 0.0f;
-    float pred = 0.0f;
-    for (int t0 = 0; t0 < kT; t0 += DCH) {
-        const int nt = min(DCH, kT - t0);
-        // staging (unconditional, token index clamped; slots past the last token zeroed / repeating the last k)
-        constexpr int QK4 = (DCH + 1) * 16;
-        constexpr int QKR = (QK4 + 63) / 64;
-        float4 rq[QKR], rk[QKR];
-        float rv[DCH * DS_COLS / 64];
+    // chunk operands in registers: loads are unconditional (token index clamped) so all of them are in flight
+    // together; slots past the last token are then zeroed (q, v, decay, beta) or repeat the last k (the next-k slot
+    // of the last token, unused downstream)
+    constexpr int QK4 = (DCH + 1) * 16;   // float4s of q (DCH rows) and k (DCH + 1 rows)
+    constexpr int QKR = (QK4 + 63) / 64;
+    constexpr int VR = DCH * DS_COLS / 64;
+    float4 rq[QKR], rk[QKR];
+    float rv[VR], ra = 0.0f, rb = 0.0f;
+    auto fetch = [&](int t0) {
 #pragma unroll
         for (int k = 0; k < QKR; ++k) {
             const int i = lane + k * 64;
@@ -400,10 +420,14 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
             }
         }
 #pragma unroll
-        for (int k = 0; k < DCH * DS_COLS / 64; ++k) {
-            const int tt = kq + KQ * k;
-            rv[k] = V[(row0 + min(t0 + tt, kT - 1)) * kVD + col];
+        for (int k = 0; k < VR; ++k) rv[k] = V[(row0 + min(t0 + kq + KQ * k, kT - 1)) * kVD + col];
+        if (lane < DCH) {
+            const int t = min(t0 + lane, kT - 1);
+            ra = dec[(row0 + t) * 8 + h];
+            rb = beta[(row0 + t) * 8 + h];
         }
+    };
+    auto stage = [&](int t0) {
 #pragma unroll
         for (int k = 0; k < QKR; ++k) {
             const int i = lane + k * 64;
@@ -415,22 +439,37 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
             }
         }
 #pragma unroll
-        for (int k = 0; k < DCH * DS_COLS / 64; ++k) {
+        for (int k = 0; k < VR; ++k) {
             const int tt = kq + KQ * k;
             sv[tt][c16] = t0 + tt < kT ? rv[k] : 0.0f;
         }
         if (lane < DCH) {
-            const int t = t0 + lane;
-            sa[lane] = t < kT ? dec[(row0 + t) * 8 + h] : 0.0f;
-            sb[lane] = t < kT ? beta[(row0 + t) * 8 + h] : 0.0f;
+            const bool in = t0 + lane < kT;
+            sa[lane] = in ? ra : 0.0f;
+            sb[lane] = in ? rb : 0.0f;
         }
+    };
+    float S[KEYS];
+#pragma unroll
+    for (int j = 0; j < KEYS; ++j) S[j] = 0.0f;
+    float pred = 0.0f;
+    float ob[DCH / KQ] = {};   // PIPE: this lane's outputs of the last full chunk, tokens kq + KQ m
+    int ob_t0 = -1;            // first token of that chunk (-1: none pending)
+    if (PIPE) fetch(0);
+    for (int t0 = 0; t0 < kT; t0 += DCH) {
+        const int nt = min(DCH, kT - t0);
+        if (!PIPE) fetch(t0);   // PIPE: fetched while the previous chunk ran
+        stage(t0);
         __syncthreads();
-        // both lane halves hold the same o after the cross-half sum and store it (same value, same address), so
-        // the token step has no branch
+        if (PIPE && ob_t0 >= 0) {
+#pragma unroll
+            for (int m = 0; m < DCH / KQ; ++m) O[(row0 + ob_t0 + kq + KQ * m) * kVD + col] = ob[m];
+            ob_t0 = -1;
+        }
+        if (PIPE && t0 + DCH < kT) fetch(t0 + DCH);
+        // all lane groups of a column hold the same o; in the rolled form every lane stores it (same value, same
+        // address), so the token step has no branch
         if (PIPE && nt == DCH) {
-            // full chunk, unrolled: token i+1's q, next k, decay, beta and v are read from LDS before token i's
-            // chain, so with one wave per SIMD (small batches) no LDS round trip sits on the serial path; token
-            // i+1's k is token i's next k, already in registers
             DTok<KEYS> cur;
             cur.load_k(&sk[0][kq * KEYS]);
             cur.load_rest(&sq[0][kq * KEYS], &sk[1][kq * KEYS], sa[0], sb[0], sv[0][c16]);
@@ -442,9 +481,11 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
                     nxt.load_rest(&sq[i + 1][kq * KEYS], &sk[i + 2][kq * KEYS], sa[i + 1], sb[i + 1],
                                   sv[i + 1][c16]);
                 }
-                O[(row0 + t0 + i) * kVD + col] = delta_token<KQ, KEYS>(cur, S, pred, g);
+                const float o = delta_token<KQ, KEYS>(cur, S, pred, g);
+                if (kq == i % KQ) ob[i / KQ] = o;
                 if (i + 1 < DCH) cur = nxt;
             }
+            ob_t0 = t0;
         } else {
             for (int i = 0; i < nt; ++i) {
                 DTok<KEYS> cur;
@@ -454,6 +495,10 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
             }
         }
         __syncthreads();
+    }
+    if (PIPE && ob_t0 >= 0) {
+#pragma unroll
+        for (int m = 0; m < DCH / KQ; ++m) O[(row0 + ob_t0 + kq + KQ * m) * kVD + col] = ob[m];
     }
 }
 
@@ -663,13 +708,17 @@ void launch_delta(const float* Q, const float* K, const float* V, const float* d
                   int B, bool exact, hipStream_t s) {
     if (exact)
         hipLaunchKernelGGL(delta_kernel, dim3(B * kHeads * 2), dim3(DCOLS), 0, s, Q, K, V, dec, beta, O);
-    else
-    {
-        const int waves = B * kHeads * (128 / (64 / DELTA_KQ));
-        if (waves <= kDeltaPipeWaves)
-            hipLaunchKernelGGL((delta_split_kernel<DELTA_KQ, true>), dim3(waves), dim3(64), 0, s, Q, K, V, dec, beta, O);
+    else {
+        // the split follows the batch (results are bitwise the same for every split): the most lane groups per
+        // column that still fit one wave per SIMD; KQ = 2 past that
+        if (B * kHeads * 16 <= kDeltaPipeWaves)
+            hipLaunchKernelGGL((delta_split_kernel<8, true>), dim3(B * kHeads * 16), dim3(64), 0, s, Q, K, V, dec, beta, O);
+        else if (B * kHeads * 8 <= kDeltaPipeWaves)
+            hipLaunchKernelGGL((delta_split_kernel<4, true>), dim3(B * kHeads * 8), dim3(64), 0, s, Q, K, V, dec, beta, O);
+        else if (B * kHeads * 4 <= kDeltaPipeWaves)
+            hipLaunchKernelGGL((delta_split_kernel<2, true>), dim3(B * kHeads * 4), dim3(64), 0, s, Q, K, V, dec, beta, O);
         else
-            hipLaunchKernelGGL((delta_split_kernel<DELTA_KQ, false>), dim3(waves), dim3(64), 0, s, Q, K, V, dec, beta, O);
+            hipLaunchKernelGGL((delta_split_kernel<2, false>), dim3(B * kHeads * 4), dim3(64), 0, s, Q, K, V, dec, beta, O);
     }
 }
 template <typename T>

@@ -301,3 +301,18 @@ def test_row_independence_half(shv, weights, clips, mode):
         single = np.concatenate([m.predict(clips[i:i + 1]) for i in range(8)])
     assert np.all(np.isfinite(batch))
     assert np.array_equal(batch.view(np.uint32), single.view(np.uint32)), float(np.abs(batch - single).max())
+
+
+@pytest.mark.parametrize("mode", ["fp16"])
+def test_delta_splits_bitwise(shv, weights, clips, mode):
+    """The half-tier delta rule picks its key split from the batch (8 lane groups per value column up to 10 windows,
+    4 up to 21, 2 beyond, unrolled up to 42 windows and rolled past that); every split sums in one canonical order,
+    so batches of 16, 24 and 48 windows give each clip bitwise the logit it gets alone (1 window: 8 groups)."""
+    print(f"[gpu] {mode} delta splits: batches of 16 / 24 / 48 vs one by one", flush=True)
+    with shv.Model(weights, mode, experimental=True, max_frames=960, max_windows=48) as m:
+        single = np.concatenate([m.predict(clips[i:i + 1]) for i in range(48)])
+        for n in (16, 24, 48):
+            batch = m.predict(clips[:n])
+            assert np.all(np.isfinite(batch))
+            assert np.array_equal(batch.view(np.uint32), single[:n].view(np.uint32)), \
+                (n, float(np.abs(batch - single[:n]).max()))
