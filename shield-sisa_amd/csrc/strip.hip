@@ -172,7 +172,9 @@ __device__ __forceinline__ void stem_fetch(const uint8_t* img, long long f, int 
 }
 
 template <typename T, class C, bool STEM = false>
-__global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int strips, int items,
+// segs: each strip's output rows are dealt over segs items of seg_rows rows (a multiple of R) when frames are few;
+// every step reads its own input rows, so the split changes no result.
+__global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int strips, int items, int segs, int seg_rows,
                                                               const float* __restrict__ stem_w,
                                                               const float* __restrict__ stem_b) {
     typedef Split16<T> S16;
@@ -262,8 +264,10 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
 
     const int H = a.H, W = a.W, Ho = a.Ho, Wo = a.Wo;
     for (int item = blockIdx.x * (ST_THREADS / 64) + wave; item < items; item += gridDim.x * (ST_THREADS / 64)) {
-        const int strip = item % strips;
-        const long long f = item / strips;
+        const int seg = item % segs, fs = item / segs;
+        const int strip = fs % strips;
+        const long long f = fs / strips;
+        const int oyA = seg * seg_rows, oyB = min(Ho, oyA + seg_rows);   // this item's output rows
         const int ox = strip * C::VALID + r - 1;                   // this lane's output column
         int ixc[C::NT];
         bool pin[C::NT];
@@ -282,7 +286,7 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
         for (int t = 0; t < C::NT; ++t) be_off[t] = pin[t] ? 0 : C::CT * 16;
 
         int sbytes[STEM ? STEM_NB : 1];   // STEM: the step's staged frame bytes
-        for (int oy0 = 0; oy0 < Ho; oy0 += C::R) {
+        for (int oy0 = oyA; oy0 < oyB; oy0 += C::R) {
             const int iy0 = C::S * oy0 - 1;
             // ---- the step's input rows: fp32 (no expand) or split into B fragments
             V4 xf[C::EXPAND ? C::IR : 1][C::NT][C::KSI][P];
@@ -291,7 +295,7 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
             float4 sx[STEM ? C::IR : 1];   // STEM: the step's stem rows (pixel r, channels 4 g ..)
             if constexpr (STEM) {
                 const int fy0 = 2 * iy0 - 1, fb0 = (2 * (strip * C::VALID - 1) - 1) * 3;   // first row, first byte
-                if (oy0 == 0) stem_fetch(a.img, f, fy0, fb0, lane, sbytes);
+                if (oy0 == oyA) stem_fetch(a.img, f, fy0, fb0, lane, sbytes);
                 wave_lds_sync();   // the previous step's reads of the tile are done
                 {
                     const int e1 = lane + 64;
@@ -313,7 +317,7 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
                     }
                 }
                 // the next step's bytes load while this step computes
-                if (oy0 + C::R < Ho) stem_fetch(a.img, f, fy0 + 2 * C::R, fb0, lane, sbytes);
+                if (oy0 + C::R < oyB) stem_fetch(a.img, f, fy0 + 2 * C::R, fb0, lane, sbytes);
                 wave_lds_sync();
 #pragma unroll
                 for (int j = 0; j < C::IR; ++j) {
@@ -480,7 +484,6 @@ template <typename T, class C, bool STEM = false> void launch_strip(int block, c
     if ((C::S == 1 && (a.Ho != a.H || a.Wo != a.W)) || (C::S == 2 && (a.Ho != (a.H + 1) / 2 || a.Wo != (a.W + 1) / 2)))
         throw std::runtime_error("ir_strip: map shape does not match the stride");
     if (a.frames != F || (long long)F * strips > (1ll << 30)) throw std::runtime_error("ir_strip: bad frame count");
-    const int items = F * strips;
     // persistent workgroups: as many as the device holds at once (per-instantiation occupancy, cached)
     static const int resident = [] {
         int dev = 0, cus = 0, per_cu = 0;
@@ -492,9 +495,19 @@ template <typename T, class C, bool STEM = false> void launch_strip(int block, c
         return std::max(1, cus) * std::max(1, per_cu);
     }();
     const int waves_per_wg = ST_THREADS / 64;
+    // fewer (frame, strip) items than resident waves: deal each strip's steps over row segments
+    const int steps = (a.Ho + C::R - 1) / C::R;
+    int seg_steps = steps;
+    if ((long long)F * strips < (long long)resident * waves_per_wg) {
+        const int want = std::min<long long>(steps, (long long)resident * waves_per_wg / ((long long)F * strips));
+        seg_steps = (steps + want - 1) / want;
+    }
+    const int segs = (steps + seg_steps - 1) / seg_steps;
+    if ((long long)F * strips * segs > (1ll << 30)) throw std::runtime_error("ir_strip: too many items");
+    const int items = F * strips * segs;
     const int grid = std::min((items + waves_per_wg - 1) / waves_per_wg, resident);
-    hipLaunchKernelGGL((ir_strip_kernel<T, C, STEM>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, items, a.stem_w,
-                       a.stem_b);
+    hipLaunchKernelGGL((ir_strip_kernel<T, C, STEM>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, items, segs,
+                       seg_steps * C::R, a.stem_w, a.stem_b);
 }
 
 
@@ -827,10 +840,11 @@ __device__ __forceinline__ void wg_rows_acc(f32x4 (&acc)[C::R], const float (&wd
 
 template <typename T, class C>
 // csplit (squeeze-excite blocks; 1 otherwise): the channel tiles of a (frame, strip) are dealt over csplit
-// workgroups (item = (frame, strip) * csplit + group), so that few frames still fill the device.  Every output is
-// computed the same way whichever workgroup takes its tile.
+// workgroups, and segs: its steps over segs items of seg_steps steps, so that few frames still fill the device
+// (item = ((frame, strip) * segs + segment) * csplit + group).  Every output is computed the same way whichever
+// workgroup takes its tile and step.
 __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items,
-                                                                           int csplit) {
+                                                                           int csplit, int segs, int seg_steps) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     typedef typename Split16<T>::V4 V4;
@@ -892,11 +906,15 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
         }
     };
 
+    // item -> (frame, strip) index, first step of its segment
+    auto item_fs = [&](int it) { return it / csplit / segs; };
+    auto item_s0 = [&](int it) { return (it / csplit % segs) * seg_steps; };
     if constexpr (!C::NOPF) {
-        if ((int)blockIdx.x < items) load_step(blockIdx.x / csplit, 0, 0);
+        if ((int)blockIdx.x < items) load_step(item_fs(blockIdx.x), item_s0(blockIdx.x), 0);
     }
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
-        const int fs = item / csplit, cgroup = item - fs * csplit;   // (frame, strip) index, channel-tile group
+        const int fs = item_fs(item), cgroup = item % csplit;   // (frame, strip) index, channel-tile group
+        const int s0 = item_s0(item), s1 = min(steps, s0 + seg_steps);
         const int strip = fs % strips;
         const long long f = fs / strips;
         // this lane's output column and the map columns of its pixel tiles
@@ -908,7 +926,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             const int ix = col_of(strip, r, t);
             pin[t] = ix >= 0 && ix < W;
         }
-        for (int step = 0; step < steps; ++step) {
+        for (int step = s0; step < s1; ++step) {
             const int oy0 = step * C::R;
             if constexpr (C::NOPF) {
                 for (int k0 = 0; k0 < XPT_ALL; k0 += XPT) {
@@ -920,8 +938,9 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                 store_step(0);
                 lds_barrier();
                 // the next step's (or next item's first) rows are in flight while this step computes
-                if (step + 1 < steps) load_step(fs, step + 1, 0);
-                else if (item + (int)gridDim.x < items) load_step((item + gridDim.x) / csplit, 0, 0);
+                if (step + 1 < s1) load_step(fs, step + 1, 0);
+                else if (item + (int)gridDim.x < items)
+                    load_step(item_fs(item + gridDim.x), item_s0(item + gridDim.x), 0);
             }
 
             f32x4 y[C::PROJ ? C::R : 1][C::PROJ ? C::OT : 1];
@@ -1101,10 +1120,18 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
     int csplit = 1;
     if (C::SE && (long long)F * strips < resident)
         csplit = std::max(1, std::min(int(resident / ((long long)F * strips)), C::CT / 4));
-    const int items = F * strips * csplit;
+    // still fewer items than resident workgroups: deal each strip's steps over segments as well
+    int seg_steps = steps;
+    if ((long long)F * strips * csplit < resident) {
+        const int want = std::min<long long>(steps, resident / ((long long)F * strips * csplit));
+        seg_steps = (steps + want - 1) / want;
+    }
+    const int segs = (steps + seg_steps - 1) / seg_steps;
+    if ((long long)F * strips * csplit * segs > (1ll << 30)) throw std::runtime_error("ir_wgstrip: too many items");
+    const int items = F * strips * csplit * segs;
     const int grid = std::min(items, resident);
     hipLaunchKernelGGL((ir_wgstrip_kernel<T, C>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, steps, items,
-                       csplit);
+                       csplit, segs, seg_steps);
 }
 
 }  // namespace
