@@ -90,6 +90,41 @@ def measured_traffic(kernel: str, revision: str) -> float | None:
     return float(t["traffic_bytes_per_launch"])
 
 
+# config 2: the pointwise-conv GEMM at the literal config shapes (bias + hardswish), every tier, through the C-ABI tool
+GEMM_SHAPES = [("b2.expand", 2560 * 28 * 28, 120, 40), ("b14.expand", 2560 * 7 * 7, 960, 160)]
+
+
+def gemm_microbench(shv, hip, stream, e0, e1, iters: int = 10) -> list:
+    """Per shape and tier: device time per GEMM (HIP events on the launching stream, automatic kernel choice),
+    TFLOP/s and the HBM rate of its algorithmic bytes (fp32 A and C, W in the tier's parts, bias) against 8 TB/s."""
+    rng = np.random.default_rng(3)
+    out = []
+    for name, M, N, K in GEMM_SHAPES:
+        A = (rng.standard_normal((M, K), dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+        W = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+        b = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+        dA, dW, db, dC = hip.upload(A), hip.upload(W), hip.upload(b), hip.malloc(M * N * 4)
+        for mode, wbytes in (("fp16", 4), ("bf16", 6), ("fp32", 4)):
+            with shv.PwGemm(mode, dW, N, K, stream) as g:
+                for _ in range(2):
+                    g.run(dA, M, dC, db, shv.ACT_HSWISH, stream=stream)
+                hip.record(e0, stream)
+                for _ in range(iters):
+                    g.run(dA, M, dC, db, shv.ACT_HSWISH, stream=stream)
+                hip.record(e1, stream)
+                ms = hip.elapsed_ms(e0, e1) / iters
+            flop = 2.0 * M * N * K
+            nbytes = M * K * 4.0 + N * K * wbytes + M * N * 4.0 + N * 4.0
+            gbs = nbytes / (ms / 1000.0) / 1e9
+            out.append({"shape": name, "M": M, "N": N, "K": K, "mode": mode, "us": round(ms * 1000.0, 1),
+                        "TFLOP/s": round(flop / (ms / 1000.0) / 1e12, 2), "GB/s": round(gbs, 1),
+                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)})
+            log(f"[bench] gemm {name} {mode}: {out[-1]}")
+        for p in (dA, dW, db, dC):
+            hip.free(p)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,6 +137,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-only", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0)
+    ap.add_argument("--no-gemm", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the SHIELD-V forward has no cross-GPU step "
@@ -181,6 +217,8 @@ def main() -> int:
             hip.free(src)
             hip.free(dst)
 
+        gemm = None if args.kernel_only or args.no_gemm else gemm_microbench(shv, hip, stream, e0, e1)
+
         enc_ms = None
         if not args.kernel_only:   # encoder only (config 1: 2560 frames)
             d_tok = hip.malloc(B * 20 * 6144 * 4)
@@ -246,6 +284,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "device_copy": copy,
+        "gemm_microbench": gemm,
         "revision": revision,
     }
     print(json.dumps(line), flush=True)

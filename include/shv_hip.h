@@ -135,6 +135,21 @@ int shv_hip_profile_read(shv_hip_model* m, const char* name, double* total_ms, l
 /* Debug: write float32 intermediates of frame 0 / window 0 of the next synchronous call into dir (graphs off). */
 int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir);
 
+/* Pointwise-conv GEMM microbench.  No counterpart in shv_cuda.h: the reference benches its GEMM from a C++ tool
+ * (bench/gpu_gemm_bench.cu:27-116: engine GEMM on the model's 1x1 shapes, and a bitwise check that every kernel
+ * variant gives the same outputs).  C[m][n] = act(A[m][k] . W[n][k]^T + bias[n]) in the arithmetic of `mode`
+ * ("fp32": exact VALU order of the CPU engine; "fp16" / "bf16": split-operand MFMA), fp32 A, W, bias and C in
+ * device memory, row-major with leading dimensions k (A, W) and n (C).  act: the reference's codes
+ * (engine/cuda/common.cuh:69): 0 none, 1 ReLU, 2 hardswish, 3 SiLU, 4 hardsigmoid.  d_bias may be NULL.
+ * create repacks W on the device (synchronising `stream`); NULL + last_error on failure (fp16 / bf16 need k % 8 == 0).
+ * run: variant 0 = the engine's own kernel choice; fp32: 1 GEMV, 2 tiled; fp16 / bf16: 1 small-M, 2..6 direct
+ * with 1..5 column tiles per wave, 7 LDS-staged.  Returns 0, or -1 + last_error.  Asynchronous on `stream`. */
+typedef struct shv_hip_gemm shv_hip_gemm;
+shv_hip_gemm* shv_hip_gemm_create(const char* mode, int n, int k, const float* d_w, void* stream);
+int shv_hip_gemm_run(shv_hip_gemm* g, const float* d_a, long long m, const float* d_bias, int act, float* d_c,
+                     int variant, void* stream);
+void shv_hip_gemm_free(shv_hip_gemm* g);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

@@ -441,6 +441,9 @@ template <class F> int guarded(F&& f) {
 struct shv_hip_model {
     std::unique_ptr<Core> core;
 };
+struct shv_hip_gemm {
+    std::unique_ptr<shv::PwGemm> g;
+};
 
 extern "C" {
 
@@ -773,5 +776,32 @@ int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir) {
         return 0;
     });
 }
+
+
+// Pointwise-conv GEMM microbench (bench/gpu_gemm_bench.cu).  The reference's activation codes (common.cuh:69):
+// 0 none, 1 ReLU, 2 hardswish, 3 SiLU, 4 hardsigmoid.
+shv_hip_gemm* shv_hip_gemm_create(const char* mode, int n, int k, const float* d_w, void* stream) {
+    try {
+        shv::Precision p;
+        if (!mode || !shv::parse_precision(mode, &p)) throw std::runtime_error("unknown mode (fp32, bf16, fp16)");
+        if (n < 1 || k < 1 || !d_w) throw std::runtime_error("invalid argument");
+        if (p != shv::Precision::FP32 && k % 8) throw std::runtime_error("the matrix-core tiers need K % 8 == 0");
+        std::unique_ptr<shv_hip_gemm> g(new shv_hip_gemm());
+        g->g.reset(new shv::PwGemm(p, n, k, d_w, static_cast<hipStream_t>(stream)));
+        return g.release();
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return nullptr;
+    }
+}
+int shv_hip_gemm_run(shv_hip_gemm* g, const float* d_a, long long m, const float* d_bias, int act, float* d_c,
+                     int variant, void* stream) {
+    return guarded([&] {
+        if (!g || !d_a || !d_c || m < 1) throw std::runtime_error("invalid argument");
+        g->g->run(d_a, m, d_bias, act, d_c, variant, static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+void shv_hip_gemm_free(shv_hip_gemm* g) { delete g; }
 
 }  // extern "C"

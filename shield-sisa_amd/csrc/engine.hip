@@ -825,6 +825,45 @@ private:
 
 }  // namespace
 
+PwGemm::PwGemm(Precision p, int N, int K, const float* d_w, hipStream_t s) : prec_(p), N_(N), K_(K) {
+    if (N < 1 || K < 1 || !d_w) throw std::runtime_error("gemm: bad weight shape or null weights");
+    const int parts = p == Precision::FP32 ? 1 : p == Precision::BF16 ? weight_parts<bf16>() : weight_parts<f16>();
+    const size_t esz = p == Precision::FP32 ? 4 : 2;
+    wstride_ = (long long)N * K;
+    SHV_HIP_CHECK(hipMalloc(&w_, size_t(parts) * size_t(wstride_) * esz));
+    switch (p) {
+    case Precision::FP32: launch_repack<float>(d_w, static_cast<float*>(w_), N, K, 0, 1, s); break;
+    case Precision::BF16: launch_repack<bf16>(d_w, static_cast<bf16*>(w_), N, K, 0, parts, s); break;
+    case Precision::FP16: launch_repack<f16>(d_w, static_cast<f16*>(w_), N, K, 0, parts, s); break;
+    }
+    const hipError_t le = hipGetLastError();
+    const hipError_t se = hipStreamSynchronize(s);
+    if (le != hipSuccess || se != hipSuccess) {
+        (void)hipFree(w_);
+        throw std::runtime_error(std::string("gemm: weight repack failed: ") +
+                                 hipGetErrorString(le != hipSuccess ? le : se));
+    }
+}
+PwGemm::~PwGemm() { (void)hipFree(w_); }
+void PwGemm::run(const float* A, long long M, const float* bias, int act, float* C, int variant, hipStream_t s) const {
+    if (M < 1 || M > (1ll << 30) || !A || !C) throw std::runtime_error("gemm: bad M or null operand");
+    // the reference's activation codes (engine/cuda/common.cuh:69) -> this engine's
+    static const int kAct[5] = {ACT_NONE, ACT_RELU, ACT_HS, ACT_SILU, ACT_HSIG};
+    if (act < 0 || act > 4) throw std::runtime_error("gemm: unknown activation code");
+    GemmArgs p;
+    p.M = int(M); p.N = N_; p.K = K_;
+    p.A = A; p.lda = K_;
+    p.W = w_; p.ldw = K_; p.wstride = wstride_;
+    p.bias = bias; p.act = kAct[act];
+    p.C = C; p.ldc = N_;
+    switch (prec_) {
+    case Precision::FP32: gemm_f32_variant(p, s, variant); break;
+    case Precision::BF16: gemm_mfma_variant<bf16>(p, s, variant); break;
+    case Precision::FP16: gemm_mfma_variant<f16>(p, s, variant); break;
+    }
+    SHV_HIP_CHECK(hipGetLastError());
+}
+
 std::unique_ptr<Engine> make_engine(const HostModel& hm, Precision p, const EngineConfig& cfg) {
     switch (p) {
     case Precision::FP32: return std::unique_ptr<Engine>(new EngineT<float>(hm, p, cfg));

@@ -105,4 +105,25 @@ protected:
 
 std::unique_ptr<Engine> make_engine(const HostModel& hm, Precision p, const EngineConfig& cfg);
 
+// Pointwise-conv GEMM tool (the reference's bench/gpu_gemm_bench.cu:27-116): C[M][N] = act(A[M][K] . W[N][K]^T + bias)
+// in the tier's arithmetic, W repacked once on the device into the tier's operand parts; A, bias and C are the
+// caller's device buffers.  act takes the reference's codes (engine/cuda/common.cuh:69): 0 none, 1 ReLU, 2 hardswish,
+// 3 SiLU, 4 hardsigmoid.
+class PwGemm {
+public:
+    PwGemm(Precision p, int N, int K, const float* d_w, hipStream_t s);
+    ~PwGemm();
+    PwGemm(const PwGemm&) = delete;
+    PwGemm& operator=(const PwGemm&) = delete;
+    // variant: kernel choice (0 = the engine's own); see gemm_f32_variant / gemm_mfma_variant
+    void run(const float* A, long long M, const float* bias, int act, float* C, int variant, hipStream_t s) const;
+    Precision precision() const { return prec_; }
+
+private:
+    Precision prec_;
+    int N_ = 0, K_ = 0;
+    void* w_ = nullptr;
+    long long wstride_ = 0;
+};
+
 }  // namespace shv

@@ -945,33 +945,70 @@ void check_args(const GemmArgs& p, bool mfma) {
 
 }  // namespace
 
-void gemm_f32(const GemmArgs& p, hipStream_t s) {
-    check_args(p, false);
+namespace {
+void launch_gemv_f32(const GemmArgs& p, hipStream_t s) {
     const int nkb = cdiv(p.K, F32_BK);
-    if (p.M <= GV_MAXM && nkb <= 32) {
-        const int opw = p.swiglu ? (64 / nkb) & ~1 : 64 / nkb;
-        const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-        const bool vec = al16(p.A) && al16(p.W) && p.lda % 4 == 0 && p.ldw % 4 == 0 &&
-                         (!p.scale || (al16(p.scale) && p.ld_scale % 4 == 0));
-        const dim3 grid(cdiv(p.N, opw), cdiv(p.M, GV_ROWS));
-        if (p.scale) {
-            if (vec) hipLaunchKernelGGL((gemv_f32_kernel<true, true>), grid, dim3(64), 0, s, p, nkb, opw);
-            else hipLaunchKernelGGL((gemv_f32_kernel<true, false>), grid, dim3(64), 0, s, p, nkb, opw);
-        } else {
-            if (vec) hipLaunchKernelGGL((gemv_f32_kernel<false, true>), grid, dim3(64), 0, s, p, nkb, opw);
-            else hipLaunchKernelGGL((gemv_f32_kernel<false, false>), grid, dim3(64), 0, s, p, nkb, opw);
-        }
-        return;
+    if (nkb > 32) throw std::runtime_error("gemm_f32: the GEMV kernel takes K <= 2048");
+    const int opw = p.swiglu ? (64 / nkb) & ~1 : 64 / nkb;
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const bool vec = al16(p.A) && al16(p.W) && p.lda % 4 == 0 && p.ldw % 4 == 0 &&
+                     (!p.scale || (al16(p.scale) && p.ld_scale % 4 == 0));
+    const long long yblocks = cdiv(p.M, GV_ROWS);
+    if (yblocks > 65535) throw std::runtime_error("gemm_f32: M too large for the GEMV kernel");
+    const dim3 grid(cdiv(p.N, opw), (unsigned)yblocks);
+    if (p.scale) {
+        if (vec) hipLaunchKernelGGL((gemv_f32_kernel<true, true>), grid, dim3(64), 0, s, p, nkb, opw);
+        else hipLaunchKernelGGL((gemv_f32_kernel<true, false>), grid, dim3(64), 0, s, p, nkb, opw);
+    } else {
+        if (vec) hipLaunchKernelGGL((gemv_f32_kernel<false, true>), grid, dim3(64), 0, s, p, nkb, opw);
+        else hipLaunchKernelGGL((gemv_f32_kernel<false, false>), grid, dim3(64), 0, s, p, nkb, opw);
     }
+}
+void launch_tiled_f32(const GemmArgs& p, hipStream_t s) {
     const dim3 grid(cdiv(p.M, F32_BM), cdiv(p.N, F32_BN));
     if (p.scale) hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(256), 0, s, p);
+}
+}  // namespace
+
+void gemm_f32(const GemmArgs& p, hipStream_t s) { gemm_f32_variant(p, s, 0); }
+
+void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
+    check_args(p, false);
+    switch (variant) {
+    case 0:
+        if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) launch_gemv_f32(p, s);
+        else launch_tiled_f32(p, s);
+        return;
+    case 1: launch_gemv_f32(p, s); return;
+    case 2: launch_tiled_f32(p, s); return;
+    }
+    throw std::runtime_error("gemm_f32: unknown kernel variant " + std::to_string(variant));
 }
 
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s) {
     check_args(p, true);
     launch_gemm<T>(p, s);
 }
+
+template <typename T> void gemm_mfma_variant(const GemmArgs& p, hipStream_t s, int variant) {
+    check_args(p, true);
+    if (variant >= 2 && variant <= 6 && (p.Ah || p.Ch || p.swiglu))
+        throw std::runtime_error("gemm: the direct kernel takes fp32 A and C and no SwiGLU");
+    switch (variant) {
+    case 0: launch_gemm<T>(p, s); return;
+    case 1: launch_small<T>(p, s); return;
+    case 2: launch_direct<T, 1>(p, s); return;
+    case 3: launch_direct<T, 2>(p, s); return;
+    case 4: launch_direct<T, 3>(p, s); return;
+    case 5: launch_direct<T, 4>(p, s); return;
+    case 6: launch_direct<T, 5>(p, s); return;
+    case 7: launch_lds<T, 4, 4, 2, 2>(p, s); return;
+    }
+    throw std::runtime_error("gemm: unknown kernel variant " + std::to_string(variant));
+}
+template void gemm_mfma_variant<f16>(const GemmArgs&, hipStream_t, int);
+template void gemm_mfma_variant<bf16>(const GemmArgs&, hipStream_t, int);
 template void gemm_mfma<f16>(const GemmArgs&, hipStream_t);
 template void gemm_mfma<bf16>(const GemmArgs&, hipStream_t);
 

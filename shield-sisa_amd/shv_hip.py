@@ -70,6 +70,9 @@ _SIGS = {
     "shv_hip_profile_enable": (ctypes.c_int, [_P, ctypes.c_int]),
     "shv_hip_profile_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P, _P]),
     "shv_hip_set_dump_dir": (ctypes.c_int, [_P, ctypes.c_char_p]),
+    "shv_hip_gemm_create": (_P, [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, _P, _P]),
+    "shv_hip_gemm_run": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P, ctypes.c_int, _P, ctypes.c_int, _P]),
+    "shv_hip_gemm_free": (None, [_P]),
 }
 
 _libs: dict[str, ctypes.CDLL] = {}
@@ -392,6 +395,37 @@ class Hip:
 
     def event_destroy(self, e: int) -> None:
         self.check(self.rt.hipEventDestroy(e), "hipEventDestroy")
+
+
+ACT_NONE, ACT_RELU, ACT_HSWISH, ACT_SILU, ACT_HSIGMOID = 0, 1, 2, 3, 4   # the reference's codes (common.cuh:69)
+GEMM_VARIANTS = {"fp32": [1, 2], "fp16": list(range(1, 8)), "bf16": list(range(1, 8))}
+
+
+class PwGemm:
+    """Pointwise-conv GEMM of one tier on device buffers (shv_hip_gemm_*): W [n][k] fp32 repacked at creation."""
+
+    def __init__(self, mode: str, d_w: int, n: int, k: int, stream: int | None = None):
+        self.lib = library()
+        self.g = self.lib.shv_hip_gemm_create(mode.encode(), n, k, d_w, stream)
+        if not self.g:
+            raise ShvError(last_error())
+        self.mode, self.n, self.k = mode, n, k
+
+    def run(self, d_a: int, m: int, d_c: int, d_bias: int | None = None, act: int = ACT_NONE, variant: int = 0,
+            stream: int | None = None) -> None:
+        if self.lib.shv_hip_gemm_run(self.g, d_a, m, d_bias, act, d_c, variant, stream) != 0:
+            raise ShvError(last_error())
+
+    def close(self) -> None:
+        if self.g:
+            self.lib.shv_hip_gemm_free(self.g)
+            self.g = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 def sigmoid64(logit: float) -> float:

@@ -21,7 +21,7 @@ def declared_functions():
 def test_every_declared_symbol_is_exported(shv):
     lib = shv.library()
     names = declared_functions()
-    assert len(names) == 28
+    assert len(names) == 31
     for n in names:
         assert hasattr(lib, n), n
     exp = shv.library(experimental=True)
@@ -132,3 +132,17 @@ def test_null_arguments(shv):
     assert lib.shv_hip_mode(None) == b""
     lib.shv_hip_job_free(None)
     lib.shv_hip_free(None)
+
+
+def test_gemm_tool_rejects_bad_arguments(shv):
+    """The GEMM microbench entry points validate before any device work (NULL / -1 plus last_error)."""
+    lib = shv.library()
+    assert not lib.shv_hip_gemm_create(b"fp8", 16, 16, 1, None)
+    assert "unknown mode" in shv.last_error()
+    assert not lib.shv_hip_gemm_create(b"fp16", 16, 12, 1, None)
+    assert "K % 8" in shv.last_error()
+    assert not lib.shv_hip_gemm_create(b"fp32", 16, 16, None, None)
+    assert "invalid argument" in shv.last_error()
+    assert lib.shv_hip_gemm_run(None, 1, 1, None, 0, 1, 0, None) == -1
+    assert "invalid argument" in shv.last_error()
+    lib.shv_hip_gemm_free(None)
