@@ -125,6 +125,54 @@ def gemm_microbench(shv, hip, stream, e0, e1, iters: int = 10) -> list:
     return out
 
 
+SEQ_FAMILIES = ["assemble", "rmsnorm", "gemm_seq", "gdn_prep", "delta", "gated_norm", "sisa", "gemm_f32_small", "head"]
+
+
+def async_bf16(shv, weights: Path, clips: np.ndarray, n_clips: int = 1024, per_job: int = 128) -> dict:
+    """Config 4: n_clips clips in bf16 through the async batched API (shv_hip_submit / job_wait) from pinned host
+    memory, per_job clips per request; the scheduler pipelines host copies and compute over its two slots and
+    streams.  Host-to-device copies are included.  Parity: the first 64 clips against the exact fp32 tier."""
+    import ctypes
+    m = shv.Model(weights, "bf16", experimental=True, max_frames=per_job * 20, max_windows=per_job)
+    lib = m.lib
+    nbytes = n_clips * 20 * shv.FRAME_BYTES
+    ptr = lib.shv_hip_host_alloc(nbytes)
+    if not ptr:
+        raise shv.ShvError("shv_hip_host_alloc failed")
+    try:
+        host = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(ptr)).reshape(n_clips, 20, shv.FRAME_BYTES)
+        for i in range(0, n_clips, len(clips)):
+            k = min(len(clips), n_clips - i)
+            host[i:i + k] = clips[:k].reshape(k, 20, shv.FRAME_BYTES)
+        logits = np.empty(n_clips, np.float32)
+        wf = np.arange(per_job * 20, dtype=np.int32)
+
+        def run():
+            jobs = [m.submit(frames=host[j:j + per_job], n_windows=per_job, window_frames=wf,
+                             logits_out=logits[j:j + per_job]) for j in range(0, n_clips, per_job)]
+            for job, _ in jobs:
+                if m.job_wait(job) != 0:
+                    raise shv.ShvError(m.job_error(job))
+                m.job_free(job)
+
+        run()   # graphs captured
+        t0 = time.perf_counter()
+        run()
+        dt = time.perf_counter() - t0
+        npar = min(64, len(clips))
+        sub = logits[:npar].copy()
+    finally:
+        lib.shv_hip_host_free(ptr)
+        m.close()
+    with shv.Model(weights, "fp32") as ex:
+        ref = ex.predict(clips[:npar])
+    flips = int(np.sum((sub >= 0) != (ref >= 0)))
+    out = {"clips": n_clips, "clips_per_job": per_job, "seconds": round(dt, 4), "clips_per_s": round(n_clips / dt, 1),
+           "h2d_included": True, "parity_clips": npar, "parity_max_abs_vs_fp32": float(np.abs(sub - ref).max()), "parity_flips": flips}
+    log(f"[bench] config 4 bf16 async: {out}")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +186,7 @@ def main() -> int:
     ap.add_argument("--kernel-only", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0)
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-async", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the SHIELD-V forward has no cross-GPU step "
@@ -185,6 +234,9 @@ def main() -> int:
         stats = {k: v for k, v in stats.items() if v and v["launches"]}
         per_step = {k: round(v["ms"] / prof_steps, 3) for k, v in stats.items()}
         log("[bench] per-step ms by kernel family: " + json.dumps(per_step))
+        seq_ms = sum(stats[k]["ms"] for k in SEQ_FAMILIES if k in stats) / prof_steps
+        seq_wps = B / (seq_ms / 1000.0)
+        log(f"[bench] sequence stages {seq_ms:.3f} ms / {B} windows -> {seq_wps:.0f} windows/s")
         # dominant kernel: the fused-block kernel with the most device time per step (each such family is one kernel
         # symbol at one shape, so rocprofv3's per-kernel average can be set beside this one)
         dom = max((k for k in stats if k.startswith("ir_")), key=lambda k: stats[k]["ms"])
@@ -257,6 +309,10 @@ def main() -> int:
                 lat = float(np.percentile(ts, 50))
                 log(f"[bench] batch-1 latency p50 {lat:.3f} ms (p95 {np.percentile(ts, 95):.3f})")
 
+        c4 = None
+        if not args.kernel_only and not args.no_async:
+            c4 = async_bf16(shv, w, clips)
+
         cpu = None
         if not args.no_cpu and not args.kernel_only:
             cpu = cpu_baseline(w, clips, args.cpu_seconds)
@@ -280,6 +336,8 @@ def main() -> int:
                    "reference_gpu_clips_per_s": round(REF_B128_CLIPS_PER_S, 1)},
         "latency_b1_ms": None if lat is None else round(lat, 3),
         "encoder_frames_per_s": None if enc_ms is None else round(B * 20 / (enc_ms / 1000.0), 1),
+        "sequence_windows_per_s": round(seq_wps, 1),
+        "async_bf16_1024": c4,
         "family_ms_per_step": per_step,
         "roofline": roofline,
         "cpu_baseline": cpu,
