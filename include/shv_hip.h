@@ -150,6 +150,16 @@ int shv_hip_gemm_run(shv_hip_gemm* g, const float* d_a, long long m, const float
                      int variant, void* stream);
 void shv_hip_gemm_free(shv_hip_gemm* g);
 
+/* Gated delta rule of one tier on device buffers (the scan of config 3 on its own; no counterpart in shv_cuda.h --
+ * the reference runs its delta_kernel only inside classify, engine/cuda/seq.cu:106-195).  Per window 321 rows; rows
+ * = n_windows * 321: q, k [rows][384] (6 heads x 64, l2-normalised; q scaled), v, o [rows][768] (6 heads x 128),
+ * decay, beta [rows][8] (head h in column h).  Per (window, head): S_0 = 0, S_t = a_t S_{t-1} + k_t u_t^T,
+ * u_t = b_t (v_t - a_t S_{t-1}^T k_t), o_t = S_t^T q_t.  variant 0: the tier's own kernel (fp32: token by token in
+ * the reference's order; fp16 / bf16: the chunked scan), 1: token by token, 2: chunked (fp16 / bf16).  Synchronous
+ * for the chunked scan (it allocates a work buffer per call).  Returns 0, or -1 + last_error. */
+int shv_hip_delta_rule(const char* mode, const float* d_q, const float* d_k, const float* d_v, const float* d_decay,
+                       const float* d_beta, int n_windows, float* d_o, int variant, void* stream);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

@@ -804,4 +804,16 @@ int shv_hip_gemm_run(shv_hip_gemm* g, const float* d_a, long long m, const float
 }
 void shv_hip_gemm_free(shv_hip_gemm* g) { delete g; }
 
+// Gated delta rule microbench / parity entry (config 3's scan on its own).
+int shv_hip_delta_rule(const char* mode, const float* d_q, const float* d_k, const float* d_v, const float* d_decay,
+                       const float* d_beta, int n_windows, float* d_o, int variant, void* stream) {
+    return guarded([&] {
+        shv::Precision p;
+        if (!mode || !shv::parse_precision(mode, &p)) throw std::runtime_error("unknown mode (fp32, bf16, fp16)");
+        shv::run_delta_rule(p, d_q, d_k, d_v, d_decay, d_beta, n_windows, d_o, variant,
+                            static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
 }  // extern "C"

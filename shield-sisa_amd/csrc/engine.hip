@@ -400,6 +400,8 @@ private:
     float *se_pool_ = nullptr, *se_hid_ = nullptr, *se_scale_ = nullptr;
     float *H_ = nullptr, *P_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *dec_ = nullptr, *beta_ = nullptr,
           *O_ = nullptr;
+    float* dwork_ = nullptr;     // half tiers: the chunked delta rule's per-chunk products
+    bool delta_chunked_ = false;
     float *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;   // fp32 tier: the sequence GEMMs' A operands
     G *XNh_ = nullptr, *ONh_ = nullptr, *HIDh_ = nullptr;    // MFMA tiers: the same, written pre-split by producers
     long long mrows_ = 0;                                     // rows of those buffers (part stride = mrows_ * width)
@@ -438,6 +440,10 @@ private:
         dec_ = amem_.make<float>(Mm * 8);
         beta_ = amem_.make<float>(Mm * 8);
         O_ = amem_.make<float>(Mm * kVD);
+        // half tiers: the chunked delta-rule scan (SHV_HIP_DELTA_SEQ=1 keeps the token-by-token kernel, for A/B runs)
+        const char* ds = std::getenv("SHV_HIP_DELTA_SEQ");
+        delta_chunked_ = !kF32 && !(ds && *ds && std::strcmp(ds, "0") != 0);
+        if (delta_chunked_) dwork_ = amem_.make<float>(delta_chunk_floats(int(Bm)));
         mrows_ = (long long)Mm;
         if constexpr (kF32) {
             XN_ = amem_.make<float>(Mm * kD);
@@ -746,8 +752,15 @@ private:
                     launch_gdn_prep(P_, g.conv_w, g.conv_b, g.neg_rate, g.dt_bias, Q_, K_, V_, dec_, beta_, B, s);
                 });
                 check_launch();
-                timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s,
-                      [&] { launch_delta(Q_, K_, V_, dec_, beta_, O_, B, kF32, s); });
+                timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s, [&] {
+                    if constexpr (!kF32) {
+                        if (delta_chunked_) {
+                            launch_delta_chunked<G>(Q_, K_, V_, dec_, beta_, O_, dwork_, B, s);
+                            return;
+                        }
+                    }
+                    launch_delta(Q_, K_, V_, dec_, beta_, O_, B, kF32, s);
+                });
                 check_launch();
                 timed("gated_norm", double(M) * (4.0 * 2 * kVD + kAS * kVD), s, [&] {
                     if constexpr (kF32) launch_gated_norm<float>(O_, P_, g.o_norm_w, ON_, M, s);
@@ -824,6 +837,29 @@ private:
 };
 
 }  // namespace
+
+void run_delta_rule(Precision p, const float* Q, const float* K, const float* V, const float* dec, const float* beta,
+                    int n_windows, float* O, int variant, hipStream_t s) {
+    if (!Q || !K || !V || !dec || !beta || !O || n_windows < 1 || n_windows > 65536)
+        throw std::runtime_error("delta rule: null buffer or bad window count");
+    if (variant < 0 || variant > 2 || (p == Precision::FP32 && variant == 2))
+        throw std::runtime_error("delta rule: unknown variant for this mode");
+    const bool chunked = p != Precision::FP32 && variant != 1;
+    if (!chunked) {
+        launch_delta(Q, K, V, dec, beta, O, n_windows, p == Precision::FP32, s);
+        SHV_HIP_CHECK(hipGetLastError());
+        return;
+    }
+    float* work = nullptr;
+    SHV_HIP_CHECK(hipMalloc(&work, delta_chunk_floats(n_windows) * sizeof(float)));
+    if (p == Precision::BF16) launch_delta_chunked<bf16>(Q, K, V, dec, beta, O, work, n_windows, s);
+    else launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s);
+    const hipError_t le = hipGetLastError();
+    const hipError_t se = hipStreamSynchronize(s);
+    (void)hipFree(work);
+    SHV_HIP_CHECK(le);
+    SHV_HIP_CHECK(se);
+}
 
 PwGemm::PwGemm(Precision p, int N, int K, const float* d_w, hipStream_t s) : prec_(p), N_(N), K_(K) {
     if (N < 1 || K < 1 || !d_w) throw std::runtime_error("gemm: bad weight shape or null weights");

@@ -109,6 +109,12 @@ std::unique_ptr<Engine> make_engine(const HostModel& hm, Precision p, const Engi
 // in the tier's arithmetic, W repacked once on the device into the tier's operand parts; A, bias and C are the
 // caller's device buffers.  act takes the reference's codes (engine/cuda/common.cuh:69): 0 none, 1 ReLU, 2 hardswish,
 // 3 SiLU, 4 hardsigmoid.
+// Gated delta rule of one tier on caller device buffers (rows = n_windows * 321; Q, K [rows][384], V, O [rows][768],
+// decay, beta [rows][8]).  variant 0: the tier's own kernel (fp32: token by token in the reference's order; fp16 /
+// bf16: the chunked scan), 1: token by token, 2: chunked (fp16 / bf16 only).  Allocates its work buffer per call.
+void run_delta_rule(Precision p, const float* Q, const float* K, const float* V, const float* dec, const float* beta,
+                    int n_windows, float* O, int variant, hipStream_t s);
+
 class PwGemm {
 public:
     PwGemm(Precision p, int N, int K, const float* d_w, hipStream_t s);

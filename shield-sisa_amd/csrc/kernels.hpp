@@ -134,6 +134,13 @@ void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, c
 // 64-key fma chains (fp32 tier); else each column's keys split over 4 lane rows, partial sums added in a fixed order
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
                   int B, bool exact, hipStream_t s);
+// Half tiers: the same recurrence over chunks of 32 tokens on the split-operand matrix cores (a parallel prep of
+// every chunk's state-independent products into `work`, delta_chunk_floats(B) floats, then one scan per
+// (window, head)); equal to the token-by-token form up to rounding.
+size_t delta_chunk_floats(int B);
+template <typename T>
+void launch_delta_chunked(const float* Q, const float* K, const float* V, const float* dec, const float* beta,
+                          float* O, float* work, int B, hipStream_t s);
 // ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768] (T = f16 / bf16: split parts, as launch_rmsnorm)
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,

@@ -24,6 +24,10 @@ template <> struct Split<f16> {
     static __device__ __forceinline__ int ap(int i) { return i == 0 ? 1 : 0; }
     static __device__ __forceinline__ int wp(int i) { return i == 1 ? 1 : 0; }
     static __device__ __forceinline__ void split(float x, f16* part) {
+        // x must be the fp32 value itself: without this the compiler may round a product a * b feeding x straight
+        // to fp16 (v_fma_mixlo_f16, one rounding of the exact product) while lo is formed from the fp32-rounded
+        // x, so that hi + lo is off by an fp16 ulp near ties
+        asm("" : "+v"(x));
         const f16 h = f16(x);
         part[0] = h;
         part[1] = f16(x - float(h));
@@ -41,6 +45,7 @@ template <> struct Split<bf16> {
     static __device__ __forceinline__ int ap(int i) { const int t[6] = {2, 0, 1, 1, 0, 0}; return t[i]; }
     static __device__ __forceinline__ int wp(int i) { const int t[6] = {0, 2, 1, 0, 1, 0}; return t[i]; }
     static __device__ __forceinline__ void split(float x, bf16* part) {
+        asm("" : "+v"(x));   // the fp32 value itself (as in Split<f16>::split)
         const bf16 h = bf16(x);
         const float r = x - float(h);
         const bf16 m = bf16(r);

@@ -7,6 +7,7 @@
 #include "kernels.hpp"
 #include "mfma.hpp"
 
+#include <stdexcept>
 #include <type_traits>
 
 namespace shv {
@@ -502,6 +503,375 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
     }
 }
 
+// ------------------------------------------------------------------------------------------------ chunked delta rule
+// Half tiers.  Per (window, head) the recurrence S_t = a_t S_{t-1} + k_t u_t^T, u_t = b_t (v_t - a_t S_{t-1}^T k_t),
+// o_t = S_t^T q_t (S: 64 keys x 128 values; isa_impl.hpp:911-947) runs over chunks of DC = 32 tokens.  Inside a
+// chunk, with g_i = a_0 ... a_i (inclusive cumulative decay) and G_ij = a_{j+1} ... a_i (j <= i, 1 on the diagonal),
+// unrolling the recurrence gives (I + L) U = diag(b) (V - diag(g) K S_0), L_ij = b_i G_ij (k_i . k_j) for j < i.
+// With T = (I + L)^-1:
+//   U   = A1V - B1 S_0,              A1V = T diag(b) V,   B1 = T diag(b g) K,
+//   O   = diag(g) Q S_0 + P U,       P_ij = G_ij (q_i . k_j) for j <= i, else 0,
+//   S_C = g_31 S_0 + Kd^T U,         Kd_j = G_31,j k_j.
+// Tokens past the window's end pad the last chunk with a = 1, b = 0, k = q = v = 0, which leaves every real
+// quantity unchanged.  delta_chunk_prep_kernel forms A1V and B1 of every chunk in parallel (nothing there depends on
+// the state); delta_chunk_scan_kernel walks the chunks of one (window, head) in order, the state's fp32 value in
+// MFMA accumulators and its split parts in LDS.  Every product runs on the split-operand matrix cores (fp32-level
+// operand precision); T comes from forward substitution in fp32, the decay products from running products of a.
+// The results equal the token-by-token recurrence up to rounding (tested against it on the GPU).
+constexpr int DC = 32;                      // tokens per chunk
+constexpr int DNC = (kT + DC - 1) / DC;     // chunks per window
+constexpr int DCF = DC * 128 + DC * 64;     // floats per chunk in the prep buffer: A1V [32][128], then B1 [32][64]
+
+// 8 fp32 values (two float4 in LDS) -> the P split-part fragments
+template <typename T>
+__device__ __forceinline__ void frag_lds(const float* p, typename Split<T>::V8* parts) {
+    const float4 u = reinterpret_cast<const float4*>(p)[0], w = reinterpret_cast<const float4*>(p)[1];
+    const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+    split8<T>(x, parts);
+}
+// 8 pre-split elements of each part (16 bytes per part) -> fragments
+template <typename T>
+__device__ __forceinline__ void frag_parts(const T* p, long long part_stride, typename Split<T>::V8* parts) {
+#pragma unroll
+    for (int q = 0; q < Split<T>::P; ++q) parts[q] = load_part8<T>(p + q * part_stride);
+}
+// 4 consecutive elements of each part <- split(v[0..3]) (8-byte stores)
+template <typename T>
+__device__ __forceinline__ void put4(T* p, long long part_stride, float v0, float v1, float v2, float v3) {
+    const float v[4] = {v0, v1, v2, v3};
+    T part[4][Split<T>::P];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Split<T>::split(v[e], part[e]);
+#pragma unroll
+    for (int q = 0; q < Split<T>::P; ++q) {
+        const T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
+        *reinterpret_cast<uint2*>(p + q * part_stride) = *reinterpret_cast<const uint2*>(four);
+    }
+}
+template <typename T>
+__device__ __forceinline__ void put1(T* p, long long part_stride, float v) {
+    T part[Split<T>::P];
+    Split<T>::split(v, part);
+#pragma unroll
+    for (int q = 0; q < Split<T>::P; ++q) p[q * part_stride] = part[q];
+}
+
+// Decay products of one chunk (one wave; lane i < 32 holds a_i in `ai`, read by every lane with readlane, so no
+// memory carries it between lanes): lane j < 32 writes column j of G, lane 32 writes g.
+__device__ __forceinline__ void chunk_decays(float ai, float (*Gs)[DC + 1], float* gs, int lane) {
+    float p = 1.0f, q = 1.0f;
+#pragma unroll
+    for (int i = 0; i < DC; ++i) {
+        const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ai), i));
+        if (i > lane) p = p * a;
+        q = q * a;
+        if (lane < DC) Gs[i][lane] = i >= lane ? p : 0.0f;
+        if (lane == DC) gs[i] = q;
+    }
+}
+
+// One wave per (window, head, chunk): A1V and B1 into CH [window][head][chunk][DCF].
+template <typename T>
+__global__ void __launch_bounds__(64)
+delta_chunk_prep_kernel(const float* __restrict__ K, const float* __restrict__ V, const float* __restrict__ dec,
+                        const float* __restrict__ beta, float* __restrict__ CH) {
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    constexpr int P = S::P;
+    const int c = blockIdx.x % DNC, wh = blockIdx.x / DNC;
+    const int b = wh / kHeads, h = wh % kHeads;
+    const int lane = threadIdx.x, r = lane & 15, g = lane >> 4;
+    const int t0 = c * DC, n = min(DC, kT - t0);
+    const long long row0 = (long long)b * kT + t0;
+    __shared__ __attribute__((aligned(16))) float Ks[DC][64 + 4];
+    __shared__ __attribute__((aligned(16))) float Vs[DC][128 + 4];
+    __shared__ __attribute__((aligned(16))) float Ls[DC][DC + 4];
+    __shared__ __attribute__((aligned(16))) float Ts[DC][DC + 4];
+    __shared__ float Gs[DC][DC + 1];
+    __shared__ float bs[DC], gs[DC];
+    {   // stage (loads at clamped rows, all in flight together; zero / a = 1 past the window's end)
+        float4 kv[8], vv[16];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = lane + 64 * k, row = i >> 4, c4 = (i & 15) * 4;
+            kv[k] = *reinterpret_cast<const float4*>(K + (row0 + min(row, n - 1)) * kD + h * 64 + c4);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int i = lane + 64 * k, row = i >> 5, c4 = (i & 31) * 4;
+            vv[k] = *reinterpret_cast<const float4*>(V + (row0 + min(row, n - 1)) * kVD + h * 128 + c4);
+        }
+        float av = 1.0f, bv = 0.0f;
+        if (lane < DC) {
+            av = dec[(row0 + min(lane, n - 1)) * 8 + h];
+            bv = beta[(row0 + min(lane, n - 1)) * 8 + h];
+        }
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = lane + 64 * k, row = i >> 4, c4 = (i & 15) * 4;
+            *reinterpret_cast<float4*>(&Ks[row][c4]) = row < n ? kv[k] : z;
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int i = lane + 64 * k, row = i >> 5, c4 = (i & 31) * 4;
+            *reinterpret_cast<float4*>(&Vs[row][c4]) = row < n ? vv[k] : z;
+        }
+        if (lane < DC) bs[lane] = lane < n ? bv : 0.0f;
+        chunk_decays(lane < n ? av : 1.0f, Gs, gs, lane);
+    }
+    __syncthreads();
+    // L = b_i G_ij (k_i . k_j) for j < i: tiles (ti, tj) of K K^T, keys in two K steps; tile (0, 1) is all zero
+#pragma unroll
+    for (int tile = 0; tile < 4; ++tile) {
+        const int ti = tile >> 1, tj = tile & 1;
+        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (ti >= tj) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                V8 ap[P], bp[P];
+                frag_lds<T>(&Ks[ti * 16 + r][ks * 32 + 8 * g], ap);
+                frag_lds<T>(&Ks[tj * 16 + r][ks * 32 + 8 * g], bp);
+                acc = mfma_split<T>(ap, bp, acc);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = ti * 16 + 4 * g + e, j = tj * 16 + r;
+            Ls[i][j] = j < i ? bs[i] * (Gs[i][j] * acc[e]) : 0.0f;
+        }
+    }
+    __syncthreads();
+    // T = (I + L)^-1: lane j solves column j, t_i = [i == j] - sum_{m < i} L_im t_m (fma chain over m in order)
+    if (lane < DC) {
+        float t[DC];
+#pragma unroll
+        for (int i = 0; i < DC; ++i) {
+            float acc = i == lane ? 1.0f : 0.0f;
+#pragma unroll
+            for (int m4 = 0; m4 < (i + 3) / 4; ++m4) {
+                const float4 l4 = *reinterpret_cast<const float4*>(&Ls[i][4 * m4]);
+                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * m4 + e < i) acc = __builtin_fmaf(-lv[e], t[4 * m4 + e], acc);
+            }
+            t[i] = acc;
+        }
+#pragma unroll
+        for (int i = 0; i < DC; ++i) Ts[i][lane] = t[i];
+    }
+    __syncthreads();
+    // A1V = T diag(b) V (32 x 128) and B1 = T diag(b g) K (32 x 64): one K step over the chunk's 32 tokens
+    float* out = CH + ((long long)wh * DNC + c) * DCF;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+        V8 ap[P];
+        frag_lds<T>(&Ts[ti * 16 + r][8 * g], ap);
+#pragma unroll 2
+        for (int tc = 0; tc < 8; ++tc) {
+            float y[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = bs[8 * g + e] * Vs[8 * g + e][tc * 16 + r];
+            V8 bp[P];
+            split8<T>(y, bp);
+            const f32x4 acc = mfma_split<T>(ap, bp, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[(ti * 16 + 4 * g + e) * 128 + tc * 16 + r] = acc[e];
+        }
+#pragma unroll
+        for (int tk = 0; tk < 4; ++tk) {
+            float y[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = (bs[8 * g + e] * gs[8 * g + e]) * Ks[8 * g + e][tk * 16 + r];
+            V8 bp[P];
+            split8<T>(y, bp);
+            const f32x4 acc = mfma_split<T>(ap, bp, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[DC * 128 + (ti * 16 + 4 * g + e) * 64 + tk * 16 + r] = acc[e];
+        }
+    }
+}
+
+// One workgroup (4 waves) per (window, head, block of VS value columns), the chunks in order.  Value columns are
+// independent in every product below, so VS = 32, 64 or 128 splits a head over 4, 2 or 1 workgroups with every
+// output computed by the same fragments in the same order (bitwise equal for every VS).  Tiles: U / Q S_0 / O
+// [token tile 0..1][value tile] as u = wave + 4 j (ti = u % 2, vt = u / 2), state S[key tile][value tile] as
+// s = wave + 4 j (kt = s % 4, vt = s / 4), P tile (wave / 2, wave % 2).  Per chunk: stage Q, K, -B1 parts (and the
+// decays) / barrier / P, U = A1V - B1 S_0, Q S_0, Kd^T parts / barrier / O = g Q S_0 + P U, S = g_31 S + Kd^T U
+// (state parts rewritten).  A chunk's outputs are stored at the start of the next chunk, after the wait for its
+// prefetched operands (one vmcnt counter retires loads and stores in order).
+template <typename T, int VS>
+__global__ void __launch_bounds__(256)
+delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ dec,
+                        const float* __restrict__ CH, float* __restrict__ O) {
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    constexpr int P = S::P;
+    constexpr int NVT = VS / 16, UT = NVT / 2, ST = NVT;   // value tiles; U and state tiles per wave
+    constexpr int NB = 128 / VS;                           // value blocks per head
+    constexpr int KL = 64 + 8, TL = DC + 8;   // element strides of key-major and token-major part rows
+    __shared__ __attribute__((aligned(16))) T Sp[P][VS][KL];    // state [value][key]
+    __shared__ __attribute__((aligned(16))) T Qp[P][DC][KL];    // q [token][key]
+    __shared__ __attribute__((aligned(16))) T Kp[P][DC][KL];    // k [token][key]
+    __shared__ __attribute__((aligned(16))) T Bp[P][DC][KL];    // -B1 [token][key]
+    __shared__ __attribute__((aligned(16))) T KdT[P][64][TL];   // Kd^T [key][token]
+    __shared__ __attribute__((aligned(16))) T Pp[P][DC][TL];    // P [token i][token j]
+    __shared__ __attribute__((aligned(16))) T Up[P][VS][TL];    // U [value][token]
+    __shared__ float Gs[DC][DC + 1];
+    __shared__ float gs[DC];
+    const int vb = blockIdx.x % NB, wh = blockIdx.x / NB, b = wh / kHeads, h = wh % kHeads;
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const long long rowb = (long long)b * kT;
+    const int vcol0 = h * 128 + vb * VS;   // first value column of this block in the [rows][768] layout
+    const float* chb = CH + (long long)wh * DNC * DCF;
+    for (int i = tid; i < P * VS * KL; i += 256) (&Sp[0][0][0])[i] = T(0.0f);
+
+    // prefetched operands of a chunk: q, k, b1 rows (2 float4 each), this wave's A1V values, the decay
+    float4 rq[2], rk[2], rb[2];
+    float ra = 1.0f, rv[UT][4];
+    auto fetch = [&](int c) {
+        const int t0 = c * DC, n = min(DC, kT - t0);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = tid + 256 * k, row = i >> 4, c4 = (i & 15) * 4;
+            const long long gr = rowb + t0 + min(row, n - 1);
+            rq[k] = *reinterpret_cast<const float4*>(Q + gr * kD + h * 64 + c4);
+            rk[k] = *reinterpret_cast<const float4*>(K + gr * kD + h * 64 + c4);
+            rb[k] = *reinterpret_cast<const float4*>(chb + (long long)c * DCF + DC * 128 + row * 64 + c4);
+        }
+#pragma unroll
+        for (int j = 0; j < UT; ++j) {
+            const int u = wave + 4 * j, ti = u % 2, vt = u / 2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                rv[j][e] = chb[(long long)c * DCF + (ti * 16 + 4 * g + e) * 128 + vb * VS + vt * 16 + r];
+        }
+        if (tid < DC) ra = dec[(rowb + t0 + min(tid, n - 1)) * 8 + h];
+    };
+    f32x4 Sacc[ST];
+#pragma unroll
+    for (int j = 0; j < ST; ++j) Sacc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float ob[UT][4];   // this lane's outputs of the previous chunk (U-tile order, rows 4 g + e)
+    int ob_t0 = -1;
+    auto store_out = [&]() {
+#pragma unroll
+        for (int j = 0; j < UT; ++j) {
+            const int u = wave + 4 * j, ti = u % 2, vt = u / 2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = ob_t0 + ti * 16 + 4 * g + e;
+                if (i < kT) O[(rowb + i) * kVD + vcol0 + vt * 16 + r] = ob[j][e];
+            }
+        }
+    };
+    fetch(0);
+    for (int c = 0; c < DNC; ++c) {
+        const int t0 = c * DC, n = min(DC, kT - t0);
+        __syncthreads();   // the previous chunk is done with every LDS operand
+        // ---- stage: q, k, -B1 parts; decays (wave 0)
+        {
+            const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int i = tid + 256 * k, row = i >> 4, c4 = (i & 15) * 4;
+                const bool in = row < n;
+                const float4 q = in ? rq[k] : z, kk = in ? rk[k] : z;
+                put4<T>(&Qp[0][row][c4], (long long)DC * KL, q.x, q.y, q.z, q.w);
+                put4<T>(&Kp[0][row][c4], (long long)DC * KL, kk.x, kk.y, kk.z, kk.w);
+                put4<T>(&Bp[0][row][c4], (long long)DC * KL, -rb[k].x, -rb[k].y, -rb[k].z, -rb[k].w);
+            }
+            if (wave == 0) chunk_decays(lane < n ? ra : 1.0f, Gs, gs, lane);
+        }
+        // the previous chunk's outputs, now that the prefetched operands have arrived
+        if (ob_t0 >= 0) {
+            store_out();
+            ob_t0 = -1;
+        }
+        __syncthreads();
+        // ---- phase 1: Kd^T parts, P tile, U = A1V - B1 S_0 and Q S_0 tiles
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = tid + 256 * k, row = i >> 4, c4 = (i & 15) * 4;
+            const float gd = Gs[DC - 1][row];
+            const float4 kk = row < n ? rk[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            put1<T>(&KdT[0][c4 + 0][row], 64LL * TL, gd * kk.x);
+            put1<T>(&KdT[0][c4 + 1][row], 64LL * TL, gd * kk.y);
+            put1<T>(&KdT[0][c4 + 2][row], 64LL * TL, gd * kk.z);
+            put1<T>(&KdT[0][c4 + 3][row], 64LL * TL, gd * kk.w);
+        }
+        {
+            const int ti = wave >> 1, tj = wave & 1;
+            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (ti >= tj) {
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    V8 ap[P], bp[P];
+                    frag_parts<T>(&Qp[0][ti * 16 + r][ks * 32 + 8 * g], (long long)DC * KL, ap);
+                    frag_parts<T>(&Kp[0][tj * 16 + r][ks * 32 + 8 * g], (long long)DC * KL, bp);
+                    acc = mfma_split<T>(ap, bp, acc);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = ti * 16 + 4 * g + e, j = tj * 16 + r;
+                put1<T>(&Pp[0][i][j], (long long)DC * TL, j <= i ? Gs[i][j] * acc[e] : 0.0f);
+            }
+        }
+        f32x4 qs[UT];
+#pragma unroll
+        for (int j = 0; j < UT; ++j) {
+            const int u = wave + 4 * j, ti = u % 2, vt = u / 2;
+            f32x4 uu = f32x4{rv[j][0], rv[j][1], rv[j][2], rv[j][3]};
+            f32x4 x = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                V8 sf[P], bf[P], qf[P];
+                frag_parts<T>(&Sp[0][vt * 16 + r][ks * 32 + 8 * g], (long long)VS * KL, sf);
+                frag_parts<T>(&Bp[0][ti * 16 + r][ks * 32 + 8 * g], (long long)DC * KL, bf);
+                frag_parts<T>(&Qp[0][ti * 16 + r][ks * 32 + 8 * g], (long long)DC * KL, qf);
+                uu = mfma_split<T>(bf, sf, uu);
+                x = mfma_split<T>(qf, sf, x);
+            }
+            qs[j] = x;
+            put4<T>(&Up[0][vt * 16 + r][ti * 16 + 4 * g], (long long)VS * TL, uu[0], uu[1], uu[2], uu[3]);
+        }
+        __syncthreads();
+        if (c + 1 < DNC) fetch(c + 1);
+        // ---- phase 2: O = g Q S_0 + P U; S = g_31 S + Kd^T U
+#pragma unroll
+        for (int j = 0; j < UT; ++j) {
+            const int u = wave + 4 * j, ti = u % 2, vt = u / 2;
+            V8 uf[P], pf[P];
+            frag_parts<T>(&Up[0][vt * 16 + r][8 * g], (long long)VS * TL, uf);
+            frag_parts<T>(&Pp[0][ti * 16 + r][8 * g], (long long)DC * TL, pf);
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = gs[ti * 16 + 4 * g + e] * qs[j][e];
+            o = mfma_split<T>(pf, uf, o);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ob[j][e] = o[e];
+        }
+        const float g31 = gs[DC - 1];
+#pragma unroll
+        for (int j = 0; j < ST; ++j) {
+            const int sidx = wave + 4 * j, kt = sidx % 4, vt = sidx / 4;
+            V8 uf[P], kf[P];
+            frag_parts<T>(&Up[0][vt * 16 + r][8 * g], (long long)VS * TL, uf);
+            frag_parts<T>(&KdT[0][kt * 16 + r][8 * g], 64LL * TL, kf);
+            f32x4 sacc;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sacc[e] = g31 * Sacc[j][e];
+            sacc = mfma_split<T>(kf, uf, sacc);
+            Sacc[j] = sacc;
+            put4<T>(&Sp[0][vt * 16 + r][kt * 16 + 4 * g], (long long)VS * KL, sacc[0], sacc[1], sacc[2], sacc[3]);
+        }
+        ob_t0 = t0;
+    }
+    store_out();
+}
+
 // ------------------------------------------------------------------------------------------------ gated norm
 // 16 lanes per (row, head): lane l accumulates o[l + 16 z]^2 (z = 0..7), tree16, then ((o * rstd) * w) * silu(g)
 template <typename T>
@@ -721,6 +1091,25 @@ void launch_delta(const float* Q, const float* K, const float* V, const float* d
             hipLaunchKernelGGL((delta_split_kernel<2, false>), dim3(B * kHeads * 4), dim3(64), 0, s, Q, K, V, dec, beta, O);
     }
 }
+size_t delta_chunk_floats(int B) { return size_t(B) * kHeads * DNC * DCF; }
+template <typename T>
+void launch_delta_chunked(const float* Q, const float* K, const float* V, const float* dec, const float* beta,
+                          float* O, float* work, int B, hipStream_t s) {
+    if (!work) throw std::runtime_error("delta: the chunked scan needs its work buffer");
+    hipLaunchKernelGGL(delta_chunk_prep_kernel<T>, dim3(B * kHeads * DNC), dim3(64), 0, s, K, V, dec, beta, work);
+    // value blocks per head by batch (bitwise the same results for every split): small batches spread a head's
+    // state over more workgroups
+    if (B <= 16)
+        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 32>), dim3(B * kHeads * 4), dim3(256), 0, s, Q, K, dec, work, O);
+    else if (B <= 64)
+        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 64>), dim3(B * kHeads * 2), dim3(256), 0, s, Q, K, dec, work, O);
+    else
+        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 128>), dim3(B * kHeads), dim3(256), 0, s, Q, K, dec, work, O);
+}
+template void launch_delta_chunked<f16>(const float*, const float*, const float*, const float*, const float*, float*,
+                                        float*, int, hipStream_t);
+template void launch_delta_chunked<bf16>(const float*, const float*, const float*, const float*, const float*,
+                                         float*, float*, int, hipStream_t);
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,
                        long long pstride) {

@@ -1,0 +1,85 @@
+"""The gated delta rule of config 3 on its own, through the C-ABI entry point shv_hip_delta_rule, against the oracle's
+restatement of the CPU engine's recurrence (orc_delta_rule, engine/model/isa_impl.hpp:911-947; pinned to a float64
+recurrence and closed forms in tests/test_oracle.py).
+
+  fp32 (token by token, the reference's order) : bitwise equal to the oracle.
+  fp16 / bf16, token by token and chunked      : max |o - oracle| <= 1e-4 max |o| per (window, head) -- rounding
+                                                 only; a wrong decay, beta, key or chunk boundary moves o by O(1).
+Inputs follow config 3: q, k l2-normalised N(0,1) rows (q scaled by 1/8), v ~ N(0,1), beta = sigmoid(N(0,1)),
+decay = exp(-exp(A_log) softplus(N(0,1))) with A_log = ln U[1,16] per head; window 2 has strongly correlated keys
+(the worst conditioning for the chunked scan's (I + L)^-1).
+"""
+import numpy as np
+import pytest
+
+T, H = 321, 6
+
+
+def inputs(n_windows, seed):
+    rng = np.random.default_rng(seed)
+    rows = n_windows * T
+
+    def l2(x):
+        return (x / np.sqrt((x * x).sum(-1, keepdims=True) + 1e-6)).astype(np.float32)
+
+    q = l2(rng.standard_normal((rows, H, 64))) * np.float32(0.125)
+    kraw = rng.standard_normal((rows, H, 64))
+    if n_windows > 2:   # window 2: keys close to one direction per head
+        kraw[2 * T:3 * T] = 0.3 * kraw[2 * T:3 * T] + rng.standard_normal((1, H, 64)) * 3.0
+    k = l2(kraw)
+    v = rng.standard_normal((rows, H * 128)).astype(np.float32)
+    a_log = np.log(rng.uniform(1.0, 16.0, H))
+    sp = np.log1p(np.exp(rng.standard_normal((rows, H))))
+    dec = np.zeros((rows, 8), np.float32)
+    beta = np.zeros((rows, 8), np.float32)
+    dec[:, :H] = np.exp(-np.exp(a_log) * sp)
+    beta[:, :H] = 1.0 / (1.0 + np.exp(-rng.standard_normal((rows, H))))
+    return q.reshape(rows, H * 64), k.reshape(rows, H * 64), v, dec, beta
+
+
+def oracle_o(orc, weights, q, k, v, dec, beta, n_windows):
+    o = orc.Oracle(weights)
+    out = np.zeros((n_windows * T, H * 128), np.float32)
+    for w in range(n_windows):
+        rs = slice(w * T, (w + 1) * T)
+        for h in range(H):
+            out[rs, h * 128:(h + 1) * 128] = o.delta_rule(q[rs, h * 64:(h + 1) * 64], k[rs, h * 64:(h + 1) * 64],
+                                                          v[rs, h * 128:(h + 1) * 128], dec[rs, h], beta[rs, h])
+    o.close()
+    return out
+
+
+@pytest.mark.gpu
+def test_delta_rule_kernels_against_oracle(shv, orc, weights):
+    n = 3
+    q, k, v, dec, beta = inputs(n, 11)
+    ref = oracle_o(orc, weights, q, k, v, dec, beta, n)
+    hip = shv.Hip()
+    bufs = [hip.upload(x) for x in (q, k, v, dec, beta)]
+    d_o = hip.malloc(n * T * H * 128 * 4)
+    try:
+        for mode, variant in (("fp32", 0), ("fp16", 1), ("fp16", 2), ("bf16", 1), ("bf16", 2)):
+            print(f"[gpu] delta rule {mode} variant {variant}, {n} windows", flush=True)
+            hip.memset(d_o, 0xFF, n * T * H * 128 * 4)
+            shv.delta_rule(mode, *bufs, n, d_o, variant)
+            hip.sync()
+            got = hip.download(d_o, (n * T, H * 128), np.float32)
+            bad = ~np.isfinite(got)
+            if bad.any():
+                rr, cc = np.nonzero(bad)
+                print(f"[gpu]   non-finite: {bad.sum()} values, rows {rr.min()}..{rr.max()}, cols {cc.min()}..{cc.max()}",
+                      flush=True)
+            assert not bad.any()
+            if mode == "fp32":
+                assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+                continue
+            for w in range(n):
+                for h in range(H):
+                    g = got[w * T:(w + 1) * T, h * 128:(h + 1) * 128]
+                    r = ref[w * T:(w + 1) * T, h * 128:(h + 1) * 128]
+                    err = float(np.abs(g - r).max()) / float(np.abs(r).max())
+                    assert err <= 1e-4, (mode, variant, w, h, err)
+            print(f"[gpu]   max rel err {max(float(np.abs(got - ref).max() / np.abs(ref).max()), 0):.2e}", flush=True)
+    finally:
+        for p in bufs + [d_o]:
+            hip.free(p)

@@ -305,14 +305,52 @@ def test_row_independence_half(shv, weights, clips, mode):
 
 @pytest.mark.parametrize("mode", ["fp16"])
 def test_delta_splits_bitwise(shv, weights, clips, mode):
-    """The half-tier delta rule picks its key split from the batch (8 lane groups per value column up to 10 windows,
-    4 up to 21, 2 beyond, unrolled up to 42 windows and rolled past that); every split sums in one canonical order,
-    so batches of 16, 24 and 48 windows give each clip bitwise the logit it gets alone (1 window: 8 groups)."""
-    print(f"[gpu] {mode} delta splits: batches of 16 / 24 / 48 vs one by one", flush=True)
-    with shv.Model(weights, mode, experimental=True, max_frames=960, max_windows=48) as m:
-        single = np.concatenate([m.predict(clips[i:i + 1]) for i in range(48)])
-        for n in (16, 24, 48):
-            batch = m.predict(clips[:n])
+    """The half tiers split the delta rule by batch size: the chunked scan deals a head's 128 value columns over
+    4 / 2 / 1 workgroups (up to 16 / 64 / more windows) and the token-by-token kernel (SHV_HIP_DELTA_SEQ=1) splits each
+    value column's keys over 8 / 4 / 2 lane groups (up to 10 / 21 / more windows).  Every split computes each output
+    with the same operations in the same order, so batches of 16, 24, 48 and 72 windows give each clip bitwise the
+    logit it gets alone."""
+    print(f"[gpu] {mode} delta splits: batches of 16 / 24 / 48 / 72 vs one by one", flush=True)
+    batch72 = np.concatenate([clips[:64], clips[:8]])
+    with shv.Model(weights, mode, experimental=True, max_frames=1440, max_windows=72) as m:
+        single = np.concatenate([m.predict(clips[i:i + 1]) for i in range(64)])
+        single = np.concatenate([single, single[:8]])
+        for n in (16, 24, 48, 72):
+            batch = m.predict(batch72[:n])
             assert np.all(np.isfinite(batch))
             assert np.array_equal(batch.view(np.uint32), single[:n].view(np.uint32)), \
                 (n, float(np.abs(batch - single[:n]).max()))
+
+
+@pytest.mark.parametrize("mode", ["fp16", "bf16"])
+def test_delta_chunked_matches_sequential(shv, weights, clips, mode, monkeypatch):
+    """The half tiers' chunked delta-rule scan (32-token chunks, split-operand matrix cores) against the
+    token-by-token kernel (SHV_HIP_DELTA_SEQ=1) on the same tokens: the GDN stage outputs agree to accumulation
+    rounding -- 1e-4 of the stage's largest magnitude, where a wrong decay, beta, key or chunk boundary moves them
+    by O(1) -- and the logits of 8 windows within 1e-3."""
+    print(f"[gpu] {mode} chunked vs token-by-token delta rule", flush=True)
+    with shv.Model(weights, "fp32") as m:
+        toks = m.encode_frames(clips[:8].reshape(-1, 180, 320, 3)).reshape(8, 20, 16 * 384)
+    stages = ("after_gdn_a", "after_gdn_b", "after_sisa_last")
+    out = {}
+    for seq in (False, True):
+        if seq:
+            monkeypatch.setenv("SHV_HIP_DELTA_SEQ", "1")
+        else:
+            monkeypatch.delenv("SHV_HIP_DELTA_SEQ", raising=False)
+        with shv.Model(weights, mode, experimental=True, max_frames=160, max_windows=8) as m:
+            logits = m.classify(toks)
+            with tempfile.TemporaryDirectory() as d:
+                m.set_dump_dir(d)
+                m.classify(toks[:1])
+                dumps = {n: np.fromfile(Path(d) / f"{n}.f32", np.float32) for n in stages}
+        out[seq] = (logits, dumps)
+    for n in stages:
+        a, b = out[False][1][n], out[True][1][n]
+        assert np.all(np.isfinite(a)), n
+        err = float(np.abs(a - b).max()) / max(1e-30, float(np.abs(b).max()))
+        print(f"[gpu] {mode} {n}: max rel diff {err:.2e}", flush=True)
+        assert err <= 1e-4, (n, err)
+    la, lb = out[False][0], out[True][0]
+    print(f"[gpu] {mode} logits max|diff| {float(np.abs(la - lb).max()):.2e}", flush=True)
+    assert np.all(np.isfinite(la)) and float(np.abs(la - lb).max()) <= 1e-3
