@@ -513,14 +513,16 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
 //   O   = diag(g) Q S_0 + P U,       P_ij = G_ij (q_i . k_j) for j <= i, else 0,
 //   S_C = g_31 S_0 + Kd^T U,         Kd_j = G_31,j k_j.
 // Tokens past the window's end pad the last chunk with a = 1, b = 0, k = q = v = 0, which leaves every real
-// quantity unchanged.  delta_chunk_prep_kernel forms A1V and B1 of every chunk in parallel (nothing there depends on
-// the state); delta_chunk_scan_kernel walks the chunks of one (window, head) in order, the state's fp32 value in
-// MFMA accumulators and its split parts in LDS.  Every product runs on the split-operand matrix cores (fp32-level
+// quantity unchanged.  delta_chunk_prep_kernel forms every state-independent operand of every chunk in parallel
+// (A1V, B1, P, g, G_31,j); delta_chunk_scan_kernel walks the chunks of one (window, head) in order, the state's fp32
+// value in MFMA accumulators and its split parts in LDS.  Every product runs on the split-operand matrix cores (fp32-level
 // operand precision); T comes from forward substitution in fp32, the decay products from running products of a.
 // The results equal the token-by-token recurrence up to rounding (tested against it on the GPU).
 constexpr int DC = 32;                      // tokens per chunk
 constexpr int DNC = (kT + DC - 1) / DC;     // chunks per window
-constexpr int DCF = DC * 128 + DC * 64;     // floats per chunk in the prep buffer: A1V [32][128], then B1 [32][64]
+// floats per chunk in the prep buffer: A1V [32][128], B1 [32][64], P [32][32], g [32], G_31,j [32]
+constexpr int DCO_B1 = DC * 128, DCO_P = DCO_B1 + DC * 64, DCO_G = DCO_P + DC * DC, DCO_GD = DCO_G + DC;
+constexpr int DCF = DCO_GD + DC;
 
 // 8 fp32 values (two float4 in LDS) -> the P split-part fragments
 template <typename T>
@@ -573,8 +575,8 @@ __device__ __forceinline__ void chunk_decays(float ai, float (*Gs)[DC + 1], floa
 // One wave per (window, head, chunk): A1V and B1 into CH [window][head][chunk][DCF].
 template <typename T>
 __global__ void __launch_bounds__(64)
-delta_chunk_prep_kernel(const float* __restrict__ K, const float* __restrict__ V, const float* __restrict__ dec,
-                        const float* __restrict__ beta, float* __restrict__ CH) {
+delta_chunk_prep_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+                        const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ CH) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     constexpr int P = S::P;
@@ -584,17 +586,19 @@ delta_chunk_prep_kernel(const float* __restrict__ K, const float* __restrict__ V
     const int t0 = c * DC, n = min(DC, kT - t0);
     const long long row0 = (long long)b * kT + t0;
     __shared__ __attribute__((aligned(16))) float Ks[DC][64 + 4];
+    __shared__ __attribute__((aligned(16))) float Qs[DC][64 + 4];
     __shared__ __attribute__((aligned(16))) float Vs[DC][128 + 4];
     __shared__ __attribute__((aligned(16))) float Ls[DC][DC + 4];
     __shared__ __attribute__((aligned(16))) float Ts[DC][DC + 4];
     __shared__ float Gs[DC][DC + 1];
     __shared__ float bs[DC], gs[DC];
     {   // stage (loads at clamped rows, all in flight together; zero / a = 1 past the window's end)
-        float4 kv[8], vv[16];
+        float4 kv[8], qv[8], vv[16];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int i = lane + 64 * k, row = i >> 4, c4 = (i & 15) * 4;
             kv[k] = *reinterpret_cast<const float4*>(K + (row0 + min(row, n - 1)) * kD + h * 64 + c4);
+            qv[k] = *reinterpret_cast<const float4*>(Q + (row0 + min(row, n - 1)) * kD + h * 64 + c4);
         }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -611,6 +615,7 @@ delta_chunk_prep_kernel(const float* __restrict__ K, const float* __restrict__ V
         for (int k = 0; k < 8; ++k) {
             const int i = lane + 64 * k, row = i >> 4, c4 = (i & 15) * 4;
             *reinterpret_cast<float4*>(&Ks[row][c4]) = row < n ? kv[k] : z;
+            *reinterpret_cast<float4*>(&Qs[row][c4]) = row < n ? qv[k] : z;
         }
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -621,25 +626,34 @@ delta_chunk_prep_kernel(const float* __restrict__ K, const float* __restrict__ V
         chunk_decays(lane < n ? av : 1.0f, Gs, gs, lane);
     }
     __syncthreads();
-    // L = b_i G_ij (k_i . k_j) for j < i: tiles (ti, tj) of K K^T, keys in two K steps; tile (0, 1) is all zero
+    // L = b_i G_ij (k_i . k_j) for j < i and P = G_ij (q_i . k_j) for j <= i: tiles (ti, tj) of K K^T and Q K^T,
+    // keys in two K steps; tile (0, 1) of both is all zero
+    float* out = CH + ((long long)wh * DNC + c) * DCF;
 #pragma unroll
     for (int tile = 0; tile < 4; ++tile) {
         const int ti = tile >> 1, tj = tile & 1;
-        f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 kk = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, qk = kk;
         if (ti >= tj) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                V8 ap[P], bp[P];
+                V8 ap[P], qp[P], bp[P];
                 frag_lds<T>(&Ks[ti * 16 + r][ks * 32 + 8 * g], ap);
+                frag_lds<T>(&Qs[ti * 16 + r][ks * 32 + 8 * g], qp);
                 frag_lds<T>(&Ks[tj * 16 + r][ks * 32 + 8 * g], bp);
-                acc = mfma_split<T>(ap, bp, acc);
+                kk = mfma_split<T>(ap, bp, kk);
+                qk = mfma_split<T>(qp, bp, qk);
             }
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = ti * 16 + 4 * g + e, j = tj * 16 + r;
-            Ls[i][j] = j < i ? bs[i] * (Gs[i][j] * acc[e]) : 0.0f;
+            Ls[i][j] = j < i ? bs[i] * (Gs[i][j] * kk[e]) : 0.0f;
+            out[DCO_P + i * DC + j] = j <= i ? Gs[i][j] * qk[e] : 0.0f;
         }
+    }
+    if (lane < DC) {
+        out[DCO_G + lane] = gs[lane];
+        out[DCO_GD + lane] = Gs[DC - 1][lane];
     }
     __syncthreads();
     // T = (I + L)^-1: lane j solves column j, t_i = [i == j] - sum_{m < i} L_im t_m (fma chain over m in order)
@@ -663,7 +677,6 @@ delta_chunk_prep_kernel(const float* __restrict__ K, const float* __restrict__ V
     }
     __syncthreads();
     // A1V = T diag(b) V (32 x 128) and B1 = T diag(b g) K (32 x 64): one K step over the chunk's 32 tokens
-    float* out = CH + ((long long)wh * DNC + c) * DCF;
 #pragma unroll
     for (int ti = 0; ti < 2; ++ti) {
         V8 ap[P];
@@ -688,23 +701,28 @@ delta_chunk_prep_kernel(const float* __restrict__ K, const float* __restrict__ V
             split8<T>(y, bp);
             const f32x4 acc = mfma_split<T>(ap, bp, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
-            for (int e = 0; e < 4; ++e) out[DC * 128 + (ti * 16 + 4 * g + e) * 64 + tk * 16 + r] = acc[e];
+            for (int e = 0; e < 4; ++e) out[DCO_B1 + (ti * 16 + 4 * g + e) * 64 + tk * 16 + r] = acc[e];
         }
     }
 }
 
 // One workgroup (4 waves) per (window, head, block of VS value columns), the chunks in order.  Value columns are
-// independent in every product below, so VS = 32, 64 or 128 splits a head over 4, 2 or 1 workgroups with every
-// output computed by the same fragments in the same order (bitwise equal for every VS).  Tiles: U / Q S_0 / O
+// independent in every product below, so VS = 32 or 64 splits a head over 4 or 2 workgroups with every output
+// computed by the same fragments in the same order (bitwise equal for every VS).  Tiles: U / Q S_0 / O
 // [token tile 0..1][value tile] as u = wave + 4 j (ti = u % 2, vt = u / 2), state S[key tile][value tile] as
-// s = wave + 4 j (kt = s % 4, vt = s / 4), P tile (wave / 2, wave % 2).  Per chunk: stage Q, K, -B1 parts (and the
-// decays) / barrier / P, U = A1V - B1 S_0, Q S_0, Kd^T parts / barrier / O = g Q S_0 + P U, S = g_31 S + Kd^T U
-// (state parts rewritten).  A chunk's outputs are stored at the start of the next chunk, after the wait for its
-// prefetched operands (one vmcnt counter retires loads and stores in order).
+// s = wave + 4 j (kt = s % 4, vt = s / 4).  Per chunk: stage Q, -B1, P, Kd^T parts and g from registers / barrier /
+// U = A1V - B1 S_0 and Q S_0 / barrier / O = g Q S_0 + P U, S = g_31 S + Kd^T U (state parts rewritten).  A chunk's
+// operands are loaded two chunks ahead (two register sets, the chunk loop unrolled by two), and its outputs are
+// stored after the next chunk's staging: one vmcnt counter retires loads and stores in order.
+template <int UT>
+struct DChunkRegs {   // one chunk's operands as a thread loads them
+    float4 q[2], k[2], b1[2], p;
+    float gd[2], g, a1v[UT][4];
+};
 template <typename T, int VS>
 __global__ void __launch_bounds__(256)
-delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ dec,
-                        const float* __restrict__ CH, float* __restrict__ O) {
+delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ CH,
+                        float* __restrict__ O) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     constexpr int P = S::P;
@@ -713,12 +731,10 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
     constexpr int KL = 64 + 8, TL = DC + 8;   // element strides of key-major and token-major part rows
     __shared__ __attribute__((aligned(16))) T Sp[P][VS][KL];    // state [value][key]
     __shared__ __attribute__((aligned(16))) T Qp[P][DC][KL];    // q [token][key]
-    __shared__ __attribute__((aligned(16))) T Kp[P][DC][KL];    // k [token][key]
     __shared__ __attribute__((aligned(16))) T Bp[P][DC][KL];    // -B1 [token][key]
     __shared__ __attribute__((aligned(16))) T KdT[P][64][TL];   // Kd^T [key][token]
     __shared__ __attribute__((aligned(16))) T Pp[P][DC][TL];    // P [token i][token j]
     __shared__ __attribute__((aligned(16))) T Up[P][VS][TL];    // U [value][token]
-    __shared__ float Gs[DC][DC + 1];
     __shared__ float gs[DC];
     const int vb = blockIdx.x % NB, wh = blockIdx.x / NB, b = wh / kHeads, h = wh % kHeads;
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
@@ -728,27 +744,27 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
     const float* chb = CH + (long long)wh * DNC * DCF;
     for (int i = tid; i < P * VS * KL; i += 256) (&Sp[0][0][0])[i] = T(0.0f);
 
-    // prefetched operands of a chunk: q, k, b1 rows (2 float4 each), this wave's A1V values, the decay
-    float4 rq[2], rk[2], rb[2];
-    float ra = 1.0f, rv[UT][4];
-    auto fetch = [&](int c) {
+    auto fetch = [&](DChunkRegs<UT>& F, int c) {   // loads at clamped rows; rows past the end are zeroed when staged
         const int t0 = c * DC, n = min(DC, kT - t0);
+        const float* cc = chb + (long long)c * DCF;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int i = tid + 256 * k, row = i >> 4, c4 = (i & 15) * 4;
             const long long gr = rowb + t0 + min(row, n - 1);
-            rq[k] = *reinterpret_cast<const float4*>(Q + gr * kD + h * 64 + c4);
-            rk[k] = *reinterpret_cast<const float4*>(K + gr * kD + h * 64 + c4);
-            rb[k] = *reinterpret_cast<const float4*>(chb + (long long)c * DCF + DC * 128 + row * 64 + c4);
+            F.q[k] = *reinterpret_cast<const float4*>(Q + gr * kD + h * 64 + c4);
+            F.k[k] = *reinterpret_cast<const float4*>(K + gr * kD + h * 64 + c4);
+            F.b1[k] = *reinterpret_cast<const float4*>(cc + DCO_B1 + row * 64 + c4);
+            F.gd[k] = cc[DCO_GD + row];
         }
+        F.p = *reinterpret_cast<const float4*>(cc + DCO_P + tid * 4);
+        F.g = cc[DCO_G + (tid & (DC - 1))];
 #pragma unroll
         for (int j = 0; j < UT; ++j) {
             const int u = wave + 4 * j, ti = u % 2, vt = u / 2;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                rv[j][e] = chb[(long long)c * DCF + (ti * 16 + 4 * g + e) * 128 + vb * VS + vt * 16 + r];
+                F.a1v[j][e] = cc[(ti * 16 + 4 * g + e) * 128 + vb * VS + vt * 16 + r];
         }
-        if (tid < DC) ra = dec[(rowb + t0 + min(tid, n - 1)) * 8 + h];
     };
     f32x4 Sacc[ST];
 #pragma unroll
@@ -766,64 +782,47 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
             }
         }
     };
-    fetch(0);
-    for (int c = 0; c < DNC; ++c) {
+    auto chunk = [&](int c, DChunkRegs<UT>& F) {
         const int t0 = c * DC, n = min(DC, kT - t0);
         __syncthreads();   // the previous chunk is done with every LDS operand
-        // ---- stage: q, k, -B1 parts; decays (wave 0)
+        // ---- stage: q, -B1, P, Kd^T parts and g
+        float av[UT][4];
         {
             const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 const int i = tid + 256 * k, row = i >> 4, c4 = (i & 15) * 4;
                 const bool in = row < n;
-                const float4 q = in ? rq[k] : z, kk = in ? rk[k] : z;
+                const float4 q = in ? F.q[k] : z, kk = in ? F.k[k] : z;
                 put4<T>(&Qp[0][row][c4], (long long)DC * KL, q.x, q.y, q.z, q.w);
-                put4<T>(&Kp[0][row][c4], (long long)DC * KL, kk.x, kk.y, kk.z, kk.w);
-                put4<T>(&Bp[0][row][c4], (long long)DC * KL, -rb[k].x, -rb[k].y, -rb[k].z, -rb[k].w);
+                put4<T>(&Bp[0][row][c4], (long long)DC * KL, -F.b1[k].x, -F.b1[k].y, -F.b1[k].z, -F.b1[k].w);
+                const float gd = F.gd[k];
+                put1<T>(&KdT[0][c4 + 0][row], 64LL * TL, gd * kk.x);
+                put1<T>(&KdT[0][c4 + 1][row], 64LL * TL, gd * kk.y);
+                put1<T>(&KdT[0][c4 + 2][row], 64LL * TL, gd * kk.z);
+                put1<T>(&KdT[0][c4 + 3][row], 64LL * TL, gd * kk.w);
             }
-            if (wave == 0) chunk_decays(lane < n ? ra : 1.0f, Gs, gs, lane);
+            put4<T>(&Pp[0][tid >> 3][(tid & 7) * 4], (long long)DC * TL, F.p.x, F.p.y, F.p.z, F.p.w);
+            if (tid < DC) gs[tid] = F.g;
+#pragma unroll
+            for (int j = 0; j < UT; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) av[j][e] = F.a1v[j][e];
         }
-        // the previous chunk's outputs, now that the prefetched operands have arrived
+        // the previous chunk's outputs, now that this chunk's operands have arrived; then the registers take the
+        // chunk after next
         if (ob_t0 >= 0) {
             store_out();
             ob_t0 = -1;
         }
+        if (c + 2 < DNC) fetch(F, c + 2);
         __syncthreads();
-        // ---- phase 1: Kd^T parts, P tile, U = A1V - B1 S_0 and Q S_0 tiles
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int i = tid + 256 * k, row = i >> 4, c4 = (i & 15) * 4;
-            const float gd = Gs[DC - 1][row];
-            const float4 kk = row < n ? rk[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            put1<T>(&KdT[0][c4 + 0][row], 64LL * TL, gd * kk.x);
-            put1<T>(&KdT[0][c4 + 1][row], 64LL * TL, gd * kk.y);
-            put1<T>(&KdT[0][c4 + 2][row], 64LL * TL, gd * kk.z);
-            put1<T>(&KdT[0][c4 + 3][row], 64LL * TL, gd * kk.w);
-        }
-        {
-            const int ti = wave >> 1, tj = wave & 1;
-            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (ti >= tj) {
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    V8 ap[P], bp[P];
-                    frag_parts<T>(&Qp[0][ti * 16 + r][ks * 32 + 8 * g], (long long)DC * KL, ap);
-                    frag_parts<T>(&Kp[0][tj * 16 + r][ks * 32 + 8 * g], (long long)DC * KL, bp);
-                    acc = mfma_split<T>(ap, bp, acc);
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = ti * 16 + 4 * g + e, j = tj * 16 + r;
-                put1<T>(&Pp[0][i][j], (long long)DC * TL, j <= i ? Gs[i][j] * acc[e] : 0.0f);
-            }
-        }
+        // ---- phase 1: U = A1V - B1 S_0 and Q S_0
         f32x4 qs[UT];
 #pragma unroll
         for (int j = 0; j < UT; ++j) {
             const int u = wave + 4 * j, ti = u % 2, vt = u / 2;
-            f32x4 uu = f32x4{rv[j][0], rv[j][1], rv[j][2], rv[j][3]};
+            f32x4 uu = f32x4{av[j][0], av[j][1], av[j][2], av[j][3]};
             f32x4 x = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
@@ -838,7 +837,6 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
             put4<T>(&Up[0][vt * 16 + r][ti * 16 + 4 * g], (long long)VS * TL, uu[0], uu[1], uu[2], uu[3]);
         }
         __syncthreads();
-        if (c + 1 < DNC) fetch(c + 1);
         // ---- phase 2: O = g Q S_0 + P U; S = g_31 S + Kd^T U
 #pragma unroll
         for (int j = 0; j < UT; ++j) {
@@ -868,6 +866,13 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
             put4<T>(&Sp[0][vt * 16 + r][kt * 16 + 4 * g], (long long)VS * KL, sacc[0], sacc[1], sacc[2], sacc[3]);
         }
         ob_t0 = t0;
+    };
+    DChunkRegs<UT> F0, F1;
+    fetch(F0, 0);
+    fetch(F1, 1);
+    for (int c = 0; c < DNC; c += 2) {
+        chunk(c, F0);
+        if (c + 1 < DNC) chunk(c + 1, F1);
     }
     store_out();
 }
@@ -1096,15 +1101,13 @@ template <typename T>
 void launch_delta_chunked(const float* Q, const float* K, const float* V, const float* dec, const float* beta,
                           float* O, float* work, int B, hipStream_t s) {
     if (!work) throw std::runtime_error("delta: the chunked scan needs its work buffer");
-    hipLaunchKernelGGL(delta_chunk_prep_kernel<T>, dim3(B * kHeads * DNC), dim3(64), 0, s, K, V, dec, beta, work);
+    hipLaunchKernelGGL(delta_chunk_prep_kernel<T>, dim3(B * kHeads * DNC), dim3(64), 0, s, Q, K, V, dec, beta, work);
     // value blocks per head by batch (bitwise the same results for every split): small batches spread a head's
     // state over more workgroups
     if (B <= 16)
-        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 32>), dim3(B * kHeads * 4), dim3(256), 0, s, Q, K, dec, work, O);
-    else if (B <= 64)
-        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 64>), dim3(B * kHeads * 2), dim3(256), 0, s, Q, K, dec, work, O);
+        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 32>), dim3(B * kHeads * 4), dim3(256), 0, s, Q, K, work, O);
     else
-        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 128>), dim3(B * kHeads), dim3(256), 0, s, Q, K, dec, work, O);
+        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 64>), dim3(B * kHeads * 2), dim3(256), 0, s, Q, K, work, O);
 }
 template void launch_delta_chunked<f16>(const float*, const float*, const float*, const float*, const float*, float*,
                                         float*, int, hipStream_t);
