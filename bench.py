@@ -173,6 +173,52 @@ def async_bf16(shv, weights: Path, clips: np.ndarray, n_clips: int = 1024, per_j
     return out
 
 
+def crop_bench(shv, hip, stream, model, clips_n: int, d_logits: int, iters: int = 5) -> dict:
+    """Face crops on the GPU (shv_hip_native_crops_rgb): clips_n x 20 crops (a batch's worth) from 20 distinct
+    1920x1080 native frames resident in HBM (INTER_AREA canvas shrink, then the 320x180 crop), rects of the
+    reference's crop_geometry family (crop height 101 -> 180x101 letterbox units); wall clock per call (the entry
+    point returns when the crops are written).  Then the device-only pipeline: crops straight into the model's
+    input layout + the forward (frames -> logits).  Beside it, the reference CPU crop (oracle/_ref,
+    shv_native_crop_rgb) on one host core over a bounded sample."""
+    rng = np.random.default_rng(7)
+    W, H, n = 1920, 1080, clips_n * 20
+    frames = [hip.upload(rng.integers(0, 256, (H, W, 3), dtype=np.uint8)) for _ in range(20)]
+    rects = [(int(rng.integers(0, 320 - 180 + 1)), int(rng.integers(0, 180 - 101 + 1)), 180, 101) for _ in range(n)]
+    fr = [(frames[i % 20], W, H, 3 * W) for i in range(n)]
+    d_crops = hip.malloc(n * shv.FRAME_BYTES)
+    shv.native_crops_rgb(fr, rects, d_crops, stream)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        shv.native_crops_rgb(fr, rects, d_crops, stream)
+    crop_s = (time.perf_counter() - t0) / iters
+    model.forward_device(d_crops, clips_n, d_logits, stream)
+    hip.stream_sync(stream)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        shv.native_crops_rgb(fr, rects, d_crops, stream)
+        model.forward_device(d_crops, clips_n, d_logits, stream)
+    hip.stream_sync(stream)
+    pipe_s = (time.perf_counter() - t0) / iters
+    out = {"crops": n, "native": f"{W}x{H}", "rect": "180x101", "ms_per_call": round(crop_s * 1000, 3),
+           "crops_per_s": round(n / crop_s, 1), "pipeline_ms_per_batch": round(pipe_s * 1000, 3),
+           "pipeline_clips_per_s": round(clips_n / pipe_s, 1)}
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    if oracle.PREP_SO.exists():
+        ref = oracle.PrepRef()
+        host = [rng.integers(0, 256, (H, W, 3), dtype=np.uint8) for _ in range(4)]
+        k, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 2.0:
+            ref.native_crop(host[k % 4], rects[k])
+            k += 1
+        out["cpu_reference_crops_per_s_1core"] = round(k / (time.perf_counter() - t0), 1)
+    log(f"[bench] crops: {out}")
+    for f in frames:
+        hip.free(f)
+    hip.free(d_crops)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -187,6 +233,7 @@ def main() -> int:
     ap.add_argument("--copy-mb", type=int, default=0)
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-async", action="store_true")
+    ap.add_argument("--no-crop", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the SHIELD-V forward has no cross-GPU step "
@@ -270,6 +317,7 @@ def main() -> int:
             hip.free(dst)
 
         gemm = None if args.kernel_only or args.no_gemm else gemm_microbench(shv, hip, stream, e0, e1)
+        crops = None if args.kernel_only or args.no_crop else crop_bench(shv, hip, stream, model, B, d_logits)
 
         enc_ms = None
         if not args.kernel_only:   # encoder only (config 1: 2560 frames)
@@ -343,6 +391,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "device_copy": copy,
         "gemm_microbench": gemm,
+        "face_crops": crops,
         "revision": revision,
     }
     print(json.dumps(line), flush=True)

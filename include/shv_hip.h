@@ -150,6 +150,22 @@ int shv_hip_gemm_run(shv_hip_gemm* g, const float* d_a, long long m, const float
                      int variant, void* stream);
 void shv_hip_gemm_free(shv_hip_gemm* g);
 
+/* Face crops on the GPU: the reference's lazy native crop (engine/include/shv_prep.h:181-186, shv_native_crop_rgb;
+ * engine/preprocess/canvas.cpp:66-91) for n frames at once, frames and crops in DEVICE memory.  Crop i =
+ * cv2.resize(canvas_i[4y:4(y+h), 4x:4(x+w)], (320,180), INTER_AREA) with canvas_i the frame letterboxed into
+ * 1280x720 (INTER_AREA when shrinking, INTER_LINEAR when enlarging, bars zero), byte-exact to the reference;
+ * written to d_out + i * SHV_HIP_FRAME_BYTES, i.e. the crop layout shv_hip_forward_device reads.  Rects must lie in
+ * the 320x180 letterbox with w >= 80, h >= 45 (the reference's crop_geometry gives h in [80,180], w = round(16h/9)).
+ * Synchronous on `stream`; one call at a time per process.  Returns 0, or -1 + last_error. */
+typedef struct {
+    const uint8_t* data;   /* device pointer */
+    int width, height;
+    ptrdiff_t stride;      /* bytes per row */
+} shv_hip_rgb_image;       /* shv_rgb_image, shv_prep.h:74-78 */
+typedef struct { int x, y, w, h; } shv_hip_rect;   /* shv_rect, shv_prep.h:86 */
+int shv_hip_native_crops_rgb(const shv_hip_rgb_image* frames, const shv_hip_rect* rects, int n, uint8_t* d_out,
+                             void* stream);
+
 /* Gated delta rule of one tier on device buffers (the scan of config 3 on its own; no counterpart in shv_cuda.h --
  * the reference runs its delta_kernel only inside classify, engine/cuda/seq.cu:106-195).  Per window 321 rows; rows
  * = n_windows * 321: q, k [rows][384] (6 heads x 64, l2-normalised; q scaled), v, o [rows][768] (6 heads x 128),

@@ -1,5 +1,6 @@
-"""TEST INFRASTRUCTURE ONLY.  ctypes access to the oracle (this repo's C restatement, oracle/_build) and to the
-reference CPU engine compiled from /root/reference (oracle/_ref).  Only tests/, __graft_entry__.smoke() and
+"""TEST INFRASTRUCTURE ONLY.  ctypes access to the oracle (this repo's C restatement, oracle/_build), to the
+reference CPU engine compiled from /root/reference (oracle/_ref) and to the reference preprocessing's crop path
+compiled from the same tree (oracle/_ref/libshield_v_prep_crop.so).  Only tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg may use this module, and only as the checker / the timed CPU baseline.
 """
 from __future__ import annotations
@@ -14,6 +15,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 ORACLE_SO = HERE / "_build" / "libshv_oracle.so"
 REF_SO = HERE / "_ref" / "libshield_v_cpu.so"
+PREP_SO = HERE / "_ref" / "libshield_v_prep_crop.so"
 FRAME_BYTES = 172800
 
 DUMP_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), ctypes.c_size_t)
@@ -171,3 +173,36 @@ class Reference:
         if self.h:
             self.lib.shv_cpu_free(self.h)
             self.h = None
+
+
+class _RgbImage(ctypes.Structure):   # shv_rgb_image (engine/include/shv_prep.h:74-78)
+    _fields_ = [("data", ctypes.c_void_p), ("width", ctypes.c_int), ("height", ctypes.c_int),
+                ("stride", ctypes.c_ssize_t)]
+
+
+class _Rect(ctypes.Structure):       # shv_rect (shv_prep.h:86)
+    _fields_ = [("x", ctypes.c_int), ("y", ctypes.c_int), ("w", ctypes.c_int), ("h", ctypes.c_int)]
+
+
+class PrepRef:
+    """The reference's lazy native crop, shv_native_crop_rgb (engine/preprocess/canvas.cpp:134-143), compiled from
+    its own sources by `make -C oracle ref`: the checker of the GPU crops."""
+
+    def __init__(self):
+        if not PREP_SO.exists():
+            raise RuntimeError(f"{PREP_SO} not built (make -C oracle ref needs /root/reference)")
+        lib = ctypes.CDLL(str(PREP_SO))
+        lib.shv_native_crop_rgb.restype = ctypes.c_int
+        lib.shv_native_crop_rgb.argtypes = [ctypes.POINTER(_RgbImage), _Rect, ctypes.c_void_p]
+        lib.shv_canvas_info_get.restype = ctypes.c_int
+        lib.shv_prep_last_error.restype = ctypes.c_char_p
+        self.lib = lib
+
+    def native_crop(self, frame: np.ndarray, rect) -> np.ndarray:
+        frame = np.ascontiguousarray(frame, np.uint8)
+        h, w = frame.shape[:2]
+        img = _RgbImage(frame.ctypes.data, w, h, w * 3)
+        out = np.empty((180, 320, 3), np.uint8)
+        if self.lib.shv_native_crop_rgb(ctypes.byref(img), _Rect(*[int(v) for v in rect]), out.ctypes.data) != 0:
+            raise RuntimeError(self.lib.shv_prep_last_error().decode())
+        return out

@@ -28,7 +28,7 @@ INCLUDE = PKG.parent / "include"
 NUMERIC_SOURCES = ["dev_common.hpp", "mfma.hpp", "kernels.hpp", "gemm.hip", "cnn.hip", "fused.hip", "strip.hip", "seq.hip",
                    "engine.hpp", "engine.hip",
                    "host_model.hpp", "host_model.cpp"]
-DEVICE_SOURCES = ["gemm.hip", "cnn.hip", "fused.hip", "strip.hip", "seq.hip", "engine.hip"]
+DEVICE_SOURCES = ["gemm.hip", "cnn.hip", "fused.hip", "strip.hip", "seq.hip", "engine.hip", "crop.hip"]
 HOST_SOURCES = ["host_model.cpp"]
 C_SOURCES = ["sha256.c"]
 

@@ -804,6 +804,22 @@ int shv_hip_gemm_run(shv_hip_gemm* g, const float* d_a, long long m, const float
 }
 void shv_hip_gemm_free(shv_hip_gemm* g) { delete g; }
 
+// Face crops on the GPU (shv_prep.h:181-186 on device frames).
+int shv_hip_native_crops_rgb(const shv_hip_rgb_image* frames, const shv_hip_rect* rects, int n, uint8_t* d_out,
+                             void* stream) {
+    return guarded([&] {
+        if (n < 0 || (n > 0 && (!frames || !rects || !d_out))) throw std::runtime_error("invalid argument");
+        std::vector<shv::CropJob> jobs(static_cast<size_t>(n));
+        for (int i = 0; i < n; ++i) {
+            const shv_hip_rgb_image& f = frames[i];
+            const shv_hip_rect& r = rects[i];
+            jobs[size_t(i)] = shv::CropJob{f.data, f.width, f.height, (long long)f.stride, r.x, r.y, r.w, r.h};
+        }
+        shv::native_crops_rgb(jobs.data(), n, d_out, static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
 // Gated delta rule microbench / parity entry (config 3's scan on its own).
 int shv_hip_delta_rule(const char* mode, const float* d_q, const float* d_k, const float* d_v, const float* d_decay,
                        const float* d_beta, int n_windows, float* d_o, int variant, void* stream) {

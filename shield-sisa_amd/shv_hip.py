@@ -74,6 +74,7 @@ _SIGS = {
     "shv_hip_gemm_run": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P, ctypes.c_int, _P, ctypes.c_int, _P]),
     "shv_hip_gemm_free": (None, [_P]),
     "shv_hip_delta_rule": (ctypes.c_int, [ctypes.c_char_p, _P, _P, _P, _P, _P, ctypes.c_int, _P, ctypes.c_int, _P]),
+    "shv_hip_native_crops_rgb": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
 }
 
 _libs: dict[str, ctypes.CDLL] = {}
@@ -427,6 +428,26 @@ class PwGemm:
 
     def __exit__(self, *exc):
         self.close()
+
+
+class RgbImage(ctypes.Structure):   # shv_hip_rgb_image (a device frame)
+    _fields_ = [("data", ctypes.c_void_p), ("width", ctypes.c_int), ("height", ctypes.c_int),
+                ("stride", ctypes.c_ssize_t)]
+
+
+class Rect(ctypes.Structure):       # shv_hip_rect
+    _fields_ = [("x", ctypes.c_int), ("y", ctypes.c_int), ("w", ctypes.c_int), ("h", ctypes.c_int)]
+
+
+def native_crops_rgb(frames, rects, d_out: int, stream: int | None = None) -> None:
+    """frames: [(device pointer, width, height, stride)], rects: [(x, y, w, h)] -> len(rects) crops at d_out."""
+    n = len(rects)
+    fa = (RgbImage * max(1, n))(*[RgbImage(*f) for f in frames])
+    ra = (Rect * max(1, n))(*[Rect(*[int(v) for v in r]) for r in rects])
+    lib = library()
+    if lib.shv_hip_native_crops_rgb(ctypes.cast(fa, ctypes.c_void_p), ctypes.cast(ra, ctypes.c_void_p), n, d_out,
+                                    stream) != 0:
+        raise ShvError(last_error())
 
 
 def delta_rule(mode: str, d_q: int, d_k: int, d_v: int, d_decay: int, d_beta: int, n_windows: int, d_o: int,
