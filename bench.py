@@ -209,7 +209,7 @@ def crop_bench(shv, hip, stream, model, clips_n: int, d_logits: int, iters: int 
         host = [rng.integers(0, 256, (H, W, 3), dtype=np.uint8) for _ in range(4)]
         k, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < 2.0:
-            ref.native_crop(host[k % 4], rects[k])
+            ref.native_crop(host[k % 4], rects[k % n])
             k += 1
         out["cpu_reference_crops_per_s_1core"] = round(k / (time.perf_counter() - t0), 1)
     log(f"[bench] crops: {out}")

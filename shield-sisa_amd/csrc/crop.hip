@@ -66,53 +66,89 @@ __device__ __forceinline__ int sat_u8(float v) {
 }
 __device__ __forceinline__ int clip_row(int y, int n) { return y >= 0 ? (y < n ? y : n - 1) : 0; }
 
-// output byte (dx, dy, c) of plan p over a source read as src(x, y, c)
+// output pixel (dx, dy), all channels c = 0..2, of plan p over a source read as src(x, y, c); the channels are
+// independent, each computed with the reference's per-byte operations (taps read once per pixel)
 template <class Src>
-__device__ __forceinline__ int resize_px(const PlanDev& p, const Src& src, int dx, int dy, int c) {
+__device__ __forceinline__ void resize_px3(const PlanDev& p, const Src& src, int dx, int dy, int (&o)[3]) {
     switch (p.kind) {
-    case 0: return src(dx, dy, c);
+    case 0:
+#pragma unroll
+        for (int c = 0; c < 3; ++c) o[c] = src(dx, dy, c);
+        return;
     case 1: {
         const int ya = p.yfirst[dy], ye = p.yfirst[dy + 1], xa = p.xfirst[dx], xe = p.xfirst[dx + 1];
-        float sum = 0.0f;
+        float sum[3] = {0.0f, 0.0f, 0.0f};
         for (int j = ya; j < ye; ++j) {
             const int sy = p.ysi[j];
-            float t = 0.0f;
-            for (int k = xa; k < xe; ++k) t = t + float(src(p.xsi[k], sy, c)) * p.xal[k];
-            const float bt = p.yal[j] * t;
-            sum = j == ya ? bt : sum + bt;
+            const float beta = p.yal[j];
+            float t[3] = {0.0f, 0.0f, 0.0f};
+            for (int k = xa; k < xe; ++k) {
+                const int sx = p.xsi[k];
+                const float al = p.xal[k];
+#pragma unroll
+                for (int c = 0; c < 3; ++c) t[c] = t[c] + float(src(sx, sy, c)) * al;
+            }
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const float bt = beta * t[c];
+                sum[c] = j == ya ? bt : sum[c] + bt;
+            }
         }
-        return sat_u8(sum);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) o[c] = sat_u8(sum[c]);
+        return;
     }
     case 2: {
         const int sx0 = dx * p.ix, sy0 = dy * p.iy;
-        if (sy0 >= p.sh) return 0;
-        if (sy0 + p.iy <= p.sh && dx < p.sw / p.ix) {   // a full block
-            if (p.ix == 2 && p.iy == 2)
-                return (src(sx0, sy0, c) + src(sx0 + 1, sy0, c) + src(sx0, sy0 + 1, c) + src(sx0 + 1, sy0 + 1, c) + 2) >> 2;
-            int s = 0;
-            for (int r = 0; r < p.iy; ++r)
-                for (int q = 0; q < p.ix; ++q) s += src(sx0 + q, sy0 + r, c);
-            return sat_u8(float(s) * p.fscale);
+        if (sy0 >= p.sh) {
+            o[0] = o[1] = o[2] = 0;
+            return;
         }
-        if (sx0 >= p.sw) return 0;
+        if (sy0 + p.iy <= p.sh && dx < p.sw / p.ix) {   // a full block
+            if (p.ix == 2 && p.iy == 2) {
+#pragma unroll
+                for (int c = 0; c < 3; ++c)
+                    o[c] = (src(sx0, sy0, c) + src(sx0 + 1, sy0, c) + src(sx0, sy0 + 1, c) + src(sx0 + 1, sy0 + 1, c) + 2) >> 2;
+                return;
+            }
+            int sm[3] = {0, 0, 0};
+            for (int r = 0; r < p.iy; ++r)
+                for (int q = 0; q < p.ix; ++q)
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) sm[c] += src(sx0 + q, sy0 + r, c);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) o[c] = sat_u8(float(sm[c]) * p.fscale);
+            return;
+        }
+        if (sx0 >= p.sw) {
+            o[0] = o[1] = o[2] = 0;
+            return;
+        }
         const int nr = min(p.iy, p.sh - sy0);
-        int s = 0, count = 0;
+        int sm[3] = {0, 0, 0}, count = 0;
         for (int r = 0; r < nr; ++r)
             for (int q = 0; q < p.ix && sx0 + q < p.sw; ++q) {
-                s += src(sx0 + q, sy0 + r, c);
+#pragma unroll
+                for (int c = 0; c < 3; ++c) sm[c] += src(sx0 + q, sy0 + r, c);
                 ++count;
             }
-        return sat_u8(float(s) / float(count));
+#pragma unroll
+        for (int c = 0; c < 3; ++c) o[c] = sat_u8(float(sm[c]) / float(count));
+        return;
     }
     default: {
         const int sx = p.lxofs[dx], a0 = p.lalpha[2 * dx], a1 = p.lalpha[2 * dx + 1];
         const int sy = p.lyofs[dy];
         const int ra = clip_row(sy, p.sh), rb = clip_row(sy + 1, p.sh);
         const bool in = dx < p.lxmax;
-        const int h0 = in ? src(sx, ra, c) * a0 + src(sx + 1, ra, c) * a1 : src(sx, ra, c) * COEF_SCALE;
-        const int h1 = in ? src(sx, rb, c) * a0 + src(sx + 1, rb, c) * a1 : src(sx, rb, c) * COEF_SCALE;
         const int b0 = p.lbeta[2 * dy], b1 = p.lbeta[2 * dy + 1];
-        return (((b0 * (h0 >> 4)) >> 16) + ((b1 * (h1 >> 4)) >> 16) + 2) >> 2;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const int h0 = in ? src(sx, ra, c) * a0 + src(sx + 1, ra, c) * a1 : src(sx, ra, c) * COEF_SCALE;
+            const int h1 = in ? src(sx, rb, c) * a0 + src(sx + 1, rb, c) * a1 : src(sx, rb, c) * COEF_SCALE;
+            o[c] = (((b0 * (h0 >> 4)) >> 16) + ((b1 * (h1 >> 4)) >> 16) + 2) >> 2;
+        }
+        return;
     }
     }
 }
@@ -128,40 +164,52 @@ struct PatchSrc {   // a crop's patch in the scratch buffer
     __device__ int operator()(int x, int y, int c) const { return p[((long long)y * pw + x) * 3 + c]; }
 };
 
-// canvas pixels of each crop's patch (blockIdx.y = crop); bars outside the pasted frame are zero
+// One block per (output row, crop): the row's vertical taps are uniform across the block, and its threads walk the
+// row's pixels, so source reads and output writes are contiguous across a wave; each thread takes all three channels
+// of its pixel (taps read once).
+
+// canvas pixels of each crop's patch (blockIdx.x = patch row, blockIdx.y = crop); bars outside the pasted frame are
+// zero
 __global__ void __launch_bounds__(256)
 crop_patch_kernel(const JobDev* __restrict__ jobs, const PlanDev* __restrict__ plans, uint8_t* __restrict__ scratch) {
     const JobDev j = jobs[blockIdx.y];
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= j.pw * j.ph) return;
-    const int px = i % j.pw, py = i / j.pw;
-    const int cx = j.px0 + px - j.left, cy = j.py0 + py - j.top;   // pixel of the resized frame
-    uint8_t* d = scratch + j.patch_off + 3LL * i;
-    if (cx < 0 || cy < 0 || cx >= j.new_w || cy >= j.new_h) {
-        d[0] = 0; d[1] = 0; d[2] = 0;
+    const int py = blockIdx.x;
+    if (py >= j.ph) return;
+    uint8_t* d = scratch + j.patch_off + 3LL * j.pw * py;
+    const int cy = j.py0 + py - j.top;   // row of the resized frame
+    const int n = 3 * j.pw;
+    if (cy < 0 || cy >= j.new_h) {
+        for (int e = threadIdx.x; e < n; e += 256) d[e] = 0;
         return;
     }
     const PlanDev p = plans[j.canvas_plan];
     const FrameSrc src{j.frame, j.stride};
-    int v[3];
-#pragma unroll
-    for (int c = 0; c < 3; ++c) v[c] = resize_px(p, src, cx, cy, c);
-    d[0] = uint8_t(v[0]); d[1] = uint8_t(v[1]); d[2] = uint8_t(v[2]);
+    for (int px = threadIdx.x; px < j.pw; px += 256) {
+        const int cx = j.px0 + px - j.left;
+        int v[3] = {0, 0, 0};
+        if (cx >= 0 && cx < j.new_w) resize_px3(p, src, cx, cy, v);
+        d[3 * px] = uint8_t(v[0]);
+        d[3 * px + 1] = uint8_t(v[1]);
+        d[3 * px + 2] = uint8_t(v[2]);
+    }
 }
 
-// 320 x 180 crop of each patch (blockIdx.y = crop)
+// 320 x 180 crop of each patch (blockIdx.x = crop row, blockIdx.y = crop)
 __global__ void __launch_bounds__(256)
 crop_resize_kernel(const JobDev* __restrict__ jobs, const PlanDev* __restrict__ plans,
                    const uint8_t* __restrict__ scratch, uint8_t* __restrict__ out) {
     const JobDev j = jobs[blockIdx.y];
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= CROP_W * CROP_H) return;
-    const int ox = i % CROP_W, oy = i / CROP_W;
+    const int oy = blockIdx.x;
     const PlanDev p = plans[j.crop_plan];
     const PatchSrc src{scratch + j.patch_off, j.pw};
-    uint8_t* d = out + (long long)blockIdx.y * (CROP_W * CROP_H * 3) + 3LL * i;
-#pragma unroll
-    for (int c = 0; c < 3; ++c) d[c] = uint8_t(resize_px(p, src, ox, oy, c));
+    uint8_t* d = out + (long long)blockIdx.y * (CROP_W * CROP_H * 3) + 3LL * CROP_W * oy;
+    for (int ox = threadIdx.x; ox < CROP_W; ox += 256) {
+        int v[3];
+        resize_px3(p, src, ox, oy, v);
+        d[3 * ox] = uint8_t(v[0]);
+        d[3 * ox + 1] = uint8_t(v[1]);
+        d[3 * ox + 2] = uint8_t(v[2]);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ host plans
@@ -304,7 +352,7 @@ public:
         device_ = dev;
         std::vector<JobDev> jd(static_cast<size_t>(n));
         long long scratch = 0;
-        int max_patch = 0;
+        int max_ph = 0;
         for (int i = 0; i < n; ++i) {
             const CropJob& j = jobs[i];
             const CanvasGeo& g = geo[size_t(i)];
@@ -317,17 +365,17 @@ public:
             d.left = g.left; d.top = g.top; d.new_w = g.new_w; d.new_h = g.new_h;
             d.patch_off = scratch;
             scratch += (3LL * d.pw * d.ph + 255) / 256 * 256;
-            max_patch = std::max(max_patch, d.pw * d.ph);
+            max_ph = std::max(max_ph, d.ph);
         }
         sync_plans();
         grow(scratch_, scratch_bytes_, size_t(scratch));
         grow(jobs_dev_, jobs_bytes_, jd.size() * sizeof(JobDev));
         CROP_CHECK(hipMemcpyAsync(jobs_dev_, jd.data(), jd.size() * sizeof(JobDev), hipMemcpyHostToDevice, s));
         const JobDev* jdev = static_cast<const JobDev*>(jobs_dev_);
-        hipLaunchKernelGGL(crop_patch_kernel, dim3((max_patch + 255) / 256, n), dim3(256), 0, s, jdev,
+        hipLaunchKernelGGL(crop_patch_kernel, dim3(max_ph, n), dim3(256), 0, s, jdev,
                            static_cast<const PlanDev*>(plans_dev_), static_cast<uint8_t*>(scratch_));
         CROP_CHECK(hipGetLastError());
-        hipLaunchKernelGGL(crop_resize_kernel, dim3((CROP_W * CROP_H + 255) / 256, n), dim3(256), 0, s, jdev,
+        hipLaunchKernelGGL(crop_resize_kernel, dim3(CROP_H, n), dim3(256), 0, s, jdev,
                            static_cast<const PlanDev*>(plans_dev_), static_cast<const uint8_t*>(scratch_), out);
         CROP_CHECK(hipGetLastError());
         CROP_CHECK(hipStreamSynchronize(s));   // the job table and scratch are reused by the next call
