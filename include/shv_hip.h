@@ -165,6 +165,16 @@ typedef struct {
 typedef struct { int x, y, w, h; } shv_hip_rect;   /* shv_rect, shv_prep.h:86 */
 int shv_hip_native_crops_rgb(const shv_hip_rgb_image* frames, const shv_hip_rect* rects, int n, uint8_t* d_out,
                              void* stream);
+/* The same for I420 frames (shv_native_crop_i420, shv_prep.h:186): equal to converting the frame to RGB24 as the
+ * reference does (ffmpeg's unscaled yuv420p -> rgb24, BT.601 limited range; engine/preprocess/color.cpp:4-11) and
+ * cropping; planes in device memory, chroma (width + 1) / 2 x (height + 1) / 2. */
+typedef struct {
+    const uint8_t *y, *u, *v;   /* device pointers */
+    ptrdiff_t y_stride, u_stride, v_stride;
+    int width, height;          /* luma size */
+} shv_hip_i420_image;           /* shv_i420_image, shv_prep.h:80-84 */
+int shv_hip_native_crops_i420(const shv_hip_i420_image* frames, const shv_hip_rect* rects, int n, uint8_t* d_out,
+                              void* stream);
 
 /* Gated delta rule of one tier on device buffers (the scan of config 3 on its own; no counterpart in shv_cuda.h --
  * the reference runs its delta_kernel only inside classify, engine/cuda/seq.cu:106-195).  Per window 321 rows; rows

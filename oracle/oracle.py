@@ -184,6 +184,12 @@ class _Rect(ctypes.Structure):       # shv_rect (shv_prep.h:86)
     _fields_ = [("x", ctypes.c_int), ("y", ctypes.c_int), ("w", ctypes.c_int), ("h", ctypes.c_int)]
 
 
+class _I420Image(ctypes.Structure):   # shv_i420_image (shv_prep.h:80-84)
+    _fields_ = [("y", ctypes.c_void_p), ("u", ctypes.c_void_p), ("v", ctypes.c_void_p), ("y_stride", ctypes.c_ssize_t),
+                ("u_stride", ctypes.c_ssize_t), ("v_stride", ctypes.c_ssize_t), ("width", ctypes.c_int),
+                ("height", ctypes.c_int)]
+
+
 class PrepRef:
     """The reference's lazy native crop, shv_native_crop_rgb (engine/preprocess/canvas.cpp:134-143), compiled from
     its own sources by `make -C oracle ref`: the checker of the GPU crops."""
@@ -194,6 +200,8 @@ class PrepRef:
         lib = ctypes.CDLL(str(PREP_SO))
         lib.shv_native_crop_rgb.restype = ctypes.c_int
         lib.shv_native_crop_rgb.argtypes = [ctypes.POINTER(_RgbImage), _Rect, ctypes.c_void_p]
+        lib.shv_native_crop_i420.restype = ctypes.c_int
+        lib.shv_native_crop_i420.argtypes = [ctypes.POINTER(_I420Image), _Rect, ctypes.c_void_p]
         lib.shv_canvas_info_get.restype = ctypes.c_int
         lib.shv_prep_last_error.restype = ctypes.c_char_p
         self.lib = lib
@@ -204,5 +212,14 @@ class PrepRef:
         img = _RgbImage(frame.ctypes.data, w, h, w * 3)
         out = np.empty((180, 320, 3), np.uint8)
         if self.lib.shv_native_crop_rgb(ctypes.byref(img), _Rect(*[int(v) for v in rect]), out.ctypes.data) != 0:
+            raise RuntimeError(self.lib.shv_prep_last_error().decode())
+        return out
+
+    def native_crop_i420(self, y: np.ndarray, u: np.ndarray, v: np.ndarray, rect) -> np.ndarray:
+        y, u, v = (np.ascontiguousarray(a, np.uint8) for a in (y, u, v))
+        img = _I420Image(y.ctypes.data, u.ctypes.data, v.ctypes.data, y.shape[1], u.shape[1], v.shape[1],
+                         y.shape[1], y.shape[0])
+        out = np.empty((180, 320, 3), np.uint8)
+        if self.lib.shv_native_crop_i420(ctypes.byref(img), _Rect(*[int(x) for x in rect]), out.ctypes.data) != 0:
             raise RuntimeError(self.lib.shv_prep_last_error().decode())
         return out

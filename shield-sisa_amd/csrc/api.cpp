@@ -815,7 +815,22 @@ int shv_hip_native_crops_rgb(const shv_hip_rgb_image* frames, const shv_hip_rect
             const shv_hip_rect& r = rects[i];
             jobs[size_t(i)] = shv::CropJob{f.data, f.width, f.height, (long long)f.stride, r.x, r.y, r.w, r.h};
         }
-        shv::native_crops_rgb(jobs.data(), n, d_out, static_cast<hipStream_t>(stream));
+        shv::native_crops(jobs.data(), n, d_out, false, static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+int shv_hip_native_crops_i420(const shv_hip_i420_image* frames, const shv_hip_rect* rects, int n, uint8_t* d_out,
+                              void* stream) {
+    return guarded([&] {
+        if (n < 0 || (n > 0 && (!frames || !rects || !d_out))) throw std::runtime_error("invalid argument");
+        std::vector<shv::CropJob> jobs(static_cast<size_t>(n));
+        for (int i = 0; i < n; ++i) {
+            const shv_hip_i420_image& f = frames[i];
+            const shv_hip_rect& r = rects[i];
+            jobs[size_t(i)] = shv::CropJob{f.y, f.width, f.height, (long long)f.y_stride, r.x, r.y, r.w, r.h,
+                                           f.u, f.v, (long long)f.u_stride, (long long)f.v_stride};
+        }
+        shv::native_crops(jobs.data(), n, d_out, true, static_cast<hipStream_t>(stream));
         return 0;
     });
 }

@@ -16,6 +16,9 @@
 //     out = (((b0 (h0 >> 4)) >> 16) + ((b1 (h1 >> 4)) >> 16) + 2) >> 2, rows clipped into the source;
 //   equal sizes: copy.
 // The plan tables (taps, weights, coefficients) are built on the host in the same double / float arithmetic.
+// I420 frames are converted per native pixel as the reference does row by row (engine/preprocess/color.cpp:4-11,
+// 57-109: ffmpeg's unscaled yuv420p -> rgb24, BT.601 limited range, 16-bit fixed point, chroma of (x, y) at
+// [y / 2][x / 2]).
 #include "dev_common.hpp"
 #include "kernels.hpp"
 
@@ -52,8 +55,10 @@ struct PlanDev {
 
 // one crop: its native frame, canvas geometry and patch
 struct JobDev {
-    const uint8_t* frame;
+    const uint8_t* frame;   // RGB, or the I420 Y plane
     long long stride;
+    const uint8_t *u, *v;   // I420 chroma planes
+    long long u_stride, v_stride;
     long long patch_off;   // byte offset of the patch in the scratch buffer
     int canvas_plan, crop_plan;
     int px0, py0, pw, ph;  // patch = canvas columns px0 .. px0+pw, rows py0 .. py0+ph
@@ -73,7 +78,8 @@ __device__ __forceinline__ void resize_px3(const PlanDev& p, const Src& src, int
     switch (p.kind) {
     case 0:
 #pragma unroll
-        for (int c = 0; c < 3; ++c) o[c] = src(dx, dy, c);
+        for (int c = 0; c < 3; ++c) o[c] = 0;
+        src.pix(dx, dy, o);
         return;
     case 1: {
         const int ya = p.yfirst[dy], ye = p.yfirst[dy + 1], xa = p.xfirst[dx], xe = p.xfirst[dx + 1];
@@ -83,10 +89,11 @@ __device__ __forceinline__ void resize_px3(const PlanDev& p, const Src& src, int
             const float beta = p.yal[j];
             float t[3] = {0.0f, 0.0f, 0.0f};
             for (int k = xa; k < xe; ++k) {
-                const int sx = p.xsi[k];
                 const float al = p.xal[k];
+                int px[3];
+                src.pix(p.xsi[k], sy, px);
 #pragma unroll
-                for (int c = 0; c < 3; ++c) t[c] = t[c] + float(src(sx, sy, c)) * al;
+                for (int c = 0; c < 3; ++c) t[c] = t[c] + float(px[c]) * al;
             }
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
@@ -105,17 +112,19 @@ __device__ __forceinline__ void resize_px3(const PlanDev& p, const Src& src, int
             return;
         }
         if (sy0 + p.iy <= p.sh && dx < p.sw / p.ix) {   // a full block
-            if (p.ix == 2 && p.iy == 2) {
-#pragma unroll
-                for (int c = 0; c < 3; ++c)
-                    o[c] = (src(sx0, sy0, c) + src(sx0 + 1, sy0, c) + src(sx0, sy0 + 1, c) + src(sx0 + 1, sy0 + 1, c) + 2) >> 2;
-                return;
-            }
             int sm[3] = {0, 0, 0};
             for (int r = 0; r < p.iy; ++r)
-                for (int q = 0; q < p.ix; ++q)
+                for (int q = 0; q < p.ix; ++q) {
+                    int px[3];
+                    src.pix(sx0 + q, sy0 + r, px);
 #pragma unroll
-                    for (int c = 0; c < 3; ++c) sm[c] += src(sx0 + q, sy0 + r, c);
+                    for (int c = 0; c < 3; ++c) sm[c] += px[c];
+                }
+            if (p.ix == 2 && p.iy == 2) {
+#pragma unroll
+                for (int c = 0; c < 3; ++c) o[c] = (sm[c] + 2) >> 2;
+                return;
+            }
 #pragma unroll
             for (int c = 0; c < 3; ++c) o[c] = sat_u8(float(sm[c]) * p.fscale);
             return;
@@ -128,8 +137,10 @@ __device__ __forceinline__ void resize_px3(const PlanDev& p, const Src& src, int
         int sm[3] = {0, 0, 0}, count = 0;
         for (int r = 0; r < nr; ++r)
             for (int q = 0; q < p.ix && sx0 + q < p.sw; ++q) {
+                int px[3];
+                src.pix(sx0 + q, sy0 + r, px);
 #pragma unroll
-                for (int c = 0; c < 3; ++c) sm[c] += src(sx0 + q, sy0 + r, c);
+                for (int c = 0; c < 3; ++c) sm[c] += px[c];
                 ++count;
             }
 #pragma unroll
@@ -142,10 +153,16 @@ __device__ __forceinline__ void resize_px3(const PlanDev& p, const Src& src, int
         const int ra = clip_row(sy, p.sh), rb = clip_row(sy + 1, p.sh);
         const bool in = dx < p.lxmax;
         const int b0 = p.lbeta[2 * dy], b1 = p.lbeta[2 * dy + 1];
+        const int sx1 = in ? sx + 1 : sx;
+        int s00[3], s01[3], s10[3], s11[3];
+        src.pix(sx, ra, s00);
+        src.pix(sx1, ra, s01);
+        src.pix(sx, rb, s10);
+        src.pix(sx1, rb, s11);
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-            const int h0 = in ? src(sx, ra, c) * a0 + src(sx + 1, ra, c) * a1 : src(sx, ra, c) * COEF_SCALE;
-            const int h1 = in ? src(sx, rb, c) * a0 + src(sx + 1, rb, c) * a1 : src(sx, rb, c) * COEF_SCALE;
+            const int h0 = in ? s00[c] * a0 + s01[c] * a1 : s00[c] * COEF_SCALE;
+            const int h1 = in ? s10[c] * a0 + s11[c] * a1 : s10[c] * COEF_SCALE;
             o[c] = (((b0 * (h0 >> 4)) >> 16) + ((b1 * (h1 >> 4)) >> 16) + 2) >> 2;
         }
         return;
@@ -156,12 +173,42 @@ __device__ __forceinline__ void resize_px3(const PlanDev& p, const Src& src, int
 struct FrameSrc {   // native RGB frame
     const uint8_t* f;
     long long stride;
-    __device__ int operator()(int x, int y, int c) const { return f[(long long)y * stride + 3 * x + c]; }
+    __device__ void pix(int x, int y, int (&v)[3]) const {
+        const uint8_t* q = f + (long long)y * stride + 3 * x;
+        v[0] = q[0]; v[1] = q[1]; v[2] = q[2];
+    }
+};
+// BT.601 limited-range coefficients of ffmpeg's yuv2rgb tables (contrast = saturation = 1 << 16, brightness 0),
+// rounded to 16 bits as av_clip_int16((x + 2^15) >> 16): Y 76309 (= 65536 * 255 / 219) and the inverse-table
+// entries 104597 (V->R), 132201 (U->B), -25675 (U->G), -53279 (V->G), each times 2^13; Y offset 16 << 19
+struct Yuv {
+    int y_coeff, vr, ub, ug, vg, y_off, uv_off;
+};
+struct I420Src {   // native I420 frame, converted per pixel
+    const uint8_t *Y, *U, *V;
+    long long ys, us, vs;
+    Yuv k;
+    __device__ static int sat16(int v) { return v < -32768 ? -32768 : (v > 32767 ? 32767 : v); }
+    __device__ static int mulhi(int a, int b) { return (a * b) >> 16; }
+    __device__ static int sat8(int v) { return v < 0 ? 0 : (v > 255 ? 255 : v); }
+    __device__ void pix(int x, int y, int (&v)[3]) const {
+        const int yp = int(short((int(Y[(long long)y * ys + x]) << 3) - k.y_off));
+        const int up = sat16((int(U[(long long)(y >> 1) * us + (x >> 1)]) << 3) - k.uv_off);
+        const int vp = sat16((int(V[(long long)(y >> 1) * vs + (x >> 1)]) << 3) - k.uv_off);
+        const int yy = mulhi(yp, k.y_coeff);
+        const int cg = sat16(mulhi(up, k.ug) + mulhi(vp, k.vg));
+        v[0] = sat8(sat16(yy + mulhi(vp, k.vr)));
+        v[1] = sat8(sat16(yy + cg));
+        v[2] = sat8(sat16(yy + mulhi(up, k.ub)));
+    }
 };
 struct PatchSrc {   // a crop's patch in the scratch buffer
     const uint8_t* p;
     int pw;
-    __device__ int operator()(int x, int y, int c) const { return p[((long long)y * pw + x) * 3 + c]; }
+    __device__ void pix(int x, int y, int (&v)[3]) const {
+        const uint8_t* q = p + ((long long)y * pw + x) * 3;
+        v[0] = q[0]; v[1] = q[1]; v[2] = q[2];
+    }
 };
 
 // One block per (output row, crop): the row's vertical taps are uniform across the block, and its threads walk the
@@ -170,8 +217,10 @@ struct PatchSrc {   // a crop's patch in the scratch buffer
 
 // canvas pixels of each crop's patch (blockIdx.x = patch row, blockIdx.y = crop); bars outside the pasted frame are
 // zero
+template <bool I420>
 __global__ void __launch_bounds__(256)
-crop_patch_kernel(const JobDev* __restrict__ jobs, const PlanDev* __restrict__ plans, uint8_t* __restrict__ scratch) {
+crop_patch_kernel(const JobDev* __restrict__ jobs, const PlanDev* __restrict__ plans, uint8_t* __restrict__ scratch,
+                  Yuv yuv) {
     const JobDev j = jobs[blockIdx.y];
     const int py = blockIdx.x;
     if (py >= j.ph) return;
@@ -183,11 +232,15 @@ crop_patch_kernel(const JobDev* __restrict__ jobs, const PlanDev* __restrict__ p
         return;
     }
     const PlanDev p = plans[j.canvas_plan];
-    const FrameSrc src{j.frame, j.stride};
+    const FrameSrc rgb{j.frame, j.stride};
+    const I420Src i420{j.frame, j.u, j.v, j.stride, j.u_stride, j.v_stride, yuv};
     for (int px = threadIdx.x; px < j.pw; px += 256) {
         const int cx = j.px0 + px - j.left;
         int v[3] = {0, 0, 0};
-        if (cx >= 0 && cx < j.new_w) resize_px3(p, src, cx, cy, v);
+        if (cx >= 0 && cx < j.new_w) {
+            if constexpr (I420) resize_px3(p, i420, cx, cy, v);
+            else resize_px3(p, rgb, cx, cy, v);
+        }
         d[3 * px] = uint8_t(v[0]);
         d[3 * px + 1] = uint8_t(v[1]);
         d[3 * px + 2] = uint8_t(v[2]);
@@ -307,6 +360,26 @@ bool make_plan(int sw, int sh, int dw, int dh, int interpolation, PlanHost& p) {
     return true;
 }
 
+// 16-bit rounding of a 2^16-scaled coefficient with saturation (ffmpeg's round + av_clip_int16)
+int round_to_16(long long f) {
+    int r = int((f + (1 << 15)) >> 16);
+    if (r < -32768) r = -32768;
+    if (r > 32767) r = 32767;
+    return r;
+}
+Yuv yuv_coeffs() {
+    const long long cy = (65536LL * 255) / 219;   // contrast = saturation = 1 << 16 leave the table entries unscaled
+    Yuv k;
+    k.y_coeff = round_to_16(cy * (1 << 13));
+    k.vr = round_to_16(104597LL * (1 << 13));
+    k.ub = round_to_16(132201LL * (1 << 13));
+    k.ug = round_to_16(-25675LL * (1 << 13));
+    k.vg = round_to_16(-53279LL * (1 << 13));
+    k.y_off = round_to_16((16LL << 16) * (1 << 3));
+    k.uv_off = 0x0400;
+    return k;
+}
+
 // canvas geometry of a w x h frame (geometry.cpp:77-88): scale min(720/h, 1280/w), centred, mode 0 copy /
 // 1 shrink (area) / 2 enlarge (linear)
 struct CanvasGeo {
@@ -331,12 +404,13 @@ public:
         static CropEngine e;
         return e;
     }
-    void run(const CropJob* jobs, int n, uint8_t* out, hipStream_t s) {
+    void run(const CropJob* jobs, int n, uint8_t* out, hipStream_t s, bool i420) {
         // every argument is checked before the device is touched
         std::vector<CanvasGeo> geo(static_cast<size_t>(n));
         for (int i = 0; i < n; ++i) {
             const CropJob& j = jobs[i];
-            if (!j.frame || j.width <= 0 || j.height <= 0 || j.stride < 3LL * j.width)
+            if (!j.frame || j.width <= 0 || j.height <= 0 || j.stride < (i420 ? 1LL : 3LL) * j.width ||
+                (i420 && (!j.u || !j.v || j.u_stride < (j.width + 1) / 2 || j.v_stride < (j.width + 1) / 2)))
                 throw std::runtime_error("crops: bad frame " + std::to_string(i));
             if (j.x < 0 || j.y < 0 || j.w <= 0 || j.h <= 0 || j.x + j.w > CROP_W || j.y + j.h > CROP_H)
                 throw std::runtime_error("crops: rect out of the 320x180 letterbox at crop " + std::to_string(i));
@@ -359,6 +433,7 @@ public:
             JobDev& d = jd[size_t(i)];
             d.frame = j.frame;
             d.stride = j.stride;
+            d.u = j.u; d.v = j.v; d.u_stride = j.u_stride; d.v_stride = j.v_stride;
             d.canvas_plan = plan_index(0, j.width, j.height, g.new_w, g.new_h, g.mode == 2 ? 1 : 3);
             d.crop_plan = plan_index(1, 4 * j.w, 4 * j.h, CROP_W, CROP_H, 3);
             d.px0 = 4 * j.x; d.py0 = 4 * j.y; d.pw = 4 * j.w; d.ph = 4 * j.h;
@@ -372,8 +447,13 @@ public:
         grow(jobs_dev_, jobs_bytes_, jd.size() * sizeof(JobDev));
         CROP_CHECK(hipMemcpyAsync(jobs_dev_, jd.data(), jd.size() * sizeof(JobDev), hipMemcpyHostToDevice, s));
         const JobDev* jdev = static_cast<const JobDev*>(jobs_dev_);
-        hipLaunchKernelGGL(crop_patch_kernel, dim3(max_ph, n), dim3(256), 0, s, jdev,
-                           static_cast<const PlanDev*>(plans_dev_), static_cast<uint8_t*>(scratch_));
+        static const Yuv yuv = yuv_coeffs();
+        if (i420)
+            hipLaunchKernelGGL(crop_patch_kernel<true>, dim3(max_ph, n), dim3(256), 0, s, jdev,
+                               static_cast<const PlanDev*>(plans_dev_), static_cast<uint8_t*>(scratch_), yuv);
+        else
+            hipLaunchKernelGGL(crop_patch_kernel<false>, dim3(max_ph, n), dim3(256), 0, s, jdev,
+                               static_cast<const PlanDev*>(plans_dev_), static_cast<uint8_t*>(scratch_), yuv);
         CROP_CHECK(hipGetLastError());
         hipLaunchKernelGGL(crop_resize_kernel, dim3(CROP_H, n), dim3(256), 0, s, jdev,
                            static_cast<const PlanDev*>(plans_dev_), static_cast<const uint8_t*>(scratch_), out);
@@ -433,10 +513,10 @@ private:
 
 }  // namespace
 
-void native_crops_rgb(const CropJob* jobs, int n, uint8_t* out, hipStream_t s) {
+void native_crops(const CropJob* jobs, int n, uint8_t* out, bool i420, hipStream_t s) {
     if (n <= 0) return;
     if (!jobs || !out || n > 65535) throw std::runtime_error("crops: null buffer or more than 65535 crops");
-    CropEngine::get().run(jobs, n, out, s);
+    CropEngine::get().run(jobs, n, out, s, i420);
 }
 
 }  // namespace shv

@@ -119,14 +119,16 @@ void launch_se_reduce(const float* part, int ntiles, int cexpp, int cexp, int hw
 
 // ---------------------------------------------------------------- face crops (uint8 RGB, device memory)
 struct CropJob {
-    const uint8_t* frame;   // native RGB frame, rows `stride` bytes apart
+    const uint8_t* frame;   // native RGB frame (or the I420 Y plane), rows `stride` bytes apart
     int width, height;
     long long stride;
     int x, y, w, h;         // crop rectangle in 320x180 letterbox units (w >= 80, h >= 45)
+    const uint8_t *u = nullptr, *v = nullptr;   // I420 chroma planes ((width + 1) / 2 wide)
+    long long u_stride = 0, v_stride = 0;
 };
-// crop i = cv2.resize(canvas(frame_i)[4y:4(y+h), 4x:4(x+w)], (320, 180), INTER_AREA) -> out + i * 172800; returns
-// after the crops are written (synchronises s)
-void native_crops_rgb(const CropJob* jobs, int n, uint8_t* out, hipStream_t s);
+// crop i = cv2.resize(canvas(frame_i)[4y:4(y+h), 4x:4(x+w)], (320, 180), INTER_AREA) -> out + i * 172800 (RGB
+// frames, or I420 frames converted per pixel); returns after the crops are written (synchronises s)
+void native_crops(const CropJob* jobs, int n, uint8_t* out, bool i420, hipStream_t s);
 
 // ---------------------------------------------------------------- sequence (fp32 residual stream)
 void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,

@@ -75,6 +75,7 @@ _SIGS = {
     "shv_hip_gemm_free": (None, [_P]),
     "shv_hip_delta_rule": (ctypes.c_int, [ctypes.c_char_p, _P, _P, _P, _P, _P, ctypes.c_int, _P, ctypes.c_int, _P]),
     "shv_hip_native_crops_rgb": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
+    "shv_hip_native_crops_i420": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
 }
 
 _libs: dict[str, ctypes.CDLL] = {}
@@ -447,6 +448,23 @@ def native_crops_rgb(frames, rects, d_out: int, stream: int | None = None) -> No
     lib = library()
     if lib.shv_hip_native_crops_rgb(ctypes.cast(fa, ctypes.c_void_p), ctypes.cast(ra, ctypes.c_void_p), n, d_out,
                                     stream) != 0:
+        raise ShvError(last_error())
+
+
+class I420Image(ctypes.Structure):   # shv_hip_i420_image (device planes)
+    _fields_ = [("y", ctypes.c_void_p), ("u", ctypes.c_void_p), ("v", ctypes.c_void_p), ("y_stride", ctypes.c_ssize_t),
+                ("u_stride", ctypes.c_ssize_t), ("v_stride", ctypes.c_ssize_t), ("width", ctypes.c_int),
+                ("height", ctypes.c_int)]
+
+
+def native_crops_i420(frames, rects, d_out: int, stream: int | None = None) -> None:
+    """frames: [(y, u, v, y_stride, u_stride, v_stride, width, height)] device planes -> len(rects) crops at d_out."""
+    n = len(rects)
+    fa = (I420Image * max(1, n))(*[I420Image(*f) for f in frames])
+    ra = (Rect * max(1, n))(*[Rect(*[int(v) for v in r]) for r in rects])
+    lib = library()
+    if lib.shv_hip_native_crops_i420(ctypes.cast(fa, ctypes.c_void_p), ctypes.cast(ra, ctypes.c_void_p), n, d_out,
+                                     stream) != 0:
         raise ShvError(last_error())
 
 

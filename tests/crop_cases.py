@@ -39,3 +39,29 @@ def cases():
         for j, r in enumerate(rects(k)):
             out.append((f"{w}x{h}#{j}", (w, h), k, r))
     return out
+
+
+I420_SIZES = [(1280, 720), (1920, 1080), (853, 480), (1365, 767), (640, 360), (720, 1280)]
+
+
+def i420_frame(w, h, seed):
+    """Y, U, V planes (chroma (w + 1) / 2 x (h + 1) / 2), seeded; even seeds smooth, odd seeds noise."""
+    rng = np.random.default_rng(50_000 + seed)
+    cw, ch = (w + 1) // 2, (h + 1) // 2
+    if seed % 2:
+        return (rng.integers(0, 256, (h, w), dtype=np.uint8), rng.integers(0, 256, (ch, cw), dtype=np.uint8),
+                rng.integers(0, 256, (ch, cw), dtype=np.uint8))
+    yy, xx = np.mgrid[0:h, 0:w]
+    cy, cx = np.mgrid[0:ch, 0:cw]
+    Y = np.clip(16 + (xx * 219 // max(1, w - 1)) + rng.integers(-2, 3, (h, w)), 0, 255).astype(np.uint8)
+    U = np.clip(128 + (cx * 100 // max(1, cw - 1)) - 50 + rng.integers(-2, 3, (ch, cw)), 0, 255).astype(np.uint8)
+    V = np.clip(128 + (cy * 100 // max(1, ch - 1)) - 50 + rng.integers(-2, 3, (ch, cw)), 0, 255).astype(np.uint8)
+    return Y, U, V
+
+
+def i420_cases():
+    out = []
+    for k, (w, h) in enumerate(I420_SIZES):
+        for j, r in enumerate(rects(100 + k)):
+            out.append((f"i420 {w}x{h}#{j}", (w, h), k, r))
+    return out

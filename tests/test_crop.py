@@ -24,6 +24,11 @@ def test_reference_crops_match_golden(orc):
         if seed not in frames:
             frames[seed] = crop_cases.frame(w, h, seed)
         assert hashlib.sha256(ref.native_crop(frames[seed], rect).tobytes()).hexdigest() == GOLDEN[cid], cid
+    planes = {}
+    for cid, (w, h), seed, rect in crop_cases.i420_cases():
+        if seed not in planes:
+            planes[seed] = crop_cases.i420_frame(w, h, seed)
+        assert hashlib.sha256(ref.native_crop_i420(*planes[seed], rect).tobytes()).hexdigest() == GOLDEN[cid], cid
 
 
 def test_crop_entry_rejects_bad_rects(shv):
@@ -68,3 +73,37 @@ def test_gpu_crops_match_reference(shv, orc):
     finally:
         for p in dev.values():
             hip.free(p)
+
+
+@pytest.mark.gpu
+def test_gpu_i420_crops_match_reference(shv, orc):
+    """I420 frames (odd sizes included: chroma planes (w + 1) / 2 wide) converted per pixel on the GPU."""
+    cases = crop_cases.i420_cases()
+    print(f"[gpu] {len(cases)} I420 crops from {len(crop_cases.I420_SIZES)} frame sizes in one call", flush=True)
+    hip = shv.Hip()
+    planes, dev = {}, {}
+    try:
+        for cid, (w, h), seed, rect in cases:
+            if seed not in planes:
+                planes[seed] = crop_cases.i420_frame(w, h, seed)
+                dev[seed] = [hip.upload(a) for a in planes[seed]]
+        d_out = hip.malloc(len(cases) * shv.FRAME_BYTES)
+        frames = [(*dev[s], w, (w + 1) // 2, (w + 1) // 2, w, h) for _, (w, h), s, _ in cases]
+        shv.native_crops_i420(frames, [r for *_, r in cases], d_out)
+        got = hip.download(d_out, (len(cases), 180, 320, 3), np.uint8)
+        hip.free(d_out)
+        ref = orc.PrepRef() if orc.PREP_SO.exists() else None
+        bad = []
+        for i, (cid, (w, h), seed, rect) in enumerate(cases):
+            if hashlib.sha256(got[i].tobytes()).hexdigest() != GOLDEN[cid]:
+                detail = ""
+                if ref is not None:
+                    r = ref.native_crop_i420(*planes[seed], rect)
+                    dif = np.argwhere(r != got[i])
+                    detail = f" {len(dif)} bytes differ, max |d| {int(np.abs(r.astype(int) - got[i]).max())}"
+                bad.append(cid + detail)
+        assert not bad, bad[:8]
+    finally:
+        for ps in dev.values():
+            for p in ps:
+                hip.free(p)
