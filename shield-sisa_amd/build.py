@@ -38,6 +38,13 @@ COMMON = ["-O3", "-fPIC", "-std=c++17", "-ffp-contract=off", "-fno-fast-math", "
           "-Wall", "-Wno-unused-function", "-Wno-unused-result"]
 # no packed-fp32 instructions anywhere in the device code
 DEVICE_FLAGS = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# MFMA accumulators in ordinary VGPRs instead of AGPRs (the unified register file holds them either way; the AGPR
+# form adds v_accvgpr moves around every accumulation chain and costs registers).  Only for sources where no inline
+# asm reads an MFMA result: the compiler inserts the MFMA-to-VALU wait states for its own instructions but not for
+# an asm operand, and an empty asm is counted as one wait state.  In these two files every asm operand is a loaded
+# value or a VALU result.
+VGPR_FORM_SOURCES = {"strip.hip", "gemm.hip"}
+VGPR_FORM_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def revision() -> str:
@@ -62,7 +69,8 @@ def build(verbose: bool = False) -> dict:
     objs: list[Path] = []
     for src in DEVICE_SOURCES:
         o = OBJ / (src + ".o")
-        jobs.append([HIPCC, *COMMON, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(o)])
+        extra = VGPR_FORM_FLAGS if src in VGPR_FORM_SOURCES else []
+        jobs.append([HIPCC, *COMMON, *DEVICE_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(o)])
         objs.append(o)
     for src in HOST_SOURCES:
         o = OBJ / (src + ".o")

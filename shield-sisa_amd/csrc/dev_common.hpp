@@ -41,6 +41,12 @@ __device__ __forceinline__ float cephes_exp(float x) {
 }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + cephes_exp(0.0f - x)); }
 __device__ __forceinline__ float relu(float x) { return x > 0.0f ? x : 0.0f; }
+// relu for the fp16 / bf16 tiers as one integer max on the bit pattern: every negative float (-0 included) is a
+// negative int and becomes +0, every positive one stays.  Equal to relu() for all inputs but +NaN, which it passes
+// on instead of mapping to 0 (the tiers' certification rejects non-finite output).  relu() costs a second op
+// whenever the compiler cannot prove x canonical (MFMA results): it quiets x first so that its float max keeps the
+// select's NaN semantics.
+__device__ __forceinline__ float relu_nb(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
 __device__ __forceinline__ float clamp06(float x) {
     float t = x + 3.0f;
     t = t > 0.0f ? t : 0.0f;
@@ -58,17 +64,14 @@ __device__ __forceinline__ float div6(float v) {
 }
 __device__ __forceinline__ float hswish(float x) { return div6(x * clamp06(x)); }
 __device__ __forceinline__ float hsigmoid(float x) { return div6(clamp06(x)); }
-// Branch-free v / 6 for the fp16 / bf16 tiers: the same refined quotient without the subnormal fallback (identical to
-// the IEEE quotient except where that is subnormal); straight-line code keeps unrolled loops schedulable.
-__device__ __forceinline__ float div6_nb(float v) {
-    const float r = 0.16666667163372039794921875f;
-    const float q = v * r;
-    return __builtin_fmaf(__builtin_fmaf(-q, 6.0f, v), r, q);
-}
+// v / 6 for the fp16 / bf16 tiers: one product with fp32(1/6), within an ulp of the IEEE quotient that div6() gives
+// the exact tier -- far below the rounding those tiers' split operands carry -- and two VALU ops cheaper, which
+// counts in the depthwise kernels, where every expanded value goes through hardswish.
+__device__ __forceinline__ float div6_nb(float v) { return v * 0.16666667163372039794921875f; }
 __device__ __forceinline__ float hswish_nb(float x) { return div6_nb(x * clamp06(x)); }
 __device__ __forceinline__ float apply_act_nb(float v, int act) {
     switch (act) {
-    case ACT_RELU: return relu(v);
+    case ACT_RELU: return relu_nb(v);
     case ACT_HS: return div6_nb(v * clamp06(v));
     case ACT_HSIG: return div6_nb(clamp06(v));
     case ACT_SILU: return silu(v);

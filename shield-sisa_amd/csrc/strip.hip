@@ -386,7 +386,7 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
 #pragma unroll
                                 for (int ks = 0; ks < C::KSI; ++ks) acc = mfma_split16<T>(wf[ks], xf[j][t][ks], acc);
 #pragma unroll
-                                for (int i = 0; i < 4; ++i) acc[i] = relu(acc[i]);
+                                for (int i = 0; i < 4; ++i) acc[i] = relu_nb(acc[i]);
                             }
                             e[j][t] = acc;
                         }
@@ -427,7 +427,7 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
                         else
                             v = dw9(wdw[ct][i], el[j0][i], e[j0][0][i], e[j0][1][i], el[j0 + 1][i], e[j0 + 1][0][i],
                                     e[j0 + 1][1][i], el[j0 + 2][i], e[j0 + 2][0][i], e[j0 + 2][1][i]);
-                        d[i] = relu(v);
+                        d[i] = relu_nb(v);
                     }
                     V4 df[P];
                     split4<T>(make_float4(d[0], d[1], d[2], d[3]), df);
@@ -859,8 +859,9 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     const T* wproj = static_cast<const T*>(a.wproj);
     const int H = a.H, W = a.W, Ho = a.Ho, Wo = a.Wo;
 
-    // staging of a step's input rows: float4 i -> (row j, tile t, pixel p, channel quad c4); loads at clamped,
-    // always valid addresses, zero outside the map and past cin
+    // staging of a step's input rows: float4 i -> (row j, tile t, pixel p, channel quad c4).  The loads read clamped,
+    // always valid addresses unconditionally (32-bit offsets from the frame's base); what lies outside the map or
+    // past cin is zeroed when the rows are split into LDS, so no load waits on a predicate
     constexpr int XQ = C::CINP / 4;
     constexpr int XN = C::XRN * C::NT * C::NPOS * XQ;
     constexpr int XPT_ALL = (XN + ST_THREADS - 1) / ST_THREADS;
@@ -869,10 +870,9 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     auto col_of = [&](int strip, int p, int t) {
         return C::S == 1 ? strip * C::VALID - C::PADK + p : 2 * (strip * C::VALID - 1 + p) + t;
     };
-    auto load_step = [&](int item, int step, int k0) {
-        const int strip = item % strips;
-        const long long f = item / strips;
-        const float* Xf = a.X + f * H * W * C::CIN;
+    auto load_step = [&](int fs, int step, int k0) {
+        const int strip = fs % strips;
+        const float* Xf = a.X + (long long)(fs / strips) * (H * W * C::CIN);
         const int iy0 = C::S * step * C::R - C::PADK + C::XR0;
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
@@ -880,21 +880,25 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             const int c4 = i % XQ, rest = i / XQ;
             const int p = rest % C::NPOS, jt = rest / C::NPOS;
             const int t = jt % C::NT, j = jt / C::NT;
-            const int iy = iy0 + j, ix = col_of(strip, p + C::POS0, t);
-            const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W && c4 * 4 < C::CIN;
-            const int cy = min(max(iy, 0), H - 1), cx = min(max(ix, 0), W - 1), cc = min(c4, C::CIN / 4 - 1);
-            const float4 v = *reinterpret_cast<const float4*>(Xf + ((long long)cy * W + cx) * C::CIN + cc * 4);
-            xpre[k] = in ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const int cy = min(max(iy0 + j, 0), H - 1), cx = min(max(col_of(strip, p + C::POS0, t), 0), W - 1);
+            const int cc = min(c4, C::CIN / 4 - 1);
+            const unsigned byte_off = unsigned(((cy * W + cx) * C::CIN + cc * 4) * 4);   // within one frame
+            xpre[k] = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(Xf) + byte_off);
         }
     };
-    auto store_step = [&](int k0) {
+    auto store_step = [&](int strip, int step, int k0) {
+        const int iy0 = C::S * step * C::R - C::PADK + C::XR0;
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
             const int i = tid + (k0 + k) * ST_THREADS;
             if (i >= XN) continue;
             const int c4 = i % XQ, rest = i / XQ;
             const int p = rest % C::NPOS, jt = rest / C::NPOS;
-            const float x[4] = {xpre[k].x, xpre[k].y, xpre[k].z, xpre[k].w};
+            const int t = jt % C::NT, j = jt / C::NT;
+            const int iy = iy0 + j, ix = col_of(strip, p + C::POS0, t);
+            const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W && c4 * 4 < C::CIN;
+            const float x[4] = {in ? xpre[k].x : 0.0f, in ? xpre[k].y : 0.0f, in ? xpre[k].z : 0.0f,
+                                in ? xpre[k].w : 0.0f};
             T part[4][P];
 #pragma unroll
             for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
@@ -931,11 +935,11 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             if constexpr (C::NOPF) {
                 for (int k0 = 0; k0 < XPT_ALL; k0 += XPT) {
                     load_step(fs, step, k0);
-                    store_step(k0);
+                    store_step(strip, step, k0);
                 }
                 lds_barrier();
             } else {
-                store_step(0);
+                store_step(strip, step, 0);
                 lds_barrier();
                 // the next step's (or next item's first) rows are in flight while this step computes
                 if (step + 1 < s1) load_step(fs, step + 1, 0);
