@@ -143,7 +143,8 @@ int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir);
  * (engine/cuda/common.cuh:69): 0 none, 1 ReLU, 2 hardswish, 3 SiLU, 4 hardsigmoid.  d_bias may be NULL.
  * create repacks W on the device (synchronising `stream`); NULL + last_error on failure (fp16 / bf16 need k % 8 == 0).
  * run: variant 0 = the engine's own kernel choice; fp32: 1 GEMV, 2 tiled; fp16 / bf16: 1 small-M, 2..6 direct
- * with 1..5 column tiles per wave, 7 LDS-staged.  Returns 0, or -1 + last_error.  Asynchronous on `stream`. */
+ * with 1..5 column tiles per wave, 7 LDS-staged, 8 streaming (n <= 160).  Returns 0, or -1 + last_error.
+ * Asynchronous on `stream`. */
 typedef struct shv_hip_gemm shv_hip_gemm;
 shv_hip_gemm* shv_hip_gemm_create(const char* mode, int n, int k, const float* d_w, void* stream);
 int shv_hip_gemm_run(shv_hip_gemm* g, const float* d_a, long long m, const float* d_bias, int act, float* d_c,

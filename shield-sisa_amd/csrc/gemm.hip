@@ -634,150 +634,183 @@ template <typename T> void launch_small(const GemmArgs& p, hipStream_t s) {
     else hipLaunchKernelGGL((gemm_small_kernel<T, false, false>), grid, dim3(64), 0, s, p);
 }
 
-// SE-block projects (A rows scaled per frame, N <= 160).  The direct kernel spends two thirds of its vector-memory
-// instructions on operands its 4 waves share: the scale row of a frame and the K step's weight tile.  Here the
-// workgroup stages the scale rows of the (at most SE_MAXF) frames its 256 rows span in LDS once, and each K step's
-// weight tile [NT*16][32] in a double-buffered LDS tile (one LDS barrier per step); only A is read per wave.  Same
-// fragments, products and K order as the direct kernel.
-constexpr int SE_MAXF = 8;
-constexpr int SE_WLD = 32 + 8;   // staged W row stride in T elements
+// Streaming GEMM for narrow N (<= 160 columns, every column in one workgroup) and large M: the SE-block projects,
+// whose A (the depthwise output, fp32) is the only large operand and is read exactly once.  A workgroup (4 waves)
+// takes 128 rows; a wave owns 32 rows x all NT column tiles.  Each wave keeps the A rows of the next ST_D K steps in
+// flight in a register ring (issued as soon as a ring slot has been split), so it waits on HBM once per ST_D steps;
+// the K step's pre-split weight tile [NT*16][32] is staged in a double-buffered LDS tile by the whole workgroup (one
+// LDS barrier per step) and the SE scale rows of the frames the workgroup's rows span are staged once.  Same
+// fragments, split products and K order per output as the direct kernel: results are bitwise those of every other
+// MFMA GEMM kernel.
+constexpr int ST_MT = 2;                        // 16-row tiles per wave
+constexpr int ST_ROWS = MFMA_WAVES * ST_MT * 16;   // rows per workgroup
+constexpr int ST_D = 2;                         // K steps of A in flight ahead of the one being multiplied
+constexpr int ST_WLD = 32 + 8;                  // staged W row stride in T elements
 
-template <typename T, int NT, bool PF>
-__global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_se_kernel(GemmArgs p, int mblocks, int nblocks) {
+template <typename T, int NT, bool SCALE, int WPF>
+__global__ void __launch_bounds__(64 * MFMA_WAVES, 2) gemm_stream_kernel(GemmArgs p) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     constexpr int P = S::P, BN = NT * 16;
     constexpr int WV = P * BN * 4;                          // 16-byte vectors of one staged W tile
     constexpr int WR = (WV + 64 * MFMA_WAVES - 1) / (64 * MFMA_WAVES);
-    __shared__ __attribute__((aligned(16))) T Ws[2][P][BN][SE_WLD];
-    extern __shared__ __attribute__((aligned(16))) float Sc[];   // [nf][K]
+    __shared__ __attribute__((aligned(16))) T Ws[2][P][BN][ST_WLD];
+    extern __shared__ __attribute__((aligned(16))) float Sc[];   // SCALE: [nf][K]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane & 15, g = lane >> 4;
-    const int xcd = blockIdx.x % XCDS, slot = blockIdx.x / XCDS;
-    const int mb = (slot / nblocks) * XCDS + xcd, nb = slot % nblocks;
-    if (mb >= mblocks) return;   // uniform over the workgroup
-    const long long m0 = (long long)mb * MFMA_WAVES * MFMA_MT * 16;
-    const long long mbase = m0 + wave * MFMA_MT * 16;
-    const int nbase = nb * BN;
+    const long long m0 = (long long)blockIdx.x * ST_ROWS;
+    const long long mbase = m0 + wave * ST_MT * 16;
     const T* W = static_cast<const T*>(p.W);
-    const long long f0 = m0 / p.scale_rows;
-    const int nf = int((min(m0 + MFMA_WAVES * MFMA_MT * 16, (long long)p.M) - 1) / p.scale_rows - f0) + 1;
-    for (int i = tid; i < nf * (p.K / 4); i += 64 * MFMA_WAVES) {
-        const int fi = i / (p.K / 4), k4 = i - fi * (p.K / 4);
-        *reinterpret_cast<float4*>(Sc + fi * p.K + k4 * 4) =
-            *reinterpret_cast<const float4*>(p.scale + (f0 + fi) * p.ld_scale + k4 * 4);
+    const int nks = (p.K + 31) / 32;
+    long long f0 = 0;
+    if constexpr (SCALE) {
+        f0 = m0 / p.scale_rows;
+        const int nf = int((min(m0 + ST_ROWS, (long long)p.M) - 1) / p.scale_rows - f0) + 1;
+        for (int i = tid; i < nf * (p.K / 4); i += 64 * MFMA_WAVES) {
+            const int fi = i / (p.K / 4), k4 = i - fi * (p.K / 4);
+            *reinterpret_cast<float4*>(Sc + fi * p.K + k4 * 4) =
+                *reinterpret_cast<const float4*>(p.scale + (f0 + fi) * p.ld_scale + k4 * 4);
+        }
     }
-    // rows of this lane (clamped) and their frames' scale rows in LDS
-    long long arow[MFMA_MT];
-    int srow[MFMA_MT];
+    // this lane's A rows (clamped into range: every load is unconditional) and their frames' scale rows in LDS
+    const float* arow[ST_MT];
+    int srow[ST_MT];
+    bool rlive[ST_MT];
 #pragma unroll
-    for (int mt = 0; mt < MFMA_MT; ++mt) {
+    for (int mt = 0; mt < ST_MT; ++mt) {
         const long long row = mbase + mt * 16 + r;
-        arow[mt] = row < p.M ? row : p.M - 1;
-        srow[mt] = int(arow[mt] / p.scale_rows - f0) * p.K;
+        const long long rc = row < p.M ? row : p.M - 1;
+        rlive[mt] = row < p.M;
+        arow[mt] = p.A + rc * p.lda;
+        srow[mt] = SCALE ? int(rc / p.scale_rows - f0) * p.K : 0;
     }
-    uint4 wr[WR];
-    auto load_w = [&](int k0) {
+    // pre-split W tiles: K step ks + WPF is loaded into a register slot while step ks multiplies and stored into the
+    // other LDS buffer at the end of step ks + WPF - 1 (WPF = 2 hides the weights' L2 latency behind two steps, at
+    // the cost of a second slot of registers)
+    static_assert(WPF == 1 || WPF == 2, "one or two steps of weight prefetch");
+    uint4 wr[WPF][WR];
+    auto load_w = [&](int ks, uint4 (&dst)[WR]) {
 #pragma unroll
         for (int k = 0; k < WR; ++k) {
             const int i = min(tid + k * 64 * MFMA_WAVES, WV - 1);
             const int c8 = i & 3, n = (i >> 2) % BN, q = (i >> 2) / BN;
-            const int col = nbase + n, kk = k0 + c8 * 8;
-            const bool in = col < p.N && kk < p.K;
-            const uint4 v = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)min(col, p.N - 1) * p.ldw +
+            const int kk = ks * 32 + c8 * 8;
+            const bool in = n < p.N && kk < p.K;
+            const uint4 v = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)min(n, p.N - 1) * p.ldw +
                                                           min(kk, p.K - 8));
-            wr[k] = in ? v : make_uint4(0u, 0u, 0u, 0u);
+            dst[k] = in ? v : make_uint4(0u, 0u, 0u, 0u);
         }
     };
-    auto store_w = [&](int buf) {
+    auto store_w = [&](int buf, const uint4 (&src)[WR]) {
 #pragma unroll
         for (int k = 0; k < WR; ++k) {
             const int i = tid + k * 64 * MFMA_WAVES;
             if (i >= WV) continue;
             const int c8 = i & 3, n = (i >> 2) % BN, q = (i >> 2) / BN;
-            *reinterpret_cast<uint4*>(&Ws[buf][q][n][c8 * 8]) = wr[k];
+            *reinterpret_cast<uint4*>(&Ws[buf][q][n][c8 * 8]) = src[k];
         }
     };
-    load_w(0);
-    store_w(0);
+    float ring[ST_D][ST_MT][8];
+    auto load_a = [&](int ks, float (&dst)[ST_MT][8]) {
+        const int kc = min(ks * 32 + g * 8, p.K - 8);
+#pragma unroll
+        for (int mt = 0; mt < ST_MT; ++mt) load8(arow[mt] + kc, dst[mt]);
+    };
+    load_w(0, wr[0]);
+#pragma unroll
+    for (int d = 0; d < ST_D; ++d)
+        if (d < nks) load_a(d, ring[d]);
+    store_w(0, wr[0]);
+    if (WPF == 2 && nks > 1) load_w(1, wr[WPF - 1]);
     lds_barrier();
 
-    f32x4 acc[MFMA_MT][NT];
+    f32x4 acc[ST_MT][NT];
 #pragma unroll
-    for (int i = 0; i < MFMA_MT; ++i)
+    for (int i = 0; i < ST_MT; ++i)
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // PF: A rows one K step ahead (the next step's loads in flight while this one computes; costs 32 VGPRs)
-    float xn[PF ? MFMA_MT : 1][8];
-    auto load_a = [&](int k0, float (*dst)[8]) {
-        const int kc = min(k0 + g * 8, p.K - 8);
-#pragma unroll
-        for (int mt = 0; mt < MFMA_MT; ++mt) load8(p.A + arow[mt] * p.lda + kc, dst[mt]);
-    };
-    if constexpr (PF) load_a(0, xn);
-    int buf = 0;
-    for (int k0 = 0; k0 < p.K; k0 += 32) {
-        const bool more = k0 + 32 < p.K;
-        const int kk = k0 + g * 8;
+    // one K step: W of step ks + WPF into register slot wload, split the A ring slot's rows (scaled), refill that
+    // slot ST_D steps ahead, multiply, stage W of step ks + 1 (register slot wstore) in the other LDS buffer
+    auto step = [&](int ks, float (&slot)[ST_MT][8], uint4 (&wload)[WR], const uint4 (&wstore)[WR]) {
+        if (ks + WPF < nks) load_w(ks + WPF, wload);
+        const int kk = ks * 32 + g * 8;
         const bool kin = kk < p.K;
         const int kc = kin ? kk : p.K - 8;
-        float x[MFMA_MT][8];
-        if constexpr (PF) {
+        V8 a[ST_MT][P];
 #pragma unroll
-            for (int mt = 0; mt < MFMA_MT; ++mt)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[mt][e] = xn[mt][e];
-            if (more) {
-                load_w(k0 + 32);
-                load_a(k0 + 32, xn);
-            }
-        } else {
-            if (more) load_w(k0 + 32);
-            load_a(k0, x);
-        }
-        V8 a[MFMA_MT][P], b[NT][P];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-            for (int q = 0; q < P; ++q) b[nt][q] = *reinterpret_cast<const V8*>(&Ws[buf][q][nt * 16 + r][g * 8]);
-#pragma unroll
-        for (int mt = 0; mt < MFMA_MT; ++mt) {
-            const bool live = kin && mbase + mt * 16 + r < p.M;
+        for (int mt = 0; mt < ST_MT; ++mt) {
+            const bool live = kin && rlive[mt];
             float sc[8];
-            load8(Sc + srow[mt] + kc, sc);
+            if constexpr (SCALE) load8(Sc + srow[mt] + kc, sc);
             float v[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = live ? sc[e] * x[mt][e] : 0.0f;
+            for (int e = 0; e < 8; ++e) {
+                float t = slot[mt][e];
+                if constexpr (SCALE) t = sc[e] * t;
+                v[e] = live ? t : 0.0f;
+            }
             split8<T>(v, a[mt]);
         }
+        if (ks + ST_D < nks) load_a(ks + ST_D, slot);
+        const int buf = ks & 1;
 #pragma unroll
-        for (int i = 0; i < S::NPROD; ++i)
+        for (int nt = 0; nt < NT; ++nt) {
+            V8 b[P];
 #pragma unroll
-            for (int mt = 0; mt < MFMA_MT; ++mt)
+            for (int q = 0; q < P; ++q) b[q] = *reinterpret_cast<const V8*>(&Ws[buf][q][nt * 16 + r][g * 8]);
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[nt][S::wp(i)], acc[mt][nt]);
-        if (more) store_w(buf ^ 1);
+            for (int i = 0; i < S::NPROD; ++i)
+#pragma unroll
+                for (int mt = 0; mt < ST_MT; ++mt) acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[S::wp(i)], acc[mt][nt]);
+        }
+        if (ks + 1 < nks) store_w(buf ^ 1, wstore);
         lds_barrier();
-        buf ^= 1;
+    };
+    static_assert(ST_D == 2, "the A ring and the W register slots alternate with the step parity");
+    for (int ks = 0; ks < nks; ks += 2) {
+        step(ks, ring[0], wr[0], wr[WPF - 1]);
+        if (ks + 1 < nks) step(ks + 1, ring[1], wr[WPF - 1], wr[0]);
     }
     if (mbase >= p.M) return;
 #pragma unroll
-    for (int mt = 0; mt < MFMA_MT; ++mt)
-        epi_block<NT>(p, [&](int i) { return mbase + mt * 16 + g * 4 + i; }, [&](int j) { return nbase + j * 16 + r; },
+    for (int mt = 0; mt < ST_MT; ++mt)
+        epi_block<NT>(p, [&](int i) { return mbase + mt * 16 + g * 4 + i; }, [&](int j) { return j * 16 + r; },
                       [&](int i, int j) { return acc[mt][j][i]; });
 }
 
-template <typename T, int NT, bool PF>
-void launch_se(const GemmArgs& p, hipStream_t s) {
-    const int rows_wg = 16 * MFMA_MT * MFMA_WAVES;
-    if ((rows_wg - 1) / p.scale_rows + 2 > SE_MAXF || p.K % 8)
-        throw std::runtime_error("gemm_se: a workgroup would span too many frames");
-    const int mblocks = (int)cdiv(p.M, rows_wg), nblocks = (int)cdiv(p.N, NT * 16);
-    const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
-    if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_se: grid too large");
-    const size_t lds = size_t(std::min(SE_MAXF, (rows_wg - 1) / p.scale_rows + 2)) * p.K * sizeof(float);
-    hipLaunchKernelGGL((gemm_se_kernel<T, NT, PF>), dim3((unsigned)blocks), dim3(64 * MFMA_WAVES), lds, s, p, mblocks,
-                       nblocks);
+template <typename T, int NT>
+void launch_stream_nt(const GemmArgs& p, hipStream_t s) {
+    if (p.K % 8 || p.N > NT * 16) throw std::runtime_error("gemm_stream: K must be a multiple of 8 and N fit the tiles");
+    size_t lds = 0;
+    if (p.scale) {
+        if (p.scale_rows < 1) throw std::runtime_error("gemm_stream: bad scale row count");
+        const size_t nf = size_t((ST_ROWS - 1) / p.scale_rows + 2);   // frames a workgroup's rows can span
+        lds = nf * size_t(p.K) * sizeof(float);
+        if (lds > 64 * 1024) throw std::runtime_error("gemm_stream: SE scale rows exceed the LDS budget");
+    }
+    const unsigned blocks = cdiv(p.M, ST_ROWS);
+    constexpr int WPF = NT >= 8 ? 2 : 1;   // measured: the second weight slot pays only for the widest tiles
+    if (p.scale)
+        hipLaunchKernelGGL((gemm_stream_kernel<T, NT, true, WPF>), dim3(blocks), dim3(64 * MFMA_WAVES), lds, s, p);
+    else
+        hipLaunchKernelGGL((gemm_stream_kernel<T, NT, false, WPF>), dim3(blocks), dim3(64 * MFMA_WAVES), 0, s, p);
+}
+
+template <typename T> void launch_stream(const GemmArgs& p, hipStream_t s) {
+    if (p.Ah || p.Ch || p.swiglu) throw std::runtime_error("gemm_stream: fp32 A and C only, no SwiGLU");
+    switch ((p.N + 15) / 16) {
+    case 1: launch_stream_nt<T, 1>(p, s); return;
+    case 2: launch_stream_nt<T, 2>(p, s); return;
+    case 3: launch_stream_nt<T, 3>(p, s); return;
+    case 4: launch_stream_nt<T, 4>(p, s); return;
+    case 5: launch_stream_nt<T, 5>(p, s); return;
+    case 6: launch_stream_nt<T, 6>(p, s); return;
+    case 7: launch_stream_nt<T, 7>(p, s); return;
+    case 8: launch_stream_nt<T, 8>(p, s); return;
+    case 9: launch_stream_nt<T, 9>(p, s); return;
+    case 10: launch_stream_nt<T, 10>(p, s); return;
+    }
+    throw std::runtime_error("gemm_stream: N must be at most 160");
 }
 
 template <typename T, int NT>
@@ -816,6 +849,7 @@ template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
     const int tiles = (p.N + 15) / 16;
     if (p.swiglu || tiles > 10) { launch_lds<T, 4, 4, 2, 2>(p, s); return; }
     if (p.Ah) throw std::runtime_error("gemm: pre-split A needs N > 160 or M <= 2048");
+    if (p.scale) { launch_stream<T>(p, s); return; }   // SE projects: A read once, all columns per workgroup
     int nt = tiles;
     if (tiles > 5) {
         int best_cols = 1 << 30;
@@ -823,11 +857,6 @@ template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
             const int cols = (tiles + c - 1) / c * c;
             if (cols < best_cols) { best_cols = cols; nt = c; }
         }
-    }
-    if (p.scale && nt >= 4) {   // wide SE projects: shared operands staged in LDS (A prefetch where registers allow;
-        if (nt == 4) launch_se<T, 4, true>(p, s);   // 3 column tiles measured faster in the direct kernel)
-        else launch_se<T, 5, false>(p, s);
-        return;
     }
     switch (nt) {
     case 1: launch_direct<T, 1>(p, s); break;
@@ -1004,6 +1033,7 @@ template <typename T> void gemm_mfma_variant(const GemmArgs& p, hipStream_t s, i
     case 5: launch_direct<T, 4>(p, s); return;
     case 6: launch_direct<T, 5>(p, s); return;
     case 7: launch_lds<T, 4, 4, 2, 2>(p, s); return;
+    case 8: launch_stream<T>(p, s); return;
     }
     throw std::runtime_error("gemm: unknown kernel variant " + std::to_string(variant));
 }

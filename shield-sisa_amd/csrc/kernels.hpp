@@ -43,7 +43,8 @@ void gemm_f32(const GemmArgs& p, hipStream_t s);
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
 // Kernel variants, for the GEMM microbench and its bitwise variant check (every variant performs the same operation
 // sequence per output, so all give bitwise equal results).  fp32: 0 automatic, 1 GEMV, 2 tiled.  MFMA tiers:
-// 0 automatic, 1 small-M, 2..6 direct with 1..5 column tiles per wave, 7 LDS-staged 128 x 128.
+// 0 automatic, 1 small-M, 2..6 direct with 1..5 column tiles per wave, 7 LDS-staged 128 x 128, 8 streaming (N <= 160,
+// every column in one workgroup; the SE projects' kernel).
 void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant);
 template <typename T> void gemm_mfma_variant(const GemmArgs& p, hipStream_t s, int variant);
 // half tiers: last 1x1 (x [F*60][160] fp32, pre-split weight parts [960][160], + bias, hardswish) fused with the 4x4

@@ -71,6 +71,8 @@ def test_pw_gemm_parity_and_variants(shv, orc, weights, name, M, N, K, mode):
                 print(f"[gpu]   max error / bound-scale {ratio.max():.3e} (bar {SPLIT_TOL:.3e})", flush=True)
                 assert ratio.max() <= SPLIT_TOL
             for v in shv.GEMM_VARIANTS[mode]:
+                if v in shv.GEMM_NARROW_VARIANTS and N > 160:
+                    continue
                 m = min(M, 65536) if (mode == "fp32" and v == 1) else M
                 hip.memset(dV, 0xFF, m * N * 4)
                 g.run(dA, m, dV, db, shv.ACT_HSWISH, variant=v)
