@@ -303,6 +303,22 @@ def test_row_independence_half(shv, weights, clips, mode):
     assert np.array_equal(batch.view(np.uint32), single.view(np.uint32)), float(np.abs(batch - single).max())
 
 
+@pytest.mark.parametrize("mode", ["fp16", "bf16"])
+def test_seq_gemm_dma_matches_lds(shv, weights, clips, mode, monkeypatch):
+    """The sequence GEMMs take pre-split A; above 2048 rows they run in the kernel that loads operand tiles straight
+    from HBM into LDS (swizzled fragment blocks, several K steps in flight).  It performs every output's MFMA
+    sequence in the register-staged LDS kernel's order (SHV_HIP_NO_GEMM_DMA=1), so 16 clips (5136 sequence rows,
+    partial last row and column blocks) give bitwise the same logits either way."""
+    print(f"[gpu] {mode} sequence GEMMs: direct-to-LDS kernel vs register-staged kernel, 16 clips", flush=True)
+    with shv.Model(weights, mode, experimental=True, use_graphs=0, max_frames=320, max_windows=16) as m:
+        monkeypatch.delenv("SHV_HIP_NO_GEMM_DMA", raising=False)
+        dma = m.predict(clips[:16])
+        monkeypatch.setenv("SHV_HIP_NO_GEMM_DMA", "1")
+        lds = m.predict(clips[:16])
+    assert np.all(np.isfinite(dma))
+    assert np.array_equal(dma.view(np.uint32), lds.view(np.uint32)), float(np.abs(dma - lds).max())
+
+
 @pytest.mark.parametrize("mode", ["fp16"])
 def test_delta_splits_bitwise(shv, weights, clips, mode):
     """The half tiers split the delta rule by batch size: the chunked scan deals a head's 128 value columns over
