@@ -527,21 +527,25 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p, int mblocks, 
 inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
 
 // Pre-split A GEMM with direct global -> LDS loads (the sequence GEMMs of the half tiers, whose A arrives already
-// split into the tier's parts).  Workgroup tile 128 x 128, 4 waves of 64 x 64 (as gemm_lds_kernel), K steps of 32.
+// split into the tier's parts).  Workgroup tile 128 x 32 WN, 4 waves of 64 x 16 WN, K steps of 32.
 // The operand tiles of a K step are sixteen-row fragment blocks of 1 KB each (A: 8 blocks per part, W: 8 per part),
 // written by global_load_lds_dwordx4 (16 bytes per lane, lane l to byte 16 l of its block) with no register staging,
 // and read back as MFMA fragments.  DMA lane l carries row l / 4 and 16-byte K chunk (l % 4) ^ ((l / 16) % 4) of the
 // block, so that the sixteen lanes of a fragment read (one chunk of rows 0..15) cover the 64 banks once.  NS K steps
-// share an LDS ring (NS = 2: fp16 2 x 32 KB, two workgroups per CU; bf16 2 x 48 KB): a step waits for its own loads
-// (s_waitcnt on the wave's count of younger loads) and one barrier, then issues the loads of step k + NS - 1 into
-// the slot step k - 1 used.  Per output the MFMA sequence is that of every other MFMA GEMM kernel (K steps in order,
+// share an LDS ring (fp16: 2 x 32 KB for 128 x 128 tiles, bf16: 2 x 36 KB for 128 x 64 tiles; two workgroups per
+// CU): a step waits for its own loads (s_waitcnt on the wave's count of younger loads) and one barrier, then issues
+// the loads of step k + NS - 1 into the slot step k - 1 used.  Per output the MFMA sequence is that of every other MFMA GEMM kernel (K steps in order,
 // the split products in order), so results are bitwise equal to theirs.
-template <typename T, int NS_> struct DmaCfg {
+template <typename T, int NS_, int WN_> struct DmaCfg {
     static constexpr int P = Split<T>::P;
     static constexpr int NS = NS_;                            // K steps in flight
+    static constexpr int WN = WN_;                            // 16-column tiles per wave (2 x WN per workgroup)
+    static constexpr int AB = 8, WB = 2 * WN;                 // fragment blocks per part: A (128 rows), W
     static constexpr int BLK = 1024;                          // bytes of one 16 x 32 fragment block
-    static constexpr int STAGE = 2 * P * 8 * BLK;             // A then W, [operand][part][block]
-    static constexpr int DPW = 2 * P * 8 / 4;                 // loads per wave per K step
+    static constexpr int TB = P * (AB + WB);                  // blocks per K step: [A part][block], [W part][block]
+    static constexpr int STAGE = TB * BLK;
+    static constexpr int DPW = TB / 4;                        // loads per wave per K step
+    static_assert(TB % 4 == 0, "the step's blocks are dealt evenly over the 4 waves");
 };
 
 // the wave's loads of one K step are issued; wait until at most N younger ones are outstanding
@@ -550,13 +554,13 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_block) {
     __builtin_amdgcn_global_load_lds(src, lds_block, 16, 0, 0);
 }
 
-template <typename T, int NS_>
+template <typename T, int NS_, int WN_>
 __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs p, int mblocks, int nblocks) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
-    typedef DmaCfg<T, NS_> D;
-    constexpr int P = S::P, NS = D::NS, DPW = D::DPW;
-    constexpr int WM = 4, WN = 4, WGN = 2;
+    typedef DmaCfg<T, NS_, WN_> D;
+    constexpr int P = S::P, NS = D::NS, DPW = D::DPW, AB = D::AB, WB = D::WB;
+    constexpr int WM = 4, WN = D::WN, WGN = 2, BN = 16 * WN * WGN;
     __shared__ __attribute__((aligned(1024))) unsigned char ring[NS * D::STAGE];
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: the LDS destinations are scalar
@@ -565,24 +569,25 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs p, int mblocks, 
     const int mb = (slot / nblocks) * XCDS + xcd, nb = slot % nblocks;
     if (mb >= mblocks) return;   // uniform over the workgroup
     const long long m0 = (long long)mb * 128;
-    const int n0 = nb * 128;
+    const int n0 = nb * BN;
     const T* Ah = static_cast<const T*>(p.Ah);
     const T* W = static_cast<const T*>(p.W);
     const int nk = p.K / 32;
 
-    // this lane's source rows of the wave's DMA_PER_WAVE loads (rows clamped into range; K chunk swizzled)
+    // this lane's source rows of the wave's DPW loads (rows clamped into range; K chunk swizzled)
     const int drow = lane >> 2, dchunk = (lane & 3) ^ ((lane >> 4) & 3);
     const T* src[DPW];
     int boff[DPW];
 #pragma unroll
     for (int j = 0; j < DPW; ++j) {
-        const int jj = wave * DPW + j;                 // 0 .. 16 P - 1: [operand][part][block]
-        const int op = jj / (8 * P), q = (jj / 8) % P, blk = jj % 8;
-        boff[j] = ((op * P + q) * 8 + blk) * D::BLK;
-        if (op == 0) {
+        const int jj = wave * DPW + j;                 // 0 .. TB - 1
+        boff[j] = jj * D::BLK;
+        if (jj < P * AB) {
+            const int q = jj / AB, blk = jj % AB;
             const long long row = min(m0 + blk * 16 + drow, (long long)p.M - 1);
             src[j] = Ah + q * p.astride + row * p.lda + dchunk * 8;
         } else {
+            const int q = (jj - P * AB) / WB, blk = (jj - P * AB) % WB;
             const int n = min(n0 + blk * 16 + drow, p.N - 1);
             src[j] = W + q * p.wstride + (long long)n * p.ldw + dchunk * 8;
         }
@@ -603,6 +608,7 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs p, int mblocks, 
 #pragma unroll
     for (int ks = 0; ks < NS - 1; ++ks)
         if (ks < nk) issue(ks);
+    static_assert(NS >= 2 && NS - 2 <= 2, "wait counts cover at most two younger steps");
     for (int ks = 0; ks < nk; ++ks) {
         // this step's loads are the oldest of the wave's outstanding ones: younger = min(NS - 2, nk - 1 - ks) steps
         const int younger = min(NS - 2, nk - 1 - ks);
@@ -617,12 +623,12 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs p, int mblocks, 
         for (int mt = 0; mt < WM; ++mt)
 #pragma unroll
             for (int q = 0; q < P; ++q)
-                a[mt][q] = *reinterpret_cast<const V8*>(st + ((0 * P + q) * 8 + wm * WM + mt) * D::BLK + foff);
+                a[mt][q] = *reinterpret_cast<const V8*>(st + (q * AB + wm * WM + mt) * D::BLK + foff);
 #pragma unroll
         for (int nt = 0; nt < WN; ++nt)
 #pragma unroll
             for (int q = 0; q < P; ++q)
-                b[nt][q] = *reinterpret_cast<const V8*>(st + ((1 * P + q) * 8 + wn * WN + nt) * D::BLK + foff);
+                b[nt][q] = *reinterpret_cast<const V8*>(st + (P * AB + q * WB + wn * WN + nt) * D::BLK + foff);
 #pragma unroll
         for (int i = 0; i < S::NPROD; ++i)
 #pragma unroll
@@ -630,7 +636,6 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs p, int mblocks, 
 #pragma unroll
                 for (int nt = 0; nt < WN; ++nt) acc[mt][nt] = S::mfma(a[mt][S::ap(i)], b[nt][S::wp(i)], acc[mt][nt]);
     }
-    static_assert(NS - 2 <= 2, "wait counts cover at most two younger steps");
     // lane holds C[m0 + (wm*WM + mt)*16 + g*4 + i][n0 + (wn*WN + nt)*16 + r]
     const int nbase = n0 + wn * WN * 16;
     if (p.swiglu) {  // 16-row panels alternate gate / up; WN is even and nbase a multiple of 32
@@ -956,15 +961,21 @@ void launch_direct(const GemmArgs& p, hipStream_t s) {
         hipLaunchKernelGGL((gemm_direct_kernel<T, NT, false>), grid, dim3(64 * MFMA_WAVES), 0, s, p, mblocks, nblocks);
 }
 
+template <typename T, int NS, int WN> void launch_dma_cfg(const GemmArgs& p, hipStream_t s) {
+    const int mblocks = (int)cdiv(p.M, 128), nblocks = (int)cdiv(p.N, 32 * WN);
+    const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
+    if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_dma: grid too large");
+    hipLaunchKernelGGL((gemm_dma_kernel<T, NS, WN>), dim3((unsigned)blocks), dim3(256), 0, s, p, mblocks, nblocks);
+}
+
 template <typename T> void launch_dma(const GemmArgs& p, hipStream_t s) {
     if (!p.Ah || p.K % 32 || p.astride % 8 || p.wstride % 8 || p.lda % 8 || p.ldw % 8)
         throw std::runtime_error("gemm_dma: needs pre-split A, K % 32 == 0 and 16-byte aligned rows");
-    const int mblocks = (int)cdiv(p.M, 128), nblocks = (int)cdiv(p.N, 128);
-    const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
-    if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_dma: grid too large");
-    // two K steps in the ring: measured faster than three or four (fp16 2.26 vs 3.37 / 3.41 ms per 128-clip step),
-    // whose LDS leaves one workgroup per CU -- a second resident workgroup hides more than a deeper ring
-    hipLaunchKernelGGL((gemm_dma_kernel<T, 2>), dim3((unsigned)blocks), dim3(256), 0, s, p, mblocks, nblocks);
+    // measured per 128-clip step (ring depth, column tiles per wave): fp16 (2,4) 2.26 ms, (2,2) 2.43, (3,2) 2.82,
+    // (3,4) 3.35, (4,2) 4.19; bf16 (2,2) 4.14 ms, (2,4) 4.71, (3,4) 4.79, (3,2) 5.91, (4,2) 6.00.  Deeper rings
+    // lose: the occupancy their LDS costs is worth more than the latency they hide.
+    if constexpr (Split<T>::P == 2) launch_dma_cfg<T, 2, 4>(p, s);
+    else launch_dma_cfg<T, 2, 2>(p, s);
 }
 
 // the direct-to-LDS kernel for pre-split A unless SHV_HIP_NO_GEMM_DMA is set (read per launch: the bitwise
