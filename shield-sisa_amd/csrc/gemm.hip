@@ -1003,6 +1003,9 @@ void launch_lds(const GemmArgs& p, hipStream_t s) {
 // padded columns (at most 5 per wave); wider N (last 1x1, sequence): LDS-staged 128 x 128 workgroup tiles.
 template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
     if (p.M <= 2048) { launch_small<T>(p, s); return; }   // latency: one clip's shapes
+    // SE excitation layers (fp32 A, M = frames): one wave per 16 x 32 tile spreads them over the device (measured
+    // at 2560 frames: 124 vs 282 us for the ten fc shapes with the tiled kernels)
+    if (!p.Ah && !p.scale && !p.swiglu && p.M <= 8192) { launch_small<T>(p, s); return; }
     const int tiles = (p.N + 15) / 16;
     if (p.Ah && p.K % 32 == 0 && gemm_dma_enabled()) { launch_dma<T>(p, s); return; }
     if (p.swiglu || tiles > 10) { launch_lds<T, 4, 4, 2, 2>(p, s); return; }
