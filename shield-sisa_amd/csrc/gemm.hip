@@ -778,13 +778,12 @@ template <typename T> void launch_small(const GemmArgs& p, hipStream_t s) {
 // LDS barrier per step) and the SE scale rows of the frames the workgroup's rows span are staged once.  Same
 // fragments, split products and K order per output as the direct kernel: results are bitwise those of every other
 // MFMA GEMM kernel.
-constexpr int ST_MT = 2;                        // 16-row tiles per wave
-constexpr int ST_ROWS = MFMA_WAVES * ST_MT * 16;   // rows per workgroup
 constexpr int ST_D = 2;                         // K steps of A in flight ahead of the one being multiplied
 constexpr int ST_WLD = 32 + 8;                  // staged W row stride in T elements
 
-template <typename T, int NT, bool SCALE, int WPF>
+template <typename T, int NT, bool SCALE, int WPF, int ST_MT>
 __global__ void __launch_bounds__(64 * MFMA_WAVES, 2) gemm_stream_kernel(GemmArgs p) {
+    constexpr int ST_ROWS = MFMA_WAVES * ST_MT * 16;   // rows per workgroup
     typedef Split<T> S;
     typedef typename S::V8 V8;
     constexpr int P = S::P, BN = NT * 16;
@@ -914,8 +913,9 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES, 2) gemm_stream_kernel(GemmArg
                       [&](int i, int j) { return acc[mt][j][i]; });
 }
 
-template <typename T, int NT>
-void launch_stream_nt(const GemmArgs& p, hipStream_t s) {
+template <typename T, int NT, int ST_MT>
+void launch_stream_mt(const GemmArgs& p, hipStream_t s) {
+    constexpr int ST_ROWS = MFMA_WAVES * ST_MT * 16;
     if (p.K % 8 || p.N > NT * 16) throw std::runtime_error("gemm_stream: K must be a multiple of 8 and N fit the tiles");
     size_t lds = 0;
     if (p.scale) {
@@ -927,10 +927,14 @@ void launch_stream_nt(const GemmArgs& p, hipStream_t s) {
     const unsigned blocks = cdiv(p.M, ST_ROWS);
     constexpr int WPF = NT >= 8 ? 2 : 1;   // measured: the second weight slot pays only for the widest tiles
     if (p.scale)
-        hipLaunchKernelGGL((gemm_stream_kernel<T, NT, true, WPF>), dim3(blocks), dim3(64 * MFMA_WAVES), lds, s, p);
+        hipLaunchKernelGGL((gemm_stream_kernel<T, NT, true, WPF, ST_MT>), dim3(blocks), dim3(64 * MFMA_WAVES), lds, s, p);
     else
-        hipLaunchKernelGGL((gemm_stream_kernel<T, NT, false, WPF>), dim3(blocks), dim3(64 * MFMA_WAVES), 0, s, p);
+        hipLaunchKernelGGL((gemm_stream_kernel<T, NT, false, WPF, ST_MT>), dim3(blocks), dim3(64 * MFMA_WAVES), 0, s, p);
 }
+// rows per wave: 32 (measured against 16 and 64 rows on the SE-project shapes: 16 wins only for N <= 48, and there
+// by 5%; 64 spills at the widest tiles)
+template <typename T, int NT>
+void launch_stream_nt(const GemmArgs& p, hipStream_t s) { launch_stream_mt<T, NT, 2>(p, s); }
 
 template <typename T> void launch_stream(const GemmArgs& p, hipStream_t s) {
     if (p.Ah || p.Ch || p.swiglu) throw std::runtime_error("gemm_stream: fp32 A and C only, no SwiGLU");

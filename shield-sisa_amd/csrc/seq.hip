@@ -572,7 +572,10 @@ __device__ __forceinline__ void chunk_decays(float ai, float (*Gs)[DC + 1], floa
     }
 }
 
-// One wave per (window, head, chunk): A1V and B1 into CH [window][head][chunk][DCF].
+// One wave per (window, head, chunk): A1V and B1 into CH [window][head][chunk][DCF].  Only K (read as both operands
+// of K K^T and by B1), L, T and the decay products live in LDS (22 KB: seven waves per CU); Q fragments and the V
+// columns of A1V are read straight from global memory, issued early so that they land during the products and the
+// forward substitution.
 template <typename T>
 __global__ void __launch_bounds__(64)
 delta_chunk_prep_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -586,45 +589,41 @@ delta_chunk_prep_kernel(const float* __restrict__ Q, const float* __restrict__ K
     const int t0 = c * DC, n = min(DC, kT - t0);
     const long long row0 = (long long)b * kT + t0;
     __shared__ __attribute__((aligned(16))) float Ks[DC][64 + 4];
-    __shared__ __attribute__((aligned(16))) float Qs[DC][64 + 4];
-    __shared__ __attribute__((aligned(16))) float Vs[DC][128 + 4];
     __shared__ __attribute__((aligned(16))) float Ls[DC][DC + 4];
     __shared__ __attribute__((aligned(16))) float Ts[DC][DC + 4];
     __shared__ float Gs[DC][DC + 1];
     __shared__ float bs[DC], gs[DC];
-    {   // stage (loads at clamped rows, all in flight together; zero / a = 1 past the window's end)
-        float4 kv[8], qv[8], vv[16];
+    // Q fragments (rows ti*16 + r, keys ks*32 + 8g..): clamped rows, zero past the window's end
+    float qf[2][2][8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int i = lane + 64 * k, row = i >> 4, c4 = (i & 15) * 4;
-            kv[k] = *reinterpret_cast<const float4*>(K + (row0 + min(row, n - 1)) * kD + h * 64 + c4);
-            qv[k] = *reinterpret_cast<const float4*>(Q + (row0 + min(row, n - 1)) * kD + h * 64 + c4);
-        }
+    for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int i = lane + 64 * k, row = i >> 5, c4 = (i & 31) * 4;
-            vv[k] = *reinterpret_cast<const float4*>(V + (row0 + min(row, n - 1)) * kVD + h * 128 + c4);
-        }
+        for (int ks = 0; ks < 2; ++ks)
+            load8(Q + (row0 + min(ti * 16 + r, n - 1)) * kD + h * 64 + ks * 32 + 8 * g, qf[ti][ks]);
+    {   // stage K (loads at clamped rows, all in flight together; zero / a = 1 past the window's end)
         float av = 1.0f, bv = 0.0f;
         if (lane < DC) {
             av = dec[(row0 + min(lane, n - 1)) * 8 + h];
             bv = beta[(row0 + min(lane, n - 1)) * 8 + h];
         }
-        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int i = lane + 64 * k, row = i >> 4, c4 = (i & 15) * 4;
-            *reinterpret_cast<float4*>(&Ks[row][c4]) = row < n ? kv[k] : z;
-            *reinterpret_cast<float4*>(&Qs[row][c4]) = row < n ? qv[k] : z;
-        }
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int i = lane + 64 * k, row = i >> 5, c4 = (i & 31) * 4;
-            *reinterpret_cast<float4*>(&Vs[row][c4]) = row < n ? vv[k] : z;
+            const float4 v = *reinterpret_cast<const float4*>(K + (row0 + min(row, n - 1)) * kD + h * 64 + c4);
+            const bool in = row < n;   // per component: a select of whole float4s went through scratch memory
+            *reinterpret_cast<float4*>(&Ks[row][c4]) =
+                make_float4(in ? v.x : 0.0f, in ? v.y : 0.0f, in ? v.z : 0.0f, in ? v.w : 0.0f);
         }
         if (lane < DC) bs[lane] = lane < n ? bv : 0.0f;
         chunk_decays(lane < n ? av : 1.0f, Gs, gs, lane);
     }
+    // V column values of A1V: lane (r, g) takes rows 8g..8g+7 of value columns tc*16 + r (issued now, used last)
+    float vcol[8][8];
+#pragma unroll
+    for (int tc = 0; tc < 8; ++tc)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            vcol[tc][e] = V[(row0 + min(8 * g + e, n - 1)) * kVD + h * 128 + tc * 16 + r];
     __syncthreads();
     // L = b_i G_ij (k_i . k_j) for j < i and P = G_ij (q_i . k_j) for j <= i: tiles (ti, tj) of K K^T and Q K^T,
     // keys in two K steps; tile (0, 1) of both is all zero
@@ -638,7 +637,10 @@ delta_chunk_prep_kernel(const float* __restrict__ Q, const float* __restrict__ K
             for (int ks = 0; ks < 2; ++ks) {
                 V8 ap[P], qp[P], bp[P];
                 frag_lds<T>(&Ks[ti * 16 + r][ks * 32 + 8 * g], ap);
-                frag_lds<T>(&Qs[ti * 16 + r][ks * 32 + 8 * g], qp);
+                float qx[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qx[e] = ti * 16 + r < n ? qf[ti][ks][e] : 0.0f;
+                split8<T>(qx, qp);
                 frag_lds<T>(&Ks[tj * 16 + r][ks * 32 + 8 * g], bp);
                 kk = mfma_split<T>(ap, bp, kk);
                 qk = mfma_split<T>(qp, bp, qk);
@@ -677,29 +679,33 @@ delta_chunk_prep_kernel(const float* __restrict__ Q, const float* __restrict__ K
     }
     __syncthreads();
     // A1V = T diag(b) V (32 x 128) and B1 = T diag(b g) K (32 x 64): one K step over the chunk's 32 tokens
+    V8 tp[2][P];
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti) {
-        V8 ap[P];
-        frag_lds<T>(&Ts[ti * 16 + r][8 * g], ap);
-#pragma unroll 2
-        for (int tc = 0; tc < 8; ++tc) {
-            float y[8];
+    for (int ti = 0; ti < 2; ++ti) frag_lds<T>(&Ts[ti * 16 + r][8 * g], tp[ti]);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) y[e] = bs[8 * g + e] * Vs[8 * g + e][tc * 16 + r];
-            V8 bp[P];
-            split8<T>(y, bp);
-            const f32x4 acc = mfma_split<T>(ap, bp, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    for (int tc = 0; tc < 8; ++tc) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = bs[8 * g + e] * (8 * g + e < n ? vcol[tc][e] : 0.0f);
+        V8 bp[P];
+        split8<T>(y, bp);
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) {
+            const f32x4 acc = mfma_split<T>(tp[ti], bp, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
             for (int e = 0; e < 4; ++e) out[(ti * 16 + 4 * g + e) * 128 + tc * 16 + r] = acc[e];
         }
+    }
 #pragma unroll
-        for (int tk = 0; tk < 4; ++tk) {
-            float y[8];
+    for (int tk = 0; tk < 4; ++tk) {
+        float y[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) y[e] = (bs[8 * g + e] * gs[8 * g + e]) * Ks[8 * g + e][tk * 16 + r];
-            V8 bp[P];
-            split8<T>(y, bp);
-            const f32x4 acc = mfma_split<T>(ap, bp, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        for (int e = 0; e < 8; ++e) y[e] = (bs[8 * g + e] * gs[8 * g + e]) * Ks[8 * g + e][tk * 16 + r];
+        V8 bp[P];
+        split8<T>(y, bp);
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) {
+            const f32x4 acc = mfma_split<T>(tp[ti], bp, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
 #pragma unroll
             for (int e = 0; e < 4; ++e) out[DCO_B1 + (ti * 16 + 4 * g + e) * 64 + tk * 16 + r] = acc[e];
         }
