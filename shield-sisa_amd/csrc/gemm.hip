@@ -1070,13 +1070,18 @@ __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict_
     }
     __syncthreads();
     float(*E)[TAIL_ELD] = Es[wave];
-    for (int nt = wave; nt < TAIL_N / 16; nt += 4) {
-        V8 w[TAIL_K / 32][P];
+    // weight fragments of the wave's next output tile load while the current one computes
+    V8 w[TAIL_K / 32][P], wn[TAIL_K / 32][P];
+    auto load_w = [&](int nt, V8 (&dst)[TAIL_K / 32][P]) {
 #pragma unroll
         for (int ks = 0; ks < TAIL_K / 32; ++ks)
 #pragma unroll
             for (int q = 0; q < P; ++q)
-                w[ks][q] = load_part8<T>(W + q * wstride + (long long)(nt * 16 + r) * TAIL_K + ks * 32 + g * 8);
+                dst[ks][q] = load_part8<T>(W + q * wstride + (long long)(nt * 16 + r) * TAIL_K + ks * 32 + g * 8);
+    };
+    load_w(wave, w);
+    for (int nt = wave; nt < TAIL_N / 16; nt += 4) {
+        if (nt + 4 < TAIL_N / 16) load_w(nt + 4, wn);
         const float b = bias[nt * 16 + r];
         f32x4 acc[4];
 #pragma unroll
@@ -1112,6 +1117,10 @@ __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict_
             out[(f * 16 + tok) * TAIL_N + nt * 16 + r] = (sum / 2.0f) / 3.0f;
         }
         asm volatile("" ::: "memory");
+#pragma unroll
+        for (int ks = 0; ks < TAIL_K / 32; ++ks)
+#pragma unroll
+            for (int q = 0; q < P; ++q) w[ks][q] = wn[ks][q];
     }
 }
 
