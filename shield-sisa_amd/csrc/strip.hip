@@ -1074,11 +1074,11 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 }
 
 //                cin  cexp cout k  s  hs se R  minb
-typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 4> G4;         // 45x80 -> 23x40
+typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 6> G4;         // 45x80 -> 23x40
 typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 6> G5;         // 23x40 (b5, b6)
-typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 2, 3, 0, 0, 0, 16, 1> G7;    // 23x40 -> 12x20
-typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 3, 2, 0, 8, 0, 16, 1> G8;       // 12x20
-typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 3, 2, 0, 8, 0, 16, 1> G9;       // 12x20 (b9, b10)
+typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 3, 2, 0, 0, 0, 16, 1> G7;    // 23x40 -> 12x20
+typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G8;       // 12x20
+typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G9;       // 12x20 (b9, b10)
 typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
 typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6> G12;      // 12x20
 typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 6, 1, 1, 16, 12, 10> G13;   // 12x20 -> 6x10: whole map, 10 columns/tile
