@@ -36,6 +36,13 @@ constexpr int ST_THREADS = 256;   // 4 independent waves; the workgroup shares t
 
 // Workgroup barrier that waits for LDS traffic only (global loads issued before it stay in flight).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The expanded values of an input row outside the map (zero).  Made opaque so that the compiler materialises them only
+// on that (rare, wave-uniform) path instead of hoisting four register moves per row into the common path.
+__device__ __forceinline__ f32x4 zero_rows() {
+    f32x4 z = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    asm volatile("" : "+v"(z));
+    return z;
+}
 
 // v_mfma_f32_16x16x16 fragments (lane l = 16 g + r): A row r, k = 4 g .. 4 g + 3; B column r, k = 4 g ..
 // 4 g + 3; C column r, rows 4 g .. 4 g + 3.  Products as in Split<T> (smallest first).
@@ -380,13 +387,15 @@ __global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int stri
                     for (int j = 0; j < C::IR; ++j)
 #pragma unroll
                         for (int t = 0; t < C::NT; ++t) {
-                            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                            f32x4 acc;
                             if (rin[j]) {   // uniform: the whole wave is on the same input row
                                 acc = init[t];
 #pragma unroll
                                 for (int ks = 0; ks < C::KSI; ++ks) acc = mfma_split16<T>(wf[ks], xf[j][t][ks], acc);
 #pragma unroll
                                 for (int i = 0; i < 4; ++i) acc[i] = relu_nb(acc[i]);
+                            } else {
+                                acc = zero_rows();
                             }
                             e[j][t] = acc;
                         }
@@ -703,7 +712,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
             }
         } else {
 #pragma unroll
-            for (int t = 0; t < C::NT; ++t) e[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int t = 0; t < C::NT; ++t) e[t] = zero_rows();
         }
         // tap variants dx = 0 .. KS-1 of this row for the lane's output column
         f32x4 v[C::KS];
