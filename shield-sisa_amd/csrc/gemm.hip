@@ -527,25 +527,27 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p, int mblocks, 
 inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
 
 // Pre-split A GEMM with direct global -> LDS loads (the sequence GEMMs of the half tiers, whose A arrives already
-// split into the tier's parts).  Workgroup tile 128 x 32 WN, 4 waves of 64 x 16 WN, K steps of 32.
+// split into the tier's parts).  Workgroup tile 64 WGM x 32 WN, 2 WGM waves of 64 x 16 WN, K steps of 32.
 // The operand tiles of a K step are sixteen-row fragment blocks of 1 KB each (A: 8 blocks per part, W: 8 per part),
 // written by global_load_lds_dwordx4 (16 bytes per lane, lane l to byte 16 l of its block) with no register staging,
 // and read back as MFMA fragments.  DMA lane l carries row l / 4 and 16-byte K chunk (l % 4) ^ ((l / 16) % 4) of the
 // block, so that the sixteen lanes of a fragment read (one chunk of rows 0..15) cover the 64 banks once.  NS K steps
-// share an LDS ring (fp16: 2 x 32 KB for 128 x 128 tiles, bf16: 2 x 36 KB for 128 x 64 tiles; two workgroups per
-// CU): a step waits for its own loads (s_waitcnt on the wave's count of younger loads) and one barrier, then issues
+// share an LDS ring (fp16: 2 x 32 KB for 128 x 128 tiles, two 4-wave workgroups per CU; bf16: 2 x 72 KB for
+// 256 x 128 tiles, one 8-wave workgroup per CU): a step waits for its own loads (s_waitcnt on the wave's count of younger loads) and one barrier, then issues
 // the loads of step k + NS - 1 into the slot step k - 1 used.  Per output the MFMA sequence is that of every other MFMA GEMM kernel (K steps in order,
 // the split products in order), so results are bitwise equal to theirs.
-template <typename T, int NS_, int WN_> struct DmaCfg {
+template <typename T, int NS_, int WN_, int WGM_> struct DmaCfg {
     static constexpr int P = Split<T>::P;
     static constexpr int NS = NS_;                            // K steps in flight
     static constexpr int WN = WN_;                            // 16-column tiles per wave (2 x WN per workgroup)
-    static constexpr int AB = 8, WB = 2 * WN;                 // fragment blocks per part: A (128 rows), W
+    static constexpr int WGM = WGM_, WAVES = 2 * WGM_;        // wave rows (64 rows each) x 2 wave columns
+    static constexpr int BM = 64 * WGM;
+    static constexpr int AB = BM / 16, WB = 2 * WN;           // fragment blocks per part: A, W
     static constexpr int BLK = 1024;                          // bytes of one 16 x 32 fragment block
     static constexpr int TB = P * (AB + WB);                  // blocks per K step: [A part][block], [W part][block]
     static constexpr int STAGE = TB * BLK;
-    static constexpr int DPW = TB / 4;                        // loads per wave per K step
-    static_assert(TB % 4 == 0, "the step's blocks are dealt evenly over the 4 waves");
+    static constexpr int DPW = TB / WAVES;                    // loads per wave per K step
+    static_assert(TB % WAVES == 0, "the step's blocks are dealt evenly over the waves");
 };
 
 // the wave's loads of one K step are issued; wait until at most N younger ones are outstanding
@@ -554,11 +556,11 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_block) {
     __builtin_amdgcn_global_load_lds(src, lds_block, 16, 0, 0);
 }
 
-template <typename T, int NS_, int WN_>
-__global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs p, int mblocks, int nblocks) {
+template <typename T, int NS_, int WN_, int WGM_>
+__global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mblocks, int nblocks) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
-    typedef DmaCfg<T, NS_, WN_> D;
+    typedef DmaCfg<T, NS_, WN_, WGM_> D;
     constexpr int P = S::P, NS = D::NS, DPW = D::DPW, AB = D::AB, WB = D::WB;
     constexpr int WM = 4, WN = D::WN, WGN = 2, BN = 16 * WN * WGN;
     __shared__ __attribute__((aligned(1024))) unsigned char ring[NS * D::STAGE];
@@ -568,7 +570,7 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs p, int mblocks, 
     const int xcd = blockIdx.x % XCDS, slot = blockIdx.x / XCDS;
     const int mb = (slot / nblocks) * XCDS + xcd, nb = slot % nblocks;
     if (mb >= mblocks) return;   // uniform over the workgroup
-    const long long m0 = (long long)mb * 128;
+    const long long m0 = (long long)mb * D::BM;
     const int n0 = nb * BN;
     const T* Ah = static_cast<const T*>(p.Ah);
     const T* W = static_cast<const T*>(p.W);
@@ -965,21 +967,24 @@ void launch_direct(const GemmArgs& p, hipStream_t s) {
         hipLaunchKernelGGL((gemm_direct_kernel<T, NT, false>), grid, dim3(64 * MFMA_WAVES), 0, s, p, mblocks, nblocks);
 }
 
-template <typename T, int NS, int WN> void launch_dma_cfg(const GemmArgs& p, hipStream_t s) {
-    const int mblocks = (int)cdiv(p.M, 128), nblocks = (int)cdiv(p.N, 32 * WN);
+template <typename T, int NS, int WN, int WGM> void launch_dma_cfg(const GemmArgs& p, hipStream_t s) {
+    const int mblocks = (int)cdiv(p.M, 64 * WGM), nblocks = (int)cdiv(p.N, 32 * WN);
     const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
     if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_dma: grid too large");
-    hipLaunchKernelGGL((gemm_dma_kernel<T, NS, WN>), dim3((unsigned)blocks), dim3(256), 0, s, p, mblocks, nblocks);
+    hipLaunchKernelGGL((gemm_dma_kernel<T, NS, WN, WGM>), dim3((unsigned)blocks), dim3(128 * WGM), 0, s, p, mblocks,
+                       nblocks);
 }
 
 template <typename T> void launch_dma(const GemmArgs& p, hipStream_t s) {
     if (!p.Ah || p.K % 32 || p.astride % 8 || p.wstride % 8 || p.lda % 8 || p.ldw % 8)
         throw std::runtime_error("gemm_dma: needs pre-split A, K % 32 == 0 and 16-byte aligned rows");
-    // measured per 128-clip step (ring depth, column tiles per wave): fp16 (2,4) 2.26 ms, (2,2) 2.43, (3,2) 2.82,
-    // (3,4) 3.35, (4,2) 4.19; bf16 (2,2) 4.14 ms, (2,4) 4.71, (3,4) 4.79, (3,2) 5.91, (4,2) 6.00.  Deeper rings
-    // lose: the occupancy their LDS costs is worth more than the latency they hide.
-    if constexpr (Split<T>::P == 2) launch_dma_cfg<T, 2, 4>(p, s);
-    else launch_dma_cfg<T, 2, 2>(p, s);
+    // measured per 128-clip step (ring depth, column tiles per wave, waves per workgroup): fp16 (2,4,4) 2.26 ms,
+    // (2,2,4) 2.43, (3,2,4) 2.82, (3,4,4) 3.35, (4,2,4) 4.19, (2,4,8) 2.42; bf16 (2,4,8) 3.42 ms, (2,2,4) 4.14,
+    // (2,4,4) 4.71, (3,4,4) 4.79, (3,2,4) 5.91, (4,2,4) 6.00.  Deeper rings lose: the occupancy their LDS costs is
+    // worth more than the latency they hide.  For bf16 the 8-wave workgroup shares each staged W tile over twice
+    // the rows, which halves the W traffic behind its six products per step.
+    if constexpr (Split<T>::P == 2) launch_dma_cfg<T, 2, 4, 2>(p, s);
+    else launch_dma_cfg<T, 2, 4, 4>(p, s);
 }
 
 // the direct-to-LDS kernel for pre-split A unless SHV_HIP_NO_GEMM_DMA is set (read per launch: the bitwise
