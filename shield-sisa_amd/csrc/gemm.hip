@@ -979,7 +979,7 @@ template <typename T> void launch_dma(const GemmArgs& p, hipStream_t s) {
     if (!p.Ah || p.K % 32 || p.astride % 8 || p.wstride % 8 || p.lda % 8 || p.ldw % 8)
         throw std::runtime_error("gemm_dma: needs pre-split A, K % 32 == 0 and 16-byte aligned rows");
     // measured per 128-clip step (ring depth, column tiles per wave, waves per workgroup): fp16 (2,4,4) 2.26 ms,
-    // (2,2,4) 2.43, (3,2,4) 2.82, (3,4,4) 3.35, (4,2,4) 4.19, (2,4,8) 2.42; bf16 (2,4,8) 3.42 ms, (2,2,4) 4.14,
+    // (2,2,4) 2.43, (3,2,4) 2.82, (3,4,4) 3.35, (4,2,4) 4.19, (2,2,8) 2.30, (2,4,8) 2.42; bf16 (2,4,8) 3.42 ms, (2,2,4) 4.14,
     // (2,4,4) 4.71, (3,4,4) 4.79, (3,2,4) 5.91, (4,2,4) 6.00.  Deeper rings lose: the occupancy their LDS costs is
     // worth more than the latency they hide.  For bf16 the 8-wave workgroup shares each staged W tile over twice
     // the rows, which halves the W traffic behind its six products per step.
