@@ -1092,6 +1092,10 @@ typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
 typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6> G12;      // 12x20
 typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 6, 1, 1, 16, 12, 10> G13;   // 12x20 -> 6x10: whole map, 10 columns/tile
 typedef WgCfg<160, 960, 160, 5, 1, 1, 1, 6, 1, 1, 1, 6> G14;   // 6x10 (b14, b15)
+// bf16 (three operand parts): fewer rows per step where the fp16 row step leaves LDS room for one workgroup per CU
+typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 3> G4B;
+typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 2, 2, 0, 0, 0, 16, 1> G7B;
+typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 4> G12B;
 
 // the block shape the engine pads weights to and sizes the SE partial sums by: tile = (R rows, VALID columns)
 template <class C> IrShape wg_shape() {
@@ -1156,13 +1160,13 @@ bool strip_kernels_enabled() {
 
 bool ir_strip_shape(int block, bool bf16_tier, IrShape* out) {
     switch (block) {
-    case 3: *out = wg_shape<G4>(); return true;
+    case 3: *out = bf16_tier ? wg_shape<G4B>() : wg_shape<G4>(); return true;
     case 4: case 5: *out = wg_shape<G5>(); return true;
-    case 6: *out = wg_shape<G7>(); return true;
+    case 6: *out = bf16_tier ? wg_shape<G7B>() : wg_shape<G7>(); return true;
     case 7: *out = wg_shape<G8>(); return true;
     case 8: case 9: *out = wg_shape<G9>(); return true;
     case 10: *out = wg_shape<G11>(); return true;
-    case 11: *out = wg_shape<G12>(); return true;
+    case 11: *out = bf16_tier ? wg_shape<G12B>() : wg_shape<G12>(); return true;
     case 12:   // whole-map staging of block 13 fits LDS with two operand parts (fp16) only
         if (bf16_tier) return false;
         *out = wg_shape<G13>();
@@ -1173,17 +1177,18 @@ bool ir_strip_shape(int block, bool bf16_tier, IrShape* out) {
 }
 
 template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hipStream_t s) {
+    constexpr bool IS_BF16 = std::is_same<T, bf16>::value;
     switch (block) {
     case 0: launch_strip<T, S1>(block, a, F, s); return true;
     case 1: launch_strip<T, S2>(block, a, F, s); return true;
     case 2: launch_strip<T, S3>(block, a, F, s); return true;
-    case 3: launch_wgstrip<T, G4>(block, a, F, s); return true;
+    case 3: launch_wgstrip<T, std::conditional_t<IS_BF16, G4B, G4>>(block, a, F, s); return true;
     case 4: case 5: launch_wgstrip<T, G5>(block, a, F, s); return true;
-    case 6: launch_wgstrip<T, G7>(block, a, F, s); return true;
+    case 6: launch_wgstrip<T, std::conditional_t<IS_BF16, G7B, G7>>(block, a, F, s); return true;
     case 7: launch_wgstrip<T, G8>(block, a, F, s); return true;
     case 8: case 9: launch_wgstrip<T, G9>(block, a, F, s); return true;
     case 10: launch_wgstrip<T, G11>(block, a, F, s); return true;
-    case 11: launch_wgstrip<T, G12>(block, a, F, s); return true;
+    case 11: launch_wgstrip<T, std::conditional_t<IS_BF16, G12B, G12>>(block, a, F, s); return true;
     case 12:
         if constexpr (std::is_same<T, f16>::value) {
             launch_wgstrip<T, G13>(block, a, F, s);
