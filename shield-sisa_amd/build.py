@@ -6,8 +6,10 @@ Outputs (shield-sisa_amd/lib/):
   libshv_synth.so                  seeded synthetic weights / crops (host only, gcc)
 
 The compute revision (shv_hip_compute_revision) is "hip-" + the first 16 hex digits of the SHA-256 over the
-SHA-256 digests of the numeric sources, in a fixed order, so any change to kernel or layout code invalidates
-certificates (the reference does the same for its CUDA sources: engine/cuda/gen_revision.cmake:1-17).
+SHA-256 digests of the numeric sources, in a fixed order, followed by the build recipe that turns them into machine
+code (target architecture, compiler path and version, every flag and the per-source flag choices), so a change to
+kernel or layout code, to a flag or to the compiler invalidates certificates (the reference hashes its CUDA sources
+and its CMakeLists.txt: engine/cuda/gen_revision.cmake:1-17, engine/cuda/CMakeLists.txt:20-25).
 """
 from __future__ import annotations
 
@@ -29,7 +31,9 @@ NUMERIC_SOURCES = ["dev_common.hpp", "mfma.hpp", "kernels.hpp", "gemm.hip", "cnn
                    "engine.hpp", "engine.hip",
                    "host_model.hpp", "host_model.cpp"]
 DEVICE_SOURCES = ["gemm.hip", "cnn.hip", "fused.hip", "strip.hip", "seq.hip", "engine.hip", "crop.hip"]
-HOST_SOURCES = ["host_model.cpp"]
+HOST_SOURCES = ["host_model.cpp", "sched.cpp", "cert.cpp"]
+HIP_HOST_SOURCES = ["lanes.cpp"]          # host code that calls the HIP runtime
+API_SOURCE = "capi.cpp"                   # built twice: certified and experimental
 C_SOURCES = ["sha256.c"]
 
 ARCH = os.environ.get("SHV_HIP_ARCH", "gfx950")
@@ -47,10 +51,29 @@ VGPR_FORM_SOURCES = {"strip.hip", "gemm.hip"}
 VGPR_FORM_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
+def _compiler_version() -> str:
+    try:
+        r = subprocess.run([HIPCC, "--version"], capture_output=True, text=True, timeout=60)
+        return r.stdout.strip()
+    except (OSError, subprocess.SubprocessError):
+        return "unknown"
+
+
+def recipe() -> str:
+    """The part of the build that decides the numerics besides the sources: one canonical text."""
+    lines = ["arch=" + ARCH, "hipcc=" + HIPCC, "compiler=" + _compiler_version(), "common=" + " ".join(COMMON),
+             "device=" + " ".join(DEVICE_FLAGS)]
+    for src in DEVICE_SOURCES:
+        extra = VGPR_FORM_FLAGS if src in VGPR_FORM_SOURCES else []
+        lines.append(f"{src}: " + " ".join(extra))
+    return "\n".join(lines)
+
+
 def revision() -> str:
     h = hashlib.sha256()
     for name in NUMERIC_SOURCES:
         h.update(hashlib.sha256((CSRC / name).read_bytes()).hexdigest().encode())
+    h.update(hashlib.sha256(recipe().encode()).hexdigest().encode())
     return "hip-" + h.hexdigest()[:16]
 
 
@@ -80,11 +103,15 @@ def build(verbose: bool = False) -> dict:
         o = OBJ / (src + ".o")
         jobs.append(["gcc", "-O2", "-fPIC", "-fvisibility=hidden", "-c", str(CSRC / src), "-o", str(o)])
         objs.append(o)
-    api = OBJ / "api.cpp.o"
-    api_exp = OBJ / "api_experimental.cpp.o"
     host_hip = ["-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include", "-I", str(INCLUDE), revdef]
-    jobs.append([HIPCC, *COMMON, *host_hip, "-c", str(CSRC / "api.cpp"), "-o", str(api)])
-    jobs.append([HIPCC, *COMMON, *host_hip, "-DSHV_HIP_EXPERIMENTAL=1", "-c", str(CSRC / "api.cpp"), "-o",
+    for src in HIP_HOST_SOURCES:
+        o = OBJ / (src + ".o")
+        jobs.append([HIPCC, *COMMON, *host_hip, "-c", str(CSRC / src), "-o", str(o)])
+        objs.append(o)
+    api = OBJ / "capi.cpp.o"
+    api_exp = OBJ / "capi_experimental.cpp.o"
+    jobs.append([HIPCC, *COMMON, *host_hip, "-c", str(CSRC / API_SOURCE), "-o", str(api)])
+    jobs.append([HIPCC, *COMMON, *host_hip, "-DSHV_HIP_EXPERIMENTAL=1", "-c", str(CSRC / API_SOURCE), "-o",
                  str(api_exp)])
     synth = LIB / "libshv_synth.so"
     jobs.append(["gcc", "-O2", "-fPIC", "-shared", "-fvisibility=hidden", "-o", str(synth) + ".tmp",

@@ -1,12 +1,13 @@
 // MobileNetV3 kernels other than the 1x1 convolutions (those are GEMMs): stem, depthwise, SE squeeze, 4x4 pool,
-// and the on-GPU weight repacker.  NHWC activations in storage type T, fp32 arithmetic.  Every output element is
-// computed by the reference CPU engine's sequence of operations (engine/model/isa_impl.hpp:558-643, 757-769,
-// 827-842), so the fp32 tier is bitwise equal to it; padding taps are skipped (adding a zero product changes
-// at most the sign of a zero).
+// and the on-GPU weight repacker.  NHWC fp32 activations.  Every output element is computed by the reference CPU
+// engine's sequence of operations (engine/model/isa_impl.hpp:558-643, 757-769, 827-842), so the fp32 tier is bitwise
+// equal to it.  The stem and the depthwise stage their inputs in LDS tiles with zeros outside the map, as the
+// reference pads its rows.
 #include "dev_common.hpp"
 #include "kernels.hpp"
 
 #include <stdexcept>
+#include <type_traits>
 
 namespace shv {
 namespace {
@@ -14,34 +15,43 @@ namespace {
 inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + b - 1) / b); }
 
 // ------------------------------------------------------------------------------------------------ stem
-// one thread per output pixel: 3x3 stride-2 conv over the LUT-normalised input (fma chain over (dy, dx, c)),
-// + bias, hardswish, 16 channels stored as two 16-byte (half) / 32-byte (fp32) vectors
-template <typename T>
-__global__ void __launch_bounds__(256)
-stem_kernel(const uint8_t* __restrict__ in, T* __restrict__ out, const float* __restrict__ lut,
-            const float* __restrict__ w, const float* __restrict__ b, int F) {
-    // the byte -> float table in LDS (per-lane index); weights and bias are read at wave-uniform constant offsets,
-    // which the compiler serves from the scalar data cache into SGPR operands
+// A workgroup owns a 6 x 32 tile of output pixels of one frame, one pixel per thread.  The 13 x 65 input patch
+// that tile needs (stride 2, pad 1) is normalised through the byte -> float table into LDS once, zeros outside the
+// image like the reference's padded rows (isa_impl.hpp:558-600); each pixel's 16 channels are then the fma chain
+// over (dy, dx, c) from +0, + bias, hardswish.  The 27 x 16 weights are read at wave-uniform addresses (scalar
+// loads into SGPR operands), one tap at a time.
+constexpr int kStemTH = 6, kStemTW = 32;
+__global__ void __launch_bounds__(kStemTH * kStemTW)
+stem_tile_kernel(const uint8_t* __restrict__ in, float* __restrict__ out, const float* __restrict__ lut,
+                 const float* __restrict__ w, const float* __restrict__ b) {
+    constexpr int IH = 2 * kStemTH + 1, IW3 = (2 * kStemTW + 1) * 3;   // 13 rows x 65 pixels x 3 channels
+    constexpr int NT = kStemTH * kStemTW;
     __shared__ float slut[768];
-    for (int i = threadIdx.x; i < 768; i += blockDim.x) slut[i] = lut[i];
+    __shared__ float patch[IH * IW3];
+    for (int i = threadIdx.x; i < 768; i += NT) slut[i] = lut[i];
     __syncthreads();
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long long)F * 90 * 160) return;
-    const int ox = int(idx % 160), oy = int((idx / 160) % 90);
-    const long long f = idx / (90 * 160);
+    const int oy0 = blockIdx.y * kStemTH, ox0 = blockIdx.x * kStemTW;
+    const uint8_t* img = in + (size_t)blockIdx.z * (180 * 320 * 3);
+    const int col0 = (2 * ox0 - 1) * 3;                                 // byte column of patch column 0
+    for (int i = threadIdx.x; i < IH * IW3; i += NT) {
+        const int r = i / IW3, q = i - r * IW3;                         // q = 3 * patch column + channel
+        const int iy = 2 * oy0 - 1 + r, bx = col0 + q;
+        float v = 0.0f;
+        if (iy >= 0 && iy < 180 && bx >= 0 && bx < 960) v = slut[(q % 3) * 256 + img[iy * 960 + bx]];
+        patch[i] = v;
+    }
+    __syncthreads();
+    const int ty = threadIdx.x / kStemTW, tx = threadIdx.x - ty * kStemTW;
     float acc[16];
 #pragma unroll
     for (int o = 0; o < 16; ++o) acc[o] = 0.0f;
-    // taps (dy, dx) in order, one at a time (rolled: one tap's 48 weights live in scalar registers)
 #pragma unroll 1
     for (int t = 0; t < 9; ++t) {
         const int dy = t / 3, dx = t - dy * 3;
-        const int iy = 2 * oy - 1 + dy, ix = 2 * ox - 1 + dx;
-        if (iy < 0 || iy >= 180 || ix < 0 || ix >= 320) continue;
-        const uint8_t* px = in + ((f * 180 + iy) * 320 + ix) * 3;
+        const float* px = patch + (2 * ty + dy) * IW3 + (2 * tx + dx) * 3;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-            const float x = slut[c * 256 + px[c]];
+            const float x = px[c];
             const float* wr = w + (t * 3 + c) * 16;
 #pragma unroll
             for (int o = 0; o < 16; ++o) acc[o] = __builtin_fmaf(x, wr[o], acc[o]);
@@ -50,50 +60,60 @@ stem_kernel(const uint8_t* __restrict__ in, T* __restrict__ out, const float* __
     float v[16];
 #pragma unroll
     for (int o = 0; o < 16; ++o) v[o] = hswish(acc[o] + b[o]);
-    store8(out + idx * 16, v);
-    store8(out + idx * 16 + 8, v + 8);
+    float* dst = out + (((size_t)blockIdx.z * 90 + oy0 + ty) * 160 + ox0 + tx) * 16;
+    store8(dst, v);
+    store8(dst + 8, v + 8);
 }
 
 // ------------------------------------------------------------------------------------------------ depthwise
-// one thread per (output pixel, 8 channels): fma chain over (dy, dx) from +0, + bias, activation
-template <typename T, int KS, int S>
+// Depthwise KS x KS, stride S, fp32.  A workgroup owns TH x 8 output pixels x 32 channels of one frame: it stages
+// the input halo [(TH-1)S+KS][7S+KS][32] in LDS with float4 loads (zeros outside the map and beyond C), then each
+// thread takes one channel and one output column and walks the TH rows.  Every output is the fma chain over
+// (dy, dx) in order from +0 -- padding taps add a zero product to a chain that started at +0, which changes
+// nothing, so this equals the reference's chain over zero-padded rows (isa_impl.hpp:603-643) -- + bias, ReLU or
+// hardswish.
+constexpr int kDwTW = 8, kDwCC = 32;
+template <int KS, int S>
 __global__ void __launch_bounds__(256)
-dw_kernel(const T* __restrict__ in, T* __restrict__ out, const float* __restrict__ w, const float* __restrict__ b,
-          int F, int H, int W, int C, int Ho, int Wo, int act) {
-    const int CG = C >> 3;
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long long)F * Ho * Wo * CG) return;
-    const int cg = int(idx % CG);
-    const long long pix = idx / CG;
-    const int ox = int(pix % Wo);
-    const long long fy = pix / Wo;
-    const int oy = int(fy % Ho);
-    const long long f = fy / Ho;
-    constexpr int P = (KS - 1) / 2;
-    const int c0 = cg * 8;
-    float acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-#pragma unroll
-    for (int dy = 0; dy < KS; ++dy) {
-        const int iy = oy * S - P + dy;
-        if (iy < 0 || iy >= H) continue;
-#pragma unroll
-        for (int dx = 0; dx < KS; ++dx) {
-            const int ix = ox * S - P + dx;
-            if (ix < 0 || ix >= W) continue;
-            float x[8], wv[8];
-            load8(in + ((f * H + iy) * W + ix) * C + c0, x);
-            load8(w + (dy * KS + dx) * C + c0, wv);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = __builtin_fmaf(x[i], wv[i], acc[i]);
-        }
+dw_tile_kernel(const float* __restrict__ in, float* __restrict__ out, const float* __restrict__ w,
+               const float* __restrict__ b, int H, int W, int C, int Ho, int Wo, int tiles_x, int act) {
+    constexpr int TH = S == 1 ? 8 : 4;
+    constexpr int IH = (TH - 1) * S + KS, IW = (kDwTW - 1) * S + KS, P = (KS - 1) / 2;
+    __shared__ float4 halo[IH * IW * (kDwCC / 4)];
+    const int f = blockIdx.z, c0 = blockIdx.y * kDwCC;
+    const int ty0 = (blockIdx.x / tiles_x) * TH, tx0 = (blockIdx.x % tiles_x) * kDwTW;
+    const float* src = in + (size_t)f * H * W * C;
+    for (int i = threadIdx.x; i < IH * IW * (kDwCC / 4); i += 256) {
+        const int quad = i % (kDwCC / 4), pix = i / (kDwCC / 4);
+        const int r = pix / IW, cx = pix - r * IW;
+        const int iy = ty0 * S - P + r, ix = tx0 * S - P + cx, ch = c0 + 4 * quad;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (iy >= 0 && iy < H && ix >= 0 && ix < W && ch < C)   // C % 8 == 0: a quad is all in or all out
+            v = *reinterpret_cast<const float4*>(src + ((size_t)iy * W + ix) * C + ch);
+        halo[i] = v;
     }
-    float bb[8], v[8];
-    load8(b + c0, bb);
+    __syncthreads();
+    const int lane_c = threadIdx.x % kDwCC, col = threadIdx.x / kDwCC;
+    const int ch = c0 + lane_c, ox = tx0 + col;
+    if (ch >= C || ox >= Wo) return;
+    float wt[KS * KS];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = apply_act(acc[i] + bb[i], act);
-    store8(out + pix * C + c0, v);
+    for (int t = 0; t < KS * KS; ++t) wt[t] = w[t * C + ch];
+    const float bias = b[ch];
+    const float* hs = reinterpret_cast<const float*>(halo);
+    float* dst = out + (size_t)f * Ho * Wo * C + ch;
+#pragma unroll 1
+    for (int yy = 0; yy < TH; ++yy) {
+        const int oy = ty0 + yy;
+        if (oy >= Ho) break;
+        float acc = 0.0f;
+#pragma unroll
+        for (int dy = 0; dy < KS; ++dy)
+#pragma unroll
+            for (int dx = 0; dx < KS; ++dx)
+                acc = __builtin_fmaf(hs[((yy * S + dy) * IW + col * S + dx) * kDwCC + lane_c], wt[dy * KS + dx], acc);
+        dst[((size_t)oy * Wo + ox) * C] = apply_act(acc + bias, act);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ SE squeeze
@@ -190,18 +210,23 @@ template void launch_repack_pad<bf16>(const float*, bf16*, int, int, int, int, i
 
 template <typename T>
 void launch_stem(const uint8_t* in, T* out, const float* lut, const float* w, const float* b, int F, hipStream_t s) {
-    hipLaunchKernelGGL(stem_kernel<T>, dim3(cdiv((long long)F * 14400, 256)), dim3(256), 0, s, in, out, lut, w, b, F);
+    static_assert(std::is_same<T, float>::value, "activations are fp32 in every tier");
+    hipLaunchKernelGGL(stem_tile_kernel, dim3(160 / kStemTW, 90 / kStemTH, F), dim3(kStemTH * kStemTW), 0, s, in, out,
+                       lut, w, b);
 }
 
 template <typename T>
 void launch_dw(const T* in, T* out, const float* w, const float* b, int F, int H, int W, int C, int K, int S, int Ho,
                int Wo, int act, hipStream_t s) {
+    static_assert(std::is_same<T, float>::value, "activations are fp32 in every tier");
     if (C % 8) throw std::runtime_error("depthwise: C % 8 != 0");
-    const dim3 grid(cdiv((long long)F * Ho * Wo * (C / 8), 256)), blk(256);
-    if (K == 3 && S == 1) hipLaunchKernelGGL((dw_kernel<T, 3, 1>), grid, blk, 0, s, in, out, w, b, F, H, W, C, Ho, Wo, act);
-    else if (K == 3 && S == 2) hipLaunchKernelGGL((dw_kernel<T, 3, 2>), grid, blk, 0, s, in, out, w, b, F, H, W, C, Ho, Wo, act);
-    else if (K == 5 && S == 1) hipLaunchKernelGGL((dw_kernel<T, 5, 1>), grid, blk, 0, s, in, out, w, b, F, H, W, C, Ho, Wo, act);
-    else if (K == 5 && S == 2) hipLaunchKernelGGL((dw_kernel<T, 5, 2>), grid, blk, 0, s, in, out, w, b, F, H, W, C, Ho, Wo, act);
+    const int th = S == 1 ? 8 : 4;
+    const int tiles_x = int(cdiv(Wo, kDwTW)), tiles = tiles_x * int(cdiv(Ho, th));
+    const dim3 grid(tiles, cdiv(C, kDwCC), F), blk(256);
+    if (K == 3 && S == 1) hipLaunchKernelGGL((dw_tile_kernel<3, 1>), grid, blk, 0, s, in, out, w, b, H, W, C, Ho, Wo, tiles_x, act);
+    else if (K == 3 && S == 2) hipLaunchKernelGGL((dw_tile_kernel<3, 2>), grid, blk, 0, s, in, out, w, b, H, W, C, Ho, Wo, tiles_x, act);
+    else if (K == 5 && S == 1) hipLaunchKernelGGL((dw_tile_kernel<5, 1>), grid, blk, 0, s, in, out, w, b, H, W, C, Ho, Wo, tiles_x, act);
+    else if (K == 5 && S == 2) hipLaunchKernelGGL((dw_tile_kernel<5, 2>), grid, blk, 0, s, in, out, w, b, H, W, C, Ho, Wo, tiles_x, act);
     else throw std::runtime_error("depthwise: unsupported kernel/stride");
 }
 

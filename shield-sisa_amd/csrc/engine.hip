@@ -18,38 +18,40 @@
 
 namespace shv {
 
+namespace {
+struct ModeName {
+    Precision p;
+    const char* name;
+};
+constexpr ModeName kModes[] = {{Precision::FP32, "fp32"}, {Precision::BF16, "bf16"}, {Precision::FP16, "fp16"}};
+
+// Batch sizes run padded to a bucket so that one HIP graph serves every size in it: n rounded up to a multiple of
+// a power of two about n / 8 (at most 12.5% padding, eight buckets per octave), never above the configured maximum.
+int bucket_for(int n, int max_n) {
+    if (n > max_n) throw std::runtime_error("batch larger than the configured maximum");
+    int top = 1;
+    while (top * 2 <= n) top *= 2;
+    const int quantum = std::max(1, top / 8);
+    return std::min(max_n, (n + quantum - 1) / quantum * quantum);
+}
+}  // namespace
+
 const char* precision_name(Precision p) {
-    switch (p) {
-    case Precision::FP32: return "fp32";
-    case Precision::BF16: return "bf16";
-    case Precision::FP16: return "fp16";
-    }
+    for (const ModeName& m : kModes)
+        if (m.p == p) return m.name;
     return "?";
 }
 bool parse_precision(const std::string& s, Precision* p) {
-    if (s == "fp32") { *p = Precision::FP32; return true; }
-    if (s == "bf16") { *p = Precision::BF16; return true; }
-    if (s == "fp16") { *p = Precision::FP16; return true; }
+    for (const ModeName& m : kModes)
+        if (s == m.name) {
+            *p = m.p;
+            return true;
+        }
     return false;
 }
 
-// batch buckets: a graph per bucket size; sizes between buckets run padded to the next one
-static std::vector<int> make_buckets(int maxv) {
-    static const int base[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128, 160, 192, 256,
-                               320, 384, 448, 512, 640, 768, 896, 1024, 1280, 1536, 2048, 2560, 3072, 4096};
-    std::vector<int> b;
-    for (int v : base)
-        if (v < maxv) b.push_back(v);
-    b.push_back(maxv);
-    return b;
-}
-static int bucket_of(const std::vector<int>& b, int n) {
-    for (int v : b)
-        if (v >= n) return v;
-    throw std::runtime_error("batch larger than the configured maximum");
-}
-int Engine::frame_bucket(int F) const { return cfg_.use_graphs ? bucket_of(fbuckets_, F) : F; }
-int Engine::window_bucket(int B) const { return cfg_.use_graphs ? bucket_of(wbuckets_, B) : B; }
+int Engine::frame_bucket(int F) const { return cfg_.use_graphs ? bucket_for(F, cfg_.max_frames) : F; }
+int Engine::window_bucket(int B) const { return cfg_.use_graphs ? bucket_for(B, cfg_.max_windows) : B; }
 
 // ------------------------------------------------------------------------------------------------ profiling
 int Engine::family_id(const char* name) {
@@ -167,8 +169,6 @@ public:
         if (cfg_.max_frames < 1 || cfg_.max_windows < 1 || cfg_.slots < 1 || cfg_.slots > 4 ||
             cfg_.max_host_tokens < 0)
             throw std::runtime_error("invalid engine configuration");
-        fbuckets_ = make_buckets(cfg_.max_frames);
-        wbuckets_ = make_buckets(cfg_.max_windows);
         // half tiers run the fused inverted-residual kernels unless SHV_HIP_NO_FUSE is set (layer-by-layer A/B)
         const char* nf = std::getenv("SHV_HIP_NO_FUSE");
         fused_ = !kF32 && !(nf && *nf && std::strcmp(nf, "0") != 0);
@@ -183,11 +183,13 @@ public:
         SHV_HIP_CHECK(hipStreamSynchronize(setup_));
         SHV_HIP_CHECK(hipStreamDestroy(setup_));
         setup_ = nullptr;
+        SHV_HIP_CHECK(hipStreamCreateWithFlags(&capture_, hipStreamNonBlocking));
         weight_bytes_ = wmem_.bytes();
         device_bytes_ = wmem_.bytes() + amem_.bytes();
     }
     ~EngineT() override {
         for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
+        if (capture_) (void)hipStreamDestroy(capture_);
         for (const Pending& p : pending_) { (void)hipEventDestroy(p.e0); (void)hipEventDestroy(p.e1); }
         for (hipEvent_t e : event_pool_) (void)hipEventDestroy(e);
     }
@@ -197,31 +199,37 @@ public:
         if (F > cfg_.max_frames) throw std::runtime_error("encode: too many frames");
         const Slot& sl = slots_.at(size_t(slot));
         const int Fb = frame_bucket(F);
-        run_graph(GraphKey{0, sl.d_frames, sl.d_tokens, Fb}, s, [&] { run_encode(sl.d_frames, Fb, sl.d_tokens, s); });
+        run_graph(GraphKey{0, sl.d_frames, sl.d_tokens, Fb}, s,
+                  [&](hipStream_t q) { run_encode(sl.d_frames, Fb, sl.d_tokens, q); });
     }
     void classify_slot(int slot, int B, hipStream_t s) override {
         if (B <= 0) return;
         if (B > cfg_.max_windows) throw std::runtime_error("classify: too many windows");
         const Slot& sl = slots_.at(size_t(slot));
         const int Bb = window_bucket(B);
-        run_graph(GraphKey{1, sl.d_tokptr, sl.d_logits, Bb}, s, [&] { run_classify(sl.d_tokptr, Bb, sl.d_logits, s); });
+        run_graph(GraphKey{1, sl.d_tokptr, sl.d_logits, Bb}, s,
+                  [&](hipStream_t q) { run_classify(sl.d_tokptr, Bb, sl.d_logits, q); });
     }
     void encode_direct(const uint8_t* d_frames, int F, float* d_tokens, hipStream_t s) override {
         if (F <= 0) return;
         if (F > cfg_.max_frames) throw std::runtime_error("encode: too many frames");
-        run_graph(GraphKey{2, d_frames, d_tokens, F}, s, [&] { run_encode(d_frames, F, d_tokens, s); });
+        run_graph(GraphKey{2, d_frames, d_tokens, F}, s, [&](hipStream_t q) { run_encode(d_frames, F, d_tokens, q); });
     }
     void forward_direct(const uint8_t* d_frames, int n, float* d_logits, hipStream_t s) override {
         if (n <= 0) return;
         if (n > cfg_.max_windows || n * kFrames > cfg_.max_frames) throw std::runtime_error("forward: too many clips");
-        run_graph(GraphKey{3, d_frames, d_logits, n}, s, [&] {
-            run_encode(d_frames, n * kFrames, tok_direct_, s);
-            run_classify(tokptr_direct_, n, d_logits, s);
+        run_graph(GraphKey{3, d_frames, d_logits, n}, s, [&](hipStream_t q) {
+            run_encode(d_frames, n * kFrames, tok_direct_, q);
+            run_classify(tokptr_direct_, n, d_logits, q);
         });
     }
 
 private:
     hipStream_t setup_ = nullptr;
+    // Graphs are captured on this private stream, never on a work stream: another thread may be waiting on an event
+    // of the work stream (the scheduler lands one lane while it starts the other), and that wait must not meet a
+    // stream in capture mode.
+    hipStream_t capture_ = nullptr;
     DevMem wmem_, amem_, staging_;
 
     // ---------------------------------------------------------------- weights
@@ -486,23 +494,24 @@ private:
 
     // ---------------------------------------------------------------- graphs
     std::map<GraphKey, hipGraphExec_t> graphs_;
+    // body(q) issues the pass on stream q: directly on s, or into a graph captured on capture_ and launched on s
     template <class F> void run_graph(const GraphKey& key, hipStream_t s, F&& body) {
         if (!cfg_.use_graphs || !dump_dir_.empty() || prof_on_) {
-            body();
+            body(s);
             return;
         }
         auto it = graphs_.find(key);
         if (it == graphs_.end()) {
             hipGraph_t g = nullptr;
-            SHV_HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            SHV_HIP_CHECK(hipStreamBeginCapture(capture_, hipStreamCaptureModeThreadLocal));
             try {
-                body();
+                body(capture_);
             } catch (...) {
-                (void)hipStreamEndCapture(s, &g);
+                (void)hipStreamEndCapture(capture_, &g);
                 if (g) (void)hipGraphDestroy(g);
                 throw;
             }
-            SHV_HIP_CHECK(hipStreamEndCapture(s, &g));
+            SHV_HIP_CHECK(hipStreamEndCapture(capture_, &g));
             hipGraphExec_t ex = nullptr;
             const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);

@@ -76,7 +76,6 @@ protected:
     Precision prec_ = Precision::FP32;
     EngineConfig cfg_;
     std::vector<Slot> slots_;
-    std::vector<int> fbuckets_, wbuckets_;
     size_t weight_bytes_ = 0, device_bytes_ = 0;
     std::string dump_dir_;
 

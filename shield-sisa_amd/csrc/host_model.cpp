@@ -6,13 +6,16 @@
 
 #include "sha256.h"
 
+#include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <iterator>
 #include <map>
-#include <set>
-#include <sstream>
+#include <memory>
 #include <stdexcept>
+#include <unordered_map>
 
 namespace shv {
 
@@ -25,153 +28,267 @@ const BlockCfg kBlocks[15] = {
 
 namespace {
 
-struct Tensor {
-    std::vector<int> shape;
-    std::vector<float> data;
-};
-
-class TensorSet {
+// ------------------------------------------------------------------------------------------ SHLDV001 container
+// "SHLDV001", u32 tensor count, then per tensor: u32 name length, name bytes, u32 rank, u32 dims[rank],
+// u64 element count, fp32 values (little endian); nothing after the last tensor (tools/export_v.py:3-8).
+class Cursor {
 public:
-    std::map<std::string, Tensor> all;
-    std::set<std::string> taken;
-
-    const std::vector<float>& get(const std::string& name, std::initializer_list<int> shape) {
-        auto it = all.find(name);
-        if (it == all.end()) throw std::runtime_error("weights: missing tensor " + name);
-        if (it->second.shape != std::vector<int>(shape)) {
-            std::ostringstream o;
-            o << "weights: tensor " << name << " has shape [";
-            for (size_t i = 0; i < it->second.shape.size(); ++i) o << (i ? "," : "") << it->second.shape[i];
-            o << "], expected [";
-            size_t i = 0;
-            for (int d : shape) o << (i++ ? "," : "") << d;
-            o << "]";
-            throw std::runtime_error(o.str());
-        }
-        taken.insert(name);
-        return it->second.data;
+    Cursor(const std::vector<uint8_t>& buf) : p_(buf.data()), end_(buf.data() + buf.size()) {}
+    const uint8_t* bytes(size_t n, const char* what) {
+        if (size_t(end_ - p_) < n) throw std::runtime_error(std::string("weights: truncated file (") + what + ")");
+        const uint8_t* at = p_;
+        p_ += n;
+        return at;
     }
-    int dim0(const std::string& name) const {
-        auto it = all.find(name);
-        if (it == all.end() || it->second.shape.empty()) throw std::runtime_error("weights: missing tensor " + name);
-        return it->second.shape[0];
+    template <class U> U number(const char* what) {
+        U v;
+        std::memcpy(&v, bytes(sizeof v, what), sizeof v);
+        return v;
     }
-};
-
-class Reader {
-public:
-    explicit Reader(const std::string& path) : in_(path, std::ios::binary) {
-        if (!in_) throw std::runtime_error("cannot open weights: " + path);
-        shv_sha256_init(&h_);
-    }
-    void read(void* dst, size_t n, const char* what) {
-        in_.read(static_cast<char*>(dst), std::streamsize(n));
-        if (size_t(in_.gcount()) != n) throw std::runtime_error(std::string("weights: truncated file (") + what + ")");
-        shv_sha256_update(&h_, dst, n);
-        bytes_ += n;
-    }
-    template <class U> U scalar(const char* what) {
-        U x{};
-        read(&x, sizeof x, what);
-        return x;
-    }
-    bool at_end() { return in_.peek() == std::char_traits<char>::eof(); }
-    std::string hex() {
-        uint8_t d[32];
-        char out[65];
-        shv_sha256_final(&h_, d);
-        shv_sha256_hex(d, out);
-        return out;
-    }
-    size_t bytes() const { return bytes_; }
+    bool done() const { return p_ == end_; }
 
 private:
-    std::ifstream in_;
-    shv_sha256 h_{};
-    size_t bytes_ = 0;
+    const uint8_t* p_;
+    const uint8_t* end_;
 };
 
-void parse(const std::string& path, TensorSet& ts, std::string& sha, size_t& file_bytes) {
-    Reader r(path);
-    char magic[8];
-    r.read(magic, 8, "magic");
-    if (std::memcmp(magic, "SHLDV001", 8)) throw std::runtime_error("weights: not a SHLDV001 file: " + path);
-    const uint32_t count = r.scalar<uint32_t>("count");
-    if (count == 0 || count > 10000) throw std::runtime_error("weights: invalid tensor count");
-    uint64_t total = 0;
-    for (uint32_t i = 0; i < count; ++i) {
-        const uint32_t nl = r.scalar<uint32_t>("name length");
-        if (nl == 0 || nl > 4096) throw std::runtime_error("weights: invalid tensor name length");
-        std::string name(nl, '\0');
-        r.read(&name[0], nl, "name");
-        const uint32_t rank = r.scalar<uint32_t>("rank");
-        if (rank > 8) throw std::runtime_error("weights: invalid tensor rank");
-        Tensor t;
-        uint64_t elements = 1;
-        for (uint32_t d = 0; d < rank; ++d) {
-            const uint32_t dim = r.scalar<uint32_t>("shape");
-            if (dim == 0 || dim > 10000000u || elements > 100000000u / dim)
-                throw std::runtime_error("weights: invalid shape of " + name);
-            t.shape.push_back(int(dim));
-            elements *= dim;
-        }
-        const uint64_t declared = r.scalar<uint64_t>("element count");
-        total += elements;
-        if (declared != elements || total > 100000000u) throw std::runtime_error("weights: invalid tensor size of " + name);
-        t.data.resize(size_t(elements));
-        r.read(t.data.data(), size_t(elements) * sizeof(float), name.c_str());
-        for (float v : t.data)
-            if (!std::isfinite(v)) throw std::runtime_error("weights: non-finite value in " + name);
-        if (!ts.all.emplace(name, std::move(t)).second) throw std::runtime_error("weights: duplicate tensor " + name);
+// Every tensor of the file, by name; each must be claimed exactly once with its expected shape.
+class Weights {
+public:
+    explicit Weights(const std::string& path) {
+        std::ifstream in(path, std::ios::binary | std::ios::ate);
+        if (!in) throw std::runtime_error("cannot open weights: " + path);
+        const std::streamoff size = in.tellg();
+        file_.resize(size_t(size));
+        in.seekg(0);
+        if (size > 0 && !in.read(reinterpret_cast<char*>(file_.data()), size))
+            throw std::runtime_error("cannot read weights: " + path);
+        uint8_t digest[32];
+        char hex[65];
+        shv_sha256 h;
+        shv_sha256_init(&h);
+        shv_sha256_update(&h, file_.data(), file_.size());
+        shv_sha256_final(&h, digest);
+        shv_sha256_hex(digest, hex);
+        sha_ = hex;
+        index(path);
     }
-    if (!r.at_end()) throw std::runtime_error("weights: trailing data after the last tensor");
-    sha = r.hex();
-    file_bytes = r.bytes();
-}
+    const std::string& sha256() const { return sha_; }
+    size_t file_bytes() const { return file_.size(); }
 
-std::string json_string(const std::string& s, const std::string& key) {
-    const size_t k = s.find("\"" + key + "\"");
-    if (k == std::string::npos) return "";
-    const size_t c = s.find(':', k);
-    if (c == std::string::npos) return "";
-    const size_t q0 = s.find('"', c + 1);
-    if (q0 == std::string::npos) return "";
-    const size_t q1 = s.find('"', q0 + 1);
-    if (q1 == std::string::npos) return "";
-    return s.substr(q0 + 1, q1 - q0 - 1);
-}
+    // the values of `name`, which must have exactly the shape `dims`
+    std::vector<float> take(const std::string& name, std::initializer_list<int> dims) {
+        Entry& e = find(name);
+        if (!std::equal(e.dims.begin(), e.dims.end(), dims.begin(), dims.end()))
+            throw std::runtime_error("weights: tensor " + name + " has shape " + shape_text(e.dims.begin(), e.dims.end()) +
+                                     ", expected " + shape_text(dims.begin(), dims.end()));
+        e.claimed = true;
+        std::vector<float> v(e.count);
+        std::memcpy(v.data(), e.data, e.count * sizeof(float));
+        return v;
+    }
+    // the leading dimension of `name` (for widths the file decides, e.g. the SE squeeze)
+    int leading(const std::string& name) {
+        Entry& e = find(name);
+        if (e.dims.empty()) throw std::runtime_error("weights: tensor " + name + " is a scalar");
+        return e.dims[0];
+    }
+    void expect_all_claimed() const {
+        for (const auto& kv : table_)
+            if (!kv.second.claimed) throw std::runtime_error("weights: unexpected tensor " + kv.first);
+    }
 
-double read_sidecar(const std::string& path, const std::string& sha) {
-    const std::string jp = path + ".json";
-    std::ifstream in(jp);
-    if (!in) throw std::runtime_error("cannot open " + jp + " (threshold)");
-    std::stringstream ss;
-    ss << in.rdbuf();
-    const std::string s = ss.str();
-    const std::string got = json_string(s, "output_sha256");
-    if (got.empty()) throw std::runtime_error("no output_sha256 in " + jp + " (the sidecar must name its weight file)");
-    if (got != sha)
-        throw std::runtime_error(jp + " output_sha256 " + got + " does not match the weights' SHA-256 " + sha +
+private:
+    struct Entry {
+        std::vector<int> dims;
+        const uint8_t* data = nullptr;   // unaligned fp32 values inside file_
+        size_t count = 0;
+        bool claimed = false;
+    };
+    std::vector<uint8_t> file_;
+    std::string sha_;
+    std::unordered_map<std::string, Entry> table_;
+
+    template <class It> static std::string shape_text(It b, It e) {
+        std::string s = "[";
+        for (It i = b; i != e; ++i) s += (i == b ? "" : ",") + std::to_string(*i);
+        return s + "]";
+    }
+    Entry& find(const std::string& name) {
+        auto it = table_.find(name);
+        if (it == table_.end()) throw std::runtime_error("weights: missing tensor " + name);
+        return it->second;
+    }
+    void index(const std::string& path) {
+        Cursor c(file_);
+        if (std::memcmp(c.bytes(8, "magic"), "SHLDV001", 8) != 0)
+            throw std::runtime_error("weights: not a SHLDV001 file: " + path);
+        const uint32_t n = c.number<uint32_t>("tensor count");
+        if (n < 1 || n > 10000) throw std::runtime_error("weights: invalid tensor count");
+        uint64_t values = 0;
+        for (uint32_t t = 0; t < n; ++t) {
+            const uint32_t len = c.number<uint32_t>("name length");
+            if (len < 1 || len > 4096) throw std::runtime_error("weights: invalid tensor name length");
+            const uint8_t* nm = c.bytes(len, "name");
+            std::string name(reinterpret_cast<const char*>(nm), len);
+            const uint32_t rank = c.number<uint32_t>("rank");
+            if (rank > 8) throw std::runtime_error("weights: invalid tensor rank");
+            Entry e;
+            uint64_t count = 1;
+            for (uint32_t d = 0; d < rank; ++d) {
+                const uint32_t dim = c.number<uint32_t>("shape");
+                if (dim < 1 || dim > 10000000u || count * dim > 100000000u)
+                    throw std::runtime_error("weights: invalid shape of " + name);
+                count *= dim;
+                e.dims.push_back(int(dim));
+            }
+            if (c.number<uint64_t>("element count") != count)
+                throw std::runtime_error("weights: invalid tensor size of " + name);
+            values += count;
+            if (values > 100000000u) throw std::runtime_error("weights: invalid tensor size of " + name);
+            e.count = size_t(count);
+            e.data = c.bytes(e.count * sizeof(float), name.c_str());
+            for (size_t i = 0; i < e.count; ++i) {
+                float v;
+                std::memcpy(&v, e.data + i * sizeof(float), sizeof v);
+                if (!std::isfinite(v)) throw std::runtime_error("weights: non-finite value in " + name);
+            }
+            if (!table_.emplace(std::move(name), std::move(e)).second)
+                throw std::runtime_error("weights: duplicate tensor " + std::string(reinterpret_cast<const char*>(nm), len));
+        }
+        if (!c.done()) throw std::runtime_error("weights: trailing data after the last tensor");
+    }
+};
+
+// ------------------------------------------------------------------------------------------ sidecar JSON
+// The top-level members of a JSON object: strings and numbers kept, nested values skipped.
+class JsonTop {
+public:
+    explicit JsonTop(const std::string& text) : s_(text) {
+        ws();
+        expect('{');
+        ws();
+        if (peek() == '}') return;
+        for (;;) {
+            ws();
+            const std::string key = string_value();
+            ws();
+            expect(':');
+            ws();
+            const char c = peek();
+            if (c == '"') strings_[key] = string_value();
+            else if (c == '-' || (c >= '0' && c <= '9')) numbers_[key] = number_value();
+            else skip_value();
+            ws();
+            if (peek() == ',') { ++i_; continue; }
+            expect('}');
+            return;
+        }
+    }
+    const std::string* str(const std::string& k) const {
+        auto it = strings_.find(k);
+        return it == strings_.end() ? nullptr : &it->second;
+    }
+    bool has(const std::string& k) const { return numbers_.count(k) || strings_.count(k); }
+    const double* num(const std::string& k) const {
+        auto it = numbers_.find(k);
+        return it == numbers_.end() ? nullptr : &it->second;
+    }
+
+private:
+    const std::string& s_;
+    size_t i_ = 0;
+    std::map<std::string, std::string> strings_;
+    std::map<std::string, double> numbers_;
+
+    char peek() const { return i_ < s_.size() ? s_[i_] : '\0'; }
+    void ws() {
+        while (i_ < s_.size() && (s_[i_] == ' ' || s_[i_] == '\n' || s_[i_] == '\r' || s_[i_] == '\t')) ++i_;
+    }
+    void expect(char c) {
+        if (peek() != c) throw std::runtime_error(std::string("malformed JSON (expected '") + c + "')");
+        ++i_;
+    }
+    std::string string_value() {
+        expect('"');
+        std::string out;
+        while (i_ < s_.size() && s_[i_] != '"') {
+            char c = s_[i_++];
+            if (c == '\\') {
+                if (i_ >= s_.size()) break;
+                const char e = s_[i_++];
+                if (e == 'u') { i_ += 4; c = '?'; }   // keys and values used here are ASCII
+                else c = e == 'n' ? '\n' : e == 't' ? '\t' : e == 'r' ? '\r' : e == 'b' ? '\b' : e == 'f' ? '\f' : e;
+            }
+            out.push_back(c);
+        }
+        expect('"');
+        return out;
+    }
+    double number_value() {
+        const char* b = s_.c_str() + i_;
+        char* e = nullptr;
+        const double v = std::strtod(b, &e);
+        if (e == b) throw std::runtime_error("malformed JSON number");
+        i_ += size_t(e - b);
+        return v;
+    }
+    void skip_value() {
+        const char c = peek();
+        if (c == '"') { string_value(); return; }
+        if (c == '{' || c == '[') {
+            const char close = c == '{' ? '}' : ']';
+            ++i_;
+            ws();
+            if (peek() == close) { ++i_; return; }
+            for (;;) {
+                ws();
+                if (c == '{') { string_value(); ws(); expect(':'); ws(); }
+                skip_value();
+                ws();
+                if (peek() == ',') { ++i_; continue; }
+                expect(close);
+                return;
+            }
+        }
+        if (c == '-' || (c >= '0' && c <= '9')) { number_value(); return; }
+        for (const char* lit : {"true", "false", "null"})
+            if (s_.compare(i_, std::strlen(lit), lit) == 0) { i_ += std::strlen(lit); return; }
+        throw std::runtime_error("malformed JSON value");
+    }
+};
+
+// "<weights>.json": output_sha256 must name this file, threshold must be finite in (0, 1).  Returns the threshold.
+double check_sidecar(const std::string& weights, const std::string& sha) {
+    const std::string path = weights + ".json";
+    std::ifstream in(path);
+    if (!in) throw std::runtime_error("cannot open " + path + " (threshold)");
+    const std::string text((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
+    std::unique_ptr<JsonTop> js;
+    try {
+        js.reset(new JsonTop(text));
+    } catch (const std::exception& e) {
+        throw std::runtime_error(path + ": " + e.what());
+    }
+    const std::string* named = js->str("output_sha256");
+    if (!named) throw std::runtime_error("no output_sha256 in " + path + " (the sidecar must name its weight file)");
+    if (*named != sha)
+        throw std::runtime_error(path + " output_sha256 " + *named + " does not match the weights' SHA-256 " + sha +
                                  " (sidecar of another export)");
-    const size_t k = s.find("\"threshold\"");
-    if (k == std::string::npos) throw std::runtime_error("no threshold in " + jp);
-    const size_t c = s.find(':', k);
-    if (c == std::string::npos) throw std::runtime_error("bad threshold in " + jp);
-    const char* b = s.c_str() + c + 1;
-    char* e = nullptr;
-    const double v = std::strtod(b, &e);
-    if (e == b) throw std::runtime_error("bad threshold in " + jp);
-    if (!(v > 0.0 && v < 1.0)) throw std::runtime_error("threshold out of (0,1) in " + jp);
-    return v;
+    if (!js->has("threshold")) throw std::runtime_error("no threshold in " + path);
+    const double* t = js->num("threshold");
+    if (!t) throw std::runtime_error("bad threshold in " + path);
+    if (!(*t > 0.0 && *t < 1.0)) throw std::runtime_error("threshold out of (0,1) in " + path);
+    return *t;
 }
 
 // conv weight [out][per] followed by BatchNorm2d(eps 1e-3): scale s = gamma / sqrt(var + eps) in double
-void fold_bn(TensorSet& ts, const std::vector<float>& w, int out, int per, const std::string& bn,
+void fold_bn(Weights& ts, const std::vector<float>& w, int out, int per, const std::string& bn,
              std::vector<float>& wf, std::vector<float>& bf) {
-    const auto& g = ts.get(bn + ".weight", {out});
-    const auto& beta = ts.get(bn + ".bias", {out});
-    const auto& mean = ts.get(bn + ".running_mean", {out});
-    const auto& var = ts.get(bn + ".running_var", {out});
+    const auto& g = ts.take(bn + ".weight", {out});
+    const auto& beta = ts.take(bn + ".bias", {out});
+    const auto& mean = ts.take(bn + ".running_mean", {out});
+    const auto& var = ts.take(bn + ".running_var", {out});
     wf.assign(size_t(out) * per, 0.0f);
     bf.assign(size_t(out), 0.0f);
     for (int o = 0; o < out; ++o) {
@@ -194,29 +311,13 @@ float softplus_host(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
 }  // namespace
 
-std::string sha256_file(const std::string& path) {
-    std::ifstream in(path, std::ios::binary);
-    if (!in) throw std::runtime_error("cannot open " + path);
-    shv_sha256 h;
-    shv_sha256_init(&h);
-    std::vector<char> buf(1 << 20);
-    while (in) {
-        in.read(buf.data(), std::streamsize(buf.size()));
-        if (in.gcount() > 0) shv_sha256_update(&h, buf.data(), size_t(in.gcount()));
-    }
-    uint8_t d[32];
-    char out[65];
-    shv_sha256_final(&h, d);
-    shv_sha256_hex(d, out);
-    return out;
-}
-
 HostModel load_host_model(const std::string& path) {
     HostModel hm;
     hm.path = path;
-    TensorSet ts;
-    parse(path, ts, hm.sha256, hm.file_bytes);
-    hm.threshold = read_sidecar(path, hm.sha256);
+    Weights ts(path);
+    hm.sha256 = ts.sha256();
+    hm.file_bytes = ts.file_bytes();
+    hm.threshold = check_sidecar(path, hm.sha256);
 
     // uint8 -> ((v / 255) - mean) / std, float32 (runtime.cpp:224-230, prepare_clips)
     const float mean[3] = {0.485f, 0.456f, 0.406f}, stdv[3] = {0.229f, 0.224f, 0.225f};
@@ -228,7 +329,7 @@ HostModel load_host_model(const std::string& path) {
         }
 
     std::vector<float> wf, bf;
-    fold_bn(ts, ts.get("cnn.0.0.weight", {16, 3, 3, 3}), 16, 27, "cnn.0.1", wf, bf);
+    fold_bn(ts, ts.take("cnn.0.0.weight", {16, 3, 3, 3}), 16, 27, "cnn.0.1", wf, bf);
     hm.stem_w.assign(27 * 16, 0.0f);
     for (int o = 0; o < 16; ++o)
         for (int c = 0; c < 3; ++c)
@@ -252,12 +353,12 @@ HostModel load_host_model(const std::string& path) {
         int j = 0;
         if (B.has_expand) {
             const std::string p = pre + std::to_string(j++);
-            fold_bn(ts, ts.get(p + ".0.weight", {c.cexp, c.cin, 1, 1}), c.cexp, c.cin, p + ".1", wf, bf);
+            fold_bn(ts, ts.take(p + ".0.weight", {c.cexp, c.cin, 1, 1}), c.cexp, c.cin, p + ".1", wf, bf);
             B.expand = linear(wf, c.cexp, c.cin, &bf);
         }
         {
             const std::string p = pre + std::to_string(j++);
-            fold_bn(ts, ts.get(p + ".0.weight", {c.cexp, 1, c.k, c.k}), c.cexp, c.k * c.k, p + ".1", wf, bf);
+            fold_bn(ts, ts.take(p + ".0.weight", {c.cexp, 1, c.k, c.k}), c.cexp, c.k * c.k, p + ".1", wf, bf);
             B.dw_w.assign(size_t(c.k) * c.k * c.cexp, 0.0f);
             for (int ch = 0; ch < c.cexp; ++ch)
                 for (int t = 0; t < c.k * c.k; ++t) B.dw_w[size_t(t) * c.cexp + ch] = wf[size_t(ch) * c.k * c.k + t];
@@ -265,31 +366,31 @@ HostModel load_host_model(const std::string& path) {
         }
         if (c.se) {
             const std::string p = pre + std::to_string(j++);
-            B.csq = ts.dim0(p + ".fc1.weight");  // squeeze width from the file (torchvision make_divisible)
-            const auto& w1 = ts.get(p + ".fc1.weight", {B.csq, c.cexp, 1, 1});
-            const auto& b1 = ts.get(p + ".fc1.bias", {B.csq});
-            const auto& w2 = ts.get(p + ".fc2.weight", {c.cexp, B.csq, 1, 1});
-            const auto& b2 = ts.get(p + ".fc2.bias", {c.cexp});
+            B.csq = ts.leading(p + ".fc1.weight");  // squeeze width from the file (torchvision make_divisible)
+            const auto& w1 = ts.take(p + ".fc1.weight", {B.csq, c.cexp, 1, 1});
+            const auto& b1 = ts.take(p + ".fc1.bias", {B.csq});
+            const auto& w2 = ts.take(p + ".fc2.weight", {c.cexp, B.csq, 1, 1});
+            const auto& b2 = ts.take(p + ".fc2.bias", {c.cexp});
             B.se1 = linear(w1, B.csq, c.cexp, &b1);
             B.se2 = linear(w2, c.cexp, B.csq, &b2);
         }
         {
             const std::string p = pre + std::to_string(j++);
-            fold_bn(ts, ts.get(p + ".0.weight", {c.cout, c.cexp, 1, 1}), c.cout, c.cexp, p + ".1", wf, bf);
+            fold_bn(ts, ts.take(p + ".0.weight", {c.cout, c.cexp, 1, 1}), c.cout, c.cexp, p + ".1", wf, bf);
             B.project = linear(wf, c.cout, c.cexp, &bf);
         }
         H = B.Ho;
         W = B.Wo;
     }
     if (H != 6 || W != 10) throw std::runtime_error("internal: unexpected CNN map size");
-    fold_bn(ts, ts.get("cnn.16.0.weight", {960, 160, 1, 1}), 960, 160, "cnn.16.1", wf, bf);
+    fold_bn(ts, ts.take("cnn.16.0.weight", {960, 160, 1, 1}), 960, 160, "cnn.16.1", wf, bf);
     hm.last = linear(wf, 960, 160, &bf);
-    hm.proj = linear(ts.get("projection.weight", {kD, 960}), kD, 960);
+    hm.proj = linear(ts.take("projection.weight", {kD, 960}), kD, 960);
 
     {
-        const auto& te = ts.get("time_embedding", {20, kD});
-        const auto& re = ts.get("row_embedding", {4, kD});
-        const auto& ce = ts.get("col_embedding", {4, kD});
+        const auto& te = ts.take("time_embedding", {20, kD});
+        const auto& re = ts.take("row_embedding", {4, kD});
+        const auto& ce = ts.take("col_embedding", {4, kD});
         hm.pos.assign(size_t(320) * kD, 0.0f);
         for (int t = 0; t < 20; ++t)
             for (int r = 0; r < 4; ++r)
@@ -298,18 +399,18 @@ HostModel load_host_model(const std::string& path) {
                         volatile float a = te[size_t(t) * kD + d] + re[size_t(r) * kD + d];
                         hm.pos[(size_t(t) * 16 + r * 4 + c) * kD + d] = a + ce[size_t(c) * kD + d];
                     }
-        hm.readout = ts.get("readout", {1, 1, kD});
+        hm.readout = ts.take("readout", {1, 1, kD});
     }
 
     for (int g = 0; g < 2; ++g) {
         GdnHost& G = hm.gdn[g];
         const std::string p = g == 0 ? "gdn_a." : "gdn_b.";
         const std::string x = p + "mixer.";
-        G.norm_w = ts.get(p + "norm.weight", {kD});
-        G.ffn_norm_w = ts.get(p + "ffn_norm.weight", {kD});
+        G.norm_w = ts.take(p + "norm.weight", {kD});
+        G.ffn_norm_w = ts.take(p + "ffn_norm.weight", {kD});
         std::vector<float> w(size_t(kGn) * kD, 0.0f);
         auto put = [&](const char* n, int rows, int at) {
-            const auto& src = ts.get(x + n, {rows, kD});
+            const auto& src = ts.take(x + n, {rows, kD});
             std::memcpy(&w[size_t(at) * kD], src.data(), sizeof(float) * size_t(rows) * kD);
         };
         put("q_proj.weight", 384, kGq);
@@ -324,34 +425,34 @@ HostModel load_host_model(const std::string& path) {
         const char* convs[3] = {"q_conv1d", "k_conv1d", "v_conv1d"};
         const int widths[3] = {384, 384, 768}, offs[3] = {0, 384, 768};
         for (int i = 0; i < 3; ++i) {
-            const auto& wt = ts.get(x + convs[i] + ".weight", {widths[i], 1, 4});
-            const auto& bt = ts.get(x + convs[i] + ".bias", {widths[i]});
+            const auto& wt = ts.take(x + convs[i] + ".weight", {widths[i], 1, 4});
+            const auto& bt = ts.take(x + convs[i] + ".bias", {widths[i]});
             for (int c = 0; c < widths[i]; ++c) {
                 for (int j = 0; j < 4; ++j) G.conv_w[size_t(j) * 1536 + offs[i] + c] = wt[size_t(c) * 4 + j];
                 G.conv_b[size_t(offs[i]) + c] = bt[c];
             }
         }
-        const auto& al = ts.get(x + "A_log", {kHeads});
-        const auto& dt = ts.get(x + "dt_bias", {kHeads});
+        const auto& al = ts.take(x + "A_log", {kHeads});
+        const auto& dt = ts.take(x + "dt_bias", {kHeads});
         for (int h = 0; h < kHeads; ++h) {
             G.neg_rate[h] = -expf(al[h]);
             G.dt_bias[h] = dt[h];
         }
-        G.o_norm_w = ts.get(x + "o_norm.weight", {kDV});
-        G.out = linear(ts.get(x + "o_proj.weight", {kD, kVD}), kD, kVD);
-        G.gate = linear(ts.get(p + "ffn.gate.weight", {kFF, kD}), kFF, kD);
-        G.up = linear(ts.get(p + "ffn.up.weight", {kFF, kD}), kFF, kD);
-        G.down = linear(ts.get(p + "ffn.down.weight", {kD, kFF}), kD, kFF);
+        G.o_norm_w = ts.take(x + "o_norm.weight", {kDV});
+        G.out = linear(ts.take(x + "o_proj.weight", {kD, kVD}), kD, kVD);
+        G.gate = linear(ts.take(p + "ffn.gate.weight", {kFF, kD}), kFF, kD);
+        G.up = linear(ts.take(p + "ffn.up.weight", {kFF, kD}), kFF, kD);
+        G.down = linear(ts.take(p + "ffn.down.weight", {kD, kFF}), kD, kFF);
     }
 
     {
         SisaHost& S = hm.sisa;
         const std::string a = "sisa.attn.";
-        S.attn_norm_w = ts.get("sisa.attn_norm.weight", {kD});
-        S.ffn_norm_w = ts.get("sisa.ffn_norm.weight", {kD});
+        S.attn_norm_w = ts.take("sisa.attn_norm.weight", {kD});
+        S.ffn_norm_w = ts.take("sisa.ffn_norm.weight", {kD});
         std::vector<float> w(size_t(kSn) * kD, 0.0f), b(kSn, 0.0f);
         auto put = [&](const char* n, int rows, int at) {
-            const auto& src = ts.get(a + n, {rows, kD});
+            const auto& src = ts.take(a + n, {rows, kD});
             std::memcpy(&w[size_t(at) * kD], src.data(), sizeof(float) * size_t(rows) * kD);
         };
         put("W_K.weight", 384, kSk);
@@ -360,32 +461,31 @@ HostModel load_host_model(const std::string& path) {
         put("theta_proj.weight", 96, kSth);
         put("alpha_proj.weight", 6, kSal);
         put("forget_proj.weight", 6, kSfg);
-        const auto& ab = ts.get(a + "alpha_proj.bias", {kHeads});
-        const auto& fb = ts.get(a + "forget_proj.bias", {kHeads});
+        const auto& ab = ts.take(a + "alpha_proj.bias", {kHeads});
+        const auto& fb = ts.take(a + "forget_proj.bias", {kHeads});
         for (int h = 0; h < kHeads; ++h) {
             b[size_t(kSal) + h] = ab[h];
             b[size_t(kSfg) + h] = fb[h];
         }
         S.in = linear(w, kSn, kD, &b);
-        S.q = linear(ts.get(a + "W_Q.weight", {kD, kD}), kD, kD);
-        S.c = linear(ts.get(a + "W_C.weight", {192, kD}), 192, kD);
-        S.o = linear(ts.get(a + "W_O.weight", {kD, kD}), kD, kD);
-        const auto& lr = ts.get(a + "lambda_raw", {kHeads});
+        S.q = linear(ts.take(a + "W_Q.weight", {kD, kD}), kD, kD);
+        S.c = linear(ts.take(a + "W_C.weight", {192, kD}), 192, kD);
+        S.o = linear(ts.take(a + "W_O.weight", {kD, kD}), kD, kD);
+        const auto& lr = ts.take(a + "lambda_raw", {kHeads});
         for (int h = 0; h < kHeads; ++h) S.lam[h] = softplus_host(lr[h]);
-        S.gate = linear(ts.get("sisa.ffn.w_gate.weight", {kFF, kD}), kFF, kD);
-        S.up = linear(ts.get("sisa.ffn.w_up.weight", {kFF, kD}), kFF, kD);
-        S.down = linear(ts.get("sisa.ffn.w_down.weight", {kD, kFF}), kD, kFF);
+        S.gate = linear(ts.take("sisa.ffn.w_gate.weight", {kFF, kD}), kFF, kD);
+        S.up = linear(ts.take("sisa.ffn.w_up.weight", {kFF, kD}), kFF, kD);
+        S.down = linear(ts.take("sisa.ffn.w_down.weight", {kD, kFF}), kD, kFF);
     }
-    hm.final_norm_w = ts.get("final_norm.weight", {kD});
+    hm.final_norm_w = ts.take("final_norm.weight", {kD});
     {
-        const auto& b0 = ts.get("head.0.bias", {128});
-        hm.head0 = linear(ts.get("head.0.weight", {128, kD}), 128, kD, &b0);
+        const auto& b0 = ts.take("head.0.bias", {128});
+        hm.head0 = linear(ts.take("head.0.weight", {128, kD}), 128, kD, &b0);
     }
-    hm.head2_w = ts.get("head.2.weight", {1, 128});
-    hm.head2_b = ts.get("head.2.bias", {1})[0];
+    hm.head2_w = ts.take("head.2.weight", {1, 128});
+    hm.head2_b = ts.take("head.2.bias", {1})[0];
 
-    for (const auto& kv : ts.all)
-        if (!ts.taken.count(kv.first)) throw std::runtime_error("weights: unexpected tensor " + kv.first);
+    ts.expect_all_claimed();
     return hm;
 }
 

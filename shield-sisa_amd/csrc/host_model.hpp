@@ -76,7 +76,4 @@ struct HostModel {
 // threshold finite in (0,1)) and folds BatchNorm (eps 1e-3) in double.  Throws std::runtime_error.
 HostModel load_host_model(const std::string& path);
 
-// SHA-256 hex of a file (throws on I/O error).
-std::string sha256_file(const std::string& path);
-
 }  // namespace shv

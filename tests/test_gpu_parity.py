@@ -370,3 +370,32 @@ def test_delta_chunked_matches_sequential(shv, weights, clips, mode, monkeypatch
     la, lb = out[False][0], out[True][0]
     print(f"[gpu] {mode} logits max|diff| {float(np.abs(la - lb).max()):.2e}", flush=True)
     assert np.all(np.isfinite(la)) and float(np.abs(la - lb).max()) <= 1e-3
+
+
+def test_async_pinned_jobs_overlap_capture_and_landing(shv, weights, clips):
+    """Jobs from pinned host memory need no staging copy, so the scheduler starts (and, on first use, graph-captures)
+    one lane while its completion thread waits on the other lane's events.  Graphs are captured on the engine's own
+    stream, so that wait never meets a stream in capture mode.  Four full jobs of 16 clips, twice (capture, then
+    replay), give bitwise the logits of predict."""
+    import ctypes
+    print("[gpu] fp16 async jobs from pinned memory, 4 x 16 clips", flush=True)
+    n, per = 64, 16
+    with shv.Model(weights, "fp16", experimental=True, max_frames=per * 20, max_windows=per) as m:
+        ref = m.predict(clips[:n])
+        nbytes = n * 20 * shv.FRAME_BYTES
+        ptr = m.lib.shv_hip_host_alloc(nbytes)
+        assert ptr
+        try:
+            host = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(ptr)).reshape(n, 20, shv.FRAME_BYTES)
+            host[:] = clips[:n].reshape(n, 20, shv.FRAME_BYTES)
+            wf = np.arange(per * 20, dtype=np.int32)
+            for rep in range(2):
+                out = np.full(n, np.nan, np.float32)
+                jobs = [m.submit(frames=host[j:j + per], n_windows=per, window_frames=wf, logits_out=out[j:j + per])
+                        for j in range(0, n, per)]
+                for job, _ in jobs:
+                    assert m.job_wait(job) == 0, m.job_error(job)
+                    m.job_free(job)
+                assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), (rep, float(np.abs(out - ref).max()))
+        finally:
+            m.lib.shv_hip_host_free(ptr)
