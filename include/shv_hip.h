@@ -187,6 +187,17 @@ int shv_hip_native_crops_i420(const shv_hip_i420_image* frames, const shv_hip_re
 int shv_hip_delta_rule(const char* mode, const float* d_q, const float* d_k, const float* d_v, const float* d_decay,
                        const float* d_beta, int n_windows, float* d_o, int variant, void* stream);
 
+/* The gated delta rule above without any allocation, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments and results as shv_hip_delta_rule (bitwise), but asynchronous on `stream` in every variant: the
+ * chunked scan (fp16 / bf16, variant 0 or 2) works in a static device array for at most 16 windows (30.5 MB per
+ * GPU, held until the process ends) and rejects more windows (-1 + last_error); fp32 and token-by-token variants
+ * need no work memory.  Every call on one GPU shares that array: calls that overlap on one GPU (other streams or
+ * threads) race -- serialise them.  Returns 0, or -1 + last_error. */
+int shv_hip_delta_rule_noalloc(const char* mode, const float* d_q, const float* d_k, const float* d_v,
+                               const float* d_decay, const float* d_beta, int n_windows, float* d_o, int variant,
+                               void* stream);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

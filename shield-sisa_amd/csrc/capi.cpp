@@ -280,4 +280,14 @@ int shv_hip_delta_rule(const char* mode, const float* d_q, const float* d_k, con
     });
 }
 
+int shv_hip_delta_rule_noalloc(const char* mode, const float* d_q, const float* d_k, const float* d_v,
+                               const float* d_decay, const float* d_beta, int n_windows, float* d_o, int variant,
+                               void* stream) {
+    return guarded([&] {
+        shv::run_delta_rule_noalloc(mode_or_throw(mode), d_q, d_k, d_v, d_decay, d_beta, n_windows, d_o, variant,
+                                    static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
 }  // extern "C"

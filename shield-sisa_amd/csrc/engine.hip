@@ -849,12 +849,7 @@ private:
 
 void run_delta_rule(Precision p, const float* Q, const float* K, const float* V, const float* dec, const float* beta,
                     int n_windows, float* O, int variant, hipStream_t s) {
-    if (!Q || !K || !V || !dec || !beta || !O || n_windows < 1 || n_windows > 65536)
-        throw std::runtime_error("delta rule: null buffer or bad window count");
-    if (variant < 0 || variant > 2 || (p == Precision::FP32 && variant == 2))
-        throw std::runtime_error("delta rule: unknown variant for this mode");
-    const bool chunked = p != Precision::FP32 && variant != 1;
-    if (!chunked) {
+    if (!delta_rule_is_chunked(p, Q, K, V, dec, beta, n_windows, O, variant)) {
         launch_delta(Q, K, V, dec, beta, O, n_windows, p == Precision::FP32, s);
         SHV_HIP_CHECK(hipGetLastError());
         return;

@@ -113,6 +113,21 @@ std::unique_ptr<Engine> make_engine(const HostModel& hm, Precision p, const Engi
 // bf16: the chunked scan), 1: token by token, 2: chunked (fp16 / bf16 only).  Allocates its work buffer per call.
 void run_delta_rule(Precision p, const float* Q, const float* K, const float* V, const float* dec, const float* beta,
                     int n_windows, float* O, int variant, hipStream_t s);
+// The same without any allocation and without synchronising: the chunked scan works in a static device array for
+// at most kDeltaNoAllocWindows windows (one per GPU, held until the process ends; looked up on the first call on
+// each device).  Calls that overlap on one GPU race on that array.
+constexpr int kDeltaNoAllocWindows = 16;
+void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const float* V, const float* dec,
+                            const float* beta, int n_windows, float* O, int variant, hipStream_t s);
+// Validates the arguments of both; true when they select the chunked scan.
+inline bool delta_rule_is_chunked(Precision p, const float* Q, const float* K, const float* V, const float* dec,
+                                  const float* beta, int n_windows, const float* O, int variant) {
+    if (!Q || !K || !V || !dec || !beta || !O || n_windows < 1 || n_windows > 65536)
+        throw std::runtime_error("delta rule: null buffer or bad window count");
+    if (variant < 0 || variant > 2 || (p == Precision::FP32 && variant == 2))
+        throw std::runtime_error("delta rule: unknown variant for this mode");
+    return p != Precision::FP32 && variant != 1;
+}
 
 class PwGemm {
 public:

@@ -3,11 +3,14 @@
 // (element i into lane i % 16, first product unfused, then fmas) and the fixed 16-lane tree
 // (engine/model/isa_impl.hpp:45-53, 854-863, 866-962, 996-1069, 1127-1133).
 #include "dev_common.hpp"
+#include "engine.hpp"
 #include "host_model.hpp"
 #include "kernels.hpp"
 #include "mfma.hpp"
 
+#include <mutex>
 #include <stdexcept>
+#include <string>
 #include <type_traits>
 
 namespace shv {
@@ -1134,6 +1137,53 @@ void launch_head(const float* X, const float* norm_w, const float* w0, const flo
 }
 void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool, int F, hipStream_t s) {
     hipLaunchKernelGGL(store_tokens_kernel, dim3(F), dim3(256), 0, s, tokens, slots, pool);
+}
+
+// ------------------------------------------------------------------------------------------------ no allocation
+// Work memory of the chunked scan for callers that cannot allocate (code under graph capture, serving loops): a
+// file-scope device array for kDeltaNoAllocWindows windows (6 heads x 11 chunks x 7232 floats each, 30.5 MB), one
+// copy per GPU for the life of the process.  The prep kernel writes every float of a chunk's area before the scan
+// reads it, so nothing has to be cleared between calls.  In host code `scratch` names a host-side stand-in, never
+// the device memory: kernels get the address hipGetSymbolAddress returns, kept per device.
+static __device__ __align__(256) float scratch[size_t(kDeltaNoAllocWindows) * kHeads * DNC * DCF];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_addr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device (no allocation).
+float* scratch_on_current_device() {
+    int dev = -1;
+    SHV_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("delta rule (no allocation): device ordinal out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            throw std::runtime_error(std::string("delta rule (no allocation): hipGetSymbolAddress failed: ") +
+                                     hipGetErrorString(e));
+        g_scratch_addr[dev] = static_cast<float*>(p);
+    }
+    return g_scratch_addr[dev];
+}
+}  // namespace
+
+void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const float* V, const float* dec,
+                            const float* beta, int n_windows, float* O, int variant, hipStream_t s) {
+    if (!delta_rule_is_chunked(p, Q, K, V, dec, beta, n_windows, O, variant)) {
+        launch_delta(Q, K, V, dec, beta, O, n_windows, p == Precision::FP32, s);
+        SHV_HIP_CHECK(hipGetLastError());
+        return;
+    }
+    if (n_windows > kDeltaNoAllocWindows)
+        throw std::runtime_error("delta rule (no allocation): " + std::to_string(n_windows) +
+                                 " windows exceed the static work area of " + std::to_string(kDeltaNoAllocWindows));
+    float* work = scratch_on_current_device();
+    if (p == Precision::BF16) launch_delta_chunked<bf16>(Q, K, V, dec, beta, O, work, n_windows, s);
+    else launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s);
+    SHV_HIP_CHECK(hipGetLastError());
 }
 
 #define SHV_NORMS(T)                                                                                             \

@@ -74,6 +74,8 @@ _SIGS = {
     "shv_hip_gemm_run": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P, ctypes.c_int, _P, ctypes.c_int, _P]),
     "shv_hip_gemm_free": (None, [_P]),
     "shv_hip_delta_rule": (ctypes.c_int, [ctypes.c_char_p, _P, _P, _P, _P, _P, ctypes.c_int, _P, ctypes.c_int, _P]),
+    "shv_hip_delta_rule_noalloc": (ctypes.c_int, [ctypes.c_char_p, _P, _P, _P, _P, _P, ctypes.c_int, _P, ctypes.c_int,
+                                                  _P]),
     "shv_hip_native_crops_rgb": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
     "shv_hip_native_crops_i420": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
 }
@@ -474,6 +476,15 @@ def delta_rule(mode: str, d_q: int, d_k: int, d_v: int, d_decay: int, d_beta: in
     """shv_hip_delta_rule on device buffers (see include/shv_hip.h for the layout)."""
     lib = library()
     if lib.shv_hip_delta_rule(mode.encode(), d_q, d_k, d_v, d_decay, d_beta, n_windows, d_o, variant, stream) != 0:
+        raise ShvError(last_error())
+
+
+def delta_rule_noalloc(mode: str, d_q: int, d_k: int, d_v: int, d_decay: int, d_beta: int, n_windows: int, d_o: int,
+                       variant: int = 0, stream: int | None = None) -> None:
+    """shv_hip_delta_rule_noalloc: the same without allocating (static work area, asynchronous on `stream`)."""
+    lib = library()
+    if lib.shv_hip_delta_rule_noalloc(mode.encode(), d_q, d_k, d_v, d_decay, d_beta, n_windows, d_o, variant,
+                                      stream) != 0:
         raise ShvError(last_error())
 
 
