@@ -5,11 +5,16 @@ value: clips/s of the full SHIELD-V forward (uint8 crops -> logit) in FP16 at ba
        inputs resident in HBM, through the C-ABI device entry point (shv_hip_forward_device), timed with HIP events
        on the launching stream over exactly --steps forwards after --warmup untimed ones.
 extra: batch-1 end-to-end latency through shv_hip_predict (pinned host clip, H2D included, like the reference's
-       2.89 ms at README.md:117), encoder-only frames/s, the roofline of the dominant kernel, and the reference CPU
-       engine (compiled from the reference sources into oracle/_ref) timed on this host's cores.
-roofline: the dominant kernel is the one with the largest device time per step; its average launch duration is
-       measured here with HIP events on the launching stream (per-kernel profiling pass, graphs off) and its
-       algorithmic bytes per launch are the input, output and side-output maps it must move (weights excluded).
+       2.89 ms at README.md:117) in fp16 and in the exact fp32 tier (config 0); the batch-128 fp16 rate end to end
+       through shv_hip_predict from pinned host memory (the reference's own method, bench/gpu_bench.cpp:93-117);
+       encoder-only frames/s (config 1); the pointwise GEMM microbench on the literal config-2 shapes, the real
+       model's 1x1 shapes and the sequence shapes (config 2); sequence-stage windows/s (config 3); bf16 1,024 clips
+       through the async API with HBM and MFMA rates and fp32 parity (config 4); the reference CPU engine
+       (compiled from the reference sources into oracle/_ref) timed on this host's cores.
+roofline: the dominant kernel is the profiling family (one kernel at the shapes the forward gives it) with the
+       largest device time per step, from a per-kernel pass with HIP events on the launching stream (graphs off).
+       Its algorithmic bytes and FLOPs per launch are recorded by the engine (maps in and out, weights; 2 M N K);
+       the binding roof is HBM when its FLOP/byte intensity is below the ridge (MFMA peak / HBM peak), else MFMA.
        `traffic` (HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a plain device copy)
        is read from profiles/roofline_traffic.json only when that file was measured on this library's compute
        revision and names the same kernel; else null.
@@ -31,15 +36,12 @@ from pathlib import Path
 import numpy as np
 
 ROOT = Path(__file__).resolve().parent
-HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+MFMA_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 / bf16 matrix cores
+FP32_PEAK_TFLOPS = 157.3        # MI355X fp32 vector
 REF_B128_CLIPS_PER_S = 128 / 0.191   # reference README.md:118 (RTX A6000, batch 128 FP16)
-# MobileNetV3-Large blocks (cin, cexp, cout): the fused kernels are profiled per instantiation "ir_<cin>x<cexp>x<cout>"
-BLOCKS = [(16, 16, 16), (16, 64, 24), (24, 72, 24), (24, 72, 40), (40, 120, 40), (40, 120, 40), (40, 240, 80),
-          (80, 200, 80), (80, 184, 80), (80, 184, 80), (80, 480, 112), (112, 672, 112), (112, 672, 160),
-          (160, 960, 160), (160, 960, 160)]
-FAMILIES = sorted({"ir_%dx%dx%d" % b for b in BLOCKS}) + [
-    "se_reduce", "gemm_pw", "dw", "stem", "stem_ir_16x16x16", "se_pool", "pool", "tail_pool", "gemm_seq", "gemm_f32_small", "gemm_se_fc", "rmsnorm", "gdn_prep",
-    "delta", "gated_norm", "sisa", "head", "assemble"]
+# families of the sequence stages (config 3): the role before ":" for GEMMs
+SEQ_ROLES = {"assemble", "rmsnorm", "gemm_seq", "gdn_prep", "delta", "gated_norm", "sisa", "gemm_f32_small", "head"}
 
 
 def load_shv():
@@ -54,12 +56,25 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(weights: Path, clips: np.ndarray, seconds: float) -> dict | None:
+    """The reference CPU engine (exact FP32) on this host's cores.  A GPU box's CPU share for one GPU is 16 cores
+    whatever the host shows, so the engine gets min(16, visible cores) threads."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
     if not oracle.REF_SO.exists():
         return None
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    visible = len(os.sched_getaffinity(0))
+    threads = max(1, min(16, visible))
     ref = oracle.Reference(weights, threads=threads)
     batch = clips[: min(len(clips), 2 * threads)]
     ref.predict(batch[:1])
@@ -73,8 +88,9 @@ def cpu_baseline(weights: Path, clips: np.ndarray, seconds: float) -> dict | Non
     isa = ref.isa
     ref.close()
     return {"value": round(n / dt, 3), "unit": "clips/s", "cores": threads, "kind": "reference",
+            "cpu": cpu_model(), "host_cpus_visible": visible,
             "sample": f"reference CPU engine exact FP32 ({isa}), shv_cpu_predict on {len(batch)}-clip batches "
-                      f"repeated for {dt:.1f} s ({n} clips)"}
+                      f"repeated for {dt:.1f} s ({n} clips), {threads} threads (the box's CPU share for one GPU)"}
 
 
 def measured_traffic(kernel: str, revision: str) -> float | None:
@@ -90,24 +106,51 @@ def measured_traffic(kernel: str, revision: str) -> float | None:
     return float(t["traffic_bytes_per_launch"])
 
 
-# config 2: the pointwise-conv GEMM at the literal config shapes (bias + hardswish), every tier, through the C-ABI tool
-GEMM_SHAPES = [("b2.expand", 2560 * 28 * 28, 120, 40), ("b14.expand", 2560 * 7 * 7, 960, 160)]
+# config 2: the pointwise GEMM through the C-ABI tool (bias + hardswish), every tier, on (set, name, M, N, K):
+# the literal config-2 shapes (224x224 MobileNetV3 at 2560 frames), the real model's 1x1 layers at 2560 frames of
+# 180x320 (engine/cuda/model.hpp:23-29 widths, maps 90x160 .. 6x10) and the sequence GEMMs at 128 windows
+# (M = 128 x 321).  The tool takes fp32 A and splits it in the kernel; the engine's sequence GEMMs read A pre-split.
+GEMM_SHAPES = [
+    ("config2", "b2.expand", 2560 * 28 * 28, 120, 40), ("config2", "b14.expand", 2560 * 7 * 7, 960, 160),
+    ("model", "b3.expand", 2560 * 45 * 80, 72, 24), ("model", "b3.project", 2560 * 45 * 80, 24, 72),
+    ("model", "b5.expand", 2560 * 23 * 40, 120, 40), ("model", "b5.project", 2560 * 23 * 40, 40, 120),
+    ("model", "b7.expand", 2560 * 23 * 40, 240, 40), ("model", "b12.expand", 2560 * 12 * 20, 672, 112),
+    ("model", "b12.project", 2560 * 12 * 20, 112, 672), ("model", "b14.expand", 2560 * 6 * 10, 960, 160),
+    ("model", "b14.project", 2560 * 6 * 10, 160, 960), ("model", "projection", 2560 * 16, 384, 960),
+    ("sequence", "gdn.in_proj", 128 * 321, 2316, 384), ("sequence", "gdn.o_proj", 128 * 321, 384, 768),
+    ("sequence", "ffn.up", 128 * 321, 1920, 384), ("sequence", "ffn.down", 128 * 321, 384, 960),
+    ("sequence", "sisa.in", 128 * 321, 1068, 384)]
 
 
-def gemm_microbench(shv, hip, stream, e0, e1, iters: int = 10) -> list:
+def device_random(hip, rng, rows: int, cols: int, block_rows: int = 1 << 20) -> int:
+    """rows x cols fp32 ~ 0.1 N(0,1) in device memory: one host block, repeated on the device."""
+    blk = min(rows, block_rows)
+    host = (rng.standard_normal((blk, cols), dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    d = hip.malloc(rows * cols * 4)
+    src = hip.upload(host)
+    for r0 in range(0, rows, blk):
+        n = min(blk, rows - r0)
+        hip.copy_d2d(d + r0 * cols * 4, src, n * cols * 4)
+    hip.sync()
+    hip.free(src)
+    return d
+
+
+def gemm_microbench(shv, hip, stream, e0, e1, iters: int = 5) -> list:
     """Per shape and tier: device time per GEMM (HIP events on the launching stream, automatic kernel choice),
-    TFLOP/s and the HBM rate of its algorithmic bytes (fp32 A and C, W in the tier's parts, bias) against 8 TB/s."""
+    TFLOP/s against the tier's peak (matrix cores for fp16 / bf16, vector fp32 for the exact tier) and the HBM rate
+    of its algorithmic bytes (fp32 A and C, W in the tier's parts, bias) against 8 TB/s."""
     rng = np.random.default_rng(3)
     out = []
-    for name, M, N, K in GEMM_SHAPES:
-        A = (rng.standard_normal((M, K), dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    for group, name, M, N, K in GEMM_SHAPES:
+        dA = device_random(hip, rng, M, K)
         W = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.1)).astype(np.float32)
         b = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
-        dA, dW, db, dC = hip.upload(A), hip.upload(W), hip.upload(b), hip.malloc(M * N * 4)
-        for mode, wbytes in (("fp16", 4), ("bf16", 6), ("fp32", 4)):
+        dW, db, dC = hip.upload(W), hip.upload(b), hip.malloc(M * N * 4)
+        for mode, wbytes, peak in (("fp16", 4, MFMA_PEAK_TFLOPS), ("bf16", 6, MFMA_PEAK_TFLOPS),
+                                   ("fp32", 4, FP32_PEAK_TFLOPS)):
             with shv.PwGemm(mode, dW, N, K, stream) as g:
-                for _ in range(2):
-                    g.run(dA, M, dC, db, shv.ACT_HSWISH, stream=stream)
+                g.run(dA, M, dC, db, shv.ACT_HSWISH, stream=stream)
                 hip.record(e0, stream)
                 for _ in range(iters):
                     g.run(dA, M, dC, db, shv.ACT_HSWISH, stream=stream)
@@ -116,22 +159,35 @@ def gemm_microbench(shv, hip, stream, e0, e1, iters: int = 10) -> list:
             flop = 2.0 * M * N * K
             nbytes = M * K * 4.0 + N * K * wbytes + M * N * 4.0 + N * 4.0
             gbs = nbytes / (ms / 1000.0) / 1e9
-            out.append({"shape": name, "M": M, "N": N, "K": K, "mode": mode, "us": round(ms * 1000.0, 1),
-                        "TFLOP/s": round(flop / (ms / 1000.0) / 1e12, 2), "GB/s": round(gbs, 1),
-                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 3)})
-            log(f"[bench] gemm {name} {mode}: {out[-1]}")
+            tflops = flop / (ms / 1000.0) / 1e12
+            out.append({"set": group, "shape": name, "M": M, "N": N, "K": K, "mode": mode,
+                        "us": round(ms * 1000.0, 1), "TFLOP/s": round(tflops, 2), "GB/s": round(gbs, 1),
+                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 3), "compute_frac": round(tflops / peak, 4)})
+            log(f"[bench] gemm {group}/{name} {mode}: {out[-1]}")
         for p in (dA, dW, db, dC):
             hip.free(p)
     return out
 
 
-SEQ_FAMILIES = ["assemble", "rmsnorm", "gemm_seq", "gdn_prep", "delta", "gated_norm", "sisa", "gemm_f32_small", "head"]
+def profile_forward(model, hip, stream, d_frames: int, n_clips: int, d_logits: int, steps: int) -> dict:
+    """Per-family device time, bytes and FLOPs of `steps` forwards (HIP events on the launching stream, graphs
+    off), summed over each family's launches."""
+    model.profile_enable(True)
+    for _ in range(steps):
+        model.forward_device(d_frames, n_clips, d_logits, stream)
+    hip.stream_sync(stream)
+    stats = {f: model.profile_read(f) for f in model.profile_families()}
+    model.profile_enable(False)
+    return {k: v for k, v in stats.items() if v and v["launches"]}
 
 
-def async_bf16(shv, weights: Path, clips: np.ndarray, n_clips: int = 1024, per_job: int = 128) -> dict:
+def async_bf16(shv, hip, weights: Path, clips: np.ndarray, n_clips: int = 1024, per_job: int = 128) -> dict:
     """Config 4: n_clips clips in bf16 through the async batched API (shv_hip_submit / job_wait) from pinned host
-    memory, per_job clips per request; the scheduler pipelines host copies and compute over its two slots and
-    streams.  Host-to-device copies are included.  Parity: the first 64 clips against the exact fp32 tier."""
+    memory, per_job clips per request; the scheduler pipelines host copies and compute over its two lanes and
+    streams.  Host-to-device copies are included.  HBM and MFMA rates: the algorithmic bytes and FLOPs per clip of a
+    bf16 forward (profiling pass of the same model) at the measured clips/s; the matrix cores issue six products per
+    bf16 multiply (three operand parts), so issued matrix work is six times the algorithmic FLOPs of the GEMMs.
+    Parity: the first 64 clips against the exact fp32 tier."""
     import ctypes
     m = shv.Model(weights, "bf16", experimental=True, max_frames=per_job * 20, max_windows=per_job)
     lib = m.lib
@@ -161,16 +217,94 @@ def async_bf16(shv, weights: Path, clips: np.ndarray, n_clips: int = 1024, per_j
         dt = time.perf_counter() - t0
         npar = min(64, len(clips))
         sub = logits[:npar].copy()
+        # algorithmic bytes and FLOPs of one bf16 forward of per_job clips (the scheduler is idle now)
+        stream = hip.stream()
+        d_frames = hip.upload(np.ascontiguousarray(host[:per_job]))
+        d_logits = hip.malloc(per_job * 4)
+        stats = profile_forward(m, hip, stream, d_frames, per_job, d_logits, 1)
+        hip.free(d_frames)
+        hip.free(d_logits)
+        hip.stream_destroy(stream)
     finally:
         lib.shv_hip_host_free(ptr)
         m.close()
     with shv.Model(weights, "fp32") as ex:
         ref = ex.predict(clips[:npar])
     flips = int(np.sum((sub >= 0) != (ref >= 0)))
-    out = {"clips": n_clips, "clips_per_job": per_job, "seconds": round(dt, 4), "clips_per_s": round(n_clips / dt, 1),
-           "h2d_included": True, "parity_clips": npar, "parity_max_abs_vs_fp32": float(np.abs(sub - ref).max()), "parity_flips": flips}
+    cps = n_clips / dt
+    bytes_clip = sum(v["bytes"] for v in stats.values()) / per_job
+    flops_clip = sum(v["flops"] for v in stats.values()) / per_job
+    gemm_flops_clip = sum(v["flops"] for k, v in stats.items() if ":" in k) / per_job
+    mfma_issued = (gemm_flops_clip * 6.0) * cps / 1e12
+    out = {"clips": n_clips, "clips_per_job": per_job, "seconds": round(dt, 4), "clips_per_s": round(cps, 1),
+           "h2d_included": True, "h2d_GB_per_s": round(20 * shv.FRAME_BYTES * cps / 1e9, 1),
+           "hbm_GB_per_s_algorithmic": round(bytes_clip * cps / 1e9, 1),
+           "hbm_frac_algorithmic": round(bytes_clip * cps / 1e9 / HBM_PEAK_GBS, 4),
+           "algorithmic_bytes_per_clip": round(bytes_clip), "algorithmic_flops_per_clip": round(flops_clip),
+           "mfma_TFLOP_per_s_algorithmic": round(flops_clip * cps / 1e12, 1),
+           "mfma_util_algorithmic": round(flops_clip * cps / 1e12 / MFMA_PEAK_TFLOPS, 4),
+           "mfma_TFLOP_per_s_issued": round(mfma_issued, 1),
+           "mfma_util_issued": round(mfma_issued / MFMA_PEAK_TFLOPS, 4),
+           "parity_clips": npar, "parity_max_abs_vs_fp32": float(np.abs(sub - ref).max()), "parity_flips": flips}
     log(f"[bench] config 4 bf16 async: {out}")
     return out
+
+
+def latency_b1(shv, weights: Path, clip: np.ndarray, mode: str, iters: int) -> dict:
+    """Batch-1 latency through shv_hip_predict from a pinned host clip (H2D included), p50 / p95 over `iters`
+    calls after 10 warm-up calls (the reference's method: README.md:117, bench/gpu_bench.cpp:93-117)."""
+    with shv.Model(weights, mode, experimental=mode != "fp32") as m:
+        lib = m.lib
+        p = lib.shv_hip_host_alloc(20 * shv.FRAME_BYTES)
+        pinned = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_uint8 * (20 * shv.FRAME_BYTES)).from_address(p))
+        pinned[:] = clip.reshape(-1)
+        out = np.empty(1, np.float32)
+        try:
+            for _ in range(10):
+                if lib.shv_hip_predict(m.h, p, 1, out.ctypes.data) != 0:
+                    raise shv.ShvError(shv.last_error())
+            ts = []
+            for _ in range(iters):
+                t0 = time.perf_counter()
+                lib.shv_hip_predict(m.h, p, 1, out.ctypes.data)
+                ts.append((time.perf_counter() - t0) * 1000.0)
+        finally:
+            lib.shv_hip_host_free(p)
+    r = {"mode": mode, "p50_ms": round(float(np.percentile(ts, 50)), 3), "p95_ms": round(float(np.percentile(ts, 95)), 3),
+         "iters": iters, "logit": float(out[0])}
+    log(f"[bench] batch-1 latency {mode}: {r}")
+    return r
+
+
+def predict_e2e(shv, weights: Path, clips: np.ndarray, mode: str, max_frames: int, max_windows: int,
+                reps: int = 5) -> dict:
+    """Batch of clips end to end through shv_hip_predict from pinned host memory (H2D and D2H included), wall
+    clock per call: the reference's measurement of its 191 ms / 128 clips (bench/gpu_bench.cpp:93-117)."""
+    import ctypes
+    n = len(clips)
+    with shv.Model(weights, mode, experimental=mode != "fp32", max_frames=max_frames, max_windows=max_windows) as m:
+        lib = m.lib
+        nbytes = n * 20 * shv.FRAME_BYTES
+        p = lib.shv_hip_host_alloc(nbytes)
+        host = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(p))
+        host[:] = clips.reshape(-1)
+        out = np.empty(n, np.float32)
+        try:
+            for _ in range(2):
+                if lib.shv_hip_predict(m.h, p, n, out.ctypes.data) != 0:
+                    raise shv.ShvError(shv.last_error())
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                lib.shv_hip_predict(m.h, p, n, out.ctypes.data)
+            dt = (time.perf_counter() - t0) / reps
+        finally:
+            lib.shv_hip_host_free(p)
+    per_batch = min(max_windows, max_frames // 20)
+    r = {"mode": mode, "clips": n, "ms": round(dt * 1000.0, 3), "clips_per_s": round(n / dt, 1),
+         "options": {"max_frames": max_frames, "max_windows": max_windows}, "clips_per_gpu_batch": per_batch,
+         "h2d_included": True, "finite": bool(np.isfinite(out).all())}
+    log(f"[bench] predict end to end: {r}")
+    return r
 
 
 def crop_bench(shv, hip, stream, model, clips_n: int, d_logits: int, iters: int = 5) -> dict:
@@ -219,6 +353,34 @@ def crop_bench(shv, hip, stream, model, clips_n: int, d_logits: int, iters: int 
     return out
 
 
+def roofline_of(stats: dict, steps: int, mode: str, revision: str) -> dict:
+    """The family with the most device time per step, against the roof its intensity selects."""
+    dom = max(stats, key=lambda k: stats[k]["ms"])
+    d = stats[dom]
+    avg_ms = d["ms"] / d["launches"]
+    bytes_l = d["bytes"] / d["launches"]
+    flops_l = d["flops"] / d["launches"]
+    gbs = bytes_l / (avg_ms / 1000.0) / 1e9
+    tflops = flops_l / (avg_ms / 1000.0) / 1e12
+    peak_tf = FP32_PEAK_TFLOPS if mode == "fp32" else MFMA_PEAK_TFLOPS
+    ridge = peak_tf * 1e12 / (HBM_PEAK_GBS * 1e9)
+    intensity = flops_l / bytes_l if bytes_l else 0.0
+    traffic = measured_traffic(dom, revision)
+    if intensity < ridge:
+        r = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+             "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    else:
+        r = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak_tf, "unit": "TFLOP/s",
+             "frac": round(tflops / peak_tf, 4)}
+    r.update({"traffic": None if traffic is None else round(traffic), "kernel": dom,
+              "algorithmic_bytes_per_launch": round(bytes_l), "algorithmic_flops_per_launch": round(flops_l),
+              "intensity_flop_per_byte": round(intensity, 1), "ridge_flop_per_byte": round(ridge, 1),
+              "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "compute_frac": round(tflops / peak_tf, 4),
+              "avg_launch_ms": round(avg_ms, 4), "launches_per_step": d["launches"] // steps,
+              "ms_per_step": round(d["ms"] / steps, 4)})
+    return r
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -234,10 +396,12 @@ def main() -> int:
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-async", action="store_true")
     ap.add_argument("--no-crop", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the SHIELD-V forward has no cross-GPU step "
-              "(clips are independent rows); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: every GPU box here has one GPU, and the SHIELD-V forward has no "
+              "cross-GPU step (clips are independent rows; each GPU would run its own model); run with --gpus 1",
+              file=sys.stderr)
         return 2
 
     shv = load_shv()
@@ -271,32 +435,14 @@ def main() -> int:
         log(f"[bench] {ms:.3f} ms/step -> {value:.1f} clips/s; finite logits {np.isfinite(logits).all()}")
 
         # per-kernel timing with HIP events on the launching stream (graphs off while profiling)
-        model.profile_enable(True)
         prof_steps = max(1, min(args.steps, 3))
-        for _ in range(prof_steps):
-            model.forward_device(d_frames, B, d_logits, stream)
-        hip.stream_sync(stream)
-        stats = {f: model.profile_read(f) for f in FAMILIES}
-        model.profile_enable(False)
-        stats = {k: v for k, v in stats.items() if v and v["launches"]}
-        per_step = {k: round(v["ms"] / prof_steps, 3) for k, v in stats.items()}
+        stats = profile_forward(model, hip, stream, d_frames, B, d_logits, prof_steps)
+        per_step = {k: round(v["ms"] / prof_steps, 3) for k, v in sorted(stats.items(), key=lambda kv: -kv[1]["ms"])}
         log("[bench] per-step ms by kernel family: " + json.dumps(per_step))
-        seq_ms = sum(stats[k]["ms"] for k in SEQ_FAMILIES if k in stats) / prof_steps
+        seq_ms = sum(v["ms"] for k, v in stats.items() if k.split(":")[0] in SEQ_ROLES) / prof_steps
         seq_wps = B / (seq_ms / 1000.0)
         log(f"[bench] sequence stages {seq_ms:.3f} ms / {B} windows -> {seq_wps:.0f} windows/s")
-        # dominant kernel: the fused-block kernel with the most device time per step (each such family is one kernel
-        # symbol at one shape, so rocprofv3's per-kernel average can be set beside this one)
-        dom = max((k for k in stats if k.startswith("ir_")), key=lambda k: stats[k]["ms"])
-        d = stats[dom]
-        avg_ms = d["ms"] / d["launches"]
-        bytes_per_launch = d["bytes"] / d["launches"]
-        achieved = bytes_per_launch / (avg_ms / 1000.0) / 1e9
-        traffic = measured_traffic(dom, revision)
-        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4),
-                    "traffic": None if traffic is None else round(traffic),
-                    "kernel": dom, "algorithmic_bytes_per_launch": round(bytes_per_launch),
-                    "avg_launch_ms": round(avg_ms, 4), "launches_per_step": d["launches"] // prof_steps}
+        roofline = roofline_of(stats, prof_steps, args.mode, revision)
         log("[bench] roofline " + json.dumps(roofline))
 
         copy = None
@@ -316,7 +462,6 @@ def main() -> int:
             hip.free(src)
             hip.free(dst)
 
-        gemm = None if args.kernel_only or args.no_gemm else gemm_microbench(shv, hip, stream, e0, e1)
         crops = None if args.kernel_only or args.no_crop else crop_bench(shv, hip, stream, model, B, d_logits)
 
         enc_ms = None
@@ -335,31 +480,24 @@ def main() -> int:
         model.close()
         hip.free(d_frames)
         hip.free(d_logits)
+        gemm = None if args.kernel_only or args.no_gemm else gemm_microbench(shv, hip, stream, e0, e1)
         hip.stream_destroy(stream)
 
-        # batch-1 latency through the synchronous API (pinned host clip, H2D included)
-        lat = None
+        lat = lat32 = None
         if not args.kernel_only and args.latency_iters > 0:
-            with shv.Model(w, args.mode, experimental=args.mode != "fp32") as m1:
-                lib = m1.lib
-                p = lib.shv_hip_host_alloc(20 * shv.FRAME_BYTES)
-                pinned = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_uint8 * (20 * shv.FRAME_BYTES)).from_address(p))
-                pinned[:] = clips[0].reshape(-1)
-                out = np.empty(1, np.float32)
-                for _ in range(10):
-                    lib.shv_hip_predict(m1.h, p, 1, out.ctypes.data)
-                ts = []
-                for _ in range(args.latency_iters):
-                    t0 = time.perf_counter()
-                    lib.shv_hip_predict(m1.h, p, 1, out.ctypes.data)
-                    ts.append((time.perf_counter() - t0) * 1000.0)
-                lib.shv_hip_host_free(p)
-                lat = float(np.percentile(ts, 50))
-                log(f"[bench] batch-1 latency p50 {lat:.3f} ms (p95 {np.percentile(ts, 95):.3f})")
+            lat = latency_b1(shv, w, clips[0], args.mode, args.latency_iters)
+            lat32 = latency_b1(shv, w, clips[0], "fp32", args.latency_iters)   # config 0: the exact tier
+
+        e2e = None
+        if not args.kernel_only and not args.no_e2e:
+            # the reference's defaults split 128 clips into 4 GPU batches of 32 pipelined over 2 lanes; beside it
+            # the same 128 clips as one GPU batch
+            e2e = {"reference_options": predict_e2e(shv, w, clips, args.mode, 640, 512),
+                   "one_gpu_batch": predict_e2e(shv, w, clips, args.mode, B * 20, B)}
 
         c4 = None
         if not args.kernel_only and not args.no_async:
-            c4 = async_bf16(shv, w, clips)
+            c4 = async_bf16(shv, hip, w, clips)
 
         cpu = None
         if not args.no_cpu and not args.kernel_only:
@@ -382,7 +520,10 @@ def main() -> int:
                    "crop": "180x320x3 uint8", "tokens_per_window": 321, "d_model": 384,
                    "inputs": "device-resident (HBM)", "entry": "shv_hip_forward_device",
                    "reference_gpu_clips_per_s": round(REF_B128_CLIPS_PER_S, 1)},
-        "latency_b1_ms": None if lat is None else round(lat, 3),
+        "latency_b1_ms": None if lat is None else lat["p50_ms"],
+        "latency_b1_fp32_ms": None if lat32 is None else lat32["p50_ms"],
+        "latency_b1": {"fp16": lat, "fp32": lat32} if lat else None,
+        "predict_b128_e2e": e2e,
         "encoder_frames_per_s": None if enc_ms is None else round(B * 20 / (enc_ms / 1000.0), 1),
         "sequence_windows_per_s": round(seq_wps, 1),
         "async_bf16_1024": c4,

@@ -127,11 +127,15 @@ void shv_hip_host_free(void* p);
 int shv_hip_forward_device(shv_hip_model* m, const uint8_t* d_frames, int n_clips, float* d_logits, void* stream);
 /* encode only: d_frames (n_frames crops) -> d_tokens (n_frames x 6144 fp32), device memory. */
 int shv_hip_encode_device(shv_hip_model* m, const uint8_t* d_frames, int n_frames, float* d_tokens, void* stream);
-/* Per-kernel-family timing with HIP events on the launching stream: enable(1)/disable(0) and read
- * the accumulated milliseconds and launch count of family `name` ("gemm_mfma", "dw", ...); returns -1 if unknown. */
+/* Per-kernel-family timing with HIP events on the launching stream (graphs are off while enabled):
+ * enable(1)/disable(0); read the accumulated milliseconds, launch count, algorithmic bytes and FLOPs of family
+ * `name` (-1 if unknown); list writes the family names seen since enabling, one per line, into buf (at most cap
+ * bytes with the terminating NUL) and returns the full length.  A family is one kernel at the shapes the forward
+ * gives it: "ir_<cin>x<cexp>x<cout>" fused blocks, "gdn_prep", ..., GEMMs as "<role>:<kernel template>". */
 int shv_hip_profile_enable(shv_hip_model* m, int on);
 int shv_hip_profile_read(shv_hip_model* m, const char* name, double* total_ms, long long* launches,
-                         double* bytes);
+                         double* bytes, double* flops);
+long long shv_hip_profile_list(shv_hip_model* m, char* buf, size_t cap);
 /* Debug: write float32 intermediates of frame 0 / window 0 of the next synchronous call into dir (graphs off). */
 int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir);
 

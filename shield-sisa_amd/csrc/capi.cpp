@@ -8,7 +8,9 @@
 #include "lanes.hpp"
 #include "sched.hpp"
 
+#include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -200,7 +202,8 @@ int shv_hip_profile_enable(shv_hip_model* m, int on) {
         return 0;
     });
 }
-int shv_hip_profile_read(shv_hip_model* m, const char* name, double* total_ms, long long* launches, double* bytes) {
+int shv_hip_profile_read(shv_hip_model* m, const char* name, double* total_ms, long long* launches, double* bytes,
+                         double* flops) {
     return guarded([&] {
         if (!m || !name) throw std::runtime_error("null argument");
         shv::ProfStat st;
@@ -208,8 +211,25 @@ int shv_hip_profile_read(shv_hip_model* m, const char* name, double* total_ms, l
         if (total_ms) *total_ms = st.ms;
         if (launches) *launches = st.launches;
         if (bytes) *bytes = st.bytes;
+        if (flops) *flops = st.flops;
         return 0;
     });
+}
+long long shv_hip_profile_list(shv_hip_model* m, char* buf, size_t cap) {
+    try {
+        if (!m) throw std::runtime_error("null model");
+        std::string all;
+        for (const std::string& f : m->lanes->engine().profile_families()) all += f + "\n";
+        if (buf && cap) {
+            const size_t n = std::min(cap - 1, all.size());
+            std::memcpy(buf, all.data(), n);
+            buf[n] = '\0';
+        }
+        return (long long)all.size();
+    } catch (const std::exception& e) {
+        shv::sched::set_error(e.what());
+        return -1;
+    }
 }
 int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir) {
     return guarded([&] {

@@ -54,7 +54,7 @@ int Engine::frame_bucket(int F) const { return cfg_.use_graphs ? bucket_for(F, c
 int Engine::window_bucket(int B) const { return cfg_.use_graphs ? bucket_for(B, cfg_.max_windows) : B; }
 
 // ------------------------------------------------------------------------------------------------ profiling
-int Engine::family_id(const char* name) {
+int Engine::family_id(const std::string& name) {
     for (size_t i = 0; i < fam_names_.size(); ++i)
         if (fam_names_[i] == name) return int(i);
     fam_names_.push_back(name);
@@ -79,6 +79,7 @@ void Engine::prof_flush() {
         ProfStat& st = fam_stats_[size_t(p.family)];
         st.ms += ms;
         st.bytes += p.bytes;
+        st.flops += p.flops;
         st.launches += 1;
         event_pool_.push_back(p.e0);
         event_pool_.push_back(p.e1);
@@ -534,16 +535,28 @@ private:
     }
 
     // GEMM in this engine's flavour (or the exact fp32 VALU kernel for the fp32-only layers)
-    void gemm(const char* fam, GemmArgs p, const DevW& w, hipStream_t s) {
+    // profiling family of a GEMM: its role and the kernel the dispatcher picks for these arguments
+    std::string gemm_family(const char* role, const GemmArgs& p, bool f32) const {
+        if (!prof_on_) return std::string();
+        if constexpr (!kF32) {
+            if (!f32) return std::string(role) + ":" + gemm_mfma_kernel<G>(p);
+        }
+        return std::string(role) + ":" + gemm_f32_kernel(p);
+    }
+    void gemm(const char* role, GemmArgs p, const DevW& w, hipStream_t s) {
         p.W = w.w;
         p.wstride = w.stride;
-        const double bytes = gemm_bytes(p.M, p.N, p.K, 4, kF32 ? 4 : int(sizeof(G)) * weight_parts<G>(),
-                                        p.swiglu ? 2 : 4, p.res ? 4 : 0);
-        timed(fam, bytes, s, [&] { gemm_t<G>(p, s); });
+        // A is read pre-split where the producer wrote parts (sequence GEMMs), else as fp32
+        const int abytes = (p.Ah && !kF32) ? int(sizeof(G)) * weight_parts<G>() : 4;
+        const double bytes = gemm_bytes(p.M, p.N, p.K, abytes, kF32 ? 4 : int(sizeof(G)) * weight_parts<G>(),
+                                        p.swiglu ? (p.Ch ? int(sizeof(G)) * weight_parts<G>() / 2 : 2) : 4,
+                                        p.res ? 4 : 0);
+        timed(gemm_family(role, p, false), bytes, s, [&] { gemm_t<G>(p, s); }, 2.0 * p.M * p.N * p.K);
         check_launch();
     }
-    void gemm32(const char* fam, const GemmArgs& p, hipStream_t s) {
-        timed(fam, gemm_bytes(p.M, p.N, p.K, 4, 4, p.swiglu ? 2 : 4, p.res ? 4 : 0), s, [&] { gemm_f32(p, s); });
+    void gemm32(const char* role, const GemmArgs& p, hipStream_t s) {
+        timed(gemm_family(role, p, true), gemm_bytes(p.M, p.N, p.K, 4, 4, p.swiglu ? 2 : 4, p.res ? 4 : 0), s,
+              [&] { gemm_f32(p, s); }, 2.0 * p.M * p.N * p.K);
         check_launch();
     }
 
@@ -631,6 +644,10 @@ private:
             const Blk& b = blk_[i];
             const BlockCfg& c = b.cfg;
             const long long HWi = (long long)b.H * b.W, HWo = (long long)b.Ho * b.Wo;
+            // multiply-adds of the fused kernel: expand, depthwise, and (non-SE blocks) project
+            const double mac = double(F) * ((b.has_expand ? double(HWi) * c.cin * c.cexp : 0.0) +
+                                            double(HWo) * c.cexp * c.k * c.k +
+                                            (c.se ? 0.0 : double(HWo) * c.cexp * c.cout));
             IrArgs a;
             a.X = cur;
             a.H = b.H; a.W = b.W; a.Ho = b.Ho; a.Wo = b.Wo;
@@ -644,16 +661,16 @@ private:
                     a.X = nullptr;
                     a.img = frames; a.lut = lut_; a.stem_w = stem_w_; a.stem_b = stem_b_;
                     timed("stem_ir_16x16x16", double(F) * (kFrameBytes + HWo * c.cout * TS), s,
-                          [&] { launch_stem_block1<G>(a, F, s); });
+                          [&] { launch_stem_block1<G>(a, F, s); }, 2.0 * (mac + double(F) * 90 * 160 * 16 * 27));
                 } else {
                     timed(b.fam, double(F) * (HWi * c.cin + HWo * c.cout) * TS, s,
-                          [&] { launch_ir_block<G>(i, a, F, s); });
+                          [&] { launch_ir_block<G>(i, a, F, s); }, 2.0 * mac);
                 }
                 check_launch();
             } else {
                 a.D = D_; a.part = se_part_;
                 timed(b.fam, double(F) * (HWi * c.cin + HWo * c.cexp + double(b.ntiles) * b.shp.cexpp) * TS, s,
-                      [&] { launch_ir_block<G>(i, a, F, s); });
+                      [&] { launch_ir_block<G>(i, a, F, s); }, 2.0 * mac);
                 check_launch();
                 timed("se_reduce", double(F) * (double(b.ntiles) * b.shp.cexpp + c.cexp) * TS, s, [&] {
                     launch_se_reduce(se_part_, b.ntiles, b.shp.cexpp, c.cexp, int(HWo), se_pool_, F, s);
@@ -769,7 +786,7 @@ private:
                         }
                     }
                     launch_delta(Q_, K_, V_, dec_, beta_, O_, B, kF32, s);
-                });
+                }, 2.0 * B * kT * kHeads * 4.0 * kDK * kDV);   // per token and head: decay, S^T k, k u^T, S^T q
                 check_launch();
                 timed("gated_norm", double(M) * (4.0 * 2 * kVD + kAS * kVD), s, [&] {
                     if constexpr (kF32) launch_gated_norm<float>(O_, P_, g.o_norm_w, ON_, M, s);

@@ -32,9 +32,10 @@ struct EngineConfig {
     int slots = 2;              // input/output buffer sets for the scheduler's pipelining
 };
 
-// Per-family kernel timing (HIP events on the launching stream) and algorithmic bytes.
+// Per-family kernel timing (HIP events on the launching stream), algorithmic bytes and FLOPs.  A family is one
+// kernel at the shapes the forward gives it: GEMM families are named "<role>:<kernel template>".
 struct ProfStat {
-    double ms = 0.0, bytes = 0.0;
+    double ms = 0.0, bytes = 0.0, flops = 0.0;
     long long launches = 0;
 };
 
@@ -71,6 +72,8 @@ public:
     void profile_enable(bool on);
     // flushes pending events; false if the family is unknown
     bool profile_read(const std::string& family, ProfStat* out);
+    // every family seen since profiling was enabled, in first-launch order
+    std::vector<std::string> profile_families() const { return fam_names_; }
 
 protected:
     Precision prec_ = Precision::FP32;
@@ -81,7 +84,7 @@ protected:
 
     struct Pending {
         int family;
-        double bytes;
+        double bytes, flops;
         hipEvent_t e0, e1;
     };
     bool prof_on_ = false;
@@ -89,12 +92,13 @@ protected:
     std::vector<ProfStat> fam_stats_;
     std::vector<Pending> pending_;
     std::vector<hipEvent_t> event_pool_;
-    int family_id(const char* name);
+    int family_id(const std::string& name);
     hipEvent_t take_event();
     void prof_flush();
-    template <class F> void timed(const char* family, double bytes, hipStream_t s, F&& launch) {
+    template <class F>
+    void timed(const std::string& family, double bytes, hipStream_t s, F&& launch, double flops = 0.0) {
         if (!prof_on_) { launch(); return; }
-        Pending p{family_id(family), bytes, take_event(), take_event()};
+        Pending p{family_id(family), bytes, flops, take_event(), take_event()};
         SHV_HIP_CHECK(hipEventRecord(p.e0, s));
         launch();
         SHV_HIP_CHECK(hipEventRecord(p.e1, s));

@@ -1008,18 +1008,23 @@ void launch_lds(const GemmArgs& p, hipStream_t s) {
                            nblocks);
 }
 
+// The kernel a GEMM of the MFMA tiers runs: one decision, used to launch and to name the launch.
 // N up to 160 (CNN projects and 1x1 layers): direct fragments, 16-column tiles per wave chosen to minimise
 // padded columns (at most 5 per wave); wider N (last 1x1, sequence): LDS-staged 128 x 128 workgroup tiles.
-template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
-    if (p.M <= 2048) { launch_small<T>(p, s); return; }   // latency: one clip's shapes
+struct GemmPlan {
+    enum Kind { Small, Dma, Lds, Stream, Direct } kind;
+    int nt;   // column tiles (Stream, Direct)
+};
+template <typename T> GemmPlan plan_gemm(const GemmArgs& p) {
+    if (p.M <= 2048) return {GemmPlan::Small, 0};   // latency: one clip's shapes
     // SE excitation layers (fp32 A, M = frames): one wave per 16 x 32 tile spreads them over the device (measured
     // at 2560 frames: 124 vs 282 us for the ten fc shapes with the tiled kernels)
-    if (!p.Ah && !p.scale && !p.swiglu && p.M <= 8192) { launch_small<T>(p, s); return; }
+    if (!p.Ah && !p.scale && !p.swiglu && p.M <= 8192) return {GemmPlan::Small, 0};
     const int tiles = (p.N + 15) / 16;
-    if (p.Ah && p.K % 32 == 0 && gemm_dma_enabled()) { launch_dma<T>(p, s); return; }
-    if (p.swiglu || tiles > 10) { launch_lds<T, 4, 4, 2, 2>(p, s); return; }
+    if (p.Ah && p.K % 32 == 0 && gemm_dma_enabled()) return {GemmPlan::Dma, 0};
+    if (p.swiglu || tiles > 10) return {GemmPlan::Lds, 0};
     if (p.Ah) throw std::runtime_error("gemm: pre-split A needs N > 160 or M <= 2048");
-    if (p.scale) { launch_stream<T>(p, s); return; }   // SE projects: A read once, all columns per workgroup
+    if (p.scale) return {GemmPlan::Stream, tiles};   // SE projects: A read once, all columns per workgroup
     int nt = tiles;
     if (tiles > 5) {
         int best_cols = 1 << 30;
@@ -1028,12 +1033,24 @@ template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
             if (cols < best_cols) { best_cols = cols; nt = c; }
         }
     }
-    switch (nt) {
-    case 1: launch_direct<T, 1>(p, s); break;
-    case 2: launch_direct<T, 2>(p, s); break;
-    case 3: launch_direct<T, 3>(p, s); break;
-    case 4: launch_direct<T, 4>(p, s); break;
-    default: launch_direct<T, 5>(p, s); break;
+    return {GemmPlan::Direct, nt};
+}
+
+template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
+    const GemmPlan pl = plan_gemm<T>(p);
+    switch (pl.kind) {
+    case GemmPlan::Small: launch_small<T>(p, s); return;
+    case GemmPlan::Dma: launch_dma<T>(p, s); return;
+    case GemmPlan::Lds: launch_lds<T, 4, 4, 2, 2>(p, s); return;
+    case GemmPlan::Stream: launch_stream<T>(p, s); return;
+    case GemmPlan::Direct:
+        switch (pl.nt) {
+        case 1: launch_direct<T, 1>(p, s); return;
+        case 2: launch_direct<T, 2>(p, s); return;
+        case 3: launch_direct<T, 3>(p, s); return;
+        case 4: launch_direct<T, 4>(p, s); return;
+        default: launch_direct<T, 5>(p, s); return;
+        }
     }
 }
 
@@ -1193,6 +1210,25 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
     }
     throw std::runtime_error("gemm_f32: unknown kernel variant " + std::to_string(variant));
 }
+
+std::string gemm_f32_kernel(const GemmArgs& p) {
+    return (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) ? "gemv_f32_kernel" : "gemm_f32_kernel";
+}
+
+template <typename T> std::string gemm_mfma_kernel(const GemmArgs& p) {
+    const std::string t = std::is_same<T, bf16>::value ? "bf16" : "f16";
+    const GemmPlan pl = plan_gemm<T>(p);
+    switch (pl.kind) {
+    case GemmPlan::Small: return "gemm_small_kernel<" + t + ">";
+    case GemmPlan::Dma: return Split<T>::P == 2 ? "gemm_dma_kernel<" + t + ",2,4,2>" : "gemm_dma_kernel<" + t + ",2,4,4>";
+    case GemmPlan::Lds: return "gemm_lds_kernel<" + t + ",4,4,2,2>";
+    case GemmPlan::Stream: return "gemm_stream_kernel<" + t + "," + std::to_string(pl.nt) + ">";
+    case GemmPlan::Direct: return "gemm_direct_kernel<" + t + "," + std::to_string(std::min(pl.nt, 5)) + ">";
+    }
+    return "gemm";
+}
+template std::string gemm_mfma_kernel<f16>(const GemmArgs&);
+template std::string gemm_mfma_kernel<bf16>(const GemmArgs&);
 
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s) {
     check_args(p, true);

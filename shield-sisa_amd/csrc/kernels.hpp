@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
 #include <type_traits>
 
 
@@ -46,6 +47,9 @@ template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
 // 0 automatic, 1 small-M, 2..6 direct with 1..5 column tiles per wave, 7 LDS-staged 128 x 128, 8 streaming (N <= 160,
 // every column in one workgroup; the SE projects' kernel).
 void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant);
+// The kernel (template name) that gemm_f32 / gemm_mfma run for these arguments: the profiler's family names.
+std::string gemm_f32_kernel(const GemmArgs& p);
+template <typename T> std::string gemm_mfma_kernel(const GemmArgs& p);
 template <typename T> void gemm_mfma_variant(const GemmArgs& p, hipStream_t s, int variant);
 // half tiers: last 1x1 (x [F*60][160] fp32, pre-split weight parts [960][160], + bias, hardswish) fused with the 4x4
 // pool -> pooled [F][16][960] fp32, bitwise equal to gemm_mfma + launch_pool

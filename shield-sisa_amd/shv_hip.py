@@ -68,7 +68,8 @@ _SIGS = {
     "shv_hip_forward_device": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
     "shv_hip_encode_device": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
     "shv_hip_profile_enable": (ctypes.c_int, [_P, ctypes.c_int]),
-    "shv_hip_profile_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P, _P]),
+    "shv_hip_profile_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P, _P, _P]),
+    "shv_hip_profile_list": (ctypes.c_longlong, [_P, _P, ctypes.c_size_t]),
     "shv_hip_set_dump_dir": (ctypes.c_int, [_P, ctypes.c_char_p]),
     "shv_hip_gemm_create": (_P, [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, _P, _P]),
     "shv_hip_gemm_run": (ctypes.c_int, [_P, _P, ctypes.c_longlong, _P, ctypes.c_int, _P, ctypes.c_int, _P]),
@@ -307,12 +308,20 @@ class Model:
             raise ShvError(self._err())
 
     def profile_read(self, family: str):
-        ms, n, b = ctypes.c_double(), ctypes.c_longlong(), ctypes.c_double()
+        ms, n, b, f = ctypes.c_double(), ctypes.c_longlong(), ctypes.c_double(), ctypes.c_double()
         rc = self.lib.shv_hip_profile_read(self.h, family.encode(), ctypes.byref(ms), ctypes.byref(n),
-                                           ctypes.byref(b))
+                                           ctypes.byref(b), ctypes.byref(f))
         if rc != 0:
             return None
-        return dict(ms=ms.value, launches=n.value, bytes=b.value)
+        return dict(ms=ms.value, launches=n.value, bytes=b.value, flops=f.value)
+
+    def profile_families(self) -> list:
+        n = self.lib.shv_hip_profile_list(self.h, None, 0)
+        if n < 0:
+            raise ShvError(self._err())
+        buf = ctypes.create_string_buffer(int(n) + 1)
+        self.lib.shv_hip_profile_list(self.h, buf, len(buf))
+        return [x for x in buf.value.decode().split("\n") if x]
 
     def set_dump_dir(self, d: str) -> None:
         if self.lib.shv_hip_set_dump_dir(self.h, d.encode()) != 0:
