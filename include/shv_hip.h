@@ -11,9 +11,12 @@
  * score >= shv_hip_threshold(m).  A NaN logit means "unavailable" (failed job or non-finite result).
  *
  * MODES: "fp32" = IEEE fp32 everywhere, same per-element operation order as the reference CPU exact engine
- * (GEMM K blocks of 64, the same reduction trees); always loadable.  "bf16" / "fp16" = convolution and all-row
- * GEMM operands in that type on MFMA with fp32 accumulation; residual stream, norms, recurrences, SE, SISA last
- * row and head in fp32, SISA prefix sums in double.  Approximate modes load only with a passing certificate line
+ * (GEMM K blocks of 64, the same reduction trees); always loadable.  "bf16" / "fp16" = every convolution and
+ * all-row GEMM, and the chunked delta-rule scan, on the matrix cores in that type with fp32 accumulation: each fp32
+ * operand is carried as 3 (bf16) or 2 (fp16) parts of that type, each part the rounding of what the earlier parts
+ * leave, and the significant part products are issued as separate MFMAs, so operands keep fp32-level precision.
+ * Activations are stored in fp32 in every mode; residual stream, norms, recurrences, SISA last row and head are
+ * fp32, SISA prefix sums double.  Approximate modes load only with a passing certificate line
  *   "<weights sha256> <mode> <shv_hip_compute_revision()> PASS <cert json> <cert json sha256> threshold=<%.17g>"
  * in "<weights>.hip.cert" (first line "SHIELDV_HIP_CERT_V2") whose threshold equals the loaded one exactly.
  * SIDECAR "<weights>.json": "output_sha256" must equal the weight file's SHA-256 and "threshold" must be present,

@@ -16,6 +16,26 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X); run with -m gpu")
 
 
+# measured parity margins, printed in the terminal summary (which shows even when test output is captured)
+_MARGINS = []
+
+
+@pytest.fixture
+def margin():
+    """margin(what, measured, bound): record a measured error next to the bound its test holds it to."""
+    def record(what, measured, bound):
+        _MARGINS.append((what, float(measured), float(bound)))
+    return record
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not _MARGINS:
+        return
+    terminalreporter.write_sep("-", "measured parity margins")
+    for what, v, b in _MARGINS:
+        terminalreporter.write_line(f"{what}: {v:.3e} (bound {b:.1e}, {v / b:.0%} of it)")
+
+
 def _load(name, path):
     spec = importlib.util.spec_from_file_location(name, path)
     mod = importlib.util.module_from_spec(spec)
