@@ -205,6 +205,40 @@ int shv_hip_delta_rule_noalloc(const char* mode, const float* d_q, const float* 
                                const float* d_decay, const float* d_beta, int n_windows, float* d_o, int variant,
                                void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * SHIELD-A sequence stages on the GPU.  The audio model's frontend (PCM -> 125 tokens of 384 per 10 s window,
+ * engine/audio/frontend.cpp) stays on the host; these entry points replace its per-window call of
+ * shield::sequence (engine/audio/core.hpp:26, engine/audio/sequence.cpp:349: tokens + readout -> GDN-A -> GDN-B x2
+ * -> SISA last row -> head -> logit), batched over windows, with the SHIELD-V sequence kernels.  The reference
+ * exports this stage through no C entry point of its own (its C API starts from PCM, engine/audio/include/shield.h:
+ * 39-41), so these have no one-to-one counterpart there.
+ * Modes: "fp32" (the reference's operation order in the GEMMs; elementwise functions are the device's, within a
+ * few ulp of glibc's) and "fp16" / "bf16" (split-operand matrix cores, fp32-level operand precision); the production
+ * library loads "fp32" only, the experimental library every mode.  A handle serialises its calls.
+ * Functions return 0 (or a non-NULL handle) on success, -1 / NULL + shv_hip_last_error() on failure. */
+typedef struct shv_hip_audio shv_hip_audio;
+
+/* The sequence tensors of a SHLDA001 file (container: engine/audio/weights.cpp:16-48; tensors and shapes:
+ * engine/audio/sequence.cpp:290-317) on `device`, buffers for max_windows (1..4096) windows per launch. */
+shv_hip_audio* shv_hip_audio_load(const char* weights, const char* mode, int device, int max_windows);
+void shv_hip_audio_free(shv_hip_audio* a);
+const char* shv_hip_audio_mode(const shv_hip_audio* a);
+const char* shv_hip_audio_fingerprint(const shv_hip_audio* a);   /* SHA-256 hex of the weight file */
+size_t shv_hip_audio_device_bytes(const shv_hip_audio* a);
+/* n windows of host tokens (window w at tokens + w * stride floats, stride >= 48000) -> logits[n] (host);
+ * synchronous, any n (batches of max_windows) */
+int shv_hip_audio_sequence(shv_hip_audio* a, const float* tokens, size_t n, size_t stride, float* logits);
+/* the same on device buffers, asynchronous on `stream` (NULL = the handle's own stream), n <= max_windows;
+ * d_tokens 16-byte aligned, stride a multiple of 4 */
+int shv_hip_audio_sequence_device(shv_hip_audio* a, const float* d_tokens, int n, size_t stride, float* d_logits,
+                                  void* stream);
+/* per-kernel-family timing and stage dumps, as shv_hip_profile_* / shv_hip_set_dump_dir (dump names: tokens, gdn_a,
+ * gdn_b, sisa_last, logit -- the reference's, sequence.cpp:324-345) */
+int shv_hip_audio_profile_enable(shv_hip_audio* a, int on);
+int shv_hip_audio_profile_read(shv_hip_audio* a, const char* name, double* total_ms, long long* launches,
+                               double* bytes, double* flops);
+int shv_hip_audio_set_dump_dir(shv_hip_audio* a, const char* dir);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

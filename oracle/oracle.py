@@ -16,6 +16,7 @@ HERE = Path(__file__).resolve().parent
 ORACLE_SO = HERE / "_build" / "libshv_oracle.so"
 REF_SO = HERE / "_ref" / "libshield_v_cpu.so"
 PREP_SO = HERE / "_ref" / "libshield_v_prep_crop.so"
+AUDIO_SO = HERE / "_ref" / "libshield_a_ref.so"
 FRAME_BYTES = 172800
 
 DUMP_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), ctypes.c_size_t)
@@ -172,6 +173,41 @@ class Reference:
     def close(self):
         if self.h:
             self.lib.shv_cpu_free(self.h)
+            self.h = None
+
+
+class AudioReference:
+    """The reference SHIELD-A engine's sequence stages (engine/audio, compiled by `make -C oracle ref` with
+    oracle/audio_ref_driver.cpp): tokens [125][384] -> logit, exact mode, optional stage dumps (tokens, gdn_a, gdn_b,
+    sisa_last, logit as .f32 files)."""
+
+    def __init__(self, weights):
+        if not AUDIO_SO.exists():
+            raise RuntimeError(f"{AUDIO_SO} not built (make -C oracle ref needs /root/reference)")
+        lib = ctypes.CDLL(str(AUDIO_SO))
+        lib.ora_audio_load.restype = ctypes.c_void_p
+        lib.ora_audio_load.argtypes = [ctypes.c_char_p]
+        lib.ora_audio_error.restype = ctypes.c_char_p
+        lib.ora_audio_sequence.restype = ctypes.c_int
+        lib.ora_audio_sequence.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p]
+        lib.ora_audio_free.argtypes = [ctypes.c_void_p]
+        self.lib = lib
+        self.h = lib.ora_audio_load(str(weights).encode())
+        if not self.h:
+            raise RuntimeError("reference audio load failed: " + lib.ora_audio_error().decode())
+
+    def sequence(self, tokens: np.ndarray, dump_dir: str | None = None) -> float:
+        t = np.ascontiguousarray(tokens, dtype=np.float32).reshape(125 * 384)
+        out = np.zeros(1, np.float32)
+        rc = self.lib.ora_audio_sequence(self.h, t.ctypes.data, out.ctypes.data,
+                                         None if dump_dir is None else str(dump_dir).encode())
+        if rc != 0:
+            raise RuntimeError(self.lib.ora_audio_error().decode())
+        return out[0]
+
+    def close(self):
+        if self.h:
+            self.lib.ora_audio_free(self.h)
             self.h = None
 
 

@@ -3,6 +3,7 @@
 // -1 / NULL plus the thread-local error string.
 #include "../../include/shv_hip.h"
 
+#include "audio.hpp"
 #include "cert.hpp"
 #include "kernels.hpp"
 #include "lanes.hpp"
@@ -12,6 +13,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -34,6 +36,13 @@ struct shv_hip_model {
 
 struct shv_hip_gemm {
     std::unique_ptr<shv::PwGemm> g;
+};
+
+struct shv_hip_audio {
+    std::string mode, fingerprint;
+    int device = 0;
+    std::mutex mu;                              // one call at a time drives the engine
+    std::unique_ptr<shv::AudioEngine> eng;
 };
 
 namespace {
@@ -59,6 +68,23 @@ bool options_valid(const shv_hip_options& o) {
            o.max_host_tokens >= 0 && o.max_host_tokens <= (1 << 20) && o.token_slots >= 0 &&
            o.token_slots <= (1 << 22) && o.max_delay_us >= 0;
 }
+
+// Makes `dev` current for a scope, restoring the caller's device after.
+class DeviceScope {
+public:
+    explicit DeviceScope(int dev) {
+        SHV_HIP_CHECK(hipGetDevice(&prev_));
+        if (dev != prev_) SHV_HIP_CHECK(hipSetDevice(dev));
+        switched_ = dev != prev_;
+    }
+    ~DeviceScope() {
+        if (switched_) (void)hipSetDevice(prev_);
+    }
+
+private:
+    int prev_ = 0;
+    bool switched_ = false;
+};
 
 hipStream_t stream_or(shv_hip_model* m, void* s) {
     return s ? static_cast<hipStream_t>(s) : m->lanes->compute_stream();
@@ -306,6 +332,111 @@ int shv_hip_delta_rule_noalloc(const char* mode, const float* d_q, const float* 
     return guarded([&] {
         shv::run_delta_rule_noalloc(mode_or_throw(mode), d_q, d_k, d_v, d_decay, d_beta, n_windows, d_o, variant,
                                     static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
+// ------------------------------------------------------------------------------------------ SHIELD-A sequence
+shv_hip_audio* shv_hip_audio_load(const char* weights, const char* mode, int device, int max_windows) {
+    try {
+        if (!weights) throw std::runtime_error("null weights path");
+        if (max_windows < 1 || max_windows > 4096) throw std::runtime_error("max_windows must be in [1, 4096]");
+        std::unique_ptr<shv_hip_audio> a(new shv_hip_audio());
+        a->mode = mode ? mode : "fp32";
+        shv::Precision p;
+        if (!shv::parse_precision(a->mode, &p))
+            throw std::runtime_error("unknown mode '" + a->mode + "' (fp32, bf16, fp16)");
+#ifndef SHV_HIP_EXPERIMENTAL
+        if (p != shv::Precision::FP32)
+            throw std::runtime_error("audio mode " + a->mode + " is for offline evaluation (experimental library)");
+#endif
+        const shv::AudioHost ah = shv::load_audio_host(weights);
+        a->fingerprint = ah.sha256;
+        int count = 0;
+        SHV_HIP_CHECK(hipGetDeviceCount(&count));
+        if (device < 0 || device >= count) throw std::runtime_error("device out of range");
+        a->device = device;
+        DeviceScope ds(device);
+        a->eng = shv::make_audio_engine(ah, p, max_windows, true);
+        shv::sched::clear_error();
+        return a.release();
+    } catch (const std::exception& e) {
+        shv::sched::set_error(e.what());
+        return nullptr;
+    }
+}
+
+void shv_hip_audio_free(shv_hip_audio* a) {
+    if (!a) return;
+    try {
+        DeviceScope ds(a->device);
+        a->eng.reset();
+    } catch (const std::exception&) {
+        a->eng.reset();
+    }
+    delete a;
+}
+
+const char* shv_hip_audio_mode(const shv_hip_audio* a) { return a ? a->mode.c_str() : nullptr; }
+const char* shv_hip_audio_fingerprint(const shv_hip_audio* a) { return a ? a->fingerprint.c_str() : nullptr; }
+size_t shv_hip_audio_device_bytes(const shv_hip_audio* a) { return a ? a->eng->device_bytes() : 0; }
+
+int shv_hip_audio_sequence(shv_hip_audio* a, const float* tokens, size_t n, size_t stride, float* logits) {
+    return guarded([&] {
+        if (!a || !tokens || !logits) throw std::runtime_error("null argument");
+        if (n == 0) throw std::runtime_error("empty request");
+        if (stride < size_t(shv::kAudioWindowFloats)) throw std::runtime_error("window stride below 48000 floats");
+        std::lock_guard<std::mutex> lk(a->mu);
+        DeviceScope ds(a->device);
+        a->eng->run_host(tokens, (long long)stride, (long long)n, logits);
+        return 0;
+    });
+}
+
+int shv_hip_audio_sequence_device(shv_hip_audio* a, const float* d_tokens, int n, size_t stride, float* d_logits,
+                                  void* stream) {
+    return guarded([&] {
+        if (!a || !d_tokens || !d_logits) throw std::runtime_error("null argument");
+        if (n < 1 || n > a->eng->max_windows()) throw std::runtime_error("window count out of range");
+        if (stride < size_t(shv::kAudioWindowFloats)) throw std::runtime_error("window stride below 48000 floats");
+        std::lock_guard<std::mutex> lk(a->mu);
+        DeviceScope ds(a->device);
+        a->eng->run_device(d_tokens, (long long)stride, n, d_logits, static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
+int shv_hip_audio_profile_enable(shv_hip_audio* a, int on) {
+    return guarded([&] {
+        if (!a) throw std::runtime_error("null handle");
+        std::lock_guard<std::mutex> lk(a->mu);
+        DeviceScope ds(a->device);
+        a->eng->profile_enable(on != 0);
+        return 0;
+    });
+}
+
+int shv_hip_audio_profile_read(shv_hip_audio* a, const char* name, double* total_ms, long long* launches,
+                               double* bytes, double* flops) {
+    return guarded([&] {
+        if (!a || !name) throw std::runtime_error("null argument");
+        std::lock_guard<std::mutex> lk(a->mu);
+        DeviceScope ds(a->device);
+        shv::ProfStat st;
+        if (!a->eng->profile_read(name, &st)) return -1;
+        if (total_ms) *total_ms = st.ms;
+        if (launches) *launches = st.launches;
+        if (bytes) *bytes = st.bytes;
+        if (flops) *flops = st.flops;
+        return 0;
+    });
+}
+
+int shv_hip_audio_set_dump_dir(shv_hip_audio* a, const char* dir) {
+    return guarded([&] {
+        if (!a) throw std::runtime_error("null handle");
+        std::lock_guard<std::mutex> lk(a->mu);
+        a->eng->set_dump_dir(dir ? dir : "");
         return 0;
     });
 }

@@ -5,6 +5,7 @@
 
 #include "dev_common.hpp"
 #include "kernels.hpp"
+#include "stack.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -54,14 +55,14 @@ int Engine::frame_bucket(int F) const { return cfg_.use_graphs ? bucket_for(F, c
 int Engine::window_bucket(int B) const { return cfg_.use_graphs ? bucket_for(B, cfg_.max_windows) : B; }
 
 // ------------------------------------------------------------------------------------------------ profiling
-int Engine::family_id(const std::string& name) {
+int Profiler::family_id(const std::string& name) {
     for (size_t i = 0; i < fam_names_.size(); ++i)
         if (fam_names_[i] == name) return int(i);
     fam_names_.push_back(name);
     fam_stats_.push_back(ProfStat{});
     return int(fam_names_.size() - 1);
 }
-hipEvent_t Engine::take_event() {
+hipEvent_t Profiler::take_event() {
     if (!event_pool_.empty()) {
         hipEvent_t e = event_pool_.back();
         event_pool_.pop_back();
@@ -71,7 +72,7 @@ hipEvent_t Engine::take_event() {
     SHV_HIP_CHECK(hipEventCreate(&e));
     return e;
 }
-void Engine::prof_flush() {
+void Profiler::prof_flush() {
     for (const Pending& p : pending_) {
         SHV_HIP_CHECK(hipEventSynchronize(p.e1));
         float ms = 0.0f;
@@ -86,12 +87,16 @@ void Engine::prof_flush() {
     }
     pending_.clear();
 }
-void Engine::profile_enable(bool on) {
+Profiler::~Profiler() {
+    for (const Pending& p : pending_) { (void)hipEventDestroy(p.e0); (void)hipEventDestroy(p.e1); }
+    for (hipEvent_t e : event_pool_) (void)hipEventDestroy(e);
+}
+void Profiler::profile_enable(bool on) {
     prof_flush();
     for (ProfStat& s : fam_stats_) s = ProfStat{};
     prof_on_ = on;
 }
-bool Engine::profile_read(const std::string& family, ProfStat* out) {
+bool Profiler::profile_read(const std::string& family, ProfStat* out) {
     prof_flush();
     for (size_t i = 0; i < fam_names_.size(); ++i)
         if (fam_names_[i] == family) {
@@ -103,47 +108,6 @@ bool Engine::profile_read(const std::string& family, ProfStat* out) {
 
 namespace {
 
-inline void check_launch() { SHV_HIP_CHECK(hipGetLastError()); }
-
-// G selects how GEMM operands reach the multipliers: float = exact-order VALU, f16 / bf16 = split-operand MFMA
-template <typename G> void gemm_t(const GemmArgs& p, hipStream_t s);
-template <> void gemm_t<float>(const GemmArgs& p, hipStream_t s) { gemm_f32(p, s); }
-template <> void gemm_t<f16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<f16>(p, s); }
-template <> void gemm_t<bf16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<bf16>(p, s); }
-
-// a GEMM weight on the device: `parts` arrays of N*K elements of the flavour's type, `stride` elements apart
-struct DevW {
-    const void* w = nullptr;
-    long long stride = 0;
-};
-
-// owner of device allocations
-class DevMem {
-public:
-    DevMem() = default;
-    DevMem(const DevMem&) = delete;
-    DevMem& operator=(const DevMem&) = delete;
-    ~DevMem() { release(); }
-    void release() {
-        for (void* p : ptrs_) (void)hipFree(p);
-        ptrs_.clear();
-        bytes_ = 0;
-    }
-    template <class U> U* make(size_t n) {
-        void* p = nullptr;
-        const size_t bytes = std::max<size_t>(n * sizeof(U), 256);
-        SHV_HIP_CHECK(hipMalloc(&p, bytes));
-        ptrs_.push_back(p);
-        bytes_ += bytes;
-        return static_cast<U*>(p);
-    }
-    size_t bytes() const { return bytes_; }
-
-private:
-    std::vector<void*> ptrs_;
-    size_t bytes_ = 0;
-};
-
 struct GraphKey {
     int kind;
     const void* in;
@@ -154,9 +118,6 @@ struct GraphKey {
     }
 };
 
-double gemm_bytes(long long M, int N, int K, int ta, int tw, int tc, int tr) {
-    return double(M) * K * ta + double(N) * K * tw + double(M) * N * tc + (tr ? double(M) * N * tr : 0.0);
-}
 
 template <typename G>
 class EngineT final : public Engine {
@@ -175,9 +136,14 @@ public:
         fused_ = !kF32 && !(nf && *nf && std::strcmp(nf, "0") != 0);
         SHV_HIP_CHECK(hipStreamCreateWithFlags(&setup_, hipStreamNonBlocking));
         try {
+            Uploader upl(wmem_, setup_);
+            upl_ = &upl;
             upload_weights(hm);
             alloc_buffers(hm);
+            upl.finish();
+            upl_ = nullptr;
         } catch (...) {
+            upl_ = nullptr;
             (void)hipStreamDestroy(setup_);
             throw;
         }
@@ -191,8 +157,6 @@ public:
     ~EngineT() override {
         for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
         if (capture_) (void)hipStreamDestroy(capture_);
-        for (const Pending& p : pending_) { (void)hipEventDestroy(p.e0); (void)hipEventDestroy(p.e1); }
-        for (hipEvent_t e : event_pool_) (void)hipEventDestroy(e);
     }
 
     void encode_slot(int slot, int F, hipStream_t s) override {
@@ -231,7 +195,8 @@ private:
     // of the work stream (the scheduler lands one lane while it starts the other), and that wait must not meet a
     // stream in capture mode.
     hipStream_t capture_ = nullptr;
-    DevMem wmem_, amem_, staging_;
+    DevMem wmem_, amem_;
+    Uploader* upl_ = nullptr;   // alive while the constructor uploads the weights
 
     // ---------------------------------------------------------------- weights
     struct Blk {
@@ -252,60 +217,23 @@ private:
         DevW fexp_w, fproj_w;
         const float *fexp_b = nullptr, *fdw_w = nullptr, *fdw_b = nullptr, *fproj_b = nullptr;
     };
-    struct Gdn {
-        const float *norm_w, *ffn_norm_w, *conv_w, *conv_b, *neg_rate, *dt_bias, *o_norm_w;
-        DevW in_w, out_w, up_w, down_w;   // up_w: SwiGLU gate/up interleaved, 1920 rows
-    };
     const float *lut_ = nullptr, *stem_w_ = nullptr, *stem_b_ = nullptr;
     Blk blk_[15];
     DevW last_w_;
     const float* last_b_ = nullptr;
     DevW proj_w_;
     const float *pos_ = nullptr, *readout_ = nullptr;
-    Gdn gdn_[2]{};
-    const float *s_attn_norm_ = nullptr, *s_ffn_norm_ = nullptr, *s_in_b_ = nullptr, *s_lam_ = nullptr;
-    DevW s_in_w_;
-    const float *s_qc_w_ = nullptr, *s_o_w_ = nullptr, *s_up_w_ = nullptr, *s_down_w_ = nullptr;
-    const float *fn_w_ = nullptr, *h_w0_ = nullptr, *h_b0_ = nullptr, *h_w2_ = nullptr;
-    float h_b2_ = 0.0f;
+    std::unique_ptr<SeqStack<G>> seq_;   // GDN-A, GDN-B x2, SISA last row, head
 
-    const float* up(const float* src, size_t n) {
-        float* d = wmem_.make<float>(n);
-        SHV_HIP_CHECK(hipMemcpy(d, src, n * sizeof(float), hipMemcpyHostToDevice));
-        return d;
-    }
-    const float* up(const std::vector<float>& v) { return up(v.data(), v.size()); }
-    // fp32 [N][K] rows -> device parts of U with a row permutation, converted by the repack kernel on the GPU
+    const float* up(const float* src, size_t n) { return upl_->up(src, n); }
+    const float* up(const std::vector<float>& v) { return upl_->up(v); }
     template <typename U> DevW repack(const std::vector<float>& src, int N, int K, int perm) {
-        const int parts = weight_parts<U>();
-        float* st = staging_.make<float>(src.size());
-        SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
-        U* d = wmem_.make<U>(size_t(parts) * N * K);
-        launch_repack<U>(st, d, N, K, perm, parts, setup_);
-        check_launch();
-        return DevW{d, (long long)N * K};
+        return upl_->repack<U>(src, N, K, perm);
     }
     template <typename U> DevW repack_pad(const std::vector<float>& src, int N, int K, int Np, int Kp) {
-        const int parts = weight_parts<U>();
-        float* st = staging_.make<float>(src.size());
-        SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
-        U* d = wmem_.make<U>(size_t(parts) * Np * Kp);
-        launch_repack_pad<U>(st, d, N, K, Np, Kp, parts, setup_);
-        check_launch();
-        return DevW{d, (long long)Np * Kp};
+        return upl_->repack_pad<U>(src, N, K, Np, Kp);
     }
-    // [rows][n] -> [rows][np], zero padded
-    const float* up_pad(const std::vector<float>& v, int rows, int n, int np) {
-        std::vector<float> o(size_t(rows) * np, 0.0f);
-        for (int r = 0; r < rows; ++r)
-            for (int j = 0; j < n; ++j) o[size_t(r) * np + j] = v[size_t(r) * n + j];
-        return up(o);
-    }
-    static std::vector<float> concat(const Linear& a, const Linear& b) {
-        std::vector<float> v(a.w);
-        v.insert(v.end(), b.w.begin(), b.w.end());
-        return v;
-    }
+    const float* up_pad(const std::vector<float>& v, int rows, int n, int np) { return upl_->up_pad(v, rows, n, np); }
 
     void upload_fused(int i, const BlockHost& b, Blk& d) {
         if constexpr (kF32) {
@@ -368,58 +296,21 @@ private:
         proj_w_ = repack<G>(hm.proj.w, hm.proj.N, hm.proj.K, 0);
         pos_ = up(hm.pos);
         readout_ = up(hm.readout);
-        const int swiglu_perm = kF32 ? 1 : 2;
-        for (int g = 0; g < 2; ++g) {
-            const GdnHost& gh = hm.gdn[g];
-            Gdn& d = gdn_[g];
-            d.norm_w = up(gh.norm_w);
-            d.ffn_norm_w = up(gh.ffn_norm_w);
-            d.conv_w = up(gh.conv_w);
-            d.conv_b = up(gh.conv_b);
-            d.neg_rate = up(gh.neg_rate, kHeads);
-            d.dt_bias = up(gh.dt_bias, kHeads);
-            d.o_norm_w = up(gh.o_norm_w);
-            d.in_w = repack<G>(gh.in.w, gh.in.N, gh.in.K, 0);
-            d.out_w = repack<G>(gh.out.w, gh.out.N, gh.out.K, 0);
-            d.up_w = repack<G>(concat(gh.gate, gh.up), 2 * kFF, kD, swiglu_perm);
-            d.down_w = repack<G>(gh.down.w, gh.down.N, gh.down.K, 0);
-        }
-        const SisaHost& S = hm.sisa;
-        s_attn_norm_ = up(S.attn_norm_w);
-        s_ffn_norm_ = up(S.ffn_norm_w);
-        s_in_w_ = repack<G>(S.in.w, S.in.N, S.in.K, 0);
-        s_in_b_ = up(S.in.b);
-        s_qc_w_ = up(concat(S.q, S.c));                      // [576][384]: W_Q rows then W_C rows
-        s_o_w_ = up(S.o.w);
-        s_up_w_ = static_cast<const float*>(repack<float>(concat(S.gate, S.up), 2 * kFF, kD, 1).w);
-        s_down_w_ = up(S.down.w);
-        s_lam_ = up(S.lam, kHeads);
-        fn_w_ = up(hm.final_norm_w);
-        h_w0_ = up(hm.head0.w);
-        h_b0_ = up(hm.head0.b);
-        h_w2_ = up(hm.head2_w);
-        h_b2_ = hm.head2_b;
-        SHV_HIP_CHECK(hipStreamSynchronize(setup_));
-        staging_.release();
+        // the sequence stages: SHIELD-V arithmetic, 321-token windows, GDN-B residual R + v / sqrt(2)
+        static constexpr SeqSpec kVideo{kT, false, 2, {"h0", "after_gdn_a", "after_gdn_b", "after_sisa_last", "logit"}};
+        seq_.reset(new SeqStack<G>(kVideo, hm.gdn, hm.sisa, hm.final_norm_w, hm.head0, hm.head2_w, hm.head2_b,
+                                   cfg_.max_windows, *upl_, amem_));
     }
 
     // ---------------------------------------------------------------- activations
     float *X_ = nullptr, *XB_ = nullptr, *E_ = nullptr, *D_ = nullptr, *PO_ = nullptr, *se_part_ = nullptr;
     bool fused_ = false;
     float *se_pool_ = nullptr, *se_hid_ = nullptr, *se_scale_ = nullptr;
-    float *H_ = nullptr, *P_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *dec_ = nullptr, *beta_ = nullptr,
-          *O_ = nullptr;
-    float* dwork_ = nullptr;     // half tiers: the chunked delta rule's per-chunk products
-    bool delta_chunked_ = false;
-    float *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;   // fp32 tier: the sequence GEMMs' A operands
-    G *XNh_ = nullptr, *ONh_ = nullptr, *HIDh_ = nullptr;    // MFMA tiers: the same, written pre-split by producers
-    long long mrows_ = 0;                                     // rows of those buffers (part stride = mrows_ * width)
-    float *XL_ = nullptr, *QC_ = nullptr, *Y_ = nullptr, *X1_ = nullptr, *X2_ = nullptr, *HIDL_ = nullptr;
     float* tok_direct_ = nullptr;
     const float** tokptr_direct_ = nullptr;
 
     void alloc_buffers(const HostModel& hm) {
-        const size_t Fm = size_t(cfg_.max_frames), Bm = size_t(cfg_.max_windows), Mm = Bm * kT;
+        const size_t Fm = size_t(cfg_.max_frames), Bm = size_t(cfg_.max_windows);
         size_t xe = size_t(90) * 160 * 16, ee = size_t(60) * kCnnOut, de = 0;
         for (int i = 0; i < 15; ++i) {
             const BlockHost& b = hm.blocks[i];
@@ -441,34 +332,6 @@ private:
         se_pool_ = amem_.make<float>(Fm * kCnnOut);
         se_hid_ = amem_.make<float>(Fm * 256);
         se_scale_ = amem_.make<float>(Fm * kCnnOut);
-        H_ = amem_.make<float>(Mm * kD);
-        P_ = amem_.make<float>(Mm * kGld);
-        Q_ = amem_.make<float>(Mm * kD);
-        K_ = amem_.make<float>(Mm * kD);
-        V_ = amem_.make<float>(Mm * kVD);
-        dec_ = amem_.make<float>(Mm * 8);
-        beta_ = amem_.make<float>(Mm * 8);
-        O_ = amem_.make<float>(Mm * kVD);
-        // half tiers: the chunked delta-rule scan (SHV_HIP_DELTA_SEQ=1 keeps the token-by-token kernel, for A/B runs)
-        const char* ds = std::getenv("SHV_HIP_DELTA_SEQ");
-        delta_chunked_ = !kF32 && !(ds && *ds && std::strcmp(ds, "0") != 0);
-        if (delta_chunked_) dwork_ = amem_.make<float>(delta_chunk_floats(int(Bm)));
-        mrows_ = (long long)Mm;
-        if constexpr (kF32) {
-            XN_ = amem_.make<float>(Mm * kD);
-            ON_ = amem_.make<float>(Mm * kVD);
-            HID_ = amem_.make<float>(Mm * kFF);
-        } else {
-            XNh_ = amem_.make<G>(weight_parts<G>() * Mm * kD);
-            ONh_ = amem_.make<G>(weight_parts<G>() * Mm * kVD);
-            HIDh_ = amem_.make<G>(weight_parts<G>() * Mm * kFF);
-        }
-        XL_ = amem_.make<float>(Bm * kD);
-        QC_ = amem_.make<float>(Bm * 576);
-        Y_ = amem_.make<float>(Bm * kD);
-        X1_ = amem_.make<float>(Bm * kD);
-        X2_ = amem_.make<float>(Bm * kD);
-        HIDL_ = amem_.make<float>(Bm * kFF);
         // direct path: the engine's own token buffer and the window -> frame table of a plain predict
         const size_t Fd = std::min(Fm, Bm * kFrames);
         tok_direct_ = amem_.make<float>(Fd * kTokenFloats);
@@ -497,7 +360,7 @@ private:
     std::map<GraphKey, hipGraphExec_t> graphs_;
     // body(q) issues the pass on stream q: directly on s, or into a graph captured on capture_ and launched on s
     template <class F> void run_graph(const GraphKey& key, hipStream_t s, F&& body) {
-        if (!cfg_.use_graphs || !dump_dir_.empty() || prof_on_) {
+        if (!cfg_.use_graphs || !dump_dir_.empty() || profiling()) {
             body(s);
             return;
         }
@@ -524,41 +387,14 @@ private:
 
     // ---------------------------------------------------------------- debug dumps (frame 0 / window 0)
     template <typename U> void dump(const char* name, const U* dev, size_t n, hipStream_t s) {
-        if (dump_dir_.empty()) return;
-        SHV_HIP_CHECK(hipStreamSynchronize(s));
-        std::vector<U> h(n);
-        SHV_HIP_CHECK(hipMemcpy(h.data(), dev, n * sizeof(U), hipMemcpyDeviceToHost));
-        std::vector<float> f(n);
-        for (size_t i = 0; i < n; ++i) f[i] = float(h[i]);
-        std::ofstream o(dump_dir_ + "/" + name + ".f32", std::ios::binary);
-        o.write(reinterpret_cast<const char*>(f.data()), std::streamsize(n * sizeof(float)));
+        dump_f32(dump_dir_, name, dev, n, s);
     }
 
-    // GEMM in this engine's flavour (or the exact fp32 VALU kernel for the fp32-only layers)
-    // profiling family of a GEMM: its role and the kernel the dispatcher picks for these arguments
-    std::string gemm_family(const char* role, const GemmArgs& p, bool f32) const {
-        if (!prof_on_) return std::string();
-        if constexpr (!kF32) {
-            if (!f32) return std::string(role) + ":" + gemm_mfma_kernel<G>(p);
-        }
-        return std::string(role) + ":" + gemm_f32_kernel(p);
+    // GEMM in this engine's flavour, and the exact fp32 VALU kernel for the fp32-only layers
+    void gemm(const char* role, const GemmArgs& p, const DevW& w, hipStream_t s) {
+        GemmRunner<G>{*this}.gemm(role, p, w, s);
     }
-    void gemm(const char* role, GemmArgs p, const DevW& w, hipStream_t s) {
-        p.W = w.w;
-        p.wstride = w.stride;
-        // A is read pre-split where the producer wrote parts (sequence GEMMs), else as fp32
-        const int abytes = (p.Ah && !kF32) ? int(sizeof(G)) * weight_parts<G>() : 4;
-        const double bytes = gemm_bytes(p.M, p.N, p.K, abytes, kF32 ? 4 : int(sizeof(G)) * weight_parts<G>(),
-                                        p.swiglu ? (p.Ch ? int(sizeof(G)) * weight_parts<G>() / 2 : 2) : 4,
-                                        p.res ? 4 : 0);
-        timed(gemm_family(role, p, false), bytes, s, [&] { gemm_t<G>(p, s); }, 2.0 * p.M * p.N * p.K);
-        check_launch();
-    }
-    void gemm32(const char* role, const GemmArgs& p, hipStream_t s) {
-        timed(gemm_family(role, p, true), gemm_bytes(p.M, p.N, p.K, 4, 4, p.swiglu ? 2 : 4, p.res ? 4 : 0), s,
-              [&] { gemm_f32(p, s); }, 2.0 * p.M * p.N * p.K);
-        check_launch();
-    }
+    void gemm32(const char* role, const GemmArgs& p, hipStream_t s) { GemmRunner<G>{*this}.gemm32(role, p, s); }
 
     // ---------------------------------------------------------------- CNN
     void run_encode(const uint8_t* frames, int F, float* tokens, hipStream_t s) {
@@ -744,121 +580,10 @@ private:
     }
 
     // ---------------------------------------------------------------- sequence
-    // the A operand of a sequence GEMM: fp32 (exact tier) or the producer's split parts (MFMA tiers)
-    static constexpr int kAS = kF32 ? 4 : int(sizeof(G)) * weight_parts<G>();   // bytes per A value
-    void set_a(GemmArgs& p, const float* a32, const G* ah, int width) const {
-        p.lda = width;
-        if constexpr (kF32) p.A = a32;
-        else { p.Ah = ah; p.astride = mrows_ * width; }
-    }
-    void rmsnorm_all(const float* w, hipStream_t s, int M) {
-        timed("rmsnorm", double(M) * kD * (4 + kAS), s, [&] {
-            if constexpr (kF32) launch_rmsnorm<float>(H_, kD, w, XN_, kD, M, s);
-            else launch_rmsnorm<G>(H_, kD, w, XNh_, kD, M, s, mrows_ * kD);
-        });
-        check_launch();
-    }
-
     void run_classify(const float* const* tokptr, int B, float* logits, hipStream_t s) {
-        const int M = B * kT;
-        timed("assemble", double(M) * kD * 8, s, [&] { launch_assemble(tokptr, pos_, readout_, H_, B, s); });
+        timed("assemble", double(B) * kT * kD * 8, s, [&] { launch_assemble(tokptr, pos_, readout_, seq_->h(), B, s); });
         check_launch();
-        dump("h0", H_, size_t(kT) * kD, s);
-        for (int st = 0; st < 2; ++st) {
-            const Gdn& g = gdn_[st];
-            const int reps = st == 0 ? 1 : 2;
-            for (int r = 0; r < reps; ++r) {
-                rmsnorm_all(g.norm_w, s, M);
-                GemmArgs pi;
-                pi.M = M; pi.N = kGn; pi.K = kD;
-                set_a(pi, XN_, XNh_, kD); pi.ldw = kD;
-                pi.C = P_; pi.ldc = kGld;
-                gemm("gemm_seq", pi, g.in_w, s);
-                timed("gdn_prep", double(M) * (4.0 * 1548 * 4 + 4.0 * (2 * kD + kVD + 16)), s, [&] {
-                    launch_gdn_prep(P_, g.conv_w, g.conv_b, g.neg_rate, g.dt_bias, Q_, K_, V_, dec_, beta_, B, s);
-                });
-                check_launch();
-                timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s, [&] {
-                    if constexpr (!kF32) {
-                        if (delta_chunked_) {
-                            launch_delta_chunked<G>(Q_, K_, V_, dec_, beta_, O_, dwork_, B, s);
-                            return;
-                        }
-                    }
-                    launch_delta(Q_, K_, V_, dec_, beta_, O_, B, kF32, s);
-                }, 2.0 * B * kT * kHeads * 4.0 * kDK * kDV);   // per token and head: decay, S^T k, k u^T, S^T q
-                check_launch();
-                timed("gated_norm", double(M) * (4.0 * 2 * kVD + kAS * kVD), s, [&] {
-                    if constexpr (kF32) launch_gated_norm<float>(O_, P_, g.o_norm_w, ON_, M, s);
-                    else launch_gated_norm<G>(O_, P_, g.o_norm_w, ONh_, M, s, mrows_ * kVD);
-                });
-                check_launch();
-                GemmArgs po;
-                po.M = M; po.N = kD; po.K = kVD;
-                set_a(po, ON_, ONh_, kVD); po.ldw = kVD;
-                po.C = H_; po.ldc = kD;
-                po.R = H_; po.ldr = kD; po.res = reps == 2 ? 2 : 1;
-                gemm("gemm_seq", po, g.out_w, s);
-            }
-            rmsnorm_all(g.ffn_norm_w, s, M);
-            GemmArgs pu;
-            pu.M = M; pu.N = 2 * kFF; pu.K = kD;
-            set_a(pu, XN_, XNh_, kD); pu.ldw = kD;
-            pu.ldc = kFF; pu.swiglu = 1;
-            if constexpr (kF32) pu.C = HID_;
-            else { pu.Ch = HIDh_; pu.cstride = mrows_ * kFF; }
-            gemm("gemm_seq", pu, g.up_w, s);
-            GemmArgs pd;
-            pd.M = M; pd.N = kD; pd.K = kFF;
-            set_a(pd, HID_, HIDh_, kFF); pd.ldw = kFF;
-            pd.C = H_; pd.ldc = kD;
-            pd.R = H_; pd.ldr = kD; pd.res = 1;
-            gemm("gemm_seq", pd, g.down_w, s);
-            dump(st == 0 ? "after_gdn_a" : "after_gdn_b", H_, size_t(kT) * kD, s);
-        }
-        // SISA block, last row only: all-row K/V/B/theta/alpha/forget projection, last-row Q|C in fp32
-        rmsnorm_all(s_attn_norm_, s, M);
-        GemmArgs pa;
-        pa.M = M; pa.N = kSn; pa.K = kD;
-        set_a(pa, XN_, XNh_, kD); pa.ldw = kD;
-        pa.bias = s_in_b_;
-        pa.C = P_; pa.ldc = kSld;
-        gemm("gemm_seq", pa, s_in_w_, s);
-        const float* hlast = H_ + size_t(kT - 1) * kD;
-        const long long ldlast = (long long)kT * kD;
-        timed("rmsnorm", double(B) * kD * 8, s,
-              [&] { launch_rmsnorm<float>(hlast, ldlast, s_attn_norm_, XL_, kD, B, s); });
-        check_launch();
-        GemmArgs pq;
-        pq.M = B; pq.N = 576; pq.K = kD;
-        pq.A = XL_; pq.lda = kD; pq.W = s_qc_w_; pq.ldw = kD;
-        pq.C = QC_; pq.ldc = 576;
-        gemm32("gemm_f32_small", pq, s);
-        timed("sisa", double(B) * kT * kSn * 4, s, [&] { launch_sisa(P_, QC_, s_lam_, Y_, B, s); });
-        check_launch();
-        GemmArgs pw;
-        pw.M = B; pw.N = kD; pw.K = kD;
-        pw.A = Y_; pw.lda = kD; pw.W = s_o_w_; pw.ldw = kD;
-        pw.C = X1_; pw.ldc = kD;
-        pw.R = hlast; pw.ldr = ldlast; pw.res = 1;
-        gemm32("gemm_f32_small", pw, s);
-        timed("rmsnorm", double(B) * kD * 8, s, [&] { launch_rmsnorm<float>(X1_, kD, s_ffn_norm_, XL_, kD, B, s); });
-        check_launch();
-        GemmArgs pu;
-        pu.M = B; pu.N = 2 * kFF; pu.K = kD;
-        pu.A = XL_; pu.lda = kD; pu.W = s_up_w_; pu.ldw = kD;
-        pu.C = HIDL_; pu.ldc = kFF; pu.swiglu = 1;
-        gemm32("gemm_f32_small", pu, s);
-        GemmArgs pd;
-        pd.M = B; pd.N = kD; pd.K = kFF;
-        pd.A = HIDL_; pd.lda = kFF; pd.W = s_down_w_; pd.ldw = kFF;
-        pd.C = X2_; pd.ldc = kD;
-        pd.R = X1_; pd.ldr = kD; pd.res = 1;
-        gemm32("gemm_f32_small", pd, s);
-        dump("after_sisa_last", X2_, kD, s);
-        timed("head", double(B) * kD * 4, s, [&] { launch_head(X2_, fn_w_, h_w0_, h_b0_, h_w2_, h_b2_, logits, B, s); });
-        check_launch();
-        dump("logit", logits, 1, s);
+        seq_->run(B, logits, s, *this, dump_dir_);
     }
 };
 

@@ -39,7 +39,47 @@ struct ProfStat {
     long long launches = 0;
 };
 
-class Engine {
+// Event timing of kernel families.  Used by one thread at a time (the engine's driver).
+class Profiler {
+public:
+    Profiler() = default;
+    Profiler(const Profiler&) = delete;
+    Profiler& operator=(const Profiler&) = delete;
+    ~Profiler();
+    void profile_enable(bool on);
+    bool profiling() const { return prof_on_; }
+    // flushes pending events; false if the family is unknown
+    bool profile_read(const std::string& family, ProfStat* out);
+    // every family seen since profiling was enabled, in first-launch order
+    std::vector<std::string> profile_families() const { return fam_names_; }
+    // launch() issues one kernel family on s; timed between two events when profiling is on
+    template <class F>
+    void timed(const std::string& family, double bytes, hipStream_t s, F&& launch, double flops = 0.0) {
+        if (!prof_on_) { launch(); return; }
+        Pending p{family_id(family), bytes, flops, take_event(), take_event()};
+        SHV_HIP_CHECK(hipEventRecord(p.e0, s));
+        launch();
+        SHV_HIP_CHECK(hipEventRecord(p.e1, s));
+        pending_.push_back(p);
+    }
+
+private:
+    struct Pending {
+        int family;
+        double bytes, flops;
+        hipEvent_t e0, e1;
+    };
+    bool prof_on_ = false;
+    std::vector<std::string> fam_names_;
+    std::vector<ProfStat> fam_stats_;
+    std::vector<Pending> pending_;
+    std::vector<hipEvent_t> event_pool_;
+    int family_id(const std::string& name);
+    hipEvent_t take_event();
+    void prof_flush();
+};
+
+class Engine : public Profiler {
 public:
     struct Slot {
         uint8_t* d_frames = nullptr;      // [max_frames][172800]
@@ -69,11 +109,6 @@ public:
     int window_bucket(int B) const;
 
     void set_dump_dir(const std::string& d) { dump_dir_ = d; }
-    void profile_enable(bool on);
-    // flushes pending events; false if the family is unknown
-    bool profile_read(const std::string& family, ProfStat* out);
-    // every family seen since profiling was enabled, in first-launch order
-    std::vector<std::string> profile_families() const { return fam_names_; }
 
 protected:
     Precision prec_ = Precision::FP32;
@@ -81,29 +116,6 @@ protected:
     std::vector<Slot> slots_;
     size_t weight_bytes_ = 0, device_bytes_ = 0;
     std::string dump_dir_;
-
-    struct Pending {
-        int family;
-        double bytes, flops;
-        hipEvent_t e0, e1;
-    };
-    bool prof_on_ = false;
-    std::vector<std::string> fam_names_;
-    std::vector<ProfStat> fam_stats_;
-    std::vector<Pending> pending_;
-    std::vector<hipEvent_t> event_pool_;
-    int family_id(const std::string& name);
-    hipEvent_t take_event();
-    void prof_flush();
-    template <class F>
-    void timed(const std::string& family, double bytes, hipStream_t s, F&& launch, double flops = 0.0) {
-        if (!prof_on_) { launch(); return; }
-        Pending p{family_id(family), bytes, flops, take_event(), take_event()};
-        SHV_HIP_CHECK(hipEventRecord(p.e0, s));
-        launch();
-        SHV_HIP_CHECK(hipEventRecord(p.e1, s));
-        pending_.push_back(p);
-    }
 };
 
 std::unique_ptr<Engine> make_engine(const HostModel& hm, Precision p, const EngineConfig& cfg);

@@ -25,11 +25,12 @@ namespace shv {
 namespace {
 
 // ------------------------------------------------------------------------------------------------ epilogue
-// out = act(v + bias) (+ residual, or + residual after / sqrt(2) when res == 2)
+// out = act(v + bias) (+ residual: res 1 R + v, res 2 R + v / sqrt(2), res 3 R + 0.70710678f * v)
 __device__ __forceinline__ float epi_value(const GemmArgs& p, float v, float b, float res) {
     if (p.bias) v = v + b;
     v = apply_act(v, p.act);
-    if (p.res) v = p.res == 2 ? res + v / 1.41421356237309515f : res + v;
+    if (p.res == 3) v = res + 0.7071067811865475244f * v;
+    else if (p.res) v = p.res == 2 ? res + v / 1.41421356237309515f : res + v;
     return v;
 }
 // Epilogue of the 4 x J outputs one thread holds (rows row(i), columns col(j)).  Every bias and residual operand is
@@ -1155,6 +1156,7 @@ void check_args(const GemmArgs& p, bool mfma) {
     if (p.Ch && (p.C || !p.swiglu || p.cstride < (long long)(p.M - 1) * p.ldc + p.N / 2))
         throw std::runtime_error("gemm: a pre-split output is a SwiGLU output with a part stride");
     if (p.res && !p.R) throw std::runtime_error("gemm: residual without R");
+    if (p.res < 0 || p.res > 3) throw std::runtime_error("gemm: unknown residual mode");
     if (p.scale && (p.scale_rows <= 0 || p.ld_scale < p.K)) throw std::runtime_error("gemm: bad SE scale");
     if (mfma) {
         // 32-byte A and 16-byte W fragments: K, lda, ldw, ld_scale multiples of 8 elements

@@ -28,9 +28,10 @@ const BlockCfg kBlocks[15] = {
 
 namespace {
 
-// ------------------------------------------------------------------------------------------ SHLDV001 container
-// "SHLDV001", u32 tensor count, then per tensor: u32 name length, name bytes, u32 rank, u32 dims[rank],
-// u64 element count, fp32 values (little endian); nothing after the last tensor (tools/export_v.py:3-8).
+// ------------------------------------------------------------------------------------------ SHLDV001 / SHLDA001
+// container: the 8-byte magic, u32 tensor count, then per tensor: u32 name length, name bytes, u32 rank, u32 dims[rank],
+// u64 element count, fp32 values (little endian); nothing after the last tensor (tools/export_v.py:3-8;
+// the audio file alike, engine/audio/weights.cpp:16-48).
 class Cursor {
 public:
     Cursor(const std::vector<uint8_t>& buf) : p_(buf.data()), end_(buf.data() + buf.size()) {}
@@ -55,7 +56,7 @@ private:
 // Every tensor of the file, by name; each must be claimed exactly once with its expected shape.
 class Weights {
 public:
-    explicit Weights(const std::string& path) {
+    Weights(const std::string& path, const char* magic) {
         std::ifstream in(path, std::ios::binary | std::ios::ate);
         if (!in) throw std::runtime_error("cannot open weights: " + path);
         const std::streamoff size = in.tellg();
@@ -71,7 +72,7 @@ public:
         shv_sha256_final(&h, digest);
         shv_sha256_hex(digest, hex);
         sha_ = hex;
-        index(path);
+        index(path, magic);
     }
     const std::string& sha256() const { return sha_; }
     size_t file_bytes() const { return file_.size(); }
@@ -119,10 +120,10 @@ private:
         if (it == table_.end()) throw std::runtime_error("weights: missing tensor " + name);
         return it->second;
     }
-    void index(const std::string& path) {
+    void index(const std::string& path, const char* magic) {
         Cursor c(file_);
-        if (std::memcmp(c.bytes(8, "magic"), "SHLDV001", 8) != 0)
-            throw std::runtime_error("weights: not a SHLDV001 file: " + path);
+        if (std::memcmp(c.bytes(8, "magic"), magic, 8) != 0)
+            throw std::runtime_error(std::string("weights: not a ") + magic + " file: " + path);
         const uint32_t n = c.number<uint32_t>("tensor count");
         if (n < 1 || n > 10000) throw std::runtime_error("weights: invalid tensor count");
         uint64_t values = 0;
@@ -309,12 +310,106 @@ Linear linear(const std::vector<float>& w, int N, int K, const std::vector<float
 
 float softplus_host(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
+// Tensor names that differ between the two models' GDN blocks (engine/model/runtime.cpp:329-380 and
+// engine/audio/sequence.cpp:299-310); the mixer tensors are named alike.
+struct GdnNames { const char *norm, *gate, *up, *down; };
+constexpr GdnNames kVideoGdn{"norm.weight", "ffn.gate.weight", "ffn.up.weight", "ffn.down.weight"};
+constexpr GdnNames kAudioGdn{"mixer_norm.weight", "ffn.w_gate.weight", "ffn.w_up.weight", "ffn.w_down.weight"};
+
+// One GDN block: in-projection fused [q|k|v|g|a|b] (kGq..kGb), short-conv taps transposed to [tap][1536],
+// neg_rate = -expf(A_log).
+void load_gdn(Weights& ts, const std::string& p, const GdnNames& nm, GdnHost& G) {
+    const std::string x = p + "mixer.";
+    G.norm_w = ts.take(p + nm.norm, {kD});
+    G.ffn_norm_w = ts.take(p + "ffn_norm.weight", {kD});
+    std::vector<float> w(size_t(kGn) * kD, 0.0f);
+    auto put = [&](const char* n, int rows, int at) {
+        const auto& src = ts.take(x + n, {rows, kD});
+        std::memcpy(&w[size_t(at) * kD], src.data(), sizeof(float) * size_t(rows) * kD);
+    };
+    put("q_proj.weight", 384, kGq);
+    put("k_proj.weight", 384, kGk);
+    put("v_proj.weight", 768, kGv);
+    put("g_proj.weight", 768, kGg);
+    put("a_proj.weight", 6, kGa);
+    put("b_proj.weight", 6, kGb);
+    G.in = linear(w, kGn, kD);
+    G.conv_w.assign(4 * 1536, 0.0f);
+    G.conv_b.assign(1536, 0.0f);
+    const char* convs[3] = {"q_conv1d", "k_conv1d", "v_conv1d"};
+    const int widths[3] = {384, 384, 768}, offs[3] = {0, 384, 768};
+    for (int i = 0; i < 3; ++i) {
+        const auto& wt = ts.take(x + convs[i] + ".weight", {widths[i], 1, 4});
+        const auto& bt = ts.take(x + convs[i] + ".bias", {widths[i]});
+        for (int c = 0; c < widths[i]; ++c) {
+            for (int j = 0; j < 4; ++j) G.conv_w[size_t(j) * 1536 + offs[i] + c] = wt[size_t(c) * 4 + j];
+            G.conv_b[size_t(offs[i]) + c] = bt[c];
+        }
+    }
+    const auto& al = ts.take(x + "A_log", {kHeads});
+    const auto& dt = ts.take(x + "dt_bias", {kHeads});
+    for (int h = 0; h < kHeads; ++h) {
+        G.neg_rate[h] = -expf(al[h]);
+        G.dt_bias[h] = dt[h];
+    }
+    G.o_norm_w = ts.take(x + "o_norm.weight", {kDV});
+    G.out = linear(ts.take(x + "o_proj.weight", {kD, kVD}), kD, kVD);
+    G.gate = linear(ts.take(p + nm.gate, {kFF, kD}), kFF, kD);
+    G.up = linear(ts.take(p + nm.up, {kFF, kD}), kFF, kD);
+    G.down = linear(ts.take(p + nm.down, {kD, kFF}), kD, kFF);
+}
+
+// The SISA block: all-row projection fused [K|V|B|theta|alpha|forget] with the alpha / forget biases,
+// lam = softplus(lambda_raw).  Both models name these tensors alike.
+void load_sisa(Weights& ts, SisaHost& S) {
+    const std::string a = "sisa.attn.";
+    S.attn_norm_w = ts.take("sisa.attn_norm.weight", {kD});
+    S.ffn_norm_w = ts.take("sisa.ffn_norm.weight", {kD});
+    std::vector<float> w(size_t(kSn) * kD, 0.0f), b(kSn, 0.0f);
+    auto put = [&](const char* n, int rows, int at) {
+        const auto& src = ts.take(a + n, {rows, kD});
+        std::memcpy(&w[size_t(at) * kD], src.data(), sizeof(float) * size_t(rows) * kD);
+    };
+    put("W_K.weight", 384, kSk);
+    put("W_V.weight", 384, kSv);
+    put("W_B.weight", 192, kSb);
+    put("theta_proj.weight", 96, kSth);
+    put("alpha_proj.weight", 6, kSal);
+    put("forget_proj.weight", 6, kSfg);
+    const auto& ab = ts.take(a + "alpha_proj.bias", {kHeads});
+    const auto& fb = ts.take(a + "forget_proj.bias", {kHeads});
+    for (int h = 0; h < kHeads; ++h) {
+        b[size_t(kSal) + h] = ab[h];
+        b[size_t(kSfg) + h] = fb[h];
+    }
+    S.in = linear(w, kSn, kD, &b);
+    S.q = linear(ts.take(a + "W_Q.weight", {kD, kD}), kD, kD);
+    S.c = linear(ts.take(a + "W_C.weight", {192, kD}), 192, kD);
+    S.o = linear(ts.take(a + "W_O.weight", {kD, kD}), kD, kD);
+    const auto& lr = ts.take(a + "lambda_raw", {kHeads});
+    for (int h = 0; h < kHeads; ++h) S.lam[h] = softplus_host(lr[h]);
+    S.gate = linear(ts.take("sisa.ffn.w_gate.weight", {kFF, kD}), kFF, kD);
+    S.up = linear(ts.take("sisa.ffn.w_up.weight", {kFF, kD}), kFF, kD);
+    S.down = linear(ts.take("sisa.ffn.w_down.weight", {kD, kFF}), kD, kFF);
+}
+
+// Final norm + Linear(384, 128) + Linear(128, 1)
+void load_head(Weights& ts, const char* norm, const std::string& out, std::vector<float>& norm_w, Linear& head0,
+               std::vector<float>& head2_w, float& head2_b) {
+    norm_w = ts.take(norm, {kD});
+    const auto& b0 = ts.take("head.0.bias", {128});
+    head0 = linear(ts.take("head.0.weight", {128, kD}), 128, kD, &b0);
+    head2_w = ts.take(out + ".weight", {1, 128});
+    head2_b = ts.take(out + ".bias", {1})[0];
+}
+
 }  // namespace
 
 HostModel load_host_model(const std::string& path) {
+
     HostModel hm;
     hm.path = path;
-    Weights ts(path);
+    Weights ts(path, "SHLDV001");
     hm.sha256 = ts.sha256();
     hm.file_bytes = ts.file_bytes();
     hm.threshold = check_sidecar(path, hm.sha256);
@@ -402,91 +497,25 @@ HostModel load_host_model(const std::string& path) {
         hm.readout = ts.take("readout", {1, 1, kD});
     }
 
-    for (int g = 0; g < 2; ++g) {
-        GdnHost& G = hm.gdn[g];
-        const std::string p = g == 0 ? "gdn_a." : "gdn_b.";
-        const std::string x = p + "mixer.";
-        G.norm_w = ts.take(p + "norm.weight", {kD});
-        G.ffn_norm_w = ts.take(p + "ffn_norm.weight", {kD});
-        std::vector<float> w(size_t(kGn) * kD, 0.0f);
-        auto put = [&](const char* n, int rows, int at) {
-            const auto& src = ts.take(x + n, {rows, kD});
-            std::memcpy(&w[size_t(at) * kD], src.data(), sizeof(float) * size_t(rows) * kD);
-        };
-        put("q_proj.weight", 384, kGq);
-        put("k_proj.weight", 384, kGk);
-        put("v_proj.weight", 768, kGv);
-        put("g_proj.weight", 768, kGg);
-        put("a_proj.weight", 6, kGa);
-        put("b_proj.weight", 6, kGb);
-        G.in = linear(w, kGn, kD);
-        G.conv_w.assign(4 * 1536, 0.0f);
-        G.conv_b.assign(1536, 0.0f);
-        const char* convs[3] = {"q_conv1d", "k_conv1d", "v_conv1d"};
-        const int widths[3] = {384, 384, 768}, offs[3] = {0, 384, 768};
-        for (int i = 0; i < 3; ++i) {
-            const auto& wt = ts.take(x + convs[i] + ".weight", {widths[i], 1, 4});
-            const auto& bt = ts.take(x + convs[i] + ".bias", {widths[i]});
-            for (int c = 0; c < widths[i]; ++c) {
-                for (int j = 0; j < 4; ++j) G.conv_w[size_t(j) * 1536 + offs[i] + c] = wt[size_t(c) * 4 + j];
-                G.conv_b[size_t(offs[i]) + c] = bt[c];
-            }
-        }
-        const auto& al = ts.take(x + "A_log", {kHeads});
-        const auto& dt = ts.take(x + "dt_bias", {kHeads});
-        for (int h = 0; h < kHeads; ++h) {
-            G.neg_rate[h] = -expf(al[h]);
-            G.dt_bias[h] = dt[h];
-        }
-        G.o_norm_w = ts.take(x + "o_norm.weight", {kDV});
-        G.out = linear(ts.take(x + "o_proj.weight", {kD, kVD}), kD, kVD);
-        G.gate = linear(ts.take(p + "ffn.gate.weight", {kFF, kD}), kFF, kD);
-        G.up = linear(ts.take(p + "ffn.up.weight", {kFF, kD}), kFF, kD);
-        G.down = linear(ts.take(p + "ffn.down.weight", {kD, kFF}), kD, kFF);
-    }
-
-    {
-        SisaHost& S = hm.sisa;
-        const std::string a = "sisa.attn.";
-        S.attn_norm_w = ts.take("sisa.attn_norm.weight", {kD});
-        S.ffn_norm_w = ts.take("sisa.ffn_norm.weight", {kD});
-        std::vector<float> w(size_t(kSn) * kD, 0.0f), b(kSn, 0.0f);
-        auto put = [&](const char* n, int rows, int at) {
-            const auto& src = ts.take(a + n, {rows, kD});
-            std::memcpy(&w[size_t(at) * kD], src.data(), sizeof(float) * size_t(rows) * kD);
-        };
-        put("W_K.weight", 384, kSk);
-        put("W_V.weight", 384, kSv);
-        put("W_B.weight", 192, kSb);
-        put("theta_proj.weight", 96, kSth);
-        put("alpha_proj.weight", 6, kSal);
-        put("forget_proj.weight", 6, kSfg);
-        const auto& ab = ts.take(a + "alpha_proj.bias", {kHeads});
-        const auto& fb = ts.take(a + "forget_proj.bias", {kHeads});
-        for (int h = 0; h < kHeads; ++h) {
-            b[size_t(kSal) + h] = ab[h];
-            b[size_t(kSfg) + h] = fb[h];
-        }
-        S.in = linear(w, kSn, kD, &b);
-        S.q = linear(ts.take(a + "W_Q.weight", {kD, kD}), kD, kD);
-        S.c = linear(ts.take(a + "W_C.weight", {192, kD}), 192, kD);
-        S.o = linear(ts.take(a + "W_O.weight", {kD, kD}), kD, kD);
-        const auto& lr = ts.take(a + "lambda_raw", {kHeads});
-        for (int h = 0; h < kHeads; ++h) S.lam[h] = softplus_host(lr[h]);
-        S.gate = linear(ts.take("sisa.ffn.w_gate.weight", {kFF, kD}), kFF, kD);
-        S.up = linear(ts.take("sisa.ffn.w_up.weight", {kFF, kD}), kFF, kD);
-        S.down = linear(ts.take("sisa.ffn.w_down.weight", {kD, kFF}), kD, kFF);
-    }
-    hm.final_norm_w = ts.take("final_norm.weight", {kD});
-    {
-        const auto& b0 = ts.take("head.0.bias", {128});
-        hm.head0 = linear(ts.take("head.0.weight", {128, kD}), 128, kD, &b0);
-    }
-    hm.head2_w = ts.take("head.2.weight", {1, 128});
-    hm.head2_b = ts.take("head.2.bias", {1})[0];
+    for (int g = 0; g < 2; ++g) load_gdn(ts, g == 0 ? "gdn_a." : "gdn_b.", kVideoGdn, hm.gdn[g]);
+    load_sisa(ts, hm.sisa);
+    load_head(ts, "final_norm.weight", "head.2", hm.final_norm_w, hm.head0, hm.head2_w, hm.head2_b);
 
     ts.expect_all_claimed();
     return hm;
+}
+
+AudioHost load_audio_host(const std::string& path) {
+    AudioHost ah;
+    ah.path = path;
+    Weights ts(path, "SHLDA001");
+    ah.sha256 = ts.sha256();
+    ah.file_bytes = ts.file_bytes();
+    ah.readout = ts.take("readout", {1, 1, kD});
+    for (int g = 0; g < 2; ++g) load_gdn(ts, g == 0 ? "gdn_a." : "gdn_b.", kAudioGdn, ah.gdn[g]);
+    load_sisa(ts, ah.sisa);
+    load_head(ts, "head_norm.weight", "head.3", ah.final_norm_w, ah.head0, ah.head2_w, ah.head2_b);
+    return ah;
 }
 
 }  // namespace shv

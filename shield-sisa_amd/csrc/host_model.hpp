@@ -8,6 +8,7 @@
 namespace shv {
 
 constexpr int kImgH = 180, kImgW = 320, kFrames = 20, kTokPerFrame = 16, kD = 384, kT = 321;
+constexpr int kTAudio = 126;   // SHIELD-A windows: 125 frontend tokens + the readout (engine/audio/sequence.cpp:19)
 constexpr int kHeads = 6, kDK = 64, kDV = 128, kVD = 768, kFF = 960, kPairs = 16, kCnnOut = 960;
 constexpr size_t kFrameBytes = size_t(kImgH) * kImgW * 3;   // 172800
 constexpr size_t kTokenFloats = size_t(kTokPerFrame) * kD;   // 6144
@@ -75,5 +76,21 @@ struct HostModel {
 // tensors, no trailing bytes), hashes it, validates the sidecar "<path>.json" (output_sha256 == file SHA-256,
 // threshold finite in (0,1)) and folds BatchNorm (eps 1e-3) in double.  Throws std::runtime_error.
 HostModel load_host_model(const std::string& path);
+
+// SHIELD-A's sequence stages (engine/audio/sequence.cpp:290-317): the tensors of a SHLDA001 file that the stages
+// read, in the same host layouts as SHIELD-V's (final norm = head_norm, head2 = head.3).  The file's frontend
+// tensors are indexed and left alone.  Throws std::runtime_error.
+struct AudioHost {
+    std::string path, sha256;
+    size_t file_bytes = 0;
+    std::vector<float> readout;          // [384]
+    GdnHost gdn[2];
+    SisaHost sisa;
+    std::vector<float> final_norm_w;
+    Linear head0;
+    std::vector<float> head2_w;
+    float head2_b = 0.0f;
+};
+AudioHost load_audio_host(const std::string& path);
 
 }  // namespace shv

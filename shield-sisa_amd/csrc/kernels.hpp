@@ -7,6 +7,8 @@
 #include <string>
 #include <type_traits>
 
+#include "host_model.hpp"
+
 
 namespace shv {
 
@@ -15,7 +17,7 @@ typedef __bf16 bf16;
 
 // C[m][n] = epilogue(sum_k A[m][k] * W[n][k]); A, C, R fp32 row-major; W row-major [N][K] (PyTorch Linear /
 // 1x1 conv layout).  Epilogue, per element in this order: + bias[n]; activation; residual (res 1: R + v,
-// res 2: R + v / 1.41421356f); stored fp32.  swiglu: fp32 tier -- W rows (2j, 2j+1) = (gate_j, up_j); MFMA tiers --
+// res 2: R + v / 1.41421356f, res 3: R + 0.70710678f * v); stored fp32.  swiglu: fp32 tier -- W rows (2j, 2j+1) = (gate_j, up_j); MFMA tiers --
 // W rows in 16-row panels (gate panel, up panel, ...); out[m][j] = silu(gate) * up.
 // Optional SE prologue: A[m][k] := scale[(m / scale_rows) * ld_scale + k] * A[m][k].
 // MFMA tiers: W holds the weight's parts (fp16: hi, lo; bf16: hi, mid, lo) wstride elements apart.
@@ -138,36 +140,43 @@ void native_crops(const CropJob* jobs, int n, uint8_t* out, bool i420, hipStream
 // ---------------------------------------------------------------- sequence (fp32 residual stream)
 void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,
                      hipStream_t s);
+// SHIELD-A windows: tokens [B] windows of [125][384] (window stride ldw floats, a multiple of 4) + readout ->
+// h [B*126][384]
+void launch_assemble_audio(const float* tokens, long long ldw, const float* readout, float* h, int B, hipStream_t s);
 // out[r] = (x[r] * (1 / sqrt(sum(x^2) / 384 + 1e-6))) * w with the reference's 16-lane sum tree.  T = f16 / bf16:
 // out holds the split parts of each value (part stride pstride elements), the pre-split A of the next GEMM.
 template <typename T>
 void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s,
                     long long pstride = 0);
-// short conv4 + SiLU on q|k|v, per-head L2 norm (q * 0.125), decay = exp(neg_rate * softplus(a + dt_bias)),
-// beta = sigmoid(b).  P [rows][2320] -> Q, K [rows][384], V [rows][768], dec, beta [rows][8]
+// Every sequence kernel takes the window length T: 321 (SHIELD-V) or 126 (SHIELD-A); others throw.
+// short conv4 + SiLU on q|k|v, per-head L2 norm, decay = exp(neg_rate * softplus(a + dt_bias)), beta = sigmoid(b).
+// P [rows][2320] -> Q, K [rows][384], V [rows][768], dec, beta [rows][8].  Video: q * (1/sqrt(max(ss,1e-6))) * 0.125;
+// audio: q and k * 1/max(sqrt(ss), 1e-12), q unscaled (engine/audio/sequence.cpp:119-124)
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
                      const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
-                     hipStream_t s);
-// gated delta rule, sequential over 321 tokens from zero state, fp32; O [rows][768].  exact: the reference's
+                     hipStream_t s, int T = kT, bool audio = false);
+// gated delta rule, sequential over T tokens from zero state, fp32; O [rows][768].  exact: the reference's
 // 64-key fma chains (fp32 tier); else each column's keys split over 4 lane rows, partial sums added in a fixed order
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
-                  int B, bool exact, hipStream_t s);
+                  int B, bool exact, hipStream_t s, int T = kT);
 // Half tiers: the same recurrence over chunks of 32 tokens on the split-operand matrix cores (a parallel prep of
-// every chunk's state-independent products into `work`, delta_chunk_floats(B) floats, then one scan per
+// every chunk's state-independent products into `work`, delta_chunk_floats(B, T) floats, then one scan per
 // (window, head)); equal to the token-by-token form up to rounding.
-size_t delta_chunk_floats(int B);
+size_t delta_chunk_floats(int B, int T = kT);
 template <typename T>
 void launch_delta_chunked(const float* Q, const float* K, const float* V, const float* dec, const float* beta,
-                          float* O, float* work, int B, hipStream_t s);
-// ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768] (T = f16 / bf16: split parts, as launch_rmsnorm)
+                          float* O, float* work, int B, hipStream_t s, int Tw = kT);
+// ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768] (T = f16 / bf16: split parts, as launch_rmsnorm).
+// audio: o * 0.125 first and eps 1e-5 (engine/audio/sequence.cpp:160-171); video eps 1e-6
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,
-                       long long pstride = 0);
+                       long long pstride = 0, bool audio = false);
 // SISA last-row attention per (window, head): S [rows][1072] (B rotated in place), QC [B][576] -> Y [B][384]
-void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s);
-// final RMSNorm + Linear(384,128) + SiLU + Linear(128,1); w0 [128][384]
+void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s, int T = kT);
+// final RMSNorm + Linear(384,128) + activation + Linear(128,1); w0 [128][384]; activation SiLU (video) or
+// exact GELU (audio, engine/audio/sequence.cpp:318-330)
 void launch_head(const float* X, const float* norm_w, const float* w0, const float* b0, const float* w2, float b2,
-                 float* logits, int B, hipStream_t s);
+                 float* logits, int B, hipStream_t s, bool audio = false);
 // pool[slots[f]] = tokens[f] for slots[f] >= 0
 void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool, int F, hipStream_t s);
 

@@ -49,6 +49,17 @@ assemble_kernel(const float* const* __restrict__ tok_ptrs, const float* __restri
     *reinterpret_cast<float4*>(h + row * kD + j) = v;
 }
 
+// SHIELD-A: h[b*126 + t] = tokens[b * ldw + t * 384] (t < 125), the readout at t = 125 (engine/audio/sequence.cpp:
+// 322-323); no position table.
+__global__ void __launch_bounds__(96)
+assemble_audio_kernel(const float* __restrict__ tokens, long long ldw, const float* __restrict__ readout,
+                      float* __restrict__ h) {
+    const long long row = blockIdx.x;
+    const int b = int(row / kTAudio), t = int(row % kTAudio), j = threadIdx.x * 4;
+    const float* src = t == kTAudio - 1 ? readout + j : tokens + b * ldw + (long long)t * kD + j;
+    *reinterpret_cast<float4*>(h + row * kD + j) = *reinterpret_cast<const float4*>(src);
+}
+
 // ------------------------------------------------------------------------------------------------ RMSNorm
 // 16 lanes per row (4 rows per wave): lane l accumulates x[l + 16 i]^2, tree16, then (x * inv) * w
 template <typename T>
@@ -88,16 +99,18 @@ __device__ __forceinline__ void row3_gather(float v, float (&out)[3]) {
 // v channels h*128+l, h*128+64+l, and keeps those columns of the last 4 rows of P in registers while it walks the
 // run, so each element of P is read once (plus a 3-row halo per run).  Per row: short conv acc from +0, taps t-3..t
 // in order, + bias, SiLU (isa_impl.hpp:871-889); L2 norms with the 16-lane structure over 64 elements
-// (isa_impl.hpp:893-906); gates with device libm (expf, log1pf).
+// (isa_impl.hpp:893-906); gates with device libm (expf, log1pf).  TT tokens per window; AUDIO selects SHIELD-A's
+// L2 norm (no q scale here: its output is scaled after the recurrence).
 constexpr int GP_T = 4;
+template <int TT, bool AUDIO>
 __global__ void __launch_bounds__(384)
 gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const float* __restrict__ cb,
                 const float* __restrict__ neg_rate, const float* __restrict__ dt_bias, float* __restrict__ Q,
                 float* __restrict__ K, float* __restrict__ V, float* __restrict__ dec, float* __restrict__ beta) {
-    constexpr int RUNS = (kT + GP_T - 1) / GP_T;
-    const int b = blockIdx.x / RUNS, t0 = (blockIdx.x % RUNS) * GP_T, t1 = min(kT, t0 + GP_T);
+    constexpr int RUNS = (TT + GP_T - 1) / GP_T;
+    const int b = blockIdx.x / RUNS, t0 = (blockIdx.x % RUNS) * GP_T, t1 = min(TT, t0 + GP_T);
     const int h = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const long long row0 = (long long)b * kT;
+    const long long row0 = (long long)b * TT;
     const int cq = kGq + h * 64 + l, ck = kGk + h * 64 + l, cv0 = kGv + h * 128 + l, cv1 = cv0 + 64;
     const int wq = h * 64 + l, wk = 384 + h * 64 + l, wv0 = 768 + h * 128 + l, wv1 = wv0 + 64;
     float w[4][4], bias[4];   // [column][tap]
@@ -184,9 +197,15 @@ gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const
         }
         aq = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tree16_lane0(aq)), 48));
         ak = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tree16_lane0(ak)), 48));
-        const float iq = 1.0f / sqrtf(aq + 1e-6f), ik = 1.0f / sqrtf(ak + 1e-6f);
-        Q[row * kD + h * 64 + l] = (q * iq) * 0.125f;
-        K[row * kD + h * 64 + l] = k * ik;
+        if constexpr (AUDIO) {   // SHIELD-A: x / max(|x|, 1e-12); q unscaled (engine/audio/sequence.cpp:136-143)
+            const float iq = 1.0f / fmaxf(sqrtf(aq), 1e-12f), ik = 1.0f / fmaxf(sqrtf(ak), 1e-12f);
+            Q[row * kD + h * 64 + l] = q * iq;
+            K[row * kD + h * 64 + l] = k * ik;
+        } else {
+            const float iq = 1.0f / sqrtf(aq + 1e-6f), ik = 1.0f / sqrtf(ak + 1e-6f);
+            Q[row * kD + h * 64 + l] = (q * iq) * 0.125f;
+            K[row * kD + h * 64 + l] = k * ik;
+        }
         if (l == 0) {
             dec[row * 8 + h] = expf(neg_rate[h] * softplus_f(ga + dt_bias[h]));
             beta[row * 8 + h] = 1.0f / (1.0f + expf(-gb));
@@ -206,6 +225,7 @@ gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const
 // 32-token chunks are staged in LDS (q and k read as broadcasts), so no global load sits on the serial chain.
 constexpr int DCH = 32;
 constexpr int DCOLS = 64;   // value columns per workgroup
+template <int TT>
 __global__ void __launch_bounds__(DCOLS)
 delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
              const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ O) {
@@ -216,13 +236,13 @@ delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const flo
     __shared__ __attribute__((aligned(16))) float sk[DCH + 1][64];
     __shared__ float sv[DCH][DCOLS];
     __shared__ float sa[DCH], sb[DCH];
-    const long long row0 = (long long)b * kT;
+    const long long row0 = (long long)b * TT;
     float S[64];
 #pragma unroll
     for (int j = 0; j < 64; ++j) S[j] = 0.0f;
     float pred = 0.0f;
-    for (int t0 = 0; t0 < kT; t0 += DCH) {
-        const int nt = min(DCH, kT - t0);
+    for (int t0 = 0; t0 < TT; t0 += DCH) {
+        const int nt = min(DCH, TT - t0);
         // staging loads are unconditional (token index clamped) so that all of them are in flight together;
         // slots past the last token are then zeroed (q, v) or repeat the last k (the next-k slot of the last
         // token, unused downstream)
@@ -234,7 +254,7 @@ delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const flo
         for (int k = 0; k < QKR; ++k) {
             const int i = threadIdx.x + k * DCOLS;
             const int tt = i >> 4, j4 = (i & 15) * 4;
-            const int t = min(t0 + tt, kT - 1);
+            const int t = min(t0 + tt, TT - 1);
             rq[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             rk[k] = rq[k];
             if (i < QK4) {
@@ -243,23 +263,23 @@ delta_kernel(const float* __restrict__ Q, const float* __restrict__ K, const flo
             }
         }
 #pragma unroll
-        for (int tt = 0; tt < DCH; ++tt) rv[tt] = V[(row0 + min(t0 + tt, kT - 1)) * kVD + col];
+        for (int tt = 0; tt < DCH; ++tt) rv[tt] = V[(row0 + min(t0 + tt, TT - 1)) * kVD + col];
 #pragma unroll
         for (int k = 0; k < QKR; ++k) {
             const int i = threadIdx.x + k * DCOLS;
             const int tt = i >> 4, j4 = (i & 15) * 4;
             if (i < QK4) {
                 if (tt < DCH)
-                    *reinterpret_cast<float4*>(&sq[tt][j4]) = t0 + tt < kT ? rq[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    *reinterpret_cast<float4*>(&sq[tt][j4]) = t0 + tt < TT ? rq[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 *reinterpret_cast<float4*>(&sk[tt][j4]) = rk[k];
             }
         }
 #pragma unroll
-        for (int tt = 0; tt < DCH; ++tt) sv[tt][c] = t0 + tt < kT ? rv[tt] : 0.0f;
+        for (int tt = 0; tt < DCH; ++tt) sv[tt][c] = t0 + tt < TT ? rv[tt] : 0.0f;
         if (threadIdx.x < DCH) {
             const int t = t0 + threadIdx.x;
-            sa[threadIdx.x] = t < kT ? dec[(row0 + t) * 8 + h] : 0.0f;
-            sb[threadIdx.x] = t < kT ? beta[(row0 + t) * 8 + h] : 0.0f;
+            sa[threadIdx.x] = t < TT ? dec[(row0 + t) * 8 + h] : 0.0f;
+            sb[threadIdx.x] = t < TT ? beta[(row0 + t) * 8 + h] : 0.0f;
         }
         __syncthreads();
         for (int i = 0; i < nt; ++i) {
@@ -387,7 +407,7 @@ constexpr int kDeltaPipeWaves = 1024;   // one wave per SIMD (256 CUs x 4)
 // into registers while the current chunk runs (the rolled form, for grids of several waves per SIMD, loads them at
 // the start of the chunk and keeps its registers for occupancy).  Both forms issue the same arithmetic per token, so their results
 // are bitwise equal.
-template <int KQ, bool PIPE>   // KQ: key groups per column: 2 (halves), 4 (rows) or 8 (half rows)
+template <int KQ, bool PIPE, int TT>   // KQ: key groups per column: 2 (halves), 4 (rows) or 8 (half rows)
 __global__ void __launch_bounds__(64)
 delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
                    const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ O) {
@@ -401,7 +421,7 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
     __shared__ __attribute__((aligned(16))) float sk[DCH + 1][64];
     __shared__ float sv[DCH][DS_COLS];
     __shared__ float sa[DCH], sb[DCH];
-    const long long row0 = (long long)b * kT;
+    const long long row0 = (long long)b * TT;
     // chunk operands in registers: loads are unconditional (token index clamped) so all of them are in flight
     // together; slots past the last token are then zeroed (q, v, decay, beta) or repeat the last k (the next-k slot
     // of the last token, unused downstream)
@@ -415,7 +435,7 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
         for (int k = 0; k < QKR; ++k) {
             const int i = lane + k * 64;
             const int tt = i >> 4, j4 = (i & 15) * 4;
-            const int t = min(t0 + tt, kT - 1);
+            const int t = min(t0 + tt, TT - 1);
             rq[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             rk[k] = rq[k];
             if (i < QK4) {
@@ -424,9 +444,9 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
             }
         }
 #pragma unroll
-        for (int k = 0; k < VR; ++k) rv[k] = V[(row0 + min(t0 + kq + KQ * k, kT - 1)) * kVD + col];
+        for (int k = 0; k < VR; ++k) rv[k] = V[(row0 + min(t0 + kq + KQ * k, TT - 1)) * kVD + col];
         if (lane < DCH) {
-            const int t = min(t0 + lane, kT - 1);
+            const int t = min(t0 + lane, TT - 1);
             ra = dec[(row0 + t) * 8 + h];
             rb = beta[(row0 + t) * 8 + h];
         }
@@ -438,17 +458,17 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
             const int tt = i >> 4, j4 = (i & 15) * 4;
             if (i < QK4) {
                 if (tt < DCH)
-                    *reinterpret_cast<float4*>(&sq[tt][j4]) = t0 + tt < kT ? rq[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    *reinterpret_cast<float4*>(&sq[tt][j4]) = t0 + tt < TT ? rq[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 *reinterpret_cast<float4*>(&sk[tt][j4]) = rk[k];
             }
         }
 #pragma unroll
         for (int k = 0; k < VR; ++k) {
             const int tt = kq + KQ * k;
-            sv[tt][c16] = t0 + tt < kT ? rv[k] : 0.0f;
+            sv[tt][c16] = t0 + tt < TT ? rv[k] : 0.0f;
         }
         if (lane < DCH) {
-            const bool in = t0 + lane < kT;
+            const bool in = t0 + lane < TT;
             sa[lane] = in ? ra : 0.0f;
             sb[lane] = in ? rb : 0.0f;
         }
@@ -460,8 +480,8 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
     float ob[DCH / KQ] = {};   // PIPE: this lane's outputs of the last full chunk, tokens kq + KQ m
     int ob_t0 = -1;            // first token of that chunk (-1: none pending)
     if (PIPE) fetch(0);
-    for (int t0 = 0; t0 < kT; t0 += DCH) {
-        const int nt = min(DCH, kT - t0);
+    for (int t0 = 0; t0 < TT; t0 += DCH) {
+        const int nt = min(DCH, TT - t0);
         if (!PIPE) fetch(t0);   // PIPE: fetched while the previous chunk ran
         stage(t0);
         __syncthreads();
@@ -470,7 +490,7 @@ delta_split_kernel(const float* __restrict__ Q, const float* __restrict__ K, con
             for (int m = 0; m < DCH / KQ; ++m) O[(row0 + ob_t0 + kq + KQ * m) * kVD + col] = ob[m];
             ob_t0 = -1;
         }
-        if (PIPE && t0 + DCH < kT) fetch(t0 + DCH);
+        if (PIPE && t0 + DCH < TT) fetch(t0 + DCH);
         // all lane groups of a column hold the same o; in the rolled form every lane stores it (same value, same
         // address), so the token step has no branch
         if (PIPE && nt == DCH) {
@@ -579,18 +599,19 @@ __device__ __forceinline__ void chunk_decays(float ai, float (*Gs)[DC + 1], floa
 // of K K^T and by B1), L, T and the decay products live in LDS (22 KB: seven waves per CU); Q fragments and the V
 // columns of A1V are read straight from global memory, issued early so that they land during the products and the
 // forward substitution.
-template <typename T>
+template <typename T, int TT>
 __global__ void __launch_bounds__(64)
 delta_chunk_prep_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
                         const float* __restrict__ dec, const float* __restrict__ beta, float* __restrict__ CH) {
+    constexpr int NC = (TT + DC - 1) / DC;   // chunks per window
     typedef Split<T> S;
     typedef typename S::V8 V8;
     constexpr int P = S::P;
-    const int c = blockIdx.x % DNC, wh = blockIdx.x / DNC;
+    const int c = blockIdx.x % NC, wh = blockIdx.x / NC;
     const int b = wh / kHeads, h = wh % kHeads;
     const int lane = threadIdx.x, r = lane & 15, g = lane >> 4;
-    const int t0 = c * DC, n = min(DC, kT - t0);
-    const long long row0 = (long long)b * kT + t0;
+    const int t0 = c * DC, n = min(DC, TT - t0);
+    const long long row0 = (long long)b * TT + t0;
     __shared__ __attribute__((aligned(16))) float Ks[DC][64 + 4];
     __shared__ __attribute__((aligned(16))) float Ls[DC][DC + 4];
     __shared__ __attribute__((aligned(16))) float Ts[DC][DC + 4];
@@ -630,7 +651,7 @@ delta_chunk_prep_kernel(const float* __restrict__ Q, const float* __restrict__ K
     __syncthreads();
     // L = b_i G_ij (k_i . k_j) for j < i and P = G_ij (q_i . k_j) for j <= i: tiles (ti, tj) of K K^T and Q K^T,
     // keys in two K steps; tile (0, 1) of both is all zero
-    float* out = CH + ((long long)wh * DNC + c) * DCF;
+    float* out = CH + ((long long)wh * NC + c) * DCF;
 #pragma unroll
     for (int tile = 0; tile < 4; ++tile) {
         const int ti = tile >> 1, tj = tile & 1;
@@ -728,10 +749,11 @@ struct DChunkRegs {   // one chunk's operands as a thread loads them
     float4 q[2], k[2], b1[2], p;
     float gd[2], g, a1v[UT][4];
 };
-template <typename T, int VS>
+template <typename T, int VS, int TT>
 __global__ void __launch_bounds__(256)
 delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ CH,
                         float* __restrict__ O) {
+    constexpr int NC = (TT + DC - 1) / DC;   // chunks per window
     typedef Split<T> S;
     typedef typename S::V8 V8;
     constexpr int P = S::P;
@@ -748,13 +770,13 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
     const int vb = blockIdx.x % NB, wh = blockIdx.x / NB, b = wh / kHeads, h = wh % kHeads;
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const long long rowb = (long long)b * kT;
+    const long long rowb = (long long)b * TT;
     const int vcol0 = h * 128 + vb * VS;   // first value column of this block in the [rows][768] layout
-    const float* chb = CH + (long long)wh * DNC * DCF;
+    const float* chb = CH + (long long)wh * NC * DCF;
     for (int i = tid; i < P * VS * KL; i += 256) (&Sp[0][0][0])[i] = T(0.0f);
 
     auto fetch = [&](DChunkRegs<UT>& F, int c) {   // loads at clamped rows; rows past the end are zeroed when staged
-        const int t0 = c * DC, n = min(DC, kT - t0);
+        const int t0 = c * DC, n = min(DC, TT - t0);
         const float* cc = chb + (long long)c * DCF;
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -787,12 +809,12 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int i = ob_t0 + ti * 16 + 4 * g + e;
-                if (i < kT) O[(rowb + i) * kVD + vcol0 + vt * 16 + r] = ob[j][e];
+                if (i < TT) O[(rowb + i) * kVD + vcol0 + vt * 16 + r] = ob[j][e];
             }
         }
     };
     auto chunk = [&](int c, DChunkRegs<UT>& F) {
-        const int t0 = c * DC, n = min(DC, kT - t0);
+        const int t0 = c * DC, n = min(DC, TT - t0);
         __syncthreads();   // the previous chunk is done with every LDS operand
         // ---- stage: q, -B1, P, Kd^T parts and g
         float av[UT][4];
@@ -824,7 +846,7 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
             store_out();
             ob_t0 = -1;
         }
-        if (c + 2 < DNC) fetch(F, c + 2);
+        if (c + 2 < NC) fetch(F, c + 2);
         __syncthreads();
         // ---- phase 1: U = A1V - B1 S_0 and Q S_0
         f32x4 qs[UT];
@@ -879,16 +901,17 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
     DChunkRegs<UT> F0, F1;
     fetch(F0, 0);
     fetch(F1, 1);
-    for (int c = 0; c < DNC; c += 2) {
+    for (int c = 0; c < NC; c += 2) {
         chunk(c, F0);
-        if (c + 1 < DNC) chunk(c + 1, F1);
+        if (c + 1 < NC) chunk(c + 1, F1);
     }
     store_out();
 }
 
 // ------------------------------------------------------------------------------------------------ gated norm
-// 16 lanes per (row, head): lane l accumulates o[l + 16 z]^2 (z = 0..7), tree16, then ((o * rstd) * w) * silu(g)
-template <typename T>
+// 16 lanes per (row, head): lane l accumulates o[l + 16 z]^2 (z = 0..7), tree16, then ((o * rstd) * w) * silu(g).
+// AUDIO: SHIELD-A scales o by 0.125 first and uses eps 1e-5 (engine/audio/sequence.cpp:196-201).
+template <typename T, bool AUDIO>
 __global__ void __launch_bounds__(256)
 gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, const float* __restrict__ w,
                   T* __restrict__ out, long long pstride, int rows) {
@@ -900,13 +923,13 @@ gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, cons
     const float* o = O + row * kVD + h * 128;
     float v[8];
 #pragma unroll
-    for (int z = 0; z < 8; ++z) v[z] = o[z * 16 + l];
+    for (int z = 0; z < 8; ++z) v[z] = AUDIO ? o[z * 16 + l] * 0.125f : o[z * 16 + l];
     float acc = v[0] * v[0];
 #pragma unroll
     for (int z = 1; z < 8; ++z) acc = __builtin_fmaf(v[z], v[z], acc);
     const float s = tree16(acc);
     if (!live) return;
-    const float rstd = 1.0f / sqrtf(s / 128.0f + 1e-6f);
+    const float rstd = 1.0f / sqrtf(s / 128.0f + (AUDIO ? 1e-5f : 1e-6f));
     const float* g = P + row * kGld + kGg + h * 128;
 #pragma unroll
     for (int z = 0; z < 8; ++z) {
@@ -922,16 +945,17 @@ gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, cons
 // 3. rotate c (last token's angles) and each b_t; scores with the 16-lane dot structure
 // 4. softmax: max, expf, sum in double in token order (one thread); y_j = sum over 64-token blocks of fma chains
 constexpr int SA_THREADS = 256;
+template <int TT>
 __global__ void __launch_bounds__(SA_THREADS)
 sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __restrict__ lam_h,
             float* __restrict__ Y) {
     const int b = blockIdx.x / kHeads, h = blockIdx.x % kHeads, tid = threadIdx.x;
-    float* S0 = S + (long long)b * kT * kSld;
-    __shared__ float gt[kT], ft[kT], sco[kT];
-    __shared__ float phi[kT][kPairs + 1];
+    float* S0 = S + (long long)b * TT * kSld;
+    __shared__ float gt[TT], ft[TT], sco[TT];
+    __shared__ float phi[TT][kPairs + 1];
     __shared__ float sq[64], crot[32];
     __shared__ float s_inv;
-    for (int t = tid; t < kT; t += SA_THREADS) {
+    for (int t = tid; t < TT; t += SA_THREADS) {
         const float* row = S0 + (long long)t * kSld;
         gt[t] = -softplus_f(row[kSal + h]);
         ft[t] = logsigmoid_f(row[kSfg + h]);
@@ -943,7 +967,7 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
     if (tid < 2 + kPairs) {
         double acc = 0.0;
         float* series = tid == 0 ? gt : tid == 1 ? ft : nullptr;
-        for (int t = 0; t < kT; ++t) {
+        for (int t = 0; t < TT; ++t) {
             if (series) {
                 acc += double(series[t]);
                 series[t] = float(acc);
@@ -956,15 +980,15 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
     __syncthreads();
     if (tid < kPairs) {
         float sn, cs;
-        sincosf(phi[kT - 1][tid], &sn, &cs);
+        sincosf(phi[TT - 1][tid], &sn, &cs);
         const float* c = QC + (long long)b * 576 + 384 + h * 32;
         const float ce = c[2 * tid], co = c[2 * tid + 1];
         crot[2 * tid] = ce * cs - co * sn;
         crot[2 * tid + 1] = ce * sn + co * cs;
     }
     __syncthreads();
-    const float lam = lam_h[h], gl = gt[kT - 1], fl = ft[kT - 1];
-    for (int t = tid; t < kT; t += SA_THREADS) {
+    const float lam = lam_h[h], gl = gt[TT - 1], fl = ft[TT - 1];
+    for (int t = tid; t < TT; t += SA_THREADS) {
         const float* row = S0 + (long long)t * kSld;
         const float* k = row + kSk + h * 64;
         const float* bb = row + kSb + h * 32;
@@ -1000,9 +1024,9 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
     __syncthreads();
     if (tid == 0) {
         float mx = -INFINITY;
-        for (int t = 0; t < kT; ++t) mx = sco[t] > mx ? sco[t] : mx;
+        for (int t = 0; t < TT; ++t) mx = sco[t] > mx ? sco[t] : mx;
         double sum = 0.0;
-        for (int t = 0; t < kT; ++t) {
+        for (int t = 0; t < TT; ++t) {
             const float e = expf(sco[t] - mx);
             sco[t] = e;
             sum += double(e);
@@ -1013,9 +1037,9 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
     if (tid < 64) {
         const float inv = s_inv;
         float tot = 0.0f;
-        for (int t0 = 0; t0 < kT; t0 += 64) {
+        for (int t0 = 0; t0 < TT; t0 += 64) {
             float blk = 0.0f;
-            const int t1 = min(kT, t0 + 64);
+            const int t1 = min(TT, t0 + 64);
             for (int t = t0; t < t1; ++t)
                 blk = __builtin_fmaf(sco[t] * inv, S0[(long long)t * kSld + kSv + h * 64 + tid], blk);
             tot = t0 == 0 ? blk : tot + blk;
@@ -1025,8 +1049,9 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
 }
 
 // ------------------------------------------------------------------------------------------------ head
-// final RMSNorm (16-lane tree), Linear(384,128) as K blocks of 64 (one thread per output), SiLU, then the
-// 128-long dot with the 16-lane structure + bias.  w0 row-major [128][384].
+// final RMSNorm (16-lane tree), Linear(384,128) as K blocks of 64 (one thread per output), SiLU (AUDIO: GELU), then
+// the 128-long dot with the 16-lane structure + bias.  w0 row-major [128][384].
+template <bool AUDIO>
 __global__ void __launch_bounds__(128)
 head_kernel(const float* __restrict__ X, const float* __restrict__ nw, const float* __restrict__ w0,
             const float* __restrict__ b0, const float* __restrict__ w2, float b2, float* __restrict__ logits) {
@@ -1050,7 +1075,9 @@ head_kernel(const float* __restrict__ X, const float* __restrict__ nw, const flo
             for (int k = k0; k < k0 + 64; ++k) blk = __builtin_fmaf(xn[k], wr[k], blk);
             tot = k0 == 0 ? blk : tot + blk;
         }
-        hid[tid] = silu(tot + b0[tid]);
+        const float z = tot + b0[tid];
+        // SHIELD-A: exact GELU 0.5 z (1 + erf(z / sqrt 2)) (engine/audio/sequence.cpp:333-334); SHIELD-V: SiLU
+        hid[tid] = AUDIO ? 0.5f * z * (1.0f + erff(z * 0.7071067811865475244f)) : silu(z);
     }
     __syncthreads();
     if (tid < 16) {
@@ -1076,64 +1103,106 @@ void launch_assemble(const float* const* tok_ptrs, const float* pos, const float
                      hipStream_t s) {
     hipLaunchKernelGGL(assemble_kernel, dim3(B * kT), dim3(96), 0, s, tok_ptrs, pos, readout, h);
 }
+void launch_assemble_audio(const float* tokens, long long ldw, const float* readout, float* h, int B, hipStream_t s) {
+    if ((reinterpret_cast<uintptr_t>(tokens) & 15) || (reinterpret_cast<uintptr_t>(readout) & 15) || ldw % 4 ||
+        ldw < (long long)(kTAudio - 1) * kD)
+        throw std::runtime_error("assemble: audio tokens need 16-byte alignment and a window stride >= 48000 floats");
+    hipLaunchKernelGGL(assemble_audio_kernel, dim3(B * kTAudio), dim3(96), 0, s, tokens, ldw, readout, h);
+}
 template <typename T>
 void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s,
                     long long pstride) {
     hipLaunchKernelGGL(rmsnorm_kernel<T>, dim3(cdiv((long long)rows * 16, 256)), dim3(256), 0, s, x, ldx, w, out, ldo,
                        pstride, rows);
 }
+// The kernels are instantiated for SHIELD-V's windows (321 tokens) and SHIELD-A's (126): f(integral_constant<TT>).
+template <class F> void for_window(int T, F&& f) {
+    if (T == kT) f(std::integral_constant<int, kT>());
+    else if (T == kTAudio) f(std::integral_constant<int, kTAudio>());
+    else throw std::runtime_error("sequence kernels: unsupported window length " + std::to_string(T));
+}
+
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
                      const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
-                     hipStream_t s) {
-    hipLaunchKernelGGL(gdn_prep_kernel, dim3(B * ((kT + GP_T - 1) / GP_T)), dim3(384), 0, s, P, conv_w, conv_b, neg_rate,
-                       dt_bias, Q, K, V, dec, beta);
+                     hipStream_t s, int T, bool audio) {
+    for_window(T, [&](auto tt) {
+        constexpr int TT = decltype(tt)::value;
+        const dim3 grid(B * ((TT + GP_T - 1) / GP_T));
+        if (audio)
+            hipLaunchKernelGGL((gdn_prep_kernel<TT, true>), grid, dim3(384), 0, s, P, conv_w, conv_b, neg_rate, dt_bias,
+                               Q, K, V, dec, beta);
+        else
+            hipLaunchKernelGGL((gdn_prep_kernel<TT, false>), grid, dim3(384), 0, s, P, conv_w, conv_b, neg_rate,
+                               dt_bias, Q, K, V, dec, beta);
+    });
 }
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
-                  int B, bool exact, hipStream_t s) {
-    if (exact)
-        hipLaunchKernelGGL(delta_kernel, dim3(B * kHeads * 2), dim3(DCOLS), 0, s, Q, K, V, dec, beta, O);
-    else {
+                  int B, bool exact, hipStream_t s, int T) {
+    for_window(T, [&](auto tt) {
+        constexpr int TT = decltype(tt)::value;
+        if (exact) {
+            hipLaunchKernelGGL((delta_kernel<TT>), dim3(B * kHeads * 2), dim3(DCOLS), 0, s, Q, K, V, dec, beta, O);
+            return;
+        }
         // the split follows the batch (results are bitwise the same for every split): the most lane groups per
         // column that still fit one wave per SIMD; KQ = 2 past that
         if (B * kHeads * 16 <= kDeltaPipeWaves)
-            hipLaunchKernelGGL((delta_split_kernel<8, true>), dim3(B * kHeads * 16), dim3(64), 0, s, Q, K, V, dec, beta, O);
+            hipLaunchKernelGGL((delta_split_kernel<8, true, TT>), dim3(B * kHeads * 16), dim3(64), 0, s, Q, K, V, dec,
+                               beta, O);
         else if (B * kHeads * 8 <= kDeltaPipeWaves)
-            hipLaunchKernelGGL((delta_split_kernel<4, true>), dim3(B * kHeads * 8), dim3(64), 0, s, Q, K, V, dec, beta, O);
+            hipLaunchKernelGGL((delta_split_kernel<4, true, TT>), dim3(B * kHeads * 8), dim3(64), 0, s, Q, K, V, dec,
+                               beta, O);
         else if (B * kHeads * 4 <= kDeltaPipeWaves)
-            hipLaunchKernelGGL((delta_split_kernel<2, true>), dim3(B * kHeads * 4), dim3(64), 0, s, Q, K, V, dec, beta, O);
+            hipLaunchKernelGGL((delta_split_kernel<2, true, TT>), dim3(B * kHeads * 4), dim3(64), 0, s, Q, K, V, dec,
+                               beta, O);
         else
-            hipLaunchKernelGGL((delta_split_kernel<2, false>), dim3(B * kHeads * 4), dim3(64), 0, s, Q, K, V, dec, beta, O);
-    }
+            hipLaunchKernelGGL((delta_split_kernel<2, false, TT>), dim3(B * kHeads * 4), dim3(64), 0, s, Q, K, V, dec,
+                               beta, O);
+    });
 }
-size_t delta_chunk_floats(int B) { return size_t(B) * kHeads * DNC * DCF; }
+size_t delta_chunk_floats(int B, int T) { return size_t(B) * kHeads * size_t((T + DC - 1) / DC) * DCF; }
 template <typename T>
 void launch_delta_chunked(const float* Q, const float* K, const float* V, const float* dec, const float* beta,
-                          float* O, float* work, int B, hipStream_t s) {
+                          float* O, float* work, int B, hipStream_t s, int Tw) {
     if (!work) throw std::runtime_error("delta: the chunked scan needs its work buffer");
-    hipLaunchKernelGGL(delta_chunk_prep_kernel<T>, dim3(B * kHeads * DNC), dim3(64), 0, s, Q, K, V, dec, beta, work);
-    // value blocks per head by batch (bitwise the same results for every split): small batches spread a head's
-    // state over more workgroups
-    if (B <= 16)
-        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 32>), dim3(B * kHeads * 4), dim3(256), 0, s, Q, K, work, O);
-    else
-        hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 64>), dim3(B * kHeads * 2), dim3(256), 0, s, Q, K, work, O);
+    for_window(Tw, [&](auto tt) {
+        constexpr int TT = decltype(tt)::value;
+        constexpr int NC = (TT + DC - 1) / DC;
+        hipLaunchKernelGGL((delta_chunk_prep_kernel<T, TT>), dim3(B * kHeads * NC), dim3(64), 0, s, Q, K, V, dec, beta,
+                           work);
+        // value blocks per head by batch (bitwise the same results for every split): small batches spread a
+        // head's state over more workgroups
+        if (B <= 16)
+            hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 32, TT>), dim3(B * kHeads * 4), dim3(256), 0, s, Q, K, work,
+                               O);
+        else
+            hipLaunchKernelGGL((delta_chunk_scan_kernel<T, 64, TT>), dim3(B * kHeads * 2), dim3(256), 0, s, Q, K, work,
+                               O);
+    });
 }
 template void launch_delta_chunked<f16>(const float*, const float*, const float*, const float*, const float*, float*,
-                                        float*, int, hipStream_t);
+                                        float*, int, hipStream_t, int);
 template void launch_delta_chunked<bf16>(const float*, const float*, const float*, const float*, const float*,
-                                         float*, float*, int, hipStream_t);
+                                         float*, float*, int, hipStream_t, int);
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,
-                       long long pstride) {
-    hipLaunchKernelGGL(gated_norm_kernel<T>, dim3(cdiv((long long)rows * kHeads * 16, 256)), dim3(256), 0, s, O, P, w,
-                       out, pstride, rows);
+                       long long pstride, bool audio) {
+    const dim3 grid(cdiv((long long)rows * kHeads * 16, 256));
+    if (audio)
+        hipLaunchKernelGGL((gated_norm_kernel<T, true>), grid, dim3(256), 0, s, O, P, w, out, pstride, rows);
+    else
+        hipLaunchKernelGGL((gated_norm_kernel<T, false>), grid, dim3(256), 0, s, O, P, w, out, pstride, rows);
 }
-void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s) {
-    hipLaunchKernelGGL(sisa_kernel, dim3(B * kHeads), dim3(SA_THREADS), 0, s, S, QC, lam, Y);
+void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s, int T) {
+    for_window(T, [&](auto tt) {
+        constexpr int TT = decltype(tt)::value;
+        hipLaunchKernelGGL((sisa_kernel<TT>), dim3(B * kHeads), dim3(SA_THREADS), 0, s, S, QC, lam, Y);
+    });
 }
 void launch_head(const float* X, const float* norm_w, const float* w0, const float* b0, const float* w2, float b2,
-                 float* logits, int B, hipStream_t s) {
-    hipLaunchKernelGGL(head_kernel, dim3(B), dim3(128), 0, s, X, norm_w, w0, b0, w2, b2, logits);
+                 float* logits, int B, hipStream_t s, bool audio) {
+    if (audio) hipLaunchKernelGGL((head_kernel<true>), dim3(B), dim3(128), 0, s, X, norm_w, w0, b0, w2, b2, logits);
+    else hipLaunchKernelGGL((head_kernel<false>), dim3(B), dim3(128), 0, s, X, norm_w, w0, b0, w2, b2, logits);
 }
 void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool, int F, hipStream_t s) {
     hipLaunchKernelGGL(store_tokens_kernel, dim3(F), dim3(256), 0, s, tokens, slots, pool);
@@ -1173,7 +1242,7 @@ float* scratch_on_current_device() {
 void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const float* V, const float* dec,
                             const float* beta, int n_windows, float* O, int variant, hipStream_t s) {
     if (!delta_rule_is_chunked(p, Q, K, V, dec, beta, n_windows, O, variant)) {
-        launch_delta(Q, K, V, dec, beta, O, n_windows, p == Precision::FP32, s);
+        launch_delta(Q, K, V, dec, beta, O, n_windows, p == Precision::FP32, s, kT);
         SHV_HIP_CHECK(hipGetLastError());
         return;
     }
@@ -1181,15 +1250,16 @@ void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const f
         throw std::runtime_error("delta rule (no allocation): " + std::to_string(n_windows) +
                                  " windows exceed the static work area of " + std::to_string(kDeltaNoAllocWindows));
     float* work = scratch_on_current_device();
-    if (p == Precision::BF16) launch_delta_chunked<bf16>(Q, K, V, dec, beta, O, work, n_windows, s);
-    else launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s);
+    if (p == Precision::BF16) launch_delta_chunked<bf16>(Q, K, V, dec, beta, O, work, n_windows, s, kT);
+    else launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s, kT);
     SHV_HIP_CHECK(hipGetLastError());
 }
 
 #define SHV_NORMS(T)                                                                                             \
     template void launch_rmsnorm<T>(const float*, long long, const float*, T*, long long, int, hipStream_t,      \
                                     long long);                                                                  \
-    template void launch_gated_norm<T>(const float*, const float*, const float*, T*, int, hipStream_t, long long);
+    template void launch_gated_norm<T>(const float*, const float*, const float*, T*, int, hipStream_t, long long,  \
+                                       bool);
 SHV_NORMS(float)
 SHV_NORMS(f16)
 SHV_NORMS(bf16)

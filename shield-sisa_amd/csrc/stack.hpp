@@ -1,0 +1,387 @@
+// Device-side pieces shared by the SHIELD-V engine and the SHIELD-A sequence engine: device memory, weight upload
+// and GPU repacking, the GEMM dispatcher with its profiling families, debug dumps, and SeqStack -- the sequence
+// stages both models run (GDN-A, GDN-B twice, SISA on the last row, head) on one set of kernels.  Included by the
+// HIP sources only.
+#pragma once
+#include "engine.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+namespace shv {
+
+inline void check_launch() { SHV_HIP_CHECK(hipGetLastError()); }
+
+// G selects how GEMM operands reach the multipliers: float = exact-order VALU, f16 / bf16 = split-operand MFMA
+template <typename G> inline void gemm_t(const GemmArgs& p, hipStream_t s);
+template <> inline void gemm_t<float>(const GemmArgs& p, hipStream_t s) { gemm_f32(p, s); }
+template <> inline void gemm_t<f16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<f16>(p, s); }
+template <> inline void gemm_t<bf16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<bf16>(p, s); }
+
+inline double gemm_bytes(long long M, int N, int K, int ta, int tw, int tc, int tr) {
+    return double(M) * K * ta + double(N) * K * tw + double(M) * N * tc + (tr ? double(M) * N * tr : 0.0);
+}
+
+// a GEMM weight on the device: `parts` arrays of N*K elements of the flavour's type, `stride` elements apart
+struct DevW {
+    const void* w = nullptr;
+    long long stride = 0;
+};
+
+// owner of device allocations
+class DevMem {
+public:
+    DevMem() = default;
+    DevMem(const DevMem&) = delete;
+    DevMem& operator=(const DevMem&) = delete;
+    ~DevMem() { release(); }
+    void release() {
+        for (void* p : ptrs_) (void)hipFree(p);
+        ptrs_.clear();
+        bytes_ = 0;
+    }
+    template <class U> U* make(size_t n) {
+        void* p = nullptr;
+        const size_t bytes = std::max<size_t>(n * sizeof(U), 256);
+        SHV_HIP_CHECK(hipMalloc(&p, bytes));
+        ptrs_.push_back(p);
+        bytes_ += bytes;
+        return static_cast<U*>(p);
+    }
+    size_t bytes() const { return bytes_; }
+
+private:
+    std::vector<void*> ptrs_;
+    size_t bytes_ = 0;
+};
+
+// Weight upload at load time: fp32 arrays copied to `wmem`, GEMM operands converted on the GPU (repack kernels on
+// `s`) from fp32 copies in `staging`, which finish() frees.
+class Uploader {
+public:
+    Uploader(DevMem& wmem, hipStream_t s) : wmem_(wmem), s_(s) {}
+    const float* up(const float* src, size_t n) {
+        float* d = wmem_.make<float>(n);
+        SHV_HIP_CHECK(hipMemcpy(d, src, n * sizeof(float), hipMemcpyHostToDevice));
+        return d;
+    }
+    const float* up(const std::vector<float>& v) { return up(v.data(), v.size()); }
+    // fp32 [N][K] rows -> device parts of U with a row permutation, converted by the repack kernel on the GPU
+    template <typename U> DevW repack(const std::vector<float>& src, int N, int K, int perm) {
+        const int parts = weight_parts<U>();
+        float* st = staging_.make<float>(src.size());
+        SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
+        U* d = wmem_.make<U>(size_t(parts) * N * K);
+        launch_repack<U>(st, d, N, K, perm, parts, s_);
+        check_launch();
+        return DevW{d, (long long)N * K};
+    }
+    template <typename U> DevW repack_pad(const std::vector<float>& src, int N, int K, int Np, int Kp) {
+        const int parts = weight_parts<U>();
+        float* st = staging_.make<float>(src.size());
+        SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
+        U* d = wmem_.make<U>(size_t(parts) * Np * Kp);
+        launch_repack_pad<U>(st, d, N, K, Np, Kp, parts, s_);
+        check_launch();
+        return DevW{d, (long long)Np * Kp};
+    }
+    // [rows][n] -> [rows][np], zero padded
+    const float* up_pad(const std::vector<float>& v, int rows, int n, int np) {
+        std::vector<float> o(size_t(rows) * np, 0.0f);
+        for (int r = 0; r < rows; ++r)
+            for (int j = 0; j < n; ++j) o[size_t(r) * np + j] = v[size_t(r) * n + j];
+        return up(o);
+    }
+    void finish() {
+        SHV_HIP_CHECK(hipStreamSynchronize(s_));
+        staging_.release();
+    }
+    static std::vector<float> concat(const Linear& a, const Linear& b) {
+        std::vector<float> v(a.w);
+        v.insert(v.end(), b.w.begin(), b.w.end());
+        return v;
+    }
+
+private:
+    DevMem& wmem_;
+    DevMem staging_;
+    hipStream_t s_;
+};
+
+// Debug dump of window 0 / frame 0 (synchronises s): `n` values of `dev` as fp32 to "<dir>/<name>.f32"
+template <typename U> void dump_f32(const std::string& dir, const char* name, const U* dev, size_t n, hipStream_t s) {
+    if (dir.empty()) return;
+    SHV_HIP_CHECK(hipStreamSynchronize(s));
+    std::vector<U> h(n);
+    SHV_HIP_CHECK(hipMemcpy(h.data(), dev, n * sizeof(U), hipMemcpyDeviceToHost));
+    std::vector<float> f(n);
+    for (size_t i = 0; i < n; ++i) f[i] = float(h[i]);
+    std::ofstream o(dir + "/" + name + ".f32", std::ios::binary);
+    o.write(reinterpret_cast<const char*>(f.data()), std::streamsize(n * sizeof(float)));
+}
+
+// GEMM launches of one engine flavour G, timed under "<role>:<kernel template>" when profiling
+template <typename G> struct GemmRunner {
+    static constexpr bool kF32 = std::is_same<G, float>::value;
+    Profiler& pf;
+    std::string family(const char* role, const GemmArgs& p, bool f32) const {
+        if (!pf.profiling()) return std::string();
+        if constexpr (!kF32) {
+            if (!f32) return std::string(role) + ":" + gemm_mfma_kernel<G>(p);
+        }
+        return std::string(role) + ":" + gemm_f32_kernel(p);
+    }
+    // in this flavour's arithmetic; A is read pre-split where the producer wrote parts, else as fp32
+    void gemm(const char* role, GemmArgs p, const DevW& w, hipStream_t s) const {
+        p.W = w.w;
+        p.wstride = w.stride;
+        const int abytes = (p.Ah && !kF32) ? int(sizeof(G)) * weight_parts<G>() : 4;
+        const double bytes = gemm_bytes(p.M, p.N, p.K, abytes, kF32 ? 4 : int(sizeof(G)) * weight_parts<G>(),
+                                        p.swiglu ? (p.Ch ? int(sizeof(G)) * weight_parts<G>() / 2 : 2) : 4,
+                                        p.res ? 4 : 0);
+        pf.timed(family(role, p, false), bytes, s, [&] { gemm_t<G>(p, s); }, 2.0 * p.M * p.N * p.K);
+        check_launch();
+    }
+    // the exact fp32 VALU kernel (layers kept in fp32 in every tier)
+    void gemm32(const char* role, const GemmArgs& p, hipStream_t s) const {
+        pf.timed(family(role, p, true), gemm_bytes(p.M, p.N, p.K, 4, 4, p.swiglu ? 2 : 4, p.res ? 4 : 0), s,
+                 [&] { gemm_f32(p, s); }, 2.0 * p.M * p.N * p.K);
+        check_launch();
+    }
+};
+
+// How one model runs the shared sequence stages.
+struct SeqSpec {
+    int T;               // tokens per window, readout last: 321 (SHIELD-V) or 126 (SHIELD-A)
+    bool audio;          // SHIELD-A arithmetic in the GDN prep, gated norm and head kernels
+    int gdn_b_res;       // GEMM residual mode of GDN-B's mixer passes: 2 R + v / sqrt(2), 3 R + 0.70710678 v
+    const char* dump[5]; // dump names: input, after GDN-A, after GDN-B, SISA last row, logit
+};
+
+// The sequence stages on the device: weights, activations for max_windows windows, and the forward from the
+// assembled residual stream h() [B*T][384] to one logit per window.  Activations are fp32 in HBM in every tier;
+// G picks the GEMM arithmetic (float: exact VALU order; f16 / bf16: split-operand MFMA with the GEMM A operands
+// written pre-split by their producers).
+template <typename G> class SeqStack {
+    static constexpr bool kF32 = std::is_same<G, float>::value;
+    static constexpr int kAS = kF32 ? 4 : int(sizeof(G)) * weight_parts<G>();   // bytes per A value
+
+public:
+    SeqStack(const SeqSpec& spec, const GdnHost (&gdn)[2], const SisaHost& S, const std::vector<float>& final_norm_w,
+             const Linear& head0, const std::vector<float>& head2_w, float head2_b, int max_windows, Uploader& up,
+             DevMem& amem)
+        : spec_(spec) {
+        const int swiglu_perm = kF32 ? 1 : 2;
+        for (int g = 0; g < 2; ++g) {
+            const GdnHost& gh = gdn[g];
+            Gdn& d = gdn_[g];
+            d.norm_w = up.up(gh.norm_w);
+            d.ffn_norm_w = up.up(gh.ffn_norm_w);
+            d.conv_w = up.up(gh.conv_w);
+            d.conv_b = up.up(gh.conv_b);
+            d.neg_rate = up.up(gh.neg_rate, kHeads);
+            d.dt_bias = up.up(gh.dt_bias, kHeads);
+            d.o_norm_w = up.up(gh.o_norm_w);
+            d.in_w = up.repack<G>(gh.in.w, gh.in.N, gh.in.K, 0);
+            d.out_w = up.repack<G>(gh.out.w, gh.out.N, gh.out.K, 0);
+            d.up_w = up.repack<G>(Uploader::concat(gh.gate, gh.up), 2 * kFF, kD, swiglu_perm);
+            d.down_w = up.repack<G>(gh.down.w, gh.down.N, gh.down.K, 0);
+        }
+        s_attn_norm_ = up.up(S.attn_norm_w);
+        s_ffn_norm_ = up.up(S.ffn_norm_w);
+        s_in_w_ = up.repack<G>(S.in.w, S.in.N, S.in.K, 0);
+        s_in_b_ = up.up(S.in.b);
+        s_qc_w_ = up.up(Uploader::concat(S.q, S.c));   // [576][384]: W_Q rows then W_C rows
+        s_o_w_ = up.up(S.o.w);
+        s_up_w_ = static_cast<const float*>(up.repack<float>(Uploader::concat(S.gate, S.up), 2 * kFF, kD, 1).w);
+        s_down_w_ = up.up(S.down.w);
+        s_lam_ = up.up(S.lam, kHeads);
+        fn_w_ = up.up(final_norm_w);
+        h_w0_ = up.up(head0.w);
+        h_b0_ = up.up(head0.b);
+        h_w2_ = up.up(head2_w);
+        h_b2_ = head2_b;
+
+        const size_t Bm = size_t(max_windows), Mm = Bm * size_t(spec_.T);
+        H_ = amem.make<float>(Mm * kD);
+        P_ = amem.make<float>(Mm * kGld);
+        Q_ = amem.make<float>(Mm * kD);
+        K_ = amem.make<float>(Mm * kD);
+        V_ = amem.make<float>(Mm * kVD);
+        dec_ = amem.make<float>(Mm * 8);
+        beta_ = amem.make<float>(Mm * 8);
+        O_ = amem.make<float>(Mm * kVD);
+        // half tiers: the chunked delta-rule scan (SHV_HIP_DELTA_SEQ=1 keeps the token-by-token kernel, for A/B runs)
+        const char* ds = std::getenv("SHV_HIP_DELTA_SEQ");
+        delta_chunked_ = !kF32 && !(ds && *ds && std::strcmp(ds, "0") != 0);
+        if (delta_chunked_) dwork_ = amem.make<float>(delta_chunk_floats(int(Bm), spec_.T));
+        mrows_ = (long long)Mm;
+        if constexpr (kF32) {
+            XN_ = amem.make<float>(Mm * kD);
+            ON_ = amem.make<float>(Mm * kVD);
+            HID_ = amem.make<float>(Mm * kFF);
+        } else {
+            XNh_ = amem.make<G>(weight_parts<G>() * Mm * kD);
+            ONh_ = amem.make<G>(weight_parts<G>() * Mm * kVD);
+            HIDh_ = amem.make<G>(weight_parts<G>() * Mm * kFF);
+        }
+        XL_ = amem.make<float>(Bm * kD);
+        QC_ = amem.make<float>(Bm * 576);
+        Y_ = amem.make<float>(Bm * kD);
+        X1_ = amem.make<float>(Bm * kD);
+        X2_ = amem.make<float>(Bm * kD);
+        HIDL_ = amem.make<float>(Bm * kFF);
+    }
+
+    // the residual stream [max_windows * T][384] the caller assembles before run()
+    float* h() const { return H_; }
+
+    // h() of B windows -> logits[B]
+    void run(int B, float* logits, hipStream_t s, Profiler& pf, const std::string& dump_dir) {
+        const int T = spec_.T, M = B * T;
+        const GemmRunner<G> gr{pf};
+        dump_f32(dump_dir, spec_.dump[0], H_, size_t(T) * kD, s);
+        for (int st = 0; st < 2; ++st) {
+            const Gdn& gd = gdn_[st];
+            const int reps = st == 0 ? 1 : 2;
+            for (int r = 0; r < reps; ++r) {
+                rmsnorm_all(pf, gd.norm_w, s, M);
+                GemmArgs pi;
+                pi.M = M; pi.N = kGn; pi.K = kD;
+                set_a(pi, XN_, XNh_, kD); pi.ldw = kD;
+                pi.C = P_; pi.ldc = kGld;
+                gr.gemm("gemm_seq", pi, gd.in_w, s);
+                pf.timed("gdn_prep", double(M) * (4.0 * 1548 * 4 + 4.0 * (2 * kD + kVD + 16)), s, [&] {
+                    launch_gdn_prep(P_, gd.conv_w, gd.conv_b, gd.neg_rate, gd.dt_bias, Q_, K_, V_, dec_, beta_, B, s,
+                                    T, spec_.audio);
+                });
+                check_launch();
+                pf.timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s, [&] {
+                    if constexpr (!kF32) {
+                        if (delta_chunked_) {
+                            launch_delta_chunked<G>(Q_, K_, V_, dec_, beta_, O_, dwork_, B, s, T);
+                            return;
+                        }
+                    }
+                    launch_delta(Q_, K_, V_, dec_, beta_, O_, B, kF32, s, T);
+                }, 2.0 * B * T * kHeads * 4.0 * kDK * kDV);   // per token and head: decay, S^T k, k u^T, S^T q
+                check_launch();
+                pf.timed("gated_norm", double(M) * (4.0 * 2 * kVD + kAS * kVD), s, [&] {
+                    if constexpr (kF32) launch_gated_norm<float>(O_, P_, gd.o_norm_w, ON_, M, s, 0, spec_.audio);
+                    else launch_gated_norm<G>(O_, P_, gd.o_norm_w, ONh_, M, s, mrows_ * kVD, spec_.audio);
+                });
+                check_launch();
+                GemmArgs po;
+                po.M = M; po.N = kD; po.K = kVD;
+                set_a(po, ON_, ONh_, kVD); po.ldw = kVD;
+                po.C = H_; po.ldc = kD;
+                po.R = H_; po.ldr = kD; po.res = reps == 2 ? spec_.gdn_b_res : 1;
+                gr.gemm("gemm_seq", po, gd.out_w, s);
+            }
+            rmsnorm_all(pf, gd.ffn_norm_w, s, M);
+            GemmArgs pu;
+            pu.M = M; pu.N = 2 * kFF; pu.K = kD;
+            set_a(pu, XN_, XNh_, kD); pu.ldw = kD;
+            pu.ldc = kFF; pu.swiglu = 1;
+            if constexpr (kF32) pu.C = HID_;
+            else { pu.Ch = HIDh_; pu.cstride = mrows_ * kFF; }
+            gr.gemm("gemm_seq", pu, gd.up_w, s);
+            GemmArgs pd;
+            pd.M = M; pd.N = kD; pd.K = kFF;
+            set_a(pd, HID_, HIDh_, kFF); pd.ldw = kFF;
+            pd.C = H_; pd.ldc = kD;
+            pd.R = H_; pd.ldr = kD; pd.res = 1;
+            gr.gemm("gemm_seq", pd, gd.down_w, s);
+            dump_f32(dump_dir, spec_.dump[1 + st], H_, size_t(T) * kD, s);
+        }
+        // SISA block, last row only: all-row K/V/B/theta/alpha/forget projection, last-row Q|C in fp32
+        rmsnorm_all(pf, s_attn_norm_, s, M);
+        GemmArgs pa;
+        pa.M = M; pa.N = kSn; pa.K = kD;
+        set_a(pa, XN_, XNh_, kD); pa.ldw = kD;
+        pa.bias = s_in_b_;
+        pa.C = P_; pa.ldc = kSld;
+        gr.gemm("gemm_seq", pa, s_in_w_, s);
+        const float* hlast = H_ + size_t(T - 1) * kD;
+        const long long ldlast = (long long)T * kD;
+        pf.timed("rmsnorm", double(B) * kD * 8, s,
+                 [&] { launch_rmsnorm<float>(hlast, ldlast, s_attn_norm_, XL_, kD, B, s); });
+        check_launch();
+        GemmArgs pq;
+        pq.M = B; pq.N = 576; pq.K = kD;
+        pq.A = XL_; pq.lda = kD; pq.W = s_qc_w_; pq.ldw = kD;
+        pq.C = QC_; pq.ldc = 576;
+        gr.gemm32("gemm_f32_small", pq, s);
+        pf.timed("sisa", double(B) * T * kSn * 4, s, [&] { launch_sisa(P_, QC_, s_lam_, Y_, B, s, T); });
+        check_launch();
+        GemmArgs pw;
+        pw.M = B; pw.N = kD; pw.K = kD;
+        pw.A = Y_; pw.lda = kD; pw.W = s_o_w_; pw.ldw = kD;
+        pw.C = X1_; pw.ldc = kD;
+        pw.R = hlast; pw.ldr = ldlast; pw.res = 1;
+        gr.gemm32("gemm_f32_small", pw, s);
+        pf.timed("rmsnorm", double(B) * kD * 8, s,
+                 [&] { launch_rmsnorm<float>(X1_, kD, s_ffn_norm_, XL_, kD, B, s); });
+        check_launch();
+        GemmArgs pu;
+        pu.M = B; pu.N = 2 * kFF; pu.K = kD;
+        pu.A = XL_; pu.lda = kD; pu.W = s_up_w_; pu.ldw = kD;
+        pu.C = HIDL_; pu.ldc = kFF; pu.swiglu = 1;
+        gr.gemm32("gemm_f32_small", pu, s);
+        GemmArgs pd;
+        pd.M = B; pd.N = kD; pd.K = kFF;
+        pd.A = HIDL_; pd.lda = kFF; pd.W = s_down_w_; pd.ldw = kFF;
+        pd.C = X2_; pd.ldc = kD;
+        pd.R = X1_; pd.ldr = kD; pd.res = 1;
+        gr.gemm32("gemm_f32_small", pd, s);
+        dump_f32(dump_dir, spec_.dump[3], X2_, kD, s);
+        pf.timed("head", double(B) * kD * 4, s,
+                 [&] { launch_head(X2_, fn_w_, h_w0_, h_b0_, h_w2_, h_b2_, logits, B, s, spec_.audio); });
+        check_launch();
+        dump_f32(dump_dir, spec_.dump[4], logits, 1, s);
+    }
+
+private:
+    SeqSpec spec_;
+    struct Gdn {
+        const float *norm_w, *ffn_norm_w, *conv_w, *conv_b, *neg_rate, *dt_bias, *o_norm_w;
+        DevW in_w, out_w, up_w, down_w;   // up_w: SwiGLU gate/up interleaved, 1920 rows
+    };
+    Gdn gdn_[2]{};
+    const float *s_attn_norm_ = nullptr, *s_ffn_norm_ = nullptr, *s_in_b_ = nullptr, *s_lam_ = nullptr;
+    DevW s_in_w_;
+    const float *s_qc_w_ = nullptr, *s_o_w_ = nullptr, *s_up_w_ = nullptr, *s_down_w_ = nullptr;
+    const float *fn_w_ = nullptr, *h_w0_ = nullptr, *h_b0_ = nullptr, *h_w2_ = nullptr;
+    float h_b2_ = 0.0f;
+
+    float *H_ = nullptr, *P_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *V_ = nullptr, *dec_ = nullptr, *beta_ = nullptr,
+          *O_ = nullptr;
+    float* dwork_ = nullptr;     // half tiers: the chunked delta rule's per-chunk products
+    bool delta_chunked_ = false;
+    float *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;   // fp32 tier: the sequence GEMMs' A operands
+    G *XNh_ = nullptr, *ONh_ = nullptr, *HIDh_ = nullptr;    // MFMA tiers: the same, written pre-split by producers
+    long long mrows_ = 0;                                     // rows of those buffers (part stride = mrows_ * width)
+    float *XL_ = nullptr, *QC_ = nullptr, *Y_ = nullptr, *X1_ = nullptr, *X2_ = nullptr, *HIDL_ = nullptr;
+
+    // the A operand of a sequence GEMM: fp32 (exact tier) or the producer's split parts (MFMA tiers)
+    void set_a(GemmArgs& p, const float* a32, const G* ah, int width) const {
+        p.lda = width;
+        if constexpr (kF32) p.A = a32;
+        else { p.Ah = ah; p.astride = mrows_ * width; }
+    }
+    void rmsnorm_all(Profiler& pf, const float* w, hipStream_t s, int M) {
+        pf.timed("rmsnorm", double(M) * kD * (4 + kAS), s, [&] {
+            if constexpr (kF32) launch_rmsnorm<float>(H_, kD, w, XN_, kD, M, s);
+            else launch_rmsnorm<G>(H_, kD, w, XNh_, kD, M, s, mrows_ * kD);
+        });
+        check_launch();
+    }
+};
+
+}  // namespace shv

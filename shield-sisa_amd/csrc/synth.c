@@ -1,4 +1,5 @@
-/* Seeded synthetic SHIELD-V inputs: a SHLDV001 weight file (+ "<file>.json" sidecar) and uint8 crops.
+/* Seeded synthetic inputs: SHIELD-V SHLDV001 weights (+ "<file>.json" sidecar), uint8 crops, and the sequence-stage
+ * weights of the SHIELD-A audio model (SHLDA001, engine/audio/weights.cpp container).
  *
  * The real checkpoint is not available offline, so every test and benchmark runs on weights drawn here from a
  * seed.  Only IEEE add/mul/div/sqrt on doubles are used (no libm transcendentals), so the same seed yields the
@@ -12,7 +13,9 @@
  *   linears: Xavier-uniform, bound sqrt(6 / (fan_in + fan_out)); all biases 0
  *   RMSNorm / gated-norm weights 1; time/row/col embeddings and readout N(0, 0.02^2)
  *   GDN: A_log = ln U[1,16], dt_bias 0, short convs He-normal (fan_in 4), conv biases 0; SISA lambda_raw 0
- * Normal deviates are Irwin-Hall sums of 12 uniforms minus 6. */
+ * Normal deviates are Irwin-Hall sums of 12 uniforms minus 6.
+ * SHIELD-A: the tensors its sequence stages read, names and shapes as engine/audio/sequence.cpp:304-331 validates
+ * them (the frontend's are not written); the same distributions, head biases 0. */
 #include "sha256.h"
 
 #include <stdint.h>
@@ -232,14 +235,65 @@ static void fill(const Spec* s, float* out, Rng* r) {
 }
 
 /* ---------------------------------------------------------------------------------------------- C API */
-/* Writes `path` (SHLDV001) and `path`.json.  Returns 0 on success, -1 on I/O failure.  sha_hex (65 bytes) may be
- * NULL; parameter/tensor totals may be NULL. */
-SHV_SYNTH_API int shv_synth_weights(const char* path, uint64_t seed, double threshold, char* sha_hex,
-                                     long long* parameters, int* tensors) {
-    Table t = {0};
-    build_table(&t);
+static void build_audio_table(Table* t) {
+    char n[96];
+    { int d[3] = {1, 1, 384}; add(t, "readout", 3, d, D_EMB, 0, 0, 1); }
+    const char* stages[2] = {"gdn_a", "gdn_b"};
+    for (int s = 0; s < 2; ++s) {
+        const char* p = stages[s];
+        snprintf(n, sizeof n, "%s.mixer_norm.weight", p); t1(t, n, 384, D_ONE);
+        snprintf(n, sizeof n, "%s.ffn_norm.weight", p); t1(t, n, 384, D_ONE);
+        snprintf(n, sizeof n, "%s.mixer.q_proj.weight", p); lin(t, n, 384, 384);
+        snprintf(n, sizeof n, "%s.mixer.k_proj.weight", p); lin(t, n, 384, 384);
+        snprintf(n, sizeof n, "%s.mixer.v_proj.weight", p); lin(t, n, 768, 384);
+        snprintf(n, sizeof n, "%s.mixer.a_proj.weight", p); lin(t, n, 6, 384);
+        snprintf(n, sizeof n, "%s.mixer.b_proj.weight", p); lin(t, n, 6, 384);
+        snprintf(n, sizeof n, "%s.mixer.g_proj.weight", p); lin(t, n, 768, 384);
+        snprintf(n, sizeof n, "%s.mixer.o_proj.weight", p); lin(t, n, 384, 768);
+        snprintf(n, sizeof n, "%s.mixer.A_log", p); t1(t, n, 6, D_ALOG);
+        snprintf(n, sizeof n, "%s.mixer.dt_bias", p); t1(t, n, 6, D_ZERO);
+        snprintf(n, sizeof n, "%s.mixer.o_norm.weight", p); t1(t, n, 128, D_ONE);
+        const char* cv[3] = {"q_conv1d", "k_conv1d", "v_conv1d"};
+        const int cw[3] = {384, 384, 768};
+        for (int c = 0; c < 3; ++c) {
+            int d[3] = {cw[c], 1, 4};
+            snprintf(n, sizeof n, "%s.mixer.%s.weight", p, cv[c]); add(t, n, 3, d, D_HE, 4, 0, 1);
+            snprintf(n, sizeof n, "%s.mixer.%s.bias", p, cv[c]); t1(t, n, cw[c], D_ZERO);
+        }
+        snprintf(n, sizeof n, "%s.ffn.w_gate.weight", p); lin(t, n, 960, 384);
+        snprintf(n, sizeof n, "%s.ffn.w_up.weight", p); lin(t, n, 960, 384);
+        snprintf(n, sizeof n, "%s.ffn.w_down.weight", p); lin(t, n, 384, 960);
+    }
+    t1(t, "sisa.attn_norm.weight", 384, D_ONE);
+    t1(t, "sisa.ffn_norm.weight", 384, D_ONE);
+    lin(t, "sisa.attn.W_Q.weight", 384, 384);
+    lin(t, "sisa.attn.W_K.weight", 384, 384);
+    lin(t, "sisa.attn.W_V.weight", 384, 384);
+    lin(t, "sisa.attn.W_O.weight", 384, 384);
+    lin(t, "sisa.attn.W_B.weight", 192, 384);
+    lin(t, "sisa.attn.W_C.weight", 192, 384);
+    lin(t, "sisa.attn.theta_proj.weight", 96, 384);
+    lin(t, "sisa.attn.alpha_proj.weight", 6, 384);
+    t1(t, "sisa.attn.alpha_proj.bias", 6, D_ZERO);
+    lin(t, "sisa.attn.forget_proj.weight", 6, 384);
+    t1(t, "sisa.attn.forget_proj.bias", 6, D_ZERO);
+    t1(t, "sisa.attn.lambda_raw", 6, D_ZERO);
+    lin(t, "sisa.ffn.w_gate.weight", 960, 384);
+    lin(t, "sisa.ffn.w_up.weight", 960, 384);
+    lin(t, "sisa.ffn.w_down.weight", 384, 960);
+    t1(t, "head_norm.weight", 384, D_ONE);
+    lin(t, "head.0.weight", 128, 384);
+    t1(t, "head.0.bias", 128, D_ZERO);
+    lin(t, "head.3.weight", 1, 128);
+    t1(t, "head.3.bias", 1, D_ZERO);
+}
+
+/* Writes the table as `magic` container (tensor count, then name, rank, dims, element count, fp32 values per
+ * tensor) drawing values in table order from one seeded stream.  0 on success, -1 on I/O failure. */
+static int write_table(const char* path, const char* magic, const Table* t, uint64_t seed, char hex[65],
+                       long long* params_out, size_t* bytes_out) {
     FILE* f = fopen(path, "wb");
-    if (!f) { free(t.v); return -1; }
+    if (!f) return -1;
     shv_sha256 h;
     shv_sha256_init(&h);
     Rng r;
@@ -253,11 +307,11 @@ SHV_SYNTH_API int shv_synth_weights(const char* path, uint64_t seed, double thre
         shv_sha256_update(&h, (p), (n));                       \
         bytes += (n);                                          \
     } while (0)
-    PUT("SHLDV001", 8);
-    const uint32_t count = (uint32_t)t.n;
+    PUT(magic, 8);
+    const uint32_t count = (uint32_t)t->n;
     PUT(&count, 4);
-    for (int i = 0; i < t.n && ok; ++i) {
-        const Spec* s = &t.v[i];
+    for (int i = 0; i < t->n && ok; ++i) {
+        const Spec* s = &t->v[i];
         const uint32_t nl = (uint32_t)strlen(s->name), rank = (uint32_t)s->rank;
         PUT(&nl, 4);
         PUT(s->name, nl);
@@ -274,9 +328,24 @@ SHV_SYNTH_API int shv_synth_weights(const char* path, uint64_t seed, double thre
 #undef PUT
     if (fclose(f) != 0) ok = 0;
     uint8_t dg[32];
-    char hex[65];
     shv_sha256_final(&h, dg);
     shv_sha256_hex(dg, hex);
+    if (params_out) *params_out = params;
+    if (bytes_out) *bytes_out = bytes;
+    return ok ? 0 : -1;
+}
+
+/* ---------------------------------------------------------------------------------------------- C API */
+/* Writes `path` (SHLDV001) and `path`.json.  Returns 0 on success, -1 on I/O failure.  sha_hex (65 bytes) may be
+ * NULL; parameter/tensor totals may be NULL. */
+SHV_SYNTH_API int shv_synth_weights(const char* path, uint64_t seed, double threshold, char* sha_hex,
+                                     long long* parameters, int* tensors) {
+    Table t = {0};
+    build_table(&t);
+    char hex[65];
+    long long params = 0;
+    size_t bytes = 0;
+    int ok = write_table(path, "SHLDV001", &t, seed, hex, &params, &bytes) == 0;
     if (ok) {
         char jp[4096];
         snprintf(jp, sizeof jp, "%s.json", path);
@@ -296,6 +365,18 @@ SHV_SYNTH_API int shv_synth_weights(const char* path, uint64_t seed, double thre
     if (tensors) *tensors = t.n;
     free(t.v);
     return ok ? 0 : -1;
+}
+
+/* SHIELD-A sequence-stage weights (SHLDA001) at `path`.  0 on success, -1 on I/O failure; sha_hex may be NULL. */
+SHV_SYNTH_API int shv_synth_audio_weights(const char* path, uint64_t seed, char* sha_hex, int* tensors) {
+    Table t = {0};
+    build_audio_table(&t);
+    char hex[65];
+    const int rc = write_table(path, "SHLDA001", &t, seed, hex, NULL, NULL);
+    if (sha_hex) memcpy(sha_hex, hex, 65);
+    if (tensors) *tensors = t.n;
+    free(t.v);
+    return rc;
 }
 
 /* n uniform bytes on {0..255} from `seed` (crops: 172800 bytes per frame, 20 frames per clip). */

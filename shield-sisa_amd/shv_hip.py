@@ -79,6 +79,16 @@ _SIGS = {
                                                   _P]),
     "shv_hip_native_crops_rgb": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
     "shv_hip_native_crops_i420": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
+    "shv_hip_audio_load": (_P, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int, ctypes.c_int]),
+    "shv_hip_audio_free": (None, [_P]),
+    "shv_hip_audio_mode": (ctypes.c_char_p, [_P]),
+    "shv_hip_audio_fingerprint": (ctypes.c_char_p, [_P]),
+    "shv_hip_audio_device_bytes": (ctypes.c_size_t, [_P]),
+    "shv_hip_audio_sequence": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, _P]),
+    "shv_hip_audio_sequence_device": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_size_t, _P, _P]),
+    "shv_hip_audio_profile_enable": (ctypes.c_int, [_P, ctypes.c_int]),
+    "shv_hip_audio_profile_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P, _P, _P]),
+    "shv_hip_audio_set_dump_dir": (ctypes.c_int, [_P, ctypes.c_char_p]),
 }
 
 _libs: dict[str, ctypes.CDLL] = {}
@@ -108,12 +118,28 @@ def synth_library() -> ctypes.CDLL:
         lib.shv_synth_weights.restype = ctypes.c_int
         lib.shv_synth_weights.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_double, ctypes.c_char_p,
                                           ctypes.POINTER(ctypes.c_longlong), ctypes.POINTER(ctypes.c_int)]
+        lib.shv_synth_audio_weights.restype = ctypes.c_int
+        lib.shv_synth_audio_weights.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_char_p,
+                                                ctypes.POINTER(ctypes.c_int)]
         lib.shv_synth_bytes.restype = None
         lib.shv_synth_bytes.argtypes = [_P, ctypes.c_size_t, ctypes.c_uint64]
         lib.shv_synth_sha256.restype = None
         lib.shv_synth_sha256.argtypes = [_P, ctypes.c_size_t, ctypes.c_char_p]
         _libs["synth"] = lib
     return _libs["synth"]
+
+
+def write_audio_weights(path, seed: int = 5) -> str:
+    """Seeded synthetic SHLDA001 weights of the SHIELD-A sequence stages; returns the SHA-256 hex."""
+    sha = ctypes.create_string_buffer(65)
+    if synth_library().shv_synth_audio_weights(str(path).encode(), seed, sha, None) != 0:
+        raise ShvError(f"cannot write {path}")
+    return sha.value.decode()
+
+
+def audio_tokens(n: int, seed: int = 17) -> np.ndarray:
+    """n windows of SHIELD-A sequence input: 125 tokens x 384, float32 ~ N(0,1) from a seeded generator."""
+    return np.random.default_rng(seed).standard_normal((n, 125, 384)).astype(np.float32)
 
 
 def write_weights(path, seed: int = 1, threshold: float = 0.5) -> str:
@@ -325,6 +351,82 @@ class Model:
 
     def set_dump_dir(self, d: str) -> None:
         if self.lib.shv_hip_set_dump_dir(self.h, d.encode()) != 0:
+            raise ShvError(self._err())
+
+
+AUDIO_WINDOW_FLOATS = 125 * 384
+
+
+class AudioModel:
+    """SHIELD-A sequence stages on the GPU (shv_hip_audio_load): windows of 125 x 384 frontend tokens -> logits."""
+
+    def __init__(self, weights, mode: str = "fp32", device: int = 0, max_windows: int = 256,
+                 experimental: bool = False):
+        self.lib = library(experimental)
+        self.h = self.lib.shv_hip_audio_load(str(weights).encode(), mode.encode(), device, max_windows)
+        if not self.h:
+            raise ShvError(self.lib.shv_hip_last_error().decode())
+
+    def close(self):
+        if self.h:
+            self.lib.shv_hip_audio_free(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _err(self) -> str:
+        return self.lib.shv_hip_last_error().decode()
+
+    @property
+    def mode(self) -> str:
+        return self.lib.shv_hip_audio_mode(self.h).decode()
+
+    @property
+    def fingerprint(self) -> str:
+        return self.lib.shv_hip_audio_fingerprint(self.h).decode()
+
+    def device_bytes(self) -> int:
+        return self.lib.shv_hip_audio_device_bytes(self.h)
+
+    def sequence(self, tokens: np.ndarray, stride: int | None = None) -> np.ndarray:
+        """tokens [n][125][384] (or a float32 array whose rows are `stride` floats apart) -> logits [n]"""
+        tokens = np.ascontiguousarray(tokens, dtype=np.float32)
+        stride = AUDIO_WINDOW_FLOATS if stride is None else stride
+        n = tokens.size // stride
+        out = np.empty(n, np.float32)
+        if self.lib.shv_hip_audio_sequence(self.h, _ptr(tokens), n, stride, _ptr(out)) != 0:
+            raise ShvError(self._err())
+        return out
+
+    def sequence_device(self, d_tokens: int, n: int, d_logits: int, stride: int = AUDIO_WINDOW_FLOATS,
+                        stream: int | None = None) -> None:
+        if self.lib.shv_hip_audio_sequence_device(self.h, d_tokens, n, stride, d_logits, stream) != 0:
+            raise ShvError(self._err())
+
+    def profile_enable(self, on: bool) -> None:
+        if self.lib.shv_hip_audio_profile_enable(self.h, 1 if on else 0) != 0:
+            raise ShvError(self._err())
+
+    def profile_read(self, family: str):
+        ms, n, b, f = ctypes.c_double(), ctypes.c_longlong(), ctypes.c_double(), ctypes.c_double()
+        rc = self.lib.shv_hip_audio_profile_read(self.h, family.encode(), ctypes.byref(ms), ctypes.byref(n),
+                                                 ctypes.byref(b), ctypes.byref(f))
+        if rc != 0:
+            return None
+        return dict(ms=ms.value, launches=n.value, bytes=b.value, flops=f.value)
+
+    def set_dump_dir(self, d: str) -> None:
+        if self.lib.shv_hip_audio_set_dump_dir(self.h, d.encode()) != 0:
             raise ShvError(self._err())
 
 
