@@ -10,7 +10,9 @@ extra: batch-1 end-to-end latency through shv_hip_predict (pinned host clip, H2D
        encoder-only frames/s (config 1); the pointwise GEMM microbench on the literal config-2 shapes, the real
        model's 1x1 shapes and the sequence shapes (config 2); sequence-stage windows/s (config 3); bf16 1,024 clips
        through the async API with HBM and MFMA rates and fp32 parity (config 4); the reference CPU engine
-       (compiled from the reference sources into oracle/_ref) timed on this host's cores.
+       (compiled from the reference sources into oracle/_ref) timed on this host's cores; the SHIELD-A sequence
+       stages at 256 windows (fp16 and fp32, device-resident and from host memory) beside the reference SHIELD-A
+       engine's CPU sequence.
 roofline: the dominant kernel is the profiling family (one kernel at the shapes the forward gives it) with the
        largest device time per step, from a per-kernel pass with HIP events on the launching stream (graphs off).
        Its algorithmic bytes and FLOPs per launch are recorded by the engine (maps in and out, weights; 2 M N K);
@@ -353,7 +355,84 @@ def crop_bench(shv, hip, stream, model, clips_n: int, d_logits: int, iters: int 
     return out
 
 
-def roofline_of(stats: dict, steps: int, mode: str, revision: str) -> dict:
+AUDIO_WINDOWS = 256
+
+
+def audio_cpu_baseline(weights: Path, tokens: np.ndarray, seconds: float) -> dict | None:
+    """The reference SHIELD-A engine's sequence stages (exact mode, compiled from the reference sources into
+    oracle/_ref) on this host's cores: one window per call, min(16, visible cores) calls in flight (the engine's
+    workspace is per thread; the box's CPU share for one GPU is 16 cores)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from concurrent.futures import ThreadPoolExecutor
+    if not oracle.AUDIO_SO.exists():
+        return None
+    visible = len(os.sched_getaffinity(0))
+    threads = max(1, min(16, visible))
+    ref = oracle.AudioReference(weights)
+    ref.sequence(tokens[0])
+    n, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        while time.perf_counter() - t0 < seconds:
+            list(ex.map(lambda i: ref.sequence(tokens[i % len(tokens)]), range(n, n + 4 * threads)))
+            n += 4 * threads
+    dt = time.perf_counter() - t0
+    ref.close()
+    return {"value": round(n / dt, 2), "unit": "windows/s", "cores": threads, "kind": "reference",
+            "cpu": cpu_model(), "host_cpus_visible": visible,
+            "sample": f"reference SHIELD-A shield::sequence, exact mode, {n} windows in {dt:.1f} s on {threads} "
+                      f"threads (one window per call)"}
+
+
+def audio_bench(shv, hip, stream, e0, e1, steps: int, revision: str, cpu_seconds: float | None) -> dict:
+    """Row f4: the SHIELD-A sequence stages (125 tokens + readout -> logit per window) at 256 windows from HBM through
+    shv_hip_audio_sequence_device, fp16 and fp32; the same from pageable host memory (PCIe inclusive); the roofline
+    of the dominant kernel family; the reference's CPU sequence beside it."""
+    out = {"workload": f"shielda_sequence_b{AUDIO_WINDOWS}", "windows": AUDIO_WINDOWS, "tokens_per_window": 126,
+           "data": "synthetic (seeded SHLDA001 sequence weights, N(0,1) tokens)"}
+    with tempfile.TemporaryDirectory() as td:
+        w = Path(td) / "audio.shlda"
+        shv.write_audio_weights(w, 5)
+        toks = shv.audio_tokens(AUDIO_WINDOWS, 17)
+        d_tok = hip.upload(toks)
+        d_out = hip.malloc(AUDIO_WINDOWS * 4)
+        for mode in ("fp16", "fp32"):
+            log(f"[bench] audio {mode}: {AUDIO_WINDOWS} windows")
+            m = shv.AudioModel(w, mode, max_windows=AUDIO_WINDOWS, experimental=mode != "fp32")
+            for _ in range(3):
+                m.sequence_device(d_tok, AUDIO_WINDOWS, d_out, stream=stream)
+            hip.stream_sync(stream)
+            hip.record(e0, stream)
+            for _ in range(steps):
+                m.sequence_device(d_tok, AUDIO_WINDOWS, d_out, stream=stream)
+            hip.record(e1, stream)
+            ms = hip.elapsed_ms(e0, e1) / steps
+            m.profile_enable(True)
+            m.sequence_device(d_tok, AUDIO_WINDOWS, d_out, stream=stream)
+            hip.stream_sync(stream)
+            stats = {f: m.profile_read(f) for f in m.profile_families()}
+            m.profile_enable(False)
+            stats = {k: v for k, v in stats.items() if v and v["launches"]}
+            fam = {k: round(v["ms"], 3) for k, v in sorted(stats.items(), key=lambda kv: -kv[1]["ms"])}
+            m.sequence(toks)
+            t0 = time.perf_counter()
+            host_logits = m.sequence(toks)
+            host_s = time.perf_counter() - t0
+            out[mode] = {"windows_per_s": round(AUDIO_WINDOWS / (ms / 1000.0), 1), "ms_per_batch": round(ms, 4),
+                         "host_memory_windows_per_s": round(AUDIO_WINDOWS / host_s, 1),
+                         "finite": bool(np.isfinite(host_logits).all()), "family_ms": fam,
+                         "roofline": roofline_of(stats, 1, mode, revision, traffic_file=False)}
+            log(f"[bench] audio {mode}: {ms:.3f} ms / {AUDIO_WINDOWS} windows -> "
+                f"{out[mode]['windows_per_s']} windows/s; dominant {out[mode]['roofline']['kernel']}")
+            m.close()
+        hip.free(d_tok)
+        hip.free(d_out)
+        if cpu_seconds:
+            out["cpu_baseline"] = audio_cpu_baseline(w, toks, cpu_seconds)
+    return out
+
+
+def roofline_of(stats: dict, steps: int, mode: str, revision: str, traffic_file: bool = True) -> dict:
     """The family with the most device time per step, against the roof its intensity selects."""
     dom = max(stats, key=lambda k: stats[k]["ms"])
     d = stats[dom]
@@ -365,7 +444,7 @@ def roofline_of(stats: dict, steps: int, mode: str, revision: str) -> dict:
     peak_tf = FP32_PEAK_TFLOPS if mode == "fp32" else MFMA_PEAK_TFLOPS
     ridge = peak_tf * 1e12 / (HBM_PEAK_GBS * 1e9)
     intensity = flops_l / bytes_l if bytes_l else 0.0
-    traffic = measured_traffic(dom, revision)
+    traffic = measured_traffic(dom, revision) if traffic_file else None
     if intensity < ridge:
         r = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
              "frac": round(gbs / HBM_PEAK_GBS, 4)}
@@ -397,6 +476,7 @@ def main() -> int:
     ap.add_argument("--no-async", action="store_true")
     ap.add_argument("--no-crop", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-audio", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every GPU box here has one GPU, and the SHIELD-V forward has no "
@@ -481,6 +561,10 @@ def main() -> int:
         hip.free(d_frames)
         hip.free(d_logits)
         gemm = None if args.kernel_only or args.no_gemm else gemm_microbench(shv, hip, stream, e0, e1)
+        audio = None
+        if not args.kernel_only and not args.no_audio:
+            audio = audio_bench(shv, hip, stream, e0, e1, max(3, args.steps // 2), revision,
+                                None if args.no_cpu else min(5.0, args.cpu_seconds))
         hip.stream_destroy(stream)
 
         lat = lat32 = None
@@ -533,6 +617,7 @@ def main() -> int:
         "device_copy": copy,
         "gemm_microbench": gemm,
         "face_crops": crops,
+        "shielda_sequence": audio,
         "revision": revision,
     }
     print(json.dumps(line), flush=True)

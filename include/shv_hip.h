@@ -237,6 +237,7 @@ int shv_hip_audio_sequence_device(shv_hip_audio* a, const float* d_tokens, int n
 int shv_hip_audio_profile_enable(shv_hip_audio* a, int on);
 int shv_hip_audio_profile_read(shv_hip_audio* a, const char* name, double* total_ms, long long* launches,
                                double* bytes, double* flops);
+long long shv_hip_audio_profile_list(shv_hip_audio* a, char* buf, size_t cap);
 int shv_hip_audio_set_dump_dir(shv_hip_audio* a, const char* dir);
 
 #if defined(__GNUC__)

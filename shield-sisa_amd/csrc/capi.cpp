@@ -432,6 +432,26 @@ int shv_hip_audio_profile_read(shv_hip_audio* a, const char* name, double* total
     });
 }
 
+long long shv_hip_audio_profile_list(shv_hip_audio* a, char* buf, size_t cap) {
+    try {
+        if (!a) throw std::runtime_error("null handle");
+        std::string all;
+        {
+            std::lock_guard<std::mutex> lk(a->mu);
+            for (const std::string& f : a->eng->profile_families()) all += f + "\n";
+        }
+        if (buf && cap) {
+            const size_t n = std::min(cap - 1, all.size());
+            std::memcpy(buf, all.data(), n);
+            buf[n] = '\0';
+        }
+        return (long long)all.size();
+    } catch (const std::exception& e) {
+        shv::sched::set_error(e.what());
+        return -1;
+    }
+}
+
 int shv_hip_audio_set_dump_dir(shv_hip_audio* a, const char* dir) {
     return guarded([&] {
         if (!a) throw std::runtime_error("null handle");

@@ -89,6 +89,7 @@ _SIGS = {
     "shv_hip_audio_profile_enable": (ctypes.c_int, [_P, ctypes.c_int]),
     "shv_hip_audio_profile_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P, _P, _P]),
     "shv_hip_audio_set_dump_dir": (ctypes.c_int, [_P, ctypes.c_char_p]),
+    "shv_hip_audio_profile_list": (ctypes.c_longlong, [_P, _P, ctypes.c_size_t]),
 }
 
 _libs: dict[str, ctypes.CDLL] = {}
@@ -424,6 +425,14 @@ class AudioModel:
         if rc != 0:
             return None
         return dict(ms=ms.value, launches=n.value, bytes=b.value, flops=f.value)
+
+    def profile_families(self) -> list:
+        n = self.lib.shv_hip_audio_profile_list(self.h, None, 0)
+        if n < 0:
+            raise ShvError(self._err())
+        buf = ctypes.create_string_buffer(int(n) + 1)
+        self.lib.shv_hip_audio_profile_list(self.h, buf, len(buf))
+        return [x for x in buf.value.decode().split("\n") if x]
 
     def set_dump_dir(self, d: str) -> None:
         if self.lib.shv_hip_audio_set_dump_dir(self.h, d.encode()) != 0:

@@ -148,8 +148,11 @@ def test_audio_profile_families(models, atokens):
     m.profile_enable(True)
     try:
         m.sequence(atokens)
+        fams = m.profile_families()
         for fam in ("assemble", "gdn_prep", "delta", "gated_norm", "sisa", "head"):
+            assert fam in fams
             st = m.profile_read(fam)
             assert st and st["launches"] >= 1 and st["ms"] > 0, fam
+        assert any(f.startswith("gemm_seq:") for f in fams)
     finally:
         m.profile_enable(False)
