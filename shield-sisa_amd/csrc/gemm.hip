@@ -531,8 +531,8 @@ inline unsigned int cdiv(long long a, long long b) { return (unsigned int)((a + 
 // split into the tier's parts).  Workgroup tile 64 WGM x 32 WN, 2 WGM waves of 64 x 16 WN, K steps of 32.
 // The operand tiles of a K step are sixteen-row fragment blocks of 1 KB each (A: 8 blocks per part, W: 8 per part),
 // written by global_load_lds_dwordx4 (16 bytes per lane, lane l to byte 16 l of its block) with no register staging,
-// and read back as MFMA fragments.  DMA lane l carries row l / 4 and 16-byte K chunk (l % 4) ^ ((l / 16) % 4) of the
-// block, so that the sixteen lanes of a fragment read (one chunk of rows 0..15) cover the 64 banks once.  NS K steps
+// and read back as MFMA fragments.  DMA lane l carries row l / 4 and 16-byte K chunk (l % 4) ^ dma_swz(l / 4) of the
+// block (a per-row chunk permutation), so that a fragment read's lanes hit distinct banks.  NS K steps
 // share an LDS ring (fp16: 2 x 32 KB for 128 x 128 tiles, two 4-wave workgroups per CU; bf16: 2 x 72 KB for
 // 256 x 128 tiles, one 8-wave workgroup per CU): a step waits for its own loads (s_waitcnt on the wave's count of younger loads) and one barrier, then issues
 // the loads of step k + NS - 1 into the slot step k - 1 used.  Per output the MFMA sequence is that of every other MFMA GEMM kernel (K steps in order,
@@ -551,6 +551,11 @@ template <typename T, int NS_, int WN_, int WGM_> struct DmaCfg {
     static_assert(TB % WAVES == 0, "the step's blocks are dealt evenly over the waves");
 };
 
+// Chunk permutation of a fragment block's row r (16-byte K chunk c stored at slot 4 r + (c ^ dma_swz(r))): the 16
+// lanes of a fragment read (one chunk of rows 0..15) then fall on 16 distinct 16-byte bank groups, and so do the
+// 8-lane halves on 8 distinct groups of a 128-byte bank row.
+__device__ __forceinline__ int dma_swz(int r) { return ((r >> 2) ^ (r >> 1)) & 3; }
+
 // the wave's loads of one K step are issued; wait until at most N younger ones are outstanding
 template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 __device__ __forceinline__ void dma16(const void* src, void* lds_block) {
@@ -558,7 +563,7 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_block) {
 }
 
 template <typename T, int NS_, int WN_, int WGM_>
-__global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mblocks, int nblocks) {
+__global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mblocks, int nblocks, int vec_c) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     typedef DmaCfg<T, NS_, WN_, WGM_> D;
@@ -578,7 +583,7 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
     const int nk = p.K / 32;
 
     // this lane's source rows of the wave's DPW loads (rows clamped into range; K chunk swizzled)
-    const int drow = lane >> 2, dchunk = (lane & 3) ^ ((lane >> 4) & 3);
+    const int drow = lane >> 2, dchunk = (lane & 3) ^ dma_swz(drow);
     const T* src[DPW];
     int boff[DPW];
 #pragma unroll
@@ -600,8 +605,8 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
 #pragma unroll
         for (int j = 0; j < DPW; ++j) dma16(src[j] + ks * 32, st + boff[j]);
     };
-    // fragment reads: lane (r, g) takes chunk g of row r of a block, stored at lane slot 4 r + (g ^ (r / 4 % 4))
-    const int foff = 16 * (4 * r + (g ^ ((r >> 2) & 3)));
+    // fragment reads: lane (r, g) takes chunk g of row r of a block, stored at lane slot 4 r + (g ^ dma_swz(r))
+    const int foff = 16 * (4 * r + (g ^ dma_swz(r)));
 
     f32x4 acc[WM][WN];
 #pragma unroll
@@ -656,6 +661,57 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
                 }
             }
         return;
+    }
+    if constexpr (WN % 4 == 0) {
+        // fp32 C in 16-byte column groups (vec_c: the host checked alignment and strides): the wave's 64 x 16 WN tile
+        // goes through its own LDS region of the (now idle) ring, then each store instruction writes four whole rows
+        // of the tile (16 WN x 4 bytes each) instead of 64-byte pieces of 16.  The region is [64][16 WN] floats with
+        // the 16-column group index XOR-ed by the row's (row / 4) % 4, so the fragment writes (rows 4g + i, 16
+        // columns per lane group g) and the row reads both hit distinct banks.
+        if (vec_c) {
+            constexpr int TW = 16 * WN, GPR = TW / 4;   // tile columns, float4 groups per row
+            static_assert(D::WAVES * 64 * TW * 4 <= NS * D::STAGE, "the ring holds every wave's C tile");
+            __syncthreads();   // every wave has read its last operands from the ring
+            float* wt = reinterpret_cast<float*>(ring) + wave * 64 * TW;
+#pragma unroll
+            for (int mt = 0; mt < WM; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < WN; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int row = mt * 16 + g * 4 + i;
+                        wt[row * TW + ((nt * 16 + r) ^ (g * 16))] = acc[mt][nt][i];
+                    }
+            __syncthreads();
+            constexpr int PASSES = 64 * GPR / 64;
+            const int c4 = lane % GPR, rsub = lane / GPR;   // this lane's column group; row within a pass
+            const int n = nbase + c4 * 4;
+            const bool ncol = n < p.N;                      // N % 4 == 0: a group is wholly in or out
+            float4 bv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (p.bias && ncol) bv = *reinterpret_cast<const float4*>(p.bias + n);
+            float4 v[PASSES], rv[PASSES];
+            const long long mw = m0 + wm * WM * 16;
+#pragma unroll
+            for (int q = 0; q < PASSES; ++q) {
+                const int row = q * (64 / GPR) + rsub;
+                v[q] = *reinterpret_cast<const float4*>(wt + row * TW + ((c4 * 4) ^ (((row >> 2) & 3) * 16)));
+                const long long m = min(mw + row, (long long)p.M - 1);
+                rv[q] = p.res ? *reinterpret_cast<const float4*>(p.R + m * p.ldr + min(n, p.N - 4))
+                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int q = 0; q < PASSES; ++q) {
+                const long long m = mw + q * (64 / GPR) + rsub;
+                if (m >= p.M || !ncol) continue;
+                float4 o;
+                o.x = epi_value(p, v[q].x, bv.x, rv[q].x);
+                o.y = epi_value(p, v[q].y, bv.y, rv[q].y);
+                o.z = epi_value(p, v[q].z, bv.z, rv[q].z);
+                o.w = epi_value(p, v[q].w, bv.w, rv[q].w);
+                *reinterpret_cast<float4*>(p.C + m * p.ldc + n) = o;
+            }
+            return;
+        }
     }
 #pragma unroll
     for (int mt = 0; mt < WM; ++mt)
@@ -972,8 +1028,12 @@ template <typename T, int NS, int WN, int WGM> void launch_dma_cfg(const GemmArg
     const int mblocks = (int)cdiv(p.M, 64 * WGM), nblocks = (int)cdiv(p.N, 32 * WN);
     const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
     if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_dma: grid too large");
+    // fp32 C stored in 16-byte column groups when N, the strides and the pointers allow it
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const int vec_c = !p.swiglu && p.ldc % 4 == 0 && p.N % 4 == 0 && al16(p.C) && (!p.bias || al16(p.bias)) &&
+                      (!p.res || (p.ldr % 4 == 0 && al16(p.R)));
     hipLaunchKernelGGL((gemm_dma_kernel<T, NS, WN, WGM>), dim3((unsigned)blocks), dim3(128 * WGM), 0, s, p, mblocks,
-                       nblocks);
+                       nblocks, vec_c);
 }
 
 template <typename T> void launch_dma(const GemmArgs& p, hipStream_t s) {
