@@ -555,6 +555,7 @@ template <typename T, int NS_, int WN_, int WGM_> struct DmaCfg {
 // lanes of a fragment read (one chunk of rows 0..15) then fall on 16 distinct 16-byte bank groups, and so do the
 // 8-lane halves on 8 distinct groups of a 128-byte bank row.
 __device__ __forceinline__ int dma_swz(int r) { return ((r >> 2) ^ (r >> 1)) & 3; }
+constexpr int DMA_GM = 8;   // local M blocks per tile-order group (see gemm_dma_kernel)
 
 // the wave's loads of one K step are issued; wait until at most N younger ones are outstanding
 template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
@@ -573,8 +574,15 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: the LDS destinations are scalar
     const int wm = wave / WGN, wn = wave % WGN;
+    // Tile order: workgroups go round-robin over the XCDs, so XCD x runs slots 0, 1, ... of its own M blocks
+    // (mb = 8 mbl + x).  Its slots walk groups of DMA_GM local M blocks column block by column block, so the ~64
+    // workgroups resident on an XCD share DMA_GM A blocks and a few W column blocks: both stay in the XCD's L2
+    // (4 MB) instead of the whole W being cycled through it once per M block.
     const int xcd = blockIdx.x % XCDS, slot = blockIdx.x / XCDS;
-    const int mb = (slot / nblocks) * XCDS + xcd, nb = slot % nblocks;
+    const int mloc = (mblocks + XCDS - 1) / XCDS;                // local M blocks per XCD
+    const int grp = slot / (DMA_GM * nblocks), within = slot % (DMA_GM * nblocks);
+    const int gsize = min(DMA_GM, mloc - grp * DMA_GM);
+    const int mb = (grp * DMA_GM + within % gsize) * XCDS + xcd, nb = within / gsize;
     if (mb >= mblocks) return;   // uniform over the workgroup
     const long long m0 = (long long)mb * D::BM;
     const int n0 = nb * BN;
