@@ -239,110 +239,145 @@ public:
         HIDL_ = amem.make<float>(Bm * kFF);
     }
 
-    // the residual stream [max_windows * T][384] the caller assembles before run()
-    float* h() const { return H_; }
+    // the residual stream [max_windows * T][384] the caller assembles before run(), from window w0 on
+    float* h(int w0 = 0) const { return H_ + size_t(w0) * spec_.T * kD; }
 
-    // h() of B windows -> logits[B]
-    void run(int B, float* logits, hipStream_t s, Profiler& pf, const std::string& dump_dir) {
+    // h(w0) of B windows -> logits[B], in windows [w0, w0 + B) of every buffer (disjoint window ranges can run at
+    // once on different streams)
+    void run(int B, float* logits, hipStream_t s, Profiler& pf, const std::string& dump_dir, int w0 = 0) {
         const int T = spec_.T, M = B * T;
         const GemmRunner<G> gr{pf};
-        dump_f32(dump_dir, spec_.dump[0], H_, size_t(T) * kD, s);
+        const size_t r0 = size_t(w0) * T;   // first row
+        float *H = this->H_ + r0 * kD, *P = this->P_ + r0 * kGld, *Q = this->Q_ + r0 * kD,
+              *K = this->K_ + r0 * kD, *V = this->V_ + r0 * kVD, *dec = this->dec_ + r0 * 8,
+              *beta = this->beta_ + r0 * 8, *O = this->O_ + r0 * kVD;
+        float* work = this->dwork_ ? this->dwork_ + delta_chunk_floats(w0, T) : nullptr;
+        float *XN = nullptr, *ON = nullptr, *HID = nullptr;
+        G *XNh = nullptr, *ONh = nullptr, *HIDh = nullptr;
+        if constexpr (kF32) {
+            XN = this->XN_ + r0 * kD;
+            ON = this->ON_ + r0 * kVD;
+            HID = this->HID_ + r0 * kFF;
+        } else {
+            XNh = this->XNh_ + r0 * kD;
+            ONh = this->ONh_ + r0 * kVD;
+            HIDh = this->HIDh_ + r0 * kFF;
+        }
+        float *XL = this->XL_ + size_t(w0) * kD, *QC = this->QC_ + size_t(w0) * 576, *Y = this->Y_ + size_t(w0) * kD,
+              *X1 = this->X1_ + size_t(w0) * kD, *X2 = this->X2_ + size_t(w0) * kD,
+              *HIDL = this->HIDL_ + size_t(w0) * kFF;
+        // the A operand of a sequence GEMM: fp32 (exact tier) or the producer's split parts (MFMA tiers)
+        const auto set_a = [&](GemmArgs& p, const float* a32, const G* ah, int width) {
+            p.lda = width;
+            if constexpr (kF32) p.A = a32;
+            else { p.Ah = ah; p.astride = mrows_ * width; }
+            (void)a32; (void)ah;
+        };
+        // the residual stream's RMSNorm into the A operand of the next GEMM
+        const auto rmsnorm_all = [&](const float* w) {
+            pf.timed("rmsnorm", double(M) * kD * (4 + kAS), s, [&] {
+                if constexpr (kF32) launch_rmsnorm<float>(H, kD, w, XN, kD, M, s);
+                else launch_rmsnorm<G>(H, kD, w, XNh, kD, M, s, mrows_ * kD);
+            });
+            check_launch();
+        };
+        dump_f32(dump_dir, spec_.dump[0], H, size_t(T) * kD, s);
         for (int st = 0; st < 2; ++st) {
             const Gdn& gd = gdn_[st];
             const int reps = st == 0 ? 1 : 2;
             for (int r = 0; r < reps; ++r) {
-                rmsnorm_all(pf, gd.norm_w, s, M);
+                rmsnorm_all(gd.norm_w);
                 GemmArgs pi;
                 pi.M = M; pi.N = kGn; pi.K = kD;
-                set_a(pi, XN_, XNh_, kD); pi.ldw = kD;
-                pi.C = P_; pi.ldc = kGld;
+                set_a(pi, XN, XNh, kD); pi.ldw = kD;
+                pi.C = P; pi.ldc = kGld;
                 gr.gemm("gemm_seq", pi, gd.in_w, s);
                 pf.timed("gdn_prep", double(M) * (4.0 * 1548 * 4 + 4.0 * (2 * kD + kVD + 16)), s, [&] {
-                    launch_gdn_prep(P_, gd.conv_w, gd.conv_b, gd.neg_rate, gd.dt_bias, Q_, K_, V_, dec_, beta_, B, s,
+                    launch_gdn_prep(P, gd.conv_w, gd.conv_b, gd.neg_rate, gd.dt_bias, Q, K, V, dec, beta, B, s,
                                     T, spec_.audio);
                 });
                 check_launch();
                 pf.timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s, [&] {
                     if constexpr (!kF32) {
                         if (delta_chunked_) {
-                            launch_delta_chunked<G>(Q_, K_, V_, dec_, beta_, O_, dwork_, B, s, T);
+                            launch_delta_chunked<G>(Q, K, V, dec, beta, O, work, B, s, T);
                             return;
                         }
                     }
-                    launch_delta(Q_, K_, V_, dec_, beta_, O_, B, kF32, s, T);
+                    launch_delta(Q, K, V, dec, beta, O, B, kF32, s, T);
                 }, 2.0 * B * T * kHeads * 4.0 * kDK * kDV);   // per token and head: decay, S^T k, k u^T, S^T q
                 check_launch();
                 pf.timed("gated_norm", double(M) * (4.0 * 2 * kVD + kAS * kVD), s, [&] {
-                    if constexpr (kF32) launch_gated_norm<float>(O_, P_, gd.o_norm_w, ON_, M, s, 0, spec_.audio);
-                    else launch_gated_norm<G>(O_, P_, gd.o_norm_w, ONh_, M, s, mrows_ * kVD, spec_.audio);
+                    if constexpr (kF32) launch_gated_norm<float>(O, P, gd.o_norm_w, ON, M, s, 0, spec_.audio);
+                    else launch_gated_norm<G>(O, P, gd.o_norm_w, ONh, M, s, mrows_ * kVD, spec_.audio);
                 });
                 check_launch();
                 GemmArgs po;
                 po.M = M; po.N = kD; po.K = kVD;
-                set_a(po, ON_, ONh_, kVD); po.ldw = kVD;
-                po.C = H_; po.ldc = kD;
-                po.R = H_; po.ldr = kD; po.res = reps == 2 ? spec_.gdn_b_res : 1;
+                set_a(po, ON, ONh, kVD); po.ldw = kVD;
+                po.C = H; po.ldc = kD;
+                po.R = H; po.ldr = kD; po.res = reps == 2 ? spec_.gdn_b_res : 1;
                 gr.gemm("gemm_seq", po, gd.out_w, s);
             }
-            rmsnorm_all(pf, gd.ffn_norm_w, s, M);
+            rmsnorm_all(gd.ffn_norm_w);
             GemmArgs pu;
             pu.M = M; pu.N = 2 * kFF; pu.K = kD;
-            set_a(pu, XN_, XNh_, kD); pu.ldw = kD;
+            set_a(pu, XN, XNh, kD); pu.ldw = kD;
             pu.ldc = kFF; pu.swiglu = 1;
-            if constexpr (kF32) pu.C = HID_;
-            else { pu.Ch = HIDh_; pu.cstride = mrows_ * kFF; }
+            if constexpr (kF32) pu.C = HID;
+            else { pu.Ch = HIDh; pu.cstride = mrows_ * kFF; }
             gr.gemm("gemm_seq", pu, gd.up_w, s);
             GemmArgs pd;
             pd.M = M; pd.N = kD; pd.K = kFF;
-            set_a(pd, HID_, HIDh_, kFF); pd.ldw = kFF;
-            pd.C = H_; pd.ldc = kD;
-            pd.R = H_; pd.ldr = kD; pd.res = 1;
+            set_a(pd, HID, HIDh, kFF); pd.ldw = kFF;
+            pd.C = H; pd.ldc = kD;
+            pd.R = H; pd.ldr = kD; pd.res = 1;
             gr.gemm("gemm_seq", pd, gd.down_w, s);
-            dump_f32(dump_dir, spec_.dump[1 + st], H_, size_t(T) * kD, s);
+            dump_f32(dump_dir, spec_.dump[1 + st], H, size_t(T) * kD, s);
         }
         // SISA block, last row only: all-row K/V/B/theta/alpha/forget projection, last-row Q|C in fp32
-        rmsnorm_all(pf, s_attn_norm_, s, M);
+        rmsnorm_all(s_attn_norm_);
         GemmArgs pa;
         pa.M = M; pa.N = kSn; pa.K = kD;
-        set_a(pa, XN_, XNh_, kD); pa.ldw = kD;
+        set_a(pa, XN, XNh, kD); pa.ldw = kD;
         pa.bias = s_in_b_;
-        pa.C = P_; pa.ldc = kSld;
+        pa.C = P; pa.ldc = kSld;
         gr.gemm("gemm_seq", pa, s_in_w_, s);
-        const float* hlast = H_ + size_t(T - 1) * kD;
+        const float* hlast = H + size_t(T - 1) * kD;
         const long long ldlast = (long long)T * kD;
         pf.timed("rmsnorm", double(B) * kD * 8, s,
-                 [&] { launch_rmsnorm<float>(hlast, ldlast, s_attn_norm_, XL_, kD, B, s); });
+                 [&] { launch_rmsnorm<float>(hlast, ldlast, s_attn_norm_, XL, kD, B, s); });
         check_launch();
         GemmArgs pq;
         pq.M = B; pq.N = 576; pq.K = kD;
-        pq.A = XL_; pq.lda = kD; pq.W = s_qc_w_; pq.ldw = kD;
-        pq.C = QC_; pq.ldc = 576;
+        pq.A = XL; pq.lda = kD; pq.W = s_qc_w_; pq.ldw = kD;
+        pq.C = QC; pq.ldc = 576;
         gr.gemm32("gemm_f32_small", pq, s);
-        pf.timed("sisa", double(B) * T * kSn * 4, s, [&] { launch_sisa(P_, QC_, s_lam_, Y_, B, s, T); });
+        pf.timed("sisa", double(B) * T * kSn * 4, s, [&] { launch_sisa(P, QC, s_lam_, Y, B, s, T); });
         check_launch();
         GemmArgs pw;
         pw.M = B; pw.N = kD; pw.K = kD;
-        pw.A = Y_; pw.lda = kD; pw.W = s_o_w_; pw.ldw = kD;
-        pw.C = X1_; pw.ldc = kD;
+        pw.A = Y; pw.lda = kD; pw.W = s_o_w_; pw.ldw = kD;
+        pw.C = X1; pw.ldc = kD;
         pw.R = hlast; pw.ldr = ldlast; pw.res = 1;
         gr.gemm32("gemm_f32_small", pw, s);
         pf.timed("rmsnorm", double(B) * kD * 8, s,
-                 [&] { launch_rmsnorm<float>(X1_, kD, s_ffn_norm_, XL_, kD, B, s); });
+                 [&] { launch_rmsnorm<float>(X1, kD, s_ffn_norm_, XL, kD, B, s); });
         check_launch();
         GemmArgs pu;
         pu.M = B; pu.N = 2 * kFF; pu.K = kD;
-        pu.A = XL_; pu.lda = kD; pu.W = s_up_w_; pu.ldw = kD;
-        pu.C = HIDL_; pu.ldc = kFF; pu.swiglu = 1;
+        pu.A = XL; pu.lda = kD; pu.W = s_up_w_; pu.ldw = kD;
+        pu.C = HIDL; pu.ldc = kFF; pu.swiglu = 1;
         gr.gemm32("gemm_f32_small", pu, s);
         GemmArgs pd;
         pd.M = B; pd.N = kD; pd.K = kFF;
-        pd.A = HIDL_; pd.lda = kFF; pd.W = s_down_w_; pd.ldw = kFF;
-        pd.C = X2_; pd.ldc = kD;
-        pd.R = X1_; pd.ldr = kD; pd.res = 1;
+        pd.A = HIDL; pd.lda = kFF; pd.W = s_down_w_; pd.ldw = kFF;
+        pd.C = X2; pd.ldc = kD;
+        pd.R = X1; pd.ldr = kD; pd.res = 1;
         gr.gemm32("gemm_f32_small", pd, s);
-        dump_f32(dump_dir, spec_.dump[3], X2_, kD, s);
+        dump_f32(dump_dir, spec_.dump[3], X2, kD, s);
         pf.timed("head", double(B) * kD * 4, s,
-                 [&] { launch_head(X2_, fn_w_, h_w0_, h_b0_, h_w2_, h_b2_, logits, B, s, spec_.audio); });
+                 [&] { launch_head(X2, fn_w_, h_w0_, h_b0_, h_w2_, h_b2_, logits, B, s, spec_.audio); });
         check_launch();
         dump_f32(dump_dir, spec_.dump[4], logits, 1, s);
     }
@@ -369,19 +404,6 @@ private:
     long long mrows_ = 0;                                     // rows of those buffers (part stride = mrows_ * width)
     float *XL_ = nullptr, *QC_ = nullptr, *Y_ = nullptr, *X1_ = nullptr, *X2_ = nullptr, *HIDL_ = nullptr;
 
-    // the A operand of a sequence GEMM: fp32 (exact tier) or the producer's split parts (MFMA tiers)
-    void set_a(GemmArgs& p, const float* a32, const G* ah, int width) const {
-        p.lda = width;
-        if constexpr (kF32) p.A = a32;
-        else { p.Ah = ah; p.astride = mrows_ * width; }
-    }
-    void rmsnorm_all(Profiler& pf, const float* w, hipStream_t s, int M) {
-        pf.timed("rmsnorm", double(M) * kD * (4 + kAS), s, [&] {
-            if constexpr (kF32) launch_rmsnorm<float>(H_, kD, w, XN_, kD, M, s);
-            else launch_rmsnorm<G>(H_, kD, w, XNh_, kD, M, s, mrows_ * kD);
-        });
-        check_launch();
-    }
 };
 
 }  // namespace shv
