@@ -46,7 +46,8 @@ DEVICE_FLAGS = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang
 # form adds v_accvgpr moves around every accumulation chain and costs registers).  Only for sources where no inline
 # asm reads an MFMA result: the compiler inserts the MFMA-to-VALU wait states for its own instructions but not for
 # an asm operand, and an empty asm is counted as one wait state.  In these two files every asm operand is a loaded
-# value or a VALU result.
+# value or a VALU result; tests/test_mfma_asm_hazard.py checks that on the built code objects (no inline-asm DPP
+# instruction reads a VGPR that an MFMA write can reach).
 VGPR_FORM_SOURCES = {"strip.hip", "gemm.hip"}
 VGPR_FORM_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 
