@@ -40,6 +40,12 @@ __device__ __forceinline__ float cephes_exp(float x) {
     return p * __int_as_float((ni + 127) << 23);
 }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + cephes_exp(0.0f - x)); }
+// SiLU of the fp16 / bf16 tiers: the hardware exp2 and reciprocal (each within 1 ulp), x * 1 / (1 + 2^(-x log2 e)).
+// Five instructions instead of about twenty-five; a few fp32 ulp from silu(), well inside those tiers' bounds.
+// Limits: x -> -inf gives -0, x -> +inf gives x, NaN stays NaN.
+__device__ __forceinline__ float silu_fast(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
 __device__ __forceinline__ float relu(float x) { return x > 0.0f ? x : 0.0f; }
 // relu for the fp16 / bf16 tiers as one integer max on the bit pattern: every negative float (-0 included) is a
 // negative int and becomes +0, every positive one stays.  Equal to relu() for all inputs but +NaN, which it passes

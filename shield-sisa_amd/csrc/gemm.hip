@@ -336,7 +336,7 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p
                 for (int nt = 0; nt + 1 < NT; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
-                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
+                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu_fast(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
                 }
             }
         return;
@@ -514,7 +514,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p, int mblocks, 
                 for (int nt = 0; nt + 1 < WN; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
-                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
+                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu_fast(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
                 }
             }
         return;
@@ -665,7 +665,7 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
                 for (int nt = 0; nt + 1 < WN; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
-                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
+                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu_fast(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
                 }
             }
         return;
@@ -822,7 +822,7 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
             const long long m = mbase + g * 4 + i;
             if (m >= p.M) continue;
             const int panel = nbase / 16;
-            if ((panel + 1) * 16 <= p.N) swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu(acc[0][i]) * acc[1][i]);
+            if ((panel + 1) * 16 <= p.N) swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu_fast(acc[0][i]) * acc[1][i]);
         }
         return;
     }

@@ -152,9 +152,10 @@ void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long 
 // short conv4 + SiLU on q|k|v, per-head L2 norm, decay = exp(neg_rate * softplus(a + dt_bias)), beta = sigmoid(b).
 // P [rows][2320] -> Q, K [rows][384], V [rows][768], dec, beta [rows][8].  Video: q * (1/sqrt(max(ss,1e-6))) * 0.125;
 // audio: q and k * 1/max(sqrt(ss), 1e-12), q unscaled (engine/audio/sequence.cpp:119-124)
+// fast: SiLU as silu_fast (the fp16 / bf16 tiers); else the exact tier's Cephes form
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
                      const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
-                     hipStream_t s, int T = kT, bool audio = false);
+                     hipStream_t s, int T = kT, bool audio = false, bool fast = false);
 // gated delta rule, sequential over T tokens from zero state, fp32; O [rows][768].  exact: the reference's
 // 64-key fma chains (fp32 tier); else each column's keys split over 4 lane rows, partial sums added in a fixed order
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,
@@ -166,7 +167,8 @@ size_t delta_chunk_floats(int B, int T = kT);
 template <typename T>
 void launch_delta_chunked(const float* Q, const float* K, const float* V, const float* dec, const float* beta,
                           float* O, float* work, int B, hipStream_t s, int Tw = kT);
-// ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768] (T = f16 / bf16: split parts, as launch_rmsnorm).
+// ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768] (T = f16 / bf16: split parts, as launch_rmsnorm,
+// with silu_fast).
 // audio: o * 0.125 first and eps 1e-5 (engine/audio/sequence.cpp:160-171); video eps 1e-6
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,

@@ -102,7 +102,7 @@ __device__ __forceinline__ void row3_gather(float v, float (&out)[3]) {
 // (isa_impl.hpp:893-906); gates with device libm (expf, log1pf).  TT tokens per window; AUDIO selects SHIELD-A's
 // L2 norm (no q scale here: its output is scaled after the recurrence).
 constexpr int GP_T = 4;
-template <int TT, bool AUDIO>
+template <int TT, bool AUDIO, bool FAST>
 __global__ void __launch_bounds__(384)
 gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const float* __restrict__ cb,
                 const float* __restrict__ neg_rate, const float* __restrict__ dt_bias, float* __restrict__ Q,
@@ -173,7 +173,7 @@ gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const
             if (t >= 2) acc = __builtin_fmaf(hist[c][1], w[c][1], acc);
             if (t >= 1) acc = __builtin_fmaf(hist[c][2], w[c][2], acc);
             acc = __builtin_fmaf(hist[c][3], w[c][3], acc);
-            y[c] = silu(acc + bias[c]);
+            y[c] = FAST ? silu_fast(acc + bias[c]) : silu(acc + bias[c]);
         }
         const float q = y[0], k = y[1];
         V[row * kVD + h * 128 + l] = y[2];
@@ -934,7 +934,8 @@ gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, cons
 #pragma unroll
     for (int z = 0; z < 8; ++z) {
         const int i = z * 16 + l;
-        put_value(out, pstride, row * kVD + h * 128 + i, ((v[z] * rstd) * w[i]) * silu(g[i]));
+        const float sg = std::is_same<T, float>::value ? silu(g[i]) : silu_fast(g[i]);
+        put_value(out, pstride, row * kVD + h * 128 + i, ((v[z] * rstd) * w[i]) * sg);
     }
 }
 
@@ -1124,16 +1125,20 @@ template <class F> void for_window(int T, F&& f) {
 
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
                      const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
-                     hipStream_t s, int T, bool audio) {
+                     hipStream_t s, int T, bool audio, bool fast) {
     for_window(T, [&](auto tt) {
         constexpr int TT = decltype(tt)::value;
         const dim3 grid(B * ((TT + GP_T - 1) / GP_T));
-        if (audio)
-            hipLaunchKernelGGL((gdn_prep_kernel<TT, true>), grid, dim3(384), 0, s, P, conv_w, conv_b, neg_rate, dt_bias,
-                               Q, K, V, dec, beta);
-        else
-            hipLaunchKernelGGL((gdn_prep_kernel<TT, false>), grid, dim3(384), 0, s, P, conv_w, conv_b, neg_rate,
-                               dt_bias, Q, K, V, dec, beta);
+        const auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(384), 0, s, P, conv_w, conv_b, neg_rate, dt_bias, Q, K, V, dec, beta);
+        };
+        if (audio) {
+            if (fast) go(gdn_prep_kernel<TT, true, true>);
+            else go(gdn_prep_kernel<TT, true, false>);
+        } else {
+            if (fast) go(gdn_prep_kernel<TT, false, true>);
+            else go(gdn_prep_kernel<TT, false, false>);
+        }
     });
 }
 void launch_delta(const float* Q, const float* K, const float* V, const float* dec, const float* beta, float* O,

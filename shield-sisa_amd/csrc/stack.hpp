@@ -294,7 +294,7 @@ public:
                 gr.gemm("gemm_seq", pi, gd.in_w, s);
                 pf.timed("gdn_prep", double(M) * (4.0 * 1548 * 4 + 4.0 * (2 * kD + kVD + 16)), s, [&] {
                     launch_gdn_prep(P, gd.conv_w, gd.conv_b, gd.neg_rate, gd.dt_bias, Q, K, V, dec, beta, B, s,
-                                    T, spec_.audio);
+                                    T, spec_.audio, !kF32);
                 });
                 check_launch();
                 pf.timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s, [&] {

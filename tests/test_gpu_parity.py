@@ -19,7 +19,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 FP32_TOL = 4e-4
-# half tiers: split-operand MFMA (fp32-level operand precision); measured max 3.7e-3 (fp16) on 64 clips
+# half tiers: split-operand MFMA (fp32-level operand precision); measured max 5.9e-3 (fp16), 3.9e-3 (bf16) on 64 clips
 FP16_TOL = 1e-2
 BF16_TOL = 1e-2
 CNN_STAGES = ["cnn%02d" % i for i in range(17)]
