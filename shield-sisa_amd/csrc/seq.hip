@@ -197,18 +197,30 @@ gdn_prep_kernel(const float* __restrict__ P, const float* __restrict__ cw, const
         }
         aq = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tree16_lane0(aq)), 48));
         ak = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tree16_lane0(ak)), 48));
+        // FAST (fp16 / bf16 tiers): the hardware reciprocal square root, exp2 and log2 (each within 1 ulp) in place
+        // of the correctly rounded division and device libm
         if constexpr (AUDIO) {   // SHIELD-A: x / max(|x|, 1e-12); q unscaled (engine/audio/sequence.cpp:136-143)
-            const float iq = 1.0f / fmaxf(sqrtf(aq), 1e-12f), ik = 1.0f / fmaxf(sqrtf(ak), 1e-12f);
+            const float iq = FAST ? __builtin_amdgcn_rsqf(fmaxf(aq, 1e-24f)) : 1.0f / fmaxf(sqrtf(aq), 1e-12f);
+            const float ik = FAST ? __builtin_amdgcn_rsqf(fmaxf(ak, 1e-24f)) : 1.0f / fmaxf(sqrtf(ak), 1e-12f);
             Q[row * kD + h * 64 + l] = q * iq;
             K[row * kD + h * 64 + l] = k * ik;
         } else {
-            const float iq = 1.0f / sqrtf(aq + 1e-6f), ik = 1.0f / sqrtf(ak + 1e-6f);
+            const float iq = FAST ? __builtin_amdgcn_rsqf(aq + 1e-6f) : 1.0f / sqrtf(aq + 1e-6f);
+            const float ik = FAST ? __builtin_amdgcn_rsqf(ak + 1e-6f) : 1.0f / sqrtf(ak + 1e-6f);
             Q[row * kD + h * 64 + l] = (q * iq) * 0.125f;
             K[row * kD + h * 64 + l] = k * ik;
         }
         if (l == 0) {
-            dec[row * 8 + h] = expf(neg_rate[h] * softplus_f(ga + dt_bias[h]));
-            beta[row * 8 + h] = 1.0f / (1.0f + expf(-gb));
+            if constexpr (FAST) {
+                constexpr float kLog2e = 1.44269504088896341f, kLn2 = 0.693147180559945309f;
+                const float x = ga + dt_bias[h];
+                const float sp = x > 20.0f ? x : __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(x * kLog2e)) * kLn2;
+                dec[row * 8 + h] = __builtin_amdgcn_exp2f((neg_rate[h] * sp) * kLog2e);
+                beta[row * 8 + h] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb * -kLog2e));
+            } else {
+                dec[row * 8 + h] = expf(neg_rate[h] * softplus_f(ga + dt_bias[h]));
+                beta[row * 8 + h] = 1.0f / (1.0f + expf(-gb));
+            }
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c)
