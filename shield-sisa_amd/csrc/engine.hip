@@ -175,7 +175,7 @@ public:
         const Slot& sl = slots_.at(size_t(slot));
         const int Fb = frame_bucket(F);
         run_graph(GraphKey{0, sl.d_frames, sl.d_tokens, Fb}, s,
-                  [&](hipStream_t q) { run_encode(sl.d_frames, Fb, sl.d_tokens, q, acts_); });
+                  [&](hipStream_t q) { encode_branched(sl.d_frames, Fb, sl.d_tokens, q); });
     }
     void classify_slot(int slot, int B, hipStream_t s) override {
         if (B <= 0) return;
@@ -189,30 +189,13 @@ public:
         if (F <= 0) return;
         if (F > cfg_.max_frames) throw std::runtime_error("encode: too many frames");
         run_graph(GraphKey{2, d_frames, d_tokens, F}, s,
-                  [&](hipStream_t q) { run_encode(d_frames, F, d_tokens, q, acts_); });
+                  [&](hipStream_t q) { encode_branched(d_frames, F, d_tokens, q); });
     }
     void forward_direct(const uint8_t* d_frames, int n, float* d_logits, hipStream_t s) override {
         if (n <= 0) return;
         if (n > cfg_.max_windows || n * kFrames > cfg_.max_frames) throw std::runtime_error("forward: too many clips");
         run_graph(GraphKey{3, d_frames, d_logits, n}, s, [&](hipStream_t q) {
-            // CNN branches of at least kBranchClips clips (one when dumping: the dumps show frame 0 / window 0), run
-            // one after another on q while profiling, so each kernel is timed alone at the shapes the forward gives it
-            const int nb = dump_dir_.empty() ? std::max(1, std::min(kBranches, n / kBranchClips)) : 1;
-            const bool fork = nb > 1 && !profiling();
-            if (fork) SHV_HIP_CHECK(hipEventRecord(fork_, q));
-            for (int b = 0; b < nb; ++b) {
-                const int c0 = int((long long)n * b / nb), c1 = int((long long)n * (b + 1) / nb);
-                hipStream_t bs = q;
-                if (fork) {
-                    bs = bstream_[b];
-                    SHV_HIP_CHECK(hipStreamWaitEvent(bs, fork_, 0));
-                }
-                run_encode(d_frames + size_t(c0) * kFrames * kFrameBytes, (c1 - c0) * kFrames,
-                           tok_direct_ + size_t(c0) * kFrames * kTokenFloats, bs, acts_at(c0 * kFrames));
-                if (fork) SHV_HIP_CHECK(hipEventRecord(join_[b], bs));
-            }
-            if (fork)
-                for (int b = 0; b < nb; ++b) SHV_HIP_CHECK(hipStreamWaitEvent(q, join_[b], 0));
+            encode_branched(d_frames, n * kFrames, tok_direct_, q);
             run_classify(tokptr_direct_, n, d_logits, q, 0);
         });
     }
@@ -354,8 +337,8 @@ private:
         return a;
     }
     bool fused_ = false;
-    // forward_direct encodes its clips' frames as up to kBranches independent branches on their own streams (forked
-    // from and joined to the caller's stream, inside one graph): while one branch's latency-bound kernels and launch
+    // Every encode (forward_direct, encode_direct, the scheduler's encode_slot) runs its frames as up to kBranches
+    // independent branches on their own streams (forked from and joined to the caller's stream, inside one graph): while one branch's latency-bound kernels and launch
     // tails run, another's fill the device (measured 21.2 -> 20.2 ms per 128 clips).  The sequence stages then run
     // once over all windows, where their GEMMs are most efficient (the same branching of the sequence gained another
     // 0.4 ms but ran its GEMMs at 0.7x their full-batch efficiency).  Frames and windows are independent rows, so the
@@ -458,6 +441,28 @@ private:
     void gemm32(const char* role, const GemmArgs& p, hipStream_t s) { GemmRunner<G>{*this}.gemm32(role, p, s); }
 
     // ---------------------------------------------------------------- CNN
+    // F frames as up to kBranches branches of at least kBranchClips clips' frames on the branch streams, forked from
+    // and joined to q (one branch when dumping: the dumps show frame 0); one after another on q while profiling, so
+    // each kernel is timed alone at the shapes the forward gives it
+    void encode_branched(const uint8_t* frames, int F, float* tokens, hipStream_t q) {
+        const int nb = dump_dir_.empty() ? std::max(1, std::min(kBranches, F / (kBranchClips * kFrames))) : 1;
+        const bool fork = nb > 1 && !profiling();
+        if (fork) SHV_HIP_CHECK(hipEventRecord(fork_, q));
+        for (int b = 0; b < nb; ++b) {
+            const int f0 = int((long long)F * b / nb), f1 = int((long long)F * (b + 1) / nb);
+            hipStream_t bs = q;
+            if (fork) {
+                bs = bstream_[b];
+                SHV_HIP_CHECK(hipStreamWaitEvent(bs, fork_, 0));
+            }
+            run_encode(frames + size_t(f0) * kFrameBytes, f1 - f0, tokens + size_t(f0) * kTokenFloats, bs,
+                       acts_at(f0));
+            if (fork) SHV_HIP_CHECK(hipEventRecord(join_[b], bs));
+        }
+        if (fork)
+            for (int b = 0; b < nb; ++b) SHV_HIP_CHECK(hipStreamWaitEvent(q, join_[b], 0));
+    }
+
     void run_encode(const uint8_t* frames, int F, float* tokens, hipStream_t s, const Acts& a) {
         if constexpr (!kF32) {
             if (fused_) {
