@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(256) pool_kernel(const T* __restrict__ in, T* 
 // ------------------------------------------------------------------------------------------------ repack
 template <typename T>
 __global__ void __launch_bounds__(256)
-repack_kernel(const float* __restrict__ src, T* __restrict__ dst, int N, int K, int perm, int parts) {
+repack_kernel(const float* __restrict__ src, T* __restrict__ dst, int N, int K, int perm, int parts, int group_major) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long long)N * K) return;
     const int r = int(idx / K), k = int(idx % K);
@@ -177,9 +177,10 @@ repack_kernel(const float* __restrict__ src, T* __restrict__ dst, int N, int K, 
         sr = ((panel & 1) ? F : 0) + (panel >> 1) * 16 + l;
     }
     float rest = src[(long long)sr * K + k];
+    const long long o = group_major ? (long long)(k >> 5) * N * 32 + r * 32 + (k & 31) : idx;
     for (int q = 0; q < parts; ++q) {   // part q = T(rounding residual left by parts 0..q-1)
         const T v = from_f<T>(rest);
-        dst[(long long)q * N * K + idx] = v;
+        dst[(long long)q * N * K + o] = v;
         rest = rest - to_f(v);
     }
 }
@@ -238,9 +239,11 @@ template <typename T> void launch_pool(const T* in, T* out, int F, hipStream_t s
     hipLaunchKernelGGL(pool_kernel<T>, dim3(cdiv((long long)F * 16 * 120, 256)), dim3(256), 0, s, in, out, F);
 }
 
-template <typename T> void launch_repack(const float* src, T* dst, int N, int K, int perm, int parts, hipStream_t s) {
+template <typename T>
+void launch_repack(const float* src, T* dst, int N, int K, int perm, int parts, hipStream_t s, bool group_major) {
+    if (group_major && K % 32) throw std::runtime_error("repack: the group-major layout needs K % 32 == 0");
     hipLaunchKernelGGL(repack_kernel<T>, dim3(cdiv((long long)N * K, 256)), dim3(256), 0, s, src, dst, N, K, perm,
-                       parts);
+                       parts, int(group_major));
 }
 
 template void launch_stem<float>(const uint8_t*, float*, const float*, const float*, const float*, int, hipStream_t);
@@ -248,8 +251,8 @@ template void launch_dw<float>(const float*, float*, const float*, const float*,
                                int, hipStream_t);
 template void launch_se_pool<float>(const float*, float*, int, int, int, int, hipStream_t);
 template void launch_pool<float>(const float*, float*, int, hipStream_t);
-template void launch_repack<float>(const float*, float*, int, int, int, int, hipStream_t);
-template void launch_repack<f16>(const float*, f16*, int, int, int, int, hipStream_t);
-template void launch_repack<bf16>(const float*, bf16*, int, int, int, int, hipStream_t);
+template void launch_repack<float>(const float*, float*, int, int, int, int, hipStream_t, bool);
+template void launch_repack<f16>(const float*, f16*, int, int, int, int, hipStream_t, bool);
+template void launch_repack<bf16>(const float*, bf16*, int, int, int, int, hipStream_t, bool);
 
 }  // namespace shv

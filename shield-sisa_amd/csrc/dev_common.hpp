@@ -47,6 +47,14 @@ __device__ __forceinline__ float silu_fast(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
 }
 __device__ __forceinline__ float relu(float x) { return x > 0.0f ? x : 0.0f; }
+
+// Element (row, col) of one part of a pre-split GEMM operand: 32-column groups kstride elements apart, rows ld
+// elements apart inside a group.  kstride 32 with ld >= the column count is plain row-major; ld 32 with
+// kstride >= rows * 32 is the group-major layout, where the 16 rows x 32 columns of an MFMA fragment block are
+// 1 KB of contiguous memory.
+__device__ __forceinline__ long long presplit_idx(long long row, int col, long long ld, long long kstride) {
+    return (long long)(col >> 5) * kstride + row * ld + (col & 31);
+}
 // relu for the fp16 / bf16 tiers as one integer max on the bit pattern: every negative float (-0 included) is a
 // negative int and becomes +0, every positive one stays.  Equal to relu() for all inputs but +NaN, which it passes
 // on instead of mapping to 0 (the tiers' certification rejects non-finite output).  relu() costs a second op

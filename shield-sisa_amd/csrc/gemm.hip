@@ -67,7 +67,8 @@ __device__ __forceinline__ void swiglu_store(const GemmArgs& p, long long m, int
         T part[Split<T>::P];
         Split<T>::split(v, part);
 #pragma unroll
-        for (int q = 0; q < Split<T>::P; ++q) static_cast<T*>(p.Ch)[q * p.cstride + m * p.ldc + col] = part[q];
+        for (int q = 0; q < Split<T>::P; ++q)
+            static_cast<T*>(p.Ch)[q * p.cstride + presplit_idx(m, col, p.ldc, p.ckstride)] = part[q];
     } else {
         p.C[m * p.ldc + col] = v;
     }
@@ -399,7 +400,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p, int mblocks, 
                 const bool in = i < A8 && gm < p.M && kk < p.K;
 #pragma unroll
                 for (int q = 0; q < P; ++q)
-                    rah[k][q] = in ? *reinterpret_cast<const uint4*>(Ah + q * p.astride + gm * p.lda + kk)
+                    rah[k][q] = in ? *reinterpret_cast<const uint4*>(Ah + q * p.astride + presplit_idx(gm, kk, p.lda, p.akstride))
                                    : make_uint4(0u, 0u, 0u, 0u);
             }
         }
@@ -427,7 +428,9 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p, int mblocks, 
             const bool in = i < W8 && gn < p.N && kk < p.K;
 #pragma unroll
             for (int q = 0; q < P; ++q)
-                rw[k][q] = in ? *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)gn * p.ldw + kk)
+                rw[k][q] = in ? *reinterpret_cast<const uint4*>(
+                                    W + q * p.wstride +
+                                    (AH ? presplit_idx(gn, kk, p.ldw, p.wkstride) : (long long)gn * p.ldw + kk))
                               : make_uint4(0u, 0u, 0u, 0u);
         }
     };
@@ -590,9 +593,11 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
     const T* W = static_cast<const T*>(p.W);
     const int nk = p.K / 32;
 
-    // this lane's source rows of the wave's DPW loads (rows clamped into range; K chunk swizzled)
+    // this lane's source rows of the wave's DPW loads (rows clamped into range; K chunk swizzled), at the first K
+    // step; each K step advances a load by its operand's 32-column group stride
     const int drow = lane >> 2, dchunk = (lane & 3) ^ dma_swz(drow);
     const T* src[DPW];
+    long long kst[DPW];
     int boff[DPW];
 #pragma unroll
     for (int j = 0; j < DPW; ++j) {
@@ -602,16 +607,18 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
             const int q = jj / AB, blk = jj % AB;
             const long long row = min(m0 + blk * 16 + drow, (long long)p.M - 1);
             src[j] = Ah + q * p.astride + row * p.lda + dchunk * 8;
+            kst[j] = p.akstride;
         } else {
             const int q = (jj - P * AB) / WB, blk = (jj - P * AB) % WB;
             const int n = min(n0 + blk * 16 + drow, p.N - 1);
             src[j] = W + q * p.wstride + (long long)n * p.ldw + dchunk * 8;
+            kst[j] = p.wkstride;
         }
     }
     auto issue = [&](int ks) {
         unsigned char* st = ring + (ks % NS) * D::STAGE;
 #pragma unroll
-        for (int j = 0; j < DPW; ++j) dma16(src[j] + ks * 32, st + boff[j]);
+        for (int j = 0; j < DPW; ++j) dma16(src[j] + ks * kst[j], st + boff[j]);
     };
     // fragment reads: lane (r, g) takes chunk g of row r of a block, stored at lane slot 4 r + (g ^ dma_swz(r))
     const int foff = 16 * (4 * r + (g ^ dma_swz(r)));
@@ -753,11 +760,16 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
     uint4 xh[AH ? SM_D : 1][P];
     uint4 wv[SM_D][SM_NT][P];
     const T* Ah = static_cast<const T*>(p.Ah);
+    // The K chunk kc of step st lies st * kstride + (kc - 32 st) past an operand row: kc - 32 st is the lane's chunk
+    // g * 8 in the group, or (row-major, last step of a K not a multiple of 32) the clamp back to K - 8, where
+    // kstride is 32.  Pre-split A comes with the sequence GEMMs' layouts; otherwise W is row-major.
     auto load = [&](int slot, int st) {
         const int kc = min(st * 32 + g * 8, p.K - 8);
+        const long long wk = AH ? (long long)st * p.wkstride + (kc - st * 32) : kc;
         if constexpr (AH) {
+            const T* a = Ah + rc * p.lda + (long long)st * p.akstride + (kc - st * 32);
 #pragma unroll
-            for (int q = 0; q < P; ++q) xh[slot][q] = *reinterpret_cast<const uint4*>(Ah + q * p.astride + rc * p.lda + kc);
+            for (int q = 0; q < P; ++q) xh[slot][q] = *reinterpret_cast<const uint4*>(a + q * p.astride);
         } else {
             load8(p.A + rc * p.lda + kc, xa[slot]);
         }
@@ -767,7 +779,7 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
             const int col = min(nbase + nt * 16 + r, p.N - 1);
 #pragma unroll
             for (int q = 0; q < P; ++q)
-                wv[slot][nt][q] = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)col * p.ldw + kc);
+                wv[slot][nt][q] = *reinterpret_cast<const uint4*>(W + q * p.wstride + (long long)col * p.ldw + wk);
         }
     };
 #pragma unroll
@@ -831,6 +843,7 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
 }
 
 template <typename T> void launch_small(const GemmArgs& p, hipStream_t s) {
+    if (!p.Ah && p.wkstride != 32) throw std::runtime_error("gemm_small: group-major W comes with pre-split A");
     const dim3 grid(cdiv(p.M, 16), cdiv(p.N, SM_NT * 16));
     if (p.Ah) hipLaunchKernelGGL((gemm_small_kernel<T, false, true>), grid, dim3(64), 0, s, p);
     else if (p.scale) hipLaunchKernelGGL((gemm_small_kernel<T, true, false>), grid, dim3(64), 0, s, p);
@@ -1062,6 +1075,7 @@ static bool gemm_dma_enabled() { return std::getenv("SHV_HIP_NO_GEMM_DMA") == nu
 
 template <typename T, int WM, int WN, int WGM, int WGN>
 void launch_lds(const GemmArgs& p, hipStream_t s) {
+    if (!p.Ah && p.wkstride != 32) throw std::runtime_error("gemm_lds: group-major W comes with pre-split A");
     const int mblocks = (int)cdiv(p.M, 16LL * WM * WGM), nblocks = (int)cdiv(p.N, 16 * WN * WGN);
     const long long blocks = (long long)cdiv(mblocks, XCDS) * XCDS * nblocks;
     if (blocks >= (1ll << 31)) throw std::runtime_error("gemm_lds: grid too large");
@@ -1107,6 +1121,8 @@ template <typename T> GemmPlan plan_gemm(const GemmArgs& p) {
 
 template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
     const GemmPlan pl = plan_gemm<T>(p);
+    if ((pl.kind == GemmPlan::Stream || pl.kind == GemmPlan::Direct) && p.wkstride != 32)
+        throw std::runtime_error("gemm: the streaming and direct kernels take a row-major W");
     switch (pl.kind) {
     case GemmPlan::Small: launch_small<T>(p, s); return;
     case GemmPlan::Dma: launch_dma<T>(p, s); return;
@@ -1215,23 +1231,44 @@ __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict_
     }
 }
 
+// One past the last element of a rows x cols part in GemmArgs' operand layout (row stride ld, 32-column group
+// stride kstride).
+long long presplit_span(long long rows, int cols, long long ld, long long kstride) {
+    return (long long)((cols - 1) >> 5) * kstride + (rows - 1) * ld + ((cols - 1) & 31) + 1;
+}
+// 16-byte aligned rows and groups, and no two elements at one address: row-major (kstride 32, ld >= cols) or
+// group-major (cols % 32 == 0, ld >= 32, a group's rows before the next group)
+bool presplit_layout_ok(long long rows, int cols, long long ld, long long kstride) {
+    if (ld % 8 || kstride % 8) return false;
+    if (kstride == 32) return ld >= cols;
+    return cols % 32 == 0 && ld >= 32 && kstride >= (rows - 1) * ld + 32;
+}
+bool row_major_operands(const GemmArgs& p) { return p.wkstride == 32 && p.akstride == 32 && p.ckstride == 32; }
+
 void check_args(const GemmArgs& p, bool mfma) {
     if (p.M <= 0 || p.N <= 0 || p.K <= 0) throw std::runtime_error("gemm: empty shape");
     if (!(p.A || p.Ah) || !p.W || !(p.C || p.Ch)) throw std::runtime_error("gemm: null operand");
     if ((p.Ah || p.Ch) && !mfma) throw std::runtime_error("gemm_f32: pre-split operands are for the MFMA tiers");
-    if (p.Ah && (p.A || p.scale || p.astride < (long long)(p.M - 1) * p.lda + p.K))
-        throw std::runtime_error("gemm: pre-split A takes no fp32 A or SE scale and needs a part stride");
-    if (p.Ch && (p.C || !p.swiglu || p.cstride < (long long)(p.M - 1) * p.ldc + p.N / 2))
-        throw std::runtime_error("gemm: a pre-split output is a SwiGLU output with a part stride");
+    if (!mfma && !row_major_operands(p)) throw std::runtime_error("gemm_f32: row-major operands only");
+    if ((!p.Ah && p.akstride != 32) || (!p.Ch && p.ckstride != 32))
+        throw std::runtime_error("gemm: fp32 A and C are row-major");
+    if (p.Ah && (p.A || p.scale || !presplit_layout_ok(p.M, p.K, p.lda, p.akstride) ||
+                 p.astride < presplit_span(p.M, p.K, p.lda, p.akstride)))
+        throw std::runtime_error("gemm: pre-split A takes no fp32 A or SE scale and needs a valid layout and part stride");
+    if (p.Ch && (p.C || !p.swiglu || !presplit_layout_ok(p.M, p.N / 2, p.ldc, p.ckstride) ||
+                 p.cstride < presplit_span(p.M, p.N / 2, p.ldc, p.ckstride)))
+        throw std::runtime_error("gemm: a pre-split output is a SwiGLU output with a valid layout and part stride");
     if (p.res && !p.R) throw std::runtime_error("gemm: residual without R");
     if (p.res < 0 || p.res > 3) throw std::runtime_error("gemm: unknown residual mode");
     if (p.scale && (p.scale_rows <= 0 || p.ld_scale < p.K)) throw std::runtime_error("gemm: bad SE scale");
     if (mfma) {
         // 32-byte A and 16-byte W fragments: K, lda, ldw, ld_scale multiples of 8 elements
-        if (p.K % 8 || p.lda % 8 || p.ldw % 8 || p.lda < p.K || p.ldw < p.K || (p.scale && p.ld_scale % 8))
+        if (p.K % 8 || p.lda % 8 || p.ldw % 8 || (!p.Ah && p.lda < p.K) || (p.scale && p.ld_scale % 8) ||
+            !presplit_layout_ok(p.N, p.K, p.ldw, p.wkstride))
             throw std::runtime_error("gemm_mfma: K/lda/ldw must be multiples of 8 (K=" + std::to_string(p.K) + ")");
         if (p.swiglu && (p.N % 32)) throw std::runtime_error("gemm_mfma: swiglu needs N % 32 == 0");
-        if (p.wstride < (long long)p.N * p.ldw) throw std::runtime_error("gemm_mfma: bad weight part stride");
+        if (p.wstride < presplit_span(p.N, p.K, p.ldw, p.wkstride))
+            throw std::runtime_error("gemm_mfma: bad weight part stride");
     } else {
         if (p.lda < p.K || p.ldw < p.K) throw std::runtime_error("gemm_f32: bad leading dimension");
         if (p.swiglu && (p.N % 2)) throw std::runtime_error("gemm_f32: swiglu needs even N");
@@ -1309,6 +1346,8 @@ template <typename T> void gemm_mfma_variant(const GemmArgs& p, hipStream_t s, i
     check_args(p, true);
     if (variant >= 2 && variant <= 6 && (p.Ah || p.Ch || p.swiglu))
         throw std::runtime_error("gemm: the direct kernel takes fp32 A and C and no SwiGLU");
+    if (((variant >= 2 && variant <= 6) || variant == 8) && p.wkstride != 32)
+        throw std::runtime_error("gemm: the streaming and direct kernels take a row-major W");
     switch (variant) {
     case 0: launch_gemm<T>(p, s); return;
     case 1: launch_small<T>(p, s); return;

@@ -30,11 +30,16 @@ struct GemmArgs {
     float* C = nullptr; long long ldc = 0;
     const float* R = nullptr; long long ldr = 0; int res = 0;
     int swiglu = 0;
-    // MFMA tiers: A given pre-split (parts [P][..][lda] of the tier's type, part stride astride elements) instead of
-    // fp32 A; and a SwiGLU output written pre-split (parts [P][..][ldc], part stride cstride) instead of fp32 C.  The
-    // split is a function of each fp32 value, so both give results bitwise equal to the fp32 forms.
+    // MFMA tiers: A given pre-split (parts of the tier's type, part stride astride elements) instead of fp32 A; and a
+    // SwiGLU output written pre-split (parts, part stride cstride) instead of fp32 C.  The split is a function of each
+    // fp32 value, so both give results bitwise equal to the fp32 forms.
     const void* Ah = nullptr; long long astride = 0;
     void* Ch = nullptr; long long cstride = 0;
+    // Layout of each part of the pre-split operands (W, Ah, Ch): element (row, col) at (col / 32) * kstride +
+    // row * ld + col % 32 (ld = ldw, lda, ldc).  32 (the default) is plain row-major; group-major operands (ld 32,
+    // kstride >= rows * 32: each 16 x 32 fragment block 1 KB contiguous) are read by the small-M, LDS-staged and
+    // direct-to-LDS kernels (the sequence GEMMs); the other kernels take the default only.
+    long long wkstride = 32, akstride = 32, ckstride = 32;
 };
 
 // fp32 tier: VALU GEMM, each output accumulated in K blocks of 64 (fma chain from +0 per block, block sums added
@@ -75,8 +80,10 @@ template <typename T> void launch_se_pool(const T* x, float* pooled, int F, int 
 template <typename T> void launch_pool(const T* in, T* out, int F, hipStream_t s);
 // weight repack on the GPU: part q of dst (q < parts, N*K elements apart) holds the q-th rounding residual of
 // src[perm(r)][k] in T (T = float: the value itself).  perm 0 identity, 1 SwiGLU pair interleave (rows 2j, 2j+1
-// <- gate j, up j of src = [gate; up]), 2 SwiGLU 16-row panel interleave.
-template <typename T> void launch_repack(const float* src, T* dst, int N, int K, int perm, int parts, hipStream_t s);
+// <- gate j, up j of src = [gate; up]), 2 SwiGLU 16-row panel interleave.  Each part row-major [N][K], or with
+// group_major (K % 32 == 0) in GemmArgs' group-major layout: (r, k) at (k / 32) * N * 32 + r * 32 + k % 32.
+template <typename T>
+void launch_repack(const float* src, T* dst, int N, int K, int perm, int parts, hipStream_t s, bool group_major = false);
 
 // padded repack: dst part q is [Np][Kp] (zero outside [N][K]) holding the q-th rounding residual of src [N][K]
 template <typename T>
@@ -144,10 +151,11 @@ void launch_assemble(const float* const* tok_ptrs, const float* pos, const float
 // h [B*126][384]
 void launch_assemble_audio(const float* tokens, long long ldw, const float* readout, float* h, int B, hipStream_t s);
 // out[r] = (x[r] * (1 / sqrt(sum(x^2) / 384 + 1e-6))) * w with the reference's 16-lane sum tree.  T = f16 / bf16:
-// out holds the split parts of each value (part stride pstride elements), the pre-split A of the next GEMM.
+// out holds the split parts of each value (part stride pstride elements), the pre-split A of the next GEMM, value
+// (r, c) of a part at (c / 32) * kstride + r * ldo + c % 32 (GemmArgs' operand layout).
 template <typename T>
 void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s,
-                    long long pstride = 0);
+                    long long pstride = 0, long long kstride = 32);
 // Every sequence kernel takes the window length T: 321 (SHIELD-V) or 126 (SHIELD-A); others throw.
 // short conv4 + SiLU on q|k|v, per-head L2 norm, decay = exp(neg_rate * softplus(a + dt_bias)), beta = sigmoid(b).
 // P [rows][2320] -> Q, K [rows][384], V [rows][768], dec, beta [rows][8].  Video: q * (1/sqrt(max(ss,1e-6))) * 0.125;
@@ -168,11 +176,11 @@ template <typename T>
 void launch_delta_chunked(const float* Q, const float* K, const float* V, const float* dec, const float* beta,
                           float* O, float* work, int B, hipStream_t s, int Tw = kT);
 // ((o * rstd) * w) * silu(gate) per (row, head) -> T [rows][768] (T = f16 / bf16: split parts, as launch_rmsnorm,
-// with silu_fast).
+// with silu_fast; row stride ld, 32-column group stride kstride).
 // audio: o * 0.125 first and eps 1e-5 (engine/audio/sequence.cpp:160-171); video eps 1e-6
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,
-                       long long pstride = 0, bool audio = false);
+                       long long pstride = 0, bool audio = false, long long ld = kVD, long long kstride = 32);
 // SISA last-row attention per (window, head): S [rows][1072] (B rotated in place), QC [B][576] -> Y [B][384]
 void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s, int T = kT);
 // final RMSNorm + Linear(384,128) + activation + Linear(128,1); w0 [128][384]; activation SiLU (video) or

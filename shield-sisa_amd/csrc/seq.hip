@@ -65,7 +65,7 @@ assemble_audio_kernel(const float* __restrict__ tokens, long long ldw, const flo
 template <typename T>
 __global__ void __launch_bounds__(256)
 rmsnorm_kernel(const float* __restrict__ x, long long ldx, const float* __restrict__ w, T* __restrict__ out,
-               long long ldo, long long pstride, int rows) {
+               long long ldo, long long pstride, long long kstride, int rows) {
     const long long row = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
     const int l = threadIdx.x & 15;
     const bool live = row < rows;
@@ -80,7 +80,8 @@ rmsnorm_kernel(const float* __restrict__ x, long long ldx, const float* __restri
     if (!live) return;
     const float inv = 1.0f / sqrtf(s / 384.0f + 1e-6f);
 #pragma unroll
-    for (int i = 0; i < 24; ++i) put_value(out, pstride, row * ldo + i * 16 + l, (v[i] * inv) * w[i * 16 + l]);
+    for (int i = 0; i < 24; ++i)
+        put_value(out, pstride, presplit_idx(row, i * 16 + l, ldo, kstride), (v[i] * inv) * w[i * 16 + l]);
 }
 
 // Row 3 (lanes 48 + l): the values of lanes l, l + 16, l + 32 (rows 0, 1, 2), moved up by row swaps.  Only the
@@ -922,16 +923,20 @@ delta_chunk_scan_kernel(const float* __restrict__ Q, const float* __restrict__ K
 
 // ------------------------------------------------------------------------------------------------ gated norm
 // 16 lanes per (row, head): lane l accumulates o[l + 16 z]^2 (z = 0..7), tree16, then ((o * rstd) * w) * silu(g).
+// A wave takes one head of four consecutive rows, so that its stores of a group-major output fill whole 64-byte
+// row pieces of four adjacent rows.
 // AUDIO: SHIELD-A scales o by 0.125 first and uses eps 1e-5 (engine/audio/sequence.cpp:196-201).
 template <typename T, bool AUDIO>
 __global__ void __launch_bounds__(256)
 gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, const float* __restrict__ w,
-                  T* __restrict__ out, long long pstride, int rows) {
+                  T* __restrict__ out, long long pstride, long long ld, long long kstride, int rows) {
     const long long grp = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
     const int l = threadIdx.x & 15;
-    const bool live = grp < (long long)rows * kHeads;
-    const long long row = live ? grp / kHeads : 0;
-    const int h = int(grp % kHeads);
+    const long long quad = grp >> 2;   // (four-row block, head)
+    const int h = int(quad % kHeads);
+    const long long r = (quad / kHeads) * 4 + (grp & 3);
+    const bool live = r < rows;
+    const long long row = live ? r : 0;
     const float* o = O + row * kVD + h * 128;
     float v[8];
 #pragma unroll
@@ -947,7 +952,7 @@ gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, cons
     for (int z = 0; z < 8; ++z) {
         const int i = z * 16 + l;
         const float sg = std::is_same<T, float>::value ? silu(g[i]) : silu_fast(g[i]);
-        put_value(out, pstride, row * kVD + h * 128 + i, ((v[z] * rstd) * w[i]) * sg);
+        put_value(out, pstride, presplit_idx(row, h * 128 + i, ld, kstride), ((v[z] * rstd) * w[i]) * sg);
     }
 }
 
@@ -1124,9 +1129,9 @@ void launch_assemble_audio(const float* tokens, long long ldw, const float* read
 }
 template <typename T>
 void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s,
-                    long long pstride) {
+                    long long pstride, long long kstride) {
     hipLaunchKernelGGL(rmsnorm_kernel<T>, dim3(cdiv((long long)rows * 16, 256)), dim3(256), 0, s, x, ldx, w, out, ldo,
-                       pstride, rows);
+                       pstride, kstride, rows);
 }
 // The kernels are instantiated for SHIELD-V's windows (321 tokens) and SHIELD-A's (126): f(integral_constant<TT>).
 template <class F> void for_window(int T, F&& f) {
@@ -1203,12 +1208,14 @@ template void launch_delta_chunked<bf16>(const float*, const float*, const float
                                          float*, float*, int, hipStream_t, int);
 template <typename T>
 void launch_gated_norm(const float* O, const float* P, const float* w, T* out, int rows, hipStream_t s,
-                       long long pstride, bool audio) {
-    const dim3 grid(cdiv((long long)rows * kHeads * 16, 256));
+                       long long pstride, bool audio, long long ld, long long kstride) {
+    const dim3 grid(cdiv((long long)cdiv(rows, 4) * 4 * kHeads * 16, 256));
     if (audio)
-        hipLaunchKernelGGL((gated_norm_kernel<T, true>), grid, dim3(256), 0, s, O, P, w, out, pstride, rows);
+        hipLaunchKernelGGL((gated_norm_kernel<T, true>), grid, dim3(256), 0, s, O, P, w, out, pstride, ld, kstride,
+                           rows);
     else
-        hipLaunchKernelGGL((gated_norm_kernel<T, false>), grid, dim3(256), 0, s, O, P, w, out, pstride, rows);
+        hipLaunchKernelGGL((gated_norm_kernel<T, false>), grid, dim3(256), 0, s, O, P, w, out, pstride, ld, kstride,
+                           rows);
 }
 void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, hipStream_t s, int T) {
     for_window(T, [&](auto tt) {
@@ -1274,9 +1281,9 @@ void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const f
 
 #define SHV_NORMS(T)                                                                                             \
     template void launch_rmsnorm<T>(const float*, long long, const float*, T*, long long, int, hipStream_t,      \
-                                    long long);                                                                  \
+                                    long long, long long);                                                       \
     template void launch_gated_norm<T>(const float*, const float*, const float*, T*, int, hipStream_t, long long,  \
-                                       bool);
+                                       bool, long long, long long);
 SHV_NORMS(float)
 SHV_NORMS(f16)
 SHV_NORMS(bf16)

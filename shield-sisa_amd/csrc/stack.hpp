@@ -28,10 +28,12 @@ inline double gemm_bytes(long long M, int N, int K, int ta, int tw, int tc, int 
     return double(M) * K * ta + double(N) * K * tw + double(M) * N * tc + (tr ? double(M) * N * tr : 0.0);
 }
 
-// a GEMM weight on the device: `parts` arrays of N*K elements of the flavour's type, `stride` elements apart
+// a GEMM weight on the device: `parts` arrays of N*K elements of the flavour's type, `stride` elements apart; each
+// row-major [N][K] (ld 0: the caller's ldw), or group-major (ld 32, 32-column groups kstride = N * 32 apart)
 struct DevW {
     const void* w = nullptr;
     long long stride = 0;
+    long long ld = 0, kstride = 32;
 };
 
 // owner of device allocations
@@ -72,15 +74,22 @@ public:
         return d;
     }
     const float* up(const std::vector<float>& v) { return up(v.data(), v.size()); }
-    // fp32 [N][K] rows -> device parts of U with a row permutation, converted by the repack kernel on the GPU
-    template <typename U> DevW repack(const std::vector<float>& src, int N, int K, int perm) {
+    // fp32 [N][K] rows -> device parts of U with a row permutation, converted by the repack kernel on the GPU;
+    // group_major: parts in the group-major GEMM operand layout
+    template <typename U>
+    DevW repack(const std::vector<float>& src, int N, int K, int perm, bool group_major = false) {
         const int parts = weight_parts<U>();
         float* st = staging_.make<float>(src.size());
         SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
         U* d = wmem_.make<U>(size_t(parts) * N * K);
-        launch_repack<U>(st, d, N, K, perm, parts, s_);
+        launch_repack<U>(st, d, N, K, perm, parts, s_, group_major);
         check_launch();
-        return DevW{d, (long long)N * K};
+        DevW w{d, (long long)N * K};
+        if (group_major) {
+            w.ld = 32;
+            w.kstride = (long long)N * 32;
+        }
+        return w;
     }
     template <typename U> DevW repack_pad(const std::vector<float>& src, int N, int K, int Np, int Kp) {
         const int parts = weight_parts<U>();
@@ -141,6 +150,10 @@ template <typename G> struct GemmRunner {
     void gemm(const char* role, GemmArgs p, const DevW& w, hipStream_t s) const {
         p.W = w.w;
         p.wstride = w.stride;
+        if (w.ld) {
+            p.ldw = w.ld;
+            p.wkstride = w.kstride;
+        }
         const int abytes = (p.Ah && !kF32) ? int(sizeof(G)) * weight_parts<G>() : 4;
         const double bytes = gemm_bytes(p.M, p.N, p.K, abytes, kF32 ? 4 : int(sizeof(G)) * weight_parts<G>(),
                                         p.swiglu ? (p.Ch ? int(sizeof(G)) * weight_parts<G>() / 2 : 2) : 4,
@@ -188,14 +201,14 @@ public:
             d.neg_rate = up.up(gh.neg_rate, kHeads);
             d.dt_bias = up.up(gh.dt_bias, kHeads);
             d.o_norm_w = up.up(gh.o_norm_w);
-            d.in_w = up.repack<G>(gh.in.w, gh.in.N, gh.in.K, 0);
-            d.out_w = up.repack<G>(gh.out.w, gh.out.N, gh.out.K, 0);
-            d.up_w = up.repack<G>(Uploader::concat(gh.gate, gh.up), 2 * kFF, kD, swiglu_perm);
-            d.down_w = up.repack<G>(gh.down.w, gh.down.N, gh.down.K, 0);
+            d.in_w = up.repack<G>(gh.in.w, gh.in.N, gh.in.K, 0, !kF32);
+            d.out_w = up.repack<G>(gh.out.w, gh.out.N, gh.out.K, 0, !kF32);
+            d.up_w = up.repack<G>(Uploader::concat(gh.gate, gh.up), 2 * kFF, kD, swiglu_perm, !kF32);
+            d.down_w = up.repack<G>(gh.down.w, gh.down.N, gh.down.K, 0, !kF32);
         }
         s_attn_norm_ = up.up(S.attn_norm_w);
         s_ffn_norm_ = up.up(S.ffn_norm_w);
-        s_in_w_ = up.repack<G>(S.in.w, S.in.N, S.in.K, 0);
+        s_in_w_ = up.repack<G>(S.in.w, S.in.N, S.in.K, 0, !kF32);
         s_in_b_ = up.up(S.in.b);
         s_qc_w_ = up.up(Uploader::concat(S.q, S.c));   // [576][384]: W_Q rows then W_C rows
         s_o_w_ = up.up(S.o.w);
@@ -259,25 +272,31 @@ public:
             ON = this->ON_ + r0 * kVD;
             HID = this->HID_ + r0 * kFF;
         } else {
-            XNh = this->XNh_ + r0 * kD;
-            ONh = this->ONh_ + r0 * kVD;
-            HIDh = this->HIDh_ + r0 * kFF;
+            XNh = this->XNh_ + r0 * 32;
+            ONh = this->ONh_ + r0 * 32;
+            HIDh = this->HIDh_ + r0 * 32;
         }
         float *XL = this->XL_ + size_t(w0) * kD, *QC = this->QC_ + size_t(w0) * 576, *Y = this->Y_ + size_t(w0) * kD,
               *X1 = this->X1_ + size_t(w0) * kD, *X2 = this->X2_ + size_t(w0) * kD,
               *HIDL = this->HIDL_ + size_t(w0) * kFF;
-        // the A operand of a sequence GEMM: fp32 (exact tier) or the producer's split parts (MFMA tiers)
+        // the A operand of a sequence GEMM: fp32 (exact tier) or the producer's split parts (MFMA tiers, group-major)
         const auto set_a = [&](GemmArgs& p, const float* a32, const G* ah, int width) {
-            p.lda = width;
-            if constexpr (kF32) p.A = a32;
-            else { p.Ah = ah; p.astride = mrows_ * width; }
+            if constexpr (kF32) {
+                p.A = a32;
+                p.lda = width;
+            } else {
+                p.Ah = ah;
+                p.lda = 32;
+                p.akstride = mrows_ * 32;
+                p.astride = mrows_ * width;
+            }
             (void)a32; (void)ah;
         };
         // the residual stream's RMSNorm into the A operand of the next GEMM
         const auto rmsnorm_all = [&](const float* w) {
             pf.timed("rmsnorm", double(M) * kD * (4 + kAS), s, [&] {
                 if constexpr (kF32) launch_rmsnorm<float>(H, kD, w, XN, kD, M, s);
-                else launch_rmsnorm<G>(H, kD, w, XNh, kD, M, s, mrows_ * kD);
+                else launch_rmsnorm<G>(H, kD, w, XNh, 32, M, s, mrows_ * kD, mrows_ * 32);
             });
             check_launch();
         };
@@ -309,7 +328,7 @@ public:
                 check_launch();
                 pf.timed("gated_norm", double(M) * (4.0 * 2 * kVD + kAS * kVD), s, [&] {
                     if constexpr (kF32) launch_gated_norm<float>(O, P, gd.o_norm_w, ON, M, s, 0, spec_.audio);
-                    else launch_gated_norm<G>(O, P, gd.o_norm_w, ONh, M, s, mrows_ * kVD, spec_.audio);
+                    else launch_gated_norm<G>(O, P, gd.o_norm_w, ONh, M, s, mrows_ * kVD, spec_.audio, 32, mrows_ * 32);
                 });
                 check_launch();
                 GemmArgs po;
@@ -323,9 +342,16 @@ public:
             GemmArgs pu;
             pu.M = M; pu.N = 2 * kFF; pu.K = kD;
             set_a(pu, XN, XNh, kD); pu.ldw = kD;
-            pu.ldc = kFF; pu.swiglu = 1;
-            if constexpr (kF32) pu.C = HID;
-            else { pu.Ch = HIDh; pu.cstride = mrows_ * kFF; }
+            pu.swiglu = 1;
+            if constexpr (kF32) {
+                pu.C = HID;
+                pu.ldc = kFF;
+            } else {
+                pu.Ch = HIDh;
+                pu.ldc = 32;
+                pu.ckstride = mrows_ * 32;
+                pu.cstride = mrows_ * kFF;
+            }
             gr.gemm("gemm_seq", pu, gd.up_w, s);
             GemmArgs pd;
             pd.M = M; pd.N = kD; pd.K = kFF;
@@ -400,8 +426,11 @@ private:
     float* dwork_ = nullptr;     // half tiers: the chunked delta rule's per-chunk products
     bool delta_chunked_ = false;
     float *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;   // fp32 tier: the sequence GEMMs' A operands
-    G *XNh_ = nullptr, *ONh_ = nullptr, *HIDh_ = nullptr;    // MFMA tiers: the same, written pre-split by producers
-    long long mrows_ = 0;                                     // rows of those buffers (part stride = mrows_ * width)
+    // MFMA tiers: the same, written pre-split by their producers in the group-major layout (part q, 32-column group
+    // j, row r at q * mrows_ * width + j * mrows_ * 32 + r * 32), so that each DMA load of the direct-to-LDS GEMM
+    // reads a 16 x 32 fragment block as 1 KB of contiguous memory (the sequence weights are laid out the same way)
+    G *XNh_ = nullptr, *ONh_ = nullptr, *HIDh_ = nullptr;
+    long long mrows_ = 0;                                     // rows of those buffers
     float *XL_ = nullptr, *QC_ = nullptr, *Y_ = nullptr, *X1_ = nullptr, *X2_ = nullptr, *HIDL_ = nullptr;
 
 };
