@@ -962,6 +962,8 @@ gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, cons
 // 2. prefix sums in double, one thread per series, rounded to float per element
 // 3. rotate c (last token's angles) and each b_t; scores with the 16-lane dot structure
 // 4. softmax: max, expf, sum in double in token order (one thread); y_j = sum over 64-token blocks of fma chains
+// The order of every rounded operation is the reference's; only order-free work (the maximum, the exponentials,
+// the independent block chains, loads) runs in parallel.
 constexpr int SA_THREADS = 256;
 template <int TT>
 __global__ void __launch_bounds__(SA_THREADS)
@@ -971,8 +973,10 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
     float* S0 = S + (long long)b * TT * kSld;
     __shared__ float gt[TT], ft[TT], sco[TT];
     __shared__ float phi[TT][kPairs + 1];
+    constexpr int SA_NB = (TT + 63) / 64;   // 64-token blocks of the output sums
     __shared__ float sq[64], crot[32];
     __shared__ float s_inv;
+    __shared__ float yblk[SA_NB][64];
     for (int t = tid; t < TT; t += SA_THREADS) {
         const float* row = S0 + (long long)t * kSld;
         gt[t] = -softplus_f(row[kSal + h]);
@@ -983,16 +987,25 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
     if (tid < 64) sq[tid] = QC[(long long)b * 576 + h * 64 + tid];
     __syncthreads();
     if (tid < 2 + kPairs) {
+        // one series per thread, in token order; 32 tokens at a time go through registers so that the LDS loads
+        // of a block are in flight together and only the additions chain
+        float* series = tid == 0 ? gt : tid == 1 ? ft : &phi[0][tid - 2];
+        const int stride = tid < 2 ? 1 : kPairs + 1;
         double acc = 0.0;
-        float* series = tid == 0 ? gt : tid == 1 ? ft : nullptr;
-        for (int t = 0; t < TT; ++t) {
-            if (series) {
-                acc += double(series[t]);
-                series[t] = float(acc);
-            } else {
-                acc += double(phi[t][tid - 2]);
-                phi[t][tid - 2] = float(acc);
-            }
+        for (int t0 = 0; t0 < TT; t0 += 32) {
+            float x[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (t0 + i < TT) x[i] = series[(t0 + i) * stride];
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (t0 + i < TT) {
+                    acc += double(x[i]);
+                    x[i] = float(acc);
+                }
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (t0 + i < TT) series[(t0 + i) * stride] = x[i];
         }
     }
     __syncthreads();
@@ -1040,28 +1053,59 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
         sco[t] = score;
     }
     __syncthreads();
-    if (tid == 0) {
+    // softmax: the maximum (exact in any order; a NaN score is never selected, as in the sequential scan), the
+    // exponentials in parallel, their sum in double in token order by one thread
+    {
         float mx = -INFINITY;
-        for (int t = 0; t < TT; ++t) mx = sco[t] > mx ? sco[t] : mx;
+        for (int t = tid; t < TT; t += SA_THREADS) mx = sco[t] > mx ? sco[t] : mx;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float o = __shfl_xor(mx, off);
+            mx = o > mx ? o : mx;
+        }
+        if ((tid & 63) == 0) sq[tid >> 6] = mx;   // sq is free again: the scores are done
+        __syncthreads();
+        mx = sq[0];
+#pragma unroll
+        for (int w = 1; w < SA_THREADS / 64; ++w) mx = sq[w] > mx ? sq[w] : mx;
+        for (int t = tid; t < TT; t += SA_THREADS) sco[t] = expf(sco[t] - mx);
+    }
+    __syncthreads();
+    if (tid == 0) {
         double sum = 0.0;
-        for (int t = 0; t < TT; ++t) {
-            const float e = expf(sco[t] - mx);
-            sco[t] = e;
-            sum += double(e);
+        for (int t0 = 0; t0 < TT; t0 += 32) {
+            float x[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) x[i] = t0 + i < TT ? sco[t0 + i] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (t0 + i < TT) sum += double(x[i]);
         }
         s_inv = 1.0f / float(sum);
     }
     __syncthreads();
-    if (tid < 64) {
+    // y_j: the 64-token blocks' fma chains on the four waves (block x on wave x % 4, its 64 values loaded
+    // together), then added in block order
+    {
         const float inv = s_inv;
-        float tot = 0.0f;
-        for (int t0 = 0; t0 < TT; t0 += 64) {
+        const int j = tid & 63;
+        const float* col = S0 + kSv + h * 64 + j;
+        for (int x = tid >> 6; x < SA_NB; x += SA_THREADS / 64) {
+            const int t0 = x * 64;
+            float v[64];
+#pragma unroll
+            for (int i = 0; i < 64; ++i) v[i] = t0 + i < TT ? col[(long long)(t0 + i) * kSld] : 0.0f;
             float blk = 0.0f;
-            const int t1 = min(TT, t0 + 64);
-            for (int t = t0; t < t1; ++t)
-                blk = __builtin_fmaf(sco[t] * inv, S0[(long long)t * kSld + kSv + h * 64 + tid], blk);
-            tot = t0 == 0 ? blk : tot + blk;
+#pragma unroll
+            for (int i = 0; i < 64; ++i)
+                if (t0 + i < TT) blk = __builtin_fmaf(sco[t0 + i] * inv, v[i], blk);
+            yblk[x][j] = blk;
         }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float tot = yblk[0][tid];
+        for (int x = 1; x < SA_NB; ++x) tot = tot + yblk[x][tid];
         Y[(long long)b * kD + h * 64 + tid] = tot;
     }
 }
