@@ -194,10 +194,8 @@ public:
     void forward_direct(const uint8_t* d_frames, int n, float* d_logits, hipStream_t s) override {
         if (n <= 0) return;
         if (n > cfg_.max_windows || n * kFrames > cfg_.max_frames) throw std::runtime_error("forward: too many clips");
-        run_graph(GraphKey{3, d_frames, d_logits, n}, s, [&](hipStream_t q) {
-            encode_branched(d_frames, n * kFrames, tok_direct_, q);
-            run_classify(tokptr_direct_, n, d_logits, q, 0);
-        });
+        run_graph(GraphKey{3, d_frames, d_logits, n}, s,
+                  [&](hipStream_t q) { forward_branched(d_frames, n, d_logits, q); });
     }
 
 private:
@@ -337,12 +335,11 @@ private:
         return a;
     }
     bool fused_ = false;
-    // Every encode (forward_direct, encode_direct, the scheduler's encode_slot) runs its frames as up to kBranches
-    // independent branches on their own streams (forked from and joined to the caller's stream, inside one graph): while one branch's latency-bound kernels and launch
-    // tails run, another's fill the device (measured 21.2 -> 20.2 ms per 128 clips).  The sequence stages then run
-    // once over all windows, where their GEMMs are most efficient (the same branching of the sequence gained another
-    // 0.4 ms but ran its GEMMs at 0.7x their full-batch efficiency).  Frames and windows are independent rows, so the
-    // results are bitwise those of one pass.
+    // Every encode (encode_direct, the scheduler's encode_slot) runs its frames as up to kBranches independent
+    // branches on their own streams (forked from and joined to the caller's stream, inside one graph): while one
+    // branch's latency-bound kernels and launch tails run, another's fill the device (measured 21.2 -> 20.2 ms per
+    // 128 clips).  forward_direct also runs the sequence stages inside the branches (forward_branched).  Frames and
+    // windows are independent rows, so the results are bitwise those of one pass.
     static constexpr int kBranches = 4, kBranchClips = 32;
     hipStream_t bstream_[kBranches] = {};
     hipEvent_t fork_ = nullptr, join_[kBranches] = {};
@@ -444,6 +441,41 @@ private:
     // F frames as up to kBranches branches of at least kBranchClips clips' frames on the branch streams, forked from
     // and joined to q (one branch when dumping: the dumps show frame 0); one after another on q while profiling, so
     // each kernel is timed alone at the shapes the forward gives it
+    // n clips end to end as up to kBranches branches of whole clips (at least kBranchClips each).  Each pair of
+    // branches runs its clips' sequence stages on the second branch's stream once both have encoded, so those
+    // stages overlap the other pair's encoders instead of waiting for all four (windows are independent rows: the
+    // logits are bitwise those of one pass).  Measured per 128 clips: sequence after all branches 19.47 ms, per pair
+    // 19.15, per branch 19.07 -- the last ran the sequence GEMMs at 32 windows, 1.5x slower per row, so the pair
+    // is kept.
+    static constexpr int kSeqGroup = 2;
+    void forward_branched(const uint8_t* frames, int n, float* logits, hipStream_t q) {
+        const int nb = dump_dir_.empty() ? std::max(1, std::min(kBranches, n / kBranchClips)) : 1;
+        const bool fork = nb > 1 && !profiling();
+        const int sg = std::min(nb, kSeqGroup);
+        const auto clip = [&](int b) { return int((long long)n * b / nb); };
+        if (fork) SHV_HIP_CHECK(hipEventRecord(fork_, q));
+        for (int b = 0; b < nb; ++b) {
+            const int c0 = clip(b), c1 = clip(b + 1);
+            hipStream_t bs = q;
+            if (fork) {
+                bs = bstream_[b];
+                SHV_HIP_CHECK(hipStreamWaitEvent(bs, fork_, 0));
+            }
+            const int f0 = c0 * kFrames;
+            run_encode(frames + size_t(f0) * kFrameBytes, (c1 - c0) * kFrames, tok_direct_ + size_t(f0) * kTokenFloats,
+                       bs, acts_at(f0));
+            if ((b + 1) % sg == 0 || b == nb - 1) {
+                const int g0 = b - b % sg;
+                if (fork)
+                    for (int bb = g0; bb < b; ++bb) SHV_HIP_CHECK(hipStreamWaitEvent(bs, join_[bb], 0));
+                const int w0 = clip(g0);
+                run_classify(tokptr_direct_ + size_t(w0) * kFrames, c1 - w0, logits + w0, bs, w0);
+            }
+            if (fork) SHV_HIP_CHECK(hipEventRecord(join_[b], bs));
+        }
+        if (fork)
+            for (int b = 0; b < nb; ++b) SHV_HIP_CHECK(hipStreamWaitEvent(q, join_[b], 0));
+    }
     void encode_branched(const uint8_t* frames, int F, float* tokens, hipStream_t q) {
         const int nb = dump_dir_.empty() ? std::max(1, std::min(kBranches, F / (kBranchClips * kFrames))) : 1;
         const bool fork = nb > 1 && !profiling();
