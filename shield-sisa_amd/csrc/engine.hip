@@ -191,11 +191,21 @@ public:
         run_graph(GraphKey{2, d_frames, d_tokens, F}, s,
                   [&](hipStream_t q) { encode_branched(d_frames, F, d_tokens, q); });
     }
+    bool forward_slot(int slot, int n, hipStream_t s) override {
+        if (n <= 0) return false;
+        const int nb = window_bucket(n);
+        if (nb > cfg_.max_windows || nb * kFrames > cfg_.max_frames) return false;
+        const Slot& sl = slots_.at(size_t(slot));
+        run_graph(GraphKey{4, sl.d_frames, sl.d_logits, nb}, s, [&](hipStream_t q) {
+            forward_branched(sl.d_frames, sl.d_tokens, sl.d_tokptr, nb, sl.d_logits, q);
+        });
+        return true;
+    }
     void forward_direct(const uint8_t* d_frames, int n, float* d_logits, hipStream_t s) override {
         if (n <= 0) return;
         if (n > cfg_.max_windows || n * kFrames > cfg_.max_frames) throw std::runtime_error("forward: too many clips");
         run_graph(GraphKey{3, d_frames, d_logits, n}, s,
-                  [&](hipStream_t q) { forward_branched(d_frames, n, d_logits, q); });
+                  [&](hipStream_t q) { forward_branched(d_frames, tok_direct_, tokptr_direct_, n, d_logits, q); });
     }
 
 private:
@@ -448,7 +458,10 @@ private:
     // 19.15, per branch 19.07 -- the last ran the sequence GEMMs at 32 windows, 1.5x slower per row, so the pair
     // is kept.
     static constexpr int kSeqGroup = 2;
-    void forward_branched(const uint8_t* frames, int n, float* logits, hipStream_t q) {
+    // frames [n * 20] -> tokens [n * 20][6144] -> logits [n], window w reading its frames' tokens through
+    // tokptr[w * 20 ..]
+    void forward_branched(const uint8_t* frames, float* tokens, const float* const* tokptr, int n, float* logits,
+                          hipStream_t q) {
         const int nb = dump_dir_.empty() ? std::max(1, std::min(kBranches, n / kBranchClips)) : 1;
         const bool fork = nb > 1 && !profiling();
         const int sg = std::min(nb, kSeqGroup);
@@ -462,14 +475,14 @@ private:
                 SHV_HIP_CHECK(hipStreamWaitEvent(bs, fork_, 0));
             }
             const int f0 = c0 * kFrames;
-            run_encode(frames + size_t(f0) * kFrameBytes, (c1 - c0) * kFrames, tok_direct_ + size_t(f0) * kTokenFloats,
-                       bs, acts_at(f0));
+            run_encode(frames + size_t(f0) * kFrameBytes, (c1 - c0) * kFrames, tokens + size_t(f0) * kTokenFloats, bs,
+                       acts_at(f0));
             if ((b + 1) % sg == 0 || b == nb - 1) {
                 const int g0 = b - b % sg;
                 if (fork)
                     for (int bb = g0; bb < b; ++bb) SHV_HIP_CHECK(hipStreamWaitEvent(bs, join_[bb], 0));
                 const int w0 = clip(g0);
-                run_classify(tokptr_direct_ + size_t(w0) * kFrames, c1 - w0, logits + w0, bs, w0);
+                run_classify(tokptr + size_t(w0) * kFrames, c1 - w0, logits + w0, bs, w0);
             }
             if (fork) SHV_HIP_CHECK(hipEventRecord(join_[b], bs));
         }

@@ -98,6 +98,10 @@ public:
     // F / B are padded to a bucket when graphs are on (padding rows are computed and ignored).
     virtual void encode_slot(int slot, int F, hipStream_t s) = 0;
     virtual void classify_slot(int slot, int B, hipStream_t s) = 0;
+    // Both for a batch whose window w reads exactly frames [20 w, 20 w + 20) of the slot (its table filled so): the
+    // branches then run their windows' sequence stages right after their encode.  false (nothing queued) if the
+    // bucket's frames do not fit the slot.
+    virtual bool forward_slot(int slot, int n, hipStream_t s) = 0;
     // Direct path on caller device buffers (no padding): frames [F] -> tokens [F][6144]
     virtual void encode_direct(const uint8_t* d_frames, int F, float* d_tokens, hipStream_t s) = 0;
     // clips [n][20] frames -> logits [n], through the engine's own token buffer

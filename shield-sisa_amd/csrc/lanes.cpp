@@ -150,13 +150,18 @@ void HipLanes::start(const sched::Batch& b) {
     // compute
     SHV_HIP_CHECK(hipStreamWaitEvent(compute_, L.uploaded, 0));
     SHV_HIP_CHECK(hipEventRecord(L.t0, compute_));
-    if (b.frames) eng_->encode_slot(b.lane, b.frames, compute_);
+    // a batch whose window w reads exactly its frames [20 w, 20 w + 20) runs as one branched forward
+    bool aligned = b.windows > 0 && b.frames == b.windows * kFrames && b.refs.size() == size_t(b.frames);
+    for (size_t e = 0; aligned && e < b.refs.size(); ++e)
+        aligned = b.refs[e].kind == sched::TokenRef::kFrame && b.refs[e].index == int32_t(e);
+    const bool fused = aligned && eng_->forward_slot(b.lane, b.windows, compute_);
+    if (b.frames && !fused) eng_->encode_slot(b.lane, b.frames, compute_);
     if (stores) {
         launch_store_tokens(d.d_tokens, d.d_store, pool_, b.frames, compute_);
         SHV_HIP_CHECK(hipGetLastError());
     }
     if (b.windows) {
-        eng_->classify_slot(b.lane, b.windows, compute_);
+        if (!fused) eng_->classify_slot(b.lane, b.windows, compute_);
         SHV_HIP_CHECK(hipMemcpyAsync(L.logits, d.d_logits, size_t(b.windows) * sizeof(float), hipMemcpyDeviceToHost,
                                      compute_));
     }
