@@ -723,7 +723,9 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
                 o.y = epi_value(p, v[q].y, bv.y, rv[q].y);
                 o.z = epi_value(p, v[q].z, bv.z, rv[q].z);
                 o.w = epi_value(p, v[q].w, bv.w, rv[q].w);
-                *reinterpret_cast<float4*>(p.C + m * p.ldc + n) = o;
+                // non-temporal: C (up to 381 MB per launch) would otherwise evict the A group and W blocks the
+                // tile order keeps in L2 (sequence GEMMs 2.09 -> 2.05 ms, step -0.5% per 128 clips)
+                __builtin_nontemporal_store(f32x4{o.x, o.y, o.z, o.w}, reinterpret_cast<f32x4*>(p.C + m * p.ldc + n));
             }
             return;
         }
