@@ -1090,7 +1090,10 @@ typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G8;       // 12x20
 typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G9;       // 12x20 (b9, b10)
 typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
 typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6> G12;      // 12x20
-typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 6, 1, 1, 16, 12, 10> G13;   // 12x20 -> 6x10: whole map, 10 columns/tile
+// Block 13 takes 2 output rows per step (7 staged input rows, 76 KB of LDS: two workgroups per CU, and room for
+// the other branches' kernels): alone 1.43 -> 1.55 ms per 128 clips against the whole-map step (130 KB), but the
+// concurrent forward 19.02 -> 18.84 ms; 1 row per step 19.08, 3 rows 19.14.
+typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 2, 1, 1, 16, 0, 10> G13;    // 12x20 -> 6x10, 10 columns/tile
 typedef WgCfg<160, 960, 160, 5, 1, 1, 1, 6, 1, 1, 1, 6> G14;   // 6x10 (b14, b15)
 // bf16 (three operand parts): fewer rows per step where the fp16 row step leaves LDS room for one workgroup per CU
 typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 3> G4B;
@@ -1167,7 +1170,7 @@ bool ir_strip_shape(int block, bool bf16_tier, IrShape* out) {
     case 8: case 9: *out = wg_shape<G9>(); return true;
     case 10: *out = wg_shape<G11>(); return true;
     case 11: *out = bf16_tier ? wg_shape<G12B>() : wg_shape<G12>(); return true;
-    case 12:   // whole-map staging of block 13 fits LDS with two operand parts (fp16) only
+    case 12:   // block 13: fp16 tier only (the bf16 tier keeps its tile kernel)
         if (bf16_tier) return false;
         *out = wg_shape<G13>();
         return true;
