@@ -117,9 +117,10 @@ __device__ __forceinline__ float dw9(float wv, float e0, float e1, float e2, flo
     return acc;
 }
 
-template <int CIN_, int CEXP_, int COUT_, int S_, int R_>
+template <int CIN_, int CEXP_, int COUT_, int S_, int R_, int MINB_ = 1>
 struct StripCfg {
     static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, S = S_, R = R_;
+    static constexpr int MINB = MINB_;   // workgroups per CU the register allocation must allow
     static constexpr bool EXPAND = CIN != CEXP;
     static constexpr bool RES = S == 1 && CIN == COUT;
     static constexpr int KSI = (CIN + 15) / 16;              // expand K steps
@@ -134,10 +135,11 @@ struct StripCfg {
     static_assert(EXPAND || (CT == 1 && KSI == 1), "blocks without expand have one 16-channel tile");
 };
 
-//                  cin cexp cout s  R
-typedef StripCfg<16, 16, 16, 1, 6> S1;    // 90x160
+//                  cin cexp cout s  R  workgroups per CU
+typedef StripCfg<16, 16, 16, 1, 6, 3> S1; // 90x160 (three workgroups per CU: stem + block 1 1.72 -> 1.27 ms, 1 spill)
 typedef StripCfg<16, 64, 24, 2, 1> S2;    // 90x160 -> 45x80
-typedef StripCfg<24, 72, 24, 1, 4> S3;    // 45x80 (R 4: 1.04 ms per 128-clip step vs 1.05 at R 3, 1.14 at R 2)
+typedef StripCfg<24, 72, 24, 1, 3, 3> S3; // 45x80 (R 3 in 164 VGPRs, three workgroups per CU: 1.12 -> 0.97 ms)
+typedef StripCfg<24, 72, 24, 1, 4> S3B;   // bf16 (three operand parts: R 3 in three workgroups per CU spills)
 
 template <typename T, class C> struct StripLds {
     static constexpr int P = Split<T>::P;
@@ -181,7 +183,7 @@ __device__ __forceinline__ void stem_fetch(const uint8_t* img, long long f, int 
 template <typename T, class C, bool STEM = false>
 // segs: each strip's output rows are dealt over segs items of seg_rows rows (a multiple of R) when frames are few;
 // every step reads its own input rows, so the split changes no result.
-__global__ void __launch_bounds__(ST_THREADS) ir_strip_kernel(IrArgs a, int strips, int items, int segs, int seg_rows,
+__global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a, int strips, int items, int segs, int seg_rows,
                                                               const float* __restrict__ stem_w,
                                                               const float* __restrict__ stem_b) {
     typedef Split16<T> S16;
@@ -1083,7 +1085,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 }
 
 //                cin  cexp cout k  s  hs se R  minb
-typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 6> G4;         // 45x80 -> 23x40
+typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 3, 3> G4;      // 45x80 -> 23x40 (R 3, three workgroups per CU: 0.94 -> 0.88 ms)
 typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 6> G5;         // 23x40 (b5, b6)
 typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 3, 2, 0, 0, 0, 16, 1> G7;    // 23x40 -> 12x20
 typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G8;       // 12x20
@@ -1184,7 +1186,7 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
     switch (block) {
     case 0: launch_strip<T, S1>(block, a, F, s); return true;
     case 1: launch_strip<T, S2>(block, a, F, s); return true;
-    case 2: launch_strip<T, S3>(block, a, F, s); return true;
+    case 2: launch_strip<T, std::conditional_t<IS_BF16, S3B, S3>>(block, a, F, s); return true;
     case 3: launch_wgstrip<T, std::conditional_t<IS_BF16, G4B, G4>>(block, a, F, s); return true;
     case 4: case 5: launch_wgstrip<T, G5>(block, a, F, s); return true;
     case 6: launch_wgstrip<T, std::conditional_t<IS_BF16, G7B, G7>>(block, a, F, s); return true;
