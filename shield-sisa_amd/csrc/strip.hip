@@ -538,10 +538,13 @@ template <typename T, class C, bool STEM = false> void launch_strip(int block, c
 // last tap.  Columns outside the map expand from -1e30 (ReLU and hardswish both give 0 there), rows outside the
 // map are skipped (E = 0).
 template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_, int MINB_ = 1, int ROLLK_ = 0,
-          int NOPF_ = 0, int WHOLE_H_ = 0, int NPOS_ = 16, int YBA_ = 0>
+          int NOPF_ = 0, int WHOLE_H_ = 0, int NPOS_ = 16, int YBA_ = 0, int WAVES_ = 4>
 struct WgCfg {
     static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, KS = KS_, S = S_, R = R_;
     static constexpr int MINB = MINB_;   // workgroups per CU the register allocation must allow
+    // waves of a workgroup sharing one staged step (channel tiles ct = wave, wave + WAVES, ...); the projection
+    // blocks add their wave partials in four-wave order and keep 4
+    static constexpr int WAVES = WAVES_, THREADS = 64 * WAVES_;
     // ROLLK: the expand runs K-step-outer in a rolled loop (weight parts loaded per K step, one step ahead), so only
     // one K step's fragments are live -- for wide inputs, where the unrolled form holds every row's fragments
     static constexpr bool ROLLK = ROLLK_ != 0;
@@ -575,6 +578,7 @@ struct WgCfg {
     static constexpr int NWR = (KS * KS + 1 + 15) / 16;    // depthwise weight registers per value (taps + bias)
     static_assert(CIN % 4 == 0 && CEXP % 4 == 0 && COUT % 4 == 0, "channel counts must be multiples of 4");
     static_assert(KS == 3 || KS == 5, "3x3 or 5x5 depthwise");
+    static_assert(WAVES == 4 || (SE && (WAVES == 8)), "projection blocks: four waves; squeeze-excite blocks: 4 or 8");
 };
 
 template <typename T, class C> struct WgLds {
@@ -854,7 +858,7 @@ template <typename T, class C>
 // workgroups, and segs: its steps over segs items of seg_steps steps, so that few frames still fill the device
 // (item = ((frame, strip) * segs + segment) * csplit + group).  Every output is computed the same way whichever
 // workgroup takes its tile and step.
-__global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items,
+__global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs a, int strips, int steps, int items,
                                                                            int csplit, int segs, int seg_steps) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
@@ -875,7 +879,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
     // past cin is zeroed when the rows are split into LDS, so no load waits on a predicate
     constexpr int XQ = C::CINP / 4;
     constexpr int XN = C::XRN * C::NT * C::NPOS * XQ;
-    constexpr int XPT_ALL = (XN + ST_THREADS - 1) / ST_THREADS;
+    constexpr int XPT_ALL = (XN + C::THREADS - 1) / C::THREADS;
     constexpr int XPT = C::NOPF ? (XPT_ALL < C::NOPF_CHUNK ? XPT_ALL : C::NOPF_CHUNK) : XPT_ALL;   // held at a time
     float4 xpre[XPT];
     auto col_of = [&](int strip, int p, int t) {
@@ -887,7 +891,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
         const int iy0 = C::S * step * C::R - C::PADK + C::XR0;
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int i = min(tid + (k0 + k) * ST_THREADS, XN - 1);
+            const int i = min(tid + (k0 + k) * C::THREADS, XN - 1);
             const int c4 = i % XQ, rest = i / XQ;
             const int p = rest % C::NPOS, jt = rest / C::NPOS;
             const int t = jt % C::NT, j = jt / C::NT;
@@ -901,7 +905,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
         const int iy0 = C::S * step * C::R - C::PADK + C::XR0;
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int i = tid + (k0 + k) * ST_THREADS;
+            const int i = tid + (k0 + k) * C::THREADS;
             if (i >= XN) continue;
             const int c4 = i % XQ, rest = i / XQ;
             const int p = rest % C::NPOS, jt = rest / C::NPOS;
@@ -968,7 +972,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                     for (int q = 0; q < C::R; ++q) y[q][ot] = f32x4{b.x, b.y, b.z, b.w};
                 }
             }
-            for (int ct = wave + 4 * cgroup; ct < C::CT; ct += 4 * csplit) {
+            for (int ct = wave + C::WAVES * cgroup; ct < C::CT; ct += C::WAVES * csplit) {
                 const int c = ct * 16 + 4 * g;
                 // ---- this tile's weights
                 V8 wf[C::ROLLK ? 1 : C::KS32][P];
@@ -1091,12 +1095,15 @@ typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 3, 2, 0, 0, 0, 16, 1> G7;    // 23x40 -> 
 typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G8;       // 12x20
 typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G9;       // 12x20 (b9, b10)
 typedef WgCfg<80, 480, 112, 3, 1, 1, 1, 4> G11;       // 12x20
-typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6> G12;      // 12x20
+typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6, 1, 0, 0, 0, 16, 0, 8> G12;   // 12x20, eight waves per staged step
+// Blocks 12-15 (squeeze-excite, wide expands) run eight waves on each staged step: the same LDS serves twice the
+// waves, so a workgroup holds half the LDS per wave (alone: block 12 1.14 -> 1.06 ms, 13 1.55 -> 1.28, 14-15
+// 1.50 -> 1.21 per 128 clips; the concurrent forward unchanged to -0.5%, bf16 async +3%).
 // Block 13 takes 2 output rows per step (7 staged input rows, 76 KB of LDS: two workgroups per CU, and room for
 // the other branches' kernels): alone 1.43 -> 1.55 ms per 128 clips against the whole-map step (130 KB), but the
 // concurrent forward 19.02 -> 18.84 ms; 1 row per step 19.08, 3 rows 19.14.
-typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 2, 1, 1, 16, 0, 10> G13;    // 12x20 -> 6x10, 10 columns/tile
-typedef WgCfg<160, 960, 160, 5, 1, 1, 1, 6, 1, 1, 1, 6> G14;   // 6x10 (b14, b15)
+typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 2, 2, 1, 16, 0, 10, 0, 8> G13;   // 12x20 -> 6x10, 10 columns/tile, eight waves
+typedef WgCfg<160, 960, 160, 5, 1, 1, 1, 6, 1, 1, 1, 6, 16, 0, 8> G14;   // 6x10 (b14, b15), eight waves
 // bf16 (three operand parts): fewer rows per step where the fp16 row step leaves LDS room for one workgroup per CU
 typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 3> G4B;
 typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 2, 2, 0, 0, 0, 16, 1> G7B;
@@ -1133,7 +1140,7 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_wgstrip_kernel<T, C>, ST_THREADS, 0) != hipSuccess)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_wgstrip_kernel<T, C>, C::THREADS, 0) != hipSuccess)
             throw std::runtime_error("ir_wgstrip: cannot query the device occupancy");
         return std::max(1, cus) * std::max(1, per_cu);
     }();
@@ -1141,7 +1148,7 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
     // tiles over several workgroups (at least one tile per wave each)
     int csplit = 1;
     if (C::SE && (long long)F * strips < resident)
-        csplit = std::max(1, std::min(int(resident / ((long long)F * strips)), C::CT / 4));
+        csplit = std::max(1, std::min(int(resident / ((long long)F * strips)), C::CT / C::WAVES));
     // still fewer items than resident workgroups: deal each strip's steps over segments as well
     int seg_steps = steps;
     if ((long long)F * strips * csplit < resident) {
@@ -1152,7 +1159,7 @@ template <typename T, class C> void launch_wgstrip(int block, const IrArgs& a, i
     if ((long long)F * strips * csplit * segs > (1ll << 30)) throw std::runtime_error("ir_wgstrip: too many items");
     const int items = F * strips * csplit * segs;
     const int grid = std::min(items, resident);
-    hipLaunchKernelGGL((ir_wgstrip_kernel<T, C>), dim3(grid), dim3(ST_THREADS), 0, s, a, strips, steps, items,
+    hipLaunchKernelGGL((ir_wgstrip_kernel<T, C>), dim3(grid), dim3(C::THREADS), 0, s, a, strips, steps, items,
                        csplit, segs, seg_steps);
 }
 
