@@ -137,7 +137,8 @@ struct StripCfg {
 
 //                  cin cexp cout s  R  workgroups per CU
 typedef StripCfg<16, 16, 16, 1, 6, 3> S1; // 90x160 (three workgroups per CU: stem + block 1 1.72 -> 1.27 ms, 1 spill)
-typedef StripCfg<16, 64, 24, 2, 1> S2;    // 90x160 -> 45x80
+typedef StripCfg<16, 64, 24, 2, 2, 3> S2; // 90x160 -> 45x80 (R 2 in three per CU: 6% slower alone, forward -0.5%)
+typedef StripCfg<16, 64, 24, 2, 1> S2B;   // bf16 (R 2 in three per CU spills)
 typedef StripCfg<24, 72, 24, 1, 3, 3> S3; // 45x80 (R 3 in 164 VGPRs, three workgroups per CU: 1.12 -> 0.97 ms)
 typedef StripCfg<24, 72, 24, 1, 4> S3B;   // bf16 (three operand parts: R 3 in three workgroups per CU spills)
 
@@ -1192,7 +1193,7 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
     constexpr bool IS_BF16 = std::is_same<T, bf16>::value;
     switch (block) {
     case 0: launch_strip<T, S1>(block, a, F, s); return true;
-    case 1: launch_strip<T, S2>(block, a, F, s); return true;
+    case 1: launch_strip<T, std::conditional_t<IS_BF16, S2B, S2>>(block, a, F, s); return true;
     case 2: launch_strip<T, std::conditional_t<IS_BF16, S3B, S3>>(block, a, F, s); return true;
     case 3: launch_wgstrip<T, std::conditional_t<IS_BF16, G4B, G4>>(block, a, F, s); return true;
     case 4: case 5: launch_wgstrip<T, G5>(block, a, F, s); return true;
