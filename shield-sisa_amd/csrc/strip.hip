@@ -1102,7 +1102,8 @@ typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6, 1, 0, 0, 0, 16, 0, 8> G12;   // 12x2
 // 1.50 -> 1.21 per 128 clips; the concurrent forward unchanged to -0.5%, bf16 async +3%).
 // Block 13 takes 2 output rows per step (7 staged input rows, 76 KB of LDS: two workgroups per CU, and room for
 // the other branches' kernels): alone 1.43 -> 1.55 ms per 128 clips against the whole-map step (130 KB), but the
-// concurrent forward 19.02 -> 18.84 ms; 1 row per step 19.08, 3 rows 19.14.
+// concurrent forward 19.02 -> 18.84 ms; 1 row per step 19.08, 3 rows 19.14.  The bf16 tier runs it too (114 KB
+// with three parts, one workgroup per CU): 2.68 -> 1.63 ms against the tile kernel, bf16 forward 27.9 -> 26.5 ms.
 typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 2, 2, 1, 16, 0, 10, 0, 8> G13;   // 12x20 -> 6x10, 10 columns/tile, eight waves
 typedef WgCfg<160, 960, 160, 5, 1, 1, 1, 6, 1, 1, 1, 6, 16, 0, 8> G14;   // 6x10 (b14, b15), eight waves
 // bf16 (three operand parts): fewer rows per step where the fp16 row step leaves LDS room for one workgroup per CU
@@ -1180,10 +1181,7 @@ bool ir_strip_shape(int block, bool bf16_tier, IrShape* out) {
     case 8: case 9: *out = wg_shape<G9>(); return true;
     case 10: *out = wg_shape<G11>(); return true;
     case 11: *out = bf16_tier ? wg_shape<G12B>() : wg_shape<G12>(); return true;
-    case 12:   // block 13: fp16 tier only (the bf16 tier keeps its tile kernel)
-        if (bf16_tier) return false;
-        *out = wg_shape<G13>();
-        return true;
+    case 12: *out = wg_shape<G13>(); return true;
     case 13: case 14: *out = wg_shape<G14>(); return true;
     default: return false;
     }
@@ -1202,12 +1200,7 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
     case 8: case 9: launch_wgstrip<T, G9>(block, a, F, s); return true;
     case 10: launch_wgstrip<T, G11>(block, a, F, s); return true;
     case 11: launch_wgstrip<T, std::conditional_t<IS_BF16, G12B, G12>>(block, a, F, s); return true;
-    case 12:
-        if constexpr (std::is_same<T, f16>::value) {
-            launch_wgstrip<T, G13>(block, a, F, s);
-            return true;
-        }
-        return false;
+    case 12: launch_wgstrip<T, G13>(block, a, F, s); return true;
     case 13: case 14: launch_wgstrip<T, G14>(block, a, F, s); return true;
     default: return false;
     }
