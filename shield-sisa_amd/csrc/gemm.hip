@@ -677,14 +677,14 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
             }
         return;
     }
-    if constexpr (WN % 4 == 0) {
-        // fp32 C in 16-byte column groups (vec_c: the host checked alignment and strides): the wave's 64 x 16 WN tile
-        // goes through its own LDS region of the (now idle) ring, then each store instruction writes four whole rows
-        // of the tile (16 WN x 4 bytes each) instead of 64-byte pieces of 16.  The region is [64][16 WN] floats with
-        // the 16-column group index XOR-ed by the row's (row / 4) % 4, so the fragment writes (rows 4g + i, 16
-        // columns per lane group g) and the row reads both hit distinct banks.
+    constexpr int TW = 16 * WN, GPR = TW / 4;   // tile columns, float4 groups per row
+    if constexpr ((TW & (TW - 1)) == 0 && TW >= 32) {
+        // fp32 C in 16-byte column groups (vec_c: the host checked alignment and strides): the wave's 64 x TW tile
+        // goes through its own LDS region of the (now idle) ring, then each store instruction writes 64 / GPR whole
+        // rows of the tile (TW x 4 bytes each) instead of 64-byte pieces of 16.  The region is [64][TW] floats with
+        // the 16-column group index XOR-ed by the row's (row / 4) % 4 (modulo the width), so the fragment writes
+        // (rows 4g + i, 16 columns per lane group g) and the row reads spread over the banks.
         if (vec_c) {
-            constexpr int TW = 16 * WN, GPR = TW / 4;   // tile columns, float4 groups per row
             static_assert(D::WAVES * 64 * TW * 4 <= NS * D::STAGE, "the ring holds every wave's C tile");
             __syncthreads();   // every wave has read its last operands from the ring
             float* wt = reinterpret_cast<float*>(ring) + wave * 64 * TW;
@@ -695,7 +695,7 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int row = mt * 16 + g * 4 + i;
-                        wt[row * TW + ((nt * 16 + r) ^ (g * 16))] = acc[mt][nt][i];
+                        wt[row * TW + ((nt * 16 + r) ^ ((g * 16) & (TW - 1)))] = acc[mt][nt][i];
                     }
             __syncthreads();
             constexpr int PASSES = 64 * GPR / 64;
@@ -709,7 +709,7 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
 #pragma unroll
             for (int q = 0; q < PASSES; ++q) {
                 const int row = q * (64 / GPR) + rsub;
-                v[q] = *reinterpret_cast<const float4*>(wt + row * TW + ((c4 * 4) ^ (((row >> 2) & 3) * 16)));
+                v[q] = *reinterpret_cast<const float4*>(wt + row * TW + ((c4 * 4) ^ ((((row >> 2) & 3) * 16) & (TW - 1))));
                 const long long m = min(mw + row, (long long)p.M - 1);
                 rv[q] = p.res ? *reinterpret_cast<const float4*>(p.R + m * p.ldr + min(n, p.N - 4))
                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -1059,16 +1059,28 @@ template <typename T, int NS, int WN, int WGM> void launch_dma_cfg(const GemmArg
                        nblocks, vec_c);
 }
 
+// fp16 sequence GEMMs that take 256 x 64 workgroup tiles: fp32 C wider than 1024 columns
+inline bool dma_narrow_tiles(const GemmArgs& p) { return !p.swiglu && p.N > 1024; }
+
 template <typename T> void launch_dma(const GemmArgs& p, hipStream_t s) {
     if (!p.Ah || p.K % 32 || p.astride % 8 || p.wstride % 8 || p.lda % 8 || p.ldw % 8)
         throw std::runtime_error("gemm_dma: needs pre-split A, K % 32 == 0 and 16-byte aligned rows");
-    // measured per 128-clip step (ring depth, column tiles per wave, waves per workgroup): fp16 (2,4,4) 2.26 ms,
-    // (2,2,4) 2.43, (3,2,4) 2.82, (3,4,4) 3.35, (4,2,4) 4.19, (2,2,8) 2.30, (2,4,8) 2.42; bf16 (2,4,8) 3.42 ms, (2,2,4) 4.14,
-    // (2,4,4) 4.71, (3,4,4) 4.79, (3,2,4) 5.91, (4,2,4) 6.00.  Deeper rings lose: the occupancy their LDS costs is
-    // worth more than the latency they hide.  For bf16 the 8-wave workgroup shares each staged W tile over twice
-    // the rows, which halves the W traffic behind its six products per step.
-    if constexpr (Split<T>::P == 2) launch_dma_cfg<T, 2, 4, 2>(p, s);
-    else launch_dma_cfg<T, 2, 4, 4>(p, s);
+    // Configurations are (ring depth NS, column tiles per wave WN, wave rows WGM): 2 WGM waves per workgroup on a
+    // (64 WGM) x (32 WN) tile.  Deeper rings lose everywhere (fp16 in-projection: ring 3 +19-52%, ring 4
+    // +96%): the occupancy their LDS costs is worth more than the latency they hide.  Per shape (64-window launches,
+    // 20,544 rows, timed alone on one box): fp16 -- the wide fp32-C GEMMs (in-projection N 2316, SISA N 1068) run
+    // 12% faster on 256 x 64 tiles (2,2,4) with the staged 16-byte C stores (in-projection 153-165 vs 176-187 us,
+    // SISA 71 vs 81-83 us); the N = 384 and SwiGLU shapes stay on 128 x 128 (2,4,2) (o_proj 47 vs 58 us, FFN down 55
+    // vs 69 us).  bf16 -- 128 x 64 tiles (2,2,2) on every shape (against 256 x 128 (2,4,4): o_proj 78 vs 123 us, FFN
+    // down 95 vs 146, SISA 125 vs 158, in-projection 278 vs 291-295, FFN up 200 vs 198-210).  A workgroup that
+    // computes several column tiles and stores the previous tile's C during the next one's K steps was bitwise
+    // equal and 35-50% slower: the registers that hold the pending outputs cost a resident workgroup per CU.
+    if constexpr (Split<T>::P == 2) {
+        if (dma_narrow_tiles(p)) launch_dma_cfg<T, 2, 2, 4>(p, s);
+        else launch_dma_cfg<T, 2, 4, 2>(p, s);
+    } else {
+        launch_dma_cfg<T, 2, 2, 2>(p, s);
+    }
 }
 
 // the direct-to-LDS kernel for pre-split A unless SHV_HIP_NO_GEMM_DMA is set (read per launch: the bitwise
@@ -1329,7 +1341,9 @@ template <typename T> std::string gemm_mfma_kernel(const GemmArgs& p) {
     const GemmPlan pl = plan_gemm<T>(p);
     switch (pl.kind) {
     case GemmPlan::Small: return "gemm_small_kernel<" + t + ">";
-    case GemmPlan::Dma: return Split<T>::P == 2 ? "gemm_dma_kernel<" + t + ",2,4,2>" : "gemm_dma_kernel<" + t + ",2,4,4>";
+    case GemmPlan::Dma:
+        if (Split<T>::P != 2) return "gemm_dma_kernel<" + t + ",2,2,2>";
+        return dma_narrow_tiles(p) ? "gemm_dma_kernel<" + t + ",2,2,4>" : "gemm_dma_kernel<" + t + ",2,4,2>";
     case GemmPlan::Lds: return "gemm_lds_kernel<" + t + ",4,4,2,2>";
     case GemmPlan::Stream: return "gemm_stream_kernel<" + t + "," + std::to_string(pl.nt) + ">";
     case GemmPlan::Direct: return "gemm_direct_kernel<" + t + "," + std::to_string(std::min(pl.nt, 5)) + ">";
