@@ -149,9 +149,10 @@ int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir);
  * device memory, row-major with leading dimensions k (A, W) and n (C).  act: the reference's codes
  * (engine/cuda/common.cuh:69): 0 none, 1 ReLU, 2 hardswish, 3 SiLU, 4 hardsigmoid.  d_bias may be NULL.
  * create repacks W on the device (synchronising `stream`); NULL + last_error on failure (fp16 / bf16 need k % 8 == 0).
- * run: variant 0 = the engine's own kernel choice; fp32: 1 GEMV, 2 tiled; fp16 / bf16: 1 small-M, 2..6 direct
- * with 1..5 column tiles per wave, 7 LDS-staged, 8 streaming (n <= 160).  Returns 0, or -1 + last_error.
- * Asynchronous on `stream`. */
+ * run: variant 0 = the engine's own kernel choice; fp32: 1 GEMV, 2 tiled, 3 K blocks in parallel (allocates its
+ * workspace of ceil(k / 64) * m * n floats and synchronises `stream`); fp16 / bf16: 1 small-M, 2..6 direct with
+ * 1..5 column tiles per wave, 7 LDS-staged, 8 streaming (n <= 160).  Returns 0, or -1 + last_error.  Asynchronous on
+ * `stream` except fp32 variant 3. */
 typedef struct shv_hip_gemm shv_hip_gemm;
 shv_hip_gemm* shv_hip_gemm_create(const char* mode, int n, int k, const float* d_w, void* stream);
 int shv_hip_gemm_run(shv_hip_gemm* g, const float* d_a, long long m, const float* d_bias, int act, float* d_c,

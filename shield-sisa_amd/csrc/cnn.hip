@@ -117,23 +117,40 @@ dw_tile_kernel(const float* __restrict__ in, float* __restrict__ out, const floa
 }
 
 // ------------------------------------------------------------------------------------------------ SE squeeze
-// one thread per (frame, channel): row sums left to right, rows added in order, divided by (float)(Ho*Wo)
+// SE mean in the CPU engine's order (engine/model/isa_impl.hpp:762-772): per channel, each row summed left to right
+// from its first element, the row sums added top to bottom from the first row's, the total divided by (float)(Ho*Wo).
+// The row sums are independent, so a workgroup (frame, 64 channels) gives each of SP_RG row groups its own rows
+// (lanes on consecutive channels: 256-byte loads) and one thread per channel adds the row sums in order from LDS:
+// the same operations as one serial loop, with a dependent chain of Wo + Ho adds instead of Ho * Wo.
+constexpr int SP_CH = 64, SP_RG = 8, SP_MAXH = 64, SP_U = 8;
 template <typename T>
-__global__ void __launch_bounds__(256)
-se_pool_kernel(const T* __restrict__ x, float* __restrict__ pooled, int F, int Ho, int Wo, int C) {
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long long)F * C) return;
-    const int c = int(idx % C);
-    const long long f = idx / C;
-    const T* base = x + f * Ho * Wo * C + c;
-    float tot = 0.0f;
-    for (int y = 0; y < Ho; ++y) {
+__global__ void __launch_bounds__(SP_CH * SP_RG)
+se_pool_kernel(const T* __restrict__ x, float* __restrict__ pooled, int Ho, int Wo, int C) {
+    __shared__ float rows[SP_MAXH][SP_CH];
+    const int cl = threadIdx.x % SP_CH, rg = threadIdx.x / SP_CH;
+    const int c = blockIdx.y * SP_CH + cl;
+    const long long f = blockIdx.x;
+    const bool live = c < C;
+    const T* base = x + f * Ho * Wo * C + (live ? c : 0);
+    for (int y = rg; y < Ho; y += SP_RG) {
         const T* row = base + (long long)y * Wo * C;
         float acc = to_f(row[0]);
-        for (int xx = 1; xx < Wo; ++xx) acc = acc + to_f(row[(long long)xx * C]);
-        tot = y == 0 ? acc : tot + acc;
+        for (int x0 = 1; x0 < Wo; x0 += SP_U) {
+            float v[SP_U];
+#pragma unroll
+            for (int i = 0; i < SP_U; ++i) v[i] = x0 + i < Wo ? to_f(row[(long long)(x0 + i) * C]) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < SP_U; ++i)
+                if (x0 + i < Wo) acc = acc + v[i];
+        }
+        rows[y][cl] = acc;
     }
-    pooled[idx] = tot / float(Ho * Wo);
+    __syncthreads();
+    if (rg == 0 && live) {
+        float tot = rows[0][cl];
+        for (int y = 1; y < Ho; ++y) tot = tot + rows[y][cl];
+        pooled[f * C + c] = tot / float(Ho * Wo);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ 4x4 pool
@@ -232,7 +249,10 @@ void launch_dw(const T* in, T* out, const float* w, const float* b, int F, int H
 }
 
 template <typename T> void launch_se_pool(const T* x, float* pooled, int F, int Ho, int Wo, int C, hipStream_t s) {
-    hipLaunchKernelGGL(se_pool_kernel<T>, dim3(cdiv((long long)F * C, 256)), dim3(256), 0, s, x, pooled, F, Ho, Wo, C);
+    if (Ho > SP_MAXH || Ho < 1 || Wo < 1) throw std::runtime_error("se_pool: map height outside 1..64");
+    if (F < 1) return;
+    hipLaunchKernelGGL(se_pool_kernel<T>, dim3((unsigned)F, cdiv(C, SP_CH)), dim3(SP_CH * SP_RG), 0, s, x, pooled, Ho,
+                       Wo, C);
 }
 
 template <typename T> void launch_pool(const T* in, T* out, int F, hipStream_t s) {

@@ -182,8 +182,10 @@ public:
         if (B > cfg_.max_windows) throw std::runtime_error("classify: too many windows");
         const Slot& sl = slots_.at(size_t(slot));
         const int Bb = window_bucket(B);
-        run_graph(GraphKey{1, sl.d_tokptr, sl.d_logits, Bb}, s,
-                  [&](hipStream_t q) { run_classify(sl.d_tokptr, Bb, sl.d_logits, q, 0); });
+        run_graph(GraphKey{1, sl.d_tokptr, sl.d_logits, Bb}, s, [&](hipStream_t q) {
+            ws_on_ = true;   // one pass on q
+            run_classify(sl.d_tokptr, Bb, sl.d_logits, q, 0);
+        });
     }
     void encode_direct(const uint8_t* d_frames, int F, float* d_tokens, hipStream_t s) override {
         if (F <= 0) return;
@@ -353,6 +355,14 @@ private:
     // the scheduler's 32-clip batches (the reference's default options) then run as two (128 clips end to end from
     // pinned memory 4,977 -> 5,286 clips/s); 8 branches of 16 clips at batch 128 measured 20.7 vs 18.4 ms.
     static constexpr int kBranches = 4, kBranchClips = 16;
+    // Exact tier: the workspace of the small-M GEMMs' K-block sums (gemm_f32 with ws).  One per engine, so only a
+    // pass that runs alone on its stream hands it out: ws_on_ is set by each pass before it queues its kernels
+    // (false for branched passes, whose branches run at once).  32 MB covers every small-M GEMM of one clip.
+    static constexpr long long kWsFloats = 8ll << 20;
+    float* ws_ = nullptr;
+    long long ws_floats_ = 0;
+    bool ws_on_ = false;
+    float* cur_ws() const { return ws_on_ ? ws_ : nullptr; }
     hipStream_t bstream_[kBranches] = {};
     hipEvent_t fork_ = nullptr, join_[kBranches] = {};
     float* tok_direct_ = nullptr;
@@ -385,6 +395,10 @@ private:
         acts_.se_pool = amem_.make<float>(Fm * kCnnOut);
         acts_.se_hid = amem_.make<float>(Fm * 256);
         acts_.se_scale = amem_.make<float>(Fm * kCnnOut);
+        if constexpr (kF32) {
+            ws_floats_ = kWsFloats;
+            ws_ = amem_.make<float>(size_t(ws_floats_));
+        }
         // direct path: the engine's own token buffer and the window -> frame table of a plain predict
         const size_t Fd = std::min(Fm, Bm * kFrames);
         tok_direct_ = amem_.make<float>(Fd * kTokenFloats);
@@ -445,9 +459,11 @@ private:
 
     // GEMM in this engine's flavour, and the exact fp32 VALU kernel for the fp32-only layers
     void gemm(const char* role, const GemmArgs& p, const DevW& w, hipStream_t s) {
-        GemmRunner<G>{*this}.gemm(role, p, w, s);
+        GemmRunner<G>{*this, cur_ws(), ws_floats_}.gemm(role, p, w, s);
     }
-    void gemm32(const char* role, const GemmArgs& p, hipStream_t s) { GemmRunner<G>{*this}.gemm32(role, p, s); }
+    void gemm32(const char* role, const GemmArgs& p, hipStream_t s) {
+        GemmRunner<G>{*this, cur_ws(), ws_floats_}.gemm32(role, p, s);
+    }
 
     // ---------------------------------------------------------------- CNN
     // F frames as up to kBranches branches of at least kBranchClips clips' frames on the branch streams, forked from
@@ -466,6 +482,7 @@ private:
                           hipStream_t q) {
         const int nb = dump_dir_.empty() ? std::max(1, std::min(kBranches, n / kBranchClips)) : 1;
         const bool fork = nb > 1 && !profiling();
+        ws_on_ = nb == 1;
         const int sg = std::min(nb, kSeqGroup);
         const auto clip = [&](int b) { return int((long long)n * b / nb); };
         if (fork) SHV_HIP_CHECK(hipEventRecord(fork_, q));
@@ -494,6 +511,7 @@ private:
     void encode_branched(const uint8_t* frames, int F, float* tokens, hipStream_t q) {
         const int nb = dump_dir_.empty() ? std::max(1, std::min(kBranches, F / (kBranchClips * kFrames))) : 1;
         const bool fork = nb > 1 && !profiling();
+        ws_on_ = nb == 1;
         if (fork) SHV_HIP_CHECK(hipEventRecord(fork_, q));
         for (int b = 0; b < nb; ++b) {
             const int f0 = int((long long)F * b / nb), f1 = int((long long)F * (b + 1) / nb);
@@ -698,7 +716,7 @@ private:
         timed("assemble", double(B) * kT * kD * 8, s,
               [&] { launch_assemble(tokptr, pos_, readout_, seq_->h(w0), B, s); });
         check_launch();
-        seq_->run(B, logits, s, *this, dump_dir_, w0);
+        seq_->run(B, logits, s, *this, dump_dir_, w0, cur_ws(), ws_floats_);
     }
 };
 
@@ -753,6 +771,17 @@ void PwGemm::run(const float* A, long long M, const float* bias, int act, float*
     p.W = w_; p.ldw = K_; p.wstride = wstride_;
     p.bias = bias; p.act = kAct[act];
     p.C = C; p.ldc = N_;
+    if (prec_ == Precision::FP32 && variant == 3) {   // K blocks in parallel: a workspace for this call
+        const size_t ws = size_t((K_ + 63) / 64) * size_t(M) * size_t(N_);
+        SHV_HIP_CHECK(hipMalloc(&p.ws, ws * sizeof(float)));
+        p.ws_floats = (long long)ws;
+        gemm_f32_variant(p, s, variant);
+        const hipError_t le = hipGetLastError(), se = hipStreamSynchronize(s);
+        (void)hipFree(p.ws);
+        SHV_HIP_CHECK(le);
+        SHV_HIP_CHECK(se);
+        return;
+    }
     switch (prec_) {
     case Precision::FP32: gemm_f32_variant(p, s, variant); break;
     case Precision::BF16: gemm_mfma_variant<bf16>(p, s, variant); break;

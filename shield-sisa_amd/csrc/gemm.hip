@@ -154,6 +154,90 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
                  [&](int i, int j) { return tot[i][j]; });
 }
 
+// Small M with few tiles (one clip's later CNN layers and sequence rows): the tiled kernel's per-output arithmetic is
+// an fma chain from +0 over each 64-wide K block, then the block sums folded left to right (tot = b0, tot = tot +
+// b1, ...).  The block chains are independent, so workgroup (M tile, N tile, K block) stages that block exactly as
+// the tiled kernel does and writes its chains to the workspace [K block][M][N]; gemm_f32_fold_kernel folds them in
+// order and applies the same epilogue.  The same operations, so bitwise the tiled kernel's results, from K / 64
+// times the workgroups.
+template <bool SCALE>
+__global__ void __launch_bounds__(256) gemm_f32_kblock_kernel(GemmArgs p) {
+    __shared__ float As[F32_BM][F32_BK + 1];
+    __shared__ float Ws[F32_BN][F32_BK + 1];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const long long m0 = (long long)blockIdx.x * F32_BM;
+    const int n0 = blockIdx.y * F32_BN;
+    const int k0 = blockIdx.z * F32_BK, kb = min(F32_BK, p.K - k0);
+    const float* A = p.A;
+    const float* W = static_cast<const float*>(p.W);
+    for (int i = tid; i < F32_BM * F32_BK; i += 256) {
+        const int r = i / F32_BK, k = i % F32_BK;
+        const long long gm = m0 + r;
+        const int gn = n0 + r, gk = k0 + k;
+        float a = 0.0f, w = 0.0f;
+        if (k < kb) {
+            if (gm < p.M) {
+                a = A[gm * p.lda + gk];
+                if (SCALE) a = p.scale[(gm / p.scale_rows) * p.ld_scale + gk] * a;
+            }
+            if (gn < p.N) w = W[(long long)gn * p.ldw + gk];
+        }
+        As[r][k] = a;
+        Ws[r][k] = w;
+    }
+    __syncthreads();
+    float blk[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) blk[i][j] = 0.0f;
+    for (int kk = 0; kk < kb; ++kk) {
+        float a[4], w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = As[ty * 4 + i][kk];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = Ws[tx * 4 + j][kk];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) blk[i][j] = __builtin_fmaf(a[i], w[j], blk[i][j]);
+    }
+    float* out = p.ws + (long long)blockIdx.z * p.M * p.N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const long long m = m0 + ty * 4 + i;
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + tx * 4 + j;
+            if (n < p.N) out[m * p.N + n] = blk[i][j];
+        }
+    }
+}
+// one thread per output: the K-block sums folded in order, then gemm_f32_kernel's epilogue (SwiGLU: weight rows
+// 2j, 2j + 1 = gate, up of output j)
+__global__ void __launch_bounds__(256) gemm_f32_fold_kernel(GemmArgs p, int nkb) {
+    const int no = p.swiglu ? p.N / 2 : p.N;
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)p.M * no) return;
+    const long long m = idx / no;
+    const int j = int(idx % no);
+    const long long plane = (long long)p.M * p.N;
+    const auto fold = [&](int n) {
+        const float* w = p.ws + m * p.N + n;
+        float tot = w[0];
+        for (int b = 1; b < nkb; ++b) tot = tot + w[b * plane];
+        return tot;
+    };
+    if (p.swiglu) {
+        p.C[m * p.ldc + j] = silu(fold(2 * j)) * fold(2 * j + 1);
+        return;
+    }
+    const float b = p.bias ? p.bias[j] : 0.0f;
+    const float r = p.res ? p.R[m * p.ldr + j] : 0.0f;
+    p.C[m * p.ldc + j] = epi_value(p, fold(j), b, r);
+}
+
 // Small M (<= 256 rows, e.g. the windows' last SISA rows): the same per-element arithmetic as gemm_f32_kernel -- K blocks
 // of 64, fma chain from +0 inside a block, the first block's sum taken as is and the later ones added in order -- so
 // results are bitwise those of the tiled kernel.  Only the chain inside a K block is serial, so a lane owns one
@@ -1315,6 +1399,23 @@ void launch_tiled_f32(const GemmArgs& p, hipStream_t s) {
     if (p.scale) hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(256), 0, s, p);
 }
+void launch_kblock_f32(const GemmArgs& p, hipStream_t s) {
+    const int nkb = cdiv(p.K, F32_BK);
+    if (!p.ws || (long long)nkb * p.M * p.N > p.ws_floats)
+        throw std::runtime_error("gemm_f32: the K-block kernel needs a workspace of ceil(K / 64) * M * N floats");
+    const dim3 grid(cdiv(p.M, F32_BM), cdiv(p.N, F32_BN), (unsigned)nkb);
+    if (p.scale) hipLaunchKernelGGL(gemm_f32_kblock_kernel<true>, grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(gemm_f32_kblock_kernel<false>, grid, dim3(256), 0, s, p);
+    const long long outs = (long long)p.M * (p.swiglu ? p.N / 2 : p.N);
+    hipLaunchKernelGGL(gemm_f32_fold_kernel, dim3(cdiv(outs, 256)), dim3(256), 0, s, p, nkb);
+}
+// The exact-tier kernel for M above the GEMV range: K blocks in parallel when the tiled grid would not give every
+// CU a workgroup and the workspace holds the block sums (measured with one clip: blocks 13-15 SE projects, 57
+// tiles, and the 321-row sequence GEMMs ran 45-200 us on the tiled kernel)
+bool use_kblock_f32(const GemmArgs& p) {
+    const long long nkb = cdiv(p.K, F32_BK), tiles = (long long)cdiv(p.M, F32_BM) * cdiv(p.N, F32_BN);
+    return p.ws && nkb >= 2 && tiles < 256 && nkb * p.M * p.N <= p.ws_floats;
+}
 }  // namespace
 
 void gemm_f32(const GemmArgs& p, hipStream_t s) { gemm_f32_variant(p, s, 0); }
@@ -1324,16 +1425,19 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
     switch (variant) {
     case 0:
         if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) launch_gemv_f32(p, s);
+        else if (use_kblock_f32(p)) launch_kblock_f32(p, s);
         else launch_tiled_f32(p, s);
         return;
     case 1: launch_gemv_f32(p, s); return;
     case 2: launch_tiled_f32(p, s); return;
+    case 3: launch_kblock_f32(p, s); return;
     }
     throw std::runtime_error("gemm_f32: unknown kernel variant " + std::to_string(variant));
 }
 
 std::string gemm_f32_kernel(const GemmArgs& p) {
-    return (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) ? "gemv_f32_kernel" : "gemm_f32_kernel";
+    if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) return "gemv_f32_kernel";
+    return use_kblock_f32(p) ? "gemm_f32_kblock_kernel" : "gemm_f32_kernel";
 }
 
 template <typename T> std::string gemm_mfma_kernel(const GemmArgs& p) {

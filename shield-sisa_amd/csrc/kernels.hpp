@@ -40,6 +40,9 @@ struct GemmArgs {
     // kstride >= rows * 32: each 16 x 32 fragment block 1 KB contiguous) are read by the small-M, LDS-staged and
     // direct-to-LDS kernels (the sequence GEMMs); the other kernels take the default only.
     long long wkstride = 32, akstride = 32, ckstride = 32;
+    // Exact tier: device workspace of ws_floats floats the GEMM may use for its K-block sums when M is small (the
+    // caller guarantees no other launch uses it meanwhile); null: never.
+    float* ws = nullptr; long long ws_floats = 0;
 };
 
 // fp32 tier: VALU GEMM, each output accumulated in K blocks of 64 (fma chain from +0 per block, block sums added
@@ -50,7 +53,8 @@ void gemm_f32(const GemmArgs& p, hipStream_t s);
 // on M, the tile, or other rows.
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
 // Kernel variants, for the GEMM microbench and its bitwise variant check (every variant performs the same operation
-// sequence per output, so all give bitwise equal results).  fp32: 0 automatic, 1 GEMV, 2 tiled.  MFMA tiers:
+// sequence per output, so all give bitwise equal results).  fp32: 0 automatic, 1 GEMV, 2 tiled, 3 K blocks in
+// parallel (needs ws for ceil(K / 64) * M * N floats).  MFMA tiers:
 // 0 automatic, 1 small-M, 2..6 direct with 1..5 column tiles per wave, 7 LDS-staged 128 x 128, 8 streaming (N <= 160,
 // every column in one workgroup; the SE projects' kernel).
 void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant);

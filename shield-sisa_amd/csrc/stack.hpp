@@ -139,6 +139,8 @@ template <typename U> void dump_f32(const std::string& dir, const char* name, co
 template <typename G> struct GemmRunner {
     static constexpr bool kF32 = std::is_same<G, float>::value;
     Profiler& pf;
+    float* ws = nullptr;   // the exact GEMM's small-M workspace (gemm_f32), null when the caller has none free
+    long long ws_floats = 0;
     std::string family(const char* role, const GemmArgs& p, bool f32) const {
         if (!pf.profiling()) return std::string();
         if constexpr (!kF32) {
@@ -148,6 +150,10 @@ template <typename G> struct GemmRunner {
     }
     // in this flavour's arithmetic; A is read pre-split where the producer wrote parts, else as fp32
     void gemm(const char* role, GemmArgs p, const DevW& w, hipStream_t s) const {
+        if constexpr (kF32) {
+            p.ws = ws;
+            p.ws_floats = ws_floats;
+        }
         p.W = w.w;
         p.wstride = w.stride;
         if (w.ld) {
@@ -162,7 +168,10 @@ template <typename G> struct GemmRunner {
         check_launch();
     }
     // the exact fp32 VALU kernel (layers kept in fp32 in every tier)
-    void gemm32(const char* role, const GemmArgs& p, hipStream_t s) const {
+    void gemm32(const char* role, const GemmArgs& p0, hipStream_t s) const {
+        GemmArgs p = p0;
+        p.ws = ws;
+        p.ws_floats = ws_floats;
         pf.timed(family(role, p, true), gemm_bytes(p.M, p.N, p.K, 4, 4, p.swiglu ? 2 : 4, p.res ? 4 : 0), s,
                  [&] { gemm_f32(p, s); }, 2.0 * p.M * p.N * p.K);
         check_launch();
@@ -257,9 +266,10 @@ public:
 
     // h(w0) of B windows -> logits[B], in windows [w0, w0 + B) of every buffer (disjoint window ranges can run at
     // once on different streams)
-    void run(int B, float* logits, hipStream_t s, Profiler& pf, const std::string& dump_dir, int w0 = 0) {
+    void run(int B, float* logits, hipStream_t s, Profiler& pf, const std::string& dump_dir, int w0 = 0,
+             float* ws = nullptr, long long ws_floats = 0) {
         const int T = spec_.T, M = B * T;
-        const GemmRunner<G> gr{pf};
+        const GemmRunner<G> gr{pf, ws, ws_floats};
         const size_t r0 = size_t(w0) * T;   // first row
         float *H = this->H_ + r0 * kD, *P = this->P_ + r0 * kGld, *Q = this->Q_ + r0 * kD,
               *K = this->K_ + r0 * kD, *V = this->V_ + r0 * kVD, *dec = this->dec_ + r0 * 8,

@@ -5,7 +5,7 @@ points shv_hip_gemm_*: the literal config shapes at full M, bias + hardswish fus
   fp16 / bf16 : |C - C_float64| <= 2^-17 (sum_k |a_k w_k| + |b|) on sampled rows -- the split-operand bound; plain
                 half-precision operands miss it by ~30x (checked on the CPU below, so the bar pins the split).
   variants    : every kernel variant gives bitwise the automatic choice's outputs (the reference's variant check);
-                the fp32 GEMV variant on a 65,536-row prefix.
+                the fp32 GEMV variant on a 65,536-row prefix, the fp32 K-block variant on an 8,192-row prefix.
 """
 import numpy as np
 import pytest
@@ -73,7 +73,7 @@ def test_pw_gemm_parity_and_variants(shv, orc, weights, name, M, N, K, mode):
             for v in shv.GEMM_VARIANTS[mode]:
                 if v in shv.GEMM_NARROW_VARIANTS and N > 160:
                     continue
-                m = min(M, 65536) if (mode == "fp32" and v == 1) else M
+                m = min(M, 65536) if (mode == "fp32" and v == 1) else min(M, 8192) if (mode == "fp32" and v == 3) else M
                 hip.memset(dV, 0xFF, m * N * 4)
                 g.run(dA, m, dV, db, shv.ACT_HSWISH, variant=v)
                 hip.sync()

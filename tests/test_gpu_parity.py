@@ -87,6 +87,9 @@ def test_fp32_stages(shv, weights, clips, golden):
 
 
 def test_row_independence_fp32(fp32_model, clips):
+    """A clip's logit does not depend on the rest of the batch.  One clip's small-M GEMMs (late SE projects, the
+    321-row sequence GEMMs) run their K blocks in parallel and fold them in order, the batch of 6 runs them on the
+    tiled kernel: the comparison holds the two to bitwise equal results."""
     print("[gpu] fp32 row independence", flush=True)
     batch = fp32_model.predict(clips[:6])
     rev = fp32_model.predict(clips[:6][::-1])[::-1]
