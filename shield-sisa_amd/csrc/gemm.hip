@@ -243,8 +243,9 @@ __global__ void __launch_bounds__(256) gemm_f32_fold_kernel(GemmArgs p, int nkb)
 // results are bitwise those of the tiled kernel.  Only the chain inside a K block is serial, so a lane owns one
 // (weight row, K block) pair: a wave covers GV_OPW = 64 / nkb weight rows (even for SwiGLU, whose gate and up rows
 // are adjacent) with all their K blocks, and the block sums are added in order through LDS.  The lane's 64 weights
-// stay in registers across the block's rows (blockIdx.y takes GV_ROWS-row chunks of M).
-constexpr int GV_ROWS = 8;      // rows per workgroup
+// stay in registers across the block's rows (blockIdx.y takes chunks of rpw <= GV_ROWS rows of M: fewer rows per
+// workgroup at small M, where the chunks are the grid's only parallelism along M).
+constexpr int GV_ROWS = 8;      // rows per workgroup at most
 constexpr int GV_MAXM = 256;    // larger M goes to the tiled kernel
 template <bool SCALE, bool VEC>
 __device__ __forceinline__ void gv_load64(float* dst, const float* src, const float* sc, int n) {
@@ -272,10 +273,10 @@ __device__ __forceinline__ void gv_load64(float* dst, const float* src, const fl
     }
 }
 template <bool SCALE, bool VEC>
-__global__ void __launch_bounds__(64) gemv_f32_kernel(GemmArgs p, int nkb, int opw) {
+__global__ void __launch_bounds__(64) gemv_f32_kernel(GemmArgs p, int nkb, int opw, int rpw) {
     __shared__ float part[GV_ROWS][64];
     const int lane = threadIdx.x;
-    const int mbase = blockIdx.y * GV_ROWS, mrows = min(GV_ROWS, p.M - mbase);
+    const int mbase = blockIdx.y * rpw, mrows = min(rpw, p.M - mbase);
     const int o = lane / nkb, kb = lane - o * nkb;
     const int wn = blockIdx.x * opw + o;
     const bool live = o < opw && wn < p.N;
@@ -1091,7 +1092,9 @@ void launch_stream_mt(const GemmArgs& p, hipStream_t s) {
         if (lds > 64 * 1024) throw std::runtime_error("gemm_stream: SE scale rows exceed the LDS budget");
     }
     const unsigned blocks = cdiv(p.M, ST_ROWS);
-    constexpr int WPF = NT >= 8 ? 2 : 1;   // measured: the second weight slot pays only for the widest tiles
+    // measured: the second weight slot pays only for the widest fp16 tiles; bf16's three-part weight tile is better
+    // single-slotted (N 160, K 960, 38,400 rows: 180 vs 195 us; fp16 82.5 vs 83.8)
+    constexpr int WPF = (NT >= 8 && Split<T>::P == 2) ? 2 : 1;
     if (p.scale)
         hipLaunchKernelGGL((gemm_stream_kernel<T, NT, true, WPF, ST_MT>), dim3(blocks), dim3(64 * MFMA_WAVES), lds, s, p);
     else
@@ -1383,15 +1386,17 @@ void launch_gemv_f32(const GemmArgs& p, hipStream_t s) {
     const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
     const bool vec = al16(p.A) && al16(p.W) && p.lda % 4 == 0 && p.ldw % 4 == 0 &&
                      (!p.scale || (al16(p.scale) && p.ld_scale % 4 == 0));
-    const long long yblocks = cdiv(p.M, GV_ROWS);
+    // rows per workgroup: one clip's SE excitation (20 rows) ran 18.5 us per layer in 8-row chunks
+    const int rpw = p.M <= 32 ? 1 : p.M <= 64 ? 2 : p.M <= 128 ? 4 : GV_ROWS;
+    const long long yblocks = cdiv(p.M, rpw);
     if (yblocks > 65535) throw std::runtime_error("gemm_f32: M too large for the GEMV kernel");
     const dim3 grid(cdiv(p.N, opw), (unsigned)yblocks);
     if (p.scale) {
-        if (vec) hipLaunchKernelGGL((gemv_f32_kernel<true, true>), grid, dim3(64), 0, s, p, nkb, opw);
-        else hipLaunchKernelGGL((gemv_f32_kernel<true, false>), grid, dim3(64), 0, s, p, nkb, opw);
+        if (vec) hipLaunchKernelGGL((gemv_f32_kernel<true, true>), grid, dim3(64), 0, s, p, nkb, opw, rpw);
+        else hipLaunchKernelGGL((gemv_f32_kernel<true, false>), grid, dim3(64), 0, s, p, nkb, opw, rpw);
     } else {
-        if (vec) hipLaunchKernelGGL((gemv_f32_kernel<false, true>), grid, dim3(64), 0, s, p, nkb, opw);
-        else hipLaunchKernelGGL((gemv_f32_kernel<false, false>), grid, dim3(64), 0, s, p, nkb, opw);
+        if (vec) hipLaunchKernelGGL((gemv_f32_kernel<false, true>), grid, dim3(64), 0, s, p, nkb, opw, rpw);
+        else hipLaunchKernelGGL((gemv_f32_kernel<false, false>), grid, dim3(64), 0, s, p, nkb, opw, rpw);
     }
 }
 void launch_tiled_f32(const GemmArgs& p, hipStream_t s) {
