@@ -1208,7 +1208,15 @@ template <typename T> GemmPlan plan_gemm(const GemmArgs& p) {
     if (p.Ah && p.K % 32 == 0 && gemm_dma_enabled()) return {GemmPlan::Dma, 0};
     if (p.swiglu || tiles > 10) return {GemmPlan::Lds, 0};
     if (p.Ah) throw std::runtime_error("gemm: pre-split A needs N > 160 or M <= 2048");
-    if (p.scale) return {GemmPlan::Stream, tiles};   // SE projects: A read once, all columns per workgroup
+    if (p.scale) {   // SE projects: A read once, all columns per workgroup -- unless that leaves the device idle
+        // measured per shape (one to four clips' blocks 4-15): the small-M kernel wins while the streaming grid
+        // (128 rows per workgroup) is under 128 workgroups (4,800 rows N 112: 15 vs 34 us; 9,600: 27 vs 34; 4,800
+        // rows N 160: 40 vs 63) or, for N <= 48, under 256 (18,400 rows N 40: 8.4 vs 10.5 us); above, streaming
+        // (19,200 rows N 112: 37 vs 45 us; 36,800 rows N 40: 13.7 vs 16.7)
+        const long long wgs = cdiv(p.M, 128);
+        if (wgs < 128 || (tiles <= 3 && wgs < 256)) return {GemmPlan::Small, 0};
+        return {GemmPlan::Stream, tiles};
+    }
     int nt = tiles;
     if (tiles > 5) {
         int best_cols = 1 << 30;
