@@ -1260,14 +1260,16 @@ constexpr int TAIL_K = 160, TAIL_N = 960, TAIL_XLD = TAIL_K + 8, TAIL_ELD = 16 +
 template <typename T>
 __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict__ X, const T* __restrict__ W,
                                                         long long wstride, const float* __restrict__ bias,
-                                                        float* __restrict__ out, int F) {
+                                                        float* __restrict__ out, int F, int ns) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
     constexpr int P = S::P;
     __shared__ __attribute__((aligned(16))) T Xs[P][64][TAIL_XLD];
     __shared__ float Es[4][64][TAIL_ELD];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
-    const long long f = blockIdx.x;
+    // ns workgroups per frame (few frames): workgroup `part` takes output tiles part * 4 + wave + 4 ns j
+    const long long f = blockIdx.x / ns;
+    const int part = int(blockIdx.x % ns), nt0 = part * 4 + wave, ntstep = 4 * ns;
     const float* Xf = X + f * 60 * TAIL_K;
     // stage: 64 rows x 40 float4 (rows 60..63 zero), split into the parts
     for (int i = tid; i < 64 * (TAIL_K / 4); i += 256) {
@@ -1295,9 +1297,9 @@ __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict_
             for (int q = 0; q < P; ++q)
                 dst[ks][q] = load_part8<T>(W + q * wstride + (long long)(nt * 16 + r) * TAIL_K + ks * 32 + g * 8);
     };
-    load_w(wave, w);
-    for (int nt = wave; nt < TAIL_N / 16; nt += 4) {
-        if (nt + 4 < TAIL_N / 16) load_w(nt + 4, wn);
+    load_w(nt0, w);
+    for (int nt = nt0; nt < TAIL_N / 16; nt += ntstep) {
+        if (nt + ntstep < TAIL_N / 16) load_w(nt + ntstep, wn);
         const float b = bias[nt * 16 + r];
         f32x4 acc[4];
 #pragma unroll
@@ -1504,8 +1506,11 @@ void launch_tail_pool(const float* x, const void* w, long long wstride, const fl
                       hipStream_t s) {
     if (F <= 0) return;
     if (wstride < (long long)TAIL_N * TAIL_K) throw std::runtime_error("tail_pool: bad weight part stride");
-    hipLaunchKernelGGL(tail_pool_kernel<T>, dim3((unsigned)F), dim3(256), 0, s, x, static_cast<const T*>(w), wstride,
-                       bias, pooled, F);
+    // workgroups per frame: a divisor of the 15 rounds of 4 tiles, so every wave gets whole tiles; one clip's 20
+    // frames ran 50 us in 20 workgroups
+    const int ns = F >= 256 ? 1 : F >= 86 ? 3 : F >= 52 ? 5 : 15;
+    hipLaunchKernelGGL(tail_pool_kernel<T>, dim3((unsigned)(F * ns)), dim3(256), 0, s, x, static_cast<const T*>(w),
+                       wstride, bias, pooled, F, ns);
 }
 template void launch_tail_pool<f16>(const float*, const void*, long long, const float*, float*, int, hipStream_t);
 template void launch_tail_pool<bf16>(const float*, const void*, long long, const float*, float*, int, hipStream_t);
