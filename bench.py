@@ -95,7 +95,9 @@ def cpu_baseline(weights: Path, clips: np.ndarray, seconds: float) -> dict | Non
                       f"repeated for {dt:.1f} s ({n} clips), {threads} threads (the box's CPU share for one GPU)"}
 
 
-def measured_traffic(kernel: str, revision: str) -> float | None:
+def measured_counters(kernel: str, revision: str) -> dict | None:
+    """The dominant family's PMC figures (profiles/roofline_traffic.json), when measured on this library revision:
+    HBM bytes per launch and, where recorded, the VALU / MFMA busy fractions of its SIMD cycles."""
     path = ROOT / "profiles" / "roofline_traffic.json"
     if not path.exists():
         return None
@@ -105,7 +107,7 @@ def measured_traffic(kernel: str, revision: str) -> float | None:
         return None
     if t.get("revision") != revision or t.get("family") != kernel:
         return None
-    return float(t["traffic_bytes_per_launch"])
+    return t
 
 
 # config 2: the pointwise GEMM through the C-ABI tool (bias + hardswish), every tier, on (set, name, M, N, K):
@@ -444,7 +446,8 @@ def roofline_of(stats: dict, steps: int, mode: str, revision: str, traffic_file:
     peak_tf = FP32_PEAK_TFLOPS if mode == "fp32" else MFMA_PEAK_TFLOPS
     ridge = peak_tf * 1e12 / (HBM_PEAK_GBS * 1e9)
     intensity = flops_l / bytes_l if bytes_l else 0.0
-    traffic = measured_traffic(dom, revision) if traffic_file else None
+    counters = measured_counters(dom, revision) if traffic_file else None
+    traffic = float(counters["traffic_bytes_per_launch"]) if counters else None
     if intensity < ridge:
         r = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
              "frac": round(gbs / HBM_PEAK_GBS, 4)}
@@ -457,6 +460,10 @@ def roofline_of(stats: dict, steps: int, mode: str, revision: str, traffic_file:
               "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "compute_frac": round(tflops / peak_tf, 4),
               "avg_launch_ms": round(avg_ms, 4), "launches_per_step": d["launches"] // steps,
               "ms_per_step": round(d["ms"] / steps, 4)})
+    # what issue-bound kernels are bound by: the fraction of SIMD cycles issuing VALU / MFMA work (PMC)
+    for k in ("valu_busy_frac", "mfma_busy_frac"):
+        if counters and k in counters:
+            r[k] = counters[k]
     return r
 
 
