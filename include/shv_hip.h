@@ -124,7 +124,9 @@ void shv_hip_host_free(void* p);
  * C++ tools (bench/gpu_kbench.cu:59-98, bench/gpu_dump.cu).  They serve benchmarks and parity tools that run the
  * forward on buffers already resident in HBM, without the scheduler or any host copy.
  * Device pointers only; `stream` is a hipStream_t (NULL = the model's compute stream).  Not thread-safe against
- * the model's own worker: call them only while no job is queued or running on `m`.
+ * the model's own worker: call them only while no job is queued or running on `m`.  The calls are asynchronous and
+ * share the model's activation buffers (and, in fp32, its small-GEMM workspace): calls on one model must run one
+ * after another on the device -- issue them on one stream, or synchronise between streams.
  */
 /* d_frames: n_clips*20 crops in device memory; d_logits: n_clips fp32 in device memory.  n_clips <= limits. */
 int shv_hip_forward_device(shv_hip_model* m, const uint8_t* d_frames, int n_clips, float* d_logits, void* stream);
