@@ -83,3 +83,28 @@ def test_delta_rule_kernels_against_oracle(shv, orc, weights):
     finally:
         for p in bufs + [d_o]:
             hip.free(p)
+
+
+
+@pytest.mark.gpu
+def test_delta_rule_fp32_row_independence(shv):
+    """A window's exact-tier recurrence does not depend on the other windows of the launch: the first 3 of 17 windows
+    equal the 3-window run bitwise (the 3-window run is pinned to the oracle by the test above)."""
+    n_big, n_small = 17, 3
+    q, k, v, dec, beta = inputs(n_big, 12)
+    hip = shv.Hip()
+    bufs = [hip.upload(x) for x in (q, k, v, dec, beta)]
+    d_big = hip.malloc(n_big * T * H * 128 * 4)
+    d_small = hip.malloc(n_small * T * H * 128 * 4)
+    try:
+        print(f"[gpu] fp32 delta rule: {n_big} windows vs {n_small}", flush=True)
+        shv.delta_rule("fp32", *bufs, n_big, d_big, 0)
+        shv.delta_rule("fp32", *bufs, n_small, d_small, 0)
+        hip.sync()
+        big = hip.download(d_big, (n_big * T, H * 128), np.float32)[:n_small * T]
+        small = hip.download(d_small, (n_small * T, H * 128), np.float32)
+        assert np.all(np.isfinite(small))
+        assert np.array_equal(big.view(np.uint32), small.view(np.uint32))
+    finally:
+        for p in bufs + [d_big, d_small]:
+            hip.free(p)
