@@ -93,18 +93,18 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs p) {
         for (int j = 0; j < 4; ++j) tot[i][j] = 0.0f;
     for (int k0 = 0; k0 < p.K; k0 += F32_BK) {
         const int kb = min(F32_BK, p.K - k0);
-        for (int i = tid; i < F32_BM * F32_BK; i += 256) {
-            const int r = i / F32_BK, k = i % F32_BK;
+        // only the block's kb columns are staged (and read below): narrow layers (K 16..40) stage a quarter to
+        // two thirds of the tile
+        for (int i = tid; i < F32_BM * kb; i += 256) {
+            const int r = i / kb, k = i - r * kb;
             const long long gm = m0 + r;
             const int gn = n0 + r, gk = k0 + k;
             float a = 0.0f, w = 0.0f;
-            if (k < kb) {
-                if (gm < p.M) {
-                    a = A[gm * p.lda + gk];
-                    if (SCALE) a = p.scale[(gm / p.scale_rows) * p.ld_scale + gk] * a;
-                }
-                if (gn < p.N) w = W[(long long)gn * p.ldw + gk];
+            if (gm < p.M) {
+                a = A[gm * p.lda + gk];
+                if (SCALE) a = p.scale[(gm / p.scale_rows) * p.ld_scale + gk] * a;
             }
+            if (gn < p.N) w = W[(long long)gn * p.ldw + gk];
             As[r][k] = a;
             Ws[r][k] = w;
         }
@@ -170,18 +170,16 @@ __global__ void __launch_bounds__(256) gemm_f32_kblock_kernel(GemmArgs p) {
     const int k0 = blockIdx.z * F32_BK, kb = min(F32_BK, p.K - k0);
     const float* A = p.A;
     const float* W = static_cast<const float*>(p.W);
-    for (int i = tid; i < F32_BM * F32_BK; i += 256) {
-        const int r = i / F32_BK, k = i % F32_BK;
+    for (int i = tid; i < F32_BM * kb; i += 256) {   // the block's kb columns, as the tiled kernel
+        const int r = i / kb, k = i - r * kb;
         const long long gm = m0 + r;
         const int gn = n0 + r, gk = k0 + k;
         float a = 0.0f, w = 0.0f;
-        if (k < kb) {
-            if (gm < p.M) {
-                a = A[gm * p.lda + gk];
-                if (SCALE) a = p.scale[(gm / p.scale_rows) * p.ld_scale + gk] * a;
-            }
-            if (gn < p.N) w = W[(long long)gn * p.ldw + gk];
+        if (gm < p.M) {
+            a = A[gm * p.lda + gk];
+            if (SCALE) a = p.scale[(gm / p.scale_rows) * p.ld_scale + gk] * a;
         }
+        if (gn < p.N) w = W[(long long)gn * p.ldw + gk];
         As[r][k] = a;
         Ws[r][k] = w;
     }
