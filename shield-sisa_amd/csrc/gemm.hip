@@ -1098,10 +1098,11 @@ void launch_stream_mt(const GemmArgs& p, hipStream_t s) {
     else
         hipLaunchKernelGGL((gemm_stream_kernel<T, NT, false, WPF, ST_MT>), dim3(blocks), dim3(64 * MFMA_WAVES), 0, s, p);
 }
-// rows per wave: 32 (measured against 16 and 64 rows on the SE-project shapes: 16 wins only for N <= 48, and there
-// by 5%; 64 spills at the widest tiles)
+// rows per wave: 32, or 16 for N <= 48 (blocks 4-6 on a 640-frame branch, 588,800 rows, N 40: fp16 62.6 vs 71.5 us
+// at K 72 and 112 vs 122.5 at K 120, bf16 78 vs 93 and 127-131 vs 139-140; 64 rows slower, and they spill at the
+// widest tiles)
 template <typename T, int NT>
-void launch_stream_nt(const GemmArgs& p, hipStream_t s) { launch_stream_mt<T, NT, 2>(p, s); }
+void launch_stream_nt(const GemmArgs& p, hipStream_t s) { launch_stream_mt<T, NT, (NT <= 3 ? 1 : 2)>(p, s); }
 
 template <typename T> void launch_stream(const GemmArgs& p, hipStream_t s) {
     if (p.Ah || p.Ch || p.swiglu) throw std::runtime_error("gemm_stream: fp32 A and C only, no SwiGLU");
