@@ -1506,8 +1506,9 @@ void launch_tail_pool(const float* x, const void* w, long long wstride, const fl
     if (F <= 0) return;
     if (wstride < (long long)TAIL_N * TAIL_K) throw std::runtime_error("tail_pool: bad weight part stride");
     // workgroups per frame: a divisor of the 15 rounds of 4 tiles, so every wave gets whole tiles; one clip's 20
-    // frames ran 50 us in 20 workgroups
-    const int ns = F >= 256 ? 1 : F >= 86 ? 3 : F >= 52 ? 5 : 15;
+    // frames ran 50 us in 20 workgroups, and three per frame also balance the batch-128 branches (640 frames: fp16
+    // 83 vs 86 us, bf16 110 vs 115; 320 frames: 43 vs 48, 57 vs 65; five per frame slower)
+    const int ns = F >= 1024 ? 1 : F >= 86 ? 3 : F >= 52 ? 5 : 15;
     hipLaunchKernelGGL(tail_pool_kernel<T>, dim3((unsigned)(F * ns)), dim3(256), 0, s, x, static_cast<const T*>(w),
                        wstride, bias, pooled, F, ns);
 }
