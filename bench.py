@@ -43,7 +43,7 @@ MFMA_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 / bf16 matrix cores
 FP32_PEAK_TFLOPS = 157.3        # MI355X fp32 vector
 REF_B128_CLIPS_PER_S = 128 / 0.191   # reference README.md:118 (RTX A6000, batch 128 FP16)
 # families of the sequence stages (config 3): the role before ":" for GEMMs
-SEQ_ROLES = {"assemble", "rmsnorm", "gemm_seq", "gdn_prep", "delta", "gated_norm", "sisa", "gemm_f32_small", "head"}
+SEQ_ROLES = {"window_input", "rmsnorm", "gemm_seq", "gdn_prep", "delta", "gated_norm", "sisa", "gemm_f32_small", "head"}
 
 
 def load_shv():

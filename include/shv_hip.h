@@ -147,12 +147,13 @@ int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir);
 /* Pointwise-conv GEMM microbench.  No counterpart in shv_cuda.h: the reference benches its GEMM from a C++ tool
  * (bench/gpu_gemm_bench.cu:27-116: engine GEMM on the model's 1x1 shapes, and a bitwise check that every kernel
  * variant gives the same outputs).  C[m][n] = act(A[m][k] . W[n][k]^T + bias[n]) in the arithmetic of `mode`
- * ("fp32": exact VALU order of the CPU engine; "fp16" / "bf16": split-operand MFMA), fp32 A, W, bias and C in
+ * ("fp32": fp32 matrix cores, or the CPU engine's VALU order; "fp16" / "bf16": split-operand MFMA), fp32 A, W, bias and C in
  * device memory, row-major with leading dimensions k (A, W) and n (C).  act: the reference's codes
  * (engine/cuda/common.cuh:69): 0 none, 1 ReLU, 2 hardswish, 3 SiLU, 4 hardsigmoid.  d_bias may be NULL.
  * create repacks W on the device (synchronising `stream`); NULL + last_error on failure (fp16 / bf16 need k % 8 == 0).
- * run: variant 0 = the engine's own kernel choice; fp32: 1 GEMV, 2 tiled, 3 K blocks in parallel (allocates its
- * workspace of ceil(k / 64) * m * n floats and synchronises `stream`); fp16 / bf16: 1 small-M, 2..6 direct with
+ * run: variant 0 = the engine's own kernel choice; fp32: 1 GEMV, 2 tiled, 3 K blocks in parallel (1-3: the CPU
+ * engine's operation order; 3 allocates its workspace of ceil(k / 64) * m * n floats and synchronises `stream`),
+ * 4 the fp32 matrix cores (k % 4 == 0), 5 row per lane (CPU order, k % 4 == 0); fp16 / bf16: 1 small-M, 2..6 direct with
  * 1..5 column tiles per wave, 7 LDS-staged, 8 streaming (n <= 160).  Returns 0, or -1 + last_error.  Asynchronous on
  * `stream` except fp32 variant 3. */
 typedef struct shv_hip_gemm shv_hip_gemm;
@@ -191,9 +192,11 @@ int shv_hip_native_crops_i420(const shv_hip_i420_image* frames, const shv_hip_re
  * the reference runs its delta_kernel only inside classify, engine/cuda/seq.cu:106-195).  Per window 321 rows; rows
  * = n_windows * 321: q, k [rows][384] (6 heads x 64, l2-normalised; q scaled), v, o [rows][768] (6 heads x 128),
  * decay, beta [rows][8] (head h in column h).  Per (window, head): S_0 = 0, S_t = a_t S_{t-1} + k_t u_t^T,
- * u_t = b_t (v_t - a_t S_{t-1}^T k_t), o_t = S_t^T q_t.  variant 0: the tier's own kernel (fp32: token by token in
- * the reference's order; fp16 / bf16: the chunked scan), 1: token by token, 2: chunked (fp16 / bf16).  Synchronous
- * for the chunked scan (it allocates a work buffer per call).  Returns 0, or -1 + last_error. */
+ * u_t = b_t (v_t - a_t S_{t-1}^T k_t), o_t = S_t^T q_t.  variant 0: the tier's own kernel (fp32: token by token
+ * with each value column's keys split over lane groups, or in the reference's order when SHV_HIP_F32_CPU_ORDER=1;
+ * fp16 / bf16: the chunked scan), 1: token by token (fp32: the reference's order; fp16 / bf16: key split),
+ * 2: chunked (fp16 / bf16), 3: key split (every tier).  Synchronous for the chunked scan (it allocates a work buffer
+ * per call).  Returns 0, or -1 + last_error. */
 int shv_hip_delta_rule(const char* mode, const float* d_q, const float* d_k, const float* d_v, const float* d_decay,
                        const float* d_beta, int n_windows, float* d_o, int variant, void* stream);
 
@@ -231,8 +234,9 @@ size_t shv_hip_audio_device_bytes(const shv_hip_audio* a);
 /* n windows of host tokens (window w at tokens + w * stride floats, stride >= 48000) -> logits[n] (host);
  * synchronous, any n (batches of max_windows) */
 int shv_hip_audio_sequence(shv_hip_audio* a, const float* tokens, size_t n, size_t stride, float* logits);
-/* the same on device buffers, asynchronous on `stream` (NULL = the handle's own stream), n <= max_windows;
- * d_tokens 16-byte aligned, stride a multiple of 4 */
+/* the same on device buffers, asynchronous on `stream` (NULL = the handle's own stream), n <= max_windows.  The
+ * calls of one handle share its activation buffers: each call's device work starts after the previous call's has
+ * ended, whatever streams they were issued on (an event of the handle orders them). */
 int shv_hip_audio_sequence_device(shv_hip_audio* a, const float* d_tokens, int n, size_t stride, float* d_logits,
                                   void* stream);
 /* per-kernel-family timing and stage dumps, as shv_hip_profile_* / shv_hip_set_dump_dir (dump names: tokens, gdn_a,

@@ -35,9 +35,12 @@ public:
             SHV_HIP_CHECK(hipMemset(d_tokens_, 0, size_t(max_windows) * kAudioWindowFloats * 4));
             SHV_HIP_CHECK(hipStreamCreateWithFlags(&work_, hipStreamNonBlocking));
             SHV_HIP_CHECK(hipStreamCreateWithFlags(&capture_, hipStreamNonBlocking));
+            SHV_HIP_CHECK(hipEventCreateWithFlags(&last_done_, hipEventDisableTiming));
+            SHV_HIP_CHECK(hipEventRecord(last_done_, work_));
         } catch (...) {
             (void)hipStreamSynchronize(setup_);
             (void)hipStreamDestroy(setup_);
+            if (last_done_) (void)hipEventDestroy(last_done_);
             if (work_) (void)hipStreamDestroy(work_);
             if (capture_) (void)hipStreamDestroy(capture_);
             throw;
@@ -48,28 +51,32 @@ public:
         device_bytes_ = wmem_.bytes() + amem_.bytes();
     }
     ~AudioEngineT() override {
+        if (last_done_) (void)hipEventSynchronize(last_done_);
         for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
+        if (last_done_) (void)hipEventDestroy(last_done_);
         if (work_) (void)hipStreamSynchronize(work_);
         if (work_) (void)hipStreamDestroy(work_);
         if (capture_) (void)hipStreamDestroy(capture_);
     }
 
+    // Every call of one handle uses the same activation buffers, so each call's device work starts after the
+    // previous call's has ended, whatever streams the two were issued on: a call waits on last_done_ on its stream
+    // and records last_done_ there at its end.  A NULL stream is the handle's own.
     void run_device(const float* d_tokens, long long ldw, int n, float* d_logits, hipStream_t s) override {
         if (n <= 0) return;
         if (n > max_windows_) throw std::runtime_error("audio: more windows than max_windows");
         if (!d_tokens || !d_logits) throw std::runtime_error("audio: null buffer");
-        run_graph(Key{d_tokens, ldw, d_logits, n}, s, [&](hipStream_t q) {
-            timed("assemble", double(n) * kTAudio * kD * 8, q,
-                  [&] { launch_assemble_audio(d_tokens, ldw, readout_, seq_->h(), n, q); });
-            check_launch();
-            seq_->run(n, d_logits, q, *this, dump_dir_);
-        });
+        const hipStream_t q = s ? s : work_;
+        SHV_HIP_CHECK(hipStreamWaitEvent(q, last_done_, 0));
+        forward(d_tokens, ldw, n, d_logits, q);
+        SHV_HIP_CHECK(hipEventRecord(last_done_, q));
     }
 
     void run_host(const float* tokens, long long ldw, long long n, float* logits) override {
         if (n <= 0) return;
         if (!tokens || !logits) throw std::runtime_error("audio: null buffer");
         if (ldw < kAudioWindowFloats) throw std::runtime_error("audio: window stride below 48000 floats");
+        SHV_HIP_CHECK(hipStreamWaitEvent(work_, last_done_, 0));
         for (long long w0 = 0; w0 < n; w0 += max_windows_) {
             const int b = int(std::min<long long>(max_windows_, n - w0));
             if (ldw == kAudioWindowFloats) {
@@ -83,8 +90,9 @@ public:
             // graphs are keyed by the window count: host batches run padded to a multiple of 8 windows (the padding
             // windows compute on stale tokens and are not copied back)
             const int bp = use_graphs_ ? std::min(max_windows_, (b + 7) / 8 * 8) : b;
-            run_device(d_tokens_, kAudioWindowFloats, bp, d_logits_, work_);
+            forward(d_tokens_, kAudioWindowFloats, bp, d_logits_, work_);
             SHV_HIP_CHECK(hipMemcpyAsync(logits + w0, d_logits_, size_t(b) * 4, hipMemcpyDeviceToHost, work_));
+            SHV_HIP_CHECK(hipEventRecord(last_done_, work_));
             SHV_HIP_CHECK(hipStreamSynchronize(work_));
         }
     }
@@ -101,11 +109,22 @@ private:
     hipStream_t setup_ = nullptr, work_ = nullptr;
     // graphs are captured on this private stream, then launched on the caller's
     hipStream_t capture_ = nullptr;
+    hipEvent_t last_done_ = nullptr;   // the end of the latest call's device work
     DevMem wmem_, amem_;
     std::unique_ptr<SeqStack<G>> seq_;
     const float* readout_ = nullptr;
     float *d_tokens_ = nullptr, *d_logits_ = nullptr;
     std::map<Key, hipGraphExec_t> graphs_;
+
+    void forward(const float* d_tokens, long long ldw, int n, float* d_logits, hipStream_t q) {
+        run_graph(Key{d_tokens, ldw, d_logits, n}, q, [&](hipStream_t r) {
+            WindowInput in;
+            in.tokens = d_tokens;
+            in.ldw = ldw;
+            in.readout = readout_;
+            seq_->run(in, n, d_logits, r, *this, dump_dir_);
+        });
+    }
 
     template <class F> void run_graph(const Key& key, hipStream_t s, F&& body) {
         auto it = graphs_.find(key);

@@ -40,13 +40,13 @@ std::string certificate_problem(const std::string& weights, const std::string& s
                                 double threshold, const std::string& revision) {
     const std::string path = weights + ".hip.cert";
     std::ifstream in(path);
-    if (!in) return "mode " + mode + " needs a quality certificate: " + path + " not found";
+    if (!in) return "mode " + mode + " is uncertified: no certificate file at " + path;
     std::vector<std::string> lines;
     for (std::string l; std::getline(in, l);) lines.push_back(l);
-    if (lines.empty()) return "empty certificate file " + path;
+    if (lines.empty()) return "certificate file " + path + " is empty";
     std::string head = lines[0];
     head.erase(head.find_last_not_of(" \r\t") + 1);
-    if (head != "SHIELDV_HIP_CERT_V2") return "invalid certificate file " + path + " (expected SHIELDV_HIP_CERT_V2)";
+    if (head != "SHIELDV_HIP_CERT_V2") return "certificate file " + path + " lacks the SHIELDV_HIP_CERT_V2 header line";
 
     bool named = false;
     double named_threshold = std::nan("");
@@ -59,14 +59,14 @@ std::string certificate_problem(const std::string& weights, const std::string& s
         named_threshold = t;
     }
     if (named) {
-        char nums[128];
-        std::snprintf(nums, sizeof nums, "certified threshold %.17g, loaded threshold %.17g", named_threshold,
+        char nums[160];
+        std::snprintf(nums, sizeof nums, "certified for threshold %.17g, the sidecar sets %.17g", named_threshold,
                       threshold);
-        return "mode " + mode + " certificate in " + path + " does not cover the threshold in " + weights +
-               ".json (" + nums + ")";
+        return "mode " + mode + " is uncertified at this threshold: certificate file " + path + " " + nums + " (" +
+               weights + ".json)";
     }
-    return "mode " + mode + " has no passing certificate for weights " + sha + " at compute revision " + revision +
-           " in " + path;
+    return "mode " + mode + " is uncertified: certificate file " + path + " has no PASS line for weights " + sha +
+           " at revision " + revision;
 }
 
 }  // namespace shv

@@ -61,8 +61,8 @@ stem_tile_kernel(const uint8_t* __restrict__ in, float* __restrict__ out, const 
 #pragma unroll
     for (int o = 0; o < 16; ++o) v[o] = hswish(acc[o] + b[o]);
     float* dst = out + (((size_t)blockIdx.z * 90 + oy0 + ty) * 160 + ox0 + tx) * 16;
-    store8(dst, v);
-    store8(dst + 8, v + 8);
+    write8(dst, v);
+    write8(dst + 8, v + 8);
 }
 
 // ------------------------------------------------------------------------------------------------ depthwise
@@ -154,29 +154,39 @@ se_pool_kernel(const T* __restrict__ x, float* __restrict__ pooled, int Ho, int 
 }
 
 // ------------------------------------------------------------------------------------------------ 4x4 pool
-// token t = r*4 + c over rows {0,1,3,4}[r]+[0,2), cols {0,2,5,7}[c]+[0,3): sum from +0, then (acc / 2) / 3
+// Adaptive 6x10 -> 4x4 average pool (overlapping bins: rows {0,1,3,4}[r] + [0,2), columns {0,2,5,7}[c] + [0,3)).
+// A workgroup owns one frame and a PL_CH-channel slice: it stages the slice of all 60 pixels in LDS with 16-byte
+// loads (every input value leaves HBM once, although the bins overlap), then each thread sums bins from LDS.  Per
+// output: +0, then the 6 values row by row, left to right, then (acc / 2) / 3 -- the reference CPU engine's
+// operation order (engine/model/isa_impl.hpp:836-842).
+constexpr int PL_CH = 240;   // channels per workgroup: 960 / 4, 57.6 KB of LDS
 template <typename T>
-__global__ void __launch_bounds__(256) pool_kernel(const T* __restrict__ in, T* __restrict__ out, int F) {
-    constexpr int CG = 960 / 8;
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long long)F * 16 * CG) return;
-    const int cg = int(idx % CG), tok = int((idx / CG) % 16);
-    const long long f = idx / (16 * CG);
-    const int r0 = ((tok >> 2) * 3) >> 1;   // floor(r * 6 / 4): 0, 1, 3, 4
-    const int c0 = ((tok & 3) * 5) >> 1;    // floor(c * 10 / 4): 0, 2, 5, 7
-    float acc[8];
+__global__ void __launch_bounds__(256) pool_kernel(const T* __restrict__ in, T* __restrict__ out) {
+    __shared__ float tile[60 * PL_CH];
+    const long long f = blockIdx.x;
+    const int c0 = blockIdx.y * PL_CH;
+    const T* src = in + f * 60 * 960 + c0;
+    constexpr int V4 = PL_CH / 4;   // 16-byte pieces per pixel
+    for (int i = threadIdx.x; i < 60 * V4; i += 256) {
+        const int px = i / V4, q = i % V4;
+        float v[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int y = r0; y < r0 + 2; ++y)
-        for (int x = c0; x < c0 + 3; ++x) {
-            float v[8];
-            load8(in + ((f * 6 + y) * 10 + x) * 960 + cg * 8, v);
+        for (int e = 0; e < 4; ++e) v[e] = to_f(src[px * 960 + q * 4 + e]);
+        *reinterpret_cast<float4*>(&tile[px * PL_CH + q * 4]) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    __syncthreads();
+    T* dst = out + f * 16 * 960 + c0;
+    for (int o = threadIdx.x; o < 16 * PL_CH; o += 256) {
+        const int tok = o / PL_CH, c = o % PL_CH;
+        const int y0 = ((tok >> 2) * 3) >> 1;   // floor(r * 6 / 4)
+        const int x0 = ((tok & 3) * 5) >> 1;    // floor(c * 10 / 4)
+        float acc = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
-        }
+        for (int dy = 0; dy < 2; ++dy)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = (acc[i] / 2.0f) / 3.0f;
-    store8(out + (f * 16 + tok) * 960 + cg * 8, acc);
+            for (int dx = 0; dx < 3; ++dx) acc = acc + tile[((y0 + dy) * 10 + x0 + dx) * PL_CH + c];
+        dst[tok * 960 + c] = from_f<T>((acc / 2.0f) / 3.0f);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ repack
@@ -256,7 +266,7 @@ template <typename T> void launch_se_pool(const T* x, float* pooled, int F, int 
 }
 
 template <typename T> void launch_pool(const T* in, T* out, int F, hipStream_t s) {
-    hipLaunchKernelGGL(pool_kernel<T>, dim3(cdiv((long long)F * 16 * 120, 256)), dim3(256), 0, s, in, out, F);
+    hipLaunchKernelGGL(pool_kernel<T>, dim3((unsigned)F, 960 / PL_CH), dim3(256), 0, s, in, out);
 }
 
 template <typename T>

@@ -105,27 +105,21 @@ __device__ __forceinline__ float apply_act(float v, int act) {
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float logsigmoid_f(float x) { return (x < 0.0f ? x : 0.0f) - log1pf(expf(-fabsf(x))); }
 
-// 8 consecutive storage elements <-> 8 floats (16-byte access for half types, 2 x 16 bytes for float)
-template <typename T> __device__ __forceinline__ void load8(const T* p, float* v) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const T* h = reinterpret_cast<const T*>(&u);
+// Eight consecutive storage elements as eight floats, moved as one vector: 16 bytes for the half types, 32 for fp32
+// (the pointer is 16-byte aligned; the vector type says so, so fp32 goes as two 16-byte accesses).  Widening is
+// exact; narrowing rounds to nearest even, as from_f.
+template <typename T> struct Row8 { typedef T type __attribute__((ext_vector_type(8), aligned(16))); };
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+template <typename T> __device__ __forceinline__ void read8(const T* p, float* v) {
+    const f32x8 x = __builtin_convertvector(*reinterpret_cast<const typename Row8<T>::type*>(p), f32x8);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = to_f(h[i]);
+    for (int i = 0; i < 8; ++i) v[i] = x[i];
 }
-template <> __device__ __forceinline__ void load8<float>(const float* p, float* v) {
-    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-template <typename T> __device__ __forceinline__ void store8(T* p, const float* v) {
-    uint4 u;
-    T* h = reinterpret_cast<T*>(&u);
+template <typename T> __device__ __forceinline__ void write8(T* p, const float* v) {
+    f32x8 x;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = from_f<T>(v[i]);
-    *reinterpret_cast<uint4*>(p) = u;
-}
-template <> __device__ __forceinline__ void store8<float>(float* p, const float* v) {
-    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    for (int i = 0; i < 8; ++i) x[i] = v[i];
+    *reinterpret_cast<typename Row8<T>::type*>(p) = __builtin_convertvector(x, typename Row8<T>::type);
 }
 
 // Sums over a 16-lane row with the fixed tree ((l_i + l_i+8) + (.. +4)) + (.. +2) + (.. +1) of the reference vector

@@ -134,6 +134,10 @@ public:
         // half tiers run the fused inverted-residual kernels unless SHV_HIP_NO_FUSE is set (layer-by-layer A/B)
         const char* nf = std::getenv("SHV_HIP_NO_FUSE");
         fused_ = !kF32 && !(nf && *nf && std::strcmp(nf, "0") != 0);
+        // the exact tier's CNN keeps the reference CPU order in every case: with the seeded random-init weights
+        // the encoder amplifies a reordered fp32 sum ~30x into the logit (fp32 matrix-core 1x1 convs moved logits
+        // by 8.1e-4, twice the exact tier's 4e-4 bar); the sequence stages take the engine's own order (SeqStack)
+        cpu_order_ = kF32;
         SHV_HIP_CHECK(hipStreamCreateWithFlags(&setup_, hipStreamNonBlocking));
         try {
             Uploader upl(wmem_, setup_);
@@ -347,6 +351,7 @@ private:
         return a;
     }
     bool fused_ = false;
+    bool cpu_order_ = false;   // the CNN GEMMs in the reference CPU engine's operation order (fp32 tier)
     // Every encode (encode_direct, the scheduler's encode_slot) runs its frames as up to kBranches independent
     // branches on their own streams (forked from and joined to the caller's stream, inside one graph): while one
     // branch's latency-bound kernels and launch tails run, another's fill the device (measured 21.2 -> 20.2 ms per
@@ -415,7 +420,7 @@ private:
             sl.d_tok_stage = amem_.make<float>(std::max<size_t>(size_t(cfg_.max_host_tokens), 1) * kTokenFloats);
             sl.d_tokptr = amem_.make<const float*>(Bm * kFrames);
             sl.d_logits = amem_.make<float>(Bm);
-            sl.d_store = amem_.make<int32_t>(Fm);
+            sl.d_store = amem_.make<int32_t>(2 * Fm);
             // every table entry starts valid: padding windows of a bucket read it
             std::vector<const float*> init(Bm * kFrames, sl.d_tokens);
             SHV_HIP_CHECK(hipMemcpy(sl.d_tokptr, init.data(), init.size() * sizeof(float*), hipMemcpyHostToDevice));
@@ -459,10 +464,10 @@ private:
 
     // GEMM in this engine's flavour, and the exact fp32 VALU kernel for the fp32-only layers
     void gemm(const char* role, const GemmArgs& p, const DevW& w, hipStream_t s) {
-        GemmRunner<G>{*this, cur_ws(), ws_floats_}.gemm(role, p, w, s);
+        GemmRunner<G>{*this, cur_ws(), ws_floats_, cpu_order_}.gemm(role, p, w, s);
     }
     void gemm32(const char* role, const GemmArgs& p, hipStream_t s) {
-        GemmRunner<G>{*this, cur_ws(), ws_floats_}.gemm32(role, p, s);
+        GemmRunner<G>{*this, cur_ws(), ws_floats_, cpu_order_}.gemm32(role, p, s);
     }
 
     // ---------------------------------------------------------------- CNN
@@ -713,31 +718,50 @@ private:
     // ---------------------------------------------------------------- sequence
     // windows [w0, w0 + B) of the sequence buffers
     void run_classify(const float* const* tokptr, int B, float* logits, hipStream_t s, int w0) {
-        timed("assemble", double(B) * kT * kD * 8, s,
-              [&] { launch_assemble(tokptr, pos_, readout_, seq_->h(w0), B, s); });
-        check_launch();
-        seq_->run(B, logits, s, *this, dump_dir_, w0, cur_ws(), ws_floats_);
+        WindowInput in;
+        in.frame_tokens = tokptr;
+        in.pos = pos_;
+        in.readout = readout_;
+        seq_->run(in, B, logits, s, *this, dump_dir_, w0, cur_ws(), ws_floats_);
     }
 };
 
 }  // namespace
 
+namespace {
+// Device memory for one call, released when the call leaves (by return or exception) once the stream it was used
+// on has drained, since kernels queued on it may still read it.
+class CallBuffer {
+public:
+    CallBuffer(size_t bytes, hipStream_t s) : s_(s) { SHV_HIP_CHECK(hipMalloc(&p_, bytes)); }
+    ~CallBuffer() {
+        (void)hipStreamSynchronize(s_);
+        (void)hipFree(p_);
+    }
+    CallBuffer(const CallBuffer&) = delete;
+    CallBuffer& operator=(const CallBuffer&) = delete;
+    void* get() const { return p_; }
+
+private:
+    void* p_ = nullptr;
+    hipStream_t s_;
+};
+}  // namespace
+
 void run_delta_rule(Precision p, const float* Q, const float* K, const float* V, const float* dec, const float* beta,
                     int n_windows, float* O, int variant, hipStream_t s) {
-    if (!delta_rule_is_chunked(p, Q, K, V, dec, beta, n_windows, O, variant)) {
-        launch_delta(Q, K, V, dec, beta, O, n_windows, p == Precision::FP32, s);
+    const DeltaKernel kern = delta_rule_kernel(p, Q, K, V, dec, beta, n_windows, O, variant);
+    if (kern != DeltaKernel::Chunked) {
+        launch_delta(Q, K, V, dec, beta, O, n_windows, kern == DeltaKernel::Reference, s);
         SHV_HIP_CHECK(hipGetLastError());
         return;
     }
-    float* work = nullptr;
-    SHV_HIP_CHECK(hipMalloc(&work, delta_chunk_floats(n_windows) * sizeof(float)));
+    const CallBuffer buf(delta_chunk_floats(n_windows) * sizeof(float), s);
+    float* work = static_cast<float*>(buf.get());
     if (p == Precision::BF16) launch_delta_chunked<bf16>(Q, K, V, dec, beta, O, work, n_windows, s);
     else launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s);
-    const hipError_t le = hipGetLastError();
-    const hipError_t se = hipStreamSynchronize(s);
-    (void)hipFree(work);
-    SHV_HIP_CHECK(le);
-    SHV_HIP_CHECK(se);
+    SHV_HIP_CHECK(hipGetLastError());
+    SHV_HIP_CHECK(hipStreamSynchronize(s));
 }
 
 PwGemm::PwGemm(Precision p, int N, int K, const float* d_w, hipStream_t s) : prec_(p), N_(N), K_(K) {
@@ -771,15 +795,19 @@ void PwGemm::run(const float* A, long long M, const float* bias, int act, float*
     p.W = w_; p.ldw = K_; p.wstride = wstride_;
     p.bias = bias; p.act = kAct[act];
     p.C = C; p.ldc = N_;
+    if (prec_ == Precision::FP32 && variant == 4) {
+        gemm_f32_mfma(p, s);
+        SHV_HIP_CHECK(hipGetLastError());
+        return;
+    }
     if (prec_ == Precision::FP32 && variant == 3) {   // K blocks in parallel: a workspace for this call
         const size_t ws = size_t((K_ + 63) / 64) * size_t(M) * size_t(N_);
-        SHV_HIP_CHECK(hipMalloc(&p.ws, ws * sizeof(float)));
+        const CallBuffer buf(ws * sizeof(float), s);
+        p.ws = static_cast<float*>(buf.get());
         p.ws_floats = (long long)ws;
         gemm_f32_variant(p, s, variant);
-        const hipError_t le = hipGetLastError(), se = hipStreamSynchronize(s);
-        (void)hipFree(p.ws);
-        SHV_HIP_CHECK(le);
-        SHV_HIP_CHECK(se);
+        SHV_HIP_CHECK(hipGetLastError());
+        SHV_HIP_CHECK(hipStreamSynchronize(s));
         return;
     }
     switch (prec_) {
@@ -790,13 +818,21 @@ void PwGemm::run(const float* A, long long M, const float* bias, int act, float*
     SHV_HIP_CHECK(hipGetLastError());
 }
 
+// One engine flavour per precision: the exact VALU tier, or the split-operand MFMA tiers with two (fp16) or three
+// (bf16) operand parts.
+template <typename G> std::unique_ptr<Engine> engine_of(const HostModel& hm, Precision p, const EngineConfig& cfg) {
+    return std::unique_ptr<Engine>(new EngineT<G>(hm, p, cfg));
+}
+
 std::unique_ptr<Engine> make_engine(const HostModel& hm, Precision p, const EngineConfig& cfg) {
-    switch (p) {
-    case Precision::FP32: return std::unique_ptr<Engine>(new EngineT<float>(hm, p, cfg));
-    case Precision::BF16: return std::unique_ptr<Engine>(new EngineT<bf16>(hm, p, cfg));
-    case Precision::FP16: return std::unique_ptr<Engine>(new EngineT<f16>(hm, p, cfg));
-    }
-    throw std::runtime_error("unknown precision");
+    using Factory = std::unique_ptr<Engine> (*)(const HostModel&, Precision, const EngineConfig&);
+    struct Flavour { Precision p; Factory make; };
+    static const Flavour flavours[] = {{Precision::FP32, engine_of<float>},
+                                       {Precision::BF16, engine_of<bf16>},
+                                       {Precision::FP16, engine_of<f16>}};
+    for (const Flavour& f : flavours)
+        if (f.p == p) return f.make(hm, p, cfg);
+    throw std::runtime_error("engine: no kernel flavour for precision code " + std::to_string(int(p)));
 }
 
 }  // namespace shv

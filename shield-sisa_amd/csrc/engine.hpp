@@ -5,6 +5,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+#include <cstring>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -19,6 +21,17 @@
     } while (0)
 
 namespace shv {
+
+// The exact tier's arithmetic in the sequence stages.  The CNN always performs the reference CPU engine's operation
+// order (its tokens are bitwise the reference's).  By default the all-row sequence GEMMs run on the fp32 matrix cores
+// and the delta rule splits each value column's keys over lane groups (fp32 values and operations, in an order of
+// this engine's own); SHV_HIP_F32_CPU_ORDER=1 at load keeps the reference's order there too (VALU GEMMs in K blocks
+// of 64, the 64-key fma chains), so that every stage output is the reference's: the check that pins the sequence
+// stage code to the reference.
+inline bool f32_cpu_order_requested() {
+    const char* e = std::getenv("SHV_HIP_F32_CPU_ORDER");
+    return e && *e && std::strcmp(e, "0") != 0;
+}
 
 enum class Precision { FP32 = 0, BF16 = 1, FP16 = 2 };
 const char* precision_name(Precision p);
@@ -87,7 +100,7 @@ public:
         float* d_tok_stage = nullptr;     // [max(max_host_tokens,1)][6144]
         const float** d_tokptr = nullptr; // [max_windows * 20]
         float* d_logits = nullptr;        // [max_windows]
-        int32_t* d_store = nullptr;       // [max_frames]
+        int32_t* d_store = nullptr;       // [max_frames][2]: (batch frame, pool slot) of each storing frame
     };
     virtual ~Engine() = default;
 
@@ -139,14 +152,24 @@ void run_delta_rule(Precision p, const float* Q, const float* K, const float* V,
 constexpr int kDeltaNoAllocWindows = 16;
 void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const float* V, const float* dec,
                             const float* beta, int n_windows, float* O, int variant, hipStream_t s);
-// Validates the arguments of both; true when they select the chunked scan.
-inline bool delta_rule_is_chunked(Precision p, const float* Q, const float* K, const float* V, const float* dec,
-                                  const float* beta, int n_windows, const float* O, int variant) {
+// The kernel a delta-rule call runs: the chunked scan (fp16 / bf16), token by token with each value column's keys
+// split over lane groups in one canonical order (every tier), or token by token in the reference CPU engine's order
+// (fp32).  variant 0 = the tier's own (fp32: key split, or the reference order under SHV_HIP_F32_CPU_ORDER; half
+// tiers: chunked), 1 = token by token (fp32: the reference order; half tiers: key split), 2 = chunked (half tiers),
+// 3 = key split.  Validates the arguments.
+enum class DeltaKernel { Chunked, KeySplit, Reference };
+inline DeltaKernel delta_rule_kernel(Precision p, const float* Q, const float* K, const float* V, const float* dec,
+                                     const float* beta, int n_windows, const float* O, int variant) {
     if (!Q || !K || !V || !dec || !beta || !O || n_windows < 1 || n_windows > 65536)
         throw std::runtime_error("delta rule: null buffer or bad window count");
-    if (variant < 0 || variant > 2 || (p == Precision::FP32 && variant == 2))
+    if (variant < 0 || variant > 3 || (p == Precision::FP32 && variant == 2))
         throw std::runtime_error("delta rule: unknown variant for this mode");
-    return p != Precision::FP32 && variant != 1;
+    if (variant == 3) return DeltaKernel::KeySplit;
+    if (p == Precision::FP32) {
+        if (variant == 1) return DeltaKernel::Reference;
+        return f32_cpu_order_requested() ? DeltaKernel::Reference : DeltaKernel::KeySplit;
+    }
+    return variant == 1 ? DeltaKernel::KeySplit : DeltaKernel::Chunked;
 }
 
 class PwGemm {
@@ -155,7 +178,9 @@ public:
     ~PwGemm();
     PwGemm(const PwGemm&) = delete;
     PwGemm& operator=(const PwGemm&) = delete;
-    // variant: kernel choice (0 = the engine's own); see gemm_f32_variant / gemm_mfma_variant
+    // variant: kernel choice (0 = the engine's own: for fp32 the CNN's, the reference CPU order); see
+    // gemm_f32_variant / gemm_mfma_variant; fp32 4 = the fp32 matrix cores (gemm_f32_mfma, the sequence stages'
+    // kernel)
     void run(const float* A, long long M, const float* bias, int act, float* C, int variant, hipStream_t s) const;
     Precision precision() const { return prec_; }
 

@@ -236,6 +236,188 @@ __global__ void __launch_bounds__(256) gemm_f32_fold_kernel(GemmArgs p, int nkb)
     p.C[m * p.ldc + j] = epi_value(p, fold(j), b, r);
 }
 
+// Exact tier, many rows and few columns (the early and middle 1x1 layers): one lane per row, one wave per 64 rows x
+// NC columns.  Per K block of 64 the wave stages its columns' weights in LDS ([NC][16] float4, read back as
+// broadcasts: every lane reads the same address) and its row's A values in registers (16-byte loads), then runs
+// the reference's per-output sequence -- an fma chain from +0 in increasing k, the first block's chain taken as
+// is and later ones added in order -- and the epilogue: bitwise gemm_f32_kernel's results, without staging a
+// 64-wide tile for layers of 16 to 128 columns or re-reading the K block through LDS for every 4 x 4 outputs.
+// K, lda, ldw (and ld_scale) multiples of 4, 16-byte aligned A, W, scale.
+template <int NC, bool SCALE>
+__global__ void __launch_bounds__(64) gemm_f32_rows_kernel(GemmArgs p) {
+    __shared__ float4 wsh[NC][F32_BK / 4];
+    const int lane = threadIdx.x;
+    const long long m = (long long)blockIdx.x * 64 + lane;
+    const int n0 = blockIdx.y * NC;
+    const bool live = m < p.M;
+    const long long mc = live ? m : p.M - 1;
+    const float* arow = p.A + mc * p.lda;
+    const float* srow = SCALE ? p.scale + (mc / p.scale_rows) * p.ld_scale : nullptr;
+    const float* W = static_cast<const float*>(p.W);
+    float tot[NC];
+    for (int k0 = 0; k0 < p.K; k0 += F32_BK) {
+        const int kb = min(F32_BK, p.K - k0);   // a multiple of 4
+        __syncthreads();                         // the previous block's weights have been read
+        for (int i = lane; i < NC * (F32_BK / 4); i += 64) {
+            const int j = i / (F32_BK / 4), q = i % (F32_BK / 4);
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (n0 + j < p.N && 4 * q < kb) v = *reinterpret_cast<const float4*>(W + (long long)(n0 + j) * p.ldw + k0 + 4 * q);
+            wsh[j][q] = v;
+        }
+        float a[F32_BK];
+#pragma unroll
+        for (int q = 0; q < F32_BK / 4; ++q) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (4 * q < kb) {
+                v = *reinterpret_cast<const float4*>(arow + k0 + 4 * q);
+                if (SCALE) {
+                    const float4 sc = *reinterpret_cast<const float4*>(srow + k0 + 4 * q);
+                    v = make_float4(sc.x * v.x, sc.y * v.y, sc.z * v.z, sc.w * v.w);
+                }
+            }
+            a[4 * q] = v.x; a[4 * q + 1] = v.y; a[4 * q + 2] = v.z; a[4 * q + 3] = v.w;
+        }
+        __syncthreads();
+        float blk[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) blk[j] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < F32_BK / 4; ++q) {
+            if (4 * q >= kb) break;
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const float4 w = wsh[j][q];
+                blk[j] = __builtin_fmaf(a[4 * q], w.x, blk[j]);
+                blk[j] = __builtin_fmaf(a[4 * q + 1], w.y, blk[j]);
+                blk[j] = __builtin_fmaf(a[4 * q + 2], w.z, blk[j]);
+                blk[j] = __builtin_fmaf(a[4 * q + 3], w.w, blk[j]);
+            }
+        }
+        if (k0 == 0) {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) tot[j] = blk[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) tot[j] = tot[j] + blk[j];
+        }
+    }
+    if (!live) return;
+    float bv[NC], rv[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int n = min(n0 + j, p.N - 1);
+        bv[j] = p.bias ? p.bias[n] : 0.0f;
+        rv[j] = p.res ? p.R[m * p.ldr + n] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+        if (n0 + j < p.N) p.C[m * p.ldc + n0 + j] = epi_value(p, tot[j], bv[j], rv[j]);
+}
+
+// ------------------------------------------------------------------------------------------------ fp32 MFMA
+// The fp32 tier's pointwise and all-row sequence GEMMs on the matrix cores: v_mfma_f32_16x16x4_f32 takes fp32
+// operands, forms fp32 products and accumulates in fp32 (no reduced-precision operand type).  Fragment layout, lane
+// l = 16 g + r: A holds row r at k slot g, B column r at k slot g, C column r at rows 4 g .. 4 g + 3.
+// A workgroup of four waves, WGN of them side by side along N, owns (4 / WGN) * MT * 16 rows x WGN * NT * 16
+// columns; a wave MT x NT blocks of 16 x 16.  Per K step of 16, lane (g, r) loads A[row][k0 + 4 g .. + 3] and
+// W[column][k0 + 4 g .. + 3] as one float4 each straight from memory (the waves of a workgroup share rows and
+// columns through L1 / L2; no LDS, no barrier) and MFMA kk (0..3) of the step takes k = k0 + 4 g + kk in slot g.
+// Every output therefore receives the same MFMA sequence (steps in increasing k, kk = 0..3, accumulator from +0)
+// whatever MT, NT, WGN, M or the other rows: results are bitwise independent of the tiling and of the batch.  The
+// next step's operands are loaded while the current step's MFMAs run.  K, lda, ldw (and ld_scale) are multiples of
+// 4; a K tail loads clamped addresses and zeros.
+template <int MT, int NT, int WGN, bool SCALE>
+__global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs p) {
+    constexpr int WGM = 4 / WGN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, r = lane & 15;
+    const long long mbase = (long long)blockIdx.x * (WGM * MT * 16) + (wave / WGN) * (MT * 16);
+    const int nbase = blockIdx.y * (WGN * NT * 16) + (wave % WGN) * (NT * 16);
+    const float* W = static_cast<const float*>(p.W);
+    const float* arow[MT];
+    const float* srow[MT];
+    bool alive[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const long long m = mbase + mt * 16 + r;
+        alive[mt] = m < p.M;
+        const long long mc = alive[mt] ? m : p.M - 1;
+        arow[mt] = p.A + mc * p.lda + 4 * g;
+        srow[mt] = SCALE ? p.scale + (mc / p.scale_rows) * p.ld_scale + 4 * g : nullptr;
+    }
+    const float* wrow[NT];
+    bool wlive[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int n = nbase + nt * 16 + r;
+        wlive[nt] = n < p.N;
+        wrow[nt] = W + (long long)(wlive[nt] ? n : p.N - 1) * p.ldw + 4 * g;
+    }
+    const auto load = [&](int k0, float4 (&a)[MT], float4 (&w)[NT]) {
+        const bool kin = k0 + 4 * g < p.K;
+        const int kc = kin ? k0 : p.K - 4 - 4 * g;   // clamped so that the float4 stays inside the row
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            float4 v = *reinterpret_cast<const float4*>(arow[mt] + kc);
+            if (SCALE) {
+                const float4 sc = *reinterpret_cast<const float4*>(srow[mt] + kc);
+                v = make_float4(sc.x * v.x, sc.y * v.y, sc.z * v.z, sc.w * v.w);
+            }
+            a[mt] = (kin && alive[mt]) ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const float4 v = *reinterpret_cast<const float4*>(wrow[nt] + kc);
+            w[nt] = (kin && wlive[nt]) ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float4 a[MT], w[NT], an[MT], wn[NT];
+    load(0, a, w);
+    for (int k0 = 0; k0 < p.K; k0 += 16) {
+        if (k0 + 16 < p.K) load(k0 + 16, an, wn);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const float av = kk == 0 ? a[mt].x : kk == 1 ? a[mt].y : kk == 2 ? a[mt].z : a[mt].w;
+                    const float wv = kk == 0 ? w[nt].x : kk == 1 ? w[nt].y : kk == 2 ? w[nt].z : w[nt].w;
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wv, acc[mt][nt], 0, 0, 0);
+                }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) a[mt] = an[mt];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) w[nt] = wn[nt];
+    }
+    // lane holds C[mbase + mt * 16 + 4 g + i][nbase + nt * 16 + r]
+    if (p.swiglu) {   // weight rows in 16-row panels alternating gate / up: NT even, nbase a multiple of 32
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const long long m = mbase + mt * 16 + 4 * g + i;
+                if (m >= p.M) continue;
+#pragma unroll
+                for (int nt = 0; nt + 1 < NT; nt += 2) {
+                    const int panel = nbase / 16 + nt;
+                    if ((panel + 1) * 16 <= p.N)
+                        p.C[m * p.ldc + (panel / 2) * 16 + r] = silu(acc[mt][nt][i]) * acc[mt][nt + 1][i];
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        epi_block<NT>(p, [&](int i) { return mbase + mt * 16 + 4 * g + i; }, [&](int j) { return nbase + j * 16 + r; },
+                      [&](int i, int j) { return acc[mt][j][i]; });
+}
+
 // Small M (<= 256 rows, e.g. the windows' last SISA rows): the same per-element arithmetic as gemm_f32_kernel -- K blocks
 // of 64, fma chain from +0 inside a block, the first block's sum taken as is and the later ones added in order -- so
 // results are bitwise those of the tiled kernel.  Only the chain inside a K block is serial, so a lane owns one
@@ -362,14 +544,14 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p
         for (int mt = 0; mt < MFMA_MT; ++mt) {
             const long long row = mbase + mt * 16 + r;
             const long long rc = row < p.M ? row : p.M - 1;
-            load8(p.A + rc * p.lda + kc, x[mt]);
+            read8(p.A + rc * p.lda + kc, x[mt]);
         }
         if constexpr (SCALE) {
 #pragma unroll
             for (int mt = 0; mt < MFMA_MT; ++mt) {
                 const long long row = mbase + mt * 16 + r;
                 const long long rc = row < p.M ? row : p.M - 1;
-                load8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, sc[mt]);
+                read8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, sc[mt]);
             }
         }
 #pragma unroll
@@ -856,9 +1038,9 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
 #pragma unroll
             for (int q = 0; q < P; ++q) xh[slot][q] = *reinterpret_cast<const uint4*>(a + q * p.astride);
         } else {
-            load8(p.A + rc * p.lda + kc, xa[slot]);
+            read8(p.A + rc * p.lda + kc, xa[slot]);
         }
-        if constexpr (SCALE) load8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, xs[slot]);
+        if constexpr (SCALE) read8(p.scale + (rc / p.scale_rows) * p.ld_scale + kc, xs[slot]);
 #pragma unroll
         for (int nt = 0; nt < SM_NT; ++nt) {
             const int col = min(nbase + nt * 16 + r, p.N - 1);
@@ -1014,7 +1196,7 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES, 2) gemm_stream_kernel(GemmArg
     auto load_a = [&](int ks, float (&dst)[ST_MT][8]) {
         const int kc = min(ks * 32 + g * 8, p.K - 8);
 #pragma unroll
-        for (int mt = 0; mt < ST_MT; ++mt) load8(arow[mt] + kc, dst[mt]);
+        for (int mt = 0; mt < ST_MT; ++mt) read8(arow[mt] + kc, dst[mt]);
     };
     load_w(0, wr[0]);
 #pragma unroll
@@ -1041,7 +1223,7 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES, 2) gemm_stream_kernel(GemmArg
         for (int mt = 0; mt < ST_MT; ++mt) {
             const bool live = kin && rlive[mt];
             float sc[8];
-            if constexpr (SCALE) load8(Sc + srow[mt] + kc, sc);
+            if constexpr (SCALE) read8(Sc + srow[mt] + kc, sc);
             float v[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -1423,6 +1605,26 @@ void launch_kblock_f32(const GemmArgs& p, hipStream_t s) {
     const long long outs = (long long)p.M * (p.swiglu ? p.N / 2 : p.N);
     hipLaunchKernelGGL(gemm_f32_fold_kernel, dim3(cdiv(outs, 256)), dim3(256), 0, s, p, nkb);
 }
+// Row-per-lane kernel: layers of at most 128 columns with rows to fill the device (a wave per 64 rows and NC
+// columns), operands laid out for its 16-byte loads
+bool use_rows_f32(const GemmArgs& p) {
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    return p.N <= 128 && p.M >= 4096 && !p.swiglu && p.K % 4 == 0 && p.lda % 4 == 0 && p.ldw % 4 == 0 &&
+           al16(p.A) && al16(p.W) && (!p.scale || (p.ld_scale % 4 == 0 && al16(p.scale)));
+}
+void launch_rows_f32(const GemmArgs& p, hipStream_t s) {
+    if (p.swiglu || p.K % 4 || p.lda % 4 || p.ldw % 4 || (p.scale && p.ld_scale % 4))
+        throw std::runtime_error("gemm_f32: the row-per-lane kernel needs K, lda, ldw, ld_scale % 4 == 0, no SwiGLU");
+    const bool wide = p.N % 16 == 0;
+    const dim3 grid(cdiv(p.M, 64), cdiv(p.N, wide ? 16 : 8));
+    if (wide) {
+        if (p.scale) hipLaunchKernelGGL((gemm_f32_rows_kernel<16, true>), grid, dim3(64), 0, s, p);
+        else hipLaunchKernelGGL((gemm_f32_rows_kernel<16, false>), grid, dim3(64), 0, s, p);
+    } else {
+        if (p.scale) hipLaunchKernelGGL((gemm_f32_rows_kernel<8, true>), grid, dim3(64), 0, s, p);
+        else hipLaunchKernelGGL((gemm_f32_rows_kernel<8, false>), grid, dim3(64), 0, s, p);
+    }
+}
 // The exact-tier kernel for M above the GEMV range: K blocks in parallel when the tiled grid would not give every
 // CU a workgroup and the workspace holds the block sums (measured with one clip: blocks 13-15 SE projects, 57
 // tiles, and the 321-row sequence GEMMs ran 45-200 us on the tiled kernel)
@@ -1432,6 +1634,50 @@ bool use_kblock_f32(const GemmArgs& p) {
 }
 }  // namespace
 
+namespace {
+// Tiles of the fp32 matrix-core GEMM by shape (every choice gives the same per-output MFMA sequence): one column
+// block per wave for N <= 16 and two for N <= 32 (the narrow early layers: no dead column blocks), else 64 x 128
+// workgroups while the grid gives every CU four of them, 64 x 64 while it gives two, 32 x 64 below (one clip).
+struct F32MfmaTile {
+    int mt, nt, wgn;
+};
+F32MfmaTile plan_f32_mfma(const GemmArgs& p) {
+    if (p.N <= 16 && !p.swiglu) return {4, 1, 1};
+    if (p.N <= 32) return {2, 2, 1};
+    const long long wide = (long long)cdiv(p.M, 64) * cdiv(p.N, 128), mid = (long long)cdiv(p.M, 64) * cdiv(p.N, 64);
+    if (wide >= 1024) return {2, 4, 2};
+    if (mid >= 512) return {2, 2, 2};
+    return {1, 2, 2};
+}
+template <int MT, int NT, int WGN> void launch_f32_mfma(const GemmArgs& p, hipStream_t s) {
+    const dim3 grid(cdiv(p.M, (4 / WGN) * MT * 16), cdiv(p.N, WGN * NT * 16));
+    if (p.scale) hipLaunchKernelGGL((gemm_f32_mfma_kernel<MT, NT, WGN, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gemm_f32_mfma_kernel<MT, NT, WGN, false>), grid, dim3(256), 0, s, p);
+}
+}  // namespace
+
+void gemm_f32_mfma(const GemmArgs& p, hipStream_t s) {
+    check_args(p, false);
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    if (p.K % 4 || p.lda % 4 || p.ldw % 4 || !al16(p.A) || !al16(p.W) ||
+        (p.scale && (p.ld_scale % 4 || !al16(p.scale))))
+        throw std::runtime_error("gemm_f32_mfma: K, lda, ldw, ld_scale must be multiples of 4 and A, W, scale "
+                                 "16-byte aligned (K=" + std::to_string(p.K) + ")");
+    if (p.swiglu && p.N % 32) throw std::runtime_error("gemm_f32_mfma: swiglu needs N % 32 == 0");
+    const F32MfmaTile t = plan_f32_mfma(p);
+    if (t.wgn == 1 && t.nt == 1) launch_f32_mfma<4, 1, 1>(p, s);
+    else if (t.wgn == 1) launch_f32_mfma<2, 2, 1>(p, s);
+    else if (t.nt == 4) launch_f32_mfma<2, 4, 2>(p, s);
+    else if (t.mt == 2) launch_f32_mfma<2, 2, 2>(p, s);
+    else launch_f32_mfma<1, 2, 2>(p, s);
+}
+
+std::string gemm_f32_mfma_kernel_name(const GemmArgs& p) {
+    const F32MfmaTile t = plan_f32_mfma(p);
+    return "gemm_f32_mfma_kernel<" + std::to_string(t.mt) + "," + std::to_string(t.nt) + "," + std::to_string(t.wgn) +
+           ">";
+}
+
 void gemm_f32(const GemmArgs& p, hipStream_t s) { gemm_f32_variant(p, s, 0); }
 
 void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
@@ -1439,18 +1685,21 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
     switch (variant) {
     case 0:
         if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) launch_gemv_f32(p, s);
+        else if (use_rows_f32(p)) launch_rows_f32(p, s);
         else if (use_kblock_f32(p)) launch_kblock_f32(p, s);
         else launch_tiled_f32(p, s);
         return;
     case 1: launch_gemv_f32(p, s); return;
     case 2: launch_tiled_f32(p, s); return;
     case 3: launch_kblock_f32(p, s); return;
+    case 5: launch_rows_f32(p, s); return;
     }
     throw std::runtime_error("gemm_f32: unknown kernel variant " + std::to_string(variant));
 }
 
 std::string gemm_f32_kernel(const GemmArgs& p) {
     if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) return "gemv_f32_kernel";
+    if (use_rows_f32(p)) return p.N % 16 == 0 ? "gemm_f32_rows_kernel<16>" : "gemm_f32_rows_kernel<8>";
     return use_kblock_f32(p) ? "gemm_f32_kblock_kernel" : "gemm_f32_kernel";
 }
 

@@ -48,13 +48,18 @@ struct GemmArgs {
 // fp32 tier: VALU GEMM, each output accumulated in K blocks of 64 (fma chain from +0 per block, block sums added
 // in order) exactly as the reference CPU engine (engine/model/isa_impl.hpp:188-317).
 void gemm_f32(const GemmArgs& p, hipStream_t s);
+// fp32 tier, pointwise and all-row sequence GEMMs: v_mfma_f32_16x16x4_f32 (fp32 operands, products and
+// accumulation).  Per output, K in steps of 16 in increasing order, four MFMAs per step, accumulator from +0: the
+// same for every tile, M and batch (row independence).  SwiGLU weights in 16-row gate / up panels (repack perm 2).
+void gemm_f32_mfma(const GemmArgs& p, hipStream_t s);
+std::string gemm_f32_mfma_kernel_name(const GemmArgs& p);
 // fp16 / bf16 tiers: MFMA 16x16x32 on split operands (fp16 2 parts / 3 products, bf16 3 parts / 6 products) with
 // fp32 accumulation, K consumed in 32-wide steps in increasing order (no split-K): a row's outputs do not depend
 // on M, the tile, or other rows.
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
 // Kernel variants, for the GEMM microbench and its bitwise variant check (every variant performs the same operation
 // sequence per output, so all give bitwise equal results).  fp32: 0 automatic, 1 GEMV, 2 tiled, 3 K blocks in
-// parallel (needs ws for ceil(K / 64) * M * N floats).  MFMA tiers:
+// parallel (needs ws for ceil(K / 64) * M * N floats), 5 row per lane (N <= 128 layers; K % 4 == 0).  MFMA tiers:
 // 0 automatic, 1 small-M, 2..6 direct with 1..5 column tiles per wave, 7 LDS-staged 128 x 128, 8 streaming (N <= 160,
 // every column in one workgroup; the SE projects' kernel).
 void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant);
@@ -149,11 +154,21 @@ struct CropJob {
 void native_crops(const CropJob* jobs, int n, uint8_t* out, bool i420, hipStream_t s);
 
 // ---------------------------------------------------------------- sequence (fp32 residual stream)
-void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,
-                     hipStream_t s);
-// SHIELD-A windows: tokens [B] windows of [125][384] (window stride ldw floats, a multiple of 4) + readout ->
-// h [B*126][384]
-void launch_assemble_audio(const float* tokens, long long ldw, const float* readout, float* h, int B, hipStream_t s);
+// Where a batch's windows take their rows.  SHIELD-V (T = 321): frame_tokens[window * 20 + position] is the
+// frame's 16 x 384 token block, plus the position table pos [320][384]; SHIELD-A (T = 126): token t of window b at
+// tokens + b * ldw + t * 384.  The last row of every window is the readout vector.
+struct WindowInput {
+    const float* const* frame_tokens = nullptr;
+    const float* pos = nullptr;
+    const float* tokens = nullptr;
+    long long ldw = 0;
+    const float* readout = nullptr;
+};
+// The residual stream h [B*T][384] of B windows and, in the same pass, its RMSNorm with weights w into out (the
+// layout of launch_rmsnorm's output)
+template <typename T>
+void launch_window_input(const WindowInput& in, const float* w, float* h, T* out, long long ldo, int B, int TT,
+                         hipStream_t s, long long pstride = 0, long long kstride = 32);
 // out[r] = (x[r] * (1 / sqrt(sum(x^2) / 384 + 1e-6))) * w with the reference's 16-lane sum tree.  T = f16 / bf16:
 // out holds the split parts of each value (part stride pstride elements), the pre-split A of the next GEMM, value
 // (r, c) of a part at (c / 32) * kstride + r * ldo + c % 32 (GemmArgs' operand layout).
@@ -191,7 +206,8 @@ void launch_sisa(float* S, const float* QC, const float* lam, float* Y, int B, h
 // exact GELU (audio, engine/audio/sequence.cpp:318-330)
 void launch_head(const float* X, const float* norm_w, const float* w0, const float* b0, const float* w2, float b2,
                  float* logits, int B, hipStream_t s, bool audio = false);
-// pool[slots[f]] = tokens[f] for slots[f] >= 0
-void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool, int F, hipStream_t s);
+// Token-slot stores: pairs[2 i] = batch frame, pairs[2 i + 1] = pool slot; the frame's 6144 token floats are
+// copied to the slot for every listed pair
+void launch_slot_store(const float* tokens, const int32_t* pairs, int n_pairs, float* pool, hipStream_t s);
 
 }  // namespace shv

@@ -39,7 +39,7 @@ HipLanes::HipLanes(const HostModel& hm, Precision p, const EngineConfig& cfg, in
             L.frames = pinned<uint8_t>(frames * FB);
             L.blocks = pinned<float>(blocks * TF);
             L.table = pinned<const float*>(windows * sched::kWindowFrames);
-            L.store = pinned<int32_t>(frames);
+            L.store = pinned<int32_t>(2 * frames);
             L.tokens = pinned<float>(frames * TF);
             L.logits = pinned<float>(windows);
             SHV_HIP_CHECK(hipEventCreateWithFlags(&L.uploaded, hipEventDisableTiming));
@@ -138,12 +138,19 @@ void HipLanes::start(const sched::Batch& b) {
     if (!b.host_blocks.empty())
         SHV_HIP_CHECK(hipMemcpyAsync(d.d_tok_stage, L.blocks, b.host_blocks.size() * TF * sizeof(float),
                                      hipMemcpyHostToDevice, copy_));
-    const bool stores = !b.store_to.empty();
-    if (stores) {
+    // token-slot stores as (batch frame, slot) pairs of the frames that store
+    int n_store = 0;
+    if (!b.store_to.empty()) {
         if (!pool_) throw std::runtime_error("batch stores tokens without a pool");
-        std::memcpy(L.store, b.store_to.data(), b.store_to.size() * sizeof(int32_t));
-        SHV_HIP_CHECK(hipMemcpyAsync(d.d_store, L.store, b.store_to.size() * sizeof(int32_t),
-                                     hipMemcpyHostToDevice, copy_));
+        for (int f = 0; f < int(b.store_to.size()); ++f)
+            if (b.store_to[size_t(f)] >= 0) {
+                L.store[2 * n_store] = f;
+                L.store[2 * n_store + 1] = b.store_to[size_t(f)];
+                ++n_store;
+            }
+        if (n_store)
+            SHV_HIP_CHECK(hipMemcpyAsync(d.d_store, L.store, size_t(n_store) * 2 * sizeof(int32_t),
+                                         hipMemcpyHostToDevice, copy_));
     }
     SHV_HIP_CHECK(hipEventRecord(L.uploaded, copy_));
 
@@ -156,8 +163,8 @@ void HipLanes::start(const sched::Batch& b) {
         aligned = b.refs[e].kind == sched::TokenRef::kFrame && b.refs[e].index == int32_t(e);
     const bool fused = aligned && eng_->forward_slot(b.lane, b.windows, compute_);
     if (b.frames && !fused) eng_->encode_slot(b.lane, b.frames, compute_);
-    if (stores) {
-        launch_store_tokens(d.d_tokens, d.d_store, pool_, b.frames, compute_);
+    if (n_store) {
+        launch_slot_store(d.d_tokens, d.d_store, n_store, pool_, compute_);
         SHV_HIP_CHECK(hipGetLastError());
     }
     if (b.windows) {

@@ -6,6 +6,7 @@
 #include <limits>
 #include <memory>
 #include <stdexcept>
+#include <utility>
 
 namespace shv {
 namespace sched {
@@ -247,15 +248,19 @@ void Frontend::finalize(shv_hip_job* j, bool ok, const std::string& err, double 
                         Clock::time_point t_start) {
     shv_hip_callback cb;
     void* user;
+    const auto ms = [](Clock::time_point a, Clock::time_point b) {
+        return std::chrono::duration<double, std::milli>(b - a).count();
+    };
+    const Clock::time_point now = Clock::now();
     {
         std::lock_guard<std::mutex> lk(j->mu);
         j->status = ok ? 1 : -1;
         j->error = ok ? std::string() : err;
-        j->t_start = t_start;
-        j->t_done = Clock::now();
-        j->device_ms = device_ms;
-        j->batch_frames = bf;
-        j->batch_windows = bw;
+        j->timing.queue_ms = ms(j->t_submit, t_start);
+        j->timing.run_ms = ms(t_start, now);
+        j->timing.device_ms = device_ms;
+        j->timing.batch_frames = bf;
+        j->timing.batch_windows = bw;
         cb = j->callback;
         user = j->user;
         if (!cb) j->settled = true;
@@ -302,41 +307,55 @@ void Frontend::completer_main() {
 }
 
 // ------------------------------------------------------------------------------------------------- jobs
+namespace {
+// Looks at a job under its lock; with `until_final`, first waits for the completer to finalise it.
+template <class Read> auto read_job(const shv_hip_job& j, bool until_final, Read&& read) {
+    std::unique_lock<std::mutex> lk(j.mu);
+    if (until_final) j.cv.wait(lk, [&] { return j.status != 0; });
+    return read(j);
+}
+}  // namespace
+
 int Frontend::job_status(const shv_hip_job* j) {
-    if (!j) return -1;
-    std::lock_guard<std::mutex> lk(j->mu);
-    return j->status;
+    return j ? read_job(*j, false, [](const shv_hip_job& x) { return x.status; }) : -1;
 }
 
 int Frontend::job_wait(shv_hip_job* j) {
     if (!j) {
-        set_error("null job");
+        set_error("job_wait: the job handle is NULL");
         return -1;
     }
-    std::unique_lock<std::mutex> lk(j->mu);
-    j->cv.wait(lk, [&] { return j->status != 0; });
-    if (j->status > 0) return 0;
-    set_error(j->error);
-    return -1;
+    std::string why;
+    const int status = read_job(*j, true, [&](const shv_hip_job& x) {
+        why = x.error;
+        return x.status;
+    });
+    if (status < 0) {
+        set_error(why);
+        return -1;
+    }
+    return 0;
 }
 
 const char* Frontend::job_error(const shv_hip_job* j) {
-    if (!j) return "null job";
-    std::lock_guard<std::mutex> lk(j->mu);
-    return j->error.c_str();
+    // the text lives in the job, which is final once it is non-empty, so the pointer stays valid until job_free
+    return j ? read_job(*j, false, [](const shv_hip_job& x) { return x.error.c_str(); }) : "job handle is NULL";
 }
 
 int Frontend::job_timing(const shv_hip_job* j, double* queue_ms, double* run_ms, double* device_ms, int* bf,
                          int* bw) {
     if (!j) return -1;
-    std::lock_guard<std::mutex> lk(j->mu);
-    if (j->status == 0) return 1;
-    const auto ms = [](Clock::duration d) { return std::chrono::duration<double, std::milli>(d).count(); };
-    if (queue_ms) *queue_ms = ms(j->t_start - j->t_submit);
-    if (run_ms) *run_ms = ms(j->t_done - j->t_start);
-    if (device_ms) *device_ms = j->device_ms;
-    if (bf) *bf = j->batch_frames;
-    if (bw) *bw = j->batch_windows;
+    shv_hip_job::Timing t;
+    const bool final = read_job(*j, false, [&](const shv_hip_job& x) {
+        t = x.timing;
+        return x.status != 0;
+    });
+    if (!final) return 1;
+    const std::pair<double*, double> d[] = {{queue_ms, t.queue_ms}, {run_ms, t.run_ms}, {device_ms, t.device_ms}};
+    for (const auto& f : d)
+        if (f.first) *f.first = f.second;
+    if (bf) *bf = t.batch_frames;
+    if (bw) *bw = t.batch_windows;
     return 0;
 }
 
@@ -349,113 +368,108 @@ void Frontend::job_free(shv_hip_job* j) {
     delete j;
 }
 
-// ------------------------------------------------------------------------------------------------- sync wrappers
-int Frontend::wait_and_free(std::vector<shv_hip_job*>& jobs) {
-    std::string first_error;
-    bool ok = true;
-    for (shv_hip_job* j : jobs) {
-        if (job_wait(j) != 0) {
-            if (ok) first_error = job_error(j);
-            ok = false;
+// ------------------------------------------------------------------------------------------------- sync calls
+// A synchronous call as requests of at most `per` of its `total` units.  Every piece is submitted before the first
+// is waited for, so the pieces pipeline over the lanes.  fill(at, count, request) describes a piece.  A failed job
+// writes NaN into its own outputs; the pieces left unsubmitted after a refused submit get poison(at, count).  Each
+// job is freed here; the result is 0, or -1 with the first failure in piece order (a refused submit comes last).
+template <class Fill, class Poison>
+int Frontend::run_pieces(size_t total, size_t per, Fill&& fill, Poison&& poison) {
+    std::vector<shv_hip_job*> submitted;
+    std::string refused;
+    size_t at = 0;
+    while (at < total) {
+        const size_t count = std::min(per, total - at);
+        shv_hip_request r{};
+        fill(at, count, r);
+        shv_hip_job* j = submit(&r);
+        if (!j) {
+            refused = last_error();
+            poison(at, total - at);
+            break;
+        }
+        submitted.push_back(j);
+        at += count;
+    }
+    bool failed = at < total;
+    std::string first;
+    for (shv_hip_job* j : submitted) {
+        if (job_wait(j) != 0 && !failed) {
+            failed = true;
+            first = job_error(j);
         }
         job_free(j);
     }
-    jobs.clear();
-    if (ok) return 0;
-    set_error(first_error);
+    if (!failed) {
+        clear_error();
+        return 0;
+    }
+    set_error(first.empty() ? refused : first);
     return -1;
 }
 
 int Frontend::encode_frames(const uint8_t* rgb, size_t n, float* tokens) {
     if (n && (!rgb || !tokens)) {
-        set_error("null argument");
+        set_error("encode_frames: frames and tokens must be non-NULL");
         return -1;
     }
-    std::vector<shv_hip_job*> jobs;
-    const size_t per = size_t(lim_.frames);
-    for (size_t at = 0; at < n; at += per) {
-        shv_hip_request r{};
-        r.frames = rgb + at * kFrameBytes;
-        r.n_frames = std::min(per, n - at);
-        r.tokens_out = tokens + at * kTokenFloats;
-        shv_hip_job* j = submit(&r);
-        if (!j) {
-            const std::string why = last_error();
-            wait_and_free(jobs);
-            std::fill(tokens, tokens + n * kTokenFloats, kNaN);
-            set_error(why);
-            return -1;
-        }
-        jobs.push_back(j);
-    }
-    return wait_and_free(jobs);
+    return run_pieces(
+        n, size_t(lim_.frames),
+        [&](size_t at, size_t count, shv_hip_request& r) {
+            r.frames = rgb + at * kFrameBytes;
+            r.n_frames = count;
+            r.tokens_out = tokens + at * kTokenFloats;
+        },
+        [&](size_t at, size_t count) { std::fill_n(tokens + at * kTokenFloats, count * kTokenFloats, kNaN); });
 }
 
 int Frontend::classify(const float* tokens, size_t b, float* logits) {
     if (b && (!tokens || !logits)) {
-        set_error("null argument");
+        set_error("classify: tokens and logits must be non-NULL");
         return -1;
     }
-    if (b && lim_.host_blocks < kWindowFrames) {
-        set_error("classify needs max_host_tokens >= 20");
+    const size_t windows_per_batch = size_t(lim_.host_blocks / kWindowFrames);
+    if (b && windows_per_batch == 0) {
+        set_error("classify: options.max_host_tokens is below the 20 token blocks of one window");
         return -1;
     }
-    const size_t per = size_t(std::max(1, std::min(lim_.windows, lim_.host_blocks / kWindowFrames)));
-    std::vector<shv_hip_job*> jobs;
-    std::vector<const float*> p;   // submit copies the pointer array
-    for (size_t at = 0; at < b; at += per) {
-        const size_t w = std::min(per, b - at);
-        p.resize(w * kWindowFrames);
-        for (size_t e = 0; e < p.size(); ++e) p[e] = tokens + (at * kWindowFrames + e) * kTokenFloats;
-        shv_hip_request r{};
-        r.n_windows = w;
-        r.window_tokens = p.data();
-        r.logits_out = logits + at;
-        shv_hip_job* j = submit(&r);
-        if (!j) {
-            const std::string why = last_error();
-            wait_and_free(jobs);
-            std::fill(logits, logits + b, kNaN);
-            set_error(why);
-            return -1;
-        }
-        jobs.push_back(j);
-    }
-    return wait_and_free(jobs);
+    std::vector<const float*> blocks;   // one piece's entry table; submit copies it
+    return run_pieces(
+        b, std::min(size_t(lim_.windows), windows_per_batch),
+        [&](size_t at, size_t count, shv_hip_request& r) {
+            blocks.resize(count * kWindowFrames);
+            const float* first = tokens + at * kWindowFrames * kTokenFloats;
+            for (size_t e = 0; e < blocks.size(); ++e) blocks[e] = first + e * kTokenFloats;
+            r.n_windows = count;
+            r.window_tokens = blocks.data();
+            r.logits_out = logits + at;
+        },
+        [&](size_t at, size_t count) { std::fill_n(logits + at, count, kNaN); });
 }
 
 int Frontend::predict(const uint8_t* clips, size_t b, float* logits) {
     if (b && (!clips || !logits)) {
-        set_error("null argument");
+        set_error("predict: clips and logits must be non-NULL");
         return -1;
     }
-    const size_t per = size_t(std::min(lim_.windows, lim_.frames / kWindowFrames));
-    if (b && per == 0) {
-        set_error("predict needs max_frames >= 20");
+    const size_t clips_per_batch = std::min(size_t(lim_.windows), size_t(lim_.frames / kWindowFrames));
+    if (b && clips_per_batch == 0) {
+        set_error("predict: options.max_frames is below the 20 frames of one clip");
         return -1;
     }
-    std::vector<int32_t> own(per * kWindowFrames);
-    for (size_t e = 0; e < own.size(); ++e) own[e] = int32_t(e);   // window w, position p -> frame 20 w + p
-    std::vector<shv_hip_job*> jobs;
-    for (size_t at = 0; at < b; at += per) {
-        const size_t w = std::min(per, b - at);
-        shv_hip_request r{};
-        r.frames = clips + at * kWindowFrames * kFrameBytes;
-        r.n_frames = w * kWindowFrames;
-        r.n_windows = w;
-        r.window_frames = own.data();
-        r.logits_out = logits + at;
-        shv_hip_job* j = submit(&r);
-        if (!j) {
-            const std::string why = last_error();
-            wait_and_free(jobs);
-            std::fill(logits, logits + b, kNaN);
-            set_error(why);
-            return -1;
-        }
-        jobs.push_back(j);
-    }
-    return wait_and_free(jobs);
+    // window w reads frames 20 w .. 20 w + 19 of its own piece
+    std::vector<int32_t> frame_of(clips_per_batch * kWindowFrames);
+    for (size_t e = 0; e < frame_of.size(); ++e) frame_of[e] = int32_t(e);
+    return run_pieces(
+        b, clips_per_batch,
+        [&](size_t at, size_t count, shv_hip_request& r) {
+            r.frames = clips + at * kWindowFrames * kFrameBytes;
+            r.n_frames = count * kWindowFrames;
+            r.n_windows = count;
+            r.window_frames = frame_of.data();
+            r.logits_out = logits + at;
+        },
+        [&](size_t at, size_t count) { std::fill_n(logits + at, count, kNaN); });
 }
 
 }  // namespace sched

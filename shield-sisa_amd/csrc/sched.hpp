@@ -110,15 +110,17 @@ struct shv_hip_job {
     float* logits_out = nullptr;
     shv_hip_callback callback = nullptr;
     void* user = nullptr;
-    // the outcome
+    shv::sched::Clock::time_point t_submit{};
+    // the outcome, written once by the completer under mu
     mutable std::mutex mu;
-    std::condition_variable cv;
+    mutable std::condition_variable cv;
     int status = 0;          // 0 pending, 1 done, -1 failed
     bool settled = false;    // status final and the callback (if any) has returned: job_free may delete
     std::string error;
-    shv::sched::Clock::time_point t_submit{}, t_start{}, t_done{};
-    double device_ms = 0.0;
-    int batch_frames = 0, batch_windows = 0;
+    struct Timing {
+        double queue_ms = 0.0, run_ms = 0.0, device_ms = 0.0;   // submit -> batch start -> outputs final; GPU time
+        int batch_frames = 0, batch_windows = 0;                  // size of the batch that carried the job
+    } timing;
 };
 
 namespace shv {
@@ -172,7 +174,7 @@ private:
     void deliver(Flight& f, const float* logits) const;
     static void finalize(shv_hip_job* j, bool ok, const std::string& err, double device_ms, int bf, int bw,
                          Clock::time_point t_start);
-    int wait_and_free(std::vector<shv_hip_job*>& jobs);
+    template <class Fill, class Poison> int run_pieces(size_t total, size_t per, Fill&& fill, Poison&& poison);
 
     Device& dev_;
     const Limits lim_;

@@ -8,6 +8,7 @@
 #include "kernels.hpp"
 #include "mfma.hpp"
 
+#include <algorithm>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -31,33 +32,48 @@ __device__ __forceinline__ void put_value(T* base, long long pstride, long long 
     }
 }
 
-// ------------------------------------------------------------------------------------------------ assemble
-// h[b*321 + t] = tokens(b, t / 16)[t % 16] + pos[t] (t < 320); readout at t = 320.  One block per row, float4.
-__global__ void __launch_bounds__(96)
-assemble_kernel(const float* const* __restrict__ tok_ptrs, const float* __restrict__ pos,
-                const float* __restrict__ readout, float* __restrict__ h) {
-    const long long row = blockIdx.x;
-    const int b = int(row / kT), t = int(row % kT), j = threadIdx.x * 4;
-    float4 v;
-    if (t == kT - 1) {
-        v = *reinterpret_cast<const float4*>(readout + j);
+// ------------------------------------------------------------------------------------------------ window input
+// A window's residual stream and the A operand of GDN-A's first in-projection in one pass (no separate assembly
+// pass over h).  Row t of window b is, for SHIELD-V, token t % 16 of the frame at window position t / 16 plus
+// position row t; for SHIELD-A, token t of the window stored at tokens + b * ldw (no position table); the last row
+// is the readout vector in both.  The row is written to h, then normalised exactly as rmsnorm_kernel does it
+// (16 lanes per row, lane l owns columns l + 16 i).
+template <typename T, int TT, bool VIDEO>
+__global__ void __launch_bounds__(256)
+window_input_kernel(WindowInput in, const float* __restrict__ w, float* __restrict__ h, T* __restrict__ out,
+                    long long ldo, long long pstride, long long kstride, int rows) {
+    const long long row = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    const int l = threadIdx.x & 15;
+    const bool live = row < rows;
+    const long long r = live ? row : 0;   // dead rows recompute row 0: the 16-lane tree needs every lane
+    const int t = int(r % TT);
+    const long long b = r / TT;
+    float v[24];
+    if (t == TT - 1) {
+#pragma unroll
+        for (int i = 0; i < 24; ++i) v[i] = in.readout[i * 16 + l];
+    } else if constexpr (VIDEO) {
+        const float* tok = in.frame_tokens[b * kFrames + t / 16] + (t % 16) * kD;
+        const float* pos = in.pos + (long long)t * kD;
+#pragma unroll
+        for (int i = 0; i < 24; ++i) v[i] = tok[i * 16 + l] + pos[i * 16 + l];
     } else {
-        const float4 a = *reinterpret_cast<const float4*>(tok_ptrs[b * kFrames + t / 16] + (t % 16) * kD + j);
-        const float4 p = *reinterpret_cast<const float4*>(pos + t * kD + j);
-        v = make_float4(a.x + p.x, a.y + p.y, a.z + p.z, a.w + p.w);
+        const float* tok = in.tokens + b * in.ldw + (long long)t * kD;
+#pragma unroll
+        for (int i = 0; i < 24; ++i) v[i] = tok[i * 16 + l];
     }
-    *reinterpret_cast<float4*>(h + row * kD + j) = v;
-}
-
-// SHIELD-A: h[b*126 + t] = tokens[b * ldw + t * 384] (t < 125), the readout at t = 125 (engine/audio/sequence.cpp:
-// 322-323); no position table.
-__global__ void __launch_bounds__(96)
-assemble_audio_kernel(const float* __restrict__ tokens, long long ldw, const float* __restrict__ readout,
-                      float* __restrict__ h) {
-    const long long row = blockIdx.x;
-    const int b = int(row / kTAudio), t = int(row % kTAudio), j = threadIdx.x * 4;
-    const float* src = t == kTAudio - 1 ? readout + j : tokens + b * ldw + (long long)t * kD + j;
-    *reinterpret_cast<float4*>(h + row * kD + j) = *reinterpret_cast<const float4*>(src);
+    float acc = v[0] * v[0];
+#pragma unroll
+    for (int i = 1; i < 24; ++i) acc = __builtin_fmaf(v[i], v[i], acc);
+    const float ss = tree16(acc);
+    if (!live) return;
+    float* hr = h + row * kD;
+#pragma unroll
+    for (int i = 0; i < 24; ++i) hr[i * 16 + l] = v[i];
+    const float inv = 1.0f / sqrtf(ss / 384.0f + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < 24; ++i)
+        put_value(out, pstride, presplit_idx(row, i * 16 + l, ldo, kstride), (v[i] * inv) * w[i * 16 + l]);
 }
 
 // ------------------------------------------------------------------------------------------------ RMSNorm
@@ -636,7 +652,7 @@ delta_chunk_prep_kernel(const float* __restrict__ Q, const float* __restrict__ K
     for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            load8(Q + (row0 + min(ti * 16 + r, n - 1)) * kD + h * 64 + ks * 32 + 8 * g, qf[ti][ks]);
+            read8(Q + (row0 + min(ti * 16 + r, n - 1)) * kD + h * 64 + ks * 32 + 8 * g, qf[ti][ks]);
     {   // stage K (loads at clamped rows, all in flight together; zero / a = 1 past the window's end)
         float av = 1.0f, bv = 0.0f;
         if (lane < DC) {
@@ -1150,27 +1166,22 @@ head_kernel(const float* __restrict__ X, const float* __restrict__ nw, const flo
     }
 }
 
+// Token-slot stores of one batch.  The host lists only the frames that store, as (batch frame, pool slot) pairs,
+// so the grid covers exactly the rows to move: thread i copies 16-byte piece i % 1536 of pair i / 1536, striding by
+// the grid.
+constexpr int kRowPieces = int(kTokenFloats / 4);
 __global__ void __launch_bounds__(256)
-store_tokens_kernel(const float* __restrict__ src, const int32_t* __restrict__ slots, float* __restrict__ pool) {
-    const int f = blockIdx.x, s = slots[f];
-    if (s < 0) return;
-    const float4* a = reinterpret_cast<const float4*>(src + (long long)f * kTokenFloats);
-    float4* d = reinterpret_cast<float4*>(pool + (long long)s * kTokenFloats);
-    for (int i = threadIdx.x; i < int(kTokenFloats / 4); i += blockDim.x) d[i] = a[i];
+slot_store_kernel(const float4* __restrict__ tokens, const int2* __restrict__ pairs, long long pieces,
+                  float4* __restrict__ pool) {
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < pieces; i += (long long)gridDim.x * blockDim.x) {
+        const int2 fs = pairs[i / kRowPieces];
+        const int c = int(i % kRowPieces);
+        pool[(long long)fs.y * kRowPieces + c] = tokens[(long long)fs.x * kRowPieces + c];
+    }
 }
 
 }  // namespace
 
-void launch_assemble(const float* const* tok_ptrs, const float* pos, const float* readout, float* h, int B,
-                     hipStream_t s) {
-    hipLaunchKernelGGL(assemble_kernel, dim3(B * kT), dim3(96), 0, s, tok_ptrs, pos, readout, h);
-}
-void launch_assemble_audio(const float* tokens, long long ldw, const float* readout, float* h, int B, hipStream_t s) {
-    if ((reinterpret_cast<uintptr_t>(tokens) & 15) || (reinterpret_cast<uintptr_t>(readout) & 15) || ldw % 4 ||
-        ldw < (long long)(kTAudio - 1) * kD)
-        throw std::runtime_error("assemble: audio tokens need 16-byte alignment and a window stride >= 48000 floats");
-    hipLaunchKernelGGL(assemble_audio_kernel, dim3(B * kTAudio), dim3(96), 0, s, tokens, ldw, readout, h);
-}
 template <typename T>
 void launch_rmsnorm(const float* x, long long ldx, const float* w, T* out, long long ldo, int rows, hipStream_t s,
                     long long pstride, long long kstride) {
@@ -1184,6 +1195,19 @@ template <class F> void for_window(int T, F&& f) {
     else throw std::runtime_error("sequence kernels: unsupported window length " + std::to_string(T));
 }
 
+template <typename T>
+void launch_window_input(const WindowInput& in, const float* w, float* h, T* out, long long ldo, int B, int TT,
+                         hipStream_t s, long long pstride, long long kstride) {
+    if (!in.readout || (TT == kT ? (!in.frame_tokens || !in.pos) : (!in.tokens || in.ldw < (long long)(TT - 1) * kD)))
+        throw std::runtime_error("window input: missing token source, or a window stride below its tokens");
+    const int rows = B * TT;
+    const dim3 grid(cdiv((long long)rows * 16, 256));
+    for_window(TT, [&](auto tt) {
+        constexpr int W = decltype(tt)::value;
+        hipLaunchKernelGGL((window_input_kernel<T, W, W == kT>), grid, dim3(256), 0, s, in, w, h, out, ldo, pstride,
+                           kstride, rows);
+    });
+}
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,
                      const float* dt_bias, float* Q, float* K, float* V, float* dec, float* beta, int B,
                      hipStream_t s, int T, bool audio, bool fast) {
@@ -1272,8 +1296,12 @@ void launch_head(const float* X, const float* norm_w, const float* w0, const flo
     if (audio) hipLaunchKernelGGL((head_kernel<true>), dim3(B), dim3(128), 0, s, X, norm_w, w0, b0, w2, b2, logits);
     else hipLaunchKernelGGL((head_kernel<false>), dim3(B), dim3(128), 0, s, X, norm_w, w0, b0, w2, b2, logits);
 }
-void launch_store_tokens(const float* tokens, const int32_t* slots, float* pool, int F, hipStream_t s) {
-    hipLaunchKernelGGL(store_tokens_kernel, dim3(F), dim3(256), 0, s, tokens, slots, pool);
+void launch_slot_store(const float* tokens, const int32_t* pairs, int n_pairs, float* pool, hipStream_t s) {
+    if (n_pairs <= 0) return;
+    const long long pieces = (long long)n_pairs * kRowPieces;
+    const unsigned grid = unsigned(std::min<long long>(cdiv(pieces, 256), 2048));
+    hipLaunchKernelGGL(slot_store_kernel, dim3(grid), dim3(256), 0, s, reinterpret_cast<const float4*>(tokens),
+                       reinterpret_cast<const int2*>(pairs), pieces, reinterpret_cast<float4*>(pool));
 }
 
 // ------------------------------------------------------------------------------------------------ no allocation
@@ -1309,8 +1337,9 @@ float* scratch_on_current_device() {
 
 void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const float* V, const float* dec,
                             const float* beta, int n_windows, float* O, int variant, hipStream_t s) {
-    if (!delta_rule_is_chunked(p, Q, K, V, dec, beta, n_windows, O, variant)) {
-        launch_delta(Q, K, V, dec, beta, O, n_windows, p == Precision::FP32, s, kT);
+    const DeltaKernel kern = delta_rule_kernel(p, Q, K, V, dec, beta, n_windows, O, variant);
+    if (kern != DeltaKernel::Chunked) {
+        launch_delta(Q, K, V, dec, beta, O, n_windows, kern == DeltaKernel::Reference, s, kT);
         SHV_HIP_CHECK(hipGetLastError());
         return;
     }
@@ -1327,7 +1356,9 @@ void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const f
     template void launch_rmsnorm<T>(const float*, long long, const float*, T*, long long, int, hipStream_t,      \
                                     long long, long long);                                                       \
     template void launch_gated_norm<T>(const float*, const float*, const float*, T*, int, hipStream_t, long long,  \
-                                       bool, long long, long long);
+                                       bool, long long, long long);                                               \
+    template void launch_window_input<T>(const WindowInput&, const float*, float*, T*, long long, int, int,       \
+                                         hipStream_t, long long, long long);
 SHV_NORMS(float)
 SHV_NORMS(f16)
 SHV_NORMS(bf16)

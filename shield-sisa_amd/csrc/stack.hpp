@@ -9,7 +9,8 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
-#include <fstream>
+#include <cstdio>
+#include <stdexcept>
 #include <string>
 #include <type_traits>
 #include <vector>
@@ -18,11 +19,15 @@ namespace shv {
 
 inline void check_launch() { SHV_HIP_CHECK(hipGetLastError()); }
 
-// G selects how GEMM operands reach the multipliers: float = exact-order VALU, f16 / bf16 = split-operand MFMA
-template <typename G> inline void gemm_t(const GemmArgs& p, hipStream_t s);
-template <> inline void gemm_t<float>(const GemmArgs& p, hipStream_t s) { gemm_f32(p, s); }
-template <> inline void gemm_t<f16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<f16>(p, s); }
-template <> inline void gemm_t<bf16>(const GemmArgs& p, hipStream_t s) { gemm_mfma<bf16>(p, s); }
+// G selects how GEMM operands reach the multipliers: float = fp32 (matrix cores, or the reference's VALU order),
+// f16 / bf16 = split-operand MFMA
+template <typename G> inline void gemm_t(const GemmArgs& p, hipStream_t s, bool cpu_order);
+template <> inline void gemm_t<float>(const GemmArgs& p, hipStream_t s, bool cpu_order) {
+    if (cpu_order) gemm_f32(p, s);
+    else gemm_f32_mfma(p, s);
+}
+template <> inline void gemm_t<f16>(const GemmArgs& p, hipStream_t s, bool) { gemm_mfma<f16>(p, s); }
+template <> inline void gemm_t<bf16>(const GemmArgs& p, hipStream_t s, bool) { gemm_mfma<bf16>(p, s); }
 
 inline double gemm_bytes(long long M, int N, int K, int ta, int tw, int tc, int tr) {
     return double(M) * K * ta + double(N) * K * tw + double(M) * N * tc + (tr ? double(M) * N * tr : 0.0);
@@ -123,16 +128,20 @@ private:
     hipStream_t s_;
 };
 
-// Debug dump of window 0 / frame 0 (synchronises s): `n` values of `dev` as fp32 to "<dir>/<name>.f32"
+// Debug dump (window 0 / frame 0; debug runs only, it synchronises s): n values at dev, read back on s itself so
+// that they are exactly what the launches queued before on s wrote, stored as fp32 in "<dir>/<name>.f32".
 template <typename U> void dump_f32(const std::string& dir, const char* name, const U* dev, size_t n, hipStream_t s) {
     if (dir.empty()) return;
+    std::vector<U> raw(n);
+    SHV_HIP_CHECK(hipMemcpyAsync(raw.data(), dev, n * sizeof(U), hipMemcpyDeviceToHost, s));
     SHV_HIP_CHECK(hipStreamSynchronize(s));
-    std::vector<U> h(n);
-    SHV_HIP_CHECK(hipMemcpy(h.data(), dev, n * sizeof(U), hipMemcpyDeviceToHost));
-    std::vector<float> f(n);
-    for (size_t i = 0; i < n; ++i) f[i] = float(h[i]);
-    std::ofstream o(dir + "/" + name + ".f32", std::ios::binary);
-    o.write(reinterpret_cast<const char*>(f.data()), std::streamsize(n * sizeof(float)));
+    std::vector<float> vals(raw.begin(), raw.end());
+    const std::string path = dir + "/" + name + ".f32";
+    std::FILE* fp = std::fopen(path.c_str(), "wb");
+    if (!fp) throw std::runtime_error("dump: cannot open " + path);
+    const size_t put = n ? std::fwrite(vals.data(), sizeof(float), n, fp) : 0;
+    const bool closed = std::fclose(fp) == 0;
+    if (put != n || !closed) throw std::runtime_error("dump: short write to " + path);
 }
 
 // GEMM launches of one engine flavour G, timed under "<role>:<kernel template>" when profiling
@@ -141,10 +150,13 @@ template <typename G> struct GemmRunner {
     Profiler& pf;
     float* ws = nullptr;   // the exact GEMM's small-M workspace (gemm_f32), null when the caller has none free
     long long ws_floats = 0;
+    bool cpu_order = false;   // fp32 tier: the reference CPU order instead of the fp32 matrix cores
     std::string family(const char* role, const GemmArgs& p, bool f32) const {
         if (!pf.profiling()) return std::string();
         if constexpr (!kF32) {
             if (!f32) return std::string(role) + ":" + gemm_mfma_kernel<G>(p);
+        } else {
+            if (!f32 && !cpu_order) return std::string(role) + ":" + gemm_f32_mfma_kernel_name(p);
         }
         return std::string(role) + ":" + gemm_f32_kernel(p);
     }
@@ -164,7 +176,7 @@ template <typename G> struct GemmRunner {
         const double bytes = gemm_bytes(p.M, p.N, p.K, abytes, kF32 ? 4 : int(sizeof(G)) * weight_parts<G>(),
                                         p.swiglu ? (p.Ch ? int(sizeof(G)) * weight_parts<G>() / 2 : 2) : 4,
                                         p.res ? 4 : 0);
-        pf.timed(family(role, p, false), bytes, s, [&] { gemm_t<G>(p, s); }, 2.0 * p.M * p.N * p.K);
+        pf.timed(family(role, p, false), bytes, s, [&] { gemm_t<G>(p, s, cpu_order); }, 2.0 * p.M * p.N * p.K);
         check_launch();
     }
     // the exact fp32 VALU kernel (layers kept in fp32 in every tier)
@@ -187,7 +199,7 @@ struct SeqSpec {
 };
 
 // The sequence stages on the device: weights, activations for max_windows windows, and the forward from the
-// assembled residual stream h() [B*T][384] to one logit per window.  Activations are fp32 in HBM in every tier;
+// windows' token rows (WindowInput) to one logit per window.  Activations are fp32 in HBM in every tier;
 // G picks the GEMM arithmetic (float: exact VALU order; f16 / bf16: split-operand MFMA with the GEMM A operands
 // written pre-split by their producers).
 template <typename G> class SeqStack {
@@ -199,7 +211,8 @@ public:
              const Linear& head0, const std::vector<float>& head2_w, float head2_b, int max_windows, Uploader& up,
              DevMem& amem)
         : spec_(spec) {
-        const int swiglu_perm = kF32 ? 1 : 2;
+        cpu_order_ = kF32 && f32_cpu_order_requested();
+        const int swiglu_perm = cpu_order_ ? 1 : 2;   // VALU pairs (2j, 2j + 1) or MFMA 16-row panels
         for (int g = 0; g < 2; ++g) {
             const GdnHost& gh = gdn[g];
             Gdn& d = gdn_[g];
@@ -261,15 +274,15 @@ public:
         HIDL_ = amem.make<float>(Bm * kFF);
     }
 
-    // the residual stream [max_windows * T][384] the caller assembles before run(), from window w0 on
+    // the residual stream [max_windows * T][384], from window w0 on
     float* h(int w0 = 0) const { return H_ + size_t(w0) * spec_.T * kD; }
 
-    // h(w0) of B windows -> logits[B], in windows [w0, w0 + B) of every buffer (disjoint window ranges can run at
-    // once on different streams)
-    void run(int B, float* logits, hipStream_t s, Profiler& pf, const std::string& dump_dir, int w0 = 0,
-             float* ws = nullptr, long long ws_floats = 0) {
+    // B windows read from `in` -> logits[B], in windows [w0, w0 + B) of every buffer (disjoint window ranges can
+    // run at once on different streams)
+    void run(const WindowInput& in, int B, float* logits, hipStream_t s, Profiler& pf, const std::string& dump_dir,
+             int w0 = 0, float* ws = nullptr, long long ws_floats = 0) {
         const int T = spec_.T, M = B * T;
-        const GemmRunner<G> gr{pf, ws, ws_floats};
+        const GemmRunner<G> gr{pf, ws, ws_floats, cpu_order_};
         const size_t r0 = size_t(w0) * T;   // first row
         float *H = this->H_ + r0 * kD, *P = this->P_ + r0 * kGld, *Q = this->Q_ + r0 * kD,
               *K = this->K_ + r0 * kD, *V = this->V_ + r0 * kVD, *dec = this->dec_ + r0 * 8,
@@ -310,12 +323,18 @@ public:
             });
             check_launch();
         };
+        // the windows' rows into h, normalised for GDN-A's in-projection in the same pass
+        pf.timed("window_input", double(M) * kD * (4 + 4 + kAS), s, [&] {
+            if constexpr (kF32) launch_window_input<float>(in, gdn_[0].norm_w, H, XN, kD, B, T, s);
+            else launch_window_input<G>(in, gdn_[0].norm_w, H, XNh, 32, B, T, s, mrows_ * kD, mrows_ * 32);
+        });
+        check_launch();
         dump_f32(dump_dir, spec_.dump[0], H, size_t(T) * kD, s);
         for (int st = 0; st < 2; ++st) {
             const Gdn& gd = gdn_[st];
             const int reps = st == 0 ? 1 : 2;
             for (int r = 0; r < reps; ++r) {
-                rmsnorm_all(gd.norm_w);
+                if (st || r) rmsnorm_all(gd.norm_w);
                 GemmArgs pi;
                 pi.M = M; pi.N = kGn; pi.K = kD;
                 set_a(pi, XN, XNh, kD); pi.ldw = kD;
@@ -333,7 +352,7 @@ public:
                             return;
                         }
                     }
-                    launch_delta(Q, K, V, dec, beta, O, B, kF32, s, T);
+                    launch_delta(Q, K, V, dec, beta, O, B, cpu_order_, s, T);
                 }, 2.0 * B * T * kHeads * 4.0 * kDK * kDV);   // per token and head: decay, S^T k, k u^T, S^T q
                 check_launch();
                 pf.timed("gated_norm", double(M) * (4.0 * 2 * kVD + kAS * kVD), s, [&] {
@@ -435,6 +454,7 @@ private:
           *O_ = nullptr;
     float* dwork_ = nullptr;     // half tiers: the chunked delta rule's per-chunk products
     bool delta_chunked_ = false;
+    bool cpu_order_ = false;     // fp32 tier in the reference CPU order (f32_cpu_order_requested at load)
     float *XN_ = nullptr, *ON_ = nullptr, *HID_ = nullptr;   // fp32 tier: the sequence GEMMs' A operands
     // MFMA tiers: the same, written pre-split by their producers in the group-major layout (part q, 32-column group
     // j, row r at q * mrows_ * width + j * mrows_ * 32 + r * 32), so that each DMA load of the direct-to-LDS GEMM

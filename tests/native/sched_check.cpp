@@ -363,7 +363,7 @@ void sync_wrappers() {
         StubDevice d2(small, 2, 0);
         Frontend f2(d2, small);
         CHECK(f2.classify(host.data(), 1, cl.data()) == -1);
-        CHECK(std::string(last_error()).find("max_host_tokens >= 20") != std::string::npos);
+        CHECK(std::string(last_error()).find("max_host_tokens is below") != std::string::npos);
     }
     // predict with fewer than 20 frames per batch
     {
@@ -371,7 +371,7 @@ void sync_wrappers() {
         StubDevice d2(small, 2, 0);
         Frontend f2(d2, small);
         CHECK(f2.predict(fr.data(), 1, lg.data()) == -1);
-        CHECK(std::string(last_error()).find("max_frames >= 20") != std::string::npos);
+        CHECK(std::string(last_error()).find("max_frames is below") != std::string::npos);
     }
 }
 
@@ -421,14 +421,14 @@ void slot_hazard() {
     const Limits lim = limits(64, 8, 64, 16);
     StubDevice dev(lim, 2, 30000);
     Frontend fe(dev, lim);
-    // occupy both lanes so that the jobs below are planned together from the queue
+    // occupy both lanes so that the jobs below are planned together from the queue: 61-frame busy jobs fit a
+    // 64-frame batch neither with each other nor with a and b, and every request is built before the first submit
+    // (building under the sanitizers can take longer than a busy batch runs)
     Req b0, b1;
-    b0.frame_ids = {1};
+    b0.frame_ids = iota_ids(61, 1000);
     b0.build();
-    b1.frame_ids = {2};
+    b1.frame_ids = iota_ids(61, 2000);
     b1.build();
-    shv_hip_job* j0 = fe.submit(&b0.r);
-    shv_hip_job* j1 = fe.submit(&b1.r);
     const std::vector<int32_t> s4 = {0, 1, 2, 3};
     std::vector<int32_t> read20;
     for (int p = 0; p < 20; ++p) read20.push_back(p % 4);
@@ -447,6 +447,8 @@ void slot_hazard() {
     e.store = {9};
     e.window_slots(std::vector<int32_t>(20, 9));
     e.build();
+    shv_hip_job* j0 = fe.submit(&b0.r);
+    shv_hip_job* j1 = fe.submit(&b1.r);
     shv_hip_job* ja = fe.submit(&a.r);
     shv_hip_job* jb = fe.submit(&b.r);
     shv_hip_job* jc = fe.submit(&c.r);
@@ -531,14 +533,15 @@ void failed_batches(int32_t poison, const char* what) {
     const Limits lim = limits(64, 4, 40, 0);
     StubDevice dev(lim, 2, 20000);
     Frontend fe(dev, lim);
+    // two busy jobs of 50 frames each: neither fits a 64-frame batch with the other or with x, so they hold both
+    // lanes alone however the launcher interleaves with the submits
     Req busy0, busy1;
-    busy0.frame_ids = {1};
+    busy0.frame_ids = iota_ids(50, 100);
     busy0.build();
-    busy1.frame_ids = {2};
+    busy1.frame_ids = iota_ids(50, 200);
     busy1.build();
-    shv_hip_job* jb0 = fe.submit(&busy0.r);
-    shv_hip_job* jb1 = fe.submit(&busy1.r);
-    // x and y are planned into one batch behind the two busy lanes; x poisons it
+    // x and y are planned into one batch behind the two busy lanes; x poisons it.  Both are built before the busy
+    // jobs start (building a request under the sanitizers can take longer than a busy batch runs)
     std::atomic<int> failed_cb{0};
     Req x, y, z;
     x.frame_ids = iota_ids(20, 10);
@@ -552,6 +555,8 @@ void failed_batches(int32_t poison, const char* what) {
     y.frame_ids = iota_ids(20, 40);
     y.window_own(0);
     y.build();
+    shv_hip_job* jb0 = fe.submit(&busy0.r);
+    shv_hip_job* jb1 = fe.submit(&busy1.r);
     shv_hip_job* jx = fe.submit(&x.r);
     shv_hip_job* jy = fe.submit(&y.r);
     CHECK(Frontend::job_wait(jx) == -1);

@@ -97,21 +97,21 @@ def test_sidecar_rules(shv, weights, tmp_path):
 def test_modes_and_certificates(shv, weights, tmp_path):
     w = copy_weights(weights, tmp_path)
     assert "unknown mode" in load_err(shv, w, "int8")
-    assert "needs a quality certificate" in load_err(shv, w, "fp16")
+    assert "no certificate file at" in load_err(shv, w, "fp16")
     cert = Path(str(w) + ".hip.cert")
     cert.write_text("SHIELDV_CUDA_CERT_V2\n")
-    assert "invalid certificate file" in load_err(shv, w, "bf16")
+    assert "lacks the SHIELDV_HIP_CERT_V2 header" in load_err(shv, w, "bf16")
     sha = shv.write_weights(tmp_path / "other.weights", seed=2)
     rev = shv.library().shv_hip_compute_revision().decode()
     cert.write_text(f"SHIELDV_HIP_CERT_V2\n{sha} fp16 {rev} PASS c.json 0 threshold=0.5\n")
-    assert "no passing certificate" in load_err(shv, w, "fp16")
+    assert "has no PASS line" in load_err(shv, w, "fp16")
     mine = Path(w).read_bytes()
     import hashlib
     msha = hashlib.sha256(mine).hexdigest()
     cert.write_text(f"SHIELDV_HIP_CERT_V2\n{msha} fp16 {rev} PASS c.json 0 threshold=0.25\n")
-    assert "does not cover the threshold" in load_err(shv, w, "fp16")
+    assert "uncertified at this threshold" in load_err(shv, w, "fp16")
     cert.write_text(f"SHIELDV_HIP_CERT_V2\n{msha} fp16 hip-0000000000000000 PASS c.json 0 threshold=0.5\n")
-    assert "no passing certificate" in load_err(shv, w, "fp16")
+    assert "has no PASS line" in load_err(shv, w, "fp16")
 
 
 def test_invalid_options(shv, weights):

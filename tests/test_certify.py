@@ -83,7 +83,7 @@ def test_loader_accepts_written_line(shv, cert, weights, tmp_path):
     # the certificate covers fp16 only
     with pytest.raises(shv.ShvError) as e:
         shv.Model(w, "bf16", max_frames=20, max_windows=1)
-    assert "no passing certificate" in str(e.value)
+    assert "has no PASS line" in str(e.value)
 
 
 @pytest.mark.gpu

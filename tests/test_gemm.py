@@ -1,7 +1,9 @@
 """Pointwise-conv GEMM (the reference's bench/gpu_gemm_bench.cu) through the C-ABI tool entry
 points shv_hip_gemm_*: the literal config shapes at full M, bias + hardswish fused, A and W ~ 0.1 N(0,1) from a seed.
 
-  fp32        : bitwise equal to the oracle's GEMM (the CPU engine's K-block-64 order) on sampled rows.
+  fp32        : the engine's CNN kernels (the CPU engine's K-block-64 order) bitwise equal to the oracle's GEMM on
+                sampled rows; the fp32 matrix-core kernel (variant 4, the sequence stages') within
+                |C - C_float64| <= 1.5 (K + 8) 2^-24 (sum_k |a_k w_k| + |b|).
   fp16 / bf16 : |C - C_float64| <= 2^-17 (sum_k |a_k w_k| + |b|) on sampled rows -- the split-operand bound; plain
                 half-precision operands miss it by ~30x (checked on the CPU below, so the bar pins the split).
   variants    : every kernel variant gives bitwise the automatic choice's outputs (the reference's variant check);
@@ -43,10 +45,31 @@ def test_split_bound_rejects_plain_half_operands():
     assert ratio.max() > 8 * SPLIT_TOL
 
 
+def f32_tol(K):
+    """fp32 accumulation of K products in any order, plus the bias add and the hardswish (slope <= 1.5, a few
+    roundings): |C - C_float64| <= 1.5 (K + 8) 2^-24 (sum_k |a_k w_k| + |b|).  A dropped or transposed term
+    (|a_k w_k| ~ 1e-2 here) misses it by orders of magnitude."""
+    return 1.5 * (K + 8) * 2.0 ** -24
+
+
+def test_f32_bound_rejects_a_dropped_term():
+    """CPU check of the fp32 bar: dropping one product of the sum breaks it, fp32 summation in any order meets it."""
+    A, W, b = operands(256, 120, 40, 9)
+    ref = A.astype(np.float64) @ W.astype(np.float64).T + b
+    rev = (A[:, ::-1].astype(np.float32) @ W[:, ::-1].T.astype(np.float32) + b).astype(np.float64)
+    scale = split_bound(A, W, b)
+    assert (np.abs(rev - ref) / scale).max() <= f32_tol(40)
+    dropped = A[:, 1:].astype(np.float64) @ W[:, 1:].astype(np.float64).T + b
+    assert (np.abs(dropped - ref) / scale).max() > 100 * f32_tol(40)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,M,N,K", SHAPES)
 @pytest.mark.parametrize("mode", ["fp32", "fp16", "bf16"])
 def test_pw_gemm_parity_and_variants(shv, orc, weights, name, M, N, K, mode):
+    """fp32: the engine's own kernel choice for the CNN (the reference CPU order) bitwise equal to the oracle, with
+    every CPU-order variant bitwise equal to it; the fp32 matrix-core kernel (the sequence stages') within the fp32
+    rounding bound.  fp16 / bf16: the split bound, every variant bitwise equal to the automatic choice."""
     print(f"[gpu] gemm {name} {mode} M={M} N={N} K={K}", flush=True)
     hip = shv.Hip()
     A, W, b = operands(M, N, K, 1 + K)
@@ -60,18 +83,27 @@ def test_pw_gemm_parity_and_variants(shv, orc, weights, name, M, N, K, mode):
             C = hip.download(dC, (M, N), np.float32)
             assert np.all(np.isfinite(C))
             rows = sample_rows(M, np.random.default_rng(5))
+            x = A[rows].astype(np.float64) @ W.astype(np.float64).T + b
             if mode == "fp32":
                 o = orc.Oracle(weights)
                 ref = o.gemm(A[rows], W, b, "hs")
                 o.close()
                 assert np.array_equal(C[rows].view(np.uint32), ref.view(np.uint32))
+                g.run(dA, M, dV, db, shv.ACT_HSWISH, variant=4)
+                hip.sync()
+                mf = hip.download(dV, (M, N), np.float32)
+                ratio = np.abs(mf[rows] - hswish64(x)) / split_bound(A[rows], W, b)
+                print(f"[gpu]   fp32 matrix cores: max error / bound-scale {ratio.max():.3e} (bar {f32_tol(K):.3e})",
+                      flush=True)
+                assert np.all(np.isfinite(mf)) and ratio.max() <= f32_tol(K)
             else:
-                x = A[rows].astype(np.float64) @ W.astype(np.float64).T + b
                 ratio = np.abs(C[rows] - hswish64(x)) / split_bound(A[rows], W, b)
                 print(f"[gpu]   max error / bound-scale {ratio.max():.3e} (bar {SPLIT_TOL:.3e})", flush=True)
                 assert ratio.max() <= SPLIT_TOL
             for v in shv.GEMM_VARIANTS[mode]:
-                if v in shv.GEMM_NARROW_VARIANTS and N > 160:
+                if (v in shv.GEMM_NARROW_VARIANTS and N > 160 and mode != "fp32") or (mode == "fp32" and v == 4):
+                    continue
+                if mode == "fp32" and v == 5 and N > 128:
                     continue
                 m = min(M, 65536) if (mode == "fp32" and v == 1) else min(M, 8192) if (mode == "fp32" and v == 3) else M
                 hip.memset(dV, 0xFF, m * N * 4)

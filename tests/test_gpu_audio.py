@@ -130,6 +130,70 @@ def test_audio_device_path_strided(shv, models, atokens):
     assert np.array_equal(host.view(np.uint32), full.view(np.uint32))
 
 
+@pytest.mark.parametrize("mode", ["fp32", "fp16"])
+def test_audio_calls_ordered_across_streams(shv, models, atokens, agold, mode):
+    """Calls of one handle share its activation buffers.  A device call on a user stream returns before its kernels
+    end; a host call issued at once, and a device call on a second stream, must still run after it: every result is
+    bitwise the one of an isolated call (windows are independent rows, so the reversed batch is the reversed
+    logits)."""
+    m = models[mode]
+    full = m.sequence(atokens)
+    rev = np.ascontiguousarray(atokens[::-1])
+    hip = shv.Hip()
+    s1, s2 = hip.stream(), hip.stream()
+    d_a, d_b = hip.upload(atokens), hip.upload(rev)
+    d_oa, d_ob = hip.malloc(8 * 4), hip.malloc(8 * 4)
+    try:
+        for rep in range(3):
+            print(f"[gpu] audio {mode} calls on two streams and the host path, round {rep}", flush=True)
+            hip.memset(d_oa, 0xFF, 8 * 4)
+            hip.memset(d_ob, 0xFF, 8 * 4)
+            m.sequence_device(d_a, 8, d_oa, stream=s1)
+            host = m.sequence(rev)
+            m.sequence_device(d_b, 8, d_ob, stream=s2)
+            hip.stream_sync(s1)
+            hip.stream_sync(s2)
+            ga = hip.download(d_oa, (8,), np.float32)
+            gb = hip.download(d_ob, (8,), np.float32)
+            assert np.array_equal(ga.view(np.uint32), full.view(np.uint32)), rep
+            assert np.array_equal(host.view(np.uint32), full[::-1].view(np.uint32)), rep
+            assert np.array_equal(gb.view(np.uint32), full[::-1].view(np.uint32)), rep
+    finally:
+        for b in (d_a, d_b, d_oa, d_ob):
+            hip.free(b)
+        hip.sync()
+    assert float(np.max(np.abs(full - gold_logits(agold)))) <= LOGIT_TOL
+
+
+@pytest.mark.parametrize("mode", ["fp16", "bf16"])
+def test_audio_large_batches(shv, aweights, atokens, agold, mode, margin):
+    """Past 16 windows per launch the chunked delta-rule scan takes 64-column value blocks and the sequence GEMMs
+    larger-M tile plans: 40 windows in one launch (the golden windows repeated) give bitwise the logits of launches
+    of 8, through the host and the device entry points, within the golden bound."""
+    print(f"[gpu] audio {mode} 40-window launches", flush=True)
+    n = 40
+    idx = np.arange(n) % 8
+    many = np.ascontiguousarray(atokens[idx])
+    with shv.AudioModel(aweights, mode, max_windows=n, experimental=True) as big, \
+            shv.AudioModel(aweights, mode, max_windows=8, experimental=True) as small:
+        ref = small.sequence(atokens)
+        got = big.sequence(many)
+        hip = shv.Hip()
+        d_t, d_o = hip.upload(many), hip.malloc(n * 4)
+        try:
+            big.sequence_device(d_t, n, d_o)
+            hip.sync()
+            dev = hip.download(d_o, (n,), np.float32)
+        finally:
+            hip.free(d_t)
+            hip.free(d_o)
+    assert np.array_equal(got.view(np.uint32), ref[idx].view(np.uint32))
+    assert np.array_equal(dev.view(np.uint32), ref[idx].view(np.uint32))
+    err = float(np.max(np.abs(ref - gold_logits(agold))))
+    margin(f"audio {mode} 40-window launch vs reference", err, LOGIT_TOL)
+    assert err <= LOGIT_TOL
+
+
 def test_audio_argument_errors(shv, models, atokens):
     m = models["fp32"]
     lib = m.lib
@@ -149,7 +213,7 @@ def test_audio_profile_families(models, atokens):
     try:
         m.sequence(atokens)
         fams = m.profile_families()
-        for fam in ("assemble", "gdn_prep", "delta", "gated_norm", "sisa", "head"):
+        for fam in ("window_input", "gdn_prep", "delta", "gated_norm", "sisa", "head"):
             assert fam in fams
             st = m.profile_read(fam)
             assert st and st["launches"] >= 1 and st["ms"] > 0, fam

@@ -1,7 +1,9 @@
 """GPU parity of the HIP engine against the reference CPU engine's golden fixtures (through the C-ABI).
 
 Bars:
-  fp32  : tokens bitwise equal to the reference; logits within 4e-4 absolute; no decision flips.
+  fp32  : tokens bitwise equal to the reference (the CNN keeps the reference CPU order); logits within 4e-4 absolute,
+          no decision flips -- both with the engine's own sequence-stage arithmetic (fp32 matrix-core GEMMs,
+          key-split delta rule) and with the reference order there too (SHV_HIP_F32_CPU_ORDER=1).
   fp16  : max |logit - exact| <= FP16_TOL on the 64-clip seeded set, 0 flips at the sidecar threshold.
   bf16  : max |logit - exact| <= BF16_TOL, 0 flips.
 Row independence: a window's logit and a frame's tokens are bitwise identical whatever else is in the batch.
@@ -40,6 +42,15 @@ def digest(a):
             "head": [int(x) for x in a[:16].view(np.uint32)]}
 
 
+def load_cpu_order(shv, weights, **kw):
+    """An fp32 model in the reference CPU engine's operation order (read at load)."""
+    os.environ["SHV_HIP_F32_CPU_ORDER"] = "1"
+    try:
+        return shv.Model(weights, "fp32", **kw)
+    finally:
+        del os.environ["SHV_HIP_F32_CPU_ORDER"]
+
+
 @pytest.fixture(scope="module")
 def fp32_model(shv, weights):
     print("[gpu] load fp32", flush=True)
@@ -48,29 +59,44 @@ def fp32_model(shv, weights):
     m.close()
 
 
-def test_fp32_tokens_bitwise(fp32_model, clips, golden_tokens):
-    print("[gpu] fp32 encode clip 0", flush=True)
-    toks = fp32_model.encode_frames(clips[0])
+@pytest.fixture(scope="module")
+def fp32_cpu_model(shv, weights):
+    print("[gpu] load fp32 in the reference CPU order", flush=True)
+    m = load_cpu_order(shv, weights)
+    yield m
+    m.close()
+
+
+@pytest.mark.parametrize("order", ["engine", "cpu"])
+def test_fp32_tokens_bitwise(fp32_model, fp32_cpu_model, clips, golden_tokens, order):
+    """The exact tier's CNN performs the reference CPU engine's operation order in both settings."""
+    m = fp32_model if order == "engine" else fp32_cpu_model
+    print(f"[gpu] fp32 ({order} order) encode clip 0", flush=True)
+    toks = m.encode_frames(clips[0])
     assert toks.shape == (20, 16, 384)
     assert np.array_equal(toks[0], golden_tokens[0]), np.abs(toks[0] - golden_tokens[0]).max()
     assert np.array_equal(toks[19], golden_tokens[1])
 
 
-def test_fp32_logits(fp32_model, clips, golden_logits, golden, margin):
-    print(f"[gpu] fp32 predict {len(clips)} clips", flush=True)
-    lg = fp32_model.predict(clips)
+@pytest.mark.parametrize("order", ["engine", "cpu"])
+def test_fp32_logits(fp32_model, fp32_cpu_model, clips, golden_logits, golden, margin, order):
+    m = fp32_model if order == "engine" else fp32_cpu_model
+    print(f"[gpu] fp32 ({order} order) predict {len(clips)} clips", flush=True)
+    lg = m.predict(clips)
     err = float(np.abs(lg - golden_logits).max())
     nf = flips(lg, golden_logits, golden["threshold"])
-    print(f"[gpu] fp32 max|dlogit| = {err:.3e} over {len(clips)} clips, flips {nf}", flush=True)
-    margin(f"fp32 max|logit - reference| over {len(clips)} clips", err, FP32_TOL)
+    print(f"[gpu] fp32 ({order} order) max|dlogit| = {err:.3e} over {len(clips)} clips, flips {nf}", flush=True)
+    margin(f"fp32 ({order} order) max|logit - reference| over {len(clips)} clips", err, FP32_TOL)
     assert err <= FP32_TOL, f"fp32 max|dlogit| {err:.3e} > {FP32_TOL}"
     assert nf == 0, f"{nf} decision flips"
 
 
 def test_fp32_stages(shv, weights, clips, golden):
-    print("[gpu] fp32 stage dumps", flush=True)
+    """The reference CPU order: the 17 CNN stage outputs and the tokens bitwise the reference engine's, the sequence
+    stages by their sums (device libm in the gates)."""
+    print("[gpu] fp32 (CPU order) stage dumps", flush=True)
     stages = golden["stages_clip0"]
-    with tempfile.TemporaryDirectory() as d, shv.Model(weights, "fp32", use_graphs=0) as m:
+    with tempfile.TemporaryDirectory() as d, load_cpu_order(shv, weights, use_graphs=0) as m:
         m.set_dump_dir(d)
         m.encode_frames(clips[0][19:20])          # golden CNN stages are frame 19's
         for name in CNN_STAGES + ["tokens"]:
@@ -87,9 +113,9 @@ def test_fp32_stages(shv, weights, clips, golden):
 
 
 def test_row_independence_fp32(fp32_model, clips):
-    """A clip's logit does not depend on the rest of the batch.  One clip's small-M GEMMs (late SE projects, the
-    321-row sequence GEMMs) run their K blocks in parallel and fold them in order, the batch of 6 runs them on the
-    tiled kernel: the comparison holds the two to bitwise equal results."""
+    """A clip's logit does not depend on the rest of the batch.  One clip's GEMMs run on the matrix-core kernel's
+    small tiles and its delta rule on eight key groups per column, the batch of 6 on larger tiles and four groups:
+    the comparison holds the tilings and splits to bitwise equal results."""
     print("[gpu] fp32 row independence", flush=True)
     batch = fp32_model.predict(clips[:6])
     rev = fp32_model.predict(clips[:6][::-1])[::-1]
