@@ -153,7 +153,8 @@ int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir);
  * create repacks W on the device (synchronising `stream`); NULL + last_error on failure (fp16 / bf16 need k % 8 == 0).
  * run: variant 0 = the engine's own kernel choice; fp32: 1 GEMV, 2 tiled, 3 K blocks in parallel (1-3: the CPU
  * engine's operation order; 3 allocates its workspace of ceil(k / 64) * m * n floats and synchronises `stream`),
- * 4 the fp32 matrix cores (k % 4 == 0), 5 row per lane (CPU order, k % 4 == 0); fp16 / bf16: 1 small-M, 2..6 direct with
+ * 4 the fp32 matrix cores (k % 4 == 0), 5 narrow (CPU order; the (k, n) shapes of blocks 1-6 only: 16x16, 16x64,
+ * 64x24, 24x72, 72x24, 72x40, 40x120, 120x40); fp16 / bf16: 1 small-M, 2..6 direct with
  * 1..5 column tiles per wave, 7 LDS-staged, 8 streaming (n <= 160).  Returns 0, or -1 + last_error.  Asynchronous on
  * `stream` except fp32 variant 3. */
 typedef struct shv_hip_gemm shv_hip_gemm;
@@ -203,9 +204,9 @@ int shv_hip_delta_rule(const char* mode, const float* d_q, const float* d_k, con
 /* The gated delta rule above without any allocation, for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
  * Same arguments and results as shv_hip_delta_rule (bitwise), but asynchronous on `stream` in every variant: the
- * chunked scan (fp16 / bf16, variant 0 or 2) works in a static device array for at most 16 windows (30.5 MB per
- * GPU, held until the process ends) and rejects more windows (-1 + last_error); fp32 and token-by-token variants
- * need no work memory.  Every call on one GPU shares that array: calls that overlap on one GPU (other streams or
+ * chunked scan (variant 0 or 2, every tier) works in a static device array for at most 16 windows (30.5 MB per
+ * GPU, held until the process ends) and rejects more windows (-1 + last_error); the token-by-token variants need no
+ * work memory.  Every call on one GPU shares that array: calls that overlap on one GPU (other streams or
  * threads) race -- serialise them.  Returns 0, or -1 + last_error. */
 int shv_hip_delta_rule_noalloc(const char* mode, const float* d_q, const float* d_k, const float* d_v,
                                const float* d_decay, const float* d_beta, int n_windows, float* d_o, int variant,

@@ -759,7 +759,8 @@ void run_delta_rule(Precision p, const float* Q, const float* K, const float* V,
     const CallBuffer buf(delta_chunk_floats(n_windows) * sizeof(float), s);
     float* work = static_cast<float*>(buf.get());
     if (p == Precision::BF16) launch_delta_chunked<bf16>(Q, K, V, dec, beta, O, work, n_windows, s);
-    else launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s);
+    else if (p == Precision::FP16) launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s);
+    else launch_delta_chunked<float>(Q, K, V, dec, beta, O, work, n_windows, s);
     SHV_HIP_CHECK(hipGetLastError());
     SHV_HIP_CHECK(hipStreamSynchronize(s));
 }

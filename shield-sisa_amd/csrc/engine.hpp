@@ -152,22 +152,22 @@ void run_delta_rule(Precision p, const float* Q, const float* K, const float* V,
 constexpr int kDeltaNoAllocWindows = 16;
 void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const float* V, const float* dec,
                             const float* beta, int n_windows, float* O, int variant, hipStream_t s);
-// The kernel a delta-rule call runs: the chunked scan (fp16 / bf16), token by token with each value column's keys
-// split over lane groups in one canonical order (every tier), or token by token in the reference CPU engine's order
-// (fp32).  variant 0 = the tier's own (fp32: key split, or the reference order under SHV_HIP_F32_CPU_ORDER; half
-// tiers: chunked), 1 = token by token (fp32: the reference order; half tiers: key split), 2 = chunked (half tiers),
-// 3 = key split.  Validates the arguments.
+// The kernel a delta-rule call runs: the chunked scan (matrix cores: split operands in the half tiers, fp32 operands
+// in the exact tier), token by token with each value column's keys split over lane groups in one canonical order
+// (every tier), or token by token in the reference CPU engine's order (fp32).  variant 0 = the tier's own (the
+// chunked scan; fp32 under SHV_HIP_F32_CPU_ORDER: the reference order), 1 = token by token (fp32: the reference
+// order; half tiers: key split), 2 = chunked, 3 = key split.  Validates the arguments.
 enum class DeltaKernel { Chunked, KeySplit, Reference };
 inline DeltaKernel delta_rule_kernel(Precision p, const float* Q, const float* K, const float* V, const float* dec,
                                      const float* beta, int n_windows, const float* O, int variant) {
     if (!Q || !K || !V || !dec || !beta || !O || n_windows < 1 || n_windows > 65536)
         throw std::runtime_error("delta rule: null buffer or bad window count");
-    if (variant < 0 || variant > 3 || (p == Precision::FP32 && variant == 2))
-        throw std::runtime_error("delta rule: unknown variant for this mode");
+    if (variant < 0 || variant > 3) throw std::runtime_error("delta rule: unknown variant");
     if (variant == 3) return DeltaKernel::KeySplit;
+    if (variant == 2) return DeltaKernel::Chunked;
     if (p == Precision::FP32) {
         if (variant == 1) return DeltaKernel::Reference;
-        return f32_cpu_order_requested() ? DeltaKernel::Reference : DeltaKernel::KeySplit;
+        return f32_cpu_order_requested() ? DeltaKernel::Reference : DeltaKernel::Chunked;
     }
     return variant == 1 ? DeltaKernel::KeySplit : DeltaKernel::Chunked;
 }

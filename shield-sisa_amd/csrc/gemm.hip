@@ -236,103 +236,118 @@ __global__ void __launch_bounds__(256) gemm_f32_fold_kernel(GemmArgs p, int nkb)
     p.C[m * p.ldc + j] = epi_value(p, fold(j), b, r);
 }
 
-// Exact tier, many rows and few columns (the early and middle 1x1 layers): one lane per row, one wave per 64 rows x
-// NC columns.  Per K block of 64 the wave stages its columns' weights in LDS ([NC][16] float4, read back as
-// broadcasts: every lane reads the same address) and its row's A values in registers (16-byte loads), then runs
-// the reference's per-output sequence -- an fma chain from +0 in increasing k, the first block's chain taken as
-// is and later ones added in order -- and the epilogue: bitwise gemm_f32_kernel's results, without staging a
-// 64-wide tile for layers of 16 to 128 columns or re-reading the K block through LDS for every 4 x 4 outputs.
-// K, lda, ldw (and ld_scale) multiples of 4, 16-byte aligned A, W, scale.
-template <int NC, bool SCALE>
-__global__ void __launch_bounds__(64) gemm_f32_rows_kernel(GemmArgs p) {
-    __shared__ float4 wsh[NC][F32_BK / 4];
-    const int lane = threadIdx.x;
-    const long long m = (long long)blockIdx.x * 64 + lane;
+// Exact tier, the narrow 1x1 layers of blocks 1-6 (K <= 128 inputs, N <= 120 outputs, many rows).  A workgroup of
+// four waves takes 256 rows (one per lane) and NC of the N columns; K, N and NC are compile-time, so the row's
+// K-block inputs, the block chains and the totals live in registers.  The workgroup stages its NC weight rows in
+// LDS once (read back as broadcasts: every lane reads the same address); the per-output sequence is the
+// reference's -- per K block of 64 an fma chain from +0 in increasing k, the second block's chain added to the
+// first -- then the epilogue: bitwise gemm_f32_kernel's results.  Empty asm statements after every four k (the
+// chains as operands, then a memory clobber) keep the compiler from hoisting all weight reads ahead of the chains
+// (it did, and spilled).  Each wave
+// stages its 64 x NC outputs in LDS and stores them as 16-byte pieces of consecutive row segments.
+template <int K, int N, int NC, bool SCALE>
+__global__ void __launch_bounds__(256) gemm_f32_narrow_kernel(GemmArgs p) {
+    static_assert(K % 4 == 0 && NC % 4 == 0 && N % NC == 0 && K <= 2 * F32_BK, "narrow exact GEMM shape");
+    constexpr int CS = NC + 4;   // LDS row stride of a wave's output tile (16-byte aligned rows)
+    __shared__ float4 wsh[NC][K / 4];
+    __shared__ float cs[4][64 * CS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long long m0 = (long long)blockIdx.x * 256 + wave * 64, m = m0 + lane;
     const int n0 = blockIdx.y * NC;
     const bool live = m < p.M;
     const long long mc = live ? m : p.M - 1;
     const float* arow = p.A + mc * p.lda;
     const float* srow = SCALE ? p.scale + (mc / p.scale_rows) * p.ld_scale : nullptr;
     const float* W = static_cast<const float*>(p.W);
+    for (int i = tid; i < NC * (K / 4); i += 256) {
+        const int j = i / (K / 4), q = i % (K / 4);
+        wsh[j][q] = *reinterpret_cast<const float4*>(W + (long long)(n0 + j) * p.ldw + 4 * q);
+    }
+    __syncthreads();
     float tot[NC];
-    for (int k0 = 0; k0 < p.K; k0 += F32_BK) {
-        const int kb = min(F32_BK, p.K - k0);   // a multiple of 4
-        __syncthreads();                         // the previous block's weights have been read
-        for (int i = lane; i < NC * (F32_BK / 4); i += 64) {
-            const int j = i / (F32_BK / 4), q = i % (F32_BK / 4);
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (n0 + j < p.N && 4 * q < kb) v = *reinterpret_cast<const float4*>(W + (long long)(n0 + j) * p.ldw + k0 + 4 * q);
-            wsh[j][q] = v;
-        }
-        float a[F32_BK];
+    // one K block: the row's inputs k0 .. k0 + KB - 1 loaded, the chains run
+    const auto block = [&](auto k0c, auto kbc, float (&out)[NC]) {
+        constexpr int k0 = decltype(k0c)::value, KB = decltype(kbc)::value;
+        float a[KB];
 #pragma unroll
-        for (int q = 0; q < F32_BK / 4; ++q) {
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (4 * q < kb) {
-                v = *reinterpret_cast<const float4*>(arow + k0 + 4 * q);
-                if (SCALE) {
-                    const float4 sc = *reinterpret_cast<const float4*>(srow + k0 + 4 * q);
-                    v = make_float4(sc.x * v.x, sc.y * v.y, sc.z * v.z, sc.w * v.w);
-                }
+        for (int q = 0; q < KB / 4; ++q) {
+            float4 v = *reinterpret_cast<const float4*>(arow + k0 + 4 * q);
+            if (SCALE) {
+                const float4 sc = *reinterpret_cast<const float4*>(srow + k0 + 4 * q);
+                v = make_float4(sc.x * v.x, sc.y * v.y, sc.z * v.z, sc.w * v.w);
             }
             a[4 * q] = v.x; a[4 * q + 1] = v.y; a[4 * q + 2] = v.z; a[4 * q + 3] = v.w;
         }
-        __syncthreads();
-        float blk[NC];
 #pragma unroll
-        for (int j = 0; j < NC; ++j) blk[j] = 0.0f;
+        for (int j = 0; j < NC; ++j) out[j] = 0.0f;
 #pragma unroll
-        for (int q = 0; q < F32_BK / 4; ++q) {
-            if (4 * q >= kb) break;
+        for (int q = 0; q < KB / 4; ++q) {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                const float4 w = wsh[j][q];
-                blk[j] = __builtin_fmaf(a[4 * q], w.x, blk[j]);
-                blk[j] = __builtin_fmaf(a[4 * q + 1], w.y, blk[j]);
-                blk[j] = __builtin_fmaf(a[4 * q + 2], w.z, blk[j]);
-                blk[j] = __builtin_fmaf(a[4 * q + 3], w.w, blk[j]);
+                const float4 w = wsh[j][k0 / 4 + q];
+                out[j] = __builtin_fmaf(a[4 * q], w.x, out[j]);
+                out[j] = __builtin_fmaf(a[4 * q + 1], w.y, out[j]);
+                out[j] = __builtin_fmaf(a[4 * q + 2], w.z, out[j]);
+                out[j] = __builtin_fmaf(a[4 * q + 3], w.w, out[j]);
             }
+            // the chains of these four k are complete before the next weights are read
+#pragma unroll
+            for (int j = 0; j < NC; ++j) asm volatile("" : "+v"(out[j]));
+            asm volatile("" ::: "memory");
         }
-        if (k0 == 0) {
+    };
+    constexpr int KB0 = K < F32_BK ? K : F32_BK;
+    block(std::integral_constant<int, 0>(), std::integral_constant<int, KB0>(), tot);
+    if constexpr (K > F32_BK) {
+        float blk[NC];
+        block(std::integral_constant<int, F32_BK>(), std::integral_constant<int, K - F32_BK>(), blk);
 #pragma unroll
-            for (int j = 0; j < NC; ++j) tot[j] = blk[j];
-        } else {
-#pragma unroll
-            for (int j = 0; j < NC; ++j) tot[j] = tot[j] + blk[j];
-        }
+        for (int j = 0; j < NC; ++j) tot[j] = tot[j] + blk[j];
     }
-    if (!live) return;
-    float bv[NC], rv[NC];
+    // epilogue: bias, activation, residual (all residual values of the tile read before its first store)
+    float* ct = cs[wave];
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        const int n = min(n0 + j, p.N - 1);
-        bv[j] = p.bias ? p.bias[n] : 0.0f;
-        rv[j] = p.res ? p.R[m * p.ldr + n] : 0.0f;
+    for (int q = 0; q < NC / 4; ++q) {
+        float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = r;
+        if (p.res) r = *reinterpret_cast<const float4*>(p.R + mc * p.ldr + n0 + 4 * q);
+        if (p.bias) b = *reinterpret_cast<const float4*>(p.bias + n0 + 4 * q);
+        float4 o;
+        o.x = epi_value(p, tot[4 * q], b.x, r.x);
+        o.y = epi_value(p, tot[4 * q + 1], b.y, r.y);
+        o.z = epi_value(p, tot[4 * q + 2], b.z, r.z);
+        o.w = epi_value(p, tot[4 * q + 3], b.w, r.w);
+        *reinterpret_cast<float4*>(&ct[lane * CS + 4 * q]) = o;
     }
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < NC; ++j)
-        if (n0 + j < p.N) p.C[m * p.ldc + n0 + j] = epi_value(p, tot[j], bv[j], rv[j]);
+    for (int i = lane; i < 64 * (NC / 4); i += 64) {
+        const int row = i / (NC / 4), q = i % (NC / 4);
+        if (m0 + row < p.M)
+            *reinterpret_cast<float4*>(p.C + (m0 + row) * p.ldc + n0 + 4 * q) =
+                *reinterpret_cast<const float4*>(&ct[row * CS + 4 * q]);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ fp32 MFMA
-// The fp32 tier's pointwise and all-row sequence GEMMs on the matrix cores: v_mfma_f32_16x16x4_f32 takes fp32
-// operands, forms fp32 products and accumulates in fp32 (no reduced-precision operand type).  Fragment layout, lane
-// l = 16 g + r: A holds row r at k slot g, B column r at k slot g, C column r at rows 4 g .. 4 g + 3.
-// A workgroup of four waves, WGN of them side by side along N, owns (4 / WGN) * MT * 16 rows x WGN * NT * 16
-// columns; a wave MT x NT blocks of 16 x 16.  Per K step of 16, lane (g, r) loads A[row][k0 + 4 g .. + 3] and
-// W[column][k0 + 4 g .. + 3] as one float4 each straight from memory (the waves of a workgroup share rows and
-// columns through L1 / L2; no LDS, no barrier) and MFMA kk (0..3) of the step takes k = k0 + 4 g + kk in slot g.
-// Every output therefore receives the same MFMA sequence (steps in increasing k, kk = 0..3, accumulator from +0)
-// whatever MT, NT, WGN, M or the other rows: results are bitwise independent of the tiling and of the batch.  The
-// next step's operands are loaded while the current step's MFMAs run.  K, lda, ldw (and ld_scale) are multiples of
-// 4; a K tail loads clamped addresses and zeros.
-template <int MT, int NT, int WGN, bool SCALE>
+// The fp32 tier's all-row sequence GEMMs on the matrix cores: v_mfma_f32_16x16x4_f32 takes fp32 operands, forms
+// fp32 products and accumulates in fp32 (no reduced-precision operand type).  Fragment layout, lane l = 16 g + r:
+// A holds row r at k slot g, B column r at k slot g, C column r at rows 4 g .. 4 g + 3.
+// A workgroup of four waves owns MT x NT blocks of 16 x 16 and splits K between its waves: K runs in steps of 16,
+// and wave w takes steps w, w + 4, w + 8, ... in increasing order.  Per step, lane (g, r) loads A[row][k0 + 4 g ..
+// + 3] and W[column][k0 + 4 g .. + 3] as one float4 each straight from memory (no LDS staging), and MFMA kk (0..3)
+// takes k = k0 + 4 g + kk in slot g, into the wave's accumulator from +0.  The four partial sums are then added as
+// (w0 + w1) + (w2 + w3) through LDS and wave 0 runs the epilogue.  Every output therefore receives the same
+// operations whatever MT, NT, D, M or the other rows: results are bitwise independent of the tiling and of the
+// batch.  Each wave keeps D of its steps' operands in flight (the 321-row GEMMs of one clip are bound by load
+// latency, not by the matrix cores).  K, lda, ldw (and ld_scale) are multiples of 4; a K tail loads clamped
+// addresses and zeros.
+template <int MT, int NT, int D, bool SCALE>
 __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs p) {
-    constexpr int WGM = 4 / WGN;
+    __shared__ f32x4 part[3][MT][NT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, r = lane & 15;
-    const long long mbase = (long long)blockIdx.x * (WGM * MT * 16) + (wave / WGN) * (MT * 16);
-    const int nbase = blockIdx.y * (WGN * NT * 16) + (wave % WGN) * (NT * 16);
+    const long long mbase = (long long)blockIdx.x * (MT * 16);
+    const int nbase = blockIdx.y * (NT * 16);
     const float* W = static_cast<const float*>(p.W);
     const float* arow[MT];
     const float* srow[MT];
@@ -376,25 +391,43 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs p) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    float4 a[MT], w[NT], an[MT], wn[NT];
-    load(0, a, w);
-    for (int k0 = 0; k0 < p.K; k0 += 16) {
-        if (k0 + 16 < p.K) load(k0 + 16, an, wn);
+    // this wave's steps wave + 4 i; step i sits in ring slot i % D and is reloaded with step i + D once consumed
+    const int nsteps = (p.K + 15) / 16, mine = (nsteps - wave + 3) / 4;
+    float4 a[D][MT], w[D][NT];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
+    for (int d = 0; d < D; ++d)
+        if (d < mine) load(16 * (wave + 4 * d), a[d], w[d]);
+    for (int i0 = 0; i0 < mine; i0 += D) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+        for (int d = 0; d < D; ++d) {
+            const int i = i0 + d;
+            if (i >= mine) break;
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    const float av = kk == 0 ? a[mt].x : kk == 1 ? a[mt].y : kk == 2 ? a[mt].z : a[mt].w;
-                    const float wv = kk == 0 ? w[nt].x : kk == 1 ? w[nt].y : kk == 2 ? w[nt].z : w[nt].w;
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wv, acc[mt][nt], 0, 0, 0);
-                }
+            for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) a[mt] = an[mt];
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) w[nt] = wn[nt];
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const float av = kk == 0 ? a[d][mt].x : kk == 1 ? a[d][mt].y : kk == 2 ? a[d][mt].z : a[d][mt].w;
+                        const float wv = kk == 0 ? w[d][nt].x : kk == 1 ? w[d][nt].y : kk == 2 ? w[d][nt].z : w[d][nt].w;
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wv, acc[mt][nt], 0, 0, 0);
+                    }
+            if (i + D < mine) load(16 * (wave + 4 * (i + D)), a[d], w[d]);
+        }
     }
+    if (wave) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) part[wave - 1][mt][nt][lane] = acc[mt][nt];
+    }
+    __syncthreads();
+    if (wave) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+            acc[mt][nt] = (acc[mt][nt] + part[0][mt][nt][lane]) + (part[1][mt][nt][lane] + part[2][mt][nt][lane]);
     // lane holds C[mbase + mt * 16 + 4 g + i][nbase + nt * 16 + r]
     if (p.swiglu) {   // weight rows in 16-row panels alternating gate / up: NT even, nbase a multiple of 32
 #pragma unroll
@@ -1605,25 +1638,40 @@ void launch_kblock_f32(const GemmArgs& p, hipStream_t s) {
     const long long outs = (long long)p.M * (p.swiglu ? p.N / 2 : p.N);
     hipLaunchKernelGGL(gemm_f32_fold_kernel, dim3(cdiv(outs, 256)), dim3(256), 0, s, p, nkb);
 }
-// Row-per-lane kernel: layers of at most 128 columns with rows to fill the device (a wave per 64 rows and NC
-// columns), operands laid out for its 16-byte loads
-bool use_rows_f32(const GemmArgs& p) {
-    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-    return p.N <= 128 && p.M >= 4096 && !p.swiglu && p.K % 4 == 0 && p.lda % 4 == 0 && p.ldw % 4 == 0 &&
-           al16(p.A) && al16(p.W) && (!p.scale || (p.ld_scale % 4 == 0 && al16(p.scale)));
+// The narrow exact kernel's shapes (K, N) and column chunks NC: the 1x1 layers of blocks 1-6, at 4096 rows or more
+// (a workgroup per 256 rows and NC columns)
+template <int K, int N, int NC> void launch_narrow_f32_shape(const GemmArgs& p, hipStream_t s) {
+    const dim3 grid(cdiv(p.M, 256), N / NC);
+    if (p.scale) hipLaunchKernelGGL((gemm_f32_narrow_kernel<K, N, NC, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gemm_f32_narrow_kernel<K, N, NC, false>), grid, dim3(256), 0, s, p);
 }
-void launch_rows_f32(const GemmArgs& p, hipStream_t s) {
-    if (p.swiglu || p.K % 4 || p.lda % 4 || p.ldw % 4 || (p.scale && p.ld_scale % 4))
-        throw std::runtime_error("gemm_f32: the row-per-lane kernel needs K, lda, ldw, ld_scale % 4 == 0, no SwiGLU");
-    const bool wide = p.N % 16 == 0;
-    const dim3 grid(cdiv(p.M, 64), cdiv(p.N, wide ? 16 : 8));
-    if (wide) {
-        if (p.scale) hipLaunchKernelGGL((gemm_f32_rows_kernel<16, true>), grid, dim3(64), 0, s, p);
-        else hipLaunchKernelGGL((gemm_f32_rows_kernel<16, false>), grid, dim3(64), 0, s, p);
-    } else {
-        if (p.scale) hipLaunchKernelGGL((gemm_f32_rows_kernel<8, true>), grid, dim3(64), 0, s, p);
-        else hipLaunchKernelGGL((gemm_f32_rows_kernel<8, false>), grid, dim3(64), 0, s, p);
-    }
+bool narrow_f32_shape(const GemmArgs& p, bool launch, hipStream_t s) {
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    if (p.swiglu || p.lda % 4 || p.ldw % 4 || p.ldc % 4 || (p.res && p.ldr % 4) || !al16(p.A) || !al16(p.W) ||
+        !al16(p.C) || (p.bias && !al16(p.bias)) || (p.res && !al16(p.R)) || p.lda < p.K || p.ldw < p.K ||
+        (p.scale && (p.ld_scale % 4 || !al16(p.scale))))
+        return false;
+    struct Shape { int K, N; void (*go)(const GemmArgs&, hipStream_t); };
+    static const Shape shapes[] = {{16, 16, launch_narrow_f32_shape<16, 16, 16>},
+                                   {16, 64, launch_narrow_f32_shape<16, 64, 16>},
+                                   {64, 24, launch_narrow_f32_shape<64, 24, 8>},
+                                   {24, 72, launch_narrow_f32_shape<24, 72, 24>},
+                                   {72, 24, launch_narrow_f32_shape<72, 24, 8>},
+                                   {72, 40, launch_narrow_f32_shape<72, 40, 8>},
+                                   {40, 120, launch_narrow_f32_shape<40, 120, 24>},
+                                   {120, 40, launch_narrow_f32_shape<120, 40, 8>}};
+    for (const Shape& sh : shapes)
+        if (sh.K == p.K && sh.N == p.N) {
+            if (launch) sh.go(p, s);
+            return true;
+        }
+    return false;
+}
+bool use_narrow_f32(const GemmArgs& p) { return p.M >= 4096 && narrow_f32_shape(p, false, nullptr); }
+void launch_narrow_f32(const GemmArgs& p, hipStream_t s) {
+    if (!narrow_f32_shape(p, true, s))
+        throw std::runtime_error("gemm_f32: no narrow kernel for K=" + std::to_string(p.K) + " N=" + std::to_string(p.N) +
+                                 " with these leading dimensions / alignments");
 }
 // The exact-tier kernel for M above the GEMV range: K blocks in parallel when the tiled grid would not give every
 // CU a workgroup and the workspace holds the block sums (measured with one clip: blocks 13-15 SE projects, 57
@@ -1635,24 +1683,21 @@ bool use_kblock_f32(const GemmArgs& p) {
 }  // namespace
 
 namespace {
-// Tiles of the fp32 matrix-core GEMM by shape (every choice gives the same per-output MFMA sequence): one column
-// block per wave for N <= 16 and two for N <= 32 (the narrow early layers: no dead column blocks), else 64 x 128
-// workgroups while the grid gives every CU four of them, 64 x 64 while it gives two, 32 x 64 below (one clip).
 struct F32MfmaTile {
-    int mt, nt, wgn;
+    int mt, nt;
 };
+// Tiles of the fp32 matrix-core GEMM by shape (every choice gives the same per-output operations): 32 x 64 per
+// workgroup while that grid gives every CU eight workgroups, 16 x 32 below (one clip's 321-row GEMMs: 252 to 1,533
+// workgroups instead of 66 to 407).
 F32MfmaTile plan_f32_mfma(const GemmArgs& p) {
-    if (p.N <= 16 && !p.swiglu) return {4, 1, 1};
-    if (p.N <= 32) return {2, 2, 1};
-    const long long wide = (long long)cdiv(p.M, 64) * cdiv(p.N, 128), mid = (long long)cdiv(p.M, 64) * cdiv(p.N, 64);
-    if (wide >= 1024) return {2, 4, 2};
-    if (mid >= 512) return {2, 2, 2};
-    return {1, 2, 2};
+    if ((long long)cdiv(p.M, 32) * cdiv(p.N, 64) >= 2048) return {2, 4};
+    return {1, 2};
 }
-template <int MT, int NT, int WGN> void launch_f32_mfma(const GemmArgs& p, hipStream_t s) {
-    const dim3 grid(cdiv(p.M, (4 / WGN) * MT * 16), cdiv(p.N, WGN * NT * 16));
-    if (p.scale) hipLaunchKernelGGL((gemm_f32_mfma_kernel<MT, NT, WGN, true>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((gemm_f32_mfma_kernel<MT, NT, WGN, false>), grid, dim3(256), 0, s, p);
+template <int MT, int NT> void launch_f32_mfma(const GemmArgs& p, hipStream_t s) {
+    constexpr int D = MT * NT >= 8 ? 2 : 4;   // K steps in flight per wave: deeper for the small tiles
+    const dim3 grid(cdiv(p.M, MT * 16), cdiv(p.N, NT * 16));
+    if (p.scale) hipLaunchKernelGGL((gemm_f32_mfma_kernel<MT, NT, D, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gemm_f32_mfma_kernel<MT, NT, D, false>), grid, dim3(256), 0, s, p);
 }
 }  // namespace
 
@@ -1665,17 +1710,13 @@ void gemm_f32_mfma(const GemmArgs& p, hipStream_t s) {
                                  "16-byte aligned (K=" + std::to_string(p.K) + ")");
     if (p.swiglu && p.N % 32) throw std::runtime_error("gemm_f32_mfma: swiglu needs N % 32 == 0");
     const F32MfmaTile t = plan_f32_mfma(p);
-    if (t.wgn == 1 && t.nt == 1) launch_f32_mfma<4, 1, 1>(p, s);
-    else if (t.wgn == 1) launch_f32_mfma<2, 2, 1>(p, s);
-    else if (t.nt == 4) launch_f32_mfma<2, 4, 2>(p, s);
-    else if (t.mt == 2) launch_f32_mfma<2, 2, 2>(p, s);
-    else launch_f32_mfma<1, 2, 2>(p, s);
+    if (t.mt == 2) launch_f32_mfma<2, 4>(p, s);
+    else launch_f32_mfma<1, 2>(p, s);
 }
 
 std::string gemm_f32_mfma_kernel_name(const GemmArgs& p) {
     const F32MfmaTile t = plan_f32_mfma(p);
-    return "gemm_f32_mfma_kernel<" + std::to_string(t.mt) + "," + std::to_string(t.nt) + "," + std::to_string(t.wgn) +
-           ">";
+    return "gemm_f32_mfma_kernel<" + std::to_string(t.mt) + "," + std::to_string(t.nt) + ">";
 }
 
 void gemm_f32(const GemmArgs& p, hipStream_t s) { gemm_f32_variant(p, s, 0); }
@@ -1685,21 +1726,21 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
     switch (variant) {
     case 0:
         if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) launch_gemv_f32(p, s);
-        else if (use_rows_f32(p)) launch_rows_f32(p, s);
+        else if (use_narrow_f32(p)) launch_narrow_f32(p, s);
         else if (use_kblock_f32(p)) launch_kblock_f32(p, s);
         else launch_tiled_f32(p, s);
         return;
     case 1: launch_gemv_f32(p, s); return;
     case 2: launch_tiled_f32(p, s); return;
     case 3: launch_kblock_f32(p, s); return;
-    case 5: launch_rows_f32(p, s); return;
+    case 5: launch_narrow_f32(p, s); return;
     }
     throw std::runtime_error("gemm_f32: unknown kernel variant " + std::to_string(variant));
 }
 
 std::string gemm_f32_kernel(const GemmArgs& p) {
     if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) return "gemv_f32_kernel";
-    if (use_rows_f32(p)) return p.N % 16 == 0 ? "gemm_f32_rows_kernel<16>" : "gemm_f32_rows_kernel<8>";
+    if (use_narrow_f32(p)) return "gemm_f32_narrow_kernel<" + std::to_string(p.K) + "," + std::to_string(p.N) + ">";
     return use_kblock_f32(p) ? "gemm_f32_kblock_kernel" : "gemm_f32_kernel";
 }
 

@@ -48,9 +48,10 @@ struct GemmArgs {
 // fp32 tier: VALU GEMM, each output accumulated in K blocks of 64 (fma chain from +0 per block, block sums added
 // in order) exactly as the reference CPU engine (engine/model/isa_impl.hpp:188-317).
 void gemm_f32(const GemmArgs& p, hipStream_t s);
-// fp32 tier, pointwise and all-row sequence GEMMs: v_mfma_f32_16x16x4_f32 (fp32 operands, products and
-// accumulation).  Per output, K in steps of 16 in increasing order, four MFMAs per step, accumulator from +0: the
-// same for every tile, M and batch (row independence).  SwiGLU weights in 16-row gate / up panels (repack perm 2).
+// fp32 tier, all-row sequence GEMMs: v_mfma_f32_16x16x4_f32 (fp32 operands, products and accumulation).  Per
+// output, K in steps of 16 dealt round robin over four partial sums (each from +0, in increasing k, four MFMAs per
+// step), added as (p0 + p1) + (p2 + p3): the same for every tile, M and batch (row independence).  SwiGLU weights in
+// 16-row gate / up panels (repack perm 2).
 void gemm_f32_mfma(const GemmArgs& p, hipStream_t s);
 std::string gemm_f32_mfma_kernel_name(const GemmArgs& p);
 // fp16 / bf16 tiers: MFMA 16x16x32 on split operands (fp16 2 parts / 3 products, bf16 3 parts / 6 products) with
@@ -59,7 +60,7 @@ std::string gemm_f32_mfma_kernel_name(const GemmArgs& p);
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
 // Kernel variants, for the GEMM microbench and its bitwise variant check (every variant performs the same operation
 // sequence per output, so all give bitwise equal results).  fp32: 0 automatic, 1 GEMV, 2 tiled, 3 K blocks in
-// parallel (needs ws for ceil(K / 64) * M * N floats), 5 row per lane (N <= 128 layers; K % 4 == 0).  MFMA tiers:
+// parallel (needs ws for ceil(K / 64) * M * N floats), 5 narrow (the (K, N) shapes of blocks 1-6 only).  MFMA tiers:
 // 0 automatic, 1 small-M, 2..6 direct with 1..5 column tiles per wave, 7 LDS-staged 128 x 128, 8 streaming (N <= 160,
 // every column in one workgroup; the SE projects' kernel).
 void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant);

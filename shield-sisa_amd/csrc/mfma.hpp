@@ -1,4 +1,4 @@
-// Split-operand MFMA for the fp16 / bf16 tiers on gfx950.
+// Split-operand MFMA for the fp16 / bf16 tiers on gfx950 (and its one-part fp32 form).
 //
 // Every fp32 operand value x is carried as a sum of T parts (fp16: hi + lo, bf16: hi + mid + lo, each part the
 // rounding of what the previous parts leave).  The products whose magnitude can exceed ~2^-24 of hi*hi are issued
@@ -58,6 +58,24 @@ template <> struct Split<bf16> {
     }
 };
 
+// fp32 (the exact tier's chunked delta rule): one part, the value itself.  A 16 x 16 x 32 product in the fragment
+// layout above is the sum of eight v_mfma_f32_16x16x4_f32 (fp32 operands and products): in step e lane (g, r)
+// feeds its element e -- A[r][8 g + e] and B[8 g + e][r] -- into k slot g, so the eight steps cover k = e, 8 + e,
+// 16 + e, 24 + e for e = 0..7, and the 16 x 16 x 4 accumulator layout (column r, rows 4 g .. 4 g + 3) is the same.
+template <> struct Split<float> {
+    typedef f32x8 V8;
+    static constexpr int P = 1;
+    static constexpr int NPROD = 1;
+    static __device__ __forceinline__ int ap(int) { return 0; }
+    static __device__ __forceinline__ int wp(int) { return 0; }
+    static __device__ __forceinline__ void split(float x, float* part) { part[0] = x; }
+    static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], c, 0, 0, 0);
+        return c;
+    }
+};
+
 // 8 fp32 values -> the P part vectors of an MFMA A / B fragment
 template <typename T>
 __device__ __forceinline__ void split8(const float* x, typename Split<T>::V8* parts) {
@@ -70,11 +88,16 @@ __device__ __forceinline__ void split8(const float* x, typename Split<T>::V8* pa
     }
 }
 
-// 16 bytes of pre-split weight parts (8 elements of part q) -> V8
+// 8 elements of one part (16 bytes for the half types, 32 for fp32; 16-byte aligned) -> V8
 template <typename T>
 __device__ __forceinline__ typename Split<T>::V8 load_part8(const T* p) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    return *reinterpret_cast<const typename Split<T>::V8*>(&u);
+    if constexpr (sizeof(T) == 4) {
+        const float4 u = reinterpret_cast<const float4*>(p)[0], w = reinterpret_cast<const float4*>(p)[1];
+        return f32x8{u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+    } else {
+        const uint4 u = *reinterpret_cast<const uint4*>(p);
+        return *reinterpret_cast<const typename Split<T>::V8*>(&u);
+    }
 }
 
 // acc += A * B over all split products (fixed order, smallest first)

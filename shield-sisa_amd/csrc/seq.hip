@@ -589,17 +589,21 @@ __device__ __forceinline__ void frag_parts(const T* p, long long part_stride, ty
 #pragma unroll
     for (int q = 0; q < Split<T>::P; ++q) parts[q] = load_part8<T>(p + q * part_stride);
 }
-// 4 consecutive elements of each part <- split(v[0..3]) (8-byte stores)
+// 4 consecutive elements of each part <- split(v[0..3]) (8-byte stores; fp32: one 16-byte store)
 template <typename T>
 __device__ __forceinline__ void put4(T* p, long long part_stride, float v0, float v1, float v2, float v3) {
-    const float v[4] = {v0, v1, v2, v3};
-    T part[4][Split<T>::P];
+    if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<float4*>(p) = make_float4(v0, v1, v2, v3);
+    } else {
+        const float v[4] = {v0, v1, v2, v3};
+        T part[4][Split<T>::P];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Split<T>::split(v[e], part[e]);
+        for (int e = 0; e < 4; ++e) Split<T>::split(v[e], part[e]);
 #pragma unroll
-    for (int q = 0; q < Split<T>::P; ++q) {
-        const T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
-        *reinterpret_cast<uint2*>(p + q * part_stride) = *reinterpret_cast<const uint2*>(four);
+        for (int q = 0; q < Split<T>::P; ++q) {
+            const T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
+            *reinterpret_cast<uint2*>(p + q * part_stride) = *reinterpret_cast<const uint2*>(four);
+        }
     }
 }
 template <typename T>
@@ -1272,6 +1276,8 @@ void launch_delta_chunked(const float* Q, const float* K, const float* V, const 
 }
 template void launch_delta_chunked<f16>(const float*, const float*, const float*, const float*, const float*, float*,
                                         float*, int, hipStream_t, int);
+template void launch_delta_chunked<float>(const float*, const float*, const float*, const float*, const float*,
+                                          float*, float*, int, hipStream_t, int);
 template void launch_delta_chunked<bf16>(const float*, const float*, const float*, const float*, const float*,
                                          float*, float*, int, hipStream_t, int);
 template <typename T>
@@ -1348,7 +1354,8 @@ void run_delta_rule_noalloc(Precision p, const float* Q, const float* K, const f
                                  " windows exceed the static work area of " + std::to_string(kDeltaNoAllocWindows));
     float* work = scratch_on_current_device();
     if (p == Precision::BF16) launch_delta_chunked<bf16>(Q, K, V, dec, beta, O, work, n_windows, s, kT);
-    else launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s, kT);
+    else if (p == Precision::FP16) launch_delta_chunked<f16>(Q, K, V, dec, beta, O, work, n_windows, s, kT);
+    else launch_delta_chunked<float>(Q, K, V, dec, beta, O, work, n_windows, s, kT);
     SHV_HIP_CHECK(hipGetLastError());
 }
 

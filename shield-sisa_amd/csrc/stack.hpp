@@ -254,7 +254,7 @@ public:
         O_ = amem.make<float>(Mm * kVD);
         // half tiers: the chunked delta-rule scan (SHV_HIP_DELTA_SEQ=1 keeps the token-by-token kernel, for A/B runs)
         const char* ds = std::getenv("SHV_HIP_DELTA_SEQ");
-        delta_chunked_ = !kF32 && !(ds && *ds && std::strcmp(ds, "0") != 0);
+        delta_chunked_ = !cpu_order_ && !(ds && *ds && std::strcmp(ds, "0") != 0);
         if (delta_chunked_) dwork_ = amem.make<float>(delta_chunk_floats(int(Bm), spec_.T));
         mrows_ = (long long)Mm;
         if constexpr (kF32) {
@@ -346,11 +346,9 @@ public:
                 });
                 check_launch();
                 pf.timed("delta", double(M) * 4.0 * (2 * kD + 2 * kVD + 16), s, [&] {
-                    if constexpr (!kF32) {
-                        if (delta_chunked_) {
-                            launch_delta_chunked<G>(Q, K, V, dec, beta, O, work, B, s, T);
-                            return;
-                        }
+                    if (delta_chunked_) {
+                        launch_delta_chunked<G>(Q, K, V, dec, beta, O, work, B, s, T);
+                        return;
                     }
                     launch_delta(Q, K, V, dec, beta, O, B, cpu_order_, s, T);
                 }, 2.0 * B * T * kHeads * 4.0 * kDK * kDV);   // per token and head: decay, S^T k, k u^T, S^T q

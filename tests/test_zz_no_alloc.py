@@ -10,7 +10,7 @@ from test_delta import H, T, inputs
 
 pytestmark = pytest.mark.gpu
 
-CASES = [("fp16", 0), ("fp16", 2), ("bf16", 0), ("bf16", 2), ("fp16", 1), ("fp32", 0)]
+CASES = [("fp16", 0), ("fp16", 2), ("bf16", 0), ("bf16", 2), ("fp16", 1), ("fp32", 0), ("fp32", 1)]
 
 
 @pytest.mark.parametrize("mode,variant", CASES)
