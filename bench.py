@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""SHIELD-V batched forward benchmark on one MI355X (BASELINE.json metric).
+"""SHIELD-V batched forward benchmark on one MI355X (the headline clips/s metric).
 
 value: clips/s of the full SHIELD-V forward (uint8 crops -> logit) in FP16 at batch 128 clips (2560 frames),
        inputs resident in HBM, through the C-ABI device entry point (shv_hip_forward_device), timed with HIP events
@@ -434,6 +434,114 @@ def audio_bench(shv, hip, stream, e0, e1, steps: int, revision: str, cpu_seconds
     return out
 
 
+def config3_classify(shv, hip, stream, e0, e1, weights: Path, steps: int, windows: int = 128) -> dict:
+    """The classify-only workload: the GDN + SISA sequence stages alone on `windows` windows of N(0,1) tokens resident in
+    HBM (shv_hip_classify_device, one pass of windows * 321 rows), in the exact tier (fp32 activations and
+    arithmetic) and the bf16 tier; HIP events on the launching stream."""
+    rng = np.random.default_rng(33)
+    toks = rng.standard_normal((windows, 20, 16, 384)).astype(np.float32)
+    d_tok = hip.upload(toks)
+    d_lg = hip.malloc(windows * 4)
+    out = {"windows": windows, "tokens_per_window": 321, "d_model": 384, "inputs": "device-resident (HBM)",
+           "entry": "shv_hip_classify_device", "data": "N(0,1) tokens, seed 33"}
+    try:
+        for mode in ("fp32", "bf16"):
+            with shv.Model(weights, mode, experimental=mode != "fp32", max_frames=20, max_windows=windows) as m:
+                for _ in range(2):
+                    m.classify_device(d_tok, windows, d_lg, stream)
+                hip.stream_sync(stream)
+                hip.record(e0, stream)
+                for _ in range(steps):
+                    m.classify_device(d_tok, windows, d_lg, stream)
+                hip.record(e1, stream)
+                ms = hip.elapsed_ms(e0, e1) / steps
+                lg = hip.download(d_lg, windows, np.float32)
+            out[mode] = {"ms_per_batch": round(ms, 4), "windows_per_s": round(windows / (ms / 1000.0), 1),
+                         "finite": bool(np.isfinite(lg).all())}
+            log(f"[bench] config 3 {mode}: {ms:.3f} ms / {windows} windows -> {out[mode]['windows_per_s']} windows/s")
+    finally:
+        hip.free(d_tok)
+        hip.free(d_lg)
+    return out
+
+
+def live_update(shv, weights: Path, mode: str = "fp16", participants: int = 512, hops: int = 3,
+                new_frames=(4, 20)) -> dict:
+    """The reference's live mode (bench/gpu_bench.cpp:142-218; docs/PERFORMANCE.md:34-36): participant p owns
+    device token slots [24 p, 24 p + 24) as a ring; a warm-up hop stores every participant's first 20 frames; then
+    each hop, all participants at once (burst), submits one job per participant that encodes its `new` frames from
+    pinned host memory into the next slots and classifies the window of its last 20 frames from the slots.  Latency
+    per job = queue + run time (shv_hip_job_timing), the reference's measure; the model runs with the reference's
+    default options and participants * 24 token slots.  Requests are built before a hop starts, so the submit
+    loop is a few microseconds per job."""
+    import ctypes
+    distinct = 16
+    res = {"mode": mode, "participants": participants, "hops": hops, "arrival": "burst",
+           "entry": "shv_hip_submit (token slots)", "reference_p99_ms": {"4": 221.0, "20": 705.0},
+           "reference_hardware": "RTX A6000 (docs/PERFORMANCE.md:34-36)"}
+    with shv.Model(weights, mode, experimental=mode != "fp32", token_slots=participants * 24) as m:
+        lib = m.lib
+        nbytes = distinct * 20 * shv.FRAME_BYTES
+        hp = lib.shv_hip_host_alloc(nbytes)
+        src = np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(hp))
+        src[:] = shv.synth_clips(distinct, 2000).reshape(-1)
+        logit = np.empty(participants, np.float32)
+        try:
+            for newf in new_frames:
+                nframes = np.zeros(participants, np.int64)
+
+                def build(pi: int, nnew: int):
+                    store = np.array([pi * 24 + int((nframes[pi] + i) % 24) for i in range(nnew)], np.int32)
+                    last = int(nframes[pi]) + nnew
+                    wslots = np.array([pi * 24 + (last - 20 + t) % 24 for t in range(20)], np.int32)
+                    f0 = int(nframes[pi]) % (distinct * 20 - nnew)
+                    r = shv.Request()
+                    r.frames = hp + f0 * shv.FRAME_BYTES
+                    r.n_frames = nnew
+                    r.store_slots = store.ctypes.data
+                    r.n_windows = 1
+                    r.window_slots = wslots.ctypes.data
+                    r.logits_out = logit.ctypes.data + 4 * pi
+                    nframes[pi] = last
+                    return r, store, wslots
+
+                def run_hop(reqs):
+                    jobs = [lib.shv_hip_submit(m.h, ctypes.byref(q[0])) for q in reqs]
+                    if not all(jobs):
+                        raise shv.ShvError(shv.last_error())
+                    out = []
+                    for j in jobs:
+                        if lib.shv_hip_job_wait(j) != 0:
+                            raise shv.ShvError(lib.shv_hip_job_error(j).decode())
+                        q, r, g = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+                        bf, bw = ctypes.c_int(), ctypes.c_int()
+                        lib.shv_hip_job_timing(j, ctypes.byref(q), ctypes.byref(r), ctypes.byref(g), ctypes.byref(bf),
+                                               ctypes.byref(bw))
+                        out.append((q.value + r.value, q.value, g.value, bw.value))
+                        lib.shv_hip_job_free(j)
+                    return out
+
+                run_hop([build(pi, 20) for pi in range(participants)])   # warm-up: 20 frames each
+                rows = []
+                t0 = time.perf_counter()
+                for _ in range(hops):
+                    rows += run_hop([build(pi, newf) for pi in range(participants)])
+                wall = (time.perf_counter() - t0) * 1000.0
+                lat = np.array([x[0] for x in rows])
+                r = {"lat_p50_ms": round(float(np.percentile(lat, 50)), 3),
+                     "lat_p95_ms": round(float(np.percentile(lat, 95)), 3),
+                     "lat_p99_ms": round(float(np.percentile(lat, 99)), 3), "lat_max_ms": round(float(lat.max()), 3),
+                     "queue_p50_ms": round(float(np.percentile([x[1] for x in rows], 50)), 3),
+                     "batch_gpu_p50_ms": round(float(np.percentile([x[2] for x in rows], 50)), 3),
+                     "mean_batch_windows": round(float(np.mean([x[3] for x in rows])), 1),
+                     "wall_ms": round(wall, 1), "finite": bool(np.isfinite(logit).all())}
+                res[str(newf)] = r
+                log(f"[bench] live {mode}: {participants} participants x {newf} new frames: {r}")
+        finally:
+            lib.shv_hip_host_free(hp)
+    return res
+
+
 def roofline_of(stats: dict, steps: int, mode: str, revision: str, traffic_file: bool = True) -> dict:
     """The family with the most device time per step, against the roof its intensity selects."""
     dom = max(stats, key=lambda k: stats[k]["ms"])
@@ -484,6 +592,7 @@ def main() -> int:
     ap.add_argument("--no-crop", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-audio", action="store_true")
+    ap.add_argument("--no-live", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every GPU box here has one GPU, and the SHIELD-V forward has no "
@@ -567,6 +676,7 @@ def main() -> int:
         model.close()
         hip.free(d_frames)
         hip.free(d_logits)
+        c3 = None if args.kernel_only else config3_classify(shv, hip, stream, e0, e1, w, max(3, args.steps // 2))
         gemm = None if args.kernel_only or args.no_gemm else gemm_microbench(shv, hip, stream, e0, e1)
         audio = None
         if not args.kernel_only and not args.no_audio:
@@ -589,6 +699,10 @@ def main() -> int:
         c4 = None
         if not args.kernel_only and not args.no_async:
             c4 = async_bf16(shv, hip, w, clips)
+
+        live = None
+        if not args.kernel_only and not args.no_live:
+            live = live_update(shv, w, args.mode)
 
         cpu = None
         if not args.no_cpu and not args.kernel_only:
@@ -616,7 +730,9 @@ def main() -> int:
         "latency_b1": {"fp16": lat, "fp32": lat32} if lat else None,
         "predict_b128_e2e": e2e,
         "encoder_frames_per_s": None if enc_ms is None else round(B * 20 / (enc_ms / 1000.0), 1),
-        "sequence_windows_per_s": round(seq_wps, 1),
+        "sequence_windows_per_s_in_forward": round(seq_wps, 1),
+        "config3_classify": c3,
+        "live_update": live,
         "async_bf16_1024": c4,
         "family_ms_per_step": per_step,
         "roofline": roofline,

@@ -132,6 +132,10 @@ void shv_hip_host_free(void* p);
 int shv_hip_forward_device(shv_hip_model* m, const uint8_t* d_frames, int n_clips, float* d_logits, void* stream);
 /* encode only: d_frames (n_frames crops) -> d_tokens (n_frames x 6144 fp32), device memory. */
 int shv_hip_encode_device(shv_hip_model* m, const uint8_t* d_frames, int n_frames, float* d_tokens, void* stream);
+/* classify only (the sequence stages alone): d_tokens n_windows x [20][16][384] fp32 (a window's 20
+ * frames' tokens back to back, the layout of shv_hip_classify's host tokens) -> d_logits [n_windows], device memory;
+ * n_windows <= limits.  One pass on `stream`. */
+int shv_hip_classify_device(shv_hip_model* m, const float* d_tokens, int n_windows, float* d_logits, void* stream);
 /* Per-kernel-family timing with HIP events on the launching stream (graphs are off while enabled):
  * enable(1)/disable(0); read the accumulated milliseconds, launch count, algorithmic bytes and FLOPs of family
  * `name` (-1 if unknown); list writes the family names seen since enabling, one per line, into buf (at most cap
@@ -154,7 +158,8 @@ int shv_hip_set_dump_dir(shv_hip_model* m, const char* dir);
  * run: variant 0 = the engine's own kernel choice; fp32: 1 GEMV, 2 tiled, 3 K blocks in parallel (1-3: the CPU
  * engine's operation order; 3 allocates its workspace of ceil(k / 64) * m * n floats and synchronises `stream`),
  * 4 the fp32 matrix cores (k % 4 == 0), 5 narrow (CPU order; the (k, n) shapes of blocks 1-6 only: 16x16, 16x64,
- * 64x24, 24x72, 72x24, 72x40, 40x120, 120x40); fp16 / bf16: 1 small-M, 2..6 direct with
+ * 64x24, 24x72, 72x24, 72x40, 40x120, 120x40), 6 column chunks (CPU order, k <= 1024, k % 4 == 0); fp16 / bf16:
+ * 1 small-M, 2..6 direct with
  * 1..5 column tiles per wave, 7 LDS-staged, 8 streaming (n <= 160).  Returns 0, or -1 + last_error.  Asynchronous on
  * `stream` except fp32 variant 3. */
 typedef struct shv_hip_gemm shv_hip_gemm;

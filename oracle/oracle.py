@@ -170,6 +170,15 @@ class Reference:
             raise RuntimeError(self.lib.shv_cpu_last_error().decode())
         return out
 
+    def classify(self, tokens: np.ndarray) -> np.ndarray:
+        """tokens: b windows x [20][16][384] float32 (shv_cpu_classify, engine/include/shv_cpu.h:106-107)."""
+        tokens = np.ascontiguousarray(tokens, np.float32)
+        b = tokens.size // (20 * 16 * 384)
+        out = np.empty(b, np.float32)
+        if self.lib.shv_cpu_classify(self.h, tokens.ctypes.data, b, out.ctypes.data) != 0:
+            raise RuntimeError(self.lib.shv_cpu_last_error().decode())
+        return out
+
     def close(self):
         if self.h:
             self.lib.shv_cpu_free(self.h)

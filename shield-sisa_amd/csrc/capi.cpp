@@ -214,6 +214,13 @@ int shv_hip_forward_device(shv_hip_model* m, const uint8_t* d_frames, int n_clip
         return 0;
     });
 }
+int shv_hip_classify_device(shv_hip_model* m, const float* d_tokens, int n_windows, float* d_logits, void* stream) {
+    return guarded([&] {
+        if (!m || !d_tokens || !d_logits || n_windows < 1) throw std::runtime_error("invalid argument");
+        m->lanes->engine().classify_direct(d_tokens, n_windows, d_logits, stream_or(m, stream));
+        return 0;
+    });
+}
 int shv_hip_encode_device(shv_hip_model* m, const uint8_t* d_frames, int n_frames, float* d_tokens, void* stream) {
     return guarded([&] {
         if (!m || !d_frames || !d_tokens || n_frames < 1) throw std::runtime_error("invalid argument");

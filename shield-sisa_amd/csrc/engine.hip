@@ -213,6 +213,19 @@ public:
         run_graph(GraphKey{3, d_frames, d_logits, n}, s,
                   [&](hipStream_t q) { forward_branched(d_frames, tok_direct_, tokptr_direct_, n, d_logits, q); });
     }
+    void classify_direct(const float* d_tokens, int n, float* d_logits, hipStream_t s) override {
+        if (n <= 0) return;
+        if (n > cfg_.max_windows) throw std::runtime_error("classify: too many windows");
+        run_graph(GraphKey{5, d_tokens, d_logits, n}, s, [&](hipStream_t q) {
+            ws_on_ = true;   // one pass on q
+            WindowInput in;
+            in.tokens = d_tokens;
+            in.ldw = (long long)kFrames * kTokenFloats;
+            in.pos = pos_;
+            in.readout = readout_;
+            seq_->run(in, n, d_logits, q, *this, dump_dir_, 0, cur_ws(), ws_floats_);
+        });
+    }
 
 private:
     hipStream_t setup_ = nullptr;
@@ -252,11 +265,12 @@ private:
 
     const float* up(const float* src, size_t n) { return upl_->up(src, n); }
     const float* up(const std::vector<float>& v) { return upl_->up(v); }
+    // CNN weights: the fp16 tier stores them pre-scaled (a power of two per tensor, undone on the GEMM sums)
     template <typename U> DevW repack(const std::vector<float>& src, int N, int K, int perm) {
-        return upl_->repack<U>(src, N, K, perm);
+        return upl_->repack<U>(src, N, K, perm, false, true);
     }
     template <typename U> DevW repack_pad(const std::vector<float>& src, int N, int K, int Np, int Kp) {
-        return upl_->repack_pad<U>(src, N, K, Np, Kp);
+        return upl_->repack_pad<U>(src, N, K, Np, Kp, true);
     }
     const float* up_pad(const std::vector<float>& v, int rows, int n, int np) { return upl_->up_pad(v, rows, n, np); }
 
@@ -548,7 +562,7 @@ private:
         if constexpr (!kF32) {
             if (dump_dir_.empty()) {   // fused last 1x1 + pool (the 60x960 map is dumped only by the unfused path)
                 timed("tail_pool", double(F) * (60.0 * 160 + 16.0 * kCnnOut) * TS, s, [&] {
-                    launch_tail_pool<G>(x, last_w_.w, last_w_.stride, last_b_, a.PO, F, s);
+                    launch_tail_pool<G>(x, last_w_.w, last_w_.stride, last_w_.scale, last_b_, a.PO, F, s);
                 });
                 check_launch();
                 GemmArgs p;
@@ -624,10 +638,11 @@ private:
             a.X = cur;
             a.H = b.H; a.W = b.W; a.Ho = b.Ho; a.Wo = b.Wo;
             a.tiles_x = b.tiles_x; a.ntiles = b.ntiles; a.frames = F;
-            a.wexp = b.fexp_w.w; a.wexp_stride = b.fexp_w.stride; a.bexp = b.fexp_b;
+            a.wexp = b.fexp_w.w; a.wexp_stride = b.fexp_w.stride; a.bexp = b.fexp_b; a.sexp = b.fexp_w.scale;
             a.wdw = b.fdw_w; a.bdw = b.fdw_b;
             if (!c.se) {
                 a.wproj = b.fproj_w.w; a.wproj_stride = b.fproj_w.stride; a.bproj = b.fproj_b;
+                a.sproj = b.fproj_w.scale;
                 a.Y = nxt;
                 if (i == 0 && stem_fused) {
                     a.X = nullptr;
@@ -770,11 +785,28 @@ PwGemm::PwGemm(Precision p, int N, int K, const float* d_w, hipStream_t s) : pre
     const int parts = p == Precision::FP32 ? 1 : p == Precision::BF16 ? weight_parts<bf16>() : weight_parts<f16>();
     const size_t esz = p == Precision::FP32 ? 4 : 2;
     wstride_ = (long long)N * K;
+    // fp16: the weight pre-scaled by a power of two as the engine stores its 1x1 convolutions (a scaled copy of the
+    // caller's weights is repacked from a call-local buffer)
+    const float* src = d_w;
+    std::vector<float> h;   // held until the stream is synchronised below
+    std::unique_ptr<CallBuffer> scaled;
+    if (p == Precision::FP16) {
+        h.resize(size_t(N) * size_t(K));
+        SHV_HIP_CHECK(hipMemcpy(h.data(), d_w, h.size() * sizeof(float), hipMemcpyDeviceToHost));
+        const int S = Uploader::prescale_exp<f16>(h);
+        if (S != 0) {
+            for (float& v : h) v = std::ldexp(v, S);
+            scaled.reset(new CallBuffer(h.size() * sizeof(float), s));
+            SHV_HIP_CHECK(hipMemcpyAsync(scaled->get(), h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice, s));
+            src = static_cast<const float*>(scaled->get());
+        }
+        wscale_ = std::ldexp(1.0f, -S);
+    }
     SHV_HIP_CHECK(hipMalloc(&w_, size_t(parts) * size_t(wstride_) * esz));
     switch (p) {
-    case Precision::FP32: launch_repack<float>(d_w, static_cast<float*>(w_), N, K, 0, 1, s); break;
-    case Precision::BF16: launch_repack<bf16>(d_w, static_cast<bf16*>(w_), N, K, 0, parts, s); break;
-    case Precision::FP16: launch_repack<f16>(d_w, static_cast<f16*>(w_), N, K, 0, parts, s); break;
+    case Precision::FP32: launch_repack<float>(src, static_cast<float*>(w_), N, K, 0, 1, s); break;
+    case Precision::BF16: launch_repack<bf16>(src, static_cast<bf16*>(w_), N, K, 0, parts, s); break;
+    case Precision::FP16: launch_repack<f16>(src, static_cast<f16*>(w_), N, K, 0, parts, s); break;
     }
     const hipError_t le = hipGetLastError();
     const hipError_t se = hipStreamSynchronize(s);
@@ -793,7 +825,7 @@ void PwGemm::run(const float* A, long long M, const float* bias, int act, float*
     GemmArgs p;
     p.M = int(M); p.N = N_; p.K = K_;
     p.A = A; p.lda = K_;
-    p.W = w_; p.ldw = K_; p.wstride = wstride_;
+    p.W = w_; p.ldw = K_; p.wstride = wstride_; p.wscale = wscale_;
     p.bias = bias; p.act = kAct[act];
     p.C = C; p.ldc = N_;
     if (prec_ == Precision::FP32 && variant == 4) {

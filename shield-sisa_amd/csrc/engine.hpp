@@ -119,6 +119,8 @@ public:
     virtual void encode_direct(const uint8_t* d_frames, int F, float* d_tokens, hipStream_t s) = 0;
     // clips [n][20] frames -> logits [n], through the engine's own token buffer
     virtual void forward_direct(const uint8_t* d_frames, int n, float* d_logits, hipStream_t s) = 0;
+    // windows [n][20][16][384] of tokens in device memory -> logits [n] (the sequence stages alone)
+    virtual void classify_direct(const float* d_tokens, int n, float* d_logits, hipStream_t s) = 0;
 
     size_t weight_bytes() const { return weight_bytes_; }
     size_t device_bytes() const { return device_bytes_; }
@@ -189,6 +191,7 @@ private:
     int N_ = 0, K_ = 0;
     void* w_ = nullptr;
     long long wstride_ = 0;
+    float wscale_ = 1.0f;   // fp16: the inverse of the power of two the weight parts are stored at
 };
 
 }  // namespace shv

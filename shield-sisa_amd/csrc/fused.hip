@@ -374,7 +374,7 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
                         for (int i = 0; i < 4; ++i) {
                             const int row = mt * 16 + g * 4 + i;
                             float v = 0.0f;
-                            if (inside & (1u << (4 * j + i))) v = apply_act_nb(eacc[j][nt][i] + eb_c[nt], C::ACT);
+                            if (inside & (1u << (4 * j + i))) v = apply_act_nb(eacc[j][nt][i] * a.sexp + eb_c[nt], C::ACT);
                             Es[row * CS_LD + col] = v;
                         }
                     }
@@ -518,7 +518,7 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
                         const int oy = p / C::TW, ox = p - oy * C::TW;
                         const int gy = ty0 + oy, gx = tx0 + ox;
                         if (gy >= a.Ho || gx >= a.Wo) continue;
-                        float v = yacc[j][nt][i] + bias[nt];
+                        float v = yacc[j][nt][i] * a.sproj + bias[nt];
                         if constexpr (C::RES) {
                             if constexpr (L::PRESPLIT) v = res[nt][i] + v;
                             else v = Xs[((oy + C::PAD) * C::IW + ox + C::PAD) * C::XS_LD + n] + v;
@@ -697,7 +697,7 @@ __global__ void __launch_bounds__(IR_THREADS) ir_se_wave_kernel(IrArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float v = 0.0f;
-                if (inside & (1u << (4 * mt + i))) v = apply_act_nb(acc[i] + bias, C::ACT);
+                if (inside & (1u << (4 * mt + i))) v = apply_act_nb(acc[i] * a.sexp + bias, C::ACT);
                 Es[(mt * 16 + g * 4 + i) * WCS_LD + r] = v;
             }
         }

@@ -17,6 +17,7 @@
 #include "kernels.hpp"
 #include "mfma.hpp"
 
+#include <cmath>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -25,8 +26,10 @@ namespace shv {
 namespace {
 
 // ------------------------------------------------------------------------------------------------ epilogue
-// out = act(v + bias) (+ residual: res 1 R + v, res 2 R + v / sqrt(2), res 3 R + 0.70710678f * v)
+// out = act(v * wscale + bias) (+ residual: res 1 R + v, res 2 R + v / sqrt(2), res 3 R + 0.70710678f * v).  wscale
+// is a power of two (1 unless the weight was stored pre-scaled), so v * wscale is exact.
 __device__ __forceinline__ float epi_value(const GemmArgs& p, float v, float b, float res) {
+    v = v * p.wscale;
     if (p.bias) v = v + b;
     v = apply_act(v, p.act);
     if (p.res == 3) v = res + 0.7071067811865475244f * v;
@@ -60,6 +63,10 @@ __device__ __forceinline__ void epi_block(const GemmArgs& p, Row row, Col col, V
     }
 }
 
+// SwiGLU of the MFMA tiers from the gate and up sums
+__device__ __forceinline__ float swiglu_value(const GemmArgs& p, float gate, float up) {
+    return silu_fast(gate * p.wscale) * (up * p.wscale);
+}
 // A SwiGLU output: fp32, or its split parts when the consumer takes pre-split A
 template <typename T>
 __device__ __forceinline__ void swiglu_store(const GemmArgs& p, long long m, int col, float v) {
@@ -325,6 +332,90 @@ __global__ void __launch_bounds__(256) gemm_f32_narrow_kernel(GemmArgs p) {
         if (m0 + row < p.M)
             *reinterpret_cast<float4*>(p.C + (m0 + row) * p.ldc + n0 + 4 * q) =
                 *reinterpret_cast<const float4*>(&ct[row * CS + 4 * q]);
+    }
+}
+
+// Exact tier, layers of at most 256 columns and up to 1024 inputs at 1k-20k rows (the later projects and SE
+// projects of one clip, where the K-block kernel needs a fold pass): the narrow kernel's form with K at run time.
+// A workgroup of four waves takes 256 rows (one per lane) and 8 columns; it stages those columns' weights (all K)
+// in LDS once, and each lane runs the reference's per-output sequence over the K blocks of 64 -- its row's block
+// inputs in registers, an fma chain from +0 per block, block sums added in order -- then the epilogue: bitwise
+// gemm_f32_kernel's results.  Empty asm statements after every four k pin the chains (see the narrow kernel).
+constexpr int COLS_NC = 8, COLS_KMAX = 1024;
+template <bool SCALE>
+__global__ void __launch_bounds__(256) gemm_f32_cols_kernel(GemmArgs p) {
+    constexpr int NC = COLS_NC, CS = NC + 4;
+    __shared__ float4 wsh[NC][COLS_KMAX / 4];
+    __shared__ float cs[4][64 * CS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const long long m0 = (long long)blockIdx.x * 256 + wave * 64, m = m0 + lane;
+    const int n0 = blockIdx.y * NC;
+    const bool live = m < p.M;
+    const long long mc = live ? m : p.M - 1;
+    const float* arow = p.A + mc * p.lda;
+    const float* srow = SCALE ? p.scale + (mc / p.scale_rows) * p.ld_scale : nullptr;
+    const float* W = static_cast<const float*>(p.W);
+    const int K4 = p.K / 4;
+    for (int i = tid; i < NC * K4; i += 256) {
+        const int j = i / K4, q = i % K4;
+        wsh[j][q] = n0 + j < p.N ? *reinterpret_cast<const float4*>(W + (long long)(n0 + j) * p.ldw + 4 * q)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    __syncthreads();
+    float tot[NC];
+    for (int k0 = 0; k0 < p.K; k0 += F32_BK) {
+        const int kb = min(F32_BK, p.K - k0);   // a multiple of 4
+        float a[F32_BK];
+#pragma unroll
+        for (int q = 0; q < F32_BK / 4; ++q) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (4 * q < kb) {
+                v = *reinterpret_cast<const float4*>(arow + k0 + 4 * q);
+                if (SCALE) {
+                    const float4 sc = *reinterpret_cast<const float4*>(srow + k0 + 4 * q);
+                    v = make_float4(sc.x * v.x, sc.y * v.y, sc.z * v.z, sc.w * v.w);
+                }
+            }
+            a[4 * q] = v.x; a[4 * q + 1] = v.y; a[4 * q + 2] = v.z; a[4 * q + 3] = v.w;
+        }
+        float blk[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) blk[j] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < F32_BK / 4; ++q) {
+            if (4 * q >= kb) break;
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const float4 w = wsh[j][k0 / 4 + q];
+                blk[j] = __builtin_fmaf(a[4 * q], w.x, blk[j]);
+                blk[j] = __builtin_fmaf(a[4 * q + 1], w.y, blk[j]);
+                blk[j] = __builtin_fmaf(a[4 * q + 2], w.z, blk[j]);
+                blk[j] = __builtin_fmaf(a[4 * q + 3], w.w, blk[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < NC; ++j) asm volatile("" : "+v"(blk[j]));
+            asm volatile("" ::: "memory");
+        }
+        if (k0 == 0) {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) tot[j] = blk[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NC; ++j) tot[j] = tot[j] + blk[j];
+        }
+    }
+    // epilogue (all residual values of the tile read before its first store), staged for row-segment stores
+    float* ct = cs[wave];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int n = min(n0 + j, p.N - 1);
+        const float b = p.bias ? p.bias[n] : 0.0f, r = p.res ? p.R[mc * p.ldr + n] : 0.0f;
+        ct[lane * CS + j] = epi_value(p, tot[j], b, r);
+    }
+    __syncthreads();
+    for (int i = lane; i < 64 * NC; i += 64) {
+        const int row = i / NC, j = i % NC;
+        if (m0 + row < p.M && n0 + j < p.N) p.C[(m0 + row) * p.ldc + n0 + j] = ct[row * CS + j];
     }
 }
 
@@ -635,7 +726,7 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p
                 for (int nt = 0; nt + 1 < NT; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
-                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu_fast(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
+                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, swiglu_value(p, acc[mt][nt][i], acc[mt][nt + 1][i]));
                 }
             }
         return;
@@ -815,7 +906,7 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p, int mblocks, 
                 for (int nt = 0; nt + 1 < WN; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
-                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu_fast(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
+                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, swiglu_value(p, acc[mt][nt][i], acc[mt][nt + 1][i]));
                 }
             }
         return;
@@ -970,7 +1061,7 @@ __global__ void __launch_bounds__(128 * WGM_) gemm_dma_kernel(GemmArgs p, int mb
                 for (int nt = 0; nt + 1 < WN; nt += 2) {
                     const int panel = nbase / 16 + nt;
                     if ((panel + 1) * 16 <= p.N)
-                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu_fast(acc[mt][nt][i]) * acc[mt][nt + 1][i]);
+                        swiglu_store<T>(p, m, (panel / 2) * 16 + r, swiglu_value(p, acc[mt][nt][i], acc[mt][nt + 1][i]));
                 }
             }
         return;
@@ -1134,7 +1225,7 @@ __global__ void __launch_bounds__(64) gemm_small_kernel(GemmArgs p) {
             const long long m = mbase + g * 4 + i;
             if (m >= p.M) continue;
             const int panel = nbase / 16;
-            if ((panel + 1) * 16 <= p.N) swiglu_store<T>(p, m, (panel / 2) * 16 + r, silu_fast(acc[0][i]) * acc[1][i]);
+            if ((panel + 1) * 16 <= p.N) swiglu_store<T>(p, m, (panel / 2) * 16 + r, swiglu_value(p, acc[0][i], acc[1][i]));
         }
         return;
     }
@@ -1473,7 +1564,7 @@ constexpr int TAIL_K = 160, TAIL_N = 960, TAIL_XLD = TAIL_K + 8, TAIL_ELD = 16 +
 
 template <typename T>
 __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict__ X, const T* __restrict__ W,
-                                                        long long wstride, const float* __restrict__ bias,
+                                                        long long wstride, float wscale, const float* __restrict__ bias,
                                                         float* __restrict__ out, int F, int ns) {
     typedef Split<T> S;
     typedef typename S::V8 V8;
@@ -1530,11 +1621,12 @@ __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict_
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) acc[mt] = S::mfma(a[mt][S::ap(i)], w[ks][S::wp(i)], acc[mt]);
         }
-        // lane holds C[mt*16 + 4g + i][nt*16 + r]: + bias, hardswish (the GEMM epilogue), into this wave's rows
+        // lane holds C[mt*16 + 4g + i][nt*16 + r]: * wscale, + bias, hardswish (the GEMM epilogue), into this
+        // wave's rows
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) E[mt * 16 + 4 * g + i][r] = apply_act(acc[mt][i] + b, ACT_HS);
+            for (int i = 0; i < 4; ++i) E[mt * 16 + 4 * g + i][r] = apply_act(acc[mt][i] * wscale + b, ACT_HS);
         asm volatile("" ::: "memory");   // one wave's LDS accesses execute in issue order
         // pool: lane (channel r, bins g, g + 4, g + 8, g + 12)
 #pragma unroll
@@ -1586,6 +1678,10 @@ void check_args(const GemmArgs& p, bool mfma) {
     if (p.res && !p.R) throw std::runtime_error("gemm: residual without R");
     if (p.res < 0 || p.res > 3) throw std::runtime_error("gemm: unknown residual mode");
     if (p.scale && (p.scale_rows <= 0 || p.ld_scale < p.K)) throw std::runtime_error("gemm: bad SE scale");
+    int wexp = 0;
+    if (!(p.wscale > 0.0f) || std::frexp(p.wscale, &wexp) != 0.5f)
+        throw std::runtime_error("gemm: the weight scale must be a power of two");
+    if (!mfma && p.wscale != 1.0f) throw std::runtime_error("gemm_f32: fp32 weights are not pre-scaled");
     if (mfma) {
         // 32-byte A and 16-byte W fragments: K, lda, ldw, ld_scale multiples of 8 elements
         if (p.K % 8 || p.lda % 8 || p.ldw % 8 || (!p.Ah && p.lda < p.K) || (p.scale && p.ld_scale % 8) ||
@@ -1668,6 +1764,24 @@ bool narrow_f32_shape(const GemmArgs& p, bool launch, hipStream_t s) {
     return false;
 }
 bool use_narrow_f32(const GemmArgs& p) { return p.M >= 4096 && narrow_f32_shape(p, false, nullptr); }
+bool cols_f32_ok(const GemmArgs& p) {
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    return !p.swiglu && p.K % 4 == 0 && p.K <= COLS_KMAX && p.lda % 4 == 0 && p.ldw % 4 == 0 && p.lda >= p.K &&
+           p.ldw >= p.K && al16(p.A) && al16(p.W) && (!p.scale || (p.ld_scale % 4 == 0 && al16(p.scale)));
+}
+// Column chunks where they beat the tiled and K-block kernels (measured at one clip: blocks 8-10's expands, 4,800
+// rows, K 80, N 184-200: 13.8 vs 17.4 us; the later projects with K 240-960 ran 1.1-2x slower than K blocks + fold)
+bool use_cols_f32(const GemmArgs& p) {
+    return p.M >= 4096 && p.M <= 8192 && p.K <= 128 && p.N > 128 && p.N <= 256 && cols_f32_ok(p);
+}
+void launch_cols_f32(const GemmArgs& p, hipStream_t s) {
+    if (!cols_f32_ok(p))
+        throw std::runtime_error("gemm_f32: the column-chunk kernel needs K <= 1024, K / lda / ldw % 4 == 0, aligned "
+                                 "operands and no SwiGLU");
+    const dim3 grid(cdiv(p.M, 256), cdiv(p.N, COLS_NC));
+    if (p.scale) hipLaunchKernelGGL(gemm_f32_cols_kernel<true>, grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(gemm_f32_cols_kernel<false>, grid, dim3(256), 0, s, p);
+}
 void launch_narrow_f32(const GemmArgs& p, hipStream_t s) {
     if (!narrow_f32_shape(p, true, s))
         throw std::runtime_error("gemm_f32: no narrow kernel for K=" + std::to_string(p.K) + " N=" + std::to_string(p.N) +
@@ -1727,6 +1841,7 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
     case 0:
         if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) launch_gemv_f32(p, s);
         else if (use_narrow_f32(p)) launch_narrow_f32(p, s);
+        else if (use_cols_f32(p)) launch_cols_f32(p, s);
         else if (use_kblock_f32(p)) launch_kblock_f32(p, s);
         else launch_tiled_f32(p, s);
         return;
@@ -1734,6 +1849,7 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
     case 2: launch_tiled_f32(p, s); return;
     case 3: launch_kblock_f32(p, s); return;
     case 5: launch_narrow_f32(p, s); return;
+    case 6: launch_cols_f32(p, s); return;
     }
     throw std::runtime_error("gemm_f32: unknown kernel variant " + std::to_string(variant));
 }
@@ -1741,6 +1857,7 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
 std::string gemm_f32_kernel(const GemmArgs& p) {
     if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) return "gemv_f32_kernel";
     if (use_narrow_f32(p)) return "gemm_f32_narrow_kernel<" + std::to_string(p.K) + "," + std::to_string(p.N) + ">";
+    if (use_cols_f32(p)) return "gemm_f32_cols_kernel";
     return use_kblock_f32(p) ? "gemm_f32_kblock_kernel" : "gemm_f32_kernel";
 }
 
@@ -1791,8 +1908,8 @@ template void gemm_mfma<f16>(const GemmArgs&, hipStream_t);
 template void gemm_mfma<bf16>(const GemmArgs&, hipStream_t);
 
 template <typename T>
-void launch_tail_pool(const float* x, const void* w, long long wstride, const float* bias, float* pooled, int F,
-                      hipStream_t s) {
+void launch_tail_pool(const float* x, const void* w, long long wstride, float wscale, const float* bias,
+                      float* pooled, int F, hipStream_t s) {
     if (F <= 0) return;
     if (wstride < (long long)TAIL_N * TAIL_K) throw std::runtime_error("tail_pool: bad weight part stride");
     // workgroups per frame: a divisor of the 15 rounds of 4 tiles, so every wave gets whole tiles; one clip's 20
@@ -1800,9 +1917,11 @@ void launch_tail_pool(const float* x, const void* w, long long wstride, const fl
     // 83 vs 86 us, bf16 110 vs 115; 320 frames: 43 vs 48, 57 vs 65; five per frame slower)
     const int ns = F >= 1024 ? 1 : F >= 86 ? 3 : F >= 52 ? 5 : 15;
     hipLaunchKernelGGL(tail_pool_kernel<T>, dim3((unsigned)(F * ns)), dim3(256), 0, s, x, static_cast<const T*>(w),
-                       wstride, bias, pooled, F, ns);
+                       wstride, wscale, bias, pooled, F, ns);
 }
-template void launch_tail_pool<f16>(const float*, const void*, long long, const float*, float*, int, hipStream_t);
-template void launch_tail_pool<bf16>(const float*, const void*, long long, const float*, float*, int, hipStream_t);
+template void launch_tail_pool<f16>(const float*, const void*, long long, float, const float*, float*, int,
+                                   hipStream_t);
+template void launch_tail_pool<bf16>(const float*, const void*, long long, float, const float*, float*, int,
+                                    hipStream_t);
 
 }  // namespace shv

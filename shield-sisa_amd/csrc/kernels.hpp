@@ -16,7 +16,8 @@ typedef _Float16 f16;   // same storage types as the device code (host-visible)
 typedef __bf16 bf16;
 
 // C[m][n] = epilogue(sum_k A[m][k] * W[n][k]); A, C, R fp32 row-major; W row-major [N][K] (PyTorch Linear /
-// 1x1 conv layout).  Epilogue, per element in this order: + bias[n]; activation; residual (res 1: R + v,
+// 1x1 conv layout).  Epilogue, per element in this order: * wscale (the inverse of the power of two a pre-scaled
+// weight was stored at; 1 leaves the sum unchanged); + bias[n]; activation; residual (res 1: R + v,
 // res 2: R + v / 1.41421356f, res 3: R + 0.70710678f * v); stored fp32.  swiglu: fp32 tier -- W rows (2j, 2j+1) = (gate_j, up_j); MFMA tiers --
 // W rows in 16-row panels (gate panel, up panel, ...); out[m][j] = silu(gate) * up.
 // Optional SE prologue: A[m][k] := scale[(m / scale_rows) * ld_scale + k] * A[m][k].
@@ -24,7 +25,7 @@ typedef __bf16 bf16;
 struct GemmArgs {
     int M = 0, N = 0, K = 0;
     const float* A = nullptr; long long lda = 0;
-    const void* W = nullptr; long long ldw = 0; long long wstride = 0;
+    const void* W = nullptr; long long ldw = 0; long long wstride = 0; float wscale = 1.0f;
     const float* scale = nullptr; int scale_rows = 1; int ld_scale = 0;
     const float* bias = nullptr; int act = 0;
     float* C = nullptr; long long ldc = 0;
@@ -60,7 +61,8 @@ std::string gemm_f32_mfma_kernel_name(const GemmArgs& p);
 template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
 // Kernel variants, for the GEMM microbench and its bitwise variant check (every variant performs the same operation
 // sequence per output, so all give bitwise equal results).  fp32: 0 automatic, 1 GEMV, 2 tiled, 3 K blocks in
-// parallel (needs ws for ceil(K / 64) * M * N floats), 5 narrow (the (K, N) shapes of blocks 1-6 only).  MFMA tiers:
+// parallel (needs ws for ceil(K / 64) * M * N floats), 5 narrow (the (K, N) shapes of blocks 1-6 only), 6 column
+// chunks (K <= 1024, K % 4 == 0).  MFMA tiers:
 // 0 automatic, 1 small-M, 2..6 direct with 1..5 column tiles per wave, 7 LDS-staged 128 x 128, 8 streaming (N <= 160,
 // every column in one workgroup; the SE projects' kernel).
 void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant);
@@ -68,11 +70,11 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant);
 std::string gemm_f32_kernel(const GemmArgs& p);
 template <typename T> std::string gemm_mfma_kernel(const GemmArgs& p);
 template <typename T> void gemm_mfma_variant(const GemmArgs& p, hipStream_t s, int variant);
-// half tiers: last 1x1 (x [F*60][160] fp32, pre-split weight parts [960][160], + bias, hardswish) fused with the 4x4
-// pool -> pooled [F][16][960] fp32, bitwise equal to gemm_mfma + launch_pool
+// half tiers: last 1x1 (x [F*60][160] fp32, pre-split weight parts [960][160], * wscale, + bias, hardswish) fused
+// with the 4x4 pool -> pooled [F][16][960] fp32, bitwise equal to gemm_mfma + launch_pool
 template <typename T>
-void launch_tail_pool(const float* x, const void* w, long long wstride, const float* bias, float* pooled, int F,
-                      hipStream_t s);
+void launch_tail_pool(const float* x, const void* w, long long wstride, float wscale, const float* bias,
+                      float* pooled, int F, hipStream_t s);
 // number of weight parts an MFMA tier stores
 template <typename T> constexpr int weight_parts() { return sizeof(T) == 4 ? 1 : (std::is_same<T, bf16>::value ? 3 : 2); }
 
@@ -119,6 +121,9 @@ struct IrArgs {
     const float* bdw = nullptr;
     const void* wproj = nullptr; long long wproj_stride = 0;
     const float* bproj = nullptr;
+    // powers of two that the expand / project sums are multiplied by before their bias (the inverse of the scale the
+    // pre-scaled weight parts were stored at; 1 when they were not)
+    float sexp = 1.0f, sproj = 1.0f;
     int H = 0, W = 0, Ho = 0, Wo = 0, tiles_x = 0, ntiles = 0, frames = 0;
     // block 1 with the stem fused in: uint8 frames [F][180][320][3], byte -> float table [3][256], stem weights
     // [27][16] (tap (dy,dx,c) major) and bias [16]; X is then unused
@@ -155,9 +160,10 @@ struct CropJob {
 void native_crops(const CropJob* jobs, int n, uint8_t* out, bool i420, hipStream_t s);
 
 // ---------------------------------------------------------------- sequence (fp32 residual stream)
-// Where a batch's windows take their rows.  SHIELD-V (T = 321): frame_tokens[window * 20 + position] is the
-// frame's 16 x 384 token block, plus the position table pos [320][384]; SHIELD-A (T = 126): token t of window b at
-// tokens + b * ldw + t * 384.  The last row of every window is the readout vector.
+// Where a batch's windows take their rows: frame_tokens[window * 20 + position] is a frame's 16 x 384 token block
+// (SHIELD-V), or token t of window b is at tokens + b * ldw + t * 384 (a SHIELD-V window's 20 frames' tokens back to
+// back, ldw 122,880; a SHIELD-A window's 125 tokens).  SHIELD-V (T = 321) adds the position table pos [320][384].
+// The last row of every window is the readout vector.
 struct WindowInput {
     const float* const* frame_tokens = nullptr;
     const float* pos = nullptr;

@@ -34,11 +34,12 @@ __device__ __forceinline__ void put_value(T* base, long long pstride, long long 
 
 // ------------------------------------------------------------------------------------------------ window input
 // A window's residual stream and the A operand of GDN-A's first in-projection in one pass (no separate assembly
-// pass over h).  Row t of window b is, for SHIELD-V, token t % 16 of the frame at window position t / 16 plus
-// position row t; for SHIELD-A, token t of the window stored at tokens + b * ldw (no position table); the last row
-// is the readout vector in both.  The row is written to h, then normalised exactly as rmsnorm_kernel does it
-// (16 lanes per row, lane l owns columns l + 16 i).
-template <typename T, int TT, bool VIDEO>
+// pass over h).  Row t of window b is token t % 16 of the frame at window position t / 16 -- found through a table
+// of frame token blocks (TABLE) or at tokens + b * ldw + t * 384 (a window's 20 frames' tokens back to back, or a
+// SHIELD-A window's 125 tokens) -- plus position row t when there is a position table (SHIELD-V); the last row is
+// the readout vector.  The row is written to h, then normalised exactly as rmsnorm_kernel does it (16 lanes per
+// row, lane l owns columns l + 16 i).
+template <typename T, int TT, bool TABLE, bool POS>
 __global__ void __launch_bounds__(256)
 window_input_kernel(WindowInput in, const float* __restrict__ w, float* __restrict__ h, T* __restrict__ out,
                     long long ldo, long long pstride, long long kstride, int rows) {
@@ -52,15 +53,17 @@ window_input_kernel(WindowInput in, const float* __restrict__ w, float* __restri
     if (t == TT - 1) {
 #pragma unroll
         for (int i = 0; i < 24; ++i) v[i] = in.readout[i * 16 + l];
-    } else if constexpr (VIDEO) {
-        const float* tok = in.frame_tokens[b * kFrames + t / 16] + (t % 16) * kD;
-        const float* pos = in.pos + (long long)t * kD;
-#pragma unroll
-        for (int i = 0; i < 24; ++i) v[i] = tok[i * 16 + l] + pos[i * 16 + l];
     } else {
-        const float* tok = in.tokens + b * in.ldw + (long long)t * kD;
+        const float* tok = TABLE ? in.frame_tokens[b * kFrames + t / 16] + (t % 16) * kD
+                                 : in.tokens + b * in.ldw + (long long)t * kD;
+        if constexpr (POS) {
+            const float* pos = in.pos + (long long)t * kD;
 #pragma unroll
-        for (int i = 0; i < 24; ++i) v[i] = tok[i * 16 + l];
+            for (int i = 0; i < 24; ++i) v[i] = tok[i * 16 + l] + pos[i * 16 + l];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 24; ++i) v[i] = tok[i * 16 + l];
+        }
     }
     float acc = v[0] * v[0];
 #pragma unroll
@@ -1202,14 +1205,20 @@ template <class F> void for_window(int T, F&& f) {
 template <typename T>
 void launch_window_input(const WindowInput& in, const float* w, float* h, T* out, long long ldo, int B, int TT,
                          hipStream_t s, long long pstride, long long kstride) {
-    if (!in.readout || (TT == kT ? (!in.frame_tokens || !in.pos) : (!in.tokens || in.ldw < (long long)(TT - 1) * kD)))
-        throw std::runtime_error("window input: missing token source, or a window stride below its tokens");
+    const bool table = in.frame_tokens != nullptr;
+    if (!in.readout || (TT == kT && !in.pos) || (!table && (!in.tokens || in.ldw < (long long)(TT - 1) * kD)))
+        throw std::runtime_error("window input: missing token source or position table, or a window stride below "
+                                 "its tokens");
     const int rows = B * TT;
     const dim3 grid(cdiv((long long)rows * 16, 256));
     for_window(TT, [&](auto tt) {
         constexpr int W = decltype(tt)::value;
-        hipLaunchKernelGGL((window_input_kernel<T, W, W == kT>), grid, dim3(256), 0, s, in, w, h, out, ldo, pstride,
-                           kstride, rows);
+        const auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, in, w, h, out, ldo, pstride, kstride, rows);
+        };
+        if (table) go(window_input_kernel<T, W, true, W == kT>);
+        else if (in.pos) go(window_input_kernel<T, W, false, true>);
+        else go(window_input_kernel<T, W, false, false>);
     });
 }
 void launch_gdn_prep(const float* P, const float* conv_w, const float* conv_b, const float* neg_rate,

@@ -7,6 +7,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <cstdio>
@@ -39,6 +40,8 @@ struct DevW {
     const void* w = nullptr;
     long long stride = 0;
     long long ld = 0, kstride = 32;
+    // the parts hold w * 2^S (exact); the GEMM multiplies its sums by scale = 2^-S (1 unless pre-scaled)
+    float scale = 1.0f;
 };
 
 // owner of device allocations
@@ -81,29 +84,49 @@ public:
     const float* up(const std::vector<float>& v) { return up(v.data(), v.size()); }
     // fp32 [N][K] rows -> device parts of U with a row permutation, converted by the repack kernel on the GPU;
     // group_major: parts in the group-major GEMM operand layout
+    // prescale (fp16 parts only): the parts hold w * 2^S with S such that max |w| * 2^S lies in [2^13, 2^14), and
+    // DevW::scale = 2^-S.  fp16 has 5 exponent bits: at He-init magnitudes (|w| ~ 0.05) the lo part of an unscaled
+    // weight is subnormal, quantised to 2^-24 in absolute terms, so hi + lo holds the weight to ~1e-6 of its size
+    // instead of ~2^-22; scaled, both parts of every weight above max |w| * 2^-16 are normal.  A power of two leaves
+    // the weight's digits unchanged, and the GEMM's sums scale back exactly.
     template <typename U>
-    DevW repack(const std::vector<float>& src, int N, int K, int perm, bool group_major = false) {
+    DevW repack(const std::vector<float>& src, int N, int K, int perm, bool group_major = false,
+                bool prescale = false) {
         const int parts = weight_parts<U>();
-        float* st = staging_.make<float>(src.size());
-        SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
+        const int S = prescale ? prescale_exp<U>(src) : 0;
+        float* st = stage(src, S);
         U* d = wmem_.make<U>(size_t(parts) * N * K);
         launch_repack<U>(st, d, N, K, perm, parts, s_, group_major);
         check_launch();
         DevW w{d, (long long)N * K};
+        w.scale = std::ldexp(1.0f, -S);
         if (group_major) {
             w.ld = 32;
             w.kstride = (long long)N * 32;
         }
         return w;
     }
-    template <typename U> DevW repack_pad(const std::vector<float>& src, int N, int K, int Np, int Kp) {
+    template <typename U>
+    DevW repack_pad(const std::vector<float>& src, int N, int K, int Np, int Kp, bool prescale = false) {
         const int parts = weight_parts<U>();
-        float* st = staging_.make<float>(src.size());
-        SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
+        const int S = prescale ? prescale_exp<U>(src) : 0;
+        float* st = stage(src, S);
         U* d = wmem_.make<U>(size_t(parts) * Np * Kp);
         launch_repack_pad<U>(st, d, N, K, Np, Kp, parts, s_);
         check_launch();
-        return DevW{d, (long long)Np * Kp};
+        DevW w{d, (long long)Np * Kp};
+        w.scale = std::ldexp(1.0f, -S);
+        return w;
+    }
+    // the exponent S of a prescaled repack (0 for the other part types, an all-zero or non-finite tensor)
+    template <typename U> static int prescale_exp(const std::vector<float>& src) {
+        if (!std::is_same<U, f16>::value) return 0;
+        float mx = 0.0f;
+        for (float v : src) mx = std::max(mx, std::fabs(v));
+        if (!(mx > 0.0f) || !std::isfinite(mx)) return 0;
+        int e = 0;
+        std::frexp(mx, &e);   // mx in [2^(e-1), 2^e)
+        return std::max(-100, std::min(100, 14 - e));
     }
     // [rows][n] -> [rows][np], zero padded
     const float* up_pad(const std::vector<float>& v, int rows, int n, int np) {
@@ -111,6 +134,18 @@ public:
         for (int r = 0; r < rows; ++r)
             for (int j = 0; j < n; ++j) o[size_t(r) * np + j] = v[size_t(r) * n + j];
         return up(o);
+    }
+    // src * 2^S into the staging buffer (exact: a power of two)
+    float* stage(const std::vector<float>& src, int S) {
+        float* st = staging_.make<float>(src.size());
+        if (S == 0) {
+            SHV_HIP_CHECK(hipMemcpy(st, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice));
+        } else {
+            std::vector<float> v(src.size());
+            for (size_t i = 0; i < v.size(); ++i) v[i] = std::ldexp(src[i], S);
+            SHV_HIP_CHECK(hipMemcpy(st, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+        }
+        return st;
     }
     void finish() {
         SHV_HIP_CHECK(hipStreamSynchronize(s_));
@@ -168,6 +203,7 @@ template <typename G> struct GemmRunner {
         }
         p.W = w.w;
         p.wstride = w.stride;
+        p.wscale = w.scale;
         if (w.ld) {
             p.ldw = w.ld;
             p.wkstride = w.kstride;

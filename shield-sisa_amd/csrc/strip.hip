@@ -212,8 +212,11 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
                 const int c = rest % (C::CT * 16), q = rest / (C::CT * 16);
                 We[(q * C::CT * 16 + c) * C::KP + k] = wexp[q * a.wexp_stride + (long long)c * CINP + k];
             }
+            // the expand sums run at the pre-scaled weights' scale 1 / sexp from a bias at that scale (exact:
+            // powers of two) and are scaled back before the activation
+            const float einv = 1.0f / a.sexp;
             for (int i = tid; i < C::CT * 16; i += ST_THREADS) {
-                Be[i] = a.bexp[i];
+                Be[i] = a.bexp[i] * einv;
                 Be[C::CT * 16 + i] = -__builtin_inff();
             }
         }
@@ -269,7 +272,8 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
 #pragma unroll
     for (int ot = 0; ot < C::OT; ++ot) {
         const float4 v = *reinterpret_cast<const float4*>(a.bproj + ot * 16 + 4 * g);
-        pb[ot] = f32x4{v.x, v.y, v.z, v.w};
+        const float pinv = 1.0f / a.sproj;   // the project sums run at the weights' scale, from the bias at it
+        pb[ot] = f32x4{v.x * pinv, v.y * pinv, v.z * pinv, v.w * pinv};
     }
 
     const int H = a.H, W = a.W, Ho = a.Ho, Wo = a.Wo;
@@ -396,7 +400,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
 #pragma unroll
                                 for (int ks = 0; ks < C::KSI; ++ks) acc = mfma_split16<T>(wf[ks], xf[j][t][ks], acc);
 #pragma unroll
-                                for (int i = 0; i < 4; ++i) acc[i] = relu_nb(acc[i]);
+                                for (int i = 0; i < 4; ++i) acc[i] = relu_nb(acc[i] * a.sexp);
                             } else {
                                 acc = zero_rows();
                             }
@@ -474,7 +478,8 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
                 for (int ot = 0; ot < C::OT; ++ot) {
                     const int n = ot * 16 + 4 * g;
                     if (!store_lane || n >= C::COUT) continue;
-                    float4 v = make_float4(y[qr][ot][0], y[qr][ot][1], y[qr][ot][2], y[qr][ot][3]);
+                    float4 v = make_float4(y[qr][ot][0] * a.sproj, y[qr][ot][1] * a.sproj, y[qr][ot][2] * a.sproj,
+                                           y[qr][ot][3] * a.sproj);
                     if constexpr (C::RES) {
                         const float4 x = res[qr][ot];
                         v.x = x.x + v.x; v.y = x.y + v.y; v.z = x.z + v.z; v.w = x.w + v.w;
@@ -695,7 +700,8 @@ __device__ __forceinline__ void accum_row(f32x4 (&acc)[C::R], const float (&wd)[
 
 template <typename T, class C, int J>
 __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4][C::NWR], const typename Split<T>::V8 (&wf)[C::KS32][Split<T>::P],
-                                        const f32x4 (&init)[C::NT], const T* Xs, int r, int g, int iy0, int H) {
+                                        const f32x4 (&init)[C::NT], const T* Xs, int r, int g, int iy0, int H,
+                                        float es) {
     if constexpr (J < C::IR) {
         typedef typename Split<T>::V8 V8;
         constexpr int P = Split<T>::P;
@@ -714,7 +720,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
                     x = mfma_wx<T>(wf[ks], xf, x);
                 }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[i] = apply_act_nb(x[i], C::ACT);
+                for (int i = 0; i < 4; ++i) x[i] = apply_act_nb(x[i] * es, C::ACT);
                 e[t] = x;
             }
         } else {
@@ -753,7 +759,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
             }
         }
         accum_row<C, J, 0>(acc, wd, v);
-        wg_rows<T, C, J + 1>(acc, wd, wf, init, Xs, r, g, iy0, H);
+        wg_rows<T, C, J + 1>(acc, wd, wf, init, Xs, r, g, iy0, H, es);
     }
 }
 
@@ -833,7 +839,7 @@ __device__ __forceinline__ void tap_variants(const f32x4 (&e)[C::NT], f32x4 (&v)
 // the depthwise over rows whose expand accumulators are ready (ROLLK)
 template <class C, int J>
 __device__ __forceinline__ void wg_rows_acc(f32x4 (&acc)[C::R], const float (&wd)[4][C::NWR],
-                                            const f32x4 (&ea)[C::XRN][C::NT], int iy0, int H) {
+                                            const f32x4 (&ea)[C::XRN][C::NT], int iy0, int H, float es) {
     if constexpr (J < C::IR) {
         f32x4 e[C::NT];
         if constexpr (J >= C::XR0 && J < C::XR0 + C::XRN) {
@@ -842,7 +848,7 @@ __device__ __forceinline__ void wg_rows_acc(f32x4 (&acc)[C::R], const float (&wd
 #pragma unroll
             for (int t = 0; t < C::NT; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) e[t][i] = in ? apply_act_nb(ea[J - C::XR0][t][i], C::ACT) : 0.0f;
+                for (int i = 0; i < 4; ++i) e[t][i] = in ? apply_act_nb(ea[J - C::XR0][t][i] * es, C::ACT) : 0.0f;
         } else {   // never staged: outside the map (whole-map staging)
 #pragma unroll
             for (int t = 0; t < C::NT; ++t) e[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -850,7 +856,7 @@ __device__ __forceinline__ void wg_rows_acc(f32x4 (&acc)[C::R], const float (&wd
         f32x4 v[C::KS];
         tap_variants<C>(e, v);
         accum_row<C, J, 0>(acc, wd, v);
-        wg_rows_acc<C, J + 1>(acc, wd, ea, iy0, H);
+        wg_rows_acc<C, J + 1>(acc, wd, ea, iy0, H, es);
     }
 }
 
@@ -969,8 +975,9 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                 for (int ot = 0; ot < C::OT; ++ot) {
                     float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                     if (wave == 0) b = *reinterpret_cast<const float4*>(a.bproj + ot * 16 + 4 * g);
+                    const float pinv = 1.0f / a.sproj;   // project sums at the weights' scale (exact)
 #pragma unroll
-                    for (int q = 0; q < C::R; ++q) y[q][ot] = f32x4{b.x, b.y, b.z, b.w};
+                    for (int q = 0; q < C::R; ++q) y[q][ot] = f32x4{b.x * pinv, b.y * pinv, b.z * pinv, b.w * pinv};
                 }
             }
             for (int ct = wave + C::WAVES * cgroup; ct < C::CT; ct += C::WAVES * csplit) {
@@ -992,11 +999,14 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                     const float4 v = *reinterpret_cast<const float4*>(src);
                     wd[0][w] = v.x; wd[1][w] = v.y; wd[2][w] = v.z; wd[3][w] = v.w;
                 }
+                // expand sums at the pre-scaled weights' scale 1 / sexp, from the bias at that scale (exact)
                 const float4 be = *reinterpret_cast<const float4*>(a.bexp + c);
+                const float einv = 1.0f / a.sexp;
                 f32x4 init[C::NT];
 #pragma unroll
                 for (int t = 0; t < C::NT; ++t)
-                    init[t] = pin[t] ? f32x4{be.x, be.y, be.z, be.w} : f32x4{-1e30f, -1e30f, -1e30f, -1e30f};
+                    init[t] = pin[t] ? f32x4{be.x * einv, be.y * einv, be.z * einv, be.w * einv}
+                                     : f32x4{-1e30f, -1e30f, -1e30f, -1e30f};
                 V4 pw[C::PROJ ? C::OT : 1][P];
                 if constexpr (C::PROJ) {
 #pragma unroll
@@ -1015,9 +1025,9 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                 if constexpr (C::ROLLK) {
                     f32x4 ea[C::XRN][C::NT];
                     wg_expand_rolled<T, C>(ea, wexp, a.wexp_stride, ct, init, Xs, r, g, C::S * oy0 - C::PADK, H);
-                    wg_rows_acc<C, 0>(acc, wd, ea, C::S * oy0 - C::PADK, H);
+                    wg_rows_acc<C, 0>(acc, wd, ea, C::S * oy0 - C::PADK, H, a.sexp);
                 } else {
-                    wg_rows<T, C, 0>(acc, wd, wf, init, Xs, r, g, C::S * oy0 - C::PADK, H);
+                    wg_rows<T, C, 0>(acc, wd, wf, init, Xs, r, g, C::S * oy0 - C::PADK, H, a.sexp);
                 }
                 constexpr int BL = C::KS * C::KS;   // bias lane index (taps 0 .. BL-1)
                 f32x4 d[C::R];
@@ -1077,6 +1087,7 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                         const float4 u = Yb[((w * C::R + q) * C::OT + ot) * 64 + lane];
                         v.x = v.x + u.x; v.y = v.y + u.y; v.z = v.z + u.z; v.w = v.w + u.w;
                     }
+                    v.x = v.x * a.sproj; v.y = v.y * a.sproj; v.z = v.z * a.sproj; v.w = v.w * a.sproj;
                     if constexpr (C::RES) {
                         v.x = res.x + v.x; v.y = res.y + v.y; v.z = res.z + v.z; v.w = res.w + v.w;
                     }

@@ -67,6 +67,7 @@ _SIGS = {
     "shv_hip_host_free": (None, [_P]),
     "shv_hip_forward_device": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
     "shv_hip_encode_device": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
+    "shv_hip_classify_device": (ctypes.c_int, [_P, _P, ctypes.c_int, _P, _P]),
     "shv_hip_profile_enable": (ctypes.c_int, [_P, ctypes.c_int]),
     "shv_hip_profile_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P, _P, _P]),
     "shv_hip_profile_list": (ctypes.c_longlong, [_P, _P, ctypes.c_size_t]),
@@ -326,6 +327,10 @@ class Model:
         if self.lib.shv_hip_forward_device(self.h, d_frames, n_clips, d_logits, stream) != 0:
             raise ShvError(self._err())
 
+    def classify_device(self, d_tokens: int, n_windows: int, d_logits: int, stream: int | None = None) -> None:
+        if self.lib.shv_hip_classify_device(self.h, d_tokens, n_windows, d_logits, stream) != 0:
+            raise ShvError(self._err())
+
     def encode_device(self, d_frames: int, n_frames: int, d_tokens: int, stream: int | None = None) -> None:
         if self.lib.shv_hip_encode_device(self.h, d_frames, n_frames, d_tokens, stream) != 0:
             raise ShvError(self._err())
@@ -523,7 +528,7 @@ class Hip:
 
 
 ACT_NONE, ACT_RELU, ACT_HSWISH, ACT_SILU, ACT_HSIGMOID = 0, 1, 2, 3, 4   # the reference's codes (common.cuh:69)
-GEMM_VARIANTS = {"fp32": [1, 2, 3, 4, 5], "fp16": list(range(1, 9)), "bf16": list(range(1, 9))}
+GEMM_VARIANTS = {"fp32": [1, 2, 3, 4, 5, 6], "fp16": list(range(1, 9)), "bf16": list(range(1, 9))}
 GEMM_NARROW_VARIANTS = {8}   # N <= 160 only
 
 

@@ -1,4 +1,4 @@
-"""Pointwise-conv GEMM (the reference's bench/gpu_gemm_bench.cu) through the C-ABI tool entry
+"""Pointwise-conv GEMM (the wide 1x1-conv workload, the reference's bench/gpu_gemm_bench.cu) through the C-ABI tool entry
 points shv_hip_gemm_*: the literal config shapes at full M, bias + hardswish fused, A and W ~ 0.1 N(0,1) from a seed.
 
   fp32        : the engine's CNN kernels (the CPU engine's K-block-64 order) bitwise equal to the oracle's GEMM on
