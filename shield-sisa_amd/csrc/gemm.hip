@@ -219,6 +219,125 @@ __global__ void __launch_bounds__(256) gemm_f32_kblock_kernel(GemmArgs p) {
         }
     }
 }
+// The tiled and K-block kernels' arithmetic with 16-byte operand traffic (K, lda, ldw, ld_scale multiples of 4, A, W,
+// scale 16-byte aligned).  A K block is staged k-major -- As[k][m], Ws[k][n] -- from float4 global loads (lane i of a
+// wave takes row i, so the transposing LDS stores are conflict-free), and each k step reads one float4 of A rows and
+// one of W columns for its 16 fmas instead of eight scalars.  The next block's float4s are loaded into registers
+// while the current one computes.  Per output the operations are the tiled kernel's (fma chain from +0 per 64-wide K
+// block in increasing k, block sums added left to right, the same epilogue), so the results are bitwise equal.
+// PART: one K block per workgroup (blockIdx.z), its chains written to the workspace for gemm_f32_fold_kernel.
+template <bool SCALE, bool PART>
+__global__ void __launch_bounds__(256) gemm_f32_v4_kernel(GemmArgs p) {
+    __shared__ float4 As[F32_BK][F32_BM / 4];
+    __shared__ float4 Ws[F32_BK][F32_BN / 4];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const long long m0 = (long long)blockIdx.x * F32_BM;
+    const int n0 = blockIdx.y * F32_BN;
+    const float* A = p.A;
+    const float* W = static_cast<const float*>(p.W);
+    const int kfirst = PART ? int(blockIdx.z) * F32_BK : 0;
+    const int kend = PART ? min(p.K, kfirst + F32_BK) : p.K;
+    // staging: float4 i of the tile is row (i & 63), k quad (i >> 6); four per thread
+    float4 ra[4], rw[4];
+    const int srow = tid & 63, sq = tid >> 6;
+    const long long gm = m0 + srow;
+    const int gn = n0 + srow;
+    const float* arow = A + min(gm, (long long)p.M - 1) * p.lda;
+    const float* wrow = W + (long long)min(gn, p.N - 1) * p.ldw;
+    const float* srow_scale = SCALE ? p.scale + (min(gm, (long long)p.M - 1) / p.scale_rows) * p.ld_scale : nullptr;
+    const auto load = [&](int k0, int kb) {
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int kq = sq + 4 * it;
+            const bool kin = 4 * kq < kb;
+            const int gk = k0 + 4 * min(kq, kb / 4 - 1);
+            float4 a = *reinterpret_cast<const float4*>(arow + gk);
+            if (SCALE) {
+                const float4 sc = *reinterpret_cast<const float4*>(srow_scale + gk);
+                a = make_float4(sc.x * a.x, sc.y * a.y, sc.z * a.z, sc.w * a.w);
+            }
+            const float4 w = *reinterpret_cast<const float4*>(wrow + gk);
+            ra[it] = kin && gm < p.M ? a : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            rw[it] = kin && gn < p.N ? w : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    const auto store = [&](int kb) {
+        float* as = reinterpret_cast<float*>(As);
+        float* ws = reinterpret_cast<float*>(Ws);
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int kq = sq + 4 * it;
+            if (4 * kq >= kb) continue;
+            const float av[4] = {ra[it].x, ra[it].y, ra[it].z, ra[it].w};
+            const float wv[4] = {rw[it].x, rw[it].y, rw[it].z, rw[it].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                as[(4 * kq + e) * F32_BM + srow] = av[e];
+                ws[(4 * kq + e) * F32_BN + srow] = wv[e];
+            }
+        }
+    };
+    float tot[4][4], blk[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tot[i][j] = 0.0f;
+    load(kfirst, min(F32_BK, kend - kfirst));
+    for (int k0 = kfirst; k0 < kend; k0 += F32_BK) {
+        const int kb = min(F32_BK, kend - k0);
+        store(kb);
+        __syncthreads();
+        if (k0 + F32_BK < kend) load(k0 + F32_BK, min(F32_BK, kend - k0 - F32_BK));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) blk[i][j] = 0.0f;
+#pragma unroll 4
+        for (int kk = 0; kk < kb; ++kk) {
+            const float4 a4 = As[kk][ty], w4 = Ws[kk][tx];
+            const float a[4] = {a4.x, a4.y, a4.z, a4.w}, w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) blk[i][j] = __builtin_fmaf(a[i], w[j], blk[i][j]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tot[i][j] = k0 == kfirst ? blk[i][j] : tot[i][j] + blk[i][j];
+        __syncthreads();
+    }
+    if constexpr (PART) {
+        float* out = p.ws + (long long)blockIdx.z * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const long long m = m0 + ty * 4 + i;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int n = n0 + tx * 4 + j;
+                if (n < p.N) out[m * p.N + n] = tot[i][j];
+            }
+        }
+        return;
+    } else {
+        if (p.swiglu) {  // rows (2j, 2j+1) = (gate_j, up_j): this thread holds pairs j0, j0+1
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const long long m = m0 + ty * 4 + i;
+                if (m >= p.M) continue;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int n = n0 + tx * 4 + 2 * q;
+                    if (n + 1 < p.N) p.C[m * p.ldc + (n >> 1)] = silu(tot[i][2 * q]) * tot[i][2 * q + 1];
+                }
+            }
+            return;
+        }
+        epi_block<4>(p, [&](int i) { return m0 + ty * 4 + i; }, [&](int j) { return n0 + tx * 4 + j; },
+                     [&](int i, int j) { return tot[i][j]; });
+    }
+}
 // one thread per output: the K-block sums folded in order, then gemm_f32_kernel's epilogue (SwiGLU: weight rows
 // 2j, 2j + 1 = gate, up of output j)
 __global__ void __launch_bounds__(256) gemm_f32_fold_kernel(GemmArgs p, int nkb) {
@@ -1719,8 +1838,19 @@ void launch_gemv_f32(const GemmArgs& p, hipStream_t s) {
         else hipLaunchKernelGGL((gemv_f32_kernel<false, false>), grid, dim3(64), 0, s, p, nkb, opw, rpw);
     }
 }
+// the 16-byte staging of gemm_f32_v4_kernel applies
+bool v4_f32_ok(const GemmArgs& p) {
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    return p.K % 4 == 0 && p.lda % 4 == 0 && p.ldw % 4 == 0 && p.lda >= p.K && p.ldw >= p.K && al16(p.A) &&
+           al16(p.W) && (!p.scale || (p.ld_scale % 4 == 0 && al16(p.scale)));
+}
 void launch_tiled_f32(const GemmArgs& p, hipStream_t s) {
     const dim3 grid(cdiv(p.M, F32_BM), cdiv(p.N, F32_BN));
+    if (v4_f32_ok(p)) {
+        if (p.scale) hipLaunchKernelGGL((gemm_f32_v4_kernel<true, false>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_f32_v4_kernel<false, false>), grid, dim3(256), 0, s, p);
+        return;
+    }
     if (p.scale) hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(256), 0, s, p);
 }
@@ -1729,8 +1859,14 @@ void launch_kblock_f32(const GemmArgs& p, hipStream_t s) {
     if (!p.ws || (long long)nkb * p.M * p.N > p.ws_floats)
         throw std::runtime_error("gemm_f32: the K-block kernel needs a workspace of ceil(K / 64) * M * N floats");
     const dim3 grid(cdiv(p.M, F32_BM), cdiv(p.N, F32_BN), (unsigned)nkb);
-    if (p.scale) hipLaunchKernelGGL(gemm_f32_kblock_kernel<true>, grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL(gemm_f32_kblock_kernel<false>, grid, dim3(256), 0, s, p);
+    if (v4_f32_ok(p)) {
+        if (p.scale) hipLaunchKernelGGL((gemm_f32_v4_kernel<true, true>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_f32_v4_kernel<false, true>), grid, dim3(256), 0, s, p);
+    } else if (p.scale) {
+        hipLaunchKernelGGL(gemm_f32_kblock_kernel<true>, grid, dim3(256), 0, s, p);
+    } else {
+        hipLaunchKernelGGL(gemm_f32_kblock_kernel<false>, grid, dim3(256), 0, s, p);
+    }
     const long long outs = (long long)p.M * (p.swiglu ? p.N / 2 : p.N);
     hipLaunchKernelGGL(gemm_f32_fold_kernel, dim3(cdiv(outs, 256)), dim3(256), 0, s, p, nkb);
 }
@@ -1769,11 +1905,9 @@ bool cols_f32_ok(const GemmArgs& p) {
     return !p.swiglu && p.K % 4 == 0 && p.K <= COLS_KMAX && p.lda % 4 == 0 && p.ldw % 4 == 0 && p.lda >= p.K &&
            p.ldw >= p.K && al16(p.A) && al16(p.W) && (!p.scale || (p.ld_scale % 4 == 0 && al16(p.scale)));
 }
-// Column chunks where they beat the tiled and K-block kernels (measured at one clip: blocks 8-10's expands, 4,800
-// rows, K 80, N 184-200: 13.8 vs 17.4 us; the later projects with K 240-960 ran 1.1-2x slower than K blocks + fold)
-bool use_cols_f32(const GemmArgs& p) {
-    return p.M >= 4096 && p.M <= 8192 && p.K <= 128 && p.N > 128 && p.N <= 256 && cols_f32_ok(p);
-}
+// Column chunks are not chosen automatically: at one clip's shapes the 16-byte tiled kernel beats them (blocks 8-10's
+// expands, 4,800 rows, K 80, N 184-200: 10.3-11.5 vs 13.6-13.8 us; N 480-960: 15-23 vs 26-42 us), and K blocks +
+// fold beat them on the long-K projects.  Kept as an explicit variant.
 void launch_cols_f32(const GemmArgs& p, hipStream_t s) {
     if (!cols_f32_ok(p))
         throw std::runtime_error("gemm_f32: the column-chunk kernel needs K <= 1024, K / lda / ldw % 4 == 0, aligned "
@@ -1841,7 +1975,6 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
     case 0:
         if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) launch_gemv_f32(p, s);
         else if (use_narrow_f32(p)) launch_narrow_f32(p, s);
-        else if (use_cols_f32(p)) launch_cols_f32(p, s);
         else if (use_kblock_f32(p)) launch_kblock_f32(p, s);
         else launch_tiled_f32(p, s);
         return;
@@ -1857,7 +1990,7 @@ void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant) {
 std::string gemm_f32_kernel(const GemmArgs& p) {
     if (p.M <= GV_MAXM && cdiv(p.K, F32_BK) <= 32) return "gemv_f32_kernel";
     if (use_narrow_f32(p)) return "gemm_f32_narrow_kernel<" + std::to_string(p.K) + "," + std::to_string(p.N) + ">";
-    if (use_cols_f32(p)) return "gemm_f32_cols_kernel";
+    if (v4_f32_ok(p)) return use_kblock_f32(p) ? "gemm_f32_v4_kernel<part>" : "gemm_f32_v4_kernel";
     return use_kblock_f32(p) ? "gemm_f32_kblock_kernel" : "gemm_f32_kernel";
 }
 
