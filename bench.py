@@ -12,7 +12,9 @@ extra: batch-1 end-to-end latency through shv_hip_predict (pinned host clip, H2D
        through the async API with HBM and MFMA rates and fp32 parity (config 4); the reference CPU engine
        (compiled from the reference sources into oracle/_ref) timed on this host's cores; the SHIELD-A sequence
        stages at 256 windows (fp16 and fp32, device-resident and from host memory) beside the reference SHIELD-A
-       engine's CPU sequence.
+       engine's CPU sequence; the whole SHIELD-A model from PCM (10 s windows, 128 per batch, device-resident, every
+       tier) beside the reference engine's CPU path from PCM; classify alone on 128 N(0,1) windows (fp32, bf16);
+       the live-update mode over device token slots (512 participants x 4 / 20 new frames).
 roofline: the dominant kernel is the profiling family (one kernel at the shapes the forward gives it) with the
        largest device time per step, from a per-kernel pass with HIP events on the launching stream (graphs off).
        Its algorithmic bytes and FLOPs per launch are recorded by the engine (maps in and out, weights; 2 M N K);
@@ -434,6 +436,80 @@ def audio_bench(shv, hip, stream, e0, e1, steps: int, revision: str, cpu_seconds
     return out
 
 
+AUDIO_PCM_WINDOWS = 128
+
+
+def audio_pcm_cpu_baseline(weights: Path, pcm: np.ndarray, seconds: float) -> dict | None:
+    """The reference SHIELD-A engine from PCM (frontend + sequence, exact mode, compiled from the reference sources
+    into oracle/_ref) on this host's cores: one window per call, min(16, visible cores) calls in flight."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from concurrent.futures import ThreadPoolExecutor
+    if not oracle.AUDIO_SO.exists():
+        return None
+    visible = len(os.sched_getaffinity(0))
+    threads = max(1, min(16, visible))
+    ref = oracle.AudioReference(weights)
+    ref.predict(pcm[:1])
+    n, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        while time.perf_counter() - t0 < seconds:
+            list(ex.map(lambda i: ref.predict(pcm[i % len(pcm):i % len(pcm) + 1]), range(n, n + 2 * threads)))
+            n += 2 * threads
+    dt = time.perf_counter() - t0
+    ref.close()
+    return {"value": round(n / dt, 2), "unit": "windows/s", "cores": threads, "kind": "reference",
+            "cpu": cpu_model(), "host_cpus_visible": visible,
+            "sample": f"reference SHIELD-A PCM -> logit (frontend_cnn + sequence), exact mode, {n} windows in "
+                      f"{dt:.1f} s on {threads} threads (one window per call)"}
+
+
+def audio_pcm_bench(shv, hip, stream, e0, e1, steps: int, revision: str, cpu_seconds: float | None) -> dict:
+    """Row f4, the whole SHIELD-A model: 10 s windows of 16 kHz PCM resident in HBM -> logits through
+    shv_hip_audio_predict_device (log-mel, CNN, frequency attention, tokens, sequence stages) in every tier; HIP events
+    on the launching stream; the roofline of the dominant kernel family; the reference's CPU path beside it."""
+    out = {"workload": f"shielda_pcm_b{AUDIO_PCM_WINDOWS}", "windows": AUDIO_PCM_WINDOWS,
+           "samples_per_window": 160000, "inputs": "device-resident (HBM)", "entry": "shv_hip_audio_predict_device",
+           "data": "synthetic (seeded SHLDA001 whole-model weights, PCM N(0, 0.1^2) clipped to [-1, 1])"}
+    with tempfile.TemporaryDirectory() as td:
+        w = Path(td) / "audio_model.shlda"
+        shv.write_audio_model_weights(w, 5)
+        pcm = shv.audio_pcm(AUDIO_PCM_WINDOWS, 23)
+        d_pcm = hip.upload(pcm)
+        d_out = hip.malloc(AUDIO_PCM_WINDOWS * 4)
+        for mode in ("fp16", "bf16", "fp32"):
+            log(f"[bench] audio PCM {mode}: {AUDIO_PCM_WINDOWS} windows")
+            m = shv.AudioModel(w, mode, max_windows=AUDIO_PCM_WINDOWS, experimental=mode != "fp32")
+            for _ in range(2):
+                m.predict_device(d_pcm, AUDIO_PCM_WINDOWS, d_out, stream=stream)
+            hip.stream_sync(stream)
+            hip.record(e0, stream)
+            for _ in range(steps):
+                m.predict_device(d_pcm, AUDIO_PCM_WINDOWS, d_out, stream=stream)
+            hip.record(e1, stream)
+            ms = hip.elapsed_ms(e0, e1) / steps
+            logits = hip.download(d_out, AUDIO_PCM_WINDOWS, np.float32)
+            m.profile_enable(True)
+            m.predict_device(d_pcm, AUDIO_PCM_WINDOWS, d_out, stream=stream)
+            hip.stream_sync(stream)
+            stats = {f: m.profile_read(f) for f in m.profile_families()}
+            m.profile_enable(False)
+            stats = {k: v for k, v in stats.items() if v and v["launches"]}
+            fam = {k: round(v["ms"], 3) for k, v in sorted(stats.items(), key=lambda kv: -kv[1]["ms"])}
+            wps = AUDIO_PCM_WINDOWS / (ms / 1000.0)
+            out[mode] = {"windows_per_s": round(wps, 1), "ms_per_batch": round(ms, 4),
+                         "audio_seconds_per_s": round(wps * 10.0, 1), "finite": bool(np.isfinite(logits).all()),
+                         "family_ms": fam, "roofline": roofline_of(stats, 1, mode, revision, traffic_file=False)}
+            log(f"[bench] audio PCM {mode}: {ms:.3f} ms / {AUDIO_PCM_WINDOWS} windows -> {wps:.0f} windows/s; "
+                f"dominant {out[mode]['roofline']['kernel']}")
+            m.close()
+        hip.free(d_pcm)
+        hip.free(d_out)
+        if cpu_seconds:
+            out["cpu_baseline"] = audio_pcm_cpu_baseline(w, pcm, cpu_seconds)
+    return out
+
+
 def config3_classify(shv, hip, stream, e0, e1, weights: Path, steps: int, windows: int = 128) -> dict:
     """The classify-only workload: the GDN + SISA sequence stages alone on `windows` windows of N(0,1) tokens resident in
     HBM (shv_hip_classify_device, one pass of windows * 321 rows), in the exact tier (fp32 activations and
@@ -678,10 +754,12 @@ def main() -> int:
         hip.free(d_logits)
         c3 = None if args.kernel_only else config3_classify(shv, hip, stream, e0, e1, w, max(3, args.steps // 2))
         gemm = None if args.kernel_only or args.no_gemm else gemm_microbench(shv, hip, stream, e0, e1)
-        audio = None
+        audio = audio_pcm = None
         if not args.kernel_only and not args.no_audio:
             audio = audio_bench(shv, hip, stream, e0, e1, max(3, args.steps // 2), revision,
                                 None if args.no_cpu else min(5.0, args.cpu_seconds))
+            audio_pcm = audio_pcm_bench(shv, hip, stream, e0, e1, max(3, args.steps // 2), revision,
+                                        None if args.no_cpu else min(5.0, args.cpu_seconds))
         hip.stream_destroy(stream)
 
         lat = lat32 = None
@@ -741,6 +819,7 @@ def main() -> int:
         "gemm_microbench": gemm,
         "face_crops": crops,
         "shielda_sequence": audio,
+        "shielda_pcm": audio_pcm,
         "revision": revision,
     }
     print(json.dumps(line), flush=True)

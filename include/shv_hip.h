@@ -218,20 +218,22 @@ int shv_hip_delta_rule_noalloc(const char* mode, const float* d_q, const float* 
                                void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
- * SHIELD-A sequence stages on the GPU.  The audio model's frontend (PCM -> 125 tokens of 384 per 10 s window,
- * engine/audio/frontend.cpp) stays on the host; these entry points replace its per-window call of
- * shield::sequence (engine/audio/core.hpp:26, engine/audio/sequence.cpp:349: tokens + readout -> GDN-A -> GDN-B x2
- * -> SISA last row -> head -> logit), batched over windows, with the SHIELD-V sequence kernels.  The reference
- * exports this stage through no C entry point of its own (its C API starts from PCM, engine/audio/include/shield.h:
- * 39-41), so these have no one-to-one counterpart there.
- * Modes: "fp32" (the reference's operation order in the GEMMs; elementwise functions are the device's, within a
- * few ulp of glibc's) and "fp16" / "bf16" (split-operand matrix cores, fp32-level operand precision); the production
- * library loads "fp32" only, the experimental library every mode.  A handle serialises its calls.
- * Functions return 0 (or a non-NULL handle) on success, -1 / NULL + shv_hip_last_error() on failure. */
+ * SHIELD-A on the GPU: the whole audio model from PCM (shv_hip_audio_predict*: the frontend, engine/audio/
+ * frontend.cpp -- log-mel frames, CNN, frequency attention, 125 tokens of 384 per 10 s window -- then the sequence
+ * stages) in place of the reference's shield_predict / shield_predict_batch (engine/audio/include/shield.h:39-41,
+ * engine/audio/api.cpp:194-216), and the sequence stages alone from tokens (shv_hip_audio_sequence*: the per-window
+ * call of shield::sequence, engine/audio/core.hpp:26, sequence.cpp:349: tokens + readout -> GDN-A -> GDN-B x2 ->
+ * SISA last row -> head -> logit, which the reference exports through no C entry point of its own), batched over
+ * windows, with the SHIELD-V sequence kernels.
+ * Modes: "fp32" (fp32 operands and arithmetic throughout; the GEMMs on the fp32 matrix cores; elementwise functions
+ * are the device's, within a few ulp of glibc's) and "fp16" / "bf16" (split-operand matrix cores, fp32-level operand
+ * precision); the production library loads "fp32" only, the experimental library every mode.  A handle serialises
+ * its calls.  Functions return 0 (or a non-NULL handle) on success, -1 / NULL + shv_hip_last_error() on failure. */
 typedef struct shv_hip_audio shv_hip_audio;
 
-/* The sequence tensors of a SHLDA001 file (container: engine/audio/weights.cpp:16-48; tensors and shapes:
- * engine/audio/sequence.cpp:290-317) on `device`, buffers for max_windows (1..4096) windows per launch. */
+/* A SHLDA001 file (container: engine/audio/weights.cpp:16-48; sequence tensors and shapes: engine/audio/
+ * sequence.cpp:290-317; frontend tensors, when present: frontend.cpp:146-160) on `device`, buffers for max_windows
+ * (1..4096) windows per launch.  Files without the frontend's tensors load for the token entry points only. */
 shv_hip_audio* shv_hip_audio_load(const char* weights, const char* mode, int device, int max_windows);
 void shv_hip_audio_free(shv_hip_audio* a);
 const char* shv_hip_audio_mode(const shv_hip_audio* a);
@@ -245,8 +247,22 @@ int shv_hip_audio_sequence(shv_hip_audio* a, const float* tokens, size_t n, size
  * ended, whatever streams they were issued on (an event of the handle orders them). */
 int shv_hip_audio_sequence_device(shv_hip_audio* a, const float* d_tokens, int n, size_t stride, float* d_logits,
                                   void* stream);
+/* 1 when the handle's weights carry the frontend (the PCM entry points work), else 0 */
+int shv_hip_audio_has_frontend(const shv_hip_audio* a);
+/* n windows of 16 kHz PCM (window w at pcm + w * stride_samples, stride_samples >= 160000; every sample finite and
+ * in [-1, 1], else -1 before any work) -> logits[n] (host); synchronous, any n (batches of max_windows).  The logits
+ * are NaN after a failure.  Replaces shield_predict_batch (engine/audio/api.cpp:200-216; shield_predict is n = 1). */
+int shv_hip_audio_predict(shv_hip_audio* a, const float* pcm, size_t n, size_t stride_samples, float* logits);
+/* the same on device buffers, asynchronous on `stream` (NULL = the handle's own stream), n <= max_windows; the PCM is
+ * not range-checked.  Ordered with the handle's other calls as shv_hip_audio_sequence_device. */
+int shv_hip_audio_predict_device(shv_hip_audio* a, const float* d_pcm, int n, size_t stride_samples,
+                                 float* d_logits, void* stream);
+/* the frontend alone (shield::frontend_cnn, engine/audio/frontend.cpp:258-280, without its stream cache): host PCM
+ * as shv_hip_audio_predict -> tokens [n][125][384] (host) */
+int shv_hip_audio_frontend(shv_hip_audio* a, const float* pcm, size_t n, size_t stride_samples, float* tokens);
 /* per-kernel-family timing and stage dumps, as shv_hip_profile_* / shv_hip_set_dump_dir (dump names: tokens, gdn_a,
- * gdn_b, sisa_last, logit -- the reference's, sequence.cpp:324-345) */
+ * gdn_b, sisa_last, logit -- the reference's, sequence.cpp:324-345; from PCM also mel ([80][997]) and cnn
+ * ([125][384]), frontend.cpp:272-275) */
 int shv_hip_audio_profile_enable(shv_hip_audio* a, int on);
 int shv_hip_audio_profile_read(shv_hip_audio* a, const char* name, double* total_ms, long long* launches,
                                double* bytes, double* flops);

@@ -1,4 +1,5 @@
-// TEST INFRASTRUCTURE ONLY: a C entry point into the reference SHIELD-A engine's sequence stages, compiled together
+// TEST INFRASTRUCTURE ONLY: C entry points into the reference SHIELD-A engine (its sequence stages, its frontend and
+// the two together), compiled together
 // with that engine's own sources (oracle/Makefile, target ref).  It loads SHLDA001 weights with the reference's
 // loader (engine/audio/weights.cpp), checks the sequence tensors (engine/audio/sequence.cpp:304-331) and evaluates
 // shield::sequence (sequence.cpp:346: 125 tokens + readout -> GDN-A -> GDN-B x2 -> SISA last row -> head -> logit)
@@ -9,7 +10,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <exception>
+#include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace {
 thread_local std::string g_err;
@@ -44,6 +47,40 @@ __attribute__((visibility("default"))) int ora_audio_sequence(void* h, const flo
         return 0;
     } catch (const std::exception& e) {
         unsetenv("SHIELD_DUMP_DIR");
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// The frontend alone (shield::frontend_cnn, engine/audio/frontend.cpp:258-280, no cache): 160,000 PCM samples ->
+// tokens [125][384].  With a dump directory the engine also writes mel.f32 ([80][997]) and cnn.f32 there.
+__attribute__((visibility("default"))) int ora_audio_frontend(void* h, const float* pcm, float* tokens,
+                                                              const char* dump_dir) {
+    try {
+        if (dump_dir && *dump_dir) setenv("SHIELD_DUMP_DIR", dump_dir, 1);
+        std::vector<float> out;
+        shield::frontend_cnn(*static_cast<shield::Weights*>(h), pcm, out, nullptr);
+        if (dump_dir && *dump_dir) unsetenv("SHIELD_DUMP_DIR");
+        if (out.size() != 125 * 384) throw std::runtime_error("frontend returned an unexpected token count");
+        std::memcpy(tokens, out.data(), out.size() * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        unsetenv("SHIELD_DUMP_DIR");
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// PCM -> logit as the engine's worker computes it (engine/audio/api.cpp:58-70 without a cache): frontend, then the
+// sequence stages.
+__attribute__((visibility("default"))) int ora_audio_predict(void* h, const float* pcm, float* logit) {
+    try {
+        std::vector<float> tokens;
+        const auto& w = *static_cast<shield::Weights*>(h);
+        shield::frontend_cnn(w, pcm, tokens, nullptr);
+        shield::sequence(w, tokens.data(), *logit);
+        return 0;
+    } catch (const std::exception& e) {
         g_err = e.what();
         return -1;
     }

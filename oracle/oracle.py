@@ -186,9 +186,10 @@ class Reference:
 
 
 class AudioReference:
-    """The reference SHIELD-A engine's sequence stages (engine/audio, compiled by `make -C oracle ref` with
-    oracle/audio_ref_driver.cpp): tokens [125][384] -> logit, exact mode, optional stage dumps (tokens, gdn_a, gdn_b,
-    sisa_last, logit as .f32 files)."""
+    """The reference SHIELD-A engine (engine/audio, compiled by `make -C oracle ref` with
+    oracle/audio_ref_driver.cpp), exact mode: its sequence stages (tokens [125][384] -> logit, optional stage dumps:
+    tokens, gdn_a, gdn_b, sisa_last, logit as .f32 files), its frontend (PCM -> tokens, dumps mel and cnn) and the
+    two together (PCM -> logit)."""
 
     def __init__(self, weights):
         if not AUDIO_SO.exists():
@@ -199,11 +200,35 @@ class AudioReference:
         lib.ora_audio_error.restype = ctypes.c_char_p
         lib.ora_audio_sequence.restype = ctypes.c_int
         lib.ora_audio_sequence.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p]
+        lib.ora_audio_frontend.restype = ctypes.c_int
+        lib.ora_audio_frontend.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p]
+        lib.ora_audio_predict.restype = ctypes.c_int
+        lib.ora_audio_predict.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         lib.ora_audio_free.argtypes = [ctypes.c_void_p]
         self.lib = lib
         self.h = lib.ora_audio_load(str(weights).encode())
         if not self.h:
             raise RuntimeError("reference audio load failed: " + lib.ora_audio_error().decode())
+
+    def frontend(self, pcm: np.ndarray, dump_dir: str | None = None) -> np.ndarray:
+        """160,000 PCM samples -> tokens [125][384] (shield::frontend_cnn); the dump holds mel.f32 [80][997] and
+        cnn.f32"""
+        x = np.ascontiguousarray(pcm, dtype=np.float32).reshape(160000)
+        out = np.zeros((125, 384), np.float32)
+        rc = self.lib.ora_audio_frontend(self.h, x.ctypes.data, out.ctypes.data,
+                                         None if dump_dir is None else str(dump_dir).encode())
+        if rc != 0:
+            raise RuntimeError(self.lib.ora_audio_error().decode())
+        return out
+
+    def predict(self, pcm: np.ndarray) -> np.ndarray:
+        """PCM windows [n][160000] -> logits [n] (frontend, then the sequence stages)"""
+        x = np.ascontiguousarray(pcm, dtype=np.float32).reshape(-1, 160000)
+        out = np.zeros(len(x), np.float32)
+        for i in range(len(x)):
+            if self.lib.ora_audio_predict(self.h, x[i].ctypes.data, out[i:].ctypes.data) != 0:
+                raise RuntimeError(self.lib.ora_audio_error().decode())
+        return out
 
     def sequence(self, tokens: np.ndarray, dump_dir: str | None = None) -> float:
         t = np.ascontiguousarray(tokens, dtype=np.float32).reshape(125 * 384)

@@ -28,9 +28,10 @@ LIB = PKG / "lib"
 INCLUDE = PKG.parent / "include"
 
 NUMERIC_SOURCES = ["dev_common.hpp", "mfma.hpp", "kernels.hpp", "gemm.hip", "cnn.hip", "fused.hip", "strip.hip", "seq.hip",
-                   "engine.hpp", "engine.hip", "stack.hpp", "audio.hpp", "audio.hip",
+                   "engine.hpp", "engine.hip", "stack.hpp", "audio.hpp", "audio.hip", "afront.hip",
                    "host_model.hpp", "host_model.cpp"]
-DEVICE_SOURCES = ["gemm.hip", "cnn.hip", "fused.hip", "strip.hip", "seq.hip", "engine.hip", "audio.hip", "crop.hip"]
+DEVICE_SOURCES = ["gemm.hip", "cnn.hip", "fused.hip", "strip.hip", "seq.hip", "engine.hip", "audio.hip", "afront.hip",
+                  "crop.hip"]
 HOST_SOURCES = ["host_model.cpp", "sched.cpp", "cert.cpp"]
 HIP_HOST_SOURCES = ["lanes.cpp"]          # host code that calls the HIP runtime
 API_SOURCE = "capi.cpp"                   # built twice: certified and experimental

@@ -1,6 +1,8 @@
-// SHIELD-A sequence engine: the audio model's sequence stages (engine/audio/sequence.cpp:319-348: 125 frontend
-// tokens + the readout -> GDN-A -> GDN-B twice -> SISA last row -> head -> one logit per window) on the GPU, batched
-// over windows, on the same kernels as SHIELD-V's sequence.  One thread drives an AudioEngine at a time.
+// SHIELD-A engine: the audio model on the GPU, batched over windows.  The frontend (engine/audio/frontend.cpp:
+// 10 s of PCM -> log-mel -> CNN -> 125 tokens of 384) when the weight file carries its tensors, and the sequence
+// stages (engine/audio/sequence.cpp:319-348: 125 tokens + the readout -> GDN-A -> GDN-B twice -> SISA last row ->
+// head -> one logit per window) on the same kernels as SHIELD-V's sequence.  One thread drives an AudioEngine at a
+// time.
 #pragma once
 #include "engine.hpp"
 
@@ -27,7 +29,17 @@ public:
     // returns when the logits are written
     virtual void run_host(const float* tokens, long long ldw, long long n, float* logits) = 0;
 
+    // The whole model from PCM (only with the frontend's tensors: has_frontend()).  Window w's 160,000 samples at
+    // pcm + w * stride (stride >= 160,000 samples).  Device: d_pcm and d_logits in device memory, n <= max_windows,
+    // issued on s.  Host: returns when the logits are written.
+    bool has_frontend() const { return has_frontend_; }
+    virtual void predict_device(const float* d_pcm, long long stride, int n, float* d_logits, hipStream_t s) = 0;
+    virtual void predict_host(const float* pcm, long long stride, long long n, float* logits) = 0;
+    // the frontend alone: host PCM -> host tokens [n][125][384]
+    virtual void frontend_host(const float* pcm, long long stride, long long n, float* tokens) = 0;
+
 protected:
+    bool has_frontend_ = false;
     Precision prec_ = Precision::FP32;
     int max_windows_ = 0;
     size_t weight_bytes_ = 0, device_bytes_ = 0;

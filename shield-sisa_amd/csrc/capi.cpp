@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <limits>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -409,6 +410,47 @@ int shv_hip_audio_sequence_device(shv_hip_audio* a, const float* d_tokens, int n
         std::lock_guard<std::mutex> lk(a->mu);
         DeviceScope ds(a->device);
         a->eng->run_device(d_tokens, (long long)stride, n, d_logits, static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
+int shv_hip_audio_has_frontend(const shv_hip_audio* a) { return a && a->eng && a->eng->has_frontend() ? 1 : 0; }
+
+int shv_hip_audio_predict(shv_hip_audio* a, const float* pcm, size_t n, size_t stride_samples, float* logits) {
+    if (logits)
+        for (size_t i = 0; i < n; ++i) logits[i] = std::numeric_limits<float>::quiet_NaN();
+    return guarded([&] {
+        if (!a || !pcm || !logits) throw std::runtime_error("null argument");
+        if (n == 0 || n > 1000000) throw std::runtime_error("window count out of range");
+        if (stride_samples < size_t(shv::kAudioWindowSamples)) throw std::runtime_error("window stride below 160000 samples");
+        std::lock_guard<std::mutex> lk(a->mu);
+        DeviceScope ds(a->device);
+        a->eng->predict_host(pcm, (long long)stride_samples, (long long)n, logits);
+        return 0;
+    });
+}
+
+int shv_hip_audio_predict_device(shv_hip_audio* a, const float* d_pcm, int n, size_t stride_samples,
+                                 float* d_logits, void* stream) {
+    return guarded([&] {
+        if (!a || !d_pcm || !d_logits) throw std::runtime_error("null argument");
+        if (n < 1 || n > a->eng->max_windows()) throw std::runtime_error("window count out of range");
+        if (stride_samples < size_t(shv::kAudioWindowSamples)) throw std::runtime_error("window stride below 160000 samples");
+        std::lock_guard<std::mutex> lk(a->mu);
+        DeviceScope ds(a->device);
+        a->eng->predict_device(d_pcm, (long long)stride_samples, n, d_logits, static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
+int shv_hip_audio_frontend(shv_hip_audio* a, const float* pcm, size_t n, size_t stride_samples, float* tokens) {
+    return guarded([&] {
+        if (!a || !pcm || !tokens) throw std::runtime_error("null argument");
+        if (n == 0 || n > 1000000) throw std::runtime_error("window count out of range");
+        if (stride_samples < size_t(shv::kAudioWindowSamples)) throw std::runtime_error("window stride below 160000 samples");
+        std::lock_guard<std::mutex> lk(a->mu);
+        DeviceScope ds(a->device);
+        a->eng->frontend_host(pcm, (long long)stride_samples, (long long)n, tokens);
         return 0;
     });
 }

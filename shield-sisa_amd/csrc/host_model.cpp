@@ -115,6 +115,10 @@ private:
         for (It i = b; i != e; ++i) s += (i == b ? "" : ",") + std::to_string(*i);
         return s + "]";
     }
+public:
+    bool has(const std::string& name) const { return table_.count(name) != 0; }
+
+private:
     Entry& find(const std::string& name) {
         auto it = table_.find(name);
         if (it == table_.end()) throw std::runtime_error("weights: missing tensor " + name);
@@ -505,6 +509,106 @@ HostModel load_host_model(const std::string& path) {
     return hm;
 }
 
+namespace {
+
+// BatchNorm `bn` of c channels as the reference folds it for its frontend, in float (frontend.cpp:136-144)
+void audio_bn(Weights& ts, const std::string& bn, int c, std::vector<float>& scale, std::vector<float>& shift) {
+    const auto& g = ts.take(bn + ".weight", {c});
+    const auto& beta = ts.take(bn + ".bias", {c});
+    const auto& mean = ts.take(bn + ".running_mean", {c});
+    const auto& var = ts.take(bn + ".running_var", {c});
+    scale.assign(size_t(c), 0.0f);
+    shift.assign(size_t(c), 0.0f);
+    for (int j = 0; j < c; ++j) {
+        const float sd = std::sqrt(var[j] + 1e-5f);
+        scale[j] = g[j] / sd;
+        const float ms = mean[j] * scale[j];
+        shift[j] = beta[j] - ms;
+    }
+}
+
+// a 1x1 layer [out][in] followed by BatchNorm, the scale folded into the rows and the shift as the bias
+Linear audio_pointwise(Weights& ts, const std::string& name, int out, int in) {
+    const auto& w = ts.take(name + ".0.weight", {out, in, 1, 1});
+    std::vector<float> scale, shift;
+    audio_bn(ts, name + ".1", out, scale, shift);
+    std::vector<float> wf(w.size());
+    for (int o = 0; o < out; ++o)
+        for (int k = 0; k < in; ++k) wf[size_t(o) * in + k] = w[size_t(o) * in + k] * scale[o];
+    return linear(wf, out, in, &shift);
+}
+
+void load_audio_front(Weights& ts, AudioFrontHost& F) {
+    constexpr int kBins = 257;
+    F.mean = ts.take("frontend.mean", {80});
+    F.stdv = ts.take("frontend.std", {80});
+    // the export writes the window and the filterbank (engine/audio/export.py:35); without them the reference's
+    // own definitions apply (frontend.cpp:127-135): periodic Hann, HTK mel triangles from 20 to 7600 Hz
+    if (ts.has("frontend.window")) {
+        F.window = ts.take("frontend.window", {400});
+    } else {
+        F.window.assign(400, 0.0f);
+        for (int j = 0; j < 400; ++j) F.window[j] = 0.5f * (1.f - std::cos(float(2. * M_PI * j / 400.)));
+    }
+    std::vector<float> fb;
+    if (ts.has("frontend.fb")) {
+        fb = ts.take("frontend.fb", {80, kBins});
+    } else {
+        fb.assign(size_t(80) * kBins, 0.0f);
+        double hz[82];
+        const double m0 = 2595. * std::log10(1. + 20. / 700.), m1 = 2595. * std::log10(1. + 7600. / 700.);
+        for (int j = 0; j < 82; ++j) hz[j] = 700. * (std::pow(10., (m0 + (m1 - m0) * j / 81.) / 2595.) - 1.);
+        for (int m = 0; m < 80; ++m)
+            for (int k = 0; k < kBins; ++k)
+                fb[size_t(m) * kBins + k] = float(std::max(0., std::min((k * 31.25 - hz[m]) / (hz[m + 1] - hz[m]),
+                                                                       (hz[m + 2] - k * 31.25) / (hz[m + 2] - hz[m + 1]))));
+    }
+    F.fb_off.assign(1, 0);
+    for (int m = 0; m < 80; ++m) {
+        for (int k = 0; k < kBins; ++k)
+            if (fb[size_t(m) * kBins + k] != 0.0f) {
+                F.fb_k.push_back(k);
+                F.fb_w.push_back(fb[size_t(m) * kBins + k]);
+            }
+        F.fb_off.push_back(int(F.fb_k.size()));
+    }
+    F.wr.assign(256, 0.0f);
+    F.wi.assign(256, 0.0f);
+    for (int j = 0; j < 256; ++j) {
+        F.wr[j] = float(std::cos(-2. * M_PI * j / 512.));
+        F.wi[j] = float(std::sin(-2. * M_PI * j / 512.));
+    }
+    F.stem_w = ts.take("cnn.stem.0.weight", {32, 1, 3, 3});
+    audio_bn(ts, "cnn.stem.1", 32, F.stem_scale, F.stem_shift);
+    static const int kChannels[4] = {48, 96, 160, 192};
+    int ci = 32;
+    for (int st = 0; st < 4; ++st)
+        for (int b = 0; b < 2; ++b) {
+            AudioBlockHost& B = F.blocks[st * 2 + b];
+            const std::string base = "cnn.stages." + std::to_string(st) + "." + std::to_string(b);
+            B.ci = ci;
+            B.hid = 2 * ci;
+            B.co = kChannels[st];
+            B.sf = b == 0 && st < 2 ? 2 : 1;   // frontend.cpp:216-218: stage 0 / 1 first blocks stride 2 in
+            B.st = b == 0 && st < 3 ? 2 : 1;   // frequency, stages 0-2 first blocks stride 2 in time
+            B.residual = B.ci == B.co && B.sf == 1 && B.st == 1;
+            B.pw1 = audio_pointwise(ts, base + ".pw1", B.hid, B.ci);
+            const auto& dw = ts.take(base + ".dw.0.weight", {B.hid, 1, 3, 3});
+            B.dw_w.assign(size_t(9) * B.hid, 0.0f);
+            for (int c = 0; c < B.hid; ++c)
+                for (int k = 0; k < 9; ++k) B.dw_w[size_t(k) * B.hid + c] = dw[size_t(c) * 9 + k];
+            audio_bn(ts, base + ".dw.1", B.hid, B.dw_scale, B.dw_shift);
+            B.pw2 = audio_pointwise(ts, base + ".pw2", B.co, B.hid);
+            ci = B.co;
+        }
+    F.fa_w = ts.take("cnn.freq_attn.weight", {1, 192, 1, 1});
+    F.fa_b = ts.take("cnn.freq_attn.bias", {1})[0];
+    F.proj = linear(ts.take("cnn.proj.weight", {kD, 192}), kD, 192);
+    F.present = true;
+}
+
+}  // namespace
+
 AudioHost load_audio_host(const std::string& path) {
     AudioHost ah;
     ah.path = path;
@@ -515,6 +619,7 @@ AudioHost load_audio_host(const std::string& path) {
     for (int g = 0; g < 2; ++g) load_gdn(ts, g == 0 ? "gdn_a." : "gdn_b.", kAudioGdn, ah.gdn[g]);
     load_sisa(ts, ah.sisa);
     load_head(ts, "head_norm.weight", "head.3", ah.final_norm_w, ah.head0, ah.head2_w, ah.head2_b);
+    if (ts.has("frontend.mean")) load_audio_front(ts, ah.front);
     return ah;
 }
 

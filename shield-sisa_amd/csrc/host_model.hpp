@@ -80,9 +80,32 @@ HostModel load_host_model(const std::string& path);
 // SHIELD-A's sequence stages (engine/audio/sequence.cpp:290-317): the tensors of a SHLDA001 file that the stages
 // read, in the same host layouts as SHIELD-V's (final norm = head_norm, head2 = head.3).  The file's frontend
 // tensors are indexed and left alone.  Throws std::runtime_error.
+// SHIELD-A frontend (engine/audio/frontend.cpp): log-mel tables, the stem, eight inverted blocks (4 stages x 2),
+// frequency attention and the token projection.  BatchNorm is kept as the reference computes it (float scale =
+// gamma / sqrt(var + 1e-5f), shift = beta - mean * scale, frontend.cpp:136-144); the 1x1 layers carry it folded into
+// their weights (w * scale per output row, bias = shift).
+struct AudioBlockHost {
+    int ci = 0, hid = 0, co = 0, sf = 1, st = 1;
+    bool residual = false;
+    Linear pw1, pw2;                                  // [hid][ci], [co][hid], BatchNorm folded
+    std::vector<float> dw_w, dw_scale, dw_shift;      // [9][hid] (tap 3 kf + kt), [hid], [hid]
+};
+struct AudioFrontHost {
+    bool present = false;
+    std::vector<float> mean, stdv, window, wr, wi;    // [80], [80], [400], [256], [256]
+    std::vector<int> fb_off, fb_k;                    // [81], nonzero taps of each filter in increasing k
+    std::vector<float> fb_w;
+    std::vector<float> stem_w, stem_scale, stem_shift;   // [32][9] (tap 3 kf + kt), [32], [32]
+    AudioBlockHost blocks[8];
+    std::vector<float> fa_w;                          // [192]
+    float fa_b = 0.0f;
+    Linear proj;                                      // [384][192]
+};
+
 struct AudioHost {
     std::string path, sha256;
     size_t file_bytes = 0;
+    AudioFrontHost front;                // present when the file carries the frontend's tensors
     std::vector<float> readout;          // [384]
     GdnHost gdn[2];
     SisaHost sisa;

@@ -146,6 +146,32 @@ template <typename T> bool launch_ir_strip(int block, const IrArgs& a, int F, hi
 void launch_se_reduce(const float* part, int ntiles, int cexpp, int cexp, int hw, float* pooled, int F,
                       hipStream_t s);
 
+// ---------------------------------------------------------------- SHIELD-A frontend (engine/audio/frontend.cpp)
+constexpr int kAudioWindowSamples = 160000;              // 10 s of 16 kHz PCM
+constexpr int kAudioMelFrames = 997, kAudioMelBins = 80;  // log-mel image [time][freq]
+constexpr int kAudioTokensPerWindow = 125;               // CNN time steps = frontend tokens
+constexpr int kAudioCnnFreq = 20, kAudioCnnCh = 192;     // CNN output image [125][20][192]
+// Device tables of the log-mel step: analysis window [400], FFT twiddles wr, wi [256] (cos, sin of -2 pi k / 512),
+// the filterbank's nonzero taps as rows m: entries fb_off[m] .. fb_off[m + 1] of (fb_k, fb_w) in increasing k, and
+// the normalisation mean, stdv [80]
+struct AudioMelTables {
+    const float *window = nullptr, *wr = nullptr, *wi = nullptr;
+    const int *fb_off = nullptr, *fb_k = nullptr;
+    const float *fb_w = nullptr, *mean = nullptr, *stdv = nullptr;
+};
+// PCM windows (window w at pcm + w * stride, stride >= 160,000 samples) -> normalised log-mel [n][997][80]
+void launch_audio_mel(const float* pcm, long long stride, int n, const AudioMelTables& tb, float* mel, hipStream_t s);
+// log-mel [n][997][80] -> stem image [n][997][80][32]: 3x3 conv (w [32][9], tap 3 kf + kt), BatchNorm scale/shift,
+// SiLU
+void launch_audio_stem(const float* mel, const float* w, const float* scale, const float* shift, float* out, int n,
+                       hipStream_t s);
+// depthwise 3x3, strides (time st, freq sf) in {1, 2}, padding 1, BatchNorm, SiLU: in [n][T][F][C] ->
+// out [n][(T + st - 1) / st][(F + sf - 1) / sf][C]; w [9][C] (tap 3 kf + kt), C % 4 == 0
+void launch_audio_dw(const float* in, float* out, const float* w, const float* scale, const float* shift, int n,
+                     int T, int F, int C, int st, int sf, hipStream_t s);
+// frequency attention: image [n][125][20][192], attention weights w [192] and bias -> pooled [n][125][192]
+void launch_audio_freq_pool(const float* h, const float* w, float bias, float* pooled, int n, hipStream_t s);
+
 // ---------------------------------------------------------------- face crops (uint8 RGB, device memory)
 struct CropJob {
     const uint8_t* frame;   // native RGB frame (or the I420 Y plane), rows `stride` bytes apart

@@ -15,7 +15,8 @@
  *   GDN: A_log = ln U[1,16], dt_bias 0, short convs He-normal (fan_in 4), conv biases 0; SISA lambda_raw 0
  * Normal deviates are Irwin-Hall sums of 12 uniforms minus 6.
  * SHIELD-A: the tensors its sequence stages read, names and shapes as engine/audio/sequence.cpp:304-331 validates
- * them (the frontend's are not written); the same distributions, head biases 0. */
+ * them; the same distributions, head biases 0.  The whole-model file adds the frontend's tensors (BatchNorm
+ * statistics drawn away from the identity, a polynomial analysis window and a triangular filterbank). */
 #include "sha256.h"
 
 #include <stdint.h>
@@ -68,7 +69,10 @@ static double ln_series(double x) {
 }
 
 /* ---------------------------------------------------------------------------------------------- tensor table */
-enum { D_HE = 0, D_XAVIER, D_ONE, D_ZERO, D_EMB, D_ALOG };
+enum { D_HE = 0, D_XAVIER, D_ONE, D_ZERO, D_EMB, D_ALOG,
+       /* SHIELD-A frontend: BatchNorm statistics drawn away from the identity, log-mel normalisation, a smooth
+        * analysis window and a triangular filterbank (position-dependent, no random draws) */
+       D_BN_W, D_BN_B, D_BN_VAR, D_MEL_MEAN, D_MEL_STD, D_WINDOW, D_MELFB };
 
 typedef struct {
     char name[96];
@@ -228,6 +232,28 @@ static void fill(const Spec* s, float* out, Rng* r) {
         case D_ZERO: v = 0.0; break;
         case D_EMB: v = rng_normal(r) * 0.02; break;
         case D_ALOG: v = ln_series(1.0 + 15.0 * rng_unit(r)); break;
+        case D_BN_W: v = 1.0 + 0.1 * rng_normal(r); break;
+        case D_BN_B: v = 0.1 * rng_normal(r); break;
+        case D_BN_VAR: { const double g = rng_normal(r); v = 1.0 + 0.2 * (g < 0.0 ? -g : g); break; }
+        case D_MEL_MEAN: v = 1.0 + 0.5 * rng_normal(r); break;
+        case D_MEL_STD: { const double g = rng_normal(r); v = 1.0 + 0.25 * (g < 0.0 ? -g : g); break; }
+        case D_WINDOW: {   /* 16 x^2 (1 - x)^2, x = i / 400: zero at the ends, 1 in the middle */
+            const double x = (double)i / 400.0;
+            v = 16.0 * x * x * (1.0 - x) * (1.0 - x);
+            break;
+        }
+        case D_MELFB: {    /* filter m over FFT bin k: a triangle on the points 1 + 254 (0.3 u + 0.7 u^2), u = j / 81 */
+            const int m = (int)(i / 257), k = (int)(i % 257);
+            double pt[3];
+            for (int q = 0; q < 3; ++q) {
+                const double u = (double)(m + q) / 81.0;
+                pt[q] = 1.0 + 254.0 * (0.3 * u + 0.7 * u * u);
+            }
+            const double up = ((double)k - pt[0]) / (pt[1] - pt[0]), down = (pt[2] - (double)k) / (pt[2] - pt[1]);
+            v = up < down ? up : down;
+            if (v < 0.0) v = 0.0;
+            break;
+        }
         default: break;
         }
         out[i] = (float)v;
@@ -365,6 +391,56 @@ SHV_SYNTH_API int shv_synth_weights(const char* path, uint64_t seed, double thre
     if (tensors) *tensors = t.n;
     free(t.v);
     return ok ? 0 : -1;
+}
+
+/* The SHIELD-A frontend's tensors, names and shapes as engine/audio/frontend.cpp:148-160 validates them (the
+ * export's frontend.window and frontend.fb included, engine/audio/export.py:35) */
+static void bn_drawn(Table* t, const char* prefix, int c) {
+    char n[96];
+    int d[1] = {c};
+    snprintf(n, sizeof n, "%s.weight", prefix); add(t, n, 1, d, D_BN_W, 0, 0, 1);
+    snprintf(n, sizeof n, "%s.bias", prefix); add(t, n, 1, d, D_BN_B, 0, 0, 1);
+    snprintf(n, sizeof n, "%s.running_mean", prefix); add(t, n, 1, d, D_BN_B, 0, 0, 0);
+    snprintf(n, sizeof n, "%s.running_var", prefix); add(t, n, 1, d, D_BN_VAR, 0, 0, 0);
+}
+static void build_audio_frontend_table(Table* t) {
+    char n[96];
+    t1(t, "frontend.mean", 80, D_MEL_MEAN);
+    t1(t, "frontend.std", 80, D_MEL_STD);
+    { int d[1] = {400}; add(t, "frontend.window", 1, d, D_WINDOW, 0, 0, 0); }
+    { int d[2] = {80, 257}; add(t, "frontend.fb", 2, d, D_MELFB, 0, 0, 0); }
+    conv(t, "cnn.stem.0.weight", 32, 1, 3);
+    bn_drawn(t, "cnn.stem.1", 32);
+    static const int channels[4] = {48, 96, 160, 192};
+    int ci = 32;
+    for (int s = 0; s < 4; ++s)
+        for (int b = 0; b < 2; ++b) {
+            const int co = channels[s], hid = 2 * ci;
+            snprintf(n, sizeof n, "cnn.stages.%d.%d.pw1.0.weight", s, b); conv(t, n, hid, ci, 1);
+            snprintf(n, sizeof n, "cnn.stages.%d.%d.pw1.1", s, b); bn_drawn(t, n, hid);
+            snprintf(n, sizeof n, "cnn.stages.%d.%d.dw.0.weight", s, b); conv(t, n, hid, 1, 3);
+            snprintf(n, sizeof n, "cnn.stages.%d.%d.dw.1", s, b); bn_drawn(t, n, hid);
+            snprintf(n, sizeof n, "cnn.stages.%d.%d.pw2.0.weight", s, b); conv(t, n, co, hid, 1);
+            snprintf(n, sizeof n, "cnn.stages.%d.%d.pw2.1", s, b); bn_drawn(t, n, co);
+            ci = co;
+        }
+    conv(t, "cnn.freq_attn.weight", 1, 192, 1);
+    t1(t, "cnn.freq_attn.bias", 1, D_ZERO);
+    lin(t, "cnn.proj.weight", 384, 192);
+}
+
+/* The whole SHIELD-A model (SHLDA001): the sequence-stage tensors drawn exactly as shv_synth_audio_weights draws
+ * them from the same seed, then the frontend's.  0 on success, -1 on I/O failure; sha_hex may be NULL. */
+SHV_SYNTH_API int shv_synth_audio_model_weights(const char* path, uint64_t seed, char* sha_hex, int* tensors) {
+    Table t = {0};
+    build_audio_table(&t);
+    build_audio_frontend_table(&t);
+    char hex[65];
+    const int rc = write_table(path, "SHLDA001", &t, seed, hex, NULL, NULL);
+    if (sha_hex) memcpy(sha_hex, hex, 65);
+    if (tensors) *tensors = t.n;
+    free(t.v);
+    return rc;
 }
 
 /* SHIELD-A sequence-stage weights (SHLDA001) at `path`.  0 on success, -1 on I/O failure; sha_hex may be NULL. */

@@ -18,6 +18,7 @@ LIB_DIR = PKG / "lib"
 FRAME_BYTES = 172800
 TOKEN_FLOATS = 6144
 WINDOW_FRAMES = 20
+AUDIO_WINDOW_SAMPLES = 160000   # one SHIELD-A window: 10 s of 16 kHz PCM (engine/audio/include/shield.h:8)
 
 
 class ShvError(RuntimeError):
@@ -87,6 +88,10 @@ _SIGS = {
     "shv_hip_audio_device_bytes": (ctypes.c_size_t, [_P]),
     "shv_hip_audio_sequence": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, _P]),
     "shv_hip_audio_sequence_device": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_size_t, _P, _P]),
+    "shv_hip_audio_has_frontend": (ctypes.c_int, [_P]),
+    "shv_hip_audio_predict": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, _P]),
+    "shv_hip_audio_predict_device": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_size_t, _P, _P]),
+    "shv_hip_audio_frontend": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_size_t, _P]),
     "shv_hip_audio_profile_enable": (ctypes.c_int, [_P, ctypes.c_int]),
     "shv_hip_audio_profile_read": (ctypes.c_int, [_P, ctypes.c_char_p, _P, _P, _P, _P]),
     "shv_hip_audio_set_dump_dir": (ctypes.c_int, [_P, ctypes.c_char_p]),
@@ -123,6 +128,9 @@ def synth_library() -> ctypes.CDLL:
         lib.shv_synth_audio_weights.restype = ctypes.c_int
         lib.shv_synth_audio_weights.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_char_p,
                                                 ctypes.POINTER(ctypes.c_int)]
+        lib.shv_synth_audio_model_weights.restype = ctypes.c_int
+        lib.shv_synth_audio_model_weights.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_char_p,
+                                                      ctypes.POINTER(ctypes.c_int)]
         lib.shv_synth_bytes.restype = None
         lib.shv_synth_bytes.argtypes = [_P, ctypes.c_size_t, ctypes.c_uint64]
         lib.shv_synth_sha256.restype = None
@@ -137,6 +145,21 @@ def write_audio_weights(path, seed: int = 5) -> str:
     if synth_library().shv_synth_audio_weights(str(path).encode(), seed, sha, None) != 0:
         raise ShvError(f"cannot write {path}")
     return sha.value.decode()
+
+
+def write_audio_model_weights(path, seed: int = 5) -> str:
+    """Seeded synthetic SHLDA001 weights of the whole SHIELD-A model (the sequence stages drawn as
+    write_audio_weights draws them, then the frontend's tensors); returns the SHA-256 hex."""
+    sha = ctypes.create_string_buffer(65)
+    if synth_library().shv_synth_audio_model_weights(str(path).encode(), seed, sha, None) != 0:
+        raise ShvError(f"cannot write {path}")
+    return sha.value.decode()
+
+
+def audio_pcm(n: int, seed: int = 23) -> np.ndarray:
+    """n SHIELD-A windows of 16 kHz PCM (160,000 samples), float32 N(0, 0.1^2) clipped to [-1, 1], seeded."""
+    x = np.random.default_rng(seed).normal(0.0, 0.1, (n, AUDIO_WINDOW_SAMPLES))
+    return np.clip(x, -1.0, 1.0).astype(np.float32)
 
 
 def audio_tokens(n: int, seed: int = 17) -> np.ndarray:
@@ -364,7 +387,8 @@ AUDIO_WINDOW_FLOATS = 125 * 384
 
 
 class AudioModel:
-    """SHIELD-A sequence stages on the GPU (shv_hip_audio_load): windows of 125 x 384 frontend tokens -> logits."""
+    """SHIELD-A on the GPU (shv_hip_audio_load): PCM windows -> logits through the whole model (weights with the
+    frontend's tensors), or windows of 125 x 384 frontend tokens -> logits through the sequence stages."""
 
     def __init__(self, weights, mode: str = "fp32", device: int = 0, max_windows: int = 256,
                  experimental: bool = False):
@@ -418,6 +442,35 @@ class AudioModel:
                         stream: int | None = None) -> None:
         if self.lib.shv_hip_audio_sequence_device(self.h, d_tokens, n, stride, d_logits, stream) != 0:
             raise ShvError(self._err())
+
+    @property
+    def has_frontend(self) -> bool:
+        return self.lib.shv_hip_audio_has_frontend(self.h) == 1
+
+    def predict(self, pcm: np.ndarray, stride: int | None = None) -> np.ndarray:
+        """PCM windows [n][160000] (or rows `stride` samples apart) -> logits [n] through the whole model"""
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        stride = AUDIO_WINDOW_SAMPLES if stride is None else stride
+        n = pcm.size // stride
+        out = np.empty(n, np.float32)
+        if self.lib.shv_hip_audio_predict(self.h, _ptr(pcm), n, stride, _ptr(out)) != 0:
+            raise ShvError(self._err())
+        return out
+
+    def predict_device(self, d_pcm: int, n: int, d_logits: int, stride: int = AUDIO_WINDOW_SAMPLES,
+                       stream: int | None = None) -> None:
+        if self.lib.shv_hip_audio_predict_device(self.h, d_pcm, n, stride, d_logits, stream) != 0:
+            raise ShvError(self._err())
+
+    def frontend(self, pcm: np.ndarray, stride: int | None = None) -> np.ndarray:
+        """PCM windows -> frontend tokens [n][125][384]"""
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        stride = AUDIO_WINDOW_SAMPLES if stride is None else stride
+        n = pcm.size // stride
+        out = np.empty((n, 125, 384), np.float32)
+        if self.lib.shv_hip_audio_frontend(self.h, _ptr(pcm), n, stride, _ptr(out)) != 0:
+            raise ShvError(self._err())
+        return out
 
     def profile_enable(self, on: bool) -> None:
         if self.lib.shv_hip_audio_profile_enable(self.h, 1 if on else 0) != 0:

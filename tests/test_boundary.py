@@ -21,7 +21,7 @@ def declared_functions():
 def test_every_declared_symbol_is_exported(shv):
     lib = shv.library()
     names = declared_functions()
-    assert len(names) == 48
+    assert len(names) == 52
     for n in names:
         assert hasattr(lib, n), n
     exp = shv.library(experimental=True)
