@@ -6,6 +6,8 @@
 // in the engine's default exact mode.  With a dump directory, the engine writes its stage tensors there
 // (SHIELD_DUMP_DIR, sequence.cpp:36-41).
 #include "core.hpp"
+#include "frontend.hpp"
+#include "sequence_cache.hpp"
 
 #include <cstdlib>
 #include <cstring>
@@ -86,5 +88,15 @@ __attribute__((visibility("default"))) int ora_audio_predict(void* h, const floa
     }
 }
 
-__attribute__((visibility("default"))) void ora_audio_free(void* h) { delete static_cast<shield::Weights*>(h); }
+// Frees the weights after dropping the engine's caches keyed by their addresses (packed GEMM weights, prepared
+// frontend tables, projected readouts), as the engine's own model free does (engine/audio/api.cpp:56-57): a later
+// load may reuse the addresses.
+__attribute__((visibility("default"))) void ora_audio_free(void* h) {
+    auto* w = static_cast<shield::Weights*>(h);
+    if (!w) return;
+    shield::release_sequence_weights(*w);
+    shield::release_frontend_weights(*w);
+    shield::release_kernel_weights(*w);
+    delete w;
+}
 }
