@@ -18,6 +18,7 @@
 #include "mfma.hpp"
 
 #include <cmath>
+#include <cstdlib>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -858,6 +859,8 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES) gemm_direct_kernel(GemmArgs p
 
 // Workgroup barrier that waits for LDS traffic only (the next K step's global loads stay in flight across it).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// waits for the wave's own LDS accesses (one wave's LDS instructions execute in order)
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // LDS-staged split-operand GEMM.  A workgroup (4 waves, WGM x WGN) owns a BM x BN tile of C; per K step of 32 it
 // stages A[BM][32] (fp32 from HBM, SE-scaled, split into the T parts once per workgroup) and the pre-split W parts
@@ -1503,6 +1506,195 @@ __global__ void __launch_bounds__(64 * MFMA_WAVES, 2) gemm_stream_kernel(GemmArg
                       [&](int i, int j) { return acc[mt][j][i]; });
 }
 
+// Wide GEMM: large M, short K (<= 256), many columns (the config-2 expand M x 160 -> 960, the audio frontend's
+// 1x1 layers).  A workgroup (4 waves) takes 64 rows: their K values are loaded once (16-byte loads), split into the
+// operand parts and staged in LDS, where every wave reads them; wave w then walks the 16-column tiles w, w + 4, ...
+// of N, each a 64 x 16 output block of 4 accumulators.  A tile's weight fragments for all KS K steps are loaded in
+// one go one tile ahead (two register sets alternating with the tile parity), so a wave waits on L2 once per tile,
+// not once per K step.  Results go through the wave's LDS region and leave as whole 64-byte row pieces,
+// non-temporal.  A is read from HBM exactly once (the direct and LDS-tiled kernels re-read it once per column block:
+// 7-12 times at N = 960).  Per output: K steps of 32 in increasing order, the split products in mfma_split's order,
+// the accumulator from +0, epi_value's epilogue -- bitwise the other MFMA kernels' results.
+constexpr int WD_ROWS = 64, WD_KMAX = 256, WD_PAD = 8, WD_SLD = 64 + 4;
+template <typename T, int KS, int GR>
+__global__ void __launch_bounds__(256, 2) gemm_wide_kernel(GemmArgs p) {
+    typedef Split<T> S;
+    typedef typename S::V8 V8;
+    constexpr int P = S::P;
+    extern __shared__ __attribute__((aligned(16))) unsigned char wd_lds[];
+    constexpr int kp = KS * 32, ld = kp + WD_PAD;
+    T* As = reinterpret_cast<T*>(wd_lds);   // [P][64][ld], then the waves' C staging regions [4][16][WD_SLD]
+    float* Cs = reinterpret_cast<float*>(wd_lds + (size_t)P * WD_ROWS * ld * sizeof(T));
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, r = lane & 15;
+    const long long m0 = (long long)blockIdx.x * WD_ROWS;
+    // stage: row i / (kp / 4), k quad i % (kp / 4); zero outside [M) x [K)
+    constexpr int q4 = kp / 4;
+#pragma unroll 2
+    for (int i = tid; i < WD_ROWS * q4; i += 256) {
+        const int row = i / q4, kq = i - row * q4, k = kq * 4;
+        const long long m = m0 + row;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (m < p.M && k < p.K) v = *reinterpret_cast<const float4*>(p.A + m * p.lda + k);
+        const float x[4] = {v.x, v.y, v.z, v.w};
+        T part[4][P];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+            T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
+            *reinterpret_cast<uint2*>(As + (q * WD_ROWS + row) * ld + k) = *reinterpret_cast<const uint2*>(four);
+        }
+    }
+    lds_barrier();
+    const T* W = static_cast<const T*>(p.W);
+    const int tiles = (p.N + 15) / 16;
+    // tile t's fragments for every K step: lane chunk k = 32 ks + 8 g (zero past K, read at a valid address)
+    const auto load_tile = [&](V8 (&dst)[KS][P], int t) {
+        const T* wrow = W + (long long)min(t * 16 + r, p.N - 1) * p.ldw + g * 8;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const bool kin = ks * 32 + g * 8 < p.K;
+#pragma unroll
+            for (int q = 0; q < P; ++q) {
+                const V8 v = load_part8<T>(wrow + q * p.wstride + (kin ? ks * 32 : 0));
+                dst[ks][q] = kin ? v : V8{};
+            }
+        }
+    };
+    float* wt = Cs + wave * 16 * WD_SLD;
+    // one 16-column tile's 64 x 16 outputs into acc (4 row tiles), from its prefetched weight fragments
+    const auto tile = [&](f32x4 (&acc)[4], const V8 (&wf)[KS][P]) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                V8 a[P];
+#pragma unroll
+                for (int q = 0; q < P; ++q)
+                    a[q] = *reinterpret_cast<const V8*>(As + (q * WD_ROWS + mt * 16 + r) * ld + ks * 32 + g * 8);
+                acc[mt] = mfma_split<T>(a, wf[ks], acc[mt]);
+            }
+            // keeps the compiler from hoisting every K step's A fragment reads ahead of the products
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])::"memory");
+        }
+    };
+    // a group's 64 x 16 GR outputs (tiles j < GR of columns nbase + 16 j ..): per 16-row block through the wave's
+    // LDS region [16][WD_SLD] (a lane group's fragment writes land 16 banks apart), then lane l stores row
+    // l / (4 GR) + (16 / GR) k, columns 4 (l % 4 GR) .. + 3: each store instruction writes whole 64 GR-byte row
+    // pieces, non-temporal
+    constexpr int C4 = 4 * GR, RPS = 64 / C4;   // float4 groups per row, rows per store instruction
+    const auto store_group = [&](const f32x4 (&acc)[GR][4], int nbase) {
+        const int c4 = lane % C4, rsub = lane / C4;
+        const int n = min(nbase + c4 * 4, p.N - 4);
+        const float4 bv = p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const auto go = [&](auto act) {
+            constexpr int ACT = decltype(act)::value;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+                for (int j = 0; j < GR; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) wt[(4 * g + i) * WD_SLD + j * 16 + r] = acc[j][mt][i];
+                wave_lds_sync();
+                float4 v[16 / RPS], rv[16 / RPS];
+#pragma unroll
+                for (int k = 0; k < 16 / RPS; ++k) {
+                    const int row = RPS * k + rsub;
+                    const long long m = min(m0 + mt * 16 + row, (long long)p.M - 1);
+                    v[k] = *reinterpret_cast<const float4*>(wt + row * WD_SLD + c4 * 4);
+                    rv[k] = p.res ? *reinterpret_cast<const float4*>(p.R + m * p.ldr + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+                wave_lds_sync();   // the region is rewritten by the next block
+#pragma unroll
+                for (int k = 0; k < 16 / RPS; ++k) {
+                    const long long m = m0 + mt * 16 + RPS * k + rsub;
+                    if (m >= p.M || nbase + c4 * 4 >= p.N) continue;
+                    const float in[4] = {v[k].x, v[k].y, v[k].z, v[k].w}, bb[4] = {bv.x, bv.y, bv.z, bv.w},
+                                rr[4] = {rv[k].x, rv[k].y, rv[k].z, rv[k].w};
+                    f32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {   // epi_value's operations with the activation fixed
+                        float x = in[e] * p.wscale;
+                        if (p.bias) x = x + bb[e];
+                        x = apply_act(x, ACT);
+                        if (p.res == 3) x = rr[e] + 0.7071067811865475244f * x;
+                        else if (p.res) x = p.res == 2 ? rr[e] + x / 1.41421356237309515f : rr[e] + x;
+                        o[e] = x;
+                    }
+                    __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(p.C + m * p.ldc + nbase + c4 * 4));
+                }
+            }
+        };
+        // the activation is uniform: one branch per group, straight-line code per element
+        switch (p.act) {
+        case ACT_RELU: go(std::integral_constant<int, ACT_RELU>{}); break;
+        case ACT_HS: go(std::integral_constant<int, ACT_HS>{}); break;
+        case ACT_HSIG: go(std::integral_constant<int, ACT_HSIG>{}); break;
+        case ACT_SILU: go(std::integral_constant<int, ACT_SILU>{}); break;
+        default: go(std::integral_constant<int, ACT_NONE>{}); break;
+        }
+    };
+    // wave w takes the GR-tile groups w, w + 4, ...; its tiles' weights alternate between two register sets, the
+    // next tile's loads in flight while one computes
+    static_assert(GR == 2 || GR == 4, "groups of 2 or 4 tiles");
+    const int groups = (tiles + GR - 1) / GR;
+    V8 w0[KS][P], w1[KS][P];
+    const auto tile_of = [&](int gi, int j) { return min(gi * GR + j, tiles - 1); };   // past N: recomputes the last
+    if (wave < groups) load_tile(w0, tile_of(wave, 0));
+    for (int gi = wave; gi < groups; gi += 4) {
+        f32x4 acc[GR][4];
+        load_tile(w1, tile_of(gi, 1));
+        tile(acc[0], w0);
+        if constexpr (GR == 4) {
+            load_tile(w0, tile_of(gi, 2));
+            tile(acc[1], w1);
+            load_tile(w1, tile_of(gi, 3));
+            tile(acc[2], w0);
+            if (gi + 4 < groups) load_tile(w0, tile_of(gi + 4, 0));
+            tile(acc[3], w1);
+        } else {
+            if (gi + 4 < groups) load_tile(w0, tile_of(gi + 4, 0));
+            tile(acc[1], w1);
+        }
+        store_group(acc, gi * GR * 16);
+    }
+}
+// groups of four tiles (256-byte row pieces) where the registers allow, else two (fp16 K <= 192, bf16 K <= 128)
+template <typename T, int KS> void launch_wide_ks(const GemmArgs& p, hipStream_t s) {
+    constexpr int GR = (Split<T>::P == 2 ? KS <= 6 : KS <= 4) ? 4 : 2;
+    const size_t lds = size_t(Split<T>::P) * WD_ROWS * (KS * 32 + WD_PAD) * sizeof(T) +
+                       size_t(4) * 16 * WD_SLD * sizeof(float);
+    hipLaunchKernelGGL((gemm_wide_kernel<T, KS, GR>), dim3(cdiv(p.M, WD_ROWS)), dim3(256), lds, s, p);
+}
+bool wide_ok(const GemmArgs& p) {
+    const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    return !p.Ah && !p.Ch && !p.swiglu && !p.scale && p.wkstride == 32 && p.K <= WD_KMAX && p.K % 8 == 0 &&
+           p.lda % 4 == 0 && al16(p.A) && p.ldc % 4 == 0 && p.N % 4 == 0 && al16(p.C) && (!p.bias || al16(p.bias)) &&
+           (!p.res || (p.ldr % 4 == 0 && al16(p.R)));
+}
+template <typename T> void launch_wide(const GemmArgs& p, hipStream_t s) {
+    if (!wide_ok(p))
+        throw std::runtime_error("gemm_wide: fp32 A and C (16-byte rows), N % 4 == 0, K <= 256 (multiple of 8), "
+                                 "row-major W, no SE scale or SwiGLU");
+    if (Split<T>::P == 3 && p.K > 192) throw std::runtime_error("gemm_wide: bf16 takes K <= 192");   // registers
+    switch ((p.K + 31) / 32) {
+    case 1: launch_wide_ks<T, 1>(p, s); return;
+    case 2: launch_wide_ks<T, 2>(p, s); return;
+    case 3: launch_wide_ks<T, 3>(p, s); return;
+    case 4: launch_wide_ks<T, 4>(p, s); return;
+    case 5: launch_wide_ks<T, 5>(p, s); return;
+    case 6: launch_wide_ks<T, 6>(p, s); return;
+    default:
+        if constexpr (Split<T>::P == 2) {
+            if (p.K <= 224) launch_wide_ks<T, 7>(p, s);
+            else launch_wide_ks<T, 8>(p, s);
+        }
+        return;
+    }
+}
+
 template <typename T, int NT, int ST_MT>
 void launch_stream_mt(const GemmArgs& p, hipStream_t s) {
     constexpr int ST_ROWS = MFMA_WAVES * ST_MT * 16;
@@ -1620,7 +1812,7 @@ void launch_lds(const GemmArgs& p, hipStream_t s) {
 // N up to 160 (CNN projects and 1x1 layers): direct fragments, 16-column tiles per wave chosen to minimise
 // padded columns (at most 5 per wave); wider N (last 1x1, sequence): LDS-staged 128 x 128 workgroup tiles.
 struct GemmPlan {
-    enum Kind { Small, Dma, Lds, Stream, Direct } kind;
+    enum Kind { Small, Dma, Lds, Stream, Direct, Wide } kind;
     int nt;   // column tiles (Stream, Direct)
 };
 template <typename T> GemmPlan plan_gemm(const GemmArgs& p) {
@@ -1630,6 +1822,15 @@ template <typename T> GemmPlan plan_gemm(const GemmArgs& p) {
     if (!p.Ah && !p.scale && !p.swiglu && p.M <= 8192) return {GemmPlan::Small, 0};
     const int tiles = (p.N + 15) / 16;
     if (p.Ah && p.K % 32 == 0 && gemm_dma_enabled()) return {GemmPlan::Dma, 0};
+    // fp32 A, no SE scale, K >= 64, large M (the GEMM tool's shapes, the layer path, the audio frontend), measured
+    // per shape: N > 160 on the wide kernel (M x 160 -> 960: fp16 268 vs 459 us, bf16 364 vs 906; 614,400 x 112 ->
+    // 672: 906 vs 1,400, bf16 1,112 vs 2,817), N <= 160 on the streaming kernel (153,600 x 960 -> 160: 298 vs 409;
+    // 614,400 x 672 -> 112: 605 vs 795; 2,355,200 x 120 -> 40: 378 vs 465); K 40 stays on the direct kernel
+    // (2,007,040 x 40 -> 120: stream 702 vs 534, wide 860)
+    if (!p.Ah && !p.scale && !p.swiglu && p.K >= 64) {
+        if (tiles > 10 && wide_ok(p) && (Split<T>::P == 2 || p.K <= 192)) return {GemmPlan::Wide, 0};
+        if (tiles <= 10 && p.K % 8 == 0 && p.wkstride == 32) return {GemmPlan::Stream, tiles};
+    }
     if (p.swiglu || tiles > 10) return {GemmPlan::Lds, 0};
     if (p.Ah) throw std::runtime_error("gemm: pre-split A needs N > 160 or M <= 2048");
     if (p.scale) {   // SE projects: A read once, all columns per workgroup -- unless that leaves the device idle
@@ -1660,6 +1861,7 @@ template <typename T> void launch_gemm(const GemmArgs& p, hipStream_t s) {
     case GemmPlan::Small: launch_small<T>(p, s); return;
     case GemmPlan::Dma: launch_dma<T>(p, s); return;
     case GemmPlan::Lds: launch_lds<T, 4, 4, 2, 2>(p, s); return;
+    case GemmPlan::Wide: launch_wide<T>(p, s); return;
     case GemmPlan::Stream: launch_stream<T>(p, s); return;
     case GemmPlan::Direct:
         switch (pl.nt) {
@@ -2004,6 +2206,7 @@ template <typename T> std::string gemm_mfma_kernel(const GemmArgs& p) {
         return dma_narrow_tiles(p) ? "gemm_dma_kernel<" + t + ",2,2,4>" : "gemm_dma_kernel<" + t + ",2,4,2>";
     case GemmPlan::Lds: return "gemm_lds_kernel<" + t + ",4,4,2,2>";
     case GemmPlan::Stream: return "gemm_stream_kernel<" + t + "," + std::to_string(pl.nt) + ">";
+    case GemmPlan::Wide: return "gemm_wide_kernel<" + t + ">";
     case GemmPlan::Direct: return "gemm_direct_kernel<" + t + "," + std::to_string(std::min(pl.nt, 5)) + ">";
     }
     return "gemm";
@@ -2032,6 +2235,7 @@ template <typename T> void gemm_mfma_variant(const GemmArgs& p, hipStream_t s, i
     case 6: launch_direct<T, 5>(p, s); return;
     case 7: launch_lds<T, 4, 4, 2, 2>(p, s); return;
     case 8: launch_stream<T>(p, s); return;
+    case 9: launch_wide<T>(p, s); return;
     }
     throw std::runtime_error("gemm: unknown kernel variant " + std::to_string(variant));
 }

@@ -64,7 +64,8 @@ template <typename T> void gemm_mfma(const GemmArgs& p, hipStream_t s);
 // parallel (needs ws for ceil(K / 64) * M * N floats), 5 narrow (the (K, N) shapes of blocks 1-6 only), 6 column
 // chunks (K <= 1024, K % 4 == 0).  MFMA tiers:
 // 0 automatic, 1 small-M, 2..6 direct with 1..5 column tiles per wave, 7 LDS-staged 128 x 128, 8 streaming (N <= 160,
-// every column in one workgroup; the SE projects' kernel).
+// every column in one workgroup; the SE projects' kernel), 9 wide (K <= 256: 64 rows' A split once into LDS, every
+// column chunk of them; no SE scale).
 void gemm_f32_variant(const GemmArgs& p, hipStream_t s, int variant);
 // The kernel (template name) that gemm_f32 / gemm_mfma run for these arguments: the profiler's family names.
 std::string gemm_f32_kernel(const GemmArgs& p);

@@ -581,7 +581,7 @@ class Hip:
 
 
 ACT_NONE, ACT_RELU, ACT_HSWISH, ACT_SILU, ACT_HSIGMOID = 0, 1, 2, 3, 4   # the reference's codes (common.cuh:69)
-GEMM_VARIANTS = {"fp32": [1, 2, 3, 4, 5, 6], "fp16": list(range(1, 9)), "bf16": list(range(1, 9))}
+GEMM_VARIANTS = {"fp32": [1, 2, 3, 4, 5, 6], "fp16": list(range(1, 10)), "bf16": list(range(1, 10))}
 GEMM_NARROW_VARIANTS = {8}   # N <= 160 only
 
 
