@@ -844,11 +844,15 @@ __device__ __forceinline__ void wg_rows_acc(f32x4 (&acc)[C::R], const float (&wd
         f32x4 e[C::NT];
         if constexpr (J >= C::XR0 && J < C::XR0 + C::XRN) {
             const int iy = iy0 + J;
-            const bool in = iy >= 0 && iy < H;   // uniform
+            // rows outside the map become +0 through an all-ones / all-zeros mask that the compiler
+            // cannot see through: as a select it turned each element into its own branch around the activation
+            int keep = iy >= 0 && iy < H ? -1 : 0;
+            asm("" : "+v"(keep));
 #pragma unroll
             for (int t = 0; t < C::NT; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) e[t][i] = in ? apply_act_nb(ea[J - C::XR0][t][i] * es, C::ACT) : 0.0f;
+                for (int i = 0; i < 4; ++i)
+                    e[t][i] = __int_as_float(__float_as_int(apply_act_nb(ea[J - C::XR0][t][i] * es, C::ACT)) & keep);
         } else {   // never staged: outside the map (whole-map staging)
 #pragma unroll
             for (int t = 0; t < C::NT; ++t) e[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
