@@ -258,15 +258,21 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
         for (int i = 0; i < 4; ++i) sbias[i] = stem_b[4 * g + i];
     }
 
-    // ---- per-lane constants: depthwise taps + bias (lane r <= 9 of each row: tap r, bias), project bias
+    // ---- per-lane constants: depthwise taps + bias (lane r <= 9 of each row: tap r, bias), project bias.  The
+    // expand sums leave the matrix cores at the scale 1 / sexp (a power of two) and go through ReLU unscaled: as
+    // relu(sexp * x) = sexp * relu(x) and scaling by a power of two is exact, the taps multiplied by sexp give every
+    // depthwise product bitwise the value of scaling each expanded element first, for one multiply per tap register
+    // instead of one per element
     constexpr int CEXPP_DW = (C::CEXP + 31) / 32 * 32;
     float wdw[C::CT][4];
+    const float tap_scale = C::EXPAND && r < 9 ? a.sexp : 1.0f;
 #pragma unroll
     for (int ct = 0; ct < C::CT; ++ct) {
         const int c = ct * 16 + 4 * g;
         const float* src = r < 9 ? a.wdw + r * CEXPP_DW + c : a.bdw + c;
         const float4 v = *reinterpret_cast<const float4*>(src);
-        wdw[ct][0] = v.x; wdw[ct][1] = v.y; wdw[ct][2] = v.z; wdw[ct][3] = v.w;
+        wdw[ct][0] = v.x * tap_scale; wdw[ct][1] = v.y * tap_scale; wdw[ct][2] = v.z * tap_scale;
+        wdw[ct][3] = v.w * tap_scale;
     }
     f32x4 pb[C::OT];
 #pragma unroll
@@ -400,7 +406,7 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
 #pragma unroll
                                 for (int ks = 0; ks < C::KSI; ++ks) acc = mfma_split16<T>(wf[ks], xf[j][t][ks], acc);
 #pragma unroll
-                                for (int i = 0; i < 4; ++i) acc[i] = relu_nb(acc[i] * a.sexp);
+                                for (int i = 0; i < 4; ++i) acc[i] = relu_nb(acc[i]);   // sexp: in the taps
                             } else {
                                 acc = zero_rows();
                             }
@@ -720,7 +726,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
                     x = mfma_wx<T>(wf[ks], xf, x);
                 }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[i] = apply_act_nb(x[i] * es, C::ACT);
+                for (int i = 0; i < 4; ++i) x[i] = apply_act_nb(C::HS ? x[i] * es : x[i], C::ACT);
                 e[t] = x;
             }
         } else {
@@ -852,7 +858,9 @@ __device__ __forceinline__ void wg_rows_acc(f32x4 (&acc)[C::R], const float (&wd
             for (int t = 0; t < C::NT; ++t)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    e[t][i] = __int_as_float(__float_as_int(apply_act_nb(ea[J - C::XR0][t][i] * es, C::ACT)) & keep);
+                    e[t][i] = __int_as_float(
+                        __float_as_int(apply_act_nb(C::HS ? ea[J - C::XR0][t][i] * es : ea[J - C::XR0][t][i], C::ACT)) &
+                        keep);
         } else {   // never staged: outside the map (whole-map staging)
 #pragma unroll
             for (int t = 0; t < C::NT; ++t) e[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -995,13 +1003,16 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                         for (int q = 0; q < P; ++q)
                             wf[ks][q] = load_part8<T>(wexp + q * a.wexp_stride + (long long)(ct * 16 + r) * C::CINP + ks * 32 + g * 8);
                 }
+                // ReLU blocks: the expand scale sexp rides in the taps, relu(sexp * x) = sexp * relu(x) exactly
+                // (a power of two); hardswish blocks scale each expanded element before the activation
                 float wd[4][C::NWR];
 #pragma unroll
                 for (int w = 0; w < C::NWR; ++w) {
                     const int t = min(w * 16 + r, C::KS * C::KS);
                     const float* src = t < C::KS * C::KS ? a.wdw + t * C::CEXPP + c : a.bdw + c;
                     const float4 v = *reinterpret_cast<const float4*>(src);
-                    wd[0][w] = v.x; wd[1][w] = v.y; wd[2][w] = v.z; wd[3][w] = v.w;
+                    const float f = !C::HS && t < C::KS * C::KS ? a.sexp : 1.0f;
+                    wd[0][w] = v.x * f; wd[1][w] = v.y * f; wd[2][w] = v.z * f; wd[3][w] = v.w * f;
                 }
                 // expand sums at the pre-scaled weights' scale 1 / sexp, from the bias at that scale (exact)
                 const float4 be = *reinterpret_cast<const float4*>(a.bexp + c);
