@@ -980,14 +980,15 @@ gated_norm_kernel(const float* __restrict__ O, const float* __restrict__ P, cons
 }
 
 // ------------------------------------------------------------------------------------------------ SISA
-// One block per (window, head), 256 threads (isa_impl.hpp:996-1069).
+// One block per (window, head), 512 threads (isa_impl.hpp:996-1069): the per-token work of a 321-token window in one
+// pass, the six 64-token output blocks on six waves at once.
 // 1. per token: -softplus(alpha), logsigmoid(forget), theta (device libm)
 // 2. prefix sums in double, one thread per series, rounded to float per element
 // 3. rotate c (last token's angles) and each b_t; scores with the 16-lane dot structure
 // 4. softmax: max, expf, sum in double in token order (one thread); y_j = sum over 64-token blocks of fma chains
 // The order of every rounded operation is the reference's; only order-free work (the maximum, the exponentials,
 // the independent block chains, loads) runs in parallel.
-constexpr int SA_THREADS = 256;
+constexpr int SA_THREADS = 512;
 template <int TT>
 __global__ void __launch_bounds__(SA_THREADS)
 sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __restrict__ lam_h,
@@ -1107,8 +1108,8 @@ sisa_kernel(float* __restrict__ S, const float* __restrict__ QC, const float* __
         s_inv = 1.0f / float(sum);
     }
     __syncthreads();
-    // y_j: the 64-token blocks' fma chains on the four waves (block x on wave x % 4, its 64 values loaded
-    // together), then added in block order
+    // y_j: the 64-token blocks' fma chains on the waves (block x on wave x % 8, its 64 values loaded together),
+    // then added in block order
     {
         const float inv = s_inv;
         const int j = tid & 63;
