@@ -113,6 +113,71 @@ def test_fp32_stages(shv, weights, clips, golden):
             assert rel < 1e-4, (name, rel)
 
 
+SEQ_STAGES = ["h0", "after_gdn_a", "after_gdn_b", "after_sisa_last", "logit"]
+# Each stage's own contribution, element by element: the stage minus its input (the residual stream before the
+# block: after_gdn_a - h0 is GDN-A's output, after_gdn_b - after_gdn_a the two GDN-B blocks', after_sisa_last - the
+# last row of after_gdn_b the SISA block's), as max |d| / max |oracle increment|.  The residual stream itself is
+# dominated by the tokens and positions, so comparing it alone would hide a block's error below the rounding of
+# its input.  Measured on clip 0: reference order 1.1e-5 / 8.5e-6 / 5.7e-7 / 8.2e-8 (GDN-A, GDN-B, SISA, logit:
+# device expf / log1pf in the gates, compounded by the decay products over 321 tokens); the chunked delta rule of
+# the other settings 2.2e-5 / 1.7e-5 / 1.5e-6 to 4.2e-6 / 1.6e-7 to 5.1e-6 in fp32, fp16 and bf16 alike (its order
+# differs from the token-by-token recurrence; the operand parts carry fp32-level precision).  A wrong weight, gate
+# or sign moves an increment by O(1).
+SEQ_INC_TOL = {"fp32-cpu": 5e-5, "fp32": 1e-4, "fp16": 2e-4, "bf16": 2e-4}
+
+
+@pytest.fixture(scope="module")
+def seq_oracle(orc, weights, fp32_model, clips):
+    """Clip 0's tokens (the exact tier's CNN: bitwise the reference's) and the oracle's sequence stages for them."""
+    toks = fp32_model.encode_frames(clips[0]).reshape(20, 16, 384)
+    print("[gpu] oracle sequence stages of clip 0 (CPU)", flush=True)
+    o = orc.Oracle(weights)
+    try:
+        stages = {}
+        o.classify(toks, stages)
+    finally:
+        o.close()
+    return toks, stages
+
+
+def seq_increments(st):
+    f = {n: st[n].astype(np.float64) for n in SEQ_STAGES}
+    return {"h0": f["h0"],
+            "gdn_a": f["after_gdn_a"] - f["h0"],
+            "gdn_b": f["after_gdn_b"] - f["after_gdn_a"],
+            "sisa_last": f["after_sisa_last"] - f["after_gdn_b"][-f["after_sisa_last"].size:],
+            "logit": f["logit"]}
+
+
+@pytest.mark.parametrize("mode", ["fp32-cpu", "fp32", "fp16", "bf16"])
+def test_sequence_stages_elementwise(shv, weights, seq_oracle, mode, margin):
+    """Each sequence stage of one window, element by element, against the oracle's (the reference CPU engine's
+    operation order, checked bitwise against its golden digests) on the same tokens: the exact tier in the reference
+    order and in its own, and the half tiers.  The window input h0 is exact in every tier."""
+    toks, ref = seq_oracle
+    print(f"[gpu] {mode}: sequence stage dumps of clip 0", flush=True)
+    with tempfile.TemporaryDirectory() as d:
+        if mode == "fp32-cpu":
+            m = load_cpu_order(shv, weights, use_graphs=0)
+        else:
+            m = shv.Model(weights, mode.split("-")[0], experimental=mode != "fp32", use_graphs=0)
+        with m:
+            m.set_dump_dir(d)
+            lg = m.classify(toks.reshape(1, 20, 16, 384))
+            got = {n: np.fromfile(Path(d) / f"{n}.f32", np.float32) for n in SEQ_STAGES}
+    assert np.all(np.isfinite(lg))
+    for n in SEQ_STAGES:
+        assert got[n].shape == ref[n].shape, (n, got[n].shape, ref[n].shape)
+    assert np.array_equal(got["h0"], ref["h0"])
+    gi, ri = seq_increments(got), seq_increments(ref)
+    for name in ["gdn_a", "gdn_b", "sisa_last", "logit"]:
+        a, b = gi[name], ri[name]
+        err = float(np.abs(a - b).max()) / max(1e-30, float(np.abs(b).max()))
+        print(f"[gpu] {mode} {name}: max|d| / max|oracle| {err:.3e}", flush=True)
+        margin(f"{mode} sequence stage {name} vs oracle (relative, every element)", err, SEQ_INC_TOL[mode])
+        assert err <= SEQ_INC_TOL[mode], (name, err)
+
+
 def test_row_independence_fp32(fp32_model, clips):
     """A clip's logit does not depend on the rest of the batch.  One clip's GEMMs run on the matrix-core kernel's
     small tiles and its delta rule on eight key groups per column, the batch of 6 on larger tiles and four groups:
