@@ -117,42 +117,67 @@ __global__ void __launch_bounds__(256) audio_stem_kernel(const float* __restrict
 
 // ---------------------------------------------------------------------------------------------------- depthwise
 // 3x3 depthwise with strides (time st, freq sf), padding 1, BatchNorm, SiLU (frontend.cpp:32-39, 188-192): per output
-// sum = sum + x * w from +0 over kf, then kt, skipping taps outside the image.  One lane per 4 channels of a pixel.
+// sum = sum + x * w from +0 over kf, then kt, skipping taps outside the image.  A lane takes 4 channels of DW_TO
+// consecutive time outputs of one frequency column: the 9 weight quads are loaded once and the input rows the outputs
+// share (kt = 2 of output j is kt = 0 of output j + 1 at stride 1) once per kf, while every output still adds its
+// products in the (kf, kt) order above.
+constexpr int DW_TO = 4;
+template <int ST>
 __global__ void __launch_bounds__(256) audio_dw_kernel(const float* __restrict__ in, float* __restrict__ out,
                                                        const float* __restrict__ w, const float* __restrict__ scale,
-                                                       const float* __restrict__ shift, int T, int F, int C, int st,
-                                                       int sf, int To, int Fo, long long total) {
+                                                       const float* __restrict__ shift, int T, int F, int C, int sf,
+                                                       int To, int Fo, long long total) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
     const int C4 = C >> 2;
     const int c = int(i % C4) * 4;
-    const long long px = i / C4;
+    const long long px = i / C4;   // (window, time group, frequency column)
     const int fo = int(px % Fo);
     const long long r = px / Fo;
-    const int to = int(r % To);
-    const long long win = r / To;
+    const int tgroups = (To + DW_TO - 1) / DW_TO;
+    const int to0 = int(r % tgroups) * DW_TO;
+    const long long win = r / tgroups;
     const float* x = in + win * T * F * C;
-    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    constexpr int NR = ST * (DW_TO - 1) + 3;   // input rows of the group's outputs: ST * to0 - 1 + 0 .. NR - 1
+    float4 k[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q) k[q] = *reinterpret_cast<const float4*>(w + q * C + c);
+    float4 sum[DW_TO];
+#pragma unroll
+    for (int j = 0; j < DW_TO; ++j) sum[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int ti0 = ST * to0 - 1;
 #pragma unroll
     for (int kf = 0; kf < 3; ++kf) {
         const int fi = fo * sf + kf - 1;
         if (fi < 0 || fi >= F) continue;
+        float4 v[NR];
 #pragma unroll
-        for (int kt = 0; kt < 3; ++kt) {
-            const int ti = to * st + kt - 1;
-            if (ti < 0 || ti >= T) continue;
-            const float4 v = *reinterpret_cast<const float4*>(x + ((long long)ti * F + fi) * C + c);
-            const float4 k = *reinterpret_cast<const float4*>(w + (kf * 3 + kt) * C + c);
-            sum.x = sum.x + v.x * k.x;
-            sum.y = sum.y + v.y * k.y;
-            sum.z = sum.z + v.z * k.z;
-            sum.w = sum.w + v.w * k.w;
+        for (int j = 0; j < NR; ++j) {
+            const int ti = min(max(ti0 + j, 0), T - 1);   // clamped: rows outside the image are skipped below
+            v[j] = *reinterpret_cast<const float4*>(x + ((long long)ti * F + fi) * C + c);
         }
+#pragma unroll
+        for (int j = 0; j < DW_TO; ++j)
+#pragma unroll
+            for (int kt = 0; kt < 3; ++kt) {
+                const int ti = ti0 + ST * j + kt;
+                if (ti < 0 || ti >= T) continue;
+                const float4 a = v[ST * j + kt], b = k[kf * 3 + kt];
+                sum[j].x = sum[j].x + a.x * b.x;
+                sum[j].y = sum[j].y + a.y * b.y;
+                sum[j].z = sum[j].z + a.z * b.z;
+                sum[j].w = sum[j].w + a.w * b.w;
+            }
     }
     const float4 sc = *reinterpret_cast<const float4*>(scale + c), sh = *reinterpret_cast<const float4*>(shift + c);
-    const float4 y = make_float4(silu_libm(sum.x * sc.x + sh.x), silu_libm(sum.y * sc.y + sh.y),
-                                 silu_libm(sum.z * sc.z + sh.z), silu_libm(sum.w * sc.w + sh.w));
-    *reinterpret_cast<float4*>(out + px * C + c) = y;
+#pragma unroll
+    for (int j = 0; j < DW_TO; ++j) {
+        const int to = to0 + j;
+        if (to >= To) break;
+        const float4 y = make_float4(silu_libm(sum[j].x * sc.x + sh.x), silu_libm(sum[j].y * sc.y + sh.y),
+                                     silu_libm(sum[j].z * sc.z + sh.z), silu_libm(sum[j].w * sc.w + sh.w));
+        *reinterpret_cast<float4*>(out + ((win * To + to) * Fo + fo) * C + c) = y;
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------- attention
@@ -214,9 +239,13 @@ void launch_audio_dw(const float* in, float* out, const float* w, const float* s
     if (n <= 0) return;
     if (C % 4 || st < 1 || st > 2 || sf < 1 || sf > 2) throw std::runtime_error("audio depthwise: bad shape");
     const int To = (T + st - 1) / st, Fo = (F + sf - 1) / sf;
-    const long long total = (long long)n * To * Fo * (C / 4);
-    hipLaunchKernelGGL(audio_dw_kernel, dim3(cdiv(total, 256)), dim3(256), 0, s, in, out, w, scale, shift, T, F, C,
-                       st, sf, To, Fo, total);
+    const long long total = (long long)n * ((To + DW_TO - 1) / DW_TO) * Fo * (C / 4);
+    if (st == 1)
+        hipLaunchKernelGGL(audio_dw_kernel<1>, dim3(cdiv(total, 256)), dim3(256), 0, s, in, out, w, scale, shift, T,
+                           F, C, sf, To, Fo, total);
+    else
+        hipLaunchKernelGGL(audio_dw_kernel<2>, dim3(cdiv(total, 256)), dim3(256), 0, s, in, out, w, scale, shift, T,
+                           F, C, sf, To, Fo, total);
 }
 
 void launch_audio_freq_pool(const float* h, const float* w, float bias, float* pooled, int n, hipStream_t s) {
