@@ -1831,6 +1831,16 @@ template <typename T> GemmPlan plan_gemm(const GemmArgs& p) {
         if (tiles > 10 && wide_ok(p) && (Split<T>::P == 2 || p.K <= 192)) return {GemmPlan::Wide, 0};
         if (tiles <= 10 && p.K % 8 == 0 && p.wkstride == 32) return {GemmPlan::Stream, tiles};
     }
+    // K < 64, large M, measured per shape: up to 5 column tiles the streaming kernel (9,216,000 x 24 -> 72: 859 vs
+    // 980 us; the SHIELD-A frontend's 1,276,160 x 32 -> 64: 156 vs 168); 6 tiles the direct kernel at 2 per wave
+    // (319,360 x 48 -> 96: 66 vs 79 at 3 per wave, streaming 77); more than 10 the wide kernel (2,355,200 x 40 ->
+    // 240: fp16 1,176 vs 1,553 LDS-tiled, bf16 1,247 vs 3,005); 7 to 10 the direct choice below (2,007,040 x 40 ->
+    // 120: fp16 531 vs 548 wide and 699 streaming; bf16 723 vs 933 wide)
+    if (!p.Ah && !p.scale && !p.swiglu && p.K < 64 && p.K % 8 == 0 && p.wkstride == 32) {
+        if (tiles <= 5) return {GemmPlan::Stream, tiles};
+        if (tiles == 6) return {GemmPlan::Direct, 2};
+        if (tiles > 10 && wide_ok(p)) return {GemmPlan::Wide, 0};
+    }
     if (p.swiglu || tiles > 10) return {GemmPlan::Lds, 0};
     if (p.Ah) throw std::runtime_error("gemm: pre-split A needs N > 160 or M <= 2048");
     if (p.scale) {   // SE projects: A read once, all columns per workgroup -- unless that leaves the device idle
