@@ -12,7 +12,10 @@ points shv_hip_gemm_*: the literal config shapes at full M, bias + hardswish fus
 import numpy as np
 import pytest
 
-SHAPES = [("b2.expand literal", 2560 * 28 * 28, 120, 40), ("b14.expand literal", 2560 * 7 * 7, 960, 160)]
+SHAPES = [("b2.expand literal", 2560 * 28 * 28, 120, 40), ("b14.expand literal", 2560 * 7 * 7, 960, 160),
+          # the short-K routes of the half tiers' planner (K < 64): streaming kernel (<= 5 column tiles), direct kernel
+          # at 2 tiles per wave (6), wide kernel (> 10), as the SHIELD-A frontend and the layer path meet them
+          ("short-K streaming", 200_000, 64, 32), ("short-K direct", 100_000, 96, 48), ("short-K wide", 100_000, 240, 40)]
 SPLIT_TOL = 2.0 ** -17
 
 
