@@ -488,13 +488,14 @@ private:
     // F frames as up to kBranches branches of at least kBranchClips clips' frames on the branch streams, forked from
     // and joined to q (one branch when dumping: the dumps show frame 0); one after another on q while profiling, so
     // each kernel is timed alone at the shapes the forward gives it
-    // n clips end to end as up to kBranches branches of whole clips (at least kBranchClips each).  Each pair of
-    // branches runs its clips' sequence stages on the second branch's stream once both have encoded, so those
-    // stages overlap the other pair's encoders instead of waiting for all four (windows are independent rows: the
-    // logits are bitwise those of one pass).  Measured per 128 clips: sequence after all branches 19.47 ms, per pair
-    // 19.15, per branch 19.07 -- the last ran the sequence GEMMs at 32 windows, 1.5x slower per row, so the pair
-    // is kept.
-    static constexpr int kSeqGroup = 2;
+    // n clips end to end as up to kBranches branches of whole clips (at least kBranchClips each).  Each group of
+    // kSeqGroup branches runs its clips' sequence stages on its last branch's stream once the group has encoded, so
+    // those stages overlap the other branches' encoders instead of waiting for all of them (windows are independent
+    // rows and every kernel choice by batch is bitwise neutral: the logits are those of one pass).  Measured per
+    // 128 clips, alternating on one box: per branch 18.48-18.60 ms, per pair 18.67-18.87, after all four 18.92 --
+    // the 32-window sequence GEMMs are slower per row than 64-window ones, but the last group's stages, which run
+    // with nothing beside them, take half as long.
+    static constexpr int kSeqGroup = 1;
     // frames [n * 20] -> tokens [n * 20][6144] -> logits [n], window w reading its frames' tokens through
     // tokptr[w * 20 ..]
     void forward_branched(const uint8_t* frames, float* tokens, const float* const* tokptr, int n, float* logits,
