@@ -669,6 +669,8 @@ def main() -> int:
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-audio", action="store_true")
     ap.add_argument("--no-live", action="store_true")
+    ap.add_argument("--gemm-only", action="store_true", help="only the GEMM microbench (config 2 and the model / "
+                    "sequence shapes), for a kernel trace of its launches")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every GPU box here has one GPU, and the SHIELD-V forward has no "
@@ -680,6 +682,12 @@ def main() -> int:
     hip = shv.Hip()
     B = args.batch
     revision = shv.library().shv_hip_compute_revision().decode()
+    if args.gemm_only:
+        stream = hip.stream()
+        e0, e1 = hip.event(), hip.event()
+        print(json.dumps({"gemm_microbench": gemm_microbench(shv, hip, stream, e0, e1), "revision": revision}),
+              flush=True)
+        return 0
     with tempfile.TemporaryDirectory() as td:
         w = Path(td) / "bench.weights"
         shv.write_weights(w, seed=1, threshold=0.5)
