@@ -550,7 +550,7 @@ template <typename T, class C, bool STEM = false> void launch_strip(int block, c
 // last tap.  Columns outside the map expand from -1e30 (ReLU and hardswish both give 0 there), rows outside the
 // map are skipped (E = 0).
 template <int CIN_, int CEXP_, int COUT_, int KS_, int S_, int HS_, int SE_, int R_, int MINB_ = 1, int ROLLK_ = 0,
-          int NOPF_ = 0, int WHOLE_H_ = 0, int NPOS_ = 16, int YBA_ = 0, int WAVES_ = 4>
+          int NOPF_ = 0, int WHOLE_H_ = 0, int NPOS_ = 16, int YBA_ = 0, int WAVES_ = 4, int RING_ = 0>
 struct WgCfg {
     static constexpr int CIN = CIN_, CEXP = CEXP_, COUT = COUT_, KS = KS_, S = S_, R = R_;
     static constexpr int MINB = MINB_;   // workgroups per CU the register allocation must allow
@@ -585,6 +585,12 @@ struct WgCfg {
     // YBA (projection blocks): the wave partials of the projection share LDS with the staged rows (two more
     // barriers per step: before the partials are written, and before the next step's rows are staged)
     static constexpr bool YBA = YBA_ != 0;
+    // RING (squeeze-excite blocks stepping down the map): the HALO = KS - S input rows a step shares with the next
+    // stay staged.  LDS holds the IR rows as a ring, row j of step st in slot (st * ADV + j) mod IR, and every step
+    // but a segment's first stages only its ADV = S * R new rows (a staged row depends on its map row alone)
+    static constexpr int ADV = S * R, HALO = IR - ADV;
+    static constexpr bool RING = RING_ != 0 && SE && !WHOLE_H_ && !YBA && HALO > 0;
+    static_assert(!RING || (XR0 == 0 && XRN == IR), "the ring holds a step's IR input rows");
     static_assert(NPOS >= 1 && NPOS <= 16 && POS0 + NPOS <= 16, "staged positions within the 16 lanes");
     static constexpr bool RES = PROJ && S == 1 && CIN == COUT;
     static constexpr int NWR = (KS * KS + 1 + 15) / 16;    // depthwise weight registers per value (taps + bias)
@@ -704,16 +710,23 @@ __device__ __forceinline__ void accum_row(f32x4 (&acc)[C::R], const float (&wd)[
     }
 }
 
+// the LDS slot of a step's staged row j (j counted from XR0; rb: the ring slot of the step's row 0)
+template <class C> __device__ __forceinline__ int row_slot(int j, int rb) {
+    if constexpr (C::RING) return rb + j < C::IR ? rb + j : rb + j - C::IR;
+    else return j;
+}
+
 template <typename T, class C, int J>
 __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4][C::NWR], const typename Split<T>::V8 (&wf)[C::KS32][Split<T>::P],
                                         const f32x4 (&init)[C::NT], const T* Xs, int r, int g, int iy0, int H,
-                                        float es) {
+                                        float es, int rb) {
     if constexpr (J < C::IR) {
         typedef typename Split<T>::V8 V8;
         constexpr int P = Split<T>::P;
         f32x4 e[C::NT];
         const int iy = iy0 + J;
         if (iy >= 0 && iy < H) {   // uniform
+            const T* Xr = Xs + row_slot<C>(J - C::XR0, rb) * (C::NT * P * C::NPOS * C::XLD);
 #pragma unroll
             for (int t = 0; t < C::NT; ++t) {
                 f32x4 x = init[t];
@@ -722,7 +735,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
                     V8 xf[P];
 #pragma unroll
                     for (int q = 0; q < P; ++q)
-                        xf[q] = *reinterpret_cast<const V8*>(Xs + ((((J - C::XR0) * C::NT + t) * P + q) * C::NPOS + staged_pos<C>(r)) * C::XLD + ks * 32 + g * 8);
+                        xf[q] = *reinterpret_cast<const V8*>(Xr + ((t * P + q) * C::NPOS + staged_pos<C>(r)) * C::XLD + ks * 32 + g * 8);
                     x = mfma_wx<T>(wf[ks], xf, x);
                 }
 #pragma unroll
@@ -765,7 +778,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
             }
         }
         accum_row<C, J, 0>(acc, wd, v);
-        wg_rows<T, C, J + 1>(acc, wd, wf, init, Xs, r, g, iy0, H, es);
+        wg_rows<T, C, J + 1>(acc, wd, wf, init, Xs, r, g, iy0, H, es, rb);
     }
 }
 
@@ -774,7 +787,7 @@ __device__ __forceinline__ void wg_rows(f32x4 (&acc)[C::R], const float (&wd)[4]
 template <typename T, class C>
 __device__ __forceinline__ void wg_expand_rolled(f32x4 (&ea)[C::XRN][C::NT], const T* wexp, long long wstride, int ct,
                                                  const f32x4 (&init)[C::NT], const T* Xs, int r, int g, int iy0,
-                                                 int H) {
+                                                 int H, int rb) {
     typedef typename Split<T>::V8 V8;
     constexpr int P = Split<T>::P;
 #pragma unroll
@@ -803,7 +816,7 @@ __device__ __forceinline__ void wg_expand_rolled(f32x4 (&ea)[C::XRN][C::NT], con
                     V8 xf[P];
 #pragma unroll
                     for (int q = 0; q < P; ++q)
-                        xf[q] = *reinterpret_cast<const V8*>(Xs + (((j * C::NT + t) * P + q) * C::NPOS + staged_pos<C>(r)) * C::XLD + ks * 32 + g * 8);
+                        xf[q] = *reinterpret_cast<const V8*>(Xs + (((row_slot<C>(j, rb) * C::NT + t) * P + q) * C::NPOS + staged_pos<C>(r)) * C::XLD + ks * 32 + g * 8);
                     ea[j][t] = mfma_wx<T>(w, xf, ea[j][t]);
                 }
             }
@@ -895,40 +908,50 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 
     // staging of a step's input rows: float4 i -> (row j, tile t, pixel p, channel quad c4).  The loads read clamped,
     // always valid addresses unconditionally (32-bit offsets from the frame's base); what lies outside the map or
-    // past cin is zeroed when the rows are split into LDS, so no load waits on a predicate
+    // past cin is zeroed when the rows are split into LDS, so no load waits on a predicate.  A full staging covers
+    // the step's XRN rows; with the ring a continuing step stages its ADV new rows (j = HALO ..) only
     constexpr int XQ = C::CINP / 4;
-    constexpr int XN = C::XRN * C::NT * C::NPOS * XQ;
-    constexpr int XPT_ALL = (XN + C::THREADS - 1) / C::THREADS;
+    constexpr int XROW = C::NT * C::NPOS * XQ;               // float4s of one staged input row
+    constexpr int XN = C::XRN * XROW, XNC = C::RING ? C::ADV * XROW : XN;
+    constexpr int XPT_ALL = (XN + C::THREADS - 1) / C::THREADS, XPTC_ALL = (XNC + C::THREADS - 1) / C::THREADS;
     constexpr int XPT = C::NOPF ? (XPT_ALL < C::NOPF_CHUNK ? XPT_ALL : C::NOPF_CHUNK) : XPT_ALL;   // held at a time
     float4 xpre[XPT];
     auto col_of = [&](int strip, int p, int t) {
         return C::S == 1 ? strip * C::VALID - C::PADK + p : 2 * (strip * C::VALID - 1 + p) + t;
     };
-    auto load_step = [&](int fs, int step, int k0) {
+    // FULL: std::true_type (every row of the step) or std::false_type (the ring's new rows)
+    auto load_step = [&](auto full, int fs, int step, int k0) {
+        constexpr bool FULL = decltype(full)::value;
+        constexpr int N = FULL ? XN : XNC, J0 = FULL ? 0 : C::XRN - XNC / XROW;
+        constexpr int NK = (FULL ? XPT_ALL : XPTC_ALL) < XPT ? (FULL ? XPT_ALL : XPTC_ALL) : XPT;
         const int strip = fs % strips;
         const float* Xf = a.X + (long long)(fs / strips) * (H * W * C::CIN);
         const int iy0 = C::S * step * C::R - C::PADK + C::XR0;
 #pragma unroll
-        for (int k = 0; k < XPT; ++k) {
-            const int i = min(tid + (k0 + k) * C::THREADS, XN - 1);
+        for (int k = 0; k < NK; ++k) {
+            const int i = min(tid + (k0 + k) * C::THREADS, N - 1);
             const int c4 = i % XQ, rest = i / XQ;
             const int p = rest % C::NPOS, jt = rest / C::NPOS;
-            const int t = jt % C::NT, j = jt / C::NT;
+            const int t = jt % C::NT, j = J0 + jt / C::NT;
             const int cy = min(max(iy0 + j, 0), H - 1), cx = min(max(col_of(strip, p + C::POS0, t), 0), W - 1);
             const int cc = min(c4, C::CIN / 4 - 1);
             const unsigned byte_off = unsigned(((cy * W + cx) * C::CIN + cc * 4) * 4);   // within one frame
             xpre[k] = *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(Xf) + byte_off);
         }
     };
-    auto store_step = [&](int strip, int step, int k0) {
+    auto store_step = [&](auto full, int strip, int step, int k0) {
+        constexpr bool FULL = decltype(full)::value;
+        constexpr int N = FULL ? XN : XNC, J0 = FULL ? 0 : C::XRN - XNC / XROW;
+        constexpr int NK = (FULL ? XPT_ALL : XPTC_ALL) < XPT ? (FULL ? XPT_ALL : XPTC_ALL) : XPT;
         const int iy0 = C::S * step * C::R - C::PADK + C::XR0;
+        const int rb = C::RING ? step * C::ADV % C::IR : 0;
 #pragma unroll
-        for (int k = 0; k < XPT; ++k) {
+        for (int k = 0; k < NK; ++k) {
             const int i = tid + (k0 + k) * C::THREADS;
-            if (i >= XN) continue;
+            if (i >= N) continue;
             const int c4 = i % XQ, rest = i / XQ;
             const int p = rest % C::NPOS, jt = rest / C::NPOS;
-            const int t = jt % C::NT, j = jt / C::NT;
+            const int t = jt % C::NT, j = J0 + jt / C::NT;
             const int iy = iy0 + j, ix = col_of(strip, p + C::POS0, t);
             const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W && c4 * 4 < C::CIN;
             const float x[4] = {in ? xpre[k].x : 0.0f, in ? xpre[k].y : 0.0f, in ? xpre[k].z : 0.0f,
@@ -936,19 +959,22 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             T part[4][P];
 #pragma unroll
             for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
+            const int jl = row_slot<C>(j, rb) * C::NT + t;
 #pragma unroll
             for (int q = 0; q < P; ++q) {
                 T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
-                *reinterpret_cast<uint2*>(Xs + ((jt * P + q) * C::NPOS + p) * C::XLD + c4 * 4) = *reinterpret_cast<const uint2*>(four);
+                *reinterpret_cast<uint2*>(Xs + ((jl * P + q) * C::NPOS + p) * C::XLD + c4 * 4) = *reinterpret_cast<const uint2*>(four);
             }
         }
     };
+    const std::true_type full_rows;
+    const std::false_type new_rows;
 
     // item -> (frame, strip) index, first step of its segment
     auto item_fs = [&](int it) { return it / csplit / segs; };
     auto item_s0 = [&](int it) { return (it / csplit % segs) * seg_steps; };
     if constexpr (!C::NOPF) {
-        if ((int)blockIdx.x < items) load_step(item_fs(blockIdx.x), item_s0(blockIdx.x), 0);
+        if ((int)blockIdx.x < items) load_step(full_rows, item_fs(blockIdx.x), item_s0(blockIdx.x), 0);
     }
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
         const int fs = item_fs(item), cgroup = item % csplit;   // (frame, strip) index, channel-tile group
@@ -966,19 +992,28 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
         }
         for (int step = s0; step < s1; ++step) {
             const int oy0 = step * C::R;
+            const int rb = C::RING ? step * C::ADV % C::IR : 0;   // ring slot of the step's first row
             if constexpr (C::NOPF) {
-                for (int k0 = 0; k0 < XPT_ALL; k0 += XPT) {
-                    load_step(fs, step, k0);
-                    store_step(strip, step, k0);
+                if (!C::RING || step == s0) {
+                    for (int k0 = 0; k0 < XPT_ALL; k0 += XPT) {
+                        load_step(full_rows, fs, step, k0);
+                        store_step(full_rows, strip, step, k0);
+                    }
+                } else {
+                    for (int k0 = 0; k0 < XPTC_ALL; k0 += XPT) {
+                        load_step(new_rows, fs, step, k0);
+                        store_step(new_rows, strip, step, k0);
+                    }
                 }
                 lds_barrier();
             } else {
-                store_step(strip, step, 0);
+                if (!C::RING || step == s0) store_step(full_rows, strip, step, 0);
+                else store_step(new_rows, strip, step, 0);
                 lds_barrier();
                 // the next step's (or next item's first) rows are in flight while this step computes
-                if (step + 1 < s1) load_step(fs, step + 1, 0);
+                if (step + 1 < s1) load_step(new_rows, fs, step + 1, 0);
                 else if (item + (int)gridDim.x < items)
-                    load_step(item_fs(item + gridDim.x), item_s0(item + gridDim.x), 0);
+                    load_step(full_rows, item_fs(item + gridDim.x), item_s0(item + gridDim.x), 0);
             }
 
             f32x4 y[C::PROJ ? C::R : 1][C::PROJ ? C::OT : 1];
@@ -1039,10 +1074,10 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
                 for (int q = 0; q < C::R; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 if constexpr (C::ROLLK) {
                     f32x4 ea[C::XRN][C::NT];
-                    wg_expand_rolled<T, C>(ea, wexp, a.wexp_stride, ct, init, Xs, r, g, C::S * oy0 - C::PADK, H);
+                    wg_expand_rolled<T, C>(ea, wexp, a.wexp_stride, ct, init, Xs, r, g, C::S * oy0 - C::PADK, H, rb);
                     wg_rows_acc<C, 0>(acc, wd, ea, C::S * oy0 - C::PADK, H, a.sexp);
                 } else {
-                    wg_rows<T, C, 0>(acc, wd, wf, init, Xs, r, g, C::S * oy0 - C::PADK, H, a.sexp);
+                    wg_rows<T, C, 0>(acc, wd, wf, init, Xs, r, g, C::S * oy0 - C::PADK, H, a.sexp, rb);
                 }
                 constexpr int BL = C::KS * C::KS;   // bias lane index (taps 0 .. BL-1)
                 f32x4 d[C::R];
@@ -1116,8 +1151,11 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
 }
 
 //                cin  cexp cout k  s  hs se R  minb
-typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 3, 3> G4;      // 45x80 -> 23x40 (R 3, three workgroups per CU: 0.94 -> 0.88 ms)
-typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 6> G5;         // 23x40 (b5, b6)
+// Blocks 4-6 keep the rows shared by consecutive steps staged (RING; bitwise unchanged): block 4 0.88 -> 0.85 ms,
+// blocks 5-6 1.80 -> 1.78 ms per 128 clips alone.  Blocks 11-13 ran slower with it (block 11 0.67 -> 0.83 ms: 165 ->
+// 181 VGPRs, two waves per SIMD instead of three; blocks 12, 13 +4%, +1%)
+typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 3, 3, 0, 0, 0, 16, 0, 4, 1> G4;   // 45x80 -> 23x40 (R 3, three workgroups per CU: 0.94 -> 0.88 ms)
+typedef WgCfg<40, 120, 40, 5, 1, 0, 1, 6, 1, 0, 0, 0, 16, 0, 4, 1> G5;   // 23x40 (b5, b6)
 typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 3, 2, 0, 0, 0, 16, 1> G7;    // 23x40 -> 12x20
 typedef WgCfg<80, 200, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G8;       // 12x20
 typedef WgCfg<80, 184, 80, 3, 1, 1, 0, 4, 2, 0, 8, 0, 16, 1> G9;       // 12x20 (b9, b10)
@@ -1133,7 +1171,7 @@ typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 6, 1, 0, 0, 0, 16, 0, 8> G12;   // 12x2
 typedef WgCfg<112, 672, 160, 5, 2, 1, 1, 2, 2, 1, 16, 0, 10, 0, 8> G13;   // 12x20 -> 6x10, 10 columns/tile, eight waves
 typedef WgCfg<160, 960, 160, 5, 1, 1, 1, 6, 1, 1, 1, 6, 16, 0, 8> G14;   // 6x10 (b14, b15), eight waves
 // bf16 (three operand parts): fewer rows per step where the fp16 row step leaves LDS room for one workgroup per CU
-typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 3> G4B;
+typedef WgCfg<24, 72, 40, 5, 2, 0, 1, 3, 1, 0, 0, 0, 16, 0, 4, 1> G4B;
 typedef WgCfg<40, 240, 80, 3, 2, 1, 0, 2, 2, 0, 0, 0, 16, 1> G7B;
 typedef WgCfg<112, 672, 112, 3, 1, 1, 1, 4> G12B;
 
