@@ -13,6 +13,9 @@ typedef __bf16 bf16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_HS = 2, ACT_HSIG = 3, ACT_SILU = 4 };
 

@@ -217,15 +217,11 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
             const int row = i / XQ, q = i - row * XQ;
             if constexpr (L::PRESPLIT) {
                 const float x[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
-                T part[4][S::P];
+                uint2 four[S::P];
+                split4_packed<T>(x, four);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
-#pragma unroll
-                for (int pq = 0; pq < S::P; ++pq) {
-                    T four[4] = {part[0][pq], part[1][pq], part[2][pq], part[3][pq]};
-                    *reinterpret_cast<uint2*>(Xh + (pq * L::XH_ROWS + row) * L::XH_LD + q * 4) =
-                        *reinterpret_cast<const uint2*>(four);
-                }
+                for (int pq = 0; pq < S::P; ++pq)
+                    *reinterpret_cast<uint2*>(Xh + (pq * L::XH_ROWS + row) * L::XH_LD + q * 4) = four[pq];
             } else {
                 *reinterpret_cast<float4*>(Xs + row * C::XS_LD + q * 4) = xr[k];
             }
@@ -262,15 +258,11 @@ __global__ void __launch_bounds__(IR_THREADS) ir_block_kernel(IrArgs a) {
                     v = *reinterpret_cast<const float4*>(Xf + ((long long)iy * a.W + ix) * C::CIN + q * 4);
                 if constexpr (L::PRESPLIT) {
                     const float x[4] = {v.x, v.y, v.z, v.w};
-                    T part[4][S::P];
+                    uint2 four[S::P];
+                    split4_packed<T>(x, four);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
-#pragma unroll
-                    for (int pq = 0; pq < S::P; ++pq) {
-                        T four[4] = {part[0][pq], part[1][pq], part[2][pq], part[3][pq]};
-                        *reinterpret_cast<uint2*>(Xh + (pq * L::XH_ROWS + row) * L::XH_LD + q * 4) =
-                            *reinterpret_cast<const uint2*>(four);
-                    }
+                    for (int pq = 0; pq < S::P; ++pq)
+                        *reinterpret_cast<uint2*>(Xh + (pq * L::XH_ROWS + row) * L::XH_LD + q * 4) = four[pq];
                 } else {
                     *reinterpret_cast<float4*>(Xs + row * C::XS_LD + q * 4) = v;
                 }
@@ -643,15 +635,11 @@ __global__ void __launch_bounds__(IR_THREADS) ir_se_wave_kernel(IrArgs a) {
             if (i >= XN) continue;
             const int row = i / XQ, q = i - row * XQ;
             const float x[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
-            T part[4][S::P];
+            uint2 four[S::P];
+            split4_packed<T>(x, four);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
-#pragma unroll
-            for (int pq = 0; pq < S::P; ++pq) {
-                T four[4] = {part[0][pq], part[1][pq], part[2][pq], part[3][pq]};
-                *reinterpret_cast<uint2*>(Xh + (pq * C::XH_ROWS + row) * C::XH_LD + q * 4) =
-                    *reinterpret_cast<const uint2*>(four);
-            }
+            for (int pq = 0; pq < S::P; ++pq)
+                *reinterpret_cast<uint2*>(Xh + (pq * C::XH_ROWS + row) * C::XH_LD + q * 4) = four[pq];
         }
     }
     // expand rows of this lane inside the map: bit 4 mt + i

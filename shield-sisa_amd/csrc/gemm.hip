@@ -962,14 +962,10 @@ __global__ void __launch_bounds__(256) gemm_lds_kernel(GemmArgs p, int mblocks, 
             if (i >= A4) continue;
             const int row = i / (LG_KT / 4), c = i % (LG_KT / 4);
             const float x[4] = {ra[k].x, ra[k].y, ra[k].z, ra[k].w};
-            T part[4][P];
+            uint2 four[P];
+            split4_packed<T>(x, four);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
-#pragma unroll
-            for (int q = 0; q < P; ++q) {
-                T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
-                *reinterpret_cast<uint2*>(&As[q][row][c * 4]) = *reinterpret_cast<const uint2*>(four);
-            }
+            for (int q = 0; q < P; ++q) *reinterpret_cast<uint2*>(&As[q][row][c * 4]) = four[q];
         }
 #pragma unroll
         for (int k = 0; k < WR; ++k) {
@@ -1536,14 +1532,10 @@ __global__ void __launch_bounds__(256, 2) gemm_wide_kernel(GemmArgs p) {
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (m < p.M && k < p.K) v = *reinterpret_cast<const float4*>(p.A + m * p.lda + k);
         const float x[4] = {v.x, v.y, v.z, v.w};
-        T part[4][P];
+        uint2 four[P];
+        split4_packed<T>(x, four);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
-#pragma unroll
-        for (int q = 0; q < P; ++q) {
-            T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
-            *reinterpret_cast<uint2*>(As + (q * WD_ROWS + row) * ld + k) = *reinterpret_cast<const uint2*>(four);
-        }
+        for (int q = 0; q < P; ++q) *reinterpret_cast<uint2*>(As + (q * WD_ROWS + row) * ld + k) = four[q];
     }
     lds_barrier();
     const T* W = static_cast<const T*>(p.W);
@@ -1913,14 +1905,10 @@ __global__ void __launch_bounds__(256) tail_pool_kernel(const float* __restrict_
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (row < 60) v = *reinterpret_cast<const float4*>(Xf + row * TAIL_K + c4 * 4);
         const float x[4] = {v.x, v.y, v.z, v.w};
-        T part[4][P];
+        uint2 four[P];
+        split4_packed<T>(x, four);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
-#pragma unroll
-        for (int q = 0; q < P; ++q) {
-            T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
-            *reinterpret_cast<uint2*>(&Xs[q][row][c4 * 4]) = *reinterpret_cast<const uint2*>(four);
-        }
+        for (int q = 0; q < P; ++q) *reinterpret_cast<uint2*>(&Xs[q][row][c4 * 4]) = four[q];
     }
     __syncthreads();
     float(*E)[TAIL_ELD] = Es[wave];

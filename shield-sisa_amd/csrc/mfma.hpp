@@ -32,6 +32,16 @@ template <> struct Split<f16> {
         part[0] = h;
         part[1] = f16(x - float(h));
     }
+    // two values at once, the same roundings as split: each part pair is one packed conversion, and hi goes back
+    // to fp32 from the packed pair (as split one by one, the compiler converts x to fp16 twice: unpacked for the
+    // remainder and again packed for the store)
+    typedef f16x2 V2;
+    static __device__ __forceinline__ void split2(float x0, float x1, V2* part) {
+        asm("" : "+v"(x0), "+v"(x1));
+        const V2 h = __builtin_convertvector(f32x2{x0, x1}, V2);
+        part[0] = h;
+        part[1] = __builtin_convertvector(f32x2{x0 - float(h[0]), x1 - float(h[1])}, V2);
+    }
     static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
@@ -52,6 +62,16 @@ template <> struct Split<bf16> {
         part[0] = h;
         part[1] = m;
         part[2] = bf16(r - float(m));
+    }
+    typedef bf16x2 V2;   // two values at once (as Split<f16>::split2)
+    static __device__ __forceinline__ void split2(float x0, float x1, V2* part) {
+        asm("" : "+v"(x0), "+v"(x1));
+        const V2 h = __builtin_convertvector(f32x2{x0, x1}, V2);
+        const float r0 = x0 - float(h[0]), r1 = x1 - float(h[1]);
+        const V2 m = __builtin_convertvector(f32x2{r0, r1}, V2);
+        part[0] = h;
+        part[1] = m;
+        part[2] = __builtin_convertvector(f32x2{r0 - float(m[0]), r1 - float(m[1])}, V2);
     }
     static __device__ __forceinline__ f32x4 mfma(V8 a, V8 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -79,13 +99,33 @@ template <> struct Split<float> {
 // 8 fp32 values -> the P part vectors of an MFMA A / B fragment
 template <typename T>
 __device__ __forceinline__ void split8(const float* x, typename Split<T>::V8* parts) {
+    if constexpr (Split<T>::P == 1) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        T p[Split<T>::P];
-        Split<T>::split(x[e], p);
+        for (int e = 0; e < 8; ++e) parts[0][e] = x[e];
+    } else {
 #pragma unroll
-        for (int q = 0; q < Split<T>::P; ++q) parts[q][e] = p[q];
+        for (int e = 0; e < 8; e += 2) {
+            typename Split<T>::V2 p[Split<T>::P];
+            Split<T>::split2(x[e], x[e + 1], p);
+#pragma unroll
+            for (int q = 0; q < Split<T>::P; ++q) {
+                parts[q][e] = p[q][0];
+                parts[q][e + 1] = p[q][1];
+            }
+        }
     }
+}
+
+// 4 fp32 values -> each part's 4 elements packed in 8 bytes (the half types)
+template <typename T>
+__device__ __forceinline__ void split4_packed(const float (&x)[4], uint2* out) {
+    static_assert(sizeof(T) == 2, "packed parts of the half types");
+    typename Split<T>::V2 p01[Split<T>::P], p23[Split<T>::P];
+    Split<T>::split2(x[0], x[1], p01);
+    Split<T>::split2(x[2], x[3], p23);
+#pragma unroll
+    for (int q = 0; q < Split<T>::P; ++q)
+        out[q] = make_uint2(__builtin_bit_cast(unsigned, p01[q]), __builtin_bit_cast(unsigned, p23[q]));
 }
 
 // 8 elements of one part (16 bytes for the half types, 32 for fp32; 16-byte aligned) -> V8

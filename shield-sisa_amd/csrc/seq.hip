@@ -599,14 +599,10 @@ __device__ __forceinline__ void put4(T* p, long long part_stride, float v0, floa
         *reinterpret_cast<float4*>(p) = make_float4(v0, v1, v2, v3);
     } else {
         const float v[4] = {v0, v1, v2, v3};
-        T part[4][Split<T>::P];
+        uint2 four[Split<T>::P];
+        split4_packed<T>(v, four);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) Split<T>::split(v[e], part[e]);
-#pragma unroll
-        for (int q = 0; q < Split<T>::P; ++q) {
-            const T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
-            *reinterpret_cast<uint2*>(p + q * part_stride) = *reinterpret_cast<const uint2*>(four);
-        }
+        for (int q = 0; q < Split<T>::P; ++q) *reinterpret_cast<uint2*>(p + q * part_stride) = four[q];
     }
 }
 template <typename T>

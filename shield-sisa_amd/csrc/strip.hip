@@ -65,13 +65,10 @@ template <> struct Split16<bf16> {
 // float4 -> the P part fragments (k = the 4 values)
 template <typename T> __device__ __forceinline__ void split4(const float4 v, typename Split16<T>::V4* parts) {
     const float x[4] = {v.x, v.y, v.z, v.w};
+    uint2 four[Split<T>::P];
+    split4_packed<T>(x, four);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        T p[Split<T>::P];
-        Split<T>::split(x[e], p);
-#pragma unroll
-        for (int q = 0; q < Split<T>::P; ++q) parts[q][e] = Split16<T>::bits(p[q]);
-    }
+    for (int q = 0; q < Split<T>::P; ++q) parts[q] = __builtin_bit_cast(typename Split16<T>::V4, four[q]);
 }
 // acc += W . A over the split products; w = weight parts (A operand), x = activation parts (B operand)
 template <typename T>
@@ -956,15 +953,12 @@ __global__ void __launch_bounds__(C::THREADS, C::MINB) ir_wgstrip_kernel(IrArgs 
             const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W && c4 * 4 < C::CIN;
             const float x[4] = {in ? xpre[k].x : 0.0f, in ? xpre[k].y : 0.0f, in ? xpre[k].z : 0.0f,
                                 in ? xpre[k].w : 0.0f};
-            T part[4][P];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) S::split(x[e], part[e]);
+            uint2 four[P];
+            split4_packed<T>(x, four);
             const int jl = row_slot<C>(j, rb) * C::NT + t;
 #pragma unroll
-            for (int q = 0; q < P; ++q) {
-                T four[4] = {part[0][q], part[1][q], part[2][q], part[3][q]};
-                *reinterpret_cast<uint2*>(Xs + ((jl * P + q) * C::NPOS + p) * C::XLD + c4 * 4) = *reinterpret_cast<const uint2*>(four);
-            }
+            for (int q = 0; q < P; ++q)
+                *reinterpret_cast<uint2*>(Xs + ((jl * P + q) * C::NPOS + p) * C::XLD + c4 * 4) = four[q];
         }
     };
     const std::true_type full_rows;
