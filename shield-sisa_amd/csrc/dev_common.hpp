@@ -70,13 +70,19 @@ __device__ __forceinline__ float clamp06(float x) {
     return t < 6.0f ? t : 6.0f;
 }
 // v / 6 correctly rounded: q = v * fp32(1/6) refined by one fma residual step.  Checked against the IEEE quotient
-// for all 2^32 fp32 inputs: identical for every finite |v| >= 2.4e-38; below that (a subnormal quotient) the
-// division itself runs, on an out-of-line path that is skipped when no lane needs it.
-__device__ __forceinline__ float div6(float v) {
+// for all 2^32 fp32 inputs: identical for every finite |v| >= 2.4e-38.  Zero is its own quotient (the step turns
+// -0 into +0), a select; for the rest below 2.4e-38 (a subnormal quotient) the division itself runs, on an
+// out-of-line path that is skipped when no lane needs it -- hardswish's zeros (x <= -3) no longer take it.
+__device__ __forceinline__ float div6_step(float v) {   // the product and the residual step, zero kept
     const float r = 0.16666667163372039794921875f;
-    float q = v * r;
-    q = __builtin_fmaf(__builtin_fmaf(-q, 6.0f, v), r, q);
-    if (__builtin_expect(__builtin_fabsf(v) < 2.4e-38f, 0)) q = v / 6.0f;
+    const float q = v * r;
+    const float s = __builtin_fmaf(__builtin_fmaf(-q, 6.0f, v), r, q);
+    return v == 0.0f ? v : s;
+}
+__device__ __forceinline__ bool div6_tiny(float v) { return __builtin_fabsf(v) < 2.4e-38f && v != 0.0f; }
+__device__ __forceinline__ float div6(float v) {
+    float q = div6_step(v);
+    if (__builtin_expect(div6_tiny(v), 0)) q = v / 6.0f;
     return q;
 }
 __device__ __forceinline__ float hswish(float x) { return div6(x * clamp06(x)); }
@@ -102,6 +108,29 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     case ACT_HSIG: return hsigmoid(v);
     case ACT_SILU: return silu(v);
     default: return v;
+    }
+}
+// apply_act on four values with the activation fixed, bitwise apply_act per value: hardswish / hardsigmoid run
+// div6's product and residual step on all four and its division only when one of the four quotients is subnormal
+// (one branch per four values instead of one per value)
+template <int ACT> __device__ __forceinline__ void apply_act4(float (&x)[4]) {
+    if constexpr (ACT == ACT_HS || ACT == ACT_HSIG) {
+        float v[4];
+        bool tiny = false;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = ACT == ACT_HS ? x[e] * clamp06(x[e]) : clamp06(x[e]);
+            x[e] = div6_step(v[e]);
+            tiny = tiny || div6_tiny(v[e]);
+        }
+        if (__builtin_expect(tiny, 0)) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (div6_tiny(v[e])) x[e] = v[e] / 6.0f;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = apply_act(x[e], ACT);
     }
 }
 // gate nonlinearities evaluated with the device libm (the reference uses glibc expf/log1pf here)

@@ -1581,8 +1581,10 @@ __global__ void __launch_bounds__(256, 2) gemm_wide_kernel(GemmArgs p) {
         const int c4 = lane % C4, rsub = lane / C4;
         const int n = min(nbase + c4 * 4, p.N - 4);
         const float4 bv = p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const auto go = [&](auto act) {
+        // PLAIN (bias, no residual: the expand layers): the flags leave the per-element code
+        const auto go = [&](auto act, auto plain) {
             constexpr int ACT = decltype(act)::value;
+            constexpr bool PLAIN = decltype(plain)::value;
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
@@ -1606,26 +1608,38 @@ __global__ void __launch_bounds__(256, 2) gemm_wide_kernel(GemmArgs p) {
                     const float in[4] = {v[k].x, v[k].y, v[k].z, v[k].w}, bb[4] = {bv.x, bv.y, bv.z, bv.w},
                                 rr[4] = {rv[k].x, rv[k].y, rv[k].z, rv[k].w};
                     f32x4 o;
+                    if constexpr (PLAIN) {   // epi_value's operations with bias, activation fixed, no residual
+                        float x[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {   // epi_value's operations with the activation fixed
-                        float x = in[e] * p.wscale;
-                        if (p.bias) x = x + bb[e];
-                        x = apply_act(x, ACT);
-                        if (p.res == 3) x = rr[e] + 0.7071067811865475244f * x;
-                        else if (p.res) x = p.res == 2 ? rr[e] + x / 1.41421356237309515f : rr[e] + x;
-                        o[e] = x;
+                        for (int e = 0; e < 4; ++e) x[e] = in[e] * p.wscale + bb[e];
+                        apply_act4<ACT>(x);
+                        o = f32x4{x[0], x[1], x[2], x[3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {   // epi_value's operations with the activation fixed
+                            float x = in[e] * p.wscale;
+                            if (p.bias) x = x + bb[e];
+                            x = apply_act(x, ACT);
+                            if (p.res == 3) x = rr[e] + 0.7071067811865475244f * x;
+                            else if (p.res) x = p.res == 2 ? rr[e] + x / 1.41421356237309515f : rr[e] + x;
+                            o[e] = x;
+                        }
                     }
                     __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(p.C + m * p.ldc + nbase + c4 * 4));
                 }
             }
         };
+        const auto go_act = [&](auto act) {
+            if (p.bias && !p.res) go(act, std::true_type{});
+            else go(act, std::false_type{});
+        };
         // the activation is uniform: one branch per group, straight-line code per element
         switch (p.act) {
-        case ACT_RELU: go(std::integral_constant<int, ACT_RELU>{}); break;
-        case ACT_HS: go(std::integral_constant<int, ACT_HS>{}); break;
-        case ACT_HSIG: go(std::integral_constant<int, ACT_HSIG>{}); break;
-        case ACT_SILU: go(std::integral_constant<int, ACT_SILU>{}); break;
-        default: go(std::integral_constant<int, ACT_NONE>{}); break;
+        case ACT_RELU: go_act(std::integral_constant<int, ACT_RELU>{}); break;
+        case ACT_HS: go_act(std::integral_constant<int, ACT_HS>{}); break;
+        case ACT_HSIG: go_act(std::integral_constant<int, ACT_HSIG>{}); break;
+        case ACT_SILU: go_act(std::integral_constant<int, ACT_SILU>{}); break;
+        default: go_act(std::integral_constant<int, ACT_NONE>{}); break;
         }
     };
     // wave w takes the GR-tile groups w, w + 4, ...; its tiles' weights alternate between two register sets, the

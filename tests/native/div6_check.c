@@ -1,7 +1,9 @@
-/* Exhaustive check of the division-by-6 formula the HIP kernels use for hardswish / hardsigmoid
- * (shield-sisa_amd/csrc/dev_common.hpp: div6): q = v * fp32(1/6); q = fma(fma(-q, 6, v), fp32(1/6), q).
- * For every finite fp32 v the result is compared with the IEEE quotient v / 6.0f.  Prints the number of
- * mismatches and the largest |v| that mismatches; the kernels fall back to the division below that bound. */
+/* Exhaustive check of the division by 6 the HIP kernels use for hardswish / hardsigmoid
+ * (shield-sisa_amd/csrc/dev_common.hpp: div6_step, div6): the step q = v * fp32(1/6);
+ * q = fma(fma(-q, 6, v), fp32(1/6), q), zero returned as itself, and the IEEE division where 0 < |v| < 2.4e-38.
+ * For every finite fp32 v both the plain step and the whole function are compared with the IEEE quotient
+ * v / 6.0f.  Prints the plain step's mismatch count, the largest |v| among them, and the whole function's mismatch
+ * count (which must be 0). */
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -9,9 +11,9 @@
 
 int main(void) {
     const float r = 0.16666667163372039794921875f;
-    unsigned long long bad = 0;
+    unsigned long long bad = 0, bad_fn = 0;
     float worst = 0.0f;
-#pragma omp parallel for reduction(+ : bad) reduction(max : worst) schedule(static)
+#pragma omp parallel for reduction(+ : bad, bad_fn) reduction(max : worst) schedule(static)
     for (long long u = 0; u <= 0xFFFFFFFFLL; ++u) {
         const uint32_t b = (uint32_t)u;
         float v;
@@ -24,7 +26,10 @@ int main(void) {
             bad++;
             if (fabsf(v) > worst) worst = fabsf(v);
         }
+        float f = v == 0.0f ? v : q;
+        if (fabsf(v) < 2.4e-38f && v != 0.0f) f = v / 6.0f;
+        if (memcmp(&ref, &f, 4) != 0) bad_fn++;
     }
-    printf("%llu %.9g\n", bad, (double)worst);
+    printf("%llu %.9g %llu\n", bad, (double)worst, bad_fn);
     return 0;
 }
