@@ -160,6 +160,9 @@ template <typename T, class C> struct StripLds {
 // execution plus a wait on the wave's own LDS traffic separates staging from use.
 constexpr int STEM_FR = 17, STEM_FC = 33 * 3;    // staged frame rows, bytes per staged row
 constexpr int STEM_TILE = STEM_FR * 33 * 4;      // T elements of one part of a wave's tile
+// byte -> parts table of one part: the three channels' 256 entries, then 256 zeros that bytes outside the frame
+// are looked up in (a row offset chosen per lane and row instead of a select per staged element and part)
+constexpr int STEM_LUT = 4 * 256, STEM_ZERO = 3 * 256;
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // Lane l stages byte columns l and l + 64 (the latter for l < STEM_FC - 64) of the step's 17 frame rows.  Addresses
 // are clamped into the frame so that every load is unconditional and all are in flight together; bytes outside the
@@ -190,8 +193,8 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
     constexpr int P = Split<T>::P;
     static_assert(!STEM || (!C::EXPAND && C::S == 1 && C::CIN == 16 && C::IR == 8), "the stem feeds block 1 only");
     __shared__ __attribute__((aligned(16))) unsigned char lds_raw[(L::BYTES + 15) / 16 * 16];
-    // STEM: the waves' frame tiles [wave][part][STEM_TILE], then the byte -> parts table [part][768]
-    __shared__ __attribute__((aligned(16))) T stem_lds[STEM ? (ST_THREADS / 64) * P * STEM_TILE + P * 768 : 1];
+    // STEM: the waves' frame tiles [wave][part][STEM_TILE], then the byte -> parts table [part][STEM_LUT]
+    __shared__ __attribute__((aligned(16))) T stem_lds[STEM ? (ST_THREADS / 64) * P * STEM_TILE + P * STEM_LUT : 1];
     T* We = reinterpret_cast<T*>(lds_raw);                               // [P][CT*16][KP]
     T* Wp = We + L::WE;                                                  // [P][OT*16][CP]
     float* Be = reinterpret_cast<float*>(lds_raw + (L::WE + L::WP) * sizeof(T));   // [2][CT*16]
@@ -225,11 +228,11 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
         (void)CEXPP;
         if constexpr (STEM) {
             for (int i = tid; i < (ST_THREADS / 64) * P * STEM_TILE; i += ST_THREADS) stem_lds[i] = T(0.0f);
-            for (int i = tid; i < 768; i += ST_THREADS) {
+            for (int i = tid; i < STEM_LUT; i += ST_THREADS) {
                 T part[P];
-                Split<T>::split(a.lut[i], part);
+                Split<T>::split(i < STEM_ZERO ? a.lut[i] : 0.0f, part);
 #pragma unroll
-                for (int q = 0; q < P; ++q) stem_lds[(ST_THREADS / 64) * P * STEM_TILE + q * 768 + i] = part[q];
+                for (int q = 0; q < P; ++q) stem_lds[(ST_THREADS / 64) * P * STEM_TILE + q * STEM_LUT + i] = part[q];
             }
         }
     }
@@ -317,19 +320,21 @@ __global__ void __launch_bounds__(ST_THREADS, C::MINB) ir_strip_kernel(IrArgs a,
                 {
                     const int e1 = lane + 64;
                     const bool c0 = fb0 + lane >= 0 && fb0 + lane < 320 * 3, c1 = e1 < STEM_FC && fb0 + e1 < 320 * 3;
-                    const int d0 = (lane / 3) * 4 + lane % 3, d1 = (e1 / 3) * 4 + e1 % 3;   // tile slots
-                    const int t0 = (lane % 3) * 256, t1 = (e1 % 3) * 256;                 // table rows
+                    // tile slots; lanes past the row's bytes store a zero into a channel-3 pad slot (zero anyway)
+                    // rather than branch around the store
+                    const int d0 = (lane / 3) * 4 + lane % 3;
+                    const int d1 = e1 < STEM_FC ? (e1 / 3) * 4 + e1 % 3 : ((e1 - STEM_FC) % 33) * 4 + 3;
+                    // table rows: the byte's channel, or the zeros for bytes outside the frame
+                    const int t0 = c0 ? (lane % 3) * 256 : STEM_ZERO, t1 = c1 ? (e1 % 3) * 256 : STEM_ZERO;
 #pragma unroll
                     for (int u = 0; u < STEM_FR; ++u) {
                         const bool rin_u = fy0 + u >= 0 && fy0 + u < 180;   // uniform
+                        const int i0 = (rin_u ? t0 : STEM_ZERO) + sbytes[2 * u];
+                        const int i1 = (rin_u ? t1 : STEM_ZERO) + sbytes[2 * u + 1];
 #pragma unroll
                         for (int q = 0; q < P; ++q) {
-                            const T x0 = stab[q * 768 + t0 + sbytes[2 * u]];
-                            stile[q * STEM_TILE + u * 132 + d0] = rin_u && c0 ? x0 : T(0.0f);
-                            if (e1 < STEM_FC) {
-                                const T x1 = stab[q * 768 + t1 + sbytes[2 * u + 1]];
-                                stile[q * STEM_TILE + u * 132 + d1] = rin_u && c1 ? x1 : T(0.0f);
-                            }
+                            stile[q * STEM_TILE + u * 132 + d0] = stab[q * STEM_LUT + i0];
+                            stile[q * STEM_TILE + u * 132 + d1] = stab[q * STEM_LUT + i1];
                         }
                     }
                 }
